@@ -1,0 +1,234 @@
+#!/usr/bin/env python3
+"""Benchmark: Gaussian-field delta-W elements/s for forward + backward on one MI355X.
+
+A step is one forward (binning + render) and one backward (gradient reduction + chain rule) of
+one layer's field, with inputs resident in HBM, issued through the sync-free C ABI path
+(guass_amd.ops.FieldPlan) and replayed from a HIP graph.  Workload
+("cfg3"), 1280x1280 fp32 delta-W from K=1024 Gaussians, 16x16 tiles, 3 sigma, clamp 80.
+
+Prints one JSON line (metric contract of the driver) with two extra objects:
+  roofline      the dominant kernel's achieved throughput against MI355X peak, from HIP events
+                recorded on the launch stream around each phase;
+  cpu_baseline  the CPU oracle (a from-scratch port of the reference's torch CPU path) timed on
+                this host on the same inputs.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "ΔW elements/sec fwd+bwd at 1280×1280,K=1024; % HBM/VALU roofline"
+HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
+VALU_FP32_PEAK = 157.3e12  # flop/s, MI355X fp32 vector (packed)
+FWD_FLOPS_PER_EVAL = 15    # per (pixel, Gaussian) evaluation, reference forward.cu:346-361
+BWD_FLOPS_PER_EVAL = 41    # reference backward.cu:313-351
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--config", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg5"])
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-graph", action="store_true", help="eager launches instead of graph replay")
+    ap.add_argument("--phase-steps", type=int, default=100, help="eager steps timed per phase")
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def algorithmic_counts(tile_ptr, M: int, N: int, K: int, tile_out: int, tile_in: int) -> dict:
+    import torch
+
+    R = (M + tile_out - 1) // tile_out
+    C = (N + tile_in - 1) // tile_in
+    counts = (tile_ptr[1:] - tile_ptr[:-1]).to(torch.float64).reshape(R, C).cpu()
+    rows = torch.full((R,), float(tile_out), dtype=torch.float64)
+    rows[-1] = M - (R - 1) * tile_out
+    cols = torch.full((C,), float(tile_in), dtype=torch.float64)
+    cols[-1] = N - (C - 1) * tile_in
+    E = float((counts * rows.reshape(-1, 1) * cols.reshape(1, -1)).sum())
+    return {
+        "pairs": int(tile_ptr[-1].item()),
+        "evals": E,
+        # per fwd+bwd: write delta + read dL/ddelta (4 B each per element), read 24 B and
+        # write 24 B of parameters / gradients per Gaussian
+        "bytes_step": 8.0 * M * N + 48.0 * K,
+        "bytes_fwd_render": 4.0 * M * N + 24.0 * K,
+        "bytes_bwd": 4.0 * M * N + 48.0 * K,
+        "flops_fwd": FWD_FLOPS_PER_EVAL * E,
+        "flops_bwd": BWD_FLOPS_PER_EVAL * E,
+    }
+
+
+def roofline(bytes_: float, flops: float, seconds: float) -> dict:
+    t_hbm = bytes_ / HBM_PEAK
+    t_valu = flops / VALU_FP32_PEAK
+    if t_valu >= t_hbm:
+        ach = flops / seconds / 1e12
+        return {"bound": "valu", "achieved": ach, "peak": VALU_FP32_PEAK / 1e12, "unit": "TFLOP/s",
+                "frac": ach / (VALU_FP32_PEAK / 1e12)}
+    ach = bytes_ / seconds / 1e9
+    return {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": ach / (HBM_PEAK / 1e9)}
+
+
+def cpu_baseline(problem, reps: int) -> dict:
+    import torch
+
+    from oracle import field_oracle as fo  # CPU baseline leg only
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    p = problem
+    run = lambda: fo.gaussian_field_fwd_bwd(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp,  # noqa: E731
+                                            p.grad, 16, 16, 3.0, False, 80.0)
+    run()  # warmup
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": p.out_features * p.in_features / med, "unit": "ΔW elements/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{p.name} seed {p.meta['seed']}: full layer fwd+bwd (per-tile loop + autograd), "
+                      f"1 warmup + median of {reps}, {med:.2f} s each"}
+
+
+def main() -> int:
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
+              "this build has no multi-GPU path to time.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from guass_amd import workloads as wl
+    from guass_amd.cuda_field import ext
+    from guass_amd.ops import FieldPlan
+
+    dev = torch.device("cuda:0")
+    prob = wl.CONFIGS[args.config](args.seed)
+    q = prob.to(dev)
+    M, N, K = prob.out_features, prob.in_features, prob.k
+
+    # Pair count of this input (one synchronising drop-in forward), then a sync-free plan.
+    _, tp0, _ = ext.gaussian_field_forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
+                                           16, 16, 3.0, False, 80.0)
+    counts = algorithmic_counts(tp0, M, N, K, 16, 16)
+    P = counts["pairs"]
+    plan = FieldPlan(M, N, K, dev, ids_capacity=P)
+
+    def step():
+        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, pairs_hint=P)
+        plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
+
+    stream = torch.cuda.Stream(dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream(dev).wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+    run = graph.replay if graph is not None else step
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        run()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    ms_per_step = 1e3 * wall / args.steps
+    status = plan.status()
+    if status:
+        print(f"device status bits {status:#x} after the timed run", file=sys.stderr)
+        return 1
+
+    # Per-phase durations, HIP events on the launch stream (torch's current stream).
+    import ctypes
+
+    from guass_amd import _native as NAT
+
+    L = NAT.lib()
+    s = NAT.stream_handle(dev)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.phase_steps)]
+    for i in range(args.phase_steps):
+        e = evs[i]
+        e[0].record()
+        NAT.check(L.gf_forward_bin(ctypes.byref(plan.cfg), M, N, K, q.mu.data_ptr(), q.chol_raw.data_ptr(),
+                                   plan.tile_ptr.data_ptr(), plan.num_pairs.data_ptr(), None,
+                                   plan.fwd_ws.data_ptr(), plan.fwd_ws_bytes, s), "bin")
+        e[1].record()
+        NAT.check(L.gf_forward_render(ctypes.byref(plan.cfg), M, N, K, q.row_coords.data_ptr(),
+                                      q.col_coords.data_ptr(), q.mu.data_ptr(), q.chol_raw.data_ptr(),
+                                      q.amp.data_ptr(), plan.tile_ptr.data_ptr(), plan.ids.data_ptr(), P, P,
+                                      plan.delta.data_ptr(), plan.fwd_ws.data_ptr(), plan.fwd_ws_bytes, s),
+                  "render")
+        e[2].record()
+        plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
+        e[3].record()
+    torch.cuda.synchronize()
+    ph = {name: statistics.median(evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(args.phase_steps))
+          for j, name in enumerate(("bin", "emit_render", "backward"))}
+
+    value = M * N / (ms_per_step / 1e3)
+    bwd_s = ph["backward"] / 1e3
+    roof = roofline(counts["bytes_bwd"], counts["flops_bwd"], bwd_s)
+    roof.update({"kernel": "k_bwd_tiles (gf_backward, one launch)", "traffic": None,
+                 "duration_us": ph["backward"] * 1e3})
+    step_roof = roofline(counts["bytes_step"], counts["flops_fwd"] + counts["flops_bwd"],
+                         ms_per_step / 1e3)
+    out = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "ΔW elements/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Gaussian field, BASELINE.json distribution)",
+        "config": {"workload": f"{prob.name} fwd+bwd, 16x16 tiles, 3 sigma, clamp 80",
+                   "out_features": M, "in_features": N, "k": K, "pairs": P,
+                   "pair_pixel_evals": counts["evals"],
+                   "launch": "hip graph replay" if graph is not None else "eager"},
+        "roofline": roof,
+        "step_roofline": step_roof,
+        "phases_us": {k: v * 1e3 for k, v in ph.items()},
+        "gpu_event_ms_per_step": gpu_ms / args.steps,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(prob, args.cpu_reps)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,102 @@
+"""ctypes binding of ``libgaussfield.so`` (C ABI declared in ``include/gaussfield.h``).
+
+``torch`` is imported before the library is opened: torch ships its own HIP runtime under the
+same SONAME (libamdhip64.so.7), so the dynamic loader then binds this library to that runtime
+and the process keeps a single HIP runtime.  There is no CPU fallback: if the library is
+missing or a call fails, a ``RuntimeError`` is raised.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_char_p, c_double, c_int, c_int32, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the dlopen below)
+
+LIB_PATH = Path(__file__).resolve().with_name("libgaussfield.so")
+
+GF_OK = 0
+GF_STATUS_CAPACITY = 0x1
+GF_STATUS_COUNT_MISMATCH = 0x2
+GF_STATUS_TILE_PTR_LAST = 0x4
+GF_STATUS_TILE_PTR_ORDER = 0x8
+GF_STATUS_IDS_NEGATIVE = 0x10
+GF_STATUS_IDS_RANGE = 0x20
+
+# Symbols include/gaussfield.h declares.
+EXPORTED = (
+    "gf_version", "gf_last_error", "gf_tile_grid", "gf_forward_workspace_bytes",
+    "gf_backward_workspace_bytes", "gf_forward_bin", "gf_forward_render", "gf_backward",
+    "gf_read_status", "gf_selftest_softplus",
+)
+
+
+class GfFieldConfig(ctypes.Structure):
+    """``gf_field_config`` (mirrors the reference ForwardConfig, csrc/field.h:11-18)."""
+
+    _fields_ = [
+        ("tile_out", c_int64),
+        ("tile_in", c_int64),
+        ("sigma_multiplier", c_double),
+        ("normalize", c_int32),
+        ("has_clamp_quad", c_int32),
+        ("clamp_quad", c_double),
+    ]
+
+
+def make_config(tile_out: int, tile_in: int, sigma_multiplier: float, normalize: bool,
+                clamp_quad: float | None) -> GfFieldConfig:
+    return GfFieldConfig(int(tile_out), int(tile_in), float(sigma_multiplier), 1 if normalize else 0,
+                         0 if clamp_quad is None else 1, 0.0 if clamp_quad is None else float(clamp_quad))
+
+
+_LIB = None
+_P = c_void_p
+_CFG = POINTER(GfFieldConfig)
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (opened once per process)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is not built; run `python -m guass_amd.build` (hipcc, gfx950). "
+            "There is no CPU fallback for the Gaussian-field kernels.")
+    L = ctypes.CDLL(str(LIB_PATH))
+    L.gf_version.restype = c_char_p
+    L.gf_last_error.restype = c_char_p
+    L.gf_tile_grid.argtypes = [c_int64, c_int64, _CFG, POINTER(c_int64), POINTER(c_int64)]
+    L.gf_forward_workspace_bytes.argtypes = [c_int64, c_int64, c_int64, _CFG]
+    L.gf_forward_workspace_bytes.restype = c_size_t
+    L.gf_backward_workspace_bytes.argtypes = [c_int64, c_int64, c_int64, _CFG]
+    L.gf_backward_workspace_bytes.restype = c_size_t
+    L.gf_forward_bin.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_size_t, _P]
+    L.gf_forward_render.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P,
+                                    c_int64, c_int64, _P, _P, c_size_t, _P]
+    L.gf_backward.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int32,
+                              _P, c_int32, c_int64, _P, _P, _P, _P, c_size_t, _P]
+    L.gf_read_status.argtypes = [_P, c_int32, POINTER(c_uint32), _P]
+    L.gf_selftest_softplus.argtypes = [POINTER(c_uint64), _P]
+    for name in ("gf_tile_grid", "gf_forward_bin", "gf_forward_render", "gf_backward",
+                 "gf_read_status", "gf_selftest_softplus"):
+        getattr(L, name).restype = c_int
+    _LIB = L
+    return L
+
+
+def check(rc: int, what: str) -> None:
+    if rc != GF_OK:
+        msg = lib().gf_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what}: {msg} (code {rc})")
+
+
+def ptr(t) -> int | None:
+    """Device address of a tensor (None for an empty tensor)."""
+    return t.data_ptr() if t is not None and t.numel() > 0 else None
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

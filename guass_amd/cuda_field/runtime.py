@@ -1,0 +1,136 @@
+"""Autograd boundary of the Gaussian-field path (gaussian_peft/cuda_field/runtime.py:11-345).
+
+Same classes, functions, argument order, saved-tensor order and backward return tuple as the
+reference, so ``GaussianLinear`` and the patchers call into it unchanged.  Forward and
+backward run on ``libgaussfield.so`` (gfx950 kernels).
+"""
+
+from __future__ import annotations
+
+import warnings
+
+import torch
+from torch import Tensor
+
+from guass_amd.cuda_field.loader import load_extension
+
+
+def _forward(ctx, row_coords, col_coords, mu, chol_raw, amp, tile_out, tile_in, sigma_multiplier,
+             normalize, clamp_quad):
+    ext = load_extension(verbose=False)
+    delta, tile_ptr, gaussian_ids_sorted = ext.gaussian_field_forward(
+        row_coords, col_coords, mu, chol_raw, amp, tile_out, tile_in, sigma_multiplier, normalize,
+        clamp_quad)
+    ctx.save_for_backward(row_coords, col_coords, mu, chol_raw, amp, tile_ptr, gaussian_ids_sorted)
+    ctx.tile_out = tile_out
+    ctx.tile_in = tile_in
+    ctx.sigma_multiplier = sigma_multiplier
+    ctx.normalize = normalize
+    ctx.clamp_quad = clamp_quad
+    return delta
+
+
+def _backward(ctx, grad_delta, entry: str):
+    ext = load_extension(verbose=False)
+    row_coords, col_coords, mu, chol_raw, amp, tile_ptr, gaussian_ids_sorted = ctx.saved_tensors
+    d_mu, d_chol_raw, d_amp = getattr(ext, entry)(
+        grad_delta.contiguous(), row_coords, col_coords, mu, chol_raw, amp, tile_ptr,
+        gaussian_ids_sorted, ctx.tile_out, ctx.tile_in, ctx.sigma_multiplier, ctx.normalize,
+        ctx.clamp_quad)
+    return (None, None, d_mu, d_chol_raw, d_amp, None, None, None, None, None)
+
+
+class GaussianFieldCudaReferenceFunction(torch.autograd.Function):
+    """Validation entry (reference runtime.py:11-104): same forward; backward through the
+    extension's reference entry, which returns the training gradients."""
+
+    _backward_warning_emitted = False
+
+    @staticmethod
+    def forward(ctx, row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol_raw: Tensor,
+                amp: Tensor, tile_out: int, tile_in: int, sigma_multiplier: float, normalize: bool,
+                clamp_quad: float | None) -> Tensor:
+        return _forward(ctx, row_coords, col_coords, mu, chol_raw, amp, tile_out, tile_in,
+                        sigma_multiplier, normalize, clamp_quad)
+
+    @staticmethod
+    def backward(ctx, grad_delta: Tensor):
+        if not GaussianFieldCudaReferenceFunction._backward_warning_emitted:
+            warnings.warn("gaussian_field_reference backward is a validation entry point; use "
+                          "gaussian_field_train for training.", stacklevel=2)
+            GaussianFieldCudaReferenceFunction._backward_warning_emitted = True
+        return _backward(ctx, grad_delta, "gaussian_field_backward_reference")
+
+
+class GaussianFieldCudaTrainFunction(torch.autograd.Function):
+    """Training entry (reference runtime.py:107-203)."""
+
+    @staticmethod
+    def forward(ctx, row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol_raw: Tensor,
+                amp: Tensor, tile_out: int, tile_in: int, sigma_multiplier: float, normalize: bool,
+                clamp_quad: float | None) -> Tensor:
+        return _forward(ctx, row_coords, col_coords, mu, chol_raw, amp, tile_out, tile_in,
+                        sigma_multiplier, normalize, clamp_quad)
+
+    @staticmethod
+    def backward(ctx, grad_delta: Tensor):
+        return _backward(ctx, grad_delta, "gaussian_field_backward")
+
+
+def gaussian_field_forward_reference(*, row_coords: Tensor, col_coords: Tensor, mu: Tensor,
+                                     chol_raw: Tensor, amp: Tensor, tile_out: int, tile_in: int,
+                                     sigma_multiplier: float, normalize: bool = False,
+                                     clamp_quad: float | None = 80.0,
+                                     verbose_build: bool = False) -> tuple[Tensor, Tensor, Tensor]:
+    ext = load_extension(verbose=verbose_build)
+    return ext.gaussian_field_forward(row_coords, col_coords, mu, chol_raw, amp, tile_out, tile_in,
+                                      sigma_multiplier, normalize, clamp_quad)
+
+
+def gaussian_field_reference(*, row_coords: Tensor, col_coords: Tensor, mu: Tensor,
+                             chol_raw: Tensor, amp: Tensor, tile_out: int, tile_in: int,
+                             sigma_multiplier: float, normalize: bool = False,
+                             clamp_quad: float | None = 80.0,
+                             allow_reference_backward: bool = False) -> Tensor:
+    if not allow_reference_backward and (mu.requires_grad or chol_raw.requires_grad
+                                         or amp.requires_grad):
+        raise RuntimeError(
+            "gaussian_field_reference is validation-only. "
+            "Set allow_reference_backward=True only for explicit gradient "
+            "alignment checks; do not use this path as a training backend.")
+    return GaussianFieldCudaReferenceFunction.apply(row_coords, col_coords, mu, chol_raw, amp,
+                                                    tile_out, tile_in, sigma_multiplier, normalize,
+                                                    clamp_quad)
+
+
+def gaussian_field_train(*, row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol_raw: Tensor,
+                         amp: Tensor, tile_out: int, tile_in: int, sigma_multiplier: float,
+                         normalize: bool = False, clamp_quad: float | None = 80.0) -> Tensor:
+    return GaussianFieldCudaTrainFunction.apply(row_coords, col_coords, mu, chol_raw, amp, tile_out,
+                                                tile_in, sigma_multiplier, normalize, clamp_quad)
+
+
+def gaussian_field_cuda_field_stage2_validation(
+        *, row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol_raw: Tensor, amp: Tensor,
+        tile_out: int, tile_in: int, sigma_multiplier: float, normalize: bool = False,
+        clamp_quad: float | None = 80.0, verbose_build: bool = False
+) -> tuple[Tensor, dict[str, Tensor | float | str]]:
+    """Forward only, plus the binning metadata the reference returns (runtime.py:300-345)."""
+    delta, tile_ptr, gaussian_ids_sorted = gaussian_field_forward_reference(
+        row_coords=row_coords, col_coords=col_coords, mu=mu, chol_raw=chol_raw, amp=amp,
+        tile_out=tile_out, tile_in=tile_in, sigma_multiplier=sigma_multiplier, normalize=normalize,
+        clamp_quad=clamp_quad, verbose_build=verbose_build)
+    per_tile_counts = tile_ptr[1:] - tile_ptr[:-1]
+    tiles_touched = torch.full((mu.size(0),), -1, device=mu.device, dtype=torch.int64)
+    metadata: dict[str, Tensor | float | str] = {
+        "execution_mode": "cuda_field_stage2_validation",
+        "tile_ptr": tile_ptr,
+        "gaussian_ids": gaussian_ids_sorted,
+        "gaussian_ids_sorted": gaussian_ids_sorted,
+        "per_tile_counts": per_tile_counts,
+        "tiles_touched": tiles_touched,
+        "num_tile_rows": float((row_coords.numel() + tile_out - 1) // tile_out),
+        "num_tile_cols": float((col_coords.numel() + tile_in - 1) // tile_in),
+        "accumulate_backend": "cuda_field_stage2_validation",
+    }
+    return delta, metadata

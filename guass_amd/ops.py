@@ -1,0 +1,89 @@
+"""Sync-free, allocation-free-per-call use of libgaussfield.so.
+
+``FieldPlan`` owns every device buffer of one layer's forward and backward (workspaces,
+tile_ptr, a gaussian-id buffer of fixed capacity, delta-W and the gradients), so a training
+step issues kernels only -- no host synchronisation and no allocation -- and can be captured
+in a HIP graph.  The pair count is not read back: if it ever exceeds the id capacity the
+kernels set ``GF_STATUS_CAPACITY`` (check with ``status()``), and the caller re-plans with a
+larger capacity.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from guass_amd import _native as N
+
+
+class FieldPlan:
+    def __init__(self, out_features: int, in_features: int, k: int, device, *, tile_out: int = 16,
+                 tile_in: int = 16, sigma_multiplier: float = 3.0, normalize: bool = False,
+                 clamp_quad: float | None = 80.0, ids_capacity: int | None = None):
+        self.M, self.N, self.K = int(out_features), int(in_features), int(k)
+        self.device = torch.device(device)
+        self.cfg = N.make_config(tile_out, tile_in, sigma_multiplier, normalize, clamp_quad)
+        L = N.lib()
+        R, C = ctypes.c_int64(), ctypes.c_int64()
+        N.check(L.gf_tile_grid(self.M, self.N, ctypes.byref(self.cfg), ctypes.byref(R),
+                               ctypes.byref(C)), "gf_tile_grid")
+        self.num_tile_rows, self.num_tile_cols = R.value, C.value
+        self.T = R.value * C.value
+        if ids_capacity is None:
+            ids_capacity = self.K * self.T  # every Gaussian on every tile
+        self.capacity = int(ids_capacity)
+        dev = self.device
+        self.fwd_ws_bytes = L.gf_forward_workspace_bytes(self.M, self.N, self.K, ctypes.byref(self.cfg))
+        self.bwd_ws_bytes = L.gf_backward_workspace_bytes(self.M, self.N, self.K, ctypes.byref(self.cfg))
+        self.fwd_ws = torch.empty(self.fwd_ws_bytes, dtype=torch.uint8, device=dev)
+        self.bwd_ws = torch.zeros(self.bwd_ws_bytes, dtype=torch.uint8, device=dev)  # self-cleaning
+        self.tile_ptr = torch.empty(self.T + 1, dtype=torch.int64, device=dev)
+        self.num_pairs = torch.empty(1, dtype=torch.int64, device=dev)
+        self.ids = torch.empty(max(self.capacity, 1), dtype=torch.int64, device=dev)
+        self.delta = torch.empty(self.M * self.N, dtype=torch.float32, device=dev)
+        self.d_mu = torch.empty(self.K, 2, dtype=torch.float32, device=dev)
+        self.d_chol_raw = torch.empty(self.K, 3, dtype=torch.float32, device=dev)
+        self.d_amp = torch.empty(self.K, 1, dtype=torch.float32, device=dev)
+
+    def _stream(self) -> int:
+        return N.stream_handle(self.device)
+
+    def forward(self, row_coords, col_coords, mu, chol_raw, amp, pairs_hint: int = 0) -> torch.Tensor:
+        """Bins and renders into ``self.delta`` (and ``tile_ptr`` / ``ids``); returns delta."""
+        L = N.lib()
+        s = self._stream()
+        N.check(L.gf_forward_bin(ctypes.byref(self.cfg), self.M, self.N, self.K, N.ptr(mu),
+                                 N.ptr(chol_raw), self.tile_ptr.data_ptr(), self.num_pairs.data_ptr(),
+                                 None, self.fwd_ws.data_ptr(), self.fwd_ws_bytes, s), "gf_forward_bin")
+        N.check(L.gf_forward_render(ctypes.byref(self.cfg), self.M, self.N, self.K,
+                                    row_coords.data_ptr(), col_coords.data_ptr(), N.ptr(mu),
+                                    N.ptr(chol_raw), N.ptr(amp), self.tile_ptr.data_ptr(),
+                                    self.ids.data_ptr(), self.capacity,
+                                    pairs_hint if pairs_hint > 0 else self.capacity,
+                                    self.delta.data_ptr(), self.fwd_ws.data_ptr(), self.fwd_ws_bytes, s),
+                "gf_forward_render")
+        return self.delta
+
+    def backward(self, grad, row_coords, col_coords, mu, chol_raw, amp, num_pairs: int | None = None):
+        """Gradients into ``d_mu``, ``d_chol_raw``, ``d_amp`` from the last forward's binning."""
+        L = N.lib()
+        n = self.capacity if num_pairs is None else int(num_pairs)
+        N.check(L.gf_backward(ctypes.byref(self.cfg), self.M, self.N, self.K, grad.data_ptr(),
+                              row_coords.data_ptr(), col_coords.data_ptr(), N.ptr(mu), N.ptr(chol_raw),
+                              N.ptr(amp), self.tile_ptr.data_ptr(), 1, self.ids.data_ptr(), 1, n,
+                              N.ptr(self.d_mu), N.ptr(self.d_chol_raw), N.ptr(self.d_amp),
+                              self.bwd_ws.data_ptr(), self.bwd_ws_bytes, self._stream()), "gf_backward")
+        return self.d_mu, self.d_chol_raw, self.d_amp
+
+    def pairs(self) -> int:
+        """Pair count of the last forward (synchronises)."""
+        return int(self.num_pairs.item())
+
+    def status(self, which: str = "forward") -> int:
+        """GF_STATUS_* bits of the last forward or backward (synchronises)."""
+        ws = self.fwd_ws if which == "forward" else self.bwd_ws
+        st = ctypes.c_uint32(0)
+        N.check(N.lib().gf_read_status(ws.data_ptr(), 0, ctypes.byref(st), self._stream()),
+                "gf_read_status")
+        return st.value

@@ -1,0 +1,138 @@
+/*
+ * gaussfield.h - C ABI of libgaussfield.so, the MI355X (gfx950) Gaussian-field
+ * weight-delta renderer.
+ *
+ * A layer's delta-W (out_features x in_features, fp32, row-major) is the sum of K
+ * anisotropic 2-D Gaussians, binned into tile_out x tile_in tiles by their
+ * sigma_multiplier-sigma bounding boxes.  Every pointer argument is a device
+ * pointer unless its name ends in _host.  Every entry point returns 0 on success
+ * and a non-zero GF_E* code otherwise; gf_last_error() then holds the message
+ * (thread-local).  `stream` is a hipStream_t (NULL = the legacy default stream).
+ *
+ * Reference interface replaced (Plutohr/GUASS, paths under gaussian_peft/cuda_field):
+ *   csrc/ext.cpp:9-37     gaussian_field_forward           -> gf_forward_bin + gf_forward_render
+ *   csrc/ext.cpp:38-72    gaussian_field_backward          -> gf_backward
+ *   csrc/ext.cpp:73-110   gaussian_field_backward_reference-> gf_backward (same gradients)
+ *   csrc/field.h:11-18    ForwardConfig                    -> gf_field_config
+ *   csrc/field_impl.cu:52-108 input / saved-state checks   -> GF_E_* codes + device-side checks
+ */
+#ifndef GAUSSFIELD_H_
+#define GAUSSFIELD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GF_OK 0
+#define GF_E_INVALID_ARGUMENT 1   /* bad size / config (tile_out<=0, sigma<=0, ...)      */
+#define GF_E_WORKSPACE 2          /* workspace missing or smaller than *_workspace_bytes  */
+#define GF_E_HIP 3                /* a HIP runtime call or kernel launch failed           */
+#define GF_E_CAPACITY 4           /* pair count exceeds the gaussian_ids capacity         */
+#define GF_E_SAVED_STATE 5        /* saved tile_ptr / gaussian_ids violate the contract   */
+#define GF_E_INTERNAL 6           /* device-side consistency check failed                 */
+
+/* Device-side status bits, written to the status word by the kernels (see gf_read_status). */
+#define GF_STATUS_CAPACITY 0x1u        /* more pairs than ids_capacity: ids truncated        */
+#define GF_STATUS_COUNT_MISMATCH 0x2u  /* per-tile counts disagree with per-Gaussian sums    */
+#define GF_STATUS_TILE_PTR_LAST 0x4u   /* backward: tile_ptr[T] != number of pairs           */
+#define GF_STATUS_TILE_PTR_ORDER 0x8u  /* backward: tile_ptr decreasing / outside [0, pairs] */
+#define GF_STATUS_IDS_NEGATIVE 0x10u   /* backward: a gaussian id < 0                        */
+#define GF_STATUS_IDS_RANGE 0x20u      /* backward: a gaussian id >= K                       */
+
+/* Mirrors ForwardConfig (reference csrc/field.h:11-18). */
+typedef struct gf_field_config {
+  int64_t tile_out;          /* tile height in rows of delta-W, > 0                         */
+  int64_t tile_in;           /* tile width in columns of delta-W, > 0                       */
+  double sigma_multiplier;   /* bounding-box half-width in standard deviations, > 0         */
+  int32_t normalize;         /* non-zero: multiply each Gaussian by 1/(2*pi*sqrt(det cov))  */
+  int32_t has_clamp_quad;    /* non-zero: clamp the quadratic form to [0, clamp_quad]       */
+  double clamp_quad;         /* upper clamp of the quadratic form (80.0 in the layer)       */
+} gf_field_config;
+
+/* Library / device facts. */
+const char* gf_version(void);
+const char* gf_last_error(void);
+
+/* Tile grid of an out_features x in_features delta-W (reference forward.cu:29-35). */
+int gf_tile_grid(int64_t out_features, int64_t in_features, const gf_field_config* cfg,
+                 int64_t* num_tile_rows_host, int64_t* num_tile_cols_host);
+
+/* Workspace sizes in bytes (device memory the caller provides, 256-byte aligned).  The
+ * backward workspace must be zero-filled before its first use; gf_backward leaves it zeroed
+ * again, so a workspace kept across calls needs one clear at allocation. */
+size_t gf_forward_workspace_bytes(int64_t out_features, int64_t in_features, int64_t k,
+                                  const gf_field_config* cfg);
+size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, int64_t k,
+                                   const gf_field_config* cfg);
+
+/*
+ * Forward phase 1 (binning): per-Gaussian geometry and sigma-box tile ranges, per-tile
+ * Gaussian counts and their exclusive scan.
+ *   tile_ptr        [T+1] int64 out: tile t owns gaussian_ids_sorted[tile_ptr[t] : tile_ptr[t+1]]
+ *   num_pairs_dev   [1] int64 out: P = tile_ptr[T] = sum over Gaussians of tiles touched
+ *   num_pairs_host  optional: if non-NULL the call synchronises `stream` and stores P here
+ *                   (the only host synchronisation in the forward, as reference forward.cu:48-73).
+ * Replaces reference forward.cu:372-511 (preprocess_geometry + build_binning_state up to tile_ptr).
+ */
+int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                   const float* mu, const float* chol_raw,
+                   int64_t* tile_ptr, int64_t* num_pairs_dev, int64_t* num_pairs_host,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Forward phase 2: emits the (tile, gaussian) pairs into gaussian_ids_sorted in canonical
+ * order (tile ascending, gaussian id ascending within a tile) and renders delta-W.
+ * Must follow gf_forward_bin on the same stream with the same workspace.
+ *   gaussian_ids_sorted [ids_capacity] int64 out (first P entries valid)
+ *   delta           [out_features*in_features] fp32 out, row-major; every element written
+ *   pairs_hint      P if the caller knows it (sizes the emission grid), else <= 0
+ * Replaces reference forward.cu:465-569 (emit + radix sort + ranges + tile_accumulate_kernel).
+ */
+int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                      const float* row_coords, const float* col_coords,
+                      const float* mu, const float* chol_raw, const float* amp,
+                      const int64_t* tile_ptr, int64_t* gaussian_ids_sorted, int64_t ids_capacity,
+                      int64_t pairs_hint, float* delta,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Backward: reduces dL/d(delta) into per-Gaussian gradients through the saved binning.
+ *   grad_delta      [out_features*in_features] fp32
+ *   tile_ptr        [T+1], int64 if tile_ptr_is_int64 else int32
+ *   gaussian_ids    [num_pairs], int64 if ids_is_int64 else int32 (any order within a tile)
+ *   d_mu [K,2], d_chol_raw [K,3], d_amp [K,1] fp32 out (fully written)
+ * Saved-state violations (non-monotone tile_ptr, tile_ptr[T] != num_pairs, ids outside
+ * [0,K)) are detected on the device, the offending pairs skipped, and status bits set.
+ * Replaces reference backward.cu:541-716 (backward_pair_reduce_train).
+ */
+int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                const float* grad_delta, const float* row_coords, const float* col_coords,
+                const float* mu, const float* chol_raw, const float* amp,
+                const void* tile_ptr, int32_t tile_ptr_is_int64,
+                const void* gaussian_ids, int32_t ids_is_int64, int64_t num_pairs,
+                float* d_mu, float* d_chol_raw, float* d_amp,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Reads (and, if clear != 0, resets) the device status word of a workspace produced by the
+ * calls above.  Synchronises `stream`.  *status_host receives GF_STATUS_* bits.
+ */
+int gf_read_status(void* workspace, int32_t clear, uint32_t* status_host, void* stream);
+
+/*
+ * Self-test hook (no reference counterpart): evaluates on the GPU the fp32 softplus the
+ * binning uses, F.softplus as the reference CPU path computes it (covariance.py:23,25),
+ * over all 2^32 float inputs and returns the order-independent checksum
+ * sum_x mix64(bits(x) << 32 | bits(softplus(x))) (NaN results canonicalised).  It must equal
+ * the checksum oracle/libm_sweep.c computes from the host C library.  Allocates 8 bytes.
+ */
+int gf_selftest_softplus(uint64_t* checksum_host, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GAUSSFIELD_H_ */

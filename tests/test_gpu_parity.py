@@ -1,0 +1,285 @@
+"""GPU parity of libgaussfield.so against the CPU oracle (runs on an MI355X).
+
+Every test calls the product path (guass_amd.cuda_field.ext -> C ABI -> gfx950 kernels) and
+compares with oracle/field_oracle.py on the same seeded fp32 inputs, at the bars of
+tests/parity.py.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from guass_amd import _native
+from guass_amd import workloads as wl
+from guass_amd.cuda_field import ext, runtime
+from guass_amd.ops import FieldPlan
+from oracle import field_oracle as fo
+from tests.parity import binning_equal, field_close, grad_close
+
+pytestmark = pytest.mark.gpu
+
+# checksum of F.softplus over all 2^32 fp32 inputs from the host C library (oracle/libm_sweep.c)
+SOFTPLUS_CHECKSUM = 0x06C0D4E444E1424F
+
+
+def say(msg: str) -> None:
+    print(f"[gpu-test] {msg}", flush=True)
+
+
+def run_gpu(p: wl.FieldProblem, device, tile_out=16, tile_in=16, sigma=3.0, normalize=False,
+            clamp=80.0, index_dtype=torch.int64):
+    q = p.to(device)
+    delta, tp, ids = ext.gaussian_field_forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
+                                                tile_out, tile_in, sigma, normalize, clamp)
+    d_mu, d_raw, d_amp = ext.gaussian_field_backward(
+        q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, tp.to(index_dtype),
+        ids.to(index_dtype), tile_out, tile_in, sigma, normalize, clamp)
+    torch.cuda.synchronize()
+    return delta, tp, ids, d_mu, d_raw, d_amp
+
+
+def oracle(p: wl.FieldProblem, tile_out=16, tile_in=16, sigma=3.0, normalize=False, clamp=80.0,
+           batched=False):
+    fn = fo.gaussian_field_fwd_bwd_batched if batched else fo.gaussian_field_fwd_bwd
+    return fn(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad, tile_out, tile_in, sigma,
+              normalize, clamp)
+
+
+def check(p: wl.FieldProblem, device, batched=False, **kw):
+    say(f"{p.name} M={p.out_features} N={p.in_features} K={p.k} {kw}")
+    g = run_gpu(p, device, **kw)
+    r = oracle(p, batched=batched, **kw)
+    binning_equal(g[1], g[2], r[1], r[2])
+    errs = {"delta": field_close(g[0], r[0])}
+    for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), g[3:], r[3:]):
+        errs[name] = grad_close(a, b, name)
+    say(f"  ok pairs={int(r[1][-1])} " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+    return g, r
+
+
+def tiny_problem(M, N, K, seed, log_scale_px=1.5, spread=0.4):
+    return wl.make_problem(f"tiny_{M}x{N}_k{K}_s{seed}", M, N, K, log_scale_px, spread, seed)
+
+
+# ------------------------------------------------------------------------------------------
+
+def test_softplus_selftest_matches_host_libm(device):
+    say("softplus self-test over 2^32 inputs")
+    h = ctypes_u64()
+    _native.check(_native.lib().gf_selftest_softplus(h, None), "gf_selftest_softplus")
+    assert h.value == SOFTPLUS_CHECKSUM, hex(h.value)
+
+
+def ctypes_u64():
+    import ctypes
+
+    return ctypes.c_uint64(0)
+
+
+@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3"])
+def test_parity_baseline_configs(cfg, device):
+    check(wl.CONFIGS[cfg](0), device)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_parity_cfg2_more_seeds(seed, device):
+    check(wl.cfg2(seed), device)
+
+
+def test_parity_cfg5_full_size(device):
+    # loop oracle for the binning and field (4 s), pair-batched oracle for the gradients
+    p = wl.cfg5(0)
+    check(p, device, batched=True)
+
+
+def test_ragged_tiles(device):
+    check(tiny_problem(37, 53, 20, 4), device)
+
+
+def test_tiles_32x32(device):
+    check(wl.cfg1(0), device, tile_out=32, tile_in=32)
+
+
+def test_tiles_8x24(device):
+    check(tiny_problem(100, 90, 40, 5), device, tile_out=8, tile_in=24)
+
+
+def test_tiles_1x1(device):
+    check(tiny_problem(24, 20, 6, 6, log_scale_px=0.7), device, tile_out=1, tile_in=1)
+
+
+def test_normalize(device):
+    check(wl.cfg1(0), device, normalize=True)
+
+
+def test_no_clamp(device):
+    check(wl.cfg2(0), device, clamp=None)
+
+
+def test_sigma_multiplier_2_5(device):
+    check(wl.cfg2(1), device, sigma=2.5)
+
+
+def test_k1_corner_and_huge(device):
+    # one Gaussian at the top-left corner, one covering the whole matrix
+    p = tiny_problem(70, 90, 2, 7)
+    p.mu[0] = torch.tensor([-1.0, -1.0])
+    p.mu[1] = torch.tensor([0.1, -0.2])
+    p.chol_raw[1] = torch.tensor([2.0, 0.5, 1.5])
+    check(p, device)
+
+
+def test_tiny_sigma_single_tile(device):
+    p = tiny_problem(64, 64, 30, 8, log_scale_px=-3.0, spread=0.1)
+    g, r = check(p, device)
+    assert int(r[1][-1]) == p.k  # every Gaussian on exactly one tile
+
+
+def test_k_zero(device):
+    p = tiny_problem(40, 33, 1, 9)
+    p.mu, p.chol_raw, p.amp = p.mu[:0], p.chol_raw[:0], p.amp[:0]
+    q = p.to(device)
+    delta, tp, ids = ext.gaussian_field_forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
+                                                16, 16, 3.0, False, 80.0)
+    d_mu, d_raw, d_amp = ext.gaussian_field_backward(q.grad, q.row_coords, q.col_coords, q.mu,
+                                                     q.chol_raw, q.amp, tp, ids, 16, 16, 3.0, False, 80.0)
+    torch.cuda.synchronize()
+    assert delta.shape == (40 * 33,) and float(delta.abs().max()) == 0.0
+    assert tp.shape == (3 * 3 + 1,) and int(tp.abs().max()) == 0 and ids.numel() == 0
+    assert d_mu.shape == (0, 2) and d_raw.shape == (0, 3) and d_amp.shape == (0, 1)
+
+
+def test_long_segments_bitmap_path(device):
+    # ~3100 Gaussians per tile (> 2048 LDS keys, K <= 131072): bitmap ordering
+    p = tiny_problem(64, 64, 50000, 10, log_scale_px=-3.0, spread=0.1)
+    check(p, device, batched=True)
+
+
+def test_long_segments_global_path(device):
+    # K > 131072 with ~8800 Gaussians per tile: in-place global-memory ordering
+    p = tiny_problem(64, 64, 140000, 11, log_scale_px=-3.0, spread=0.1)
+    check(p, device, batched=True)
+
+
+def test_int32_saved_state(device):
+    p = wl.cfg1(1)
+    g64 = run_gpu(p, device)
+    g32 = run_gpu(p, device, index_dtype=torch.int32)
+    for a, b in zip(g64[3:], g32[3:]):
+        grad_close(a, b, "int32 vs int64", rtol=1e-6)
+
+
+@pytest.mark.parametrize("kind", ["last", "order", "negative", "range"])
+def test_saved_state_errors(kind, device):
+    p = tiny_problem(48, 48, 12, 12).to(device)
+    delta, tp, ids = ext.gaussian_field_forward(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp,
+                                                16, 16, 3.0, False, 80.0)
+    tp, ids = tp.clone(), ids.clone()
+    if kind == "last":
+        tp[-1] += 1
+        msg = "tile_ptr\\[-1\\] must equal"
+    elif kind == "order":
+        tp[1], tp[2] = tp[2] + 1, tp[1]
+        msg = "monotonic"
+    elif kind == "negative":
+        ids[0] = -3
+        msg = "non-negative"
+    else:
+        ids[-1] = p.k + 5
+        msg = "out-of-range"
+    with pytest.raises(RuntimeError, match=msg):
+        ext.gaussian_field_backward(p.grad, p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, tp,
+                                    ids, 16, 16, 3.0, False, 80.0)
+    torch.cuda.synchronize()
+
+
+def test_autograd_train_function(device):
+    p = wl.cfg2(4)
+    q = p.to(device)
+    mu = q.mu.clone().requires_grad_(True)
+    raw = q.chol_raw.clone().requires_grad_(True)
+    amp = q.amp.clone().requires_grad_(True)
+    delta = runtime.gaussian_field_train(row_coords=q.row_coords, col_coords=q.col_coords, mu=mu,
+                                         chol_raw=raw, amp=amp, tile_out=16, tile_in=16,
+                                         sigma_multiplier=3.0, normalize=False, clamp_quad=80.0)
+    (delta * q.grad).sum().backward()
+    torch.cuda.synchronize()
+    r = oracle(p)
+    field_close(delta, r[0])
+    grad_close(mu.grad, r[3], "mu.grad")
+    grad_close(raw.grad, r[4], "chol_raw.grad")
+    grad_close(amp.grad, r[5], "amp.grad")
+
+
+def test_stage2_validation_metadata(device):
+    p = wl.cfg1(2)
+    q = p.to(device)
+    delta, meta = runtime.gaussian_field_cuda_field_stage2_validation(
+        row_coords=q.row_coords, col_coords=q.col_coords, mu=q.mu, chol_raw=q.chol_raw, amp=q.amp,
+        tile_out=16, tile_in=16, sigma_multiplier=3.0)
+    ref_delta, ref_tp, ref_ids = fo.gaussian_field_forward(p.row_coords, p.col_coords, p.mu,
+                                                           p.chol_raw, p.amp, 16, 16, 3.0)
+    field_close(delta, ref_delta)
+    binning_equal(meta["tile_ptr"], meta["gaussian_ids_sorted"], ref_tp, ref_ids)
+    assert torch.equal(meta["per_tile_counts"].cpu(), ref_tp[1:] - ref_tp[:-1])
+    assert meta["num_tile_rows"] == 20.0 and meta["num_tile_cols"] == 20.0
+    assert meta["execution_mode"] == "cuda_field_stage2_validation"
+
+
+def test_plan_sync_free_and_capacity(device):
+    p = wl.cfg2(5)
+    q = p.to(device)
+    ref = run_gpu(p, device)
+    P = int(ref[1][-1])
+    plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=P)
+    plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+    plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
+    torch.cuda.synchronize()
+    assert plan.status() == 0 and plan.pairs() == P
+    assert torch.equal(plan.delta, ref[0]) and torch.equal(plan.tile_ptr, ref[1])
+    assert torch.equal(plan.ids[:P], ref[2])
+    for a, b in zip((plan.d_mu, plan.d_chol_raw, plan.d_amp), ref[3:]):
+        grad_close(a, b, "plan", rtol=1e-6)
+    small = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=P // 2)
+    small.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+    torch.cuda.synchronize()
+    assert small.status() & _native.GF_STATUS_CAPACITY
+
+
+def test_deterministic_forward(device):
+    p = wl.cfg3(1)
+    a = run_gpu(p, device)
+    b = run_gpu(p, device)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]) and torch.equal(a[2], b[2])
+
+
+def test_graph_replay_matches_eager(device):
+    p = wl.cfg3(2)
+    q = p.to(device)
+    eager = run_gpu(p, device)
+    P = int(eager[1][-1])
+    plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=P)
+    s = torch.cuda.Stream(device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(s):
+        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, pairs_hint=P)
+        plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
+    torch.cuda.current_stream(device).wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, pairs_hint=P)
+        plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
+    for rep in range(3):
+        plan.delta.fill_(float("nan"))
+        plan.d_mu.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(plan.delta, eager[0]), f"replay {rep}: delta"
+        assert torch.equal(plan.ids[:P], eager[2]), f"replay {rep}: ids"
+        for a, b in zip((plan.d_mu, plan.d_chol_raw, plan.d_amp), eager[3:]):
+            grad_close(a, b, f"replay {rep}", rtol=1e-6)
+        _ = (eager[0] * 2.0).sum().item()  # eager work between replays
