@@ -38,9 +38,11 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg5"])
+    ap.add_argument("--config", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg5", "cfg5c"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of graph replay")
+    ap.add_argument("--graph-steps", type=int, default=10,
+                    help="steps captured per HIP graph (replay overhead is paid once per graph)")
     ap.add_argument("--phase-steps", type=int, default=100, help="eager steps timed per phase")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -144,19 +146,26 @@ def main() -> int:
     torch.cuda.current_stream(dev).wait_stream(stream)
     torch.cuda.synchronize()
     graph = None
+    per_run = 1
     if not args.no_graph:
+        # A graph of `per_run` consecutive steps, per_run dividing --steps so that exactly
+        # --steps steps are timed.
+        per_run = max(1, min(args.graph_steps, args.steps))
+        while args.steps % per_run:
+            per_run -= 1
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            step()
+            for _ in range(per_run):
+                step()
     run = graph.replay if graph is not None else step
 
-    for _ in range(args.warmup):
+    for _ in range(max(1, args.warmup // per_run)):
         run()
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record()
-    for _ in range(args.steps):
+    for _ in range(args.steps // per_run):
         run()
     ev1.record()
     torch.cuda.synchronize()
@@ -168,38 +177,34 @@ def main() -> int:
         print(f"device status bits {status:#x} after the timed run", file=sys.stderr)
         return 1
 
-    # Per-phase durations, HIP events on the launch stream (torch's current stream).
-    import ctypes
-
-    from guass_amd import _native as NAT
-
-    L = NAT.lib()
-    s = NAT.stream_handle(dev)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.phase_steps)]
+    # Per-kernel durations: HIP events recorded on the launch stream (torch's current stream)
+    # around each of the five kernels of a step, eager launches.
+    phases = (
+        ("k_bin", lambda: plan.bin(q.mu, q.chol_raw)),
+        ("k_emit", lambda: plan.emit(P)),
+        ("k_render", lambda: plan.render(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)),
+        ("k_bwd", lambda: plan.backward_reduce(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, P)),
+        ("k_bwd_finish", lambda: plan.backward_finish(q.chol_raw, q.amp)),
+    )
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)]
+           for _ in range(args.phase_steps)]
     for i in range(args.phase_steps):
-        e = evs[i]
-        e[0].record()
-        NAT.check(L.gf_forward_bin(ctypes.byref(plan.cfg), M, N, K, q.mu.data_ptr(), q.chol_raw.data_ptr(),
-                                   plan.tile_ptr.data_ptr(), plan.num_pairs.data_ptr(), None,
-                                   plan.fwd_ws.data_ptr(), plan.fwd_ws_bytes, s), "bin")
-        e[1].record()
-        NAT.check(L.gf_forward_render(ctypes.byref(plan.cfg), M, N, K, q.row_coords.data_ptr(),
-                                      q.col_coords.data_ptr(), q.mu.data_ptr(), q.chol_raw.data_ptr(),
-                                      q.amp.data_ptr(), plan.tile_ptr.data_ptr(), plan.ids.data_ptr(), P, P,
-                                      plan.delta.data_ptr(), plan.fwd_ws.data_ptr(), plan.fwd_ws_bytes, s),
-                  "render")
-        e[2].record()
-        plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
-        e[3].record()
+        evs[i][0].record()
+        for j, (_, fn) in enumerate(phases):
+            fn()
+            evs[i][j + 1].record()
     torch.cuda.synchronize()
     ph = {name: statistics.median(evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(args.phase_steps))
-          for j, name in enumerate(("bin", "emit_render", "backward"))}
+          for j, (name, _) in enumerate(phases)}
 
     value = M * N / (ms_per_step / 1e3)
-    bwd_s = ph["backward"] / 1e3
-    roof = roofline(counts["bytes_bwd"], counts["flops_bwd"], bwd_s)
-    roof.update({"kernel": "k_bwd_tiles (gf_backward, one launch)", "traffic": None,
-                 "duration_us": ph["backward"] * 1e3})
+    kernel_rooflines = {
+        "k_render": roofline(counts["bytes_fwd_render"], counts["flops_fwd"], ph["k_render"] / 1e3),
+        "k_bwd": roofline(counts["bytes_bwd"], counts["flops_bwd"], ph["k_bwd"] / 1e3),
+    }
+    dominant = max(kernel_rooflines, key=lambda k: ph[k])
+    roof = dict(kernel_rooflines[dominant])
+    roof.update({"kernel": dominant, "traffic": None, "duration_us": ph[dominant] * 1e3})
     step_roof = roofline(counts["bytes_step"], counts["flops_fwd"] + counts["flops_bwd"],
                          ms_per_step / 1e3)
     out = {
@@ -218,10 +223,12 @@ def main() -> int:
         "config": {"workload": f"{prob.name} fwd+bwd, 16x16 tiles, 3 sigma, clamp 80",
                    "out_features": M, "in_features": N, "k": K, "pairs": P,
                    "pair_pixel_evals": counts["evals"],
-                   "launch": "hip graph replay" if graph is not None else "eager"},
+                   "launch": (f"hip graph replay, {per_run} steps per graph" if graph is not None
+                              else "eager")},
         "roofline": roof,
         "step_roofline": step_roof,
-        "phases_us": {k: v * 1e3 for k, v in ph.items()},
+        "kernels_us": {k: v * 1e3 for k, v in ph.items()},
+        "kernel_rooflines": kernel_rooflines,
         "gpu_event_ms_per_step": gpu_ms / args.steps,
     }
     if not args.no_cpu_baseline:

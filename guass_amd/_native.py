@@ -27,8 +27,9 @@ GF_STATUS_IDS_RANGE = 0x20
 # Symbols include/gaussfield.h declares.
 EXPORTED = (
     "gf_version", "gf_last_error", "gf_tile_grid", "gf_forward_workspace_bytes",
-    "gf_backward_workspace_bytes", "gf_forward_bin", "gf_forward_render", "gf_backward",
-    "gf_read_status", "gf_selftest_softplus",
+    "gf_backward_workspace_bytes", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
+    "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
+    "gf_selftest_softplus",
 )
 
 
@@ -74,14 +75,19 @@ def lib() -> ctypes.CDLL:
     L.gf_backward_workspace_bytes.argtypes = [c_int64, c_int64, c_int64, _CFG]
     L.gf_backward_workspace_bytes.restype = c_size_t
     L.gf_forward_bin.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_size_t, _P]
+    L.gf_forward_emit.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, c_int64, c_int64, _P, c_size_t, _P]
     L.gf_forward_render.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P,
-                                    c_int64, c_int64, _P, _P, c_size_t, _P]
+                                    c_int64, _P, _P, c_size_t, _P]
     L.gf_backward.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int32,
                               _P, c_int32, c_int64, _P, _P, _P, _P, c_size_t, _P]
+    L.gf_backward_reduce.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int32,
+                                     _P, c_int32, c_int64, _P, c_size_t, _P]
+    L.gf_backward_finish.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_size_t, _P]
     L.gf_read_status.argtypes = [_P, c_int32, POINTER(c_uint32), _P]
     L.gf_selftest_softplus.argtypes = [POINTER(c_uint64), _P]
-    for name in ("gf_tile_grid", "gf_forward_bin", "gf_forward_render", "gf_backward",
-                 "gf_read_status", "gf_selftest_softplus"):
+    for name in ("gf_tile_grid", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
+                 "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
+                 "gf_selftest_softplus"):
         getattr(L, name).restype = c_int
     _LIB = L
     return L

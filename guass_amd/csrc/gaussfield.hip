@@ -1,21 +1,28 @@
 // gaussfield.hip - gfx950 kernels and C ABI of libgaussfield.so.
 //
-// Forward (reference forward.cu:372-569):
-//   k_bin     one workgroup per problem: per-Gaussian geometry, sigma-box tile rectangles
-//             (bit-exact with the CPU path), exclusive scan of tiles touched per Gaussian
-//             ("point offsets"), per-tile Gaussian counts from row-wise difference arrays in
-//             LDS, exclusive scan of the counts -> tile_ptr.  No global atomics, no host sync.
-//   k_emit    one thread per (gaussian, tile) pair: finds its Gaussian by binary search of the
-//             point offsets, claims a slot in its tile's range (a counting sort on the tile key:
-//             one 64-bit atomic per pair on a per-tile cursor) and stores the gaussian id.
-//   k_render  one workgroup per tile: puts the tile's ids in canonical (ascending gid) order in
-//             LDS and writes them back, stages the tile's Gaussians in LDS and evaluates every
-//             pixel of the tile, writing delta-W with row-coalesced stores.  Empty tiles get 0.
-// Backward (reference backward.cu:541-716), one kernel:
-//   k_bwd_tiles one workgroup per tile: geometry of the tile's Gaussians in LDS, six
-//               per-Gaussian pixel sums reduced across the workgroup, one atomic per
-//               (Gaussian, tile, sum); the last workgroup to finish applies the chain rule to
-//               (mu, chol_raw, amp) and clears the accumulators for the next call.
+// Forward (reference forward.cu:372-569), three kernels:
+//   k_bin      one workgroup per field: bit-exact sigma-box tile rectangle of every Gaussian,
+//              exclusive scan of the tiles each touches ("point offsets"), per-tile Gaussian
+//              counts from row-wise difference arrays, and their scan -> tile_ptr; every scan
+//              runs in LDS and global memory is only written, coalesced.
+//   k_emit     one thread per (gaussian, tile) pair: the pair's Gaussian from a 64-ary ballot
+//              search plus an LDS binary search over the point offsets, then a slot in its
+//              tile's range from a per-tile cursor (a counting sort on the tile key).
+//   k_render16 one wave per 16x16 tile, four independent tiles per workgroup, no workgroup
+//              barriers: canonical (ascending gid) order of the tile's ids (written back),
+//              per-Gaussian constants computed one Gaussian per lane and broadcast with
+//              readlane, 4 pixels per lane with per-row terms hoisted.
+//   (k_render_any handles other tile shapes.)
+// Backward (reference backward.cu:541-716), two kernels:
+//   k_bwd16    one wave per 16x16 tile: lanes are (Gaussian slot, tile row); each lane sums
+//              16 pixels of its row for its Gaussian into six moments, a 16-lane butterfly
+//              reduces them, and one atomic per (Gaussian, tile, moment) accumulates them.
+//   k_bwd_finish  per Gaussian: chain rule from the six moments to (mu, chol_raw, amp), in
+//              double, then clears the accumulators so the workspace stays zeroed.
+//   (k_bwd_any handles other tile shapes.)
+// The quadratic form of a pixel is evaluated in whitened form, q = |R d|^2 with R the inverse
+// of the exact Cholesky factor of the fp32 covariance: its fp32 rounding error grows like
+// sqrt(cond) instead of cond, which matters for strongly anisotropic Gaussians.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -27,17 +34,22 @@
 #include "../../include/gaussfield.h"
 #include "geometry.h"
 
-#define GF_VERSION "gaussfield-mi355x 0.1.0"
+#define GF_VERSION "gaussfield-mi355x 0.2.0"
 
 namespace {
 
 constexpr int kBinThreads = 1024;
 constexpr int kTileThreads = 256;
 constexpr int kEmitThreads = 256;
-constexpr int kLdsDiffWords = 12288;   // 48 KiB row-difference band in k_bin
-constexpr int kSortLdsKeys = 2048;     // segments up to this length are ordered in LDS
-constexpr int kBitmapMaxK = 131072;    // longer segments use a K-bit bitmap when K fits
-constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kLdsDiffWords = 12288;  // 48 KiB row-difference band in k_bin
+constexpr int kBinMaxBandRows = 1024; // row totals kept in LDS per band in k_bin
+constexpr int kSortLdsKeys = 2048;    // (any-shape kernels) segments up to this length in LDS
+constexpr int kBitmapMaxK = 131072;   // (any-shape kernels) longer segments: K-bit bitmap
+constexpr int kSortLdsWords = (kSortLdsKeys > kBitmapMaxK / 32) ? kSortLdsKeys : kBitmapMaxK / 32;
+constexpr int kWaveSortKeys = 512;    // (16x16 kernels) per-wave LDS keys / bitmap words
+// exp(-q/2) = 2^(q * kHalfLog2e); the clamp q in [0, clamp] maps to [clamp * kHalfLog2e, 0].
+constexpr float kHalfLog2e = -0.72134752044448170368f;
+constexpr double kSqrtHalfLog2e = 0.84932180028801904272;  // sqrt(-kHalfLog2e)
 
 thread_local char g_err[1024];
 
@@ -64,40 +76,40 @@ int set_err(int code, const char* fmt, ...) {
   } while (0)
 
 // ------------------------------------------------------------------------------------------
-// Problem description (passed by value as a kernel argument).
+// Problem description (passed by value as a kernel argument).  Sizes are < 2^31 (checked).
 struct Problem {
-  int64_t M, N, K;
-  int64_t tile_out, tile_in;
-  int64_t R, C;  // tile rows / cols
+  int64_t K;
+  int32_t M, N;
+  int32_t tile_out, tile_in;
+  int32_t R, C;  // tile rows / cols
   float sigma;
-  float clamp_quad;
+  float q_lo, q_hi;  // clamp range of the scaled quadratic form q * kHalfLog2e
   int32_t normalize;
-  int32_t has_clamp;
 };
 
-// Render geometry of one Gaussian in fp32 (32 bytes).
-struct __align__(16) GeomF {
-  float mu0, mu1, i00, i01, i11, norm, det, pad;
+// Per-Gaussian constants of the tile kernels: with dx = x - mu0, dy = y - mu1,
+//   a = wa dx,  z = wb dx + wc dy,  q' = -(a^2 + z^2) = kHalfLog2e * (d^T cov^-1 d),
+//   basis = 2^clamp(q') = exp(-q/2).
+struct __align__(16) GaussEval {
+  float mu0, mu1, wa, wb, wc, w;  // w = amp * norm
+  float pad0, pad1;
 };
 
-// Header of every workspace.
 struct WsHeader {
   uint32_t status;
-  uint32_t ticket;
-  uint32_t pad[62];
+  uint32_t pad[63];
 };
 static_assert(sizeof(WsHeader) == 256, "workspace header must be 256 bytes");
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// Forward workspace: header, rect[K] (int4 tile ranges), point offsets[K+1], cursor[T].
 struct FwdLayout {
-  size_t geo, rect, offs, cursor, total;
+  size_t rect, offs, cursor, total;
 };
 FwdLayout fwd_layout(int64_t K, int64_t T) {
   FwdLayout L;
   size_t o = sizeof(WsHeader);
-  L.geo = o;
-  o = align256(o + sizeof(GeomF) * (size_t)K);
   L.rect = o;
   o = align256(o + sizeof(int4) * (size_t)K);
   L.offs = o;
@@ -109,8 +121,8 @@ FwdLayout fwd_layout(int64_t K, int64_t T) {
 }
 
 // Backward workspace: header + eight fp32 accumulators per Gaussian.  It must be zero before
-// the first backward; every backward leaves it zero again (the last workgroup clears what it
-// consumed), so a workspace kept across calls is zeroed once.
+// the first backward; every backward leaves it zero again (k_bwd_finish clears what it reads),
+// so a workspace kept across calls is zeroed once.
 struct BwdLayout {
   size_t acc, total;
 };
@@ -125,23 +137,92 @@ BwdLayout bwd_layout(int64_t K) {
 
 __device__ inline void set_status(uint32_t* status, uint32_t bit) { atomicOr(status, bit); }
 
-// Render geometry + bit-exact rectangle of Gaussian g.
-__device__ inline void gaussian_geometry(const Problem& p, const float* __restrict__ mu,
-                                         const float* __restrict__ chol_raw, int64_t g, GeomF* geo,
-                                         GfRect* rect) {
+__device__ inline int32_t clamp_i32(int32_t v, int32_t lo, int32_t hi) {
+  return v < lo ? lo : (v > hi ? hi : v);
+}
+
+// Bit-exact tile rectangle of Gaussian g (same fp32 operation sequence as gf_tile_rect, with
+// the row/column indices, already clamped into [0, M-1], divided in 32-bit integers).
+__device__ inline int4 bin_rect(const Problem& p, const float* __restrict__ mu,
+                                const float* __restrict__ chol_raw, int64_t g, int32_t* touched) {
+#pragma clang fp contract(off)
   const float mu0 = mu[2 * g + 0], mu1 = mu[2 * g + 1];
   const GfChol L = gf_activate_cholesky(chol_raw[3 * g + 0], chol_raw[3 * g + 1], chol_raw[3 * g + 2]);
-  const GfCov cov = gf_cov_from_chol(L);
-  if (rect) *rect = gf_tile_rect(mu0, mu1, cov, p.M, p.N, p.tile_out, p.tile_in, p.R, p.C, p.sigma);
-  const GfRenderGeom rg = gf_render_geom(cov, p.normalize);
-  geo->mu0 = mu0;
-  geo->mu1 = mu1;
-  geo->i00 = (float)rg.i00;
-  geo->i01 = (float)rg.i01;
-  geo->i11 = (float)rg.i11;
-  geo->norm = rg.norm;
-  geo->det = rg.det_f;
-  geo->pad = 0.0f;
+  const GfCov c = gf_cov_from_chol(L);
+  const float std_r = gf_sqrt_rn(gf_clamp_min_nan(c.s00, GF_COV_FLOOR));
+  const float std_c = gf_sqrt_rn(gf_clamp_min_nan(c.s11, GF_COV_FLOOR));
+  const float centre_r = ((mu0 + 1.0f) * 0.5f) * (float)(p.M - 1);
+  const float centre_c = ((mu1 + 1.0f) * 0.5f) * (float)(p.N - 1);
+  const float half_r = ((p.sigma * std_r) * 0.5f) * (float)(p.M - 1 > 1 ? p.M - 1 : 1);
+  const float half_c = ((p.sigma * std_c) * 0.5f) * (float)(p.N - 1 > 1 ? p.N - 1 : 1);
+  const int32_t row_lo = (int32_t)gf_clamp_i64(gf_f32_to_i64_torch(__builtin_floorf(centre_r - half_r)), 0, p.M - 1);
+  const int32_t row_hi = (int32_t)gf_clamp_i64(gf_f32_to_i64_torch(__builtin_ceilf(centre_r + half_r)), 0, p.M - 1);
+  const int32_t col_lo = (int32_t)gf_clamp_i64(gf_f32_to_i64_torch(__builtin_floorf(centre_c - half_c)), 0, p.N - 1);
+  const int32_t col_hi = (int32_t)gf_clamp_i64(gf_f32_to_i64_torch(__builtin_ceilf(centre_c + half_c)), 0, p.N - 1);
+  int4 r;
+  r.x = clamp_i32(row_lo / p.tile_out, 0, p.R - 1);
+  r.y = clamp_i32(row_hi / p.tile_out, 0, p.R - 1);
+  r.z = clamp_i32(col_lo / p.tile_in, 0, p.C - 1);
+  r.w = clamp_i32(col_hi / p.tile_in, 0, p.C - 1);
+  *touched = (r.y - r.x + 1) * (r.w - r.z + 1);
+  return r;
+}
+
+// Evaluation constants of Gaussian g: the Cholesky factor L' of the fp32 covariance and
+// R = L'^-1 in double (R^T R = cov^-1), scaled by sqrt(log2(e)/2) and rounded once.
+__device__ inline GaussEval eval_geom(const Problem& p, const float* __restrict__ mu,
+                                      const float* __restrict__ chol_raw,
+                                      const float* __restrict__ amp, int64_t g) {
+  const GfChol L = gf_activate_cholesky(chol_raw[3 * g + 0], chol_raw[3 * g + 1], chol_raw[3 * g + 2]);
+  const GfCov c = gf_cov_from_chol(L);
+  const double a = (double)c.s00, b = (double)c.s01, d = (double)c.s11;
+  double det = a * d - b * b;  // exact products, one rounding
+  if (!(det > 0.0)) det = 1e-300;  // singular fp32 covariance: a (numerically) degenerate line
+  const double l11 = sqrt(a);
+  const double r00 = 1.0 / l11;
+  const double r11 = sqrt(a / det);       // 1 / l22 with l22 = sqrt(det / a)
+  const double r10 = -(b / a) * r11;      // -l21 / (l11 l22)
+  GaussEval v;
+  v.mu0 = mu[2 * g + 0];
+  v.mu1 = mu[2 * g + 1];
+  v.wa = (float)(kSqrtHalfLog2e * r00);
+  v.wb = (float)(kSqrtHalfLog2e * r10);
+  v.wc = (float)(kSqrtHalfLog2e * r11);
+  if (amp) {
+    float norm = 1.0f;
+    if (p.normalize) {
+#pragma clang fp contract(off)
+      const float sq = gf_sqrt_rn((float)det);
+      norm = gf_div_f32(1.0f, GF_TWO_PI_F32 * (sq < GF_FLT_EPS ? GF_FLT_EPS : sq));
+    }
+    v.w = amp[g] * norm;
+  } else {
+    v.w = 0.0f;
+  }
+  v.pad0 = v.pad1 = 0.0f;
+  return v;
+}
+
+__device__ inline GaussEval zero_eval() {
+  GaussEval v;
+  v.mu0 = v.mu1 = v.wa = v.wb = v.wc = v.w = v.pad0 = v.pad1 = 0.0f;
+  return v;
+}
+
+// 2^clamp(q'), q' = -(A + z^2).
+__device__ inline float basis_w(const Problem& p, float A, float z) {
+  const float q = -fmaf(z, z, A);
+  return __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(q, p.q_lo, p.q_hi));
+}
+
+__device__ inline float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Orders the memory operations of one wave (its lanes exchange data through LDS / global).
+__device__ inline void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  __builtin_amdgcn_wave_barrier();
 }
 
 // ------------------------------------------------------------------------------------------
@@ -202,83 +283,142 @@ __device__ int64_t block_scan_runs(int64_t* data, int64_t n, int64_t* lds) {
 // ------------------------------------------------------------------------------------------
 // k_bin: one workgroup.
 
+__device__ inline int32_t wave_inclusive_scan32(int32_t x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int32_t y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// Exclusive scan of the int32 values lds[0..n) by the workgroup (each thread owns a contiguous
+// run), written to out[0..n) as int64; returns the total.
+__device__ int64_t bin_scan_lds_to_global(const int32_t* lds, int64_t n, int64_t* out, int64_t* scan_lds) {
+  const int64_t per = (n + kBinThreads - 1) / kBinThreads;
+  const int64_t b = (int64_t)threadIdx.x * per;
+  const int64_t e = b + per < n ? b + per : n;
+  int64_t s = 0;
+  for (int64_t i = b; i < e; ++i) s += lds[i];
+  int64_t total;
+  int64_t run = block_exclusive_scan<kBinThreads>(s, &total, scan_lds);
+  for (int64_t i = b; i < e; ++i) {
+    out[i] = run;
+    run += lds[i];
+  }
+  return total;
+}
+
 __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __restrict__ mu,
                                                      const float* __restrict__ chol_raw,
                                                      int64_t* __restrict__ tile_ptr,
                                                      int64_t* __restrict__ num_pairs, uint8_t* ws,
                                                      FwdLayout L) {
-  __shared__ int32_t diff[kLdsDiffWords];
+  __shared__ int32_t lds[kLdsDiffWords];
+  __shared__ int64_t rowbase[kBinMaxBandRows + 1];
   __shared__ int64_t scan_lds[kBinThreads / 64 + 1];
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
-  GeomF* geo = reinterpret_cast<GeomF*>(ws + L.geo);
   int4* rect = reinterpret_cast<int4*>(ws + L.rect);
   int64_t* offs = reinterpret_cast<int64_t*>(ws + L.offs);
   int64_t* cursor = reinterpret_cast<int64_t*>(ws + L.cursor);
-  const int64_t K = p.K, T = p.R * p.C;
-  if (threadIdx.x == 0) {
-    hdr->status = 0u;
-    hdr->ticket = 0u;
-  }
+  const int64_t K = p.K, T = (int64_t)p.R * p.C;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (threadIdx.x == 0) hdr->status = 0u;
 
-  // A: geometry, rectangles, tiles touched.
+  // A: rectangles and tiles touched (touched counts in LDS when they fit).
+  const bool k_in_lds = K <= kLdsDiffWords;
   for (int64_t g = threadIdx.x; g < K; g += kBinThreads) {
-    GeomF gf;
-    GfRect r;
-    gaussian_geometry(p, mu, chol_raw, g, &gf, &r);
-    geo[g] = gf;
-    rect[g] = make_int4((int)r.r0, (int)r.r1, (int)r.c0, (int)r.c1);
-    offs[g] = (r.r1 - r.r0 + 1) * (r.c1 - r.c0 + 1);
+    int32_t touched;
+    rect[g] = bin_rect(p, mu, chol_raw, g, &touched);
+    if (k_in_lds) lds[g] = touched;
+    else offs[g] = touched;
   }
   __syncthreads();
 
   // B: point offsets (exclusive scan of tiles touched); offs[K] = P.
-  const int64_t P = block_scan_runs<kBinThreads>(offs, K, scan_lds);
+  const int64_t P = k_in_lds ? bin_scan_lds_to_global(lds, K, offs, scan_lds)
+                             : block_scan_runs<kBinThreads>(offs, K, scan_lds);
   if (threadIdx.x == 0) offs[K] = P;
+  __syncthreads();
 
-  // C: per-tile counts, band by band.  A band covers rows [b0, b0+nb) and columns
-  // [cb0, cb0+W) of the tile grid; each covered row of each rectangle adds +1 at its first
-  // column and -1 after its last, and a row scan turns the differences into counts.
-  const int64_t W = p.C < kLdsDiffWords ? p.C : kLdsDiffWords;
-  const int64_t band_rows = kLdsDiffWords / W;
-  for (int64_t cb0 = 0; cb0 < p.C; cb0 += W) {
-    const int64_t wb = (p.C - cb0) < W ? (p.C - cb0) : W;
+  // C: per-tile counts and tile_ptr, band by band of whole tile rows.  Each covered row of each
+  // rectangle adds +1 at its first column and -1 after its last; one wave per row turns the
+  // differences into counts (inclusive scan) and the counts into row offsets (exclusive
+  // scan), the row totals are scanned, and tile_ptr / cursor are written coalesced.
+  int64_t Pc = 0;
+  if (p.C <= kLdsDiffWords && K * p.C < (int64_t)INT32_MAX) {
+    const int64_t C = p.C;
+    int64_t band_rows = kLdsDiffWords / C;
+    if (band_rows > kBinMaxBandRows) band_rows = kBinMaxBandRows;
+    int64_t band_base = 0;
     for (int64_t b0 = 0; b0 < p.R; b0 += band_rows) {
       const int64_t nb = (p.R - b0) < band_rows ? (p.R - b0) : band_rows;
-      for (int64_t i = threadIdx.x; i < nb * wb; i += kBinThreads) diff[i] = 0;
+      for (int64_t i = threadIdx.x; i < nb * C; i += kBinThreads) lds[i] = 0;
       __syncthreads();
       for (int64_t g = threadIdx.x; g < K; g += kBinThreads) {
         const int4 r = rect[g];
         const int64_t rlo = r.x > b0 ? r.x : b0;
         const int64_t rhi = r.y < b0 + nb - 1 ? r.y : b0 + nb - 1;
-        const int64_t clo = r.z > cb0 ? r.z : cb0;
-        const int64_t chi = r.w < cb0 + wb - 1 ? r.w : cb0 + wb - 1;
-        if (rlo > rhi || clo > chi) continue;
         for (int64_t row = rlo; row <= rhi; ++row) {
-          int32_t* d = diff + (row - b0) * wb;
-          atomicAdd(d + (clo - cb0), 1);
-          if (chi + 1 < cb0 + wb) atomicAdd(d + (chi + 1 - cb0), -1);
+          int32_t* d = lds + (row - b0) * C;
+          atomicAdd(d + r.z, 1);
+          if (r.w + 1 < C) atomicAdd(d + r.w + 1, -1);
         }
       }
       __syncthreads();
-      // Row scans: one wave per row.
-      const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
       for (int64_t row = wid; row < nb; row += kBinThreads / 64) {
-        int64_t carry = 0;
-        for (int64_t j0 = 0; j0 < wb; j0 += 64) {
+        int32_t carry_d = 0, carry_c = 0;
+        for (int64_t j0 = 0; j0 < C; j0 += 64) {
           const int64_t j = j0 + lane;
-          const int64_t v = j < wb ? diff[row * wb + j] : 0;
-          const int64_t inc = wave_inclusive_scan(v) + carry;
-          if (j < wb) tile_ptr[(b0 + row) * p.C + cb0 + j] = inc;  // count of tile
-          carry = __shfl(inc, 63, 64);
+          const int32_t dv = j < C ? lds[row * C + j] : 0;
+          const int32_t cnt = wave_inclusive_scan32(dv) + carry_d;
+          const int32_t cnt_in = j < C ? cnt : 0;
+          const int32_t inc = wave_inclusive_scan32(cnt_in);
+          if (j < C) lds[row * C + j] = carry_c + inc - cnt_in;  // exclusive offset in the row
+          carry_d = __shfl(cnt, 63, 64);
+          carry_c += __shfl(inc, 63, 64);
         }
+        if (lane == 0) rowbase[row] = carry_c;  // row total (scanned below)
       }
+      __syncthreads();
+      if (wid == 0) {
+        int64_t carry = 0;
+        for (int64_t r0 = 0; r0 < nb; r0 += 64) {
+          const int64_t r = r0 + lane;
+          const int64_t v = r < nb ? rowbase[r] : 0;
+          const int64_t inc = wave_inclusive_scan(v);
+          if (r < nb) rowbase[r] = band_base + carry + inc - v;
+          carry += __shfl(inc, 63, 64);
+        }
+        if (lane == 0) rowbase[kBinMaxBandRows] = band_base + carry;
+      }
+      __syncthreads();
+      for (int64_t i = threadIdx.x; i < nb * C; i += kBinThreads) {
+        const int64_t row = i / C;
+        const int64_t v = rowbase[row] + lds[i];
+        tile_ptr[b0 * C + i] = v;
+        cursor[b0 * C + i] = v;
+      }
+      band_base = rowbase[kBinMaxBandRows];
       __syncthreads();
     }
+    Pc = band_base;
+  } else {
+    // Very wide tile grids (> kLdsDiffWords tile columns): counts through global memory.
+    for (int64_t i = threadIdx.x; i < T; i += kBinThreads) tile_ptr[i] = 0;
+    __syncthreads();
+    for (int64_t g = threadIdx.x; g < K; g += kBinThreads) {
+      const int4 r = rect[g];
+      for (int64_t row = r.x; row <= r.y; ++row)
+        for (int64_t col = r.z; col <= r.w; ++col)
+          atomicAdd(reinterpret_cast<unsigned long long*>(tile_ptr + row * p.C + col), 1ull);
+    }
+    __threadfence();
+    __syncthreads();
+    Pc = block_scan_runs<kBinThreads>(tile_ptr, T, scan_lds);
+    for (int64_t t = threadIdx.x; t < T; t += kBinThreads) cursor[t] = tile_ptr[t];
   }
-
-  // D: tile_ptr = exclusive scan of counts; cursors start at each tile's first slot.
-  const int64_t Pc = block_scan_runs<kBinThreads>(tile_ptr, T, scan_lds);
-  for (int64_t t = threadIdx.x; t < T; t += kBinThreads) cursor[t] = tile_ptr[t];
   if (threadIdx.x == 0) {
     tile_ptr[T] = Pc;
     *num_pairs = P;
@@ -287,34 +427,64 @@ __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __r
 }
 
 // ------------------------------------------------------------------------------------------
-// k_emit: one thread per pair (grid-stride).
+// k_emit: one thread per pair, 256 consecutive pairs per workgroup pass.
 
 __global__ __launch_bounds__(kEmitThreads) void k_emit(Problem p, uint8_t* ws, FwdLayout L,
                                                        int64_t* __restrict__ ids, int64_t capacity) {
+  __shared__ int64_t s_offs[kEmitThreads + 1];
+  __shared__ int64_t s_g0;
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   const int4* __restrict__ rect = reinterpret_cast<const int4*>(ws + L.rect);
   const int64_t* __restrict__ offs = reinterpret_cast<const int64_t*>(ws + L.offs);
   unsigned long long* cursor = reinterpret_cast<unsigned long long*>(ws + L.cursor);
   const int64_t K = p.K;
   const int64_t P = offs[K];
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t pi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; pi < P; pi += stride) {
-    // Largest g with offs[g] <= pi (offs strictly increasing: every Gaussian touches >= 1 tile).
-    int64_t lo = 0, hi = K - 1;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi + 1) >> 1;
-      if (offs[mid] <= pi) lo = mid; else hi = mid - 1;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  for (int64_t base = (int64_t)blockIdx.x * kEmitThreads; base < P;
+       base += (int64_t)gridDim.x * kEmitThreads) {
+    // Wave 0: largest g with offs[g] <= base, by 64-ary search (offs strictly increasing: every
+    // Gaussian touches >= 1 tile, so offs[0] = 0 <= base).
+    if (wid == 0) {
+      int64_t lo = 0, hi = K - 1;
+      while (hi - lo >= 64) {
+        const int64_t step = (hi - lo + 64) / 64;
+        const int64_t idx = lo + (int64_t)lane * step;
+        const bool le = idx <= hi && offs[idx] <= base;
+        const unsigned long long m = __ballot(le);
+        const int last = 63 - __clzll((long long)m);
+        lo = lo + (int64_t)last * step;
+        hi = (lo + step - 1) < hi ? (lo + step - 1) : hi;
+      }
+      const int64_t idx = lo + lane;
+      const bool le = idx <= hi && offs[idx] <= base;
+      const unsigned long long m = __ballot(le);
+      if (lane == 0) s_g0 = lo + (63 - __clzll((long long)m));
     }
-    const int64_t g = lo;
-    const int64_t local = pi - offs[g];
-    const int4 r = rect[g];
-    const int64_t w = (int64_t)(r.w - r.z + 1);
-    const int64_t tr = r.x + local / w;
-    const int64_t tc = r.z + local % w;
-    const int64_t t = tr * p.C + tc;
-    const unsigned long long pos = atomicAdd(cursor + t, 1ull);
-    if ((int64_t)pos < capacity) ids[pos] = g;
-    else set_status(&hdr->status, GF_STATUS_CAPACITY);
+    __syncthreads();
+    const int64_t g0 = s_g0;
+    // The pairs [base, base+256) belong to Gaussians g0 .. g0+255 (each has >= 1 pair).
+    for (int i = threadIdx.x; i <= kEmitThreads; i += kEmitThreads)
+      s_offs[i] = (g0 + i <= K) ? offs[g0 + i] : INT64_MAX;
+    __syncthreads();
+    const int64_t pi = base + threadIdx.x;
+    if (pi < P) {
+      int lo = 0, hi = kEmitThreads - 1;  // largest i with s_offs[i] <= pi
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_offs[mid] <= pi) lo = mid; else hi = mid - 1;
+      }
+      const int64_t g = g0 + lo;
+      const int32_t local = (int32_t)(pi - s_offs[lo]);
+      const int4 r = rect[g];
+      const int32_t w = r.w - r.z + 1;
+      const int32_t tr = r.x + local / w;
+      const int32_t tc = r.z + local % w;
+      const int64_t t = (int64_t)tr * p.C + tc;
+      const unsigned long long pos = atomicAdd(cursor + t, 1ull);
+      if ((int64_t)pos < capacity) ids[pos] = g;
+      else set_status(&hdr->status, GF_STATUS_CAPACITY);
+    }
+    __syncthreads();
   }
 }
 
@@ -323,8 +493,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(Problem p, uint8_t* ws, F
 
 // Ascending bitonic sort by one workgroup, "flip" form: the first step of every merge stage
 // pairs i with its mirror i ^ (k-1), later steps pair i with i ^ j, and the smaller key always
-// goes to the lower index.  Indices >= n behave as +infinity and are never touched, so no
-// padding is stored.
+// goes to the lower index.  Indices >= n behave as +infinity and are never touched.
 template <typename Key>
 __device__ void bitonic_sort_ascending(Key* keys, int64_t n) {
   int64_t np = 1;
@@ -347,10 +516,26 @@ __device__ void bitonic_sort_ascending(Key* keys, int64_t n) {
   }
 }
 
-// Orders seg[0..n) ascending.  lds_words: LDS scratch (>= max(kSortLdsKeys, K/32) int32).
-__device__ void sort_segment(int64_t* seg, int64_t n, int64_t K, int32_t* lds, int64_t* lds_small,
-                             uint32_t* status) {
-  if (n <= 1) return;
+// Orders seg[0..n) ascending (ids are distinct values in [0, K)).  On return, if
+// n <= kSortLdsKeys, lds[0..n) also holds the ordered ids.  Must be called by the whole
+// workgroup; ends with a barrier.
+__device__ void order_segment(int64_t* seg, int64_t n, int64_t K, int32_t* lds, int64_t* lds_small,
+                              uint32_t* status) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (n <= 64) {
+    // Rank sort in wave 0: each lane counts the keys smaller than its own.
+    if (wid == 0) {
+      const int32_t key = lane < n ? (int32_t)seg[lane] : INT32_MAX;
+      int rank = 0;
+      for (int j = 0; j < (int)n; ++j) rank += (__shfl(key, j, 64) < key) ? 1 : 0;
+      if (lane < n) {
+        seg[rank] = key;
+        lds[rank] = key;
+      }
+    }
+    __syncthreads();
+    return;
+  }
   if (n <= kSortLdsKeys) {
     for (int64_t i = threadIdx.x; i < n; i += blockDim.x) lds[i] = (int32_t)seg[i];
     __syncthreads();
@@ -360,7 +545,7 @@ __device__ void sort_segment(int64_t* seg, int64_t n, int64_t K, int32_t* lds, i
     return;
   }
   if (K <= kBitmapMaxK) {
-    // Distinct ids in [0, K): set bits, scan popcounts, expand in order.
+    // Set one bit per id, scan the popcounts, expand in order.
     const int64_t words = (K + 31) >> 5;
     uint32_t* bits = reinterpret_cast<uint32_t*>(lds);
     for (int64_t i = threadIdx.x; i < words; i += blockDim.x) bits[i] = 0u;
@@ -371,7 +556,6 @@ __device__ void sort_segment(int64_t* seg, int64_t n, int64_t K, int32_t* lds, i
       else set_status(status, GF_STATUS_COUNT_MISMATCH);
     }
     __syncthreads();
-    // Each thread owns a contiguous run of words.
     const int64_t per = (words + blockDim.x - 1) / blockDim.x;
     const int64_t wb = (int64_t)threadIdx.x * per;
     const int64_t we = wb + per < words ? wb + per : words;
@@ -379,9 +563,7 @@ __device__ void sort_segment(int64_t* seg, int64_t n, int64_t K, int32_t* lds, i
     for (int64_t w = wb; w < we; ++w) cnt += __popc(bits[w]);
     int64_t total;
     int64_t pos = block_exclusive_scan<kTileThreads>(cnt, &total, lds_small);
-    if (total != n) {
-      if (threadIdx.x == 0) set_status(status, GF_STATUS_COUNT_MISMATCH);
-    }
+    if (total != n && threadIdx.x == 0) set_status(status, GF_STATUS_COUNT_MISMATCH);
     for (int64_t w = wb; w < we; ++w) {
       uint32_t m = bits[w];
       while (m) {
@@ -397,80 +579,368 @@ __device__ void sort_segment(int64_t* seg, int64_t n, int64_t K, int32_t* lds, i
   bitonic_sort_ascending<int64_t>(seg, n);
 }
 
+// Orders seg[0..n) ascending with one wave (ids are distinct values in [0, K)); keys is the
+// wave's private LDS region of kWaveSortKeys int32.  On return keys[0..n) holds the ordered ids
+// if n <= kWaveSortKeys.  No workgroup barriers: other waves of the workgroup are unaffected.
+__device__ void order_segment_wave(int64_t* seg, int64_t n, int64_t K, int32_t* keys,
+                                   uint32_t* status) {
+  const int lane = threadIdx.x & 63;
+  if (n <= 64) {
+    // Rank sort: each lane counts the keys smaller than its own (keys broadcast by readlane).
+    const int32_t key = lane < n ? (int32_t)seg[lane] : INT32_MAX;
+    int rank = 0;
+    for (int j = 0; j < (int)n; ++j) rank += (__builtin_amdgcn_readlane(key, j) < key) ? 1 : 0;
+    if (lane < n) {
+      keys[rank] = key;
+      if (rank != lane) seg[rank] = key;
+    }
+    wave_sync();
+    return;
+  }
+  if (n <= kWaveSortKeys) {
+    for (int64_t i = lane; i < n; i += 64) keys[i] = (int32_t)seg[i];
+    wave_sync();
+    int64_t np = 1;
+    while (np < n) np <<= 1;
+    for (int64_t k = 2; k <= np; k <<= 1) {
+      for (int64_t j = k >> 1; j > 0; j >>= 1) {
+        const int64_t flip = (j == (k >> 1)) ? (k - 1) : j;
+        for (int64_t i = lane; i < n; i += 64) {
+          const int64_t partner = i ^ flip;
+          if (partner > i && partner < n) {
+            const int32_t a = keys[i], b = keys[partner];
+            if (a > b) {
+              keys[i] = b;
+              keys[partner] = a;
+            }
+          }
+        }
+        wave_sync();
+      }
+    }
+    for (int64_t i = lane; i < n; i += 64) seg[i] = keys[i];
+    wave_sync();
+    return;
+  }
+  if (K <= (int64_t)kWaveSortKeys * 32) {
+    // One bit per id in LDS, popcount scan, in-order expansion.
+    const int64_t words = (K + 31) >> 5;
+    uint32_t* bits = reinterpret_cast<uint32_t*>(keys);
+    for (int64_t i = lane; i < words; i += 64) bits[i] = 0u;
+    wave_sync();
+    for (int64_t i = lane; i < n; i += 64) {
+      const int64_t g = seg[i];
+      if (g >= 0 && g < K) atomicOr(bits + (g >> 5), 1u << (g & 31));
+      else set_status(status, GF_STATUS_COUNT_MISMATCH);
+    }
+    wave_sync();
+    const int64_t per = (words + 63) / 64;
+    const int64_t wb = (int64_t)lane * per;
+    const int64_t we = wb + per < words ? wb + per : words;
+    int64_t cnt = 0;
+    for (int64_t w = wb; w < we; ++w) cnt += __popc(bits[w]);
+    int64_t pos = wave_inclusive_scan(cnt) - cnt;
+    for (int64_t w = wb; w < we; ++w) {
+      uint32_t m = bits[w];
+      while (m) {
+        const int b = __ffs(m) - 1;
+        m &= m - 1;
+        if (pos < n) seg[pos] = (w << 5) + b;
+        ++pos;
+      }
+    }
+    wave_sync();
+    return;
+  }
+  // In place in global memory (segments longer than kWaveSortKeys with K > 16384).
+  int64_t np = 1;
+  while (np < n) np <<= 1;
+  for (int64_t k = 2; k <= np; k <<= 1) {
+    for (int64_t j = k >> 1; j > 0; j >>= 1) {
+      const int64_t flip = (j == (k >> 1)) ? (k - 1) : j;
+      for (int64_t i = lane; i < n; i += 64) {
+        const int64_t partner = i ^ flip;
+        if (partner > i && partner < n) {
+          const int64_t a = seg[i], b = seg[partner];
+          if (a > b) {
+            seg[i] = b;
+            seg[partner] = a;
+          }
+        }
+      }
+      wave_sync();
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------------
-// k_render: one workgroup per tile.
+// Forward render.
 
-struct __align__(16) GaussLds {
-  float mu0, mu1, i00, i01, i11, w;  // w = amp * norm
-  float pad0, pad1;
-};
+__device__ inline void tile_range(const int64_t* __restrict__ tile_ptr, int64_t t, int64_t capacity,
+                                  int64_t* s, int64_t* n) {
+  int64_t a = tile_ptr[t], b = tile_ptr[t + 1];
+  if (b > capacity) b = capacity;
+  if (a > b) a = b;
+  *s = a;
+  *n = b - a;
+}
 
-__global__ __launch_bounds__(kTileThreads) void k_render(
+// 16x16 tiles, one wave per tile (tile blockIdx.x * 4 + wave).  Lane l covers tile row l/4,
+// columns 4*(l%4)..+3.  Gaussian constants are computed one per lane for up to 64 Gaussians at
+// a time and broadcast with readlane while every lane accumulates its 4 pixels.
+__global__ __launch_bounds__(kTileThreads) void k_render16(
     Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
-    const float* __restrict__ amp, const int64_t* __restrict__ tile_ptr, int64_t* ids,
-    int64_t capacity, float* __restrict__ delta, uint8_t* ws, FwdLayout L) {
-  __shared__ int32_t sort_lds[(kSortLdsKeys > kBitmapMaxK / 32) ? kSortLdsKeys : kBitmapMaxK / 32];
-  __shared__ int64_t small_lds[kTileThreads / 64 + 1];
-  __shared__ GaussLds gl[kTileThreads];
+    const float* __restrict__ mu, const float* __restrict__ chol_raw, const float* __restrict__ amp,
+    const int64_t* __restrict__ tile_ptr, int64_t* ids, int64_t capacity, float* __restrict__ delta,
+    uint8_t* ws) {
+  __shared__ int32_t wkeys[kTileThreads / 64][kWaveSortKeys];
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
-  const GeomF* __restrict__ geo = reinterpret_cast<const GeomF*>(ws + L.geo);
-  const int64_t t = blockIdx.x;
-  const int64_t tr = t / p.C, tc = t % p.C;
-  int64_t s = tile_ptr[t], e = tile_ptr[t + 1];
-  if (e > capacity) e = capacity;
-  if (s > e) s = e;
-  const int64_t n = e - s;
-  int64_t* seg = ids + s;
-  sort_segment(seg, n, p.K, sort_lds, small_lds, &hdr->status);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * (kTileThreads / 64) + wid;
+  if (t >= (int64_t)p.R * p.C) return;
+  const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (t / p.C) * p.C);
+  const int32_t pr = tr * 16 + (lane >> 2), pc = tc * 16 + ((lane & 3) << 2);
+  int64_t s, n;
+  tile_range(tile_ptr, t, capacity, &s, &n);
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  if (n > 0) {
+    int64_t* seg = ids + s;
+    int32_t* keys = wkeys[wid];
+    order_segment_wave(seg, n, p.K, keys, &hdr->status);
+    const float x = row_coords[min(pr, p.M - 1)];
+    float y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = col_coords[min(pc + i, p.N - 1)];
+    for (int64_t j0 = 0; j0 < n; j0 += 64) {
+      const int nj = (int)((n - j0) < 64 ? (n - j0) : 64);
+      GaussEval my = zero_eval();
+      if (lane < nj) {
+        const int64_t g = (n <= kWaveSortKeys) ? (int64_t)keys[j0 + lane] : seg[j0 + lane];
+        if (g >= 0 && g < p.K) my = eval_geom(p, mu, chol_raw, amp, g);
+        else set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);  // internal mismatch only
+      }
+      for (int j = 0; j < nj; ++j) {
+        const float mu0 = readlane_f(my.mu0, j), mu1 = readlane_f(my.mu1, j);
+        const float wa = readlane_f(my.wa, j), wb = readlane_f(my.wb, j);
+        const float wc = readlane_f(my.wc, j), w = readlane_f(my.w, j);
+        const float dx = x - mu0;
+        const float a = wa * dx;
+        const float A = a * a;
+        const float b = wb * dx;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float z = fmaf(wc, y[i] - mu1, b);
+          acc[i] = fmaf(w, basis_w(p, A, z), acc[i]);
+        }
+      }
+    }
+  }
+  if (pr < p.M) {
+    float* out = delta + (int64_t)pr * p.N + pc;
+    if (pc + 3 < p.N && ((reinterpret_cast<uintptr_t>(out) & 15) == 0)) {
+      *reinterpret_cast<float4*>(out) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (pc + i < p.N) out[i] = acc[i];
+    }
+  }
+}
 
-  const int64_t r0 = tr * p.tile_out, c0 = tc * p.tile_in;
-  const int64_t r1 = (r0 + p.tile_out) < p.M ? (r0 + p.tile_out) : p.M;
-  const int64_t c1 = (c0 + p.tile_in) < p.N ? (c0 + p.tile_in) : p.N;
-  const int64_t w = c1 - c0;
-  const int64_t npx = (r1 - r0) * w;
-  for (int64_t px0 = 0; px0 < npx; px0 += kTileThreads) {
-    const int64_t px = px0 + threadIdx.x;
+// Any tile shape: each thread evaluates pixels p = tid, tid+256, ... of the tile.
+__global__ __launch_bounds__(kTileThreads) void k_render_any(
+    Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
+    const float* __restrict__ mu, const float* __restrict__ chol_raw, const float* __restrict__ amp,
+    const int64_t* __restrict__ tile_ptr, int64_t* ids, int64_t capacity, float* __restrict__ delta,
+    uint8_t* ws) {
+  __shared__ int32_t keys[kSortLdsWords];
+  __shared__ int64_t small_lds[kTileThreads / 64 + 1];
+  __shared__ GaussEval gl[kTileThreads];
+  WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
+  const int32_t t = blockIdx.x;
+  const int32_t tr = t / p.C, tc = t - (t / p.C) * p.C;
+  int64_t s, n;
+  tile_range(tile_ptr, t, capacity, &s, &n);
+  int64_t* seg = ids + s;
+  order_segment(seg, n, p.K, keys, small_lds, &hdr->status);
+  const bool keys_in_lds = n <= kSortLdsKeys;
+  const int32_t r0 = tr * p.tile_out, c0 = tc * p.tile_in;
+  const int32_t r1 = min(r0 + p.tile_out, p.M), c1 = min(c0 + p.tile_in, p.N);
+  const int32_t w = c1 - c0;
+  const int32_t npx = (r1 - r0) * w;
+  for (int32_t px0 = 0; px0 < npx; px0 += kTileThreads) {
+    const int32_t px = px0 + (int32_t)threadIdx.x;
     const bool have = px < npx;
-    const int64_t r = r0 + (have ? px / w : 0);
-    const int64_t c = c0 + (have ? px % w : 0);
+    const int32_t r = r0 + (have ? px / w : 0);
+    const int32_t c = c0 + (have ? px - (px / w) * w : 0);
     const float x = row_coords[r], y = col_coords[c];
     float acc = 0.0f;
     for (int64_t j0 = 0; j0 < n; j0 += kTileThreads) {
-      const int64_t nj = (n - j0) < kTileThreads ? (n - j0) : kTileThreads;
+      const int nj = (int)((n - j0) < kTileThreads ? (n - j0) : kTileThreads);
       __syncthreads();
-      if (threadIdx.x < nj) {
-        const int64_t g = seg[j0 + threadIdx.x];
-        GaussLds v;
+      if ((int)threadIdx.x < nj) {
+        const int64_t g = keys_in_lds ? (int64_t)keys[j0 + threadIdx.x] : seg[j0 + threadIdx.x];
         if (g >= 0 && g < p.K) {
-          const GeomF q = geo[g];
-          v.mu0 = q.mu0;
-          v.mu1 = q.mu1;
-          v.i00 = q.i00;
-          v.i01 = q.i01;
-          v.i11 = q.i11;
-          v.w = amp[g] * q.norm;
-        } else {  // only reachable after an internal count mismatch (status already flagged)
-          v.mu0 = v.mu1 = v.i00 = v.i01 = v.i11 = v.w = 0.0f;
+          gl[threadIdx.x] = eval_geom(p, mu, chol_raw, amp, g);
+        } else {
+          gl[threadIdx.x] = zero_eval();
           set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);
         }
-        v.pad0 = v.pad1 = 0.0f;
-        gl[threadIdx.x] = v;
       }
       __syncthreads();
-      for (int j = 0; j < (int)nj; ++j) {
-        const GaussLds v = gl[j];
+      for (int j = 0; j < nj; ++j) {
+        const GaussEval v = gl[j];
         const float dx = x - v.mu0, dy = y - v.mu1;
-        float q = (dx * v.i00 + dy * v.i01) * dx + (dx * v.i01 + dy * v.i11) * dy;
-        if (p.has_clamp) q = fminf(fmaxf(q, 0.0f), p.clamp_quad);
-        acc += v.w * expf(-0.5f * q);
+        const float a = v.wa * dx;
+        acc = fmaf(v.w, basis_w(p, a * a, fmaf(v.wc, dy, v.wb * dx)), acc);
       }
     }
-    if (have) delta[r * p.N + c] = acc;
+    if (have) delta[(int64_t)r * p.N + c] = acc;
   }
 }
 
 // ------------------------------------------------------------------------------------------
 // Backward.
+//
+// Six moments of one Gaussian over a set of pixels (e = basis without normalisation):
+//   S0 = sum g e, S1 = sum g e dx, S2 = sum g e dy, S3 = sum g e dx^2, S4 = sum g e dx dy,
+//   S5 = sum g e dy^2.
+// The reference zeroes the quadratic-form terms of pixels whose form is clamped (q > clamp or
+// q < 0); there e <= e^{-clamp/2} (4e-18 for clamp 80) or the pixel sits at the centre, so
+// those terms are below fp32 resolution of the sums and are kept.
+
+template <typename Idx>
+__device__ inline void backward_tile_checks(const Problem& p, const Idx* __restrict__ tile_ptr,
+                                            int64_t t, int64_t num_pairs, uint32_t* status,
+                                            int64_t* s_out, int64_t* n_out) {
+  const int64_t T = (int64_t)p.R * p.C;
+  int64_t s = (int64_t)tile_ptr[t], e = (int64_t)tile_ptr[t + 1];
+  if (threadIdx.x == 0) {
+    if (s < 0 || e < s || e > num_pairs) set_status(status, GF_STATUS_TILE_PTR_ORDER);
+    if (t == T - 1 && e != num_pairs) set_status(status, GF_STATUS_TILE_PTR_LAST);
+  }
+  if (s < 0) s = 0;
+  if (e > num_pairs) e = num_pairs;
+  *s_out = s;
+  *n_out = e > s ? e - s : 0;
+}
+
+// Loads Gaussians [j0, j0+nj) of the tile into LDS; invalid ids get gid -1.
+template <typename GIdx>
+__device__ inline void stage_gaussians(const Problem& p, const GIdx* __restrict__ gids, int64_t s,
+                                       int64_t j0, int nj, const float* __restrict__ mu,
+                                       const float* __restrict__ chol_raw, GaussEval* gl,
+                                       int32_t* gid_lds, uint32_t* status) {
+  if ((int)threadIdx.x < nj) {
+    const int64_t g = (int64_t)gids[s + j0 + threadIdx.x];
+    if (g < 0 || g >= p.K) {
+      set_status(status, g < 0 ? GF_STATUS_IDS_NEGATIVE : GF_STATUS_IDS_RANGE);
+      gid_lds[threadIdx.x] = -1;
+      gl[threadIdx.x] = zero_eval();
+    } else {
+      gl[threadIdx.x] = eval_geom(p, mu, chol_raw, nullptr, g);
+      gid_lds[threadIdx.x] = (int32_t)g;
+    }
+  }
+}
+
+// 16x16 tiles, one wave per tile (tile blockIdx.x * 4 + wave).  Lane l: slot = l/16, row =
+// l%16; per round the four slots take four Gaussians of the tile and each lane sums its row's
+// 16 pixels.  Gaussian constants are computed one per lane for up to 64 Gaussians at a time
+// and fetched by slot with a lane permute.
+template <typename TpIdx, typename GIdx>
+__global__ __launch_bounds__(kTileThreads) void k_bwd16(
+    Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
+    const float* __restrict__ col_coords, const float* __restrict__ mu,
+    const float* __restrict__ chol_raw, const TpIdx* __restrict__ tile_ptr,
+    const GIdx* __restrict__ gids, int64_t num_pairs, uint8_t* ws, BwdLayout L) {
+  WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
+  float* acc = reinterpret_cast<float*>(ws + L.acc);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * (kTileThreads / 64) + wid;
+  const int64_t T = (int64_t)p.R * p.C;
+  if (t >= T) return;
+  int64_t s = (int64_t)tile_ptr[t], e = (int64_t)tile_ptr[t + 1];
+  if (lane == 0) {
+    if (s < 0 || e < s || e > num_pairs) set_status(&hdr->status, GF_STATUS_TILE_PTR_ORDER);
+    if (t == T - 1 && e != num_pairs) set_status(&hdr->status, GF_STATUS_TILE_PTR_LAST);
+  }
+  if (s < 0) s = 0;
+  if (e > num_pairs) e = num_pairs;
+  const int64_t n = e > s ? e - s : 0;
+  if (n == 0) return;
+  const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (t / p.C) * p.C);
+  const int32_t r0 = tr * 16, c0 = tc * 16;
+  const int slot = lane >> 4, row = lane & 15;
+  const int32_t pr = r0 + row;
+  // this lane's row of dL/d(delta) (0 outside the matrix) and the tile's column coordinates
+  float gv[16], yv[16];
+  const float* grow = grad + (int64_t)min(pr, p.M - 1) * p.N + c0;
+  if (pr < p.M && c0 + 15 < p.N && ((reinterpret_cast<uintptr_t>(grow) & 15) == 0)) {
+#pragma unroll
+    for (int c = 0; c < 16; c += 4) {
+      const float4 g4 = *reinterpret_cast<const float4*>(grow + c);
+      gv[c] = g4.x;
+      gv[c + 1] = g4.y;
+      gv[c + 2] = g4.z;
+      gv[c + 3] = g4.w;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) gv[c] = (pr < p.M && c0 + c < p.N) ? grow[c] : 0.0f;
+  }
+#pragma unroll
+  for (int c = 0; c < 16; ++c) yv[c] = col_coords[min(c0 + c, p.N - 1)];
+  const float x = row_coords[min(pr, p.M - 1)];
+
+  for (int64_t j0 = 0; j0 < n; j0 += 64) {
+    const int nj = (int)((n - j0) < 64 ? (n - j0) : 64);
+    GaussEval my = zero_eval();
+    int32_t myg = -1;
+    if (lane < nj) {
+      const int64_t g = (int64_t)gids[s + j0 + lane];
+      if (g < 0 || g >= p.K) {
+        set_status(&hdr->status, g < 0 ? GF_STATUS_IDS_NEGATIVE : GF_STATUS_IDS_RANGE);
+      } else {
+        my = eval_geom(p, mu, chol_raw, nullptr, g);
+        myg = (int32_t)g;
+      }
+    }
+    for (int jb = 0; jb < nj; jb += 4) {
+      const int j = jb + slot;
+      const int src = j < nj ? j : 0;
+      const float mu0 = __shfl(my.mu0, src, 64), mu1 = __shfl(my.mu1, src, 64);
+      const float wa = __shfl(my.wa, src, 64), wb = __shfl(my.wb, src, 64);
+      const float wc = __shfl(my.wc, src, 64);
+      int32_t g = __shfl(myg, src, 64);
+      if (j >= nj) g = -1;
+      const float dx = x - mu0;
+      const float a = wa * dx;
+      const float A = a * a;
+      const float b = wb * dx;
+      float t0 = 0.f, t2 = 0.f, t3 = 0.f;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const float dy = yv[c] - mu1;
+        const float ge = gv[c] * basis_w(p, A, fmaf(wc, dy, b));
+        t0 += ge;
+        const float tt = ge * dy;
+        t2 += tt;
+        t3 = fmaf(tt, dy, t3);
+      }
+      float m[6] = {t0, dx * t0, t2, dx * dx * t0, dx * t2, t3};
+#pragma unroll
+      for (int k = 0; k < 6; ++k) {
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) m[k] += __shfl_xor(m[k], o, 16);
+      }
+      if (g >= 0 && row < 6) {
+        const float val = row == 0 ? m[0] : row == 1 ? m[1] : row == 2 ? m[2] : row == 3 ? m[3] : row == 4 ? m[4] : m[5];
+        unsafeAtomicAdd(acc + 8 * (int64_t)g + row, val);
+      }
+    }
+  }
+}
 
 __device__ inline float wave_sum(float v) {
 #pragma unroll
@@ -478,26 +948,91 @@ __device__ inline float wave_sum(float v) {
   return v;
 }
 
-template <typename Idx>
-__device__ inline int64_t load_idx(const void* p, int64_t i) {
-  return (int64_t)reinterpret_cast<const Idx*>(p)[i];
+// Any tile shape: per Gaussian, every thread sums its pixels, then a workgroup reduction.
+template <typename TpIdx, typename GIdx>
+__global__ __launch_bounds__(kTileThreads) void k_bwd_any(
+    Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
+    const float* __restrict__ col_coords, const float* __restrict__ mu,
+    const float* __restrict__ chol_raw, const TpIdx* __restrict__ tile_ptr,
+    const GIdx* __restrict__ gids, int64_t num_pairs, uint8_t* ws, BwdLayout L) {
+  __shared__ GaussEval gl[kTileThreads];
+  __shared__ int32_t gid_lds[kTileThreads];
+  __shared__ float red[kTileThreads / 64][8];
+  WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
+  float* acc = reinterpret_cast<float*>(ws + L.acc);
+  const int64_t t = blockIdx.x;
+  int64_t s, n;
+  backward_tile_checks<TpIdx>(p, tile_ptr, t, num_pairs, &hdr->status, &s, &n);
+  if (n == 0) return;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (t / p.C) * p.C);
+  const int32_t r0 = tr * p.tile_out, c0 = tc * p.tile_in;
+  const int32_t r1 = min(r0 + p.tile_out, p.M), c1 = min(c0 + p.tile_in, p.N);
+  const int32_t w = c1 - c0;
+  const int32_t npx = (r1 - r0) * w;
+  for (int64_t j0 = 0; j0 < n; j0 += kTileThreads) {
+    const int nj = (int)((n - j0) < kTileThreads ? (n - j0) : kTileThreads);
+    __syncthreads();
+    stage_gaussians<GIdx>(p, gids, s, j0, nj, mu, chol_raw, gl, gid_lds, &hdr->status);
+    __syncthreads();
+    for (int j = 0; j < nj; ++j) {
+      const int32_t g = gid_lds[j];
+      if (g < 0) continue;
+      const GaussEval v = gl[j];
+      float m[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int32_t px = threadIdx.x; px < npx; px += kTileThreads) {
+        const int32_t r = r0 + px / w, c = c0 + (px - (px / w) * w);
+        const float gr = grad[(int64_t)r * p.N + c];
+        const float dx = row_coords[r] - v.mu0, dy = col_coords[c] - v.mu1;
+        const float a = v.wa * dx;
+        const float ge = gr * basis_w(p, a * a, fmaf(v.wc, dy, v.wb * dx));
+        m[0] += ge;
+        m[1] += ge * dx;
+        m[2] += ge * dy;
+        m[3] += ge * dx * dx;
+        m[4] += ge * dx * dy;
+        m[5] += ge * dy * dy;
+      }
+#pragma unroll
+      for (int k = 0; k < 6; ++k) m[k] = wave_sum(m[k]);
+      if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < 6; ++k) red[wid][k] = m[k];
+      }
+      __syncthreads();
+      if (threadIdx.x < 6) {
+        float tot = 0.f;
+#pragma unroll
+        for (int q = 0; q < kTileThreads / 64; ++q) tot += red[q][threadIdx.x];
+        unsafeAtomicAdd(acc + 8 * (int64_t)g + threadIdx.x, tot);
+      }
+      __syncthreads();
+    }
+  }
 }
 
-// Chain rule from the six pixel sums of Gaussian g to (d_mu, d_chol_raw, d_amp), in double.
-//   S0 = sum g e, S1 = sum w dx, S2 = sum w dy, S3 = sum w dx^2, S4 = sum w dx dy, S5 = sum w dy^2
-// with e = exp(-q/2) (clamped q), w = g e [q inside the clamp range].  Derivation:
+// Chain rule from the six moments of Gaussian g to (d_mu, d_chol_raw, d_amp), in double:
 //   d_amp = norm S0;  d_mu = amp norm A (S1, S2);  dL/dA = -amp norm / 2 [[S3,S4],[S4,S5]];
-//   dL/ddet = amp S0 (-norm / (2 det)) if normalize and sqrt(det) >= eps;
-//   dL/dcov = -A (dL/dA) A + dL/ddet det A;  dL/dL = (G + G^T) L;  softplus' on the diagonal.
-__device__ void chain_one(const Problem& p, const float* __restrict__ mu, const float* __restrict__ chol_raw,
-                          const float* __restrict__ amp, const float* acc8, int64_t g,
-                          float* __restrict__ d_mu, float* __restrict__ d_chol_raw,
-                          float* __restrict__ d_amp) {
+//   dL/ddet = amp S0 (-norm / (2 det)) if normalize and sqrt(det) >= eps (else 0);
+//   G = dL/dcov = -A (dL/dA) A + dL/ddet det A;  dL/dL = (G + G^T) L;  softplus' on the diagonal.
+// A is the inverse of the fp32 covariance; the algebra follows torch's autograd of the
+// reference CPU path (linalg.inv, linalg.det, L L^T, softplus).
+__global__ __launch_bounds__(kTileThreads) void k_bwd_finish(
+    Problem p, const float* __restrict__ chol_raw, const float* __restrict__ amp,
+    float* __restrict__ d_mu, float* __restrict__ d_chol_raw, float* __restrict__ d_amp, uint8_t* ws,
+    BwdLayout L) {
+  float* acc = reinterpret_cast<float*>(ws + L.acc);
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= p.K) return;
+  const float4 a0 = reinterpret_cast<const float4*>(acc)[2 * g + 0];
+  const float4 a1 = reinterpret_cast<const float4*>(acc)[2 * g + 1];
+  reinterpret_cast<float4*>(acc)[2 * g + 0] = make_float4(0.f, 0.f, 0.f, 0.f);
+  reinterpret_cast<float4*>(acc)[2 * g + 1] = make_float4(0.f, 0.f, 0.f, 0.f);
   const float raw11 = chol_raw[3 * g + 0], raw21 = chol_raw[3 * g + 1], raw22 = chol_raw[3 * g + 2];
   const GfChol Lc = gf_activate_cholesky(raw11, raw21, raw22);
   const GfCov cov = gf_cov_from_chol(Lc);
   const GfRenderGeom rg = gf_render_geom(cov, p.normalize);
-  const double S0 = acc8[0], S1 = acc8[1], S2 = acc8[2], S3 = acc8[3], S4 = acc8[4], S5 = acc8[5];
+  const double S0 = a0.x, S1 = a0.y, S2 = a0.z, S3 = a0.w, S4 = a1.x, S5 = a1.y;
   const double a = (double)amp[g];
   const double nrm = (double)rg.norm;
   const double an = a * nrm;
@@ -505,7 +1040,6 @@ __device__ void chain_one(const Problem& p, const float* __restrict__ mu, const 
   d_mu[2 * g + 0] = (float)(an * (rg.i00 * S1 + rg.i01 * S2));
   d_mu[2 * g + 1] = (float)(an * (rg.i01 * S1 + rg.i11 * S2));
   const double G00 = -0.5 * an * S3, G01 = -0.5 * an * S4, G11 = -0.5 * an * S5;
-  // AG = A G, AGA = A G A  (A, G symmetric)
   const double ag00 = rg.i00 * G00 + rg.i01 * G01, ag01 = rg.i00 * G01 + rg.i01 * G11;
   const double ag10 = rg.i01 * G00 + rg.i11 * G01, ag11 = rg.i01 * G01 + rg.i11 * G11;
   double c00 = -(ag00 * rg.i00 + ag01 * rg.i01);
@@ -515,8 +1049,7 @@ __device__ void chain_one(const Problem& p, const float* __restrict__ mu, const 
   if (p.normalize) {
     const float sq = gf_sqrt_rn(rg.det_f);
     if (sq >= GF_FLT_EPS) {
-      const double gdet = a * S0 * (-nrm / (2.0 * (double)rg.det_f));
-      const double f = gdet * (double)rg.det_f;
+      const double f = a * S0 * (-nrm / 2.0);  // dL/ddet * det
       c00 += f * rg.i00;
       c01 += f * rg.i01;
       c10 += f * rg.i01;
@@ -530,135 +1063,6 @@ __device__ void chain_one(const Problem& p, const float* __restrict__ mu, const 
   d_chol_raw[3 * g + 0] = (float)(dl11 * gf_softplus_grad(raw11));
   d_chol_raw[3 * g + 1] = (float)dl21;
   d_chol_raw[3 * g + 2] = (float)(dl22 * gf_softplus_grad(raw22));
-}
-
-template <typename TpIdx, typename GIdx>
-__global__ __launch_bounds__(kTileThreads) void k_bwd_tiles(
-    Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
-    const float* __restrict__ col_coords, const float* __restrict__ mu,
-    const float* __restrict__ chol_raw, const float* __restrict__ amp,
-    const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
-    float* __restrict__ d_mu, float* __restrict__ d_chol_raw, float* __restrict__ d_amp,
-    uint8_t* ws, BwdLayout L) {
-  __shared__ GaussLds gl[kTileThreads];
-  __shared__ int32_t gid_lds[kTileThreads];
-  __shared__ float red[kTileThreads / 64][8];
-  __shared__ int is_last;
-  WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
-  float* acc = reinterpret_cast<float*>(ws + L.acc);
-  const int64_t T = p.R * p.C;
-  const int64_t t = blockIdx.x;
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-
-  int64_t s = (int64_t)tile_ptr[t], e = (int64_t)tile_ptr[t + 1];
-  if (threadIdx.x == 0) {
-    if (s < 0 || e < s || e > num_pairs) set_status(&hdr->status, GF_STATUS_TILE_PTR_ORDER);
-    if (t == T - 1 && e != num_pairs) set_status(&hdr->status, GF_STATUS_TILE_PTR_LAST);
-  }
-  if (s < 0) s = 0;
-  if (e > num_pairs) e = num_pairs;
-  const int64_t n = e > s ? e - s : 0;
-
-  const int64_t tr = t / p.C, tc = t % p.C;
-  const int64_t r0 = tr * p.tile_out, c0 = tc * p.tile_in;
-  const int64_t r1 = (r0 + p.tile_out) < p.M ? (r0 + p.tile_out) : p.M;
-  const int64_t c1 = (c0 + p.tile_in) < p.N ? (c0 + p.tile_in) : p.N;
-  const int64_t w = c1 - c0;
-  const int64_t npx = (r1 - r0) * w;
-
-  for (int64_t j0 = 0; j0 < n; j0 += kTileThreads) {
-    const int64_t nj = (n - j0) < kTileThreads ? (n - j0) : kTileThreads;
-    __syncthreads();
-    if (threadIdx.x < nj) {
-      const int64_t g = (int64_t)gids[s + j0 + threadIdx.x];
-      if (g < 0 || g >= p.K) {
-        set_status(&hdr->status, g < 0 ? GF_STATUS_IDS_NEGATIVE : GF_STATUS_IDS_RANGE);
-        gid_lds[threadIdx.x] = -1;
-      } else {
-        GeomF q;
-        gaussian_geometry(p, mu, chol_raw, g, &q, nullptr);
-        GaussLds v;
-        v.mu0 = q.mu0;
-        v.mu1 = q.mu1;
-        v.i00 = q.i00;
-        v.i01 = q.i01;
-        v.i11 = q.i11;
-        v.w = 0.0f;
-        v.pad0 = v.pad1 = 0.0f;
-        gl[threadIdx.x] = v;
-        gid_lds[threadIdx.x] = (int32_t)g;
-      }
-    }
-    __syncthreads();
-    for (int j = 0; j < (int)nj; ++j) {
-      const int32_t g = gid_lds[j];
-      if (g < 0) continue;
-      const GaussLds v = gl[j];
-      float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f, s4 = 0.f, s5 = 0.f;
-      for (int64_t px = threadIdx.x; px < npx; px += kTileThreads) {
-        const int64_t r = r0 + px / w, c = c0 + px % w;
-        const float gr = grad[r * p.N + c];
-        const float dx = row_coords[r] - v.mu0, dy = col_coords[c] - v.mu1;
-        float q = (dx * v.i00 + dy * v.i01) * dx + (dx * v.i01 + dy * v.i11) * dy;
-        bool live = true;
-        if (p.has_clamp) {
-          live = (q >= 0.0f) && (q <= p.clamp_quad);
-          q = fminf(fmaxf(q, 0.0f), p.clamp_quad);
-        }
-        const float ge = gr * expf(-0.5f * q);
-        s0 += ge;
-        const float wv = live ? ge : 0.0f;
-        s1 += wv * dx;
-        s2 += wv * dy;
-        s3 += wv * dx * dx;
-        s4 += wv * dx * dy;
-        s5 += wv * dy * dy;
-      }
-      s0 = wave_sum(s0);
-      s1 = wave_sum(s1);
-      s2 = wave_sum(s2);
-      s3 = wave_sum(s3);
-      s4 = wave_sum(s4);
-      s5 = wave_sum(s5);
-      if (lane == 0) {
-        red[wid][0] = s0;
-        red[wid][1] = s1;
-        red[wid][2] = s2;
-        red[wid][3] = s3;
-        red[wid][4] = s4;
-        red[wid][5] = s5;
-      }
-      __syncthreads();
-      if (threadIdx.x < 6) {
-        float tot = 0.f;
-#pragma unroll
-        for (int q = 0; q < kTileThreads / 64; ++q) tot += red[q][threadIdx.x];
-        unsafeAtomicAdd(acc + 8 * (int64_t)g + threadIdx.x, tot);
-      }
-      __syncthreads();
-    }
-  }
-
-  // Last workgroup applies the chain rule.
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = atomicAdd(&hdr->ticket, 1u);
-    is_last = (prev == (uint32_t)(gridDim.x - 1));
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  for (int64_t g = threadIdx.x; g < p.K; g += kTileThreads) {
-    float a8[6];
-#pragma unroll
-    for (int q = 0; q < 6; ++q) {
-      a8[q] = __hip_atomic_load(acc + 8 * g + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      acc[8 * g + q] = 0.0f;  // leave the workspace zeroed for the next call
-    }
-    chain_one(p, mu, chol_raw, amp, a8, g, d_mu, d_chol_raw, d_amp);
-  }
-  if (threadIdx.x == 0) hdr->ticket = 0u;
 }
 
 // Self-test: order-independent checksum of gf_softplus_torch_cpu over all 2^32 inputs.
@@ -677,7 +1081,6 @@ __global__ __launch_bounds__(256) void k_selftest_softplus(unsigned long long* o
     const uint32_t yb = (y != y) ? 0x7fc00000u : gf_bits_f32(y);
     h += mix64((u << 32) | yb);
   }
-  // wave reduction then one atomic per wave
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) h += __shfl_xor(h, o, 64);
   if ((threadIdx.x & 63) == 0) atomicAdd(out, (unsigned long long)h);
@@ -695,20 +1098,48 @@ int make_problem(const gf_field_config* cfg, int64_t M, int64_t N, int64_t K, Pr
   if (M <= 0 || N <= 0)
     return set_err(GF_E_INVALID_ARGUMENT, "out_features and in_features must be positive");
   if (K < 0) return set_err(GF_E_INVALID_ARGUMENT, "K must be non-negative");
-  if (K > INT32_MAX) return set_err(GF_E_INVALID_ARGUMENT, "K must be < 2^31");
-  p->M = M;
-  p->N = N;
+  if (K > INT32_MAX || M > INT32_MAX || N > INT32_MAX)
+    return set_err(GF_E_INVALID_ARGUMENT, "K, out_features and in_features must be < 2^31");
+  const int64_t R = (M + cfg->tile_out - 1) / cfg->tile_out, C = (N + cfg->tile_in - 1) / cfg->tile_in;
+  if (R * C > INT32_MAX) return set_err(GF_E_INVALID_ARGUMENT, "too many tiles (>= 2^31)");
   p->K = K;
-  p->tile_out = cfg->tile_out;
-  p->tile_in = cfg->tile_in;
-  p->R = (M + cfg->tile_out - 1) / cfg->tile_out;
-  p->C = (N + cfg->tile_in - 1) / cfg->tile_in;
-  if (p->R * p->C > INT32_MAX) return set_err(GF_E_INVALID_ARGUMENT, "too many tiles (>= 2^31)");
+  p->M = (int32_t)M;
+  p->N = (int32_t)N;
+  // A tile larger than the matrix covers it once; clamping keeps the 32-bit tile arithmetic exact.
+  p->tile_out = (int32_t)std::min<int64_t>(cfg->tile_out, M);
+  p->tile_in = (int32_t)std::min<int64_t>(cfg->tile_in, N);
+  p->R = (int32_t)R;
+  p->C = (int32_t)C;
   p->sigma = (float)cfg->sigma_multiplier;
-  p->clamp_quad = (float)cfg->clamp_quad;
+  if (cfg->has_clamp_quad) {
+    // q in [0, clamp] -> q * kHalfLog2e in [clamp * kHalfLog2e, 0]
+    p->q_lo = (float)(cfg->clamp_quad * (double)kHalfLog2e);
+    p->q_hi = 0.0f;
+    if (p->q_lo > p->q_hi) p->q_lo = p->q_hi;  // negative clamp: the form is pinned at 0
+  } else {
+    p->q_lo = -INFINITY;
+    p->q_hi = INFINITY;
+  }
   p->normalize = cfg->normalize ? 1 : 0;
-  p->has_clamp = cfg->has_clamp_quad ? 1 : 0;
   return GF_OK;
+}
+
+bool fast16(const Problem& p) { return p.tile_out == 16 && p.tile_in == 16; }
+
+unsigned wave_tile_grid(int64_t T) { return (unsigned)((T + kTileThreads / 64 - 1) / (kTileThreads / 64)); }
+
+template <typename TP, typename GI>
+void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, const float* rc,
+                const float* cc, const float* mu, const float* raw, const void* tile_ptr,
+                const void* gids, int64_t num_pairs, uint8_t* ws, const BwdLayout& L) {
+  if (fast16(p))
+    hipLaunchKernelGGL((k_bwd16<TP, GI>), dim3(wave_tile_grid((int64_t)p.R * p.C)), dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw,
+                       reinterpret_cast<const TP*>(tile_ptr), reinterpret_cast<const GI*>(gids),
+                       num_pairs, ws, L);
+  else
+    hipLaunchKernelGGL((k_bwd_any<TP, GI>), grid, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw,
+                       reinterpret_cast<const TP*>(tile_ptr), reinterpret_cast<const GI*>(gids),
+                       num_pairs, ws, L);
 }
 
 }  // namespace
@@ -735,7 +1166,7 @@ size_t gf_forward_workspace_bytes(int64_t out_features, int64_t in_features, int
                                   const gf_field_config* cfg) {
   Problem p;
   if (make_problem(cfg, out_features, in_features, k, &p)) return 0;
-  return fwd_layout(k, p.R * p.C).total;
+  return fwd_layout(k, (int64_t)p.R * p.C).total;
 }
 
 size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, int64_t k,
@@ -752,7 +1183,7 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
-  const FwdLayout L = fwd_layout(k, p.R * p.C);
+  const FwdLayout L = fwd_layout(k, (int64_t)p.R * p.C);
   if (!workspace || workspace_bytes < L.total)
     return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
   if (!tile_ptr || !num_pairs_dev) return set_err(GF_E_INVALID_ARGUMENT, "tile_ptr / num_pairs_dev must not be NULL");
@@ -772,17 +1203,37 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
   return GF_OK;
 }
 
-int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                      const float* row_coords, const float* col_coords, const float* mu,
-                      const float* chol_raw, const float* amp, const int64_t* tile_ptr,
-                      int64_t* gaussian_ids_sorted, int64_t ids_capacity, int64_t pairs_hint,
-                      float* delta, void* workspace, size_t workspace_bytes, void* stream) {
-  (void)mu;
-  (void)chol_raw;
+int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                    int64_t* gaussian_ids_sorted, int64_t ids_capacity, int64_t pairs_hint,
+                    void* workspace, size_t workspace_bytes, void* stream) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
-  const int64_t T = p.R * p.C;
+  const FwdLayout L = fwd_layout(k, (int64_t)p.R * p.C);
+  if (!workspace || workspace_bytes < L.total)
+    return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
+  if (ids_capacity < 0 || (ids_capacity > 0 && !gaussian_ids_sorted))
+    return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / ids_capacity invalid");
+  if (k == 0) return GF_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  int64_t work = pairs_hint > 0 ? pairs_hint : (ids_capacity > 0 ? ids_capacity : 1);
+  int64_t blocks = (work + kEmitThreads - 1) / kEmitThreads;
+  blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, 1 << 16));
+  hipLaunchKernelGGL(k_emit, dim3((unsigned)blocks), dim3(kEmitThreads), 0, st, p,
+                     reinterpret_cast<uint8_t*>(workspace), L, gaussian_ids_sorted, ids_capacity);
+  GF_LAUNCH_CHECK("k_emit");
+  return GF_OK;
+}
+
+int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                      const float* row_coords, const float* col_coords, const float* mu,
+                      const float* chol_raw, const float* amp, const int64_t* tile_ptr,
+                      int64_t* gaussian_ids_sorted, int64_t ids_capacity, float* delta,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  Problem p;
+  int rc = make_problem(cfg, out_features, in_features, k, &p);
+  if (rc) return rc;
+  const int64_t T = (int64_t)p.R * p.C;
   const FwdLayout L = fwd_layout(k, T);
   if (!workspace || workspace_bytes < L.total)
     return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
@@ -790,21 +1241,70 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
     return set_err(GF_E_INVALID_ARGUMENT, "coords / tile_ptr / delta must not be NULL");
   if (ids_capacity < 0 || (ids_capacity > 0 && !gaussian_ids_sorted))
     return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / ids_capacity invalid");
-  if (k > 0 && !amp) return set_err(GF_E_INVALID_ARGUMENT, "amp must not be NULL");
+  if (k > 0 && (!mu || !chol_raw || !amp)) return set_err(GF_E_INVALID_ARGUMENT, "mu / chol_raw / amp must not be NULL");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
-  if (k > 0) {
-    int64_t work = pairs_hint > 0 ? pairs_hint : (ids_capacity > 0 ? ids_capacity : 1);
-    int64_t blocks = (work + kEmitThreads - 1) / kEmitThreads;
-    if (blocks < 1) blocks = 1;
-    if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(k_emit, dim3((unsigned)blocks), dim3(kEmitThreads), 0, st, p, ws, L,
-                       gaussian_ids_sorted, ids_capacity);
-    GF_LAUNCH_CHECK("k_emit");
-  }
-  hipLaunchKernelGGL(k_render, dim3((unsigned)T), dim3(kTileThreads), 0, st, p, row_coords,
-                     col_coords, amp, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws, L);
+  if (fast16(p))
+    hipLaunchKernelGGL(k_render16, dim3(wave_tile_grid(T)), dim3(kTileThreads), 0, st, p, row_coords,
+                       col_coords, mu, chol_raw, amp, tile_ptr, gaussian_ids_sorted, ids_capacity,
+                       delta, ws);
+  else
+    hipLaunchKernelGGL(k_render_any, dim3((unsigned)T), dim3(kTileThreads), 0, st, p, row_coords,
+                       col_coords, mu, chol_raw, amp, tile_ptr, gaussian_ids_sorted, ids_capacity,
+                       delta, ws);
   GF_LAUNCH_CHECK("k_render");
+  return GF_OK;
+}
+
+int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                       const float* grad_delta, const float* row_coords, const float* col_coords,
+                       const float* mu, const float* chol_raw, const void* tile_ptr,
+                       int32_t tile_ptr_is_int64, const void* gaussian_ids, int32_t ids_is_int64,
+                       int64_t num_pairs, void* workspace, size_t workspace_bytes, void* stream) {
+  Problem p;
+  int rc = make_problem(cfg, out_features, in_features, k, &p);
+  if (rc) return rc;
+  const int64_t T = (int64_t)p.R * p.C;
+  const BwdLayout L = bwd_layout(k);
+  if (!workspace || workspace_bytes < L.total)
+    return set_err(GF_E_WORKSPACE, "backward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
+  if (num_pairs < 0) return set_err(GF_E_INVALID_ARGUMENT, "num_pairs must be non-negative");
+  if (!grad_delta || !row_coords || !col_coords || !tile_ptr)
+    return set_err(GF_E_INVALID_ARGUMENT, "grad_delta / coords / tile_ptr must not be NULL");
+  if (num_pairs > 0 && !gaussian_ids) return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids must not be NULL");
+  if (k > 0 && (!mu || !chol_raw)) return set_err(GF_E_INVALID_ARGUMENT, "mu / chol_raw must not be NULL");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  const dim3 grid((unsigned)T);
+  if (tile_ptr_is_int64 && ids_is_int64)
+    launch_bwd<int64_t, int64_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, tile_ptr, gaussian_ids, num_pairs, ws, L);
+  else if (tile_ptr_is_int64)
+    launch_bwd<int64_t, int32_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, tile_ptr, gaussian_ids, num_pairs, ws, L);
+  else if (ids_is_int64)
+    launch_bwd<int32_t, int64_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, tile_ptr, gaussian_ids, num_pairs, ws, L);
+  else
+    launch_bwd<int32_t, int32_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, tile_ptr, gaussian_ids, num_pairs, ws, L);
+  GF_LAUNCH_CHECK("k_bwd");
+  return GF_OK;
+}
+
+int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                       const float* chol_raw, const float* amp, float* d_mu, float* d_chol_raw,
+                       float* d_amp, void* workspace, size_t workspace_bytes, void* stream) {
+  Problem p;
+  int rc = make_problem(cfg, out_features, in_features, k, &p);
+  if (rc) return rc;
+  const BwdLayout L = bwd_layout(k);
+  if (!workspace || workspace_bytes < L.total)
+    return set_err(GF_E_WORKSPACE, "backward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
+  if (k == 0) return GF_OK;
+  if (!chol_raw || !amp || !d_mu || !d_chol_raw || !d_amp)
+    return set_err(GF_E_INVALID_ARGUMENT, "parameter / gradient pointers must not be NULL");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const unsigned blocks = (unsigned)((k + kTileThreads - 1) / kTileThreads);
+  hipLaunchKernelGGL(k_bwd_finish, dim3(blocks), dim3(kTileThreads), 0, st, p, chol_raw, amp, d_mu,
+                     d_chol_raw, d_amp, reinterpret_cast<uint8_t*>(workspace), L);
+  GF_LAUNCH_CHECK("k_bwd_finish");
   return GF_OK;
 }
 
@@ -814,33 +1314,13 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
                 int32_t tile_ptr_is_int64, const void* gaussian_ids, int32_t ids_is_int64,
                 int64_t num_pairs, float* d_mu, float* d_chol_raw, float* d_amp, void* workspace,
                 size_t workspace_bytes, void* stream) {
-  Problem p;
-  int rc = make_problem(cfg, out_features, in_features, k, &p);
+  if (k > 0 && !amp) return set_err(GF_E_INVALID_ARGUMENT, "amp must not be NULL");
+  int rc = gf_backward_reduce(cfg, out_features, in_features, k, grad_delta, row_coords, col_coords,
+                              mu, chol_raw, tile_ptr, tile_ptr_is_int64, gaussian_ids, ids_is_int64,
+                              num_pairs, workspace, workspace_bytes, stream);
   if (rc) return rc;
-  const int64_t T = p.R * p.C;
-  const BwdLayout L = bwd_layout(k);
-  if (!workspace || workspace_bytes < L.total)
-    return set_err(GF_E_WORKSPACE, "backward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
-  if (num_pairs < 0) return set_err(GF_E_INVALID_ARGUMENT, "num_pairs must be non-negative");
-  if (!grad_delta || !row_coords || !col_coords || !tile_ptr)
-    return set_err(GF_E_INVALID_ARGUMENT, "grad_delta / coords / tile_ptr must not be NULL");
-  if (num_pairs > 0 && !gaussian_ids) return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids must not be NULL");
-  if (k > 0 && (!mu || !chol_raw || !amp || !d_mu || !d_chol_raw || !d_amp))
-    return set_err(GF_E_INVALID_ARGUMENT, "parameter / gradient pointers must not be NULL");
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
-#define GF_BWD_LAUNCH(TP, GI)                                                                      \
-  hipLaunchKernelGGL((k_bwd_tiles<TP, GI>), dim3((unsigned)T), dim3(kTileThreads), 0, st, p,      \
-                     grad_delta, row_coords, col_coords, mu, chol_raw, amp,                       \
-                     reinterpret_cast<const TP*>(tile_ptr), reinterpret_cast<const GI*>(gaussian_ids), \
-                     num_pairs, d_mu, d_chol_raw, d_amp, ws, L)
-  if (tile_ptr_is_int64 && ids_is_int64) GF_BWD_LAUNCH(int64_t, int64_t);
-  else if (tile_ptr_is_int64) GF_BWD_LAUNCH(int64_t, int32_t);
-  else if (ids_is_int64) GF_BWD_LAUNCH(int32_t, int64_t);
-  else GF_BWD_LAUNCH(int32_t, int32_t);
-#undef GF_BWD_LAUNCH
-  GF_LAUNCH_CHECK("k_bwd_tiles");
-  return GF_OK;
+  return gf_backward_finish(cfg, out_features, in_features, k, chol_raw, amp, d_mu, d_chol_raw, d_amp,
+                            workspace, workspace_bytes, stream);
 }
 
 int gf_read_status(void* workspace, int32_t clear, uint32_t* status_host, void* stream) {
@@ -852,7 +1332,9 @@ int gf_read_status(void* workspace, int32_t clear, uint32_t* status_host, void* 
   GF_HIP_CHECK(hipStreamSynchronize(st));
   *status_host = v;
   if (clear) {
-    GF_HIP_CHECK(hipMemsetAsync(&hdr->status, 0, sizeof(uint32_t), st));
+    const uint32_t zero = 0;
+    GF_HIP_CHECK(hipMemcpyAsync(&hdr->status, &zero, sizeof(uint32_t), hipMemcpyHostToDevice, st));
+    GF_HIP_CHECK(hipStreamSynchronize(st));
   }
   return GF_OK;
 }
@@ -862,7 +1344,8 @@ int gf_selftest_softplus(uint64_t* checksum_host, void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   unsigned long long* d = nullptr;
   GF_HIP_CHECK(hipMalloc(&d, sizeof(unsigned long long)));
-  hipError_t e = hipMemsetAsync(d, 0, sizeof(unsigned long long), st);
+  const unsigned long long zero = 0;
+  hipError_t e = hipMemcpyAsync(d, &zero, sizeof(zero), hipMemcpyHostToDevice, st);
   if (e == hipSuccess) {
     hipLaunchKernelGGL(k_selftest_softplus, dim3(8192), dim3(256), 0, st, d);
     e = hipGetLastError();

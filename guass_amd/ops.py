@@ -49,32 +49,56 @@ class FieldPlan:
     def _stream(self) -> int:
         return N.stream_handle(self.device)
 
-    def forward(self, row_coords, col_coords, mu, chol_raw, amp, pairs_hint: int = 0) -> torch.Tensor:
-        """Bins and renders into ``self.delta`` (and ``tile_ptr`` / ``ids``); returns delta."""
-        L = N.lib()
-        s = self._stream()
-        N.check(L.gf_forward_bin(ctypes.byref(self.cfg), self.M, self.N, self.K, N.ptr(mu),
-                                 N.ptr(chol_raw), self.tile_ptr.data_ptr(), self.num_pairs.data_ptr(),
-                                 None, self.fwd_ws.data_ptr(), self.fwd_ws_bytes, s), "gf_forward_bin")
-        N.check(L.gf_forward_render(ctypes.byref(self.cfg), self.M, self.N, self.K,
-                                    row_coords.data_ptr(), col_coords.data_ptr(), N.ptr(mu),
-                                    N.ptr(chol_raw), N.ptr(amp), self.tile_ptr.data_ptr(),
-                                    self.ids.data_ptr(), self.capacity,
-                                    pairs_hint if pairs_hint > 0 else self.capacity,
-                                    self.delta.data_ptr(), self.fwd_ws.data_ptr(), self.fwd_ws_bytes, s),
+    # The three forward phases and two backward phases are exposed separately so that each
+    # kernel can be timed on its own; forward() / backward() run them in order.
+    def bin(self, mu, chol_raw) -> None:
+        N.check(N.lib().gf_forward_bin(ctypes.byref(self.cfg), self.M, self.N, self.K, N.ptr(mu),
+                                       N.ptr(chol_raw), self.tile_ptr.data_ptr(),
+                                       self.num_pairs.data_ptr(), None, self.fwd_ws.data_ptr(),
+                                       self.fwd_ws_bytes, self._stream()), "gf_forward_bin")
+
+    def emit(self, pairs_hint: int = 0) -> None:
+        N.check(N.lib().gf_forward_emit(ctypes.byref(self.cfg), self.M, self.N, self.K,
+                                        self.ids.data_ptr(), self.capacity,
+                                        pairs_hint if pairs_hint > 0 else self.capacity,
+                                        self.fwd_ws.data_ptr(), self.fwd_ws_bytes, self._stream()),
+                "gf_forward_emit")
+
+    def render(self, row_coords, col_coords, mu, chol_raw, amp) -> torch.Tensor:
+        N.check(N.lib().gf_forward_render(ctypes.byref(self.cfg), self.M, self.N, self.K,
+                                          row_coords.data_ptr(), col_coords.data_ptr(), N.ptr(mu),
+                                          N.ptr(chol_raw), N.ptr(amp), self.tile_ptr.data_ptr(),
+                                          self.ids.data_ptr(), self.capacity, self.delta.data_ptr(),
+                                          self.fwd_ws.data_ptr(), self.fwd_ws_bytes, self._stream()),
                 "gf_forward_render")
         return self.delta
 
+    def forward(self, row_coords, col_coords, mu, chol_raw, amp, pairs_hint: int = 0) -> torch.Tensor:
+        """Bins and renders into ``self.delta`` (and ``tile_ptr`` / ``ids``); returns delta."""
+        self.bin(mu, chol_raw)
+        self.emit(pairs_hint)
+        return self.render(row_coords, col_coords, mu, chol_raw, amp)
+
+    def backward_reduce(self, grad, row_coords, col_coords, mu, chol_raw, num_pairs: int | None = None):
+        n = self.capacity if num_pairs is None else int(num_pairs)
+        N.check(N.lib().gf_backward_reduce(ctypes.byref(self.cfg), self.M, self.N, self.K,
+                                           grad.data_ptr(), row_coords.data_ptr(), col_coords.data_ptr(),
+                                           N.ptr(mu), N.ptr(chol_raw), self.tile_ptr.data_ptr(), 1,
+                                           self.ids.data_ptr(), 1, n, self.bwd_ws.data_ptr(),
+                                           self.bwd_ws_bytes, self._stream()), "gf_backward_reduce")
+
+    def backward_finish(self, chol_raw, amp):
+        N.check(N.lib().gf_backward_finish(ctypes.byref(self.cfg), self.M, self.N, self.K,
+                                           N.ptr(chol_raw), N.ptr(amp), N.ptr(self.d_mu),
+                                           N.ptr(self.d_chol_raw), N.ptr(self.d_amp),
+                                           self.bwd_ws.data_ptr(), self.bwd_ws_bytes, self._stream()),
+                "gf_backward_finish")
+        return self.d_mu, self.d_chol_raw, self.d_amp
+
     def backward(self, grad, row_coords, col_coords, mu, chol_raw, amp, num_pairs: int | None = None):
         """Gradients into ``d_mu``, ``d_chol_raw``, ``d_amp`` from the last forward's binning."""
-        L = N.lib()
-        n = self.capacity if num_pairs is None else int(num_pairs)
-        N.check(L.gf_backward(ctypes.byref(self.cfg), self.M, self.N, self.K, grad.data_ptr(),
-                              row_coords.data_ptr(), col_coords.data_ptr(), N.ptr(mu), N.ptr(chol_raw),
-                              N.ptr(amp), self.tile_ptr.data_ptr(), 1, self.ids.data_ptr(), 1, n,
-                              N.ptr(self.d_mu), N.ptr(self.d_chol_raw), N.ptr(self.d_amp),
-                              self.bwd_ws.data_ptr(), self.bwd_ws_bytes, self._stream()), "gf_backward")
-        return self.d_mu, self.d_chol_raw, self.d_amp
+        self.backward_reduce(grad, row_coords, col_coords, mu, chol_raw, num_pairs)
+        return self.backward_finish(chol_raw, amp)
 
     def pairs(self) -> int:
         """Pair count of the last forward (synchronises)."""

@@ -82,7 +82,7 @@ def axes(M: int, N: int) -> tuple[torch.Tensor, torch.Tensor]:
 def make_problem(name: str, M: int, N: int, K: int, log_scale_mean: float, log_scale_std: float,
                  seed: int, *, clusters: int = 0, cluster_sigma_px: float = 40.0,
                  student_t_scale: float | None = None, amp_std: float = 1e-3,
-                 with_grad: bool = True) -> FieldProblem:
+                 clip_log_scale: float | None = None, with_grad: bool = True) -> FieldProblem:
     g = torch.Generator().manual_seed(seed)
     f64 = torch.float64
     if clusters > 0:
@@ -99,6 +99,8 @@ def make_problem(name: str, M: int, N: int, K: int, log_scale_mean: float, log_s
         log_scale = log_scale_mean + student_t_scale * z / torch.sqrt(chi2 / 3.0)
     else:
         log_scale = log_scale_mean + log_scale_std * torch.randn(K, 2, generator=g, dtype=f64)
+    if clip_log_scale is not None:
+        log_scale = log_scale.clamp(log_scale_mean - clip_log_scale, log_scale_mean + clip_log_scale)
     theta = torch.rand(K, generator=g, dtype=f64) * math.pi
     amp = amp_std * torch.randn(K, generator=g, dtype=f64)
     mu, chol_raw, amp32 = pixel_to_params(M, N, mean_px, log_scale, theta, amp)
@@ -126,6 +128,14 @@ def cfg5(seed: int = 0, t_scale: float = 0.5, **kw) -> FieldProblem:
                         seed, clusters=8, student_t_scale=t_scale, **kw)
 
 
+def cfg5c(seed: int = 0, **kw) -> FieldProblem:
+    """cfg5 with the Student-t log-scales clipped to log 5 +- 1.5 (covariance condition number
+    <= e^6 ~ 403): the same size, clustering and load imbalance without the near-degenerate
+    Gaussians whose fp32 field is ill-conditioned (see cfg5)."""
+    return make_problem("cfg5c_1280x5120_k4096_clip1.5", 1280, 5120, 4096, math.log(5.0), 0.0, seed,
+                        clusters=8, student_t_scale=0.5, clip_log_scale=1.5, **kw)
+
+
 def sd15_attention_shapes() -> list[tuple[str, int, int]]:
     """(name, out_features, in_features) of the 128 attention linears of an SD1.5 UNet.
 
@@ -150,4 +160,4 @@ def cfg4(seed: int = 0, layers: int | None = None, **kw) -> list[FieldProblem]:
             for i, (name, m, n) in enumerate(shapes)]
 
 
-CONFIGS = {"cfg1": cfg1, "cfg2": cfg2, "cfg3": cfg3, "cfg5": cfg5}
+CONFIGS = {"cfg1": cfg1, "cfg2": cfg2, "cfg3": cfg3, "cfg5": cfg5, "cfg5c": cfg5c}

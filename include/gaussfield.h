@@ -83,23 +83,35 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Forward phase 2: emits the (tile, gaussian) pairs into gaussian_ids_sorted in canonical
- * order (tile ascending, gaussian id ascending within a tile) and renders delta-W.
+ * Forward phase 2 (emission): writes the (tile, gaussian) pairs into gaussian_ids_sorted,
+ * each tile's ids inside its [tile_ptr[t], tile_ptr[t+1]) range (order fixed by phase 3).
  * Must follow gf_forward_bin on the same stream with the same workspace.
- *   gaussian_ids_sorted [ids_capacity] int64 out (first P entries valid)
+ *   gaussian_ids_sorted [ids_capacity] int64 out; pairs beyond the capacity are dropped and
+ *                   GF_STATUS_CAPACITY is set
+ *   pairs_hint      P if the caller knows it (sizes the grid), else <= 0 (ids_capacity is used)
+ * Replaces reference forward.cu:465-482 (emit_tile_pairs_kernel + radix sort on the tile key).
+ */
+int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                    int64_t* gaussian_ids_sorted, int64_t ids_capacity, int64_t pairs_hint,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Forward phase 3 (render): puts every tile's ids in canonical order (gaussian id ascending;
+ * with tile-major ranges this is the (tile, gaussian) order of a stable sort) and renders
+ * delta-W.  Must follow gf_forward_emit on the same stream with the same workspace.
  *   delta           [out_features*in_features] fp32 out, row-major; every element written
- *   pairs_hint      P if the caller knows it (sizes the emission grid), else <= 0
- * Replaces reference forward.cu:465-569 (emit + radix sort + ranges + tile_accumulate_kernel).
+ * Replaces reference forward.cu:513-569 (tile_accumulate_kernel; delta needs no pre-zeroing).
  */
 int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                       const float* row_coords, const float* col_coords,
                       const float* mu, const float* chol_raw, const float* amp,
                       const int64_t* tile_ptr, int64_t* gaussian_ids_sorted, int64_t ids_capacity,
-                      int64_t pairs_hint, float* delta,
-                      void* workspace, size_t workspace_bytes, void* stream);
+                      float* delta, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Backward: reduces dL/d(delta) into per-Gaussian gradients through the saved binning.
+ * gf_backward = gf_backward_reduce (per-tile moments, atomics into the workspace) followed by
+ * gf_backward_finish (chain rule, clears the workspace accumulators).
  *   grad_delta      [out_features*in_features] fp32
  *   tile_ptr        [T+1], int64 if tile_ptr_is_int64 else int32
  *   gaussian_ids    [num_pairs], int64 if ids_is_int64 else int32 (any order within a tile)
@@ -115,6 +127,20 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
                 const void* gaussian_ids, int32_t ids_is_int64, int64_t num_pairs,
                 float* d_mu, float* d_chol_raw, float* d_amp,
                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* First half of gf_backward (reference backward.cu:592-702: per-pair partials + reduce-by-key). */
+int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                       const float* grad_delta, const float* row_coords, const float* col_coords,
+                       const float* mu, const float* chol_raw,
+                       const void* tile_ptr, int32_t tile_ptr_is_int64,
+                       const void* gaussian_ids, int32_t ids_is_int64, int64_t num_pairs,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* Second half of gf_backward (reference backward.cu:436-496,704-715: cov -> chol_raw chain). */
+int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                       const float* chol_raw, const float* amp,
+                       float* d_mu, float* d_chol_raw, float* d_amp,
+                       void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Reads (and, if clear != 0, resets) the device status word of a workspace produced by the

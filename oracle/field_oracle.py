@@ -149,6 +149,21 @@ def build_tile_index(b: TileBounds) -> TileIndex:
 # --------------------------------------------------------------------------- render
 
 
+def _inv_det(cov: Tensor, exact_linalg: bool) -> tuple[Tensor, Tensor]:
+    """torch.linalg.inv / det of the 2x2 covariances (gaussian_core.py:42-44, covariance.py:35-38).
+
+    With ``exact_linalg`` the inverse and determinant of the same fp32 matrices are taken in
+    float64 and rounded to fp32 (autograd runs through the casts).  fp32 LU carries an error of
+    order cond(cov) * 2^-24 whose value depends on the BLAS (MKL) and the CPU; for the
+    well-conditioned configs it is below fp32 rounding of the field, for strongly anisotropic
+    Gaussians (cond up to 4e8 in cfg5) it is not, and only the exact form is reproducible.
+    """
+    if exact_linalg and cov.dtype == torch.float32:
+        c64 = cov.to(torch.float64)
+        return torch.linalg.inv(c64).to(cov.dtype), torch.linalg.det(c64).to(cov.dtype)
+    return torch.linalg.inv(cov), torch.linalg.det(cov)
+
+
 def _basis(coords: Tensor, mu: Tensor, inv_cov: Tensor, det_cov: Tensor, normalize: bool,
            clamp_quad: float | None) -> Tensor:
     """amp-free Gaussian basis [n, pixels] (gaussian_core.py:55-82)."""
@@ -165,7 +180,7 @@ def _basis(coords: Tensor, mu: Tensor, inv_cov: Tensor, det_cov: Tensor, normali
 
 def render_tiles(row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol: Tensor, amp: Tensor,
                  index: TileIndex, tile_out: int, tile_in: int, normalize: bool,
-                 clamp_quad: float | None) -> Tensor:
+                 clamp_quad: float | None, exact_linalg: bool = True) -> Tensor:
     """Per-tile Python loop of the reference CPU path (tile_accumulate.py:95-131).
 
     Differentiable in mu, chol and amp.  Tiles are written by assignment; empty tiles stay 0.
@@ -173,9 +188,7 @@ def render_tiles(row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol: Tenso
     m = int(row_coords.shape[0])
     n = int(col_coords.shape[0])
     dtype = row_coords.dtype
-    cov = chol @ chol.transpose(-1, -2)
-    inv_cov = torch.linalg.inv(chol @ chol.transpose(-1, -2))
-    det_cov = torch.linalg.det(cov)
+    inv_cov, det_cov = _inv_det(chol @ chol.transpose(-1, -2), exact_linalg)
     delta = torch.zeros(m, n, dtype=dtype)
     n_tc = index.num_tile_cols
     ptr = index.tile_ptr.tolist()
@@ -202,7 +215,8 @@ def render_tiles(row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol: Tenso
 
 def gaussian_field_forward(row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol_raw: Tensor,
                            amp: Tensor, tile_out: int, tile_in: int, sigma_multiplier: float,
-                           normalize: bool = False, clamp_quad: float | None = 80.0):
+                           normalize: bool = False, clamp_quad: float | None = 80.0,
+                           exact_linalg: bool = True):
     """(delta[M*N], tile_ptr[T+1] int64, gaussian_ids_sorted[P] int64), all CPU tensors."""
     chol = activate_cholesky(chol_raw)
     b = tile_bounds(mu, chol, int(row_coords.shape[0]), int(col_coords.shape[0]), tile_out,
@@ -210,14 +224,14 @@ def gaussian_field_forward(row_coords: Tensor, col_coords: Tensor, mu: Tensor, c
     index = build_tile_index(b)
     with torch.no_grad():
         delta = render_tiles(row_coords, col_coords, mu, chol, amp, index, tile_out, tile_in,
-                             normalize, clamp_quad)
+                             normalize, clamp_quad, exact_linalg)
     return delta, index.tile_ptr, index.gaussian_ids
 
 
 def gaussian_field_fwd_bwd(row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol_raw: Tensor,
                            amp: Tensor, grad_delta: Tensor, tile_out: int, tile_in: int,
                            sigma_multiplier: float, normalize: bool = False,
-                           clamp_quad: float | None = 80.0):
+                           clamp_quad: float | None = 80.0, exact_linalg: bool = True):
     """Forward plus autograd backward through the same tensor program.
 
     Returns (delta, tile_ptr, gaussian_ids_sorted, d_mu[K,2], d_chol_raw[K,3], d_amp[K,1]).
@@ -230,7 +244,7 @@ def gaussian_field_fwd_bwd(row_coords: Tensor, col_coords: Tensor, mu: Tensor, c
                     tile_out, tile_in, sigma_multiplier)
     index = build_tile_index(b)
     delta = render_tiles(row_coords, col_coords, mu_, chol, amp_, index, tile_out, tile_in,
-                         normalize, clamp_quad)
+                         normalize, clamp_quad, exact_linalg)
     if delta.requires_grad:
         d_mu, d_raw, d_amp = torch.autograd.grad(delta, (mu_, raw_, amp_),
                                                  grad_outputs=grad_delta.reshape(-1).to(delta.dtype),
@@ -246,7 +260,8 @@ def gaussian_field_fwd_bwd(row_coords: Tensor, col_coords: Tensor, mu: Tensor, c
 def gaussian_field_fwd_bwd_batched(row_coords: Tensor, col_coords: Tensor, mu: Tensor,
                                    chol_raw: Tensor, amp: Tensor, grad_delta: Tensor, tile_out: int,
                                    tile_in: int, sigma_multiplier: float, normalize: bool = False,
-                                   clamp_quad: float | None = 80.0, pair_chunk: int = 65536):
+                                   clamp_quad: float | None = 80.0, pair_chunk: int = 65536,
+                                   exact_linalg: bool = True):
     """Same tensor program as ``gaussian_field_fwd_bwd`` evaluated for all (tile, gaussian) pairs
     at once instead of a Python loop over tiles; only the fp32 summation order differs.  Used for
     full-size configurations where the loop's autograd graph is too slow.  Cross-checked against
@@ -259,9 +274,7 @@ def gaussian_field_fwd_bwd_batched(row_coords: Tensor, col_coords: Tensor, mu: T
     chol = activate_cholesky(raw_)
     b = tile_bounds(mu_.detach(), chol.detach(), m, n, tile_out, tile_in, sigma_multiplier)
     index = build_tile_index(b)
-    cov = chol @ chol.transpose(-1, -2)
-    inv_cov = torch.linalg.inv(chol @ chol.transpose(-1, -2))
-    det_cov = torch.linalg.det(cov)
+    inv_cov, det_cov = _inv_det(chol @ chol.transpose(-1, -2), exact_linalg)
     n_tc = index.num_tile_cols
     # padded pixel grid of every tile; out-of-matrix pixels are masked
     lr = torch.arange(tile_out)
@@ -307,6 +320,72 @@ def gaussian_field_fwd_bwd_batched(row_coords: Tensor, col_coords: Tensor, mu: T
     return delta, index.tile_ptr, index.gaussian_ids, d_mu, d_raw, d_amp
 
 
+def gaussian_field_fwd_bwd_fp64(row_coords: Tensor, col_coords: Tensor, mu: Tensor,
+                                chol_raw: Tensor, amp: Tensor, grad_delta: Tensor, tile_out: int,
+                                tile_in: int, sigma_multiplier: float, normalize: bool = False,
+                                clamp_quad: float | None = 80.0):
+    """The batched program evaluated in float64 on the same fp32 inputs, with the binning, the
+    activated Cholesky factor and the covariance computed in fp32 exactly as the reference does
+    (so the same Gaussians and the same pairs), then every later step in float64.  Accuracy
+    yardstick for ill-conditioned Gaussians, where no two fp32 evaluation orders agree.
+    """
+    chol32 = activate_cholesky(chol_raw)
+    cov32 = chol32 @ chol32.transpose(-1, -2)
+    b = tile_bounds(mu, chol32, int(row_coords.shape[0]), int(col_coords.shape[0]), tile_out, tile_in,
+                    sigma_multiplier)
+    index = build_tile_index(b)
+    f64 = torch.float64
+    mu_ = mu.to(f64).requires_grad_(True)
+    raw_ = chol_raw.to(f64).requires_grad_(True)
+    amp_ = amp.to(f64).requires_grad_(True)
+    # L from fp64 softplus, with the fp32 values substituted (straight-through) so that the
+    # covariance is the reference's fp32 one while gradients flow in float64.
+    chol64 = torch.zeros(raw_.shape[0], 2, 2, dtype=f64)
+    sp11 = F.softplus(raw_[:, 0]) + CHOLESKY_EPS
+    sp22 = F.softplus(raw_[:, 2]) + CHOLESKY_EPS
+    chol64[:, 0, 0] = sp11 + (chol32[:, 0, 0].to(f64) - sp11).detach()
+    chol64[:, 1, 0] = raw_[:, 1]
+    chol64[:, 1, 1] = sp22 + (chol32[:, 1, 1].to(f64) - sp22).detach()
+    cov64 = chol64 @ chol64.transpose(-1, -2)
+    cov64 = cov64 + (cov32.to(f64) - cov64).detach()
+    inv_cov = torch.linalg.inv(cov64)
+    det_cov = torch.linalg.det(cov64)
+    m, n = int(row_coords.shape[0]), int(col_coords.shape[0])
+    rc, cc = row_coords.to(f64), col_coords.to(f64)
+    grad_flat = grad_delta.reshape(-1).to(f64)
+    delta = torch.zeros(m * n, dtype=f64)
+    loss = torch.zeros((), dtype=f64)
+    n_tc = index.num_tile_cols
+    lr, lc = torch.arange(tile_out), torch.arange(tile_in)
+    P = int(index.gaussian_ids.numel())
+    for s in range(0, P, 32768):
+        e = min(P, s + 32768)
+        tiles, ids = index.tile_ids[s:e], index.gaussian_ids[s:e]
+        rows = (tiles // n_tc).unsqueeze(1) * tile_out + lr.unsqueeze(0)
+        cols = (tiles % n_tc).unsqueeze(1) * tile_in + lc.unsqueeze(0)
+        valid = ((rows < m).unsqueeze(2) & (cols < n).unsqueeze(1)).reshape(e - s, -1)
+        rr, cl = rows.clamp(max=m - 1), cols.clamp(max=n - 1)
+        dx = (rc[rr].unsqueeze(2) - mu_[ids, 0].view(-1, 1, 1)).expand(-1, -1, tile_in)
+        dy = (cc[cl].unsqueeze(1) - mu_[ids, 1].view(-1, 1, 1)).expand(-1, tile_out, -1)
+        A = inv_cov.index_select(0, ids)
+        quad = (A[:, 0, 0].view(-1, 1, 1) * dx * dx + (A[:, 0, 1] + A[:, 1, 0]).view(-1, 1, 1) * dx * dy
+                + A[:, 1, 1].view(-1, 1, 1) * dy * dy).reshape(e - s, -1)
+        if clamp_quad is not None:
+            quad = quad.clamp(min=0.0, max=clamp_quad)
+        basis = torch.exp(-0.5 * quad)
+        if normalize:
+            nrm = 1.0 / (2.0 * math.pi * torch.sqrt(det_cov.index_select(0, ids))
+                         .clamp_min(torch.finfo(torch.float32).eps))
+            basis = basis * nrm.unsqueeze(-1)
+        contrib = amp_.index_select(0, ids).reshape(-1, 1) * basis * valid
+        flat = (rr.unsqueeze(2) * n + cl.unsqueeze(1)).reshape(e - s, -1)
+        delta.index_add_(0, flat[valid], contrib.detach()[valid])
+        loss = loss + (contrib * grad_flat[flat]).sum()
+    d_mu, d_raw, d_amp = torch.autograd.grad(loss, (mu_, raw_, amp_), allow_unused=True)
+    z = lambda g, like: torch.zeros_like(like) if g is None else g  # noqa: E731
+    return delta, index.tile_ptr, index.gaussian_ids, z(d_mu, mu_), z(d_raw, raw_), z(d_amp, amp_)
+
+
 def dense_field(row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol_raw: Tensor, amp: Tensor,
                 normalize: bool = False, clamp_quad: float | None = 80.0) -> Tensor:
     """Untruncated sum over all K Gaussians at every pixel (kernels/gaussian_field.py:100-127).
@@ -317,8 +396,8 @@ def dense_field(row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol_raw: Te
     chol = activate_cholesky(chol_raw)
     gr, gc = torch.meshgrid(row_coords, col_coords, indexing="ij")
     coords = torch.stack((gr, gc), dim=-1).reshape(-1, 2)
-    cov = chol @ chol.transpose(-1, -2)
-    basis = _basis(coords, mu, torch.linalg.inv(cov), torch.linalg.det(cov), normalize, clamp_quad)
+    inv_cov, det_cov = _inv_det(chol @ chol.transpose(-1, -2), True)
+    basis = _basis(coords, mu, inv_cov, det_cov, normalize, clamp_quad)
     return (amp.reshape(-1, 1) * basis).sum(dim=0)
 
 

