@@ -7,8 +7,9 @@ one layer's field, with inputs resident in HBM, issued through the sync-free C A
 ("cfg3"), 1280x1280 fp32 delta-W from K=1024 Gaussians, 16x16 tiles, 3 sigma, clamp 80.
 
 Prints one JSON line (metric contract of the driver) with two extra objects:
-  roofline      the dominant kernel's achieved throughput against MI355X peak, from HIP events
-                recorded on the launch stream around each phase;
+  roofline      the dominant kernel's achieved throughput against MI355X peak; its duration is
+                measured live with HIP events on the launch stream around a graph of repeated
+                launches of that kernel (replay time / launch count);
   cpu_baseline  the CPU oracle (a from-scratch port of the reference's torch CPU path) timed on
                 this host on the same inputs.
 """
@@ -43,7 +44,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of graph replay")
     ap.add_argument("--graph-steps", type=int, default=10,
                     help="steps captured per HIP graph (replay overhead is paid once per graph)")
-    ap.add_argument("--phase-steps", type=int, default=100, help="eager steps timed per phase")
+    ap.add_argument("--kernel-reps", type=int, default=20, help="launches per per-kernel timing graph")
+    ap.add_argument("--kernel-replays", type=int, default=25, help="timed replays per kernel graph")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
@@ -135,7 +137,7 @@ def main() -> int:
     plan = FieldPlan(M, N, K, dev, ids_capacity=P)
 
     def step():
-        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, pairs_hint=P)
+        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
         plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
 
     stream = torch.cuda.Stream(dev)
@@ -177,25 +179,49 @@ def main() -> int:
         print(f"device status bits {status:#x} after the timed run", file=sys.stderr)
         return 1
 
-    # Per-kernel durations: HIP events recorded on the launch stream (torch's current stream)
-    # around each of the five kernels of a step, eager launches.
-    phases = (
-        ("k_bin", lambda: plan.bin(q.mu, q.chol_raw)),
-        ("k_emit", lambda: plan.emit(P)),
-        ("k_render", lambda: plan.render(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)),
-        ("k_bwd", lambda: plan.backward_reduce(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, P)),
-        ("k_bwd_finish", lambda: plan.backward_finish(q.chol_raw, q.amp)),
-    )
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)]
-           for _ in range(args.phase_steps)]
-    for i in range(args.phase_steps):
-        evs[i][0].record()
-        for j, (_, fn) in enumerate(phases):
-            fn()
-            evs[i][j + 1].record()
+    # Per-kernel durations: each kernel captured `--kernel-reps` times back to back in one HIP
+    # graph, replayed on a side stream bracketed by HIP events recorded on that same stream; the
+    # duration is the replay time over the launch count, which matches what rocprofv3's kernel
+    # trace reports for the same launches (back-to-back kernels, no host gaps).  Every kernel is
+    # idempotent under repetition except k_emit (its tile cursors advance), so k_emit is timed
+    # as (k_bin + k_emit) minus k_bin; repeated k_bwd only grows the accumulators, which the
+    # trailing k_bwd_finish clears.
+    def graph_time_us(fns) -> float:
+        s = torch.cuda.Stream(dev)
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                for _ in range(args.kernel_reps):
+                    for fn in fns:
+                        fn()
+            g.replay()
+            times = []
+            for _ in range(args.kernel_replays):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(s)
+                g.replay()
+                e1.record(s)
+                e1.synchronize()
+                times.append(e0.elapsed_time(e1) * 1e3 / args.kernel_reps)
+        torch.cuda.current_stream(dev).wait_stream(s)
+        torch.cuda.synchronize()
+        return statistics.median(times)
+
+    k_bin = lambda: plan.bin(q.mu, q.chol_raw)  # noqa: E731
+    k_emit = plan.emit
+    k_render = lambda: plan.render(q.row_coords, q.col_coords, q.amp)  # noqa: E731
+    k_bwd = lambda: plan.backward_reduce(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, P)  # noqa: E731
+    k_fin = lambda: plan.backward_finish(q.chol_raw, q.amp)  # noqa: E731
+    ph = {"k_bin": graph_time_us([k_bin])}
+    ph["k_emit"] = graph_time_us([k_bin, k_emit]) - ph["k_bin"]
+    ph["k_render"] = graph_time_us([k_render])
+    ph["k_bwd"] = graph_time_us([k_bwd])
+    ph["k_bwd_finish"] = graph_time_us([k_fin])
+    ph = {k: v / 1e3 for k, v in ph.items()}  # ms
+    # leave the plan in the state of one clean step
+    step()
     torch.cuda.synchronize()
-    ph = {name: statistics.median(evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(args.phase_steps))
-          for j, (name, _) in enumerate(phases)}
 
     value = M * N / (ms_per_step / 1e3)
     kernel_rooflines = {

@@ -75,13 +75,13 @@ def lib() -> ctypes.CDLL:
     L.gf_backward_workspace_bytes.argtypes = [c_int64, c_int64, c_int64, _CFG]
     L.gf_backward_workspace_bytes.restype = c_size_t
     L.gf_forward_bin.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_size_t, _P]
-    L.gf_forward_emit.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, c_int64, c_int64, _P, c_size_t, _P]
-    L.gf_forward_render.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P,
+    L.gf_forward_emit.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, c_int64, _P, c_size_t, _P]
+    L.gf_forward_render.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P,
                                     c_int64, _P, _P, c_size_t, _P]
     L.gf_backward.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int32,
-                              _P, c_int32, c_int64, _P, _P, _P, _P, c_size_t, _P]
+                              _P, c_int32, c_int64, _P, _P, _P, _P, _P, c_size_t, _P]
     L.gf_backward_reduce.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int32,
-                                     _P, c_int32, c_int64, _P, c_size_t, _P]
+                                     _P, c_int32, c_int64, _P, _P, c_size_t, _P]
     L.gf_backward_finish.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_size_t, _P]
     L.gf_read_status.argtypes = [_P, c_int32, POINTER(c_uint32), _P]
     L.gf_selftest_softplus.argtypes = [POINTER(c_uint64), _P]

@@ -2,21 +2,21 @@
 //
 // Forward (reference forward.cu:372-569), three kernels:
 //   k_bin      one workgroup per field: bit-exact sigma-box tile rectangle of every Gaussian,
-//              exclusive scan of the tiles each touches ("point offsets"), per-tile Gaussian
-//              counts from row-wise difference arrays, and their scan -> tile_ptr; every scan
-//              runs in LDS and global memory is only written, coalesced.
-//   k_emit     one thread per (gaussian, tile) pair: the pair's Gaussian from a 64-ary ballot
-//              search plus an LDS binary search over the point offsets, then a slot in its
-//              tile's range from a per-tile cursor (a counting sort on the tile key).
+//              its evaluation constants (kept in the workspace for the render and the
+//              backward), the pair total, per-tile Gaussian counts from row-wise difference
+//              arrays and their scan -> tile_ptr; every scan runs in LDS (DPP wave scans) and
+//              global memory is only written, coalesced.
+//   k_emit     one wave per Gaussian: a slot in each touched tile's range from a per-tile
+//              cursor (a counting sort on the tile key).
 //   k_render16 one wave per 16x16 tile, four independent tiles per workgroup, no workgroup
 //              barriers: canonical (ascending gid) order of the tile's ids (written back),
-//              per-Gaussian constants computed one Gaussian per lane and broadcast with
+//              per-Gaussian constants loaded one Gaussian per lane and broadcast with
 //              readlane, 4 pixels per lane with per-row terms hoisted.
 //   (k_render_any handles other tile shapes.)
 // Backward (reference backward.cu:541-716), two kernels:
 //   k_bwd16    one wave per 16x16 tile: lanes are (Gaussian slot, tile row); each lane sums
-//              16 pixels of its row for its Gaussian into six moments, a 16-lane butterfly
-//              reduces them, and one atomic per (Gaussian, tile, moment) accumulates them.
+//              16 pixels of its row for its Gaussian into six moments, 16-lane DPP row sums
+//              reduce them, and one atomic per (Gaussian, tile, moment) accumulates them.
 //   k_bwd_finish  per Gaussian: chain rule from the six moments to (mu, chol_raw, amp), in
 //              double, then clears the accumulators so the workspace stays zeroed.
 //   (k_bwd_any handles other tile shapes.)
@@ -103,17 +103,18 @@ static_assert(sizeof(WsHeader) == 256, "workspace header must be 256 bytes");
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Forward workspace: header, rect[K] (int4 tile ranges), point offsets[K+1], cursor[T].
+// Forward workspace: header, per-Gaussian evaluation constants eval[K] (GaussEval), rect[K]
+// (int4 tile ranges), cursor[T] (next free slot of each tile's id segment).
 struct FwdLayout {
-  size_t rect, offs, cursor, total;
+  size_t eval, rect, cursor, total;
 };
 FwdLayout fwd_layout(int64_t K, int64_t T) {
   FwdLayout L;
   size_t o = sizeof(WsHeader);
+  L.eval = o;
+  o = align256(o + 32 * (size_t)K);
   L.rect = o;
   o = align256(o + sizeof(int4) * (size_t)K);
-  L.offs = o;
-  o = align256(o + sizeof(int64_t) * (size_t)(K + 1));
   L.cursor = o;
   o = align256(o + sizeof(int64_t) * (size_t)T);
   L.total = o;
@@ -141,14 +142,11 @@ __device__ inline int32_t clamp_i32(int32_t v, int32_t lo, int32_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
 }
 
-// Bit-exact tile rectangle of Gaussian g (same fp32 operation sequence as gf_tile_rect, with
-// the row/column indices, already clamped into [0, M-1], divided in 32-bit integers).
-__device__ inline int4 bin_rect(const Problem& p, const float* __restrict__ mu,
-                                const float* __restrict__ chol_raw, int64_t g, int32_t* touched) {
+// Bit-exact tile rectangle of a Gaussian from its fp32 covariance (same fp32 operation
+// sequence as gf_tile_rect, with the row/column indices, already clamped into [0, M-1],
+// divided in 32-bit integers).
+__device__ inline int4 bin_rect(const Problem& p, float mu0, float mu1, GfCov c, int32_t* touched) {
 #pragma clang fp contract(off)
-  const float mu0 = mu[2 * g + 0], mu1 = mu[2 * g + 1];
-  const GfChol L = gf_activate_cholesky(chol_raw[3 * g + 0], chol_raw[3 * g + 1], chol_raw[3 * g + 2]);
-  const GfCov c = gf_cov_from_chol(L);
   const float std_r = gf_sqrt_rn(gf_clamp_min_nan(c.s00, GF_COV_FLOOR));
   const float std_c = gf_sqrt_rn(gf_clamp_min_nan(c.s11, GF_COV_FLOOR));
   const float centre_r = ((mu0 + 1.0f) * 0.5f) * (float)(p.M - 1);
@@ -168,37 +166,49 @@ __device__ inline int4 bin_rect(const Problem& p, const float* __restrict__ mu,
   return r;
 }
 
-// Evaluation constants of Gaussian g: the Cholesky factor L' of the fp32 covariance and
+// Evaluation constants of a Gaussian: the Cholesky factor L' of its fp32 covariance and
 // R = L'^-1 in double (R^T R = cov^-1), scaled by sqrt(log2(e)/2) and rounded once.
+__device__ inline GaussEval eval_from_cov(const Problem& p, float mu0, float mu1, GfCov c, float amp) {
+  const double a = (double)c.s00, b = (double)c.s01, d = (double)c.s11;
+  double det = a * d - b * b;  // exact products, one rounding
+  if (!(det > 0.0)) det = 1e-300;  // singular fp32 covariance: a (numerically) degenerate line
+  const double r00 = 1.0 / sqrt(a);
+  const double r11 = sqrt(a / det);  // 1 / l22 with l22 = sqrt(det / a)
+  const double r10 = -(b / a) * r11;  // -l21 / (l11 l22)
+  GaussEval v;
+  v.mu0 = mu0;
+  v.mu1 = mu1;
+  v.wa = (float)(kSqrtHalfLog2e * r00);
+  v.wb = (float)(kSqrtHalfLog2e * r10);
+  v.wc = (float)(kSqrtHalfLog2e * r11);
+  float norm = 1.0f;
+  if (p.normalize) {
+#pragma clang fp contract(off)
+    const float sq = gf_sqrt_rn((float)det);
+    norm = gf_div_f32(1.0f, GF_TWO_PI_F32 * (sq < GF_FLT_EPS ? GF_FLT_EPS : sq));
+  }
+  v.w = amp * norm;
+  v.pad0 = v.pad1 = 0.0f;
+  return v;
+}
+
 __device__ inline GaussEval eval_geom(const Problem& p, const float* __restrict__ mu,
                                       const float* __restrict__ chol_raw,
                                       const float* __restrict__ amp, int64_t g) {
   const GfChol L = gf_activate_cholesky(chol_raw[3 * g + 0], chol_raw[3 * g + 1], chol_raw[3 * g + 2]);
-  const GfCov c = gf_cov_from_chol(L);
-  const double a = (double)c.s00, b = (double)c.s01, d = (double)c.s11;
-  double det = a * d - b * b;  // exact products, one rounding
-  if (!(det > 0.0)) det = 1e-300;  // singular fp32 covariance: a (numerically) degenerate line
-  const double l11 = sqrt(a);
-  const double r00 = 1.0 / l11;
-  const double r11 = sqrt(a / det);       // 1 / l22 with l22 = sqrt(det / a)
-  const double r10 = -(b / a) * r11;      // -l21 / (l11 l22)
+  return eval_from_cov(p, mu[2 * g + 0], mu[2 * g + 1], gf_cov_from_chol(L), amp ? amp[g] : 0.0f);
+}
+
+__device__ inline GaussEval load_eval(const GaussEval* __restrict__ ev, int64_t g) {
+  const float4* q = reinterpret_cast<const float4*>(ev + g);
+  const float4 a = q[0], b = q[1];
   GaussEval v;
-  v.mu0 = mu[2 * g + 0];
-  v.mu1 = mu[2 * g + 1];
-  v.wa = (float)(kSqrtHalfLog2e * r00);
-  v.wb = (float)(kSqrtHalfLog2e * r10);
-  v.wc = (float)(kSqrtHalfLog2e * r11);
-  if (amp) {
-    float norm = 1.0f;
-    if (p.normalize) {
-#pragma clang fp contract(off)
-      const float sq = gf_sqrt_rn((float)det);
-      norm = gf_div_f32(1.0f, GF_TWO_PI_F32 * (sq < GF_FLT_EPS ? GF_FLT_EPS : sq));
-    }
-    v.w = amp[g] * norm;
-  } else {
-    v.w = 0.0f;
-  }
+  v.mu0 = a.x;
+  v.mu1 = a.y;
+  v.wa = a.z;
+  v.wb = a.w;
+  v.wc = b.x;
+  v.w = b.y;
   v.pad0 = v.pad1 = 0.0f;
   return v;
 }
@@ -219,6 +229,12 @@ __device__ inline float readlane_f(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+__device__ inline int64_t readlane_i64(int64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int32_t)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int32_t)(v >> 32), lane);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 // Orders the memory operations of one wave (its lanes exchange data through LDS / global).
 __device__ inline void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
@@ -226,17 +242,59 @@ __device__ inline void wave_sync() {
 }
 
 // ------------------------------------------------------------------------------------------
+// DPP wave primitives (gfx9 row_shr / row_bcast; no LDS traffic).
+
+template <int CTRL, int ROWS>
+__device__ inline int32_t dpp_i32(int32_t v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xf, false);
+}
+
+// Inclusive scan over the 64 lanes: row_shr 1,2,4,8 within rows of 16, then row_bcast 15 / 31.
+__device__ inline int32_t dpp_scan_i32(int32_t v) {
+  v += dpp_i32<0x111, 0xf>(v);
+  v += dpp_i32<0x112, 0xf>(v);
+  v += dpp_i32<0x114, 0xf>(v);
+  v += dpp_i32<0x118, 0xf>(v);
+  v += dpp_i32<0x142, 0xa>(v);
+  v += dpp_i32<0x143, 0xc>(v);
+  return v;
+}
+
+template <int CTRL, int ROWS>
+__device__ inline int64_t dpp_i64(int64_t v) {
+  const int32_t lo = __builtin_amdgcn_update_dpp(0, (int32_t)(uint32_t)v, CTRL, ROWS, 0xf, false);
+  const int32_t hi = __builtin_amdgcn_update_dpp(0, (int32_t)(v >> 32), CTRL, ROWS, 0xf, false);
+  return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+__device__ inline int64_t dpp_scan_i64(int64_t v) {
+  v += dpp_i64<0x111, 0xf>(v);
+  v += dpp_i64<0x112, 0xf>(v);
+  v += dpp_i64<0x114, 0xf>(v);
+  v += dpp_i64<0x118, 0xf>(v);
+  v += dpp_i64<0x142, 0xa>(v);
+  v += dpp_i64<0x143, 0xc>(v);
+  return v;
+}
+
+template <int CTRL>
+__device__ inline float dpp_f32(float v) {
+  return __int_as_float(dpp_i32<CTRL, 0xf>(__float_as_int(v)));
+}
+
+// Sum over each row of 16 lanes, left in lane 15 of the row (other lanes hold partial sums).
+__device__ inline float dpp_row_sum_f32(float v) {
+  v += __int_as_float(dpp_i32<0x111, 0xf>(__float_as_int(v)));
+  v += __int_as_float(dpp_i32<0x112, 0xf>(__float_as_int(v)));
+  v += __int_as_float(dpp_i32<0x114, 0xf>(__float_as_int(v)));
+  v += __int_as_float(dpp_i32<0x118, 0xf>(__float_as_int(v)));
+  return v;
+}
+
+// ------------------------------------------------------------------------------------------
 // Workgroup scans.
 
-__device__ inline int64_t wave_inclusive_scan(int64_t x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int64_t y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  return x;
-}
+__device__ inline int64_t wave_inclusive_scan(int64_t x) { return dpp_scan_i64(x); }
 
 // Exclusive scan across a workgroup of BLOCK threads; *total receives the sum.
 // lds must hold BLOCK/64 + 1 int64.
@@ -283,15 +341,7 @@ __device__ int64_t block_scan_runs(int64_t* data, int64_t n, int64_t* lds) {
 // ------------------------------------------------------------------------------------------
 // k_bin: one workgroup.
 
-__device__ inline int32_t wave_inclusive_scan32(int32_t x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int32_t y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  return x;
-}
+__device__ inline int32_t wave_inclusive_scan32(int32_t x) { return dpp_scan_i32(x); }
 
 // Exclusive scan of the int32 values lds[0..n) by the workgroup (each thread owns a contiguous
 // run), written to out[0..n) as int64; returns the total.
@@ -310,6 +360,16 @@ __device__ int64_t bin_scan_lds_to_global(const int32_t* lds, int64_t n, int64_t
   return total;
 }
 
+__device__ inline void store_eval(GaussEval* ev, int64_t g, const GaussEval& v) {
+  float4* q = reinterpret_cast<float4*>(ev + g);
+  q[0] = make_float4(v.mu0, v.mu1, v.wa, v.wb);
+  q[1] = make_float4(v.wc, v.w, 0.0f, 0.0f);
+}
+
+// Gaussians g = threadIdx.x + i * kBinThreads, i < kBinRectRegs, keep their tile rectangle in
+// registers between the phases of k_bin; the rest re-read it from the workspace.
+constexpr int kBinRectRegs = 4;
+
 __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __restrict__ mu,
                                                      const float* __restrict__ chol_raw,
                                                      int64_t* __restrict__ tile_ptr,
@@ -319,28 +379,39 @@ __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __r
   __shared__ int64_t rowbase[kBinMaxBandRows + 1];
   __shared__ int64_t scan_lds[kBinThreads / 64 + 1];
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
+  GaussEval* ev = reinterpret_cast<GaussEval*>(ws + L.eval);
   int4* rect = reinterpret_cast<int4*>(ws + L.rect);
-  int64_t* offs = reinterpret_cast<int64_t*>(ws + L.offs);
   int64_t* cursor = reinterpret_cast<int64_t*>(ws + L.cursor);
   const int64_t K = p.K, T = (int64_t)p.R * p.C;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   if (threadIdx.x == 0) hdr->status = 0u;
 
-  // A: rectangles and tiles touched (touched counts in LDS when they fit).
-  const bool k_in_lds = K <= kLdsDiffWords;
-  for (int64_t g = threadIdx.x; g < K; g += kBinThreads) {
+  // A: rectangles, pairs (tiles touched) and evaluation constants (the weight slot holds the
+  // normalisation; the render applies the amplitude).
+  int4 myrect[kBinRectRegs];
+  int64_t my_pairs = 0;
+  auto prep = [&](int64_t g) -> int4 {
+    const GfChol Lc = gf_activate_cholesky(chol_raw[3 * g + 0], chol_raw[3 * g + 1], chol_raw[3 * g + 2]);
+    const GfCov c = gf_cov_from_chol(Lc);
+    const float m0 = mu[2 * g + 0], m1 = mu[2 * g + 1];
     int32_t touched;
-    rect[g] = bin_rect(p, mu, chol_raw, g, &touched);
-    if (k_in_lds) lds[g] = touched;
-    else offs[g] = touched;
+    const int4 r = bin_rect(p, m0, m1, c, &touched);
+    rect[g] = r;
+    store_eval(ev, g, eval_from_cov(p, m0, m1, c, 1.0f));
+    my_pairs += touched;
+    return r;
+  };
+#pragma unroll
+  for (int i = 0; i < kBinRectRegs; ++i) {
+    const int64_t g = threadIdx.x + (int64_t)i * kBinThreads;
+    myrect[i] = make_int4(1, 0, 1, 0);  // empty
+    if (g < K) myrect[i] = prep(g);
   }
-  __syncthreads();
+  for (int64_t g = threadIdx.x + (int64_t)kBinRectRegs * kBinThreads; g < K; g += kBinThreads) prep(g);
 
-  // B: point offsets (exclusive scan of tiles touched); offs[K] = P.
-  const int64_t P = k_in_lds ? bin_scan_lds_to_global(lds, K, offs, scan_lds)
-                             : block_scan_runs<kBinThreads>(offs, K, scan_lds);
-  if (threadIdx.x == 0) offs[K] = P;
-  __syncthreads();
+  // B: P = total pairs.
+  int64_t P;
+  (void)block_exclusive_scan<kBinThreads>(my_pairs, &P, scan_lds);
 
   // C: per-tile counts and tile_ptr, band by band of whole tile rows.  Each covered row of each
   // rectangle adds +1 at its first column and -1 after its last; one wave per row turns the
@@ -356,46 +427,52 @@ __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __r
       const int64_t nb = (p.R - b0) < band_rows ? (p.R - b0) : band_rows;
       for (int64_t i = threadIdx.x; i < nb * C; i += kBinThreads) lds[i] = 0;
       __syncthreads();
-      for (int64_t g = threadIdx.x; g < K; g += kBinThreads) {
-        const int4 r = rect[g];
-        const int64_t rlo = r.x > b0 ? r.x : b0;
-        const int64_t rhi = r.y < b0 + nb - 1 ? r.y : b0 + nb - 1;
-        for (int64_t row = rlo; row <= rhi; ++row) {
-          int32_t* d = lds + (row - b0) * C;
+      auto diff = [&](const int4 r) {
+        const int32_t rlo = r.x > (int32_t)b0 ? r.x : (int32_t)b0;
+        const int32_t rhi = r.y < (int32_t)(b0 + nb - 1) ? r.y : (int32_t)(b0 + nb - 1);
+        for (int32_t row = rlo; row <= rhi; ++row) {
+          int32_t* d = lds + (row - (int32_t)b0) * (int32_t)C;
           atomicAdd(d + r.z, 1);
-          if (r.w + 1 < C) atomicAdd(d + r.w + 1, -1);
+          if (r.w + 1 < (int32_t)C) atomicAdd(d + r.w + 1, -1);
         }
-      }
+      };
+#pragma unroll
+      for (int i = 0; i < kBinRectRegs; ++i) diff(myrect[i]);
+      for (int64_t g = threadIdx.x + (int64_t)kBinRectRegs * kBinThreads; g < K; g += kBinThreads)
+        diff(rect[g]);
       __syncthreads();
-      for (int64_t row = wid; row < nb; row += kBinThreads / 64) {
+      const int32_t Ci = (int32_t)C, nbi = (int32_t)nb;
+      for (int32_t row = wid; row < nbi; row += kBinThreads / 64) {
         int32_t carry_d = 0, carry_c = 0;
-        for (int64_t j0 = 0; j0 < C; j0 += 64) {
-          const int64_t j = j0 + lane;
-          const int32_t dv = j < C ? lds[row * C + j] : 0;
+        for (int32_t j0 = 0; j0 < Ci; j0 += 64) {
+          const int32_t j = j0 + lane;
+          const int32_t dv = j < Ci ? lds[row * Ci + j] : 0;
           const int32_t cnt = wave_inclusive_scan32(dv) + carry_d;
-          const int32_t cnt_in = j < C ? cnt : 0;
+          const int32_t cnt_in = j < Ci ? cnt : 0;
           const int32_t inc = wave_inclusive_scan32(cnt_in);
-          if (j < C) lds[row * C + j] = carry_c + inc - cnt_in;  // exclusive offset in the row
-          carry_d = __shfl(cnt, 63, 64);
-          carry_c += __shfl(inc, 63, 64);
+          if (j < Ci) lds[row * Ci + j] = carry_c + inc - cnt_in;  // exclusive offset in the row
+          carry_d = __builtin_amdgcn_readlane(cnt, 63);
+          carry_c += __builtin_amdgcn_readlane(inc, 63);
         }
         if (lane == 0) rowbase[row] = carry_c;  // row total (scanned below)
       }
       __syncthreads();
       if (wid == 0) {
         int64_t carry = 0;
-        for (int64_t r0 = 0; r0 < nb; r0 += 64) {
-          const int64_t r = r0 + lane;
-          const int64_t v = r < nb ? rowbase[r] : 0;
+        for (int32_t r0 = 0; r0 < nbi; r0 += 64) {
+          const int32_t r = r0 + lane;
+          const int64_t v = r < nbi ? rowbase[r] : 0;
           const int64_t inc = wave_inclusive_scan(v);
-          if (r < nb) rowbase[r] = band_base + carry + inc - v;
-          carry += __shfl(inc, 63, 64);
+          if (r < nbi) rowbase[r] = band_base + carry + inc - v;
+          carry += readlane_i64(inc, 63);
         }
         if (lane == 0) rowbase[kBinMaxBandRows] = band_base + carry;
       }
       __syncthreads();
-      for (int64_t i = threadIdx.x; i < nb * C; i += kBinThreads) {
-        const int64_t row = i / C;
+      // 32-bit row/column split: the band holds at most kLdsDiffWords tiles.
+      const int32_t nbc = nbi * Ci;
+      for (int32_t i = threadIdx.x; i < nbc; i += kBinThreads) {
+        const int32_t row = (int32_t)((uint32_t)i / (uint32_t)Ci);
         const int64_t v = rowbase[row] + lds[i];
         tile_ptr[b0 * C + i] = v;
         cursor[b0 * C + i] = v;
@@ -408,12 +485,15 @@ __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __r
     // Very wide tile grids (> kLdsDiffWords tile columns): counts through global memory.
     for (int64_t i = threadIdx.x; i < T; i += kBinThreads) tile_ptr[i] = 0;
     __syncthreads();
-    for (int64_t g = threadIdx.x; g < K; g += kBinThreads) {
-      const int4 r = rect[g];
+    auto count = [&](const int4 r) {
       for (int64_t row = r.x; row <= r.y; ++row)
         for (int64_t col = r.z; col <= r.w; ++col)
           atomicAdd(reinterpret_cast<unsigned long long*>(tile_ptr + row * p.C + col), 1ull);
-    }
+    };
+#pragma unroll
+    for (int i = 0; i < kBinRectRegs; ++i) count(myrect[i]);
+    for (int64_t g = threadIdx.x + (int64_t)kBinRectRegs * kBinThreads; g < K; g += kBinThreads)
+      count(rect[g]);
     __threadfence();
     __syncthreads();
     Pc = block_scan_runs<kBinThreads>(tile_ptr, T, scan_lds);
@@ -427,66 +507,31 @@ __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __r
 }
 
 // ------------------------------------------------------------------------------------------
-// k_emit: one thread per pair, 256 consecutive pairs per workgroup pass.
+// k_emit: one wave per Gaussian; the wave's lanes walk the Gaussian's tile rectangle row-major
+// and claim a slot of each tile's id segment with an atomic on the tile's cursor.  The order
+// inside a segment is fixed afterwards by the render, which sorts each segment.
 
 __global__ __launch_bounds__(kEmitThreads) void k_emit(Problem p, uint8_t* ws, FwdLayout L,
                                                        int64_t* __restrict__ ids, int64_t capacity) {
-  __shared__ int64_t s_offs[kEmitThreads + 1];
-  __shared__ int64_t s_g0;
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   const int4* __restrict__ rect = reinterpret_cast<const int4*>(ws + L.rect);
-  const int64_t* __restrict__ offs = reinterpret_cast<const int64_t*>(ws + L.offs);
   unsigned long long* cursor = reinterpret_cast<unsigned long long*>(ws + L.cursor);
-  const int64_t K = p.K;
-  const int64_t P = offs[K];
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  for (int64_t base = (int64_t)blockIdx.x * kEmitThreads; base < P;
-       base += (int64_t)gridDim.x * kEmitThreads) {
-    // Wave 0: largest g with offs[g] <= base, by 64-ary search (offs strictly increasing: every
-    // Gaussian touches >= 1 tile, so offs[0] = 0 <= base).
-    if (wid == 0) {
-      int64_t lo = 0, hi = K - 1;
-      while (hi - lo >= 64) {
-        const int64_t step = (hi - lo + 64) / 64;
-        const int64_t idx = lo + (int64_t)lane * step;
-        const bool le = idx <= hi && offs[idx] <= base;
-        const unsigned long long m = __ballot(le);
-        const int last = 63 - __clzll((long long)m);
-        lo = lo + (int64_t)last * step;
-        hi = (lo + step - 1) < hi ? (lo + step - 1) : hi;
-      }
-      const int64_t idx = lo + lane;
-      const bool le = idx <= hi && offs[idx] <= base;
-      const unsigned long long m = __ballot(le);
-      if (lane == 0) s_g0 = lo + (63 - __clzll((long long)m));
-    }
-    __syncthreads();
-    const int64_t g0 = s_g0;
-    // The pairs [base, base+256) belong to Gaussians g0 .. g0+255 (each has >= 1 pair).
-    for (int i = threadIdx.x; i <= kEmitThreads; i += kEmitThreads)
-      s_offs[i] = (g0 + i <= K) ? offs[g0 + i] : INT64_MAX;
-    __syncthreads();
-    const int64_t pi = base + threadIdx.x;
-    if (pi < P) {
-      int lo = 0, hi = kEmitThreads - 1;  // largest i with s_offs[i] <= pi
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (s_offs[mid] <= pi) lo = mid; else hi = mid - 1;
-      }
-      const int64_t g = g0 + lo;
-      const int32_t local = (int32_t)(pi - s_offs[lo]);
-      const int4 r = rect[g];
-      const int32_t w = r.w - r.z + 1;
-      const int32_t tr = r.x + local / w;
-      const int32_t tc = r.z + local % w;
-      const int64_t t = (int64_t)tr * p.C + tc;
-      const unsigned long long pos = atomicAdd(cursor + t, 1ull);
-      if ((int64_t)pos < capacity) ids[pos] = g;
-      else set_status(&hdr->status, GF_STATUS_CAPACITY);
-    }
-    __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int64_t g = (int64_t)blockIdx.x * (kEmitThreads / 64) +
+                    __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
+  if (g >= p.K) return;
+  const int4 r = rect[g];
+  const int32_t w = r.w - r.z + 1;
+  const int32_t n = (r.y - r.x + 1) * w;
+  for (int32_t l = lane; l < n; l += 64) {
+    const int32_t dr = (int32_t)((uint32_t)l / (uint32_t)w);
+    const int32_t tr = r.x + dr, tc = r.z + (l - dr * w);
+    const unsigned long long pos = atomicAdd(cursor + (int64_t)tr * p.C + tc, 1ull);
+    if ((int64_t)pos < capacity) ids[pos] = g;
+    else set_status(&hdr->status, GF_STATUS_CAPACITY);
   }
 }
+
 
 // ------------------------------------------------------------------------------------------
 // Canonical (ascending) order of a tile's id segment.
@@ -690,7 +735,7 @@ __device__ inline void tile_range(const int64_t* __restrict__ tile_ptr, int64_t 
 // a time and broadcast with readlane while every lane accumulates its 4 pixels.
 __global__ __launch_bounds__(kTileThreads) void k_render16(
     Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
-    const float* __restrict__ mu, const float* __restrict__ chol_raw, const float* __restrict__ amp,
+    const GaussEval* __restrict__ ev, const float* __restrict__ amp,
     const int64_t* __restrict__ tile_ptr, int64_t* ids, int64_t capacity, float* __restrict__ delta,
     uint8_t* ws) {
   __shared__ int32_t wkeys[kTileThreads / 64][kWaveSortKeys];
@@ -716,8 +761,12 @@ __global__ __launch_bounds__(kTileThreads) void k_render16(
       GaussEval my = zero_eval();
       if (lane < nj) {
         const int64_t g = (n <= kWaveSortKeys) ? (int64_t)keys[j0 + lane] : seg[j0 + lane];
-        if (g >= 0 && g < p.K) my = eval_geom(p, mu, chol_raw, amp, g);
-        else set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);  // internal mismatch only
+        if (g >= 0 && g < p.K) {
+          my = load_eval(ev, g);
+          my.w *= amp[g];
+        } else {
+          set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);  // internal mismatch only
+        }
       }
       for (int j = 0; j < nj; ++j) {
         const float mu0 = readlane_f(my.mu0, j), mu1 = readlane_f(my.mu1, j);
@@ -750,7 +799,7 @@ __global__ __launch_bounds__(kTileThreads) void k_render16(
 // Any tile shape: each thread evaluates pixels p = tid, tid+256, ... of the tile.
 __global__ __launch_bounds__(kTileThreads) void k_render_any(
     Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
-    const float* __restrict__ mu, const float* __restrict__ chol_raw, const float* __restrict__ amp,
+    const GaussEval* __restrict__ ev, const float* __restrict__ amp,
     const int64_t* __restrict__ tile_ptr, int64_t* ids, int64_t capacity, float* __restrict__ delta,
     uint8_t* ws) {
   __shared__ int32_t keys[kSortLdsWords];
@@ -781,7 +830,9 @@ __global__ __launch_bounds__(kTileThreads) void k_render_any(
       if ((int)threadIdx.x < nj) {
         const int64_t g = keys_in_lds ? (int64_t)keys[j0 + threadIdx.x] : seg[j0 + threadIdx.x];
         if (g >= 0 && g < p.K) {
-          gl[threadIdx.x] = eval_geom(p, mu, chol_raw, amp, g);
+          GaussEval v = load_eval(ev, g);
+          v.w *= amp[g];
+          gl[threadIdx.x] = v;
         } else {
           gl[threadIdx.x] = zero_eval();
           set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);
@@ -829,7 +880,8 @@ __device__ inline void backward_tile_checks(const Problem& p, const Idx* __restr
 template <typename GIdx>
 __device__ inline void stage_gaussians(const Problem& p, const GIdx* __restrict__ gids, int64_t s,
                                        int64_t j0, int nj, const float* __restrict__ mu,
-                                       const float* __restrict__ chol_raw, GaussEval* gl,
+                                       const float* __restrict__ chol_raw,
+                                       const GaussEval* __restrict__ ev, GaussEval* gl,
                                        int32_t* gid_lds, uint32_t* status) {
   if ((int)threadIdx.x < nj) {
     const int64_t g = (int64_t)gids[s + j0 + threadIdx.x];
@@ -838,7 +890,7 @@ __device__ inline void stage_gaussians(const Problem& p, const GIdx* __restrict_
       gid_lds[threadIdx.x] = -1;
       gl[threadIdx.x] = zero_eval();
     } else {
-      gl[threadIdx.x] = eval_geom(p, mu, chol_raw, nullptr, g);
+      gl[threadIdx.x] = ev ? load_eval(ev, g) : eval_geom(p, mu, chol_raw, nullptr, g);
       gid_lds[threadIdx.x] = (int32_t)g;
     }
   }
@@ -852,8 +904,9 @@ template <typename TpIdx, typename GIdx>
 __global__ __launch_bounds__(kTileThreads) void k_bwd16(
     Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
-    const float* __restrict__ chol_raw, const TpIdx* __restrict__ tile_ptr,
-    const GIdx* __restrict__ gids, int64_t num_pairs, uint8_t* ws, BwdLayout L) {
+    const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
+    const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
+    uint8_t* ws, BwdLayout L) {
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   float* acc = reinterpret_cast<float*>(ws + L.acc);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -902,7 +955,7 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd16(
       if (g < 0 || g >= p.K) {
         set_status(&hdr->status, g < 0 ? GF_STATUS_IDS_NEGATIVE : GF_STATUS_IDS_RANGE);
       } else {
-        my = eval_geom(p, mu, chol_raw, nullptr, g);
+        my = ev ? load_eval(ev, g) : eval_geom(p, mu, chol_raw, nullptr, g);
         myg = (int32_t)g;
       }
     }
@@ -930,13 +983,15 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd16(
       }
       float m[6] = {t0, dx * t0, t2, dx * dx * t0, dx * t2, t3};
 #pragma unroll
-      for (int k = 0; k < 6; ++k) {
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) m[k] += __shfl_xor(m[k], o, 16);
-      }
-      if (g >= 0 && row < 6) {
-        const float val = row == 0 ? m[0] : row == 1 ? m[1] : row == 2 ? m[2] : row == 3 ? m[3] : row == 4 ? m[4] : m[5];
-        unsafeAtomicAdd(acc + 8 * (int64_t)g + row, val);
+      for (int k = 0; k < 6; ++k) m[k] = dpp_row_sum_f32(m[k]);
+      // Lane 15 of each 16-lane row holds the six sums; moment k moves to lane 10 + k
+      // (row_shl by 5 - k) and lanes 10..15 issue one atomic each.
+      const float v0 = dpp_f32<0x105>(m[0]), v1 = dpp_f32<0x104>(m[1]), v2 = dpp_f32<0x103>(m[2]);
+      const float v3 = dpp_f32<0x102>(m[3]), v4 = dpp_f32<0x101>(m[4]);
+      if (g >= 0 && row >= 10) {
+        const int k = row - 10;
+        const float val = k == 0 ? v0 : k == 1 ? v1 : k == 2 ? v2 : k == 3 ? v3 : k == 4 ? v4 : m[5];
+        unsafeAtomicAdd(acc + 8 * (int64_t)g + k, val);
       }
     }
   }
@@ -953,8 +1008,9 @@ template <typename TpIdx, typename GIdx>
 __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
     Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
-    const float* __restrict__ chol_raw, const TpIdx* __restrict__ tile_ptr,
-    const GIdx* __restrict__ gids, int64_t num_pairs, uint8_t* ws, BwdLayout L) {
+    const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
+    const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
+    uint8_t* ws, BwdLayout L) {
   __shared__ GaussEval gl[kTileThreads];
   __shared__ int32_t gid_lds[kTileThreads];
   __shared__ float red[kTileThreads / 64][8];
@@ -973,7 +1029,7 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
   for (int64_t j0 = 0; j0 < n; j0 += kTileThreads) {
     const int nj = (int)((n - j0) < kTileThreads ? (n - j0) : kTileThreads);
     __syncthreads();
-    stage_gaussians<GIdx>(p, gids, s, j0, nj, mu, chol_raw, gl, gid_lds, &hdr->status);
+    stage_gaussians<GIdx>(p, gids, s, j0, nj, mu, chol_raw, ev, gl, gid_lds, &hdr->status);
     __syncthreads();
     for (int j = 0; j < nj; ++j) {
       const int32_t g = gid_lds[j];
@@ -1130,14 +1186,15 @@ unsigned wave_tile_grid(int64_t T) { return (unsigned)((T + kTileThreads / 64 - 
 
 template <typename TP, typename GI>
 void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, const float* rc,
-                const float* cc, const float* mu, const float* raw, const void* tile_ptr,
-                const void* gids, int64_t num_pairs, uint8_t* ws, const BwdLayout& L) {
+                const float* cc, const float* mu, const float* raw, const GaussEval* ev,
+                const void* tile_ptr, const void* gids, int64_t num_pairs, uint8_t* ws,
+                const BwdLayout& L) {
   if (fast16(p))
-    hipLaunchKernelGGL((k_bwd16<TP, GI>), dim3(wave_tile_grid((int64_t)p.R * p.C)), dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw,
-                       reinterpret_cast<const TP*>(tile_ptr), reinterpret_cast<const GI*>(gids),
-                       num_pairs, ws, L);
+    hipLaunchKernelGGL((k_bwd16<TP, GI>), dim3(wave_tile_grid((int64_t)p.R * p.C)), dim3(kTileThreads), 0, st,
+                       p, grad, rc, cc, mu, raw, ev, reinterpret_cast<const TP*>(tile_ptr),
+                       reinterpret_cast<const GI*>(gids), num_pairs, ws, L);
   else
-    hipLaunchKernelGGL((k_bwd_any<TP, GI>), grid, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw,
+    hipLaunchKernelGGL((k_bwd_any<TP, GI>), grid, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw, ev,
                        reinterpret_cast<const TP*>(tile_ptr), reinterpret_cast<const GI*>(gids),
                        num_pairs, ws, L);
 }
@@ -1204,8 +1261,8 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
 }
 
 int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                    int64_t* gaussian_ids_sorted, int64_t ids_capacity, int64_t pairs_hint,
-                    void* workspace, size_t workspace_bytes, void* stream) {
+                    int64_t* gaussian_ids_sorted, int64_t ids_capacity, void* workspace,
+                    size_t workspace_bytes, void* stream) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
@@ -1216,9 +1273,7 @@ int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in
     return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / ids_capacity invalid");
   if (k == 0) return GF_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  int64_t work = pairs_hint > 0 ? pairs_hint : (ids_capacity > 0 ? ids_capacity : 1);
-  int64_t blocks = (work + kEmitThreads - 1) / kEmitThreads;
-  blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, 1 << 16));
+  const int64_t blocks = (k + kEmitThreads / 64 - 1) / (kEmitThreads / 64);
   hipLaunchKernelGGL(k_emit, dim3((unsigned)blocks), dim3(kEmitThreads), 0, st, p,
                      reinterpret_cast<uint8_t*>(workspace), L, gaussian_ids_sorted, ids_capacity);
   GF_LAUNCH_CHECK("k_emit");
@@ -1226,10 +1281,9 @@ int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in
 }
 
 int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                      const float* row_coords, const float* col_coords, const float* mu,
-                      const float* chol_raw, const float* amp, const int64_t* tile_ptr,
-                      int64_t* gaussian_ids_sorted, int64_t ids_capacity, float* delta,
-                      void* workspace, size_t workspace_bytes, void* stream) {
+                      const float* row_coords, const float* col_coords, const float* amp,
+                      const int64_t* tile_ptr, int64_t* gaussian_ids_sorted, int64_t ids_capacity,
+                      float* delta, void* workspace, size_t workspace_bytes, void* stream) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
@@ -1241,17 +1295,16 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
     return set_err(GF_E_INVALID_ARGUMENT, "coords / tile_ptr / delta must not be NULL");
   if (ids_capacity < 0 || (ids_capacity > 0 && !gaussian_ids_sorted))
     return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / ids_capacity invalid");
-  if (k > 0 && (!mu || !chol_raw || !amp)) return set_err(GF_E_INVALID_ARGUMENT, "mu / chol_raw / amp must not be NULL");
+  if (k > 0 && !amp) return set_err(GF_E_INVALID_ARGUMENT, "amp must not be NULL");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  const GaussEval* ev = reinterpret_cast<const GaussEval*>(ws + L.eval);
   if (fast16(p))
     hipLaunchKernelGGL(k_render16, dim3(wave_tile_grid(T)), dim3(kTileThreads), 0, st, p, row_coords,
-                       col_coords, mu, chol_raw, amp, tile_ptr, gaussian_ids_sorted, ids_capacity,
-                       delta, ws);
+                       col_coords, ev, amp, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws);
   else
     hipLaunchKernelGGL(k_render_any, dim3((unsigned)T), dim3(kTileThreads), 0, st, p, row_coords,
-                       col_coords, mu, chol_raw, amp, tile_ptr, gaussian_ids_sorted, ids_capacity,
-                       delta, ws);
+                       col_coords, ev, amp, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws);
   GF_LAUNCH_CHECK("k_render");
   return GF_OK;
 }
@@ -1260,7 +1313,8 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
                        const float* grad_delta, const float* row_coords, const float* col_coords,
                        const float* mu, const float* chol_raw, const void* tile_ptr,
                        int32_t tile_ptr_is_int64, const void* gaussian_ids, int32_t ids_is_int64,
-                       int64_t num_pairs, void* workspace, size_t workspace_bytes, void* stream) {
+                       int64_t num_pairs, const void* forward_workspace, void* workspace,
+                       size_t workspace_bytes, void* stream) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
@@ -1275,15 +1329,18 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
   if (k > 0 && (!mu || !chol_raw)) return set_err(GF_E_INVALID_ARGUMENT, "mu / chol_raw must not be NULL");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  const GaussEval* ev = forward_workspace
+      ? reinterpret_cast<const GaussEval*>(reinterpret_cast<const uint8_t*>(forward_workspace) + fwd_layout(k, T).eval)
+      : nullptr;
   const dim3 grid((unsigned)T);
   if (tile_ptr_is_int64 && ids_is_int64)
-    launch_bwd<int64_t, int64_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, tile_ptr, gaussian_ids, num_pairs, ws, L);
+    launch_bwd<int64_t, int64_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs, ws, L);
   else if (tile_ptr_is_int64)
-    launch_bwd<int64_t, int32_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, tile_ptr, gaussian_ids, num_pairs, ws, L);
+    launch_bwd<int64_t, int32_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs, ws, L);
   else if (ids_is_int64)
-    launch_bwd<int32_t, int64_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, tile_ptr, gaussian_ids, num_pairs, ws, L);
+    launch_bwd<int32_t, int64_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs, ws, L);
   else
-    launch_bwd<int32_t, int32_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, tile_ptr, gaussian_ids, num_pairs, ws, L);
+    launch_bwd<int32_t, int32_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs, ws, L);
   GF_LAUNCH_CHECK("k_bwd");
   return GF_OK;
 }
@@ -1312,12 +1369,12 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
                 const float* grad_delta, const float* row_coords, const float* col_coords,
                 const float* mu, const float* chol_raw, const float* amp, const void* tile_ptr,
                 int32_t tile_ptr_is_int64, const void* gaussian_ids, int32_t ids_is_int64,
-                int64_t num_pairs, float* d_mu, float* d_chol_raw, float* d_amp, void* workspace,
-                size_t workspace_bytes, void* stream) {
+                int64_t num_pairs, float* d_mu, float* d_chol_raw, float* d_amp,
+                const void* forward_workspace, void* workspace, size_t workspace_bytes, void* stream) {
   if (k > 0 && !amp) return set_err(GF_E_INVALID_ARGUMENT, "amp must not be NULL");
   int rc = gf_backward_reduce(cfg, out_features, in_features, k, grad_delta, row_coords, col_coords,
                               mu, chol_raw, tile_ptr, tile_ptr_is_int64, gaussian_ids, ids_is_int64,
-                              num_pairs, workspace, workspace_bytes, stream);
+                              num_pairs, forward_workspace, workspace, workspace_bytes, stream);
   if (rc) return rc;
   return gf_backward_finish(cfg, out_features, in_features, k, chol_raw, amp, d_mu, d_chol_raw, d_amp,
                             workspace, workspace_bytes, stream);

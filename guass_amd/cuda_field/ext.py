@@ -91,6 +91,18 @@ def gaussian_field_forward(row_coords: Tensor, col_coords: Tensor, mu: Tensor, c
                            amp: Tensor, tile_out: int, tile_in: int, sigma_multiplier: float,
                            normalize: bool, clamp_quad: float | None):
     """Returns (delta f32[M*N], tile_ptr i64[T+1], gaussian_ids_sorted i64[P])."""
+    delta, tile_ptr, ids, _ = forward_with_workspace(row_coords, col_coords, mu, chol_raw, amp,
+                                                     tile_out, tile_in, sigma_multiplier, normalize,
+                                                     clamp_quad)
+    return delta, tile_ptr, ids
+
+
+def forward_with_workspace(row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol_raw: Tensor,
+                           amp: Tensor, tile_out: int, tile_in: int, sigma_multiplier: float,
+                           normalize: bool, clamp_quad: float | None):
+    """gaussian_field_forward plus its forward workspace, which holds the Gaussians' evaluation
+    constants; passing it to gaussian_field_backward(forward_workspace=...) with the same
+    parameters skips recomputing them."""
     validate_forward_inputs(row_coords, col_coords, mu, chol_raw, amp)
     _check_config(tile_out, tile_in, sigma_multiplier)
     dev = _same_device(row_coords, col_coords, mu, chol_raw, amp)
@@ -114,13 +126,13 @@ def gaussian_field_forward(row_coords: Tensor, col_coords: Tensor, mu: Tensor, c
                                  ws.data_ptr(), ws_bytes, stream), "gaussian_field_forward (binning)")
         ids = torch.empty(P.value, dtype=torch.int64, device=dev)
         delta = torch.empty(M * Nf, dtype=torch.float32, device=dev)
-        N.check(L.gf_forward_emit(ctypes.byref(cfg), M, Nf, K, N.ptr(ids), P.value, P.value,
+        N.check(L.gf_forward_emit(ctypes.byref(cfg), M, Nf, K, N.ptr(ids), P.value,
                                   ws.data_ptr(), ws_bytes, stream), "gaussian_field_forward (emit)")
         N.check(L.gf_forward_render(ctypes.byref(cfg), M, Nf, K, row_coords.data_ptr(),
-                                    col_coords.data_ptr(), N.ptr(mu), N.ptr(chol_raw), N.ptr(amp),
-                                    tile_ptr.data_ptr(), N.ptr(ids), P.value, delta.data_ptr(),
-                                    ws.data_ptr(), ws_bytes, stream), "gaussian_field_forward (render)")
-    return delta, tile_ptr, ids
+                                    col_coords.data_ptr(), N.ptr(amp), tile_ptr.data_ptr(),
+                                    N.ptr(ids), P.value, delta.data_ptr(), ws.data_ptr(), ws_bytes,
+                                    stream), "gaussian_field_forward (render)")
+    return delta, tile_ptr, ids, ws
 
 
 # ------------------------------------------------------------------ backward
@@ -134,7 +146,7 @@ _SAVED_STATE_MESSAGES = (  # order of the reference checks, field_impl.cu:92-106
 
 
 def _backward(grad_delta, row_coords, col_coords, mu, chol_raw, amp, tile_ptr, gaussian_ids_sorted,
-              tile_out, tile_in, sigma_multiplier, normalize, clamp_quad):
+              tile_out, tile_in, sigma_multiplier, normalize, clamp_quad, forward_workspace):
     # validate_backward_inputs (field_impl.cu:73-84)
     _check_f32(grad_delta, "grad_delta")
     _check_f32(row_coords, "saved.row_coords")
@@ -173,6 +185,13 @@ def _backward(grad_delta, row_coords, col_coords, mu, chol_raw, amp, tile_ptr, g
         stream = N.stream_handle(dev)
         ws_bytes = L.gf_backward_workspace_bytes(M, Nf, K, ctypes.byref(cfg))
         ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+        fwd_ptr = None
+        if forward_workspace is not None:
+            need = L.gf_forward_workspace_bytes(M, Nf, K, ctypes.byref(cfg))
+            if (forward_workspace.device != dev or forward_workspace.dtype != torch.uint8
+                    or forward_workspace.numel() < need):
+                raise RuntimeError("forward_workspace does not belong to this field's forward")
+            fwd_ptr = forward_workspace.data_ptr()
         d_mu = torch.empty(K, 2, dtype=torch.float32, device=dev)
         d_chol_raw = torch.empty(K, 3, dtype=torch.float32, device=dev)
         d_amp = torch.empty(K, 1, dtype=torch.float32, device=dev)
@@ -181,7 +200,7 @@ def _backward(grad_delta, row_coords, col_coords, mu, chol_raw, amp, tile_ptr, g
                               tile_ptr.data_ptr(), int(tile_ptr.dtype == torch.int64),
                               N.ptr(gaussian_ids_sorted), int(gaussian_ids_sorted.dtype == torch.int64),
                               gaussian_ids_sorted.numel(), N.ptr(d_mu), N.ptr(d_chol_raw), N.ptr(d_amp),
-                              ws.data_ptr(), ws_bytes, stream), "gaussian_field_backward")
+                              fwd_ptr, ws.data_ptr(), ws_bytes, stream), "gaussian_field_backward")
         if VALIDATE_SAVED_STATE:
             status = ctypes.c_uint32(0)
             N.check(L.gf_read_status(ws.data_ptr(), 0, ctypes.byref(status), stream), "gf_read_status")
@@ -194,10 +213,15 @@ def _backward(grad_delta, row_coords, col_coords, mu, chol_raw, amp, tile_ptr, g
 def gaussian_field_backward(grad_delta: Tensor, row_coords: Tensor, col_coords: Tensor, mu: Tensor,
                             chol_raw: Tensor, amp: Tensor, tile_ptr: Tensor,
                             gaussian_ids_sorted: Tensor, tile_out: int, tile_in: int,
-                            sigma_multiplier: float, normalize: bool, clamp_quad: float | None):
-    """Returns [d_mu f32[K,2], d_chol_raw f32[K,3], d_amp f32[K,1]]."""
+                            sigma_multiplier: float, normalize: bool, clamp_quad: float | None,
+                            *, forward_workspace: Tensor | None = None):
+    """Returns [d_mu f32[K,2], d_chol_raw f32[K,3], d_amp f32[K,1]].
+
+    ``forward_workspace`` (keyword, optional): the workspace from ``forward_with_workspace`` over
+    the same parameters, whose Gaussian constants are then reused."""
     return _backward(grad_delta, row_coords, col_coords, mu, chol_raw, amp, tile_ptr,
-                     gaussian_ids_sorted, tile_out, tile_in, sigma_multiplier, normalize, clamp_quad)
+                     gaussian_ids_sorted, tile_out, tile_in, sigma_multiplier, normalize, clamp_quad,
+                     forward_workspace)
 
 
 def gaussian_field_backward_reference(grad_delta: Tensor, row_coords: Tensor, col_coords: Tensor,
@@ -209,4 +233,5 @@ def gaussian_field_backward_reference(grad_delta: Tensor, row_coords: Tensor, co
     (its delta has no grad_fn, backward.cu:500-539); this returns the same gradients as
     ``gaussian_field_backward``, which tests pin against the CPU autograd oracle."""
     return _backward(grad_delta, row_coords, col_coords, mu, chol_raw, amp, tile_ptr,
-                     gaussian_ids_sorted, tile_out, tile_in, sigma_multiplier, normalize, clamp_quad)
+                     gaussian_ids_sorted, tile_out, tile_in, sigma_multiplier, normalize, clamp_quad,
+                     None)

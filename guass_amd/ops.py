@@ -57,34 +57,38 @@ class FieldPlan:
                                        self.num_pairs.data_ptr(), None, self.fwd_ws.data_ptr(),
                                        self.fwd_ws_bytes, self._stream()), "gf_forward_bin")
 
-    def emit(self, pairs_hint: int = 0) -> None:
+    def emit(self) -> None:
         N.check(N.lib().gf_forward_emit(ctypes.byref(self.cfg), self.M, self.N, self.K,
-                                        self.ids.data_ptr(), self.capacity,
-                                        pairs_hint if pairs_hint > 0 else self.capacity,
-                                        self.fwd_ws.data_ptr(), self.fwd_ws_bytes, self._stream()),
+                                        self.ids.data_ptr(), self.capacity, self.fwd_ws.data_ptr(),
+                                        self.fwd_ws_bytes, self._stream()),
                 "gf_forward_emit")
 
-    def render(self, row_coords, col_coords, mu, chol_raw, amp) -> torch.Tensor:
+    def render(self, row_coords, col_coords, amp) -> torch.Tensor:
+        """Renders from the Gaussian constants the last ``bin`` stored in the workspace."""
         N.check(N.lib().gf_forward_render(ctypes.byref(self.cfg), self.M, self.N, self.K,
-                                          row_coords.data_ptr(), col_coords.data_ptr(), N.ptr(mu),
-                                          N.ptr(chol_raw), N.ptr(amp), self.tile_ptr.data_ptr(),
-                                          self.ids.data_ptr(), self.capacity, self.delta.data_ptr(),
-                                          self.fwd_ws.data_ptr(), self.fwd_ws_bytes, self._stream()),
+                                          row_coords.data_ptr(), col_coords.data_ptr(), N.ptr(amp),
+                                          self.tile_ptr.data_ptr(), self.ids.data_ptr(), self.capacity,
+                                          self.delta.data_ptr(), self.fwd_ws.data_ptr(),
+                                          self.fwd_ws_bytes, self._stream()),
                 "gf_forward_render")
         return self.delta
 
-    def forward(self, row_coords, col_coords, mu, chol_raw, amp, pairs_hint: int = 0) -> torch.Tensor:
+    def forward(self, row_coords, col_coords, mu, chol_raw, amp) -> torch.Tensor:
         """Bins and renders into ``self.delta`` (and ``tile_ptr`` / ``ids``); returns delta."""
         self.bin(mu, chol_raw)
-        self.emit(pairs_hint)
-        return self.render(row_coords, col_coords, mu, chol_raw, amp)
+        self.emit()
+        return self.render(row_coords, col_coords, amp)
 
-    def backward_reduce(self, grad, row_coords, col_coords, mu, chol_raw, num_pairs: int | None = None):
+    def backward_reduce(self, grad, row_coords, col_coords, mu, chol_raw, num_pairs: int | None = None,
+                        reuse_forward: bool = True):
+        """Per-tile moments.  With ``reuse_forward`` the Gaussian constants come from the last
+        forward's workspace (same mu / chol_raw), else they are recomputed from mu / chol_raw."""
         n = self.capacity if num_pairs is None else int(num_pairs)
+        fwd = self.fwd_ws.data_ptr() if reuse_forward else None
         N.check(N.lib().gf_backward_reduce(ctypes.byref(self.cfg), self.M, self.N, self.K,
                                            grad.data_ptr(), row_coords.data_ptr(), col_coords.data_ptr(),
                                            N.ptr(mu), N.ptr(chol_raw), self.tile_ptr.data_ptr(), 1,
-                                           self.ids.data_ptr(), 1, n, self.bwd_ws.data_ptr(),
+                                           self.ids.data_ptr(), 1, n, fwd, self.bwd_ws.data_ptr(),
                                            self.bwd_ws_bytes, self._stream()), "gf_backward_reduce")
 
     def backward_finish(self, chol_raw, amp):
@@ -95,9 +99,10 @@ class FieldPlan:
                 "gf_backward_finish")
         return self.d_mu, self.d_chol_raw, self.d_amp
 
-    def backward(self, grad, row_coords, col_coords, mu, chol_raw, amp, num_pairs: int | None = None):
+    def backward(self, grad, row_coords, col_coords, mu, chol_raw, amp, num_pairs: int | None = None,
+                 reuse_forward: bool = True):
         """Gradients into ``d_mu``, ``d_chol_raw``, ``d_amp`` from the last forward's binning."""
-        self.backward_reduce(grad, row_coords, col_coords, mu, chol_raw, num_pairs)
+        self.backward_reduce(grad, row_coords, col_coords, mu, chol_raw, num_pairs, reuse_forward)
         return self.backward_finish(chol_raw, amp)
 
     def pairs(self) -> int:

@@ -70,7 +70,8 @@ size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, in
 
 /*
  * Forward phase 1 (binning): per-Gaussian geometry and sigma-box tile ranges, per-tile
- * Gaussian counts and their exclusive scan.
+ * Gaussian counts and their exclusive scan.  The workspace also receives each Gaussian's
+ * evaluation constants, which gf_forward_render and (optionally) gf_backward reuse.
  *   tile_ptr        [T+1] int64 out: tile t owns gaussian_ids_sorted[tile_ptr[t] : tile_ptr[t+1]]
  *   num_pairs_dev   [1] int64 out: P = tile_ptr[T] = sum over Gaussians of tiles touched
  *   num_pairs_host  optional: if non-NULL the call synchronises `stream` and stores P here
@@ -88,23 +89,22 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
  * Must follow gf_forward_bin on the same stream with the same workspace.
  *   gaussian_ids_sorted [ids_capacity] int64 out; pairs beyond the capacity are dropped and
  *                   GF_STATUS_CAPACITY is set
- *   pairs_hint      P if the caller knows it (sizes the grid), else <= 0 (ids_capacity is used)
  * Replaces reference forward.cu:465-482 (emit_tile_pairs_kernel + radix sort on the tile key).
  */
 int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                    int64_t* gaussian_ids_sorted, int64_t ids_capacity, int64_t pairs_hint,
+                    int64_t* gaussian_ids_sorted, int64_t ids_capacity,
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Forward phase 3 (render): puts every tile's ids in canonical order (gaussian id ascending;
  * with tile-major ranges this is the (tile, gaussian) order of a stable sort) and renders
- * delta-W.  Must follow gf_forward_emit on the same stream with the same workspace.
+ * delta-W.  Must follow gf_forward_emit on the same stream with the same workspace (the
+ * Gaussian geometry comes from the constants gf_forward_bin stored there; amp is read here).
  *   delta           [out_features*in_features] fp32 out, row-major; every element written
  * Replaces reference forward.cu:513-569 (tile_accumulate_kernel; delta needs no pre-zeroing).
  */
 int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                      const float* row_coords, const float* col_coords,
-                      const float* mu, const float* chol_raw, const float* amp,
+                      const float* row_coords, const float* col_coords, const float* amp,
                       const int64_t* tile_ptr, int64_t* gaussian_ids_sorted, int64_t ids_capacity,
                       float* delta, void* workspace, size_t workspace_bytes, void* stream);
 
@@ -116,6 +116,9 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
  *   tile_ptr        [T+1], int64 if tile_ptr_is_int64 else int32
  *   gaussian_ids    [num_pairs], int64 if ids_is_int64 else int32 (any order within a tile)
  *   d_mu [K,2], d_chol_raw [K,3], d_amp [K,1] fp32 out (fully written)
+ *   forward_workspace  optional: the workspace of the gf_forward_bin call over the same
+ *                   (mu, chol_raw) and config; its evaluation constants are reused instead of
+ *                   recomputed from mu / chol_raw.  NULL recomputes them.
  * Saved-state violations (non-monotone tile_ptr, tile_ptr[T] != num_pairs, ids outside
  * [0,K)) are detected on the device, the offending pairs skipped, and status bits set.
  * Replaces reference backward.cu:541-716 (backward_pair_reduce_train).
@@ -125,7 +128,7 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
                 const float* mu, const float* chol_raw, const float* amp,
                 const void* tile_ptr, int32_t tile_ptr_is_int64,
                 const void* gaussian_ids, int32_t ids_is_int64, int64_t num_pairs,
-                float* d_mu, float* d_chol_raw, float* d_amp,
+                float* d_mu, float* d_chol_raw, float* d_amp, const void* forward_workspace,
                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* First half of gf_backward (reference backward.cu:592-702: per-pair partials + reduce-by-key). */
@@ -134,7 +137,8 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
                        const float* mu, const float* chol_raw,
                        const void* tile_ptr, int32_t tile_ptr_is_int64,
                        const void* gaussian_ids, int32_t ids_is_int64, int64_t num_pairs,
-                       void* workspace, size_t workspace_bytes, void* stream);
+                       const void* forward_workspace, void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 /* Second half of gf_backward (reference backward.cu:436-496,704-715: cov -> chol_raw chain). */
 int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,

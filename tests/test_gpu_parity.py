@@ -271,6 +271,11 @@ def test_plan_sync_free_and_capacity(device):
     assert torch.equal(plan.ids[:P], ref[2])
     for a, b in zip((plan.d_mu, plan.d_chol_raw, plan.d_amp), ref[3:]):
         grad_close(a, b, "plan", rtol=1e-6)
+    # Gaussian constants recomputed from mu / chol_raw instead of reused from the forward.
+    fresh = [t.clone() for t in plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw,
+                                              q.amp, num_pairs=P, reuse_forward=False)]
+    for a, b in zip(fresh, ref[3:]):
+        grad_close(a, b, "plan without the forward's constants", rtol=1e-6)
     small = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=P // 2)
     small.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
     torch.cuda.synchronize()
@@ -293,13 +298,13 @@ def test_graph_replay_matches_eager(device):
     s = torch.cuda.Stream(device)
     s.wait_stream(torch.cuda.current_stream(device))
     with torch.cuda.stream(s):
-        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, pairs_hint=P)
+        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
         plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
     torch.cuda.current_stream(device).wait_stream(s)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, pairs_hint=P)
+        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
         plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
     for rep in range(3):
         plan.delta.fill_(float("nan"))
