@@ -14,6 +14,10 @@ import torch
 FWD_RTOL = 1e-5
 GRAD_RTOL = 1e-4
 
+# Order-independent checksum of F.softplus over all 2^32 fp32 inputs, computed from the host C
+# library by oracle/libm_sweep.c; the GPU self-test (gf_selftest_softplus) must reproduce it.
+SOFTPLUS_CHECKSUM = 0x06C0D4E444E1424F
+
 
 def binning_equal(tile_ptr, ids, tile_ptr_ref, ids_ref) -> None:
     tp = tile_ptr.detach().cpu().to(torch.int64)

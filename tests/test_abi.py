@@ -1,0 +1,147 @@
+"""The C ABI and the drop-in shim without a GPU.
+
+* libgaussfield.so loads and exports every function include/gaussfield.h declares (and the
+  ctypes binding declares the same set);
+* host-side argument validation returns the documented GF_E_* codes and messages before any
+  device work, so these calls are safe on a machine without a GPU;
+* the drop-in ``ext`` functions raise the reference's error messages for non-CUDA inputs and
+  bad configurations (common.h:8-24, field_impl.cu:52-71,143-145);
+* the runtime exports the names GaussianLinear and the patchers import (cuda_field/__init__.py).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from guass_amd import _native as N
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "gaussfield.h"
+
+GF_E_INVALID_ARGUMENT = 1
+GF_E_WORKSPACE = 2
+
+
+def declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"^[A-Za-z_][\w \t\*]*?\b(gf_\w+)\s*\(", text, flags=re.M))
+
+
+def test_header_error_codes():
+    text = HEADER.read_text()
+    assert re.search(r"#define\s+GF_E_INVALID_ARGUMENT\s+1\b", text)
+    assert re.search(r"#define\s+GF_E_WORKSPACE\s+2\b", text)
+    for name in ("CAPACITY", "COUNT_MISMATCH", "TILE_PTR_LAST", "TILE_PTR_ORDER", "IDS_NEGATIVE",
+                 "IDS_RANGE"):
+        m = re.search(rf"#define\s+GF_STATUS_{name}\s+(0x[0-9a-fA-F]+)u", text)
+        assert m and int(m.group(1), 16) == getattr(N, f"GF_STATUS_{name}"), name
+
+
+def test_library_exports_every_declared_symbol():
+    declared = declared_functions()
+    assert len(declared) >= 13
+    assert declared == set(N.EXPORTED)
+    lib = N.lib()
+    for name in sorted(declared):
+        assert hasattr(lib, name), f"{name} declared in include/gaussfield.h but not exported"
+    assert lib.gf_version().decode().startswith("gaussfield-mi355x")
+
+
+def _cfg(**kw):
+    base = dict(tile_out=16, tile_in=16, sigma_multiplier=3.0, normalize=False, clamp_quad=80.0)
+    base.update(kw)
+    return N.make_config(**base)
+
+
+def test_tile_grid_and_workspace_sizes():
+    lib = N.lib()
+    R, C = ctypes.c_int64(), ctypes.c_int64()
+    assert lib.gf_tile_grid(1280, 5120, ctypes.byref(_cfg()), ctypes.byref(R), ctypes.byref(C)) == 0
+    assert (R.value, C.value) == (80, 320)
+    assert lib.gf_tile_grid(45, 70, ctypes.byref(_cfg(tile_out=8, tile_in=24)), ctypes.byref(R),
+                            ctypes.byref(C)) == 0
+    assert (R.value, C.value) == (6, 3)
+    fwd = lib.gf_forward_workspace_bytes(1280, 1280, 1024, ctypes.byref(_cfg()))
+    bwd = lib.gf_backward_workspace_bytes(1280, 1280, 1024, ctypes.byref(_cfg()))
+    # header + 32 B constants + 16 B rectangle per Gaussian + 8 B cursor per tile; 32 B per
+    # Gaussian of accumulators
+    assert fwd >= 256 + 48 * 1024 + 8 * 6400 and fwd % 256 == 0
+    assert bwd >= 256 + 32 * 1024 and bwd % 256 == 0
+    assert lib.gf_forward_workspace_bytes(10, 10, 4, ctypes.byref(_cfg(tile_out=0))) == 0
+
+
+@pytest.mark.parametrize("kw,msg", [({"tile_out": 0}, "tile_out must be positive"),
+                                    ({"tile_in": -2}, "tile_in must be positive"),
+                                    ({"sigma_multiplier": 0.0}, "sigma_multiplier must be positive")])
+def test_invalid_config_is_rejected_before_device_work(kw, msg):
+    lib = N.lib()
+    R, C = ctypes.c_int64(), ctypes.c_int64()
+    rc = lib.gf_tile_grid(64, 64, ctypes.byref(_cfg(**kw)), ctypes.byref(R), ctypes.byref(C))
+    assert rc == GF_E_INVALID_ARGUMENT
+    assert msg in lib.gf_last_error().decode()
+    # the same check guards every entry point that takes a config
+    rc = lib.gf_forward_bin(ctypes.byref(_cfg(**kw)), 64, 64, 4, None, None, None, None, None,
+                            None, 0, None)
+    assert rc == GF_E_INVALID_ARGUMENT and msg in lib.gf_last_error().decode()
+
+
+def test_workspace_and_pointer_checks():
+    lib = N.lib()
+    cfg = _cfg()
+    need = lib.gf_forward_workspace_bytes(64, 64, 4, ctypes.byref(cfg))
+    rc = lib.gf_forward_bin(ctypes.byref(cfg), 64, 64, 4, None, None, None, None, None, None,
+                            need - 1, None)
+    assert rc == GF_E_WORKSPACE and "workspace" in lib.gf_last_error().decode()
+    rc = lib.gf_tile_grid(0, 64, ctypes.byref(cfg), None, None)
+    assert rc == GF_E_INVALID_ARGUMENT
+    rc = lib.gf_tile_grid(64, 64, None, None, None)
+    assert rc == GF_E_INVALID_ARGUMENT
+    rc = lib.gf_read_status(None, 0, None, None)
+    assert rc == GF_E_INVALID_ARGUMENT
+
+
+def test_shim_rejects_cpu_tensors_with_reference_messages():
+    from guass_amd.cuda_field import ext
+
+    M, Nn, K = 32, 48, 3
+    rc, cc = torch.linspace(-1, 1, M), torch.linspace(-1, 1, Nn)
+    mu, raw, amp = torch.zeros(K, 2), torch.zeros(K, 3), torch.zeros(K, 1)
+    with pytest.raises(RuntimeError, match="row_coords must be a CUDA tensor"):
+        ext.gaussian_field_forward(rc, cc, mu, raw, amp, 16, 16, 3.0, False, 80.0)
+    grad = torch.zeros(M * Nn)
+    tp, ids = torch.zeros(7, dtype=torch.int64), torch.zeros(0, dtype=torch.int64)
+    with pytest.raises(RuntimeError, match="grad_delta must be a CUDA tensor"):
+        ext.gaussian_field_backward(grad, rc, cc, mu, raw, amp, tp, ids, 16, 16, 3.0, False, 80.0)
+    with pytest.raises(RuntimeError, match="grad_delta must be a CUDA tensor"):
+        ext.gaussian_field_backward_reference(grad, rc, cc, mu, raw, amp, tp, ids, 16, 16, 3.0,
+                                              False, 80.0)
+
+
+def test_runtime_surface():
+    from guass_amd import cuda_field
+    from guass_amd.cuda_field import contracts, runtime
+
+    for name in ("gaussian_field_train", "gaussian_field_reference", "gaussian_field_forward_reference",
+                 "gaussian_field_cuda_field_stage2_validation", "load_extension"):
+        assert callable(getattr(cuda_field, name)), name
+    assert issubclass(runtime.GaussianFieldCudaTrainFunction, torch.autograd.Function)
+    assert issubclass(runtime.GaussianFieldCudaReferenceFunction, torch.autograd.Function)
+    th = contracts.CudaFieldStage0Thresholds()
+    assert th.default_sigma_multiplier == 3.0 and th.partial_grad_bytes_limit == 256 * 1024 * 1024
+    ext = cuda_field.load_extension()
+    for name in ("gaussian_field_forward", "gaussian_field_backward", "gaussian_field_backward_reference"):
+        assert callable(getattr(ext, name)), name
+
+
+def test_product_path_has_no_cpu_fallback(monkeypatch, tmp_path):
+    """Without the built library the product path raises instead of computing anything."""
+    monkeypatch.setattr(N, "_LIB", None)
+    monkeypatch.setattr(N, "LIB_PATH", tmp_path / "missing.so")
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        N.lib()

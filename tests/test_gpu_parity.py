@@ -17,12 +17,9 @@ from guass_amd import workloads as wl
 from guass_amd.cuda_field import ext, runtime
 from guass_amd.ops import FieldPlan
 from oracle import field_oracle as fo
-from tests.parity import binning_equal, field_close, grad_close
+from tests.parity import SOFTPLUS_CHECKSUM, binning_equal, field_close, grad_close
 
 pytestmark = pytest.mark.gpu
-
-# checksum of F.softplus over all 2^32 fp32 inputs from the host C library (oracle/libm_sweep.c)
-SOFTPLUS_CHECKSUM = 0x06C0D4E444E1424F
 
 
 def say(msg: str) -> None:
@@ -316,3 +313,22 @@ def test_graph_replay_matches_eager(device):
         for a, b in zip((plan.d_mu, plan.d_chol_raw, plan.d_amp), eager[3:]):
             grad_close(a, b, f"replay {rep}", rtol=1e-6)
         _ = (eager[0] * 2.0).sum().item()  # eager work between replays
+
+
+def test_golden_fixture_tiny_ragged(device):
+    """The committed fixture (tests/golden/tiny_ragged.npz) through the product path."""
+    import numpy as np
+    from pathlib import Path
+
+    d = np.load(Path(__file__).resolve().parent / "golden" / "tiny_ragged.npz")
+    t = lambda k: torch.from_numpy(d[k].copy()).to(device)  # noqa: E731
+    say("golden tiny_ragged 45x70 K=12")
+    delta, tp, ids = ext.gaussian_field_forward(t("row_coords"), t("col_coords"), t("mu"), t("chol_raw"),
+                                                t("amp"), 16, 16, 3.0, False, 80.0)
+    grads = ext.gaussian_field_backward(t("grad"), t("row_coords"), t("col_coords"), t("mu"),
+                                        t("chol_raw"), t("amp"), tp, ids, 16, 16, 3.0, False, 80.0)
+    torch.cuda.synchronize()
+    binning_equal(tp, ids, torch.from_numpy(d["tile_ptr"]), torch.from_numpy(d["gaussian_ids"]))
+    field_close(delta, torch.from_numpy(d["delta"]))
+    for name, a in zip(("d_mu", "d_chol_raw", "d_amp"), grads):
+        grad_close(a, torch.from_numpy(d[name]), name)
