@@ -2,6 +2,7 @@
 (reference gaussian_peft/cuda_field/__init__.py:1-32)."""
 
 from guass_amd.cuda_field.contracts import (
+    GaussianFieldCudaFunctionStage0,
     NON_DIFFERENTIABLE_ARGS,
     SAVED_TENSOR_SPEC,
     STAGE0_THRESHOLDS,
@@ -26,6 +27,7 @@ __all__ = [
     "CUDA_FIELD_EXTENSION_NAME",
     "CUDA_FIELD_REFERENCE_EXTENSION_NAME",
     "CUDA_FIELD_SOURCES",
+    "GaussianFieldCudaFunctionStage0",
     "NON_DIFFERENTIABLE_ARGS",
     "SAVED_TENSOR_SPEC",
     "STAGE0_THRESHOLDS",

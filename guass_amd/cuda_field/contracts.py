@@ -1,4 +1,4 @@
-"""Tensor contract of the Gaussian-field path (gaussian_peft/cuda_field/contracts.py:8-62).
+"""Tensor contract of the Gaussian-field path (gaussian_peft/cuda_field/contracts.py:8-174).
 
 Kept with the same names and values so code that imports them keeps working.  The
 thresholds are the reference's tiled-vs-dense error bounds; they are informational (the
@@ -8,6 +8,8 @@ reference exports them without consuming them).
 from __future__ import annotations
 
 from dataclasses import dataclass
+
+import torch
 
 
 @dataclass(frozen=True, slots=True)
@@ -63,3 +65,22 @@ SAVED_TENSOR_SPEC = CudaFieldSavedTensorSpec()
 NON_DIFFERENTIABLE_ARGS = CudaFieldNonDifferentiableArgs()
 SAVED_TENSOR_ORDER = ("row_coords", "col_coords", "mu", "chol_raw", "amp", "tile_ptr",
                       "gaussian_ids_sorted")
+
+
+class GaussianFieldCudaFunctionStage0(torch.autograd.Function):
+    """Signature skeleton of the path's autograd Function (contracts.py:64-174).
+
+    Forward: (row_coords, col_coords, mu, chol_raw, amp, tile_out, tile_in, sigma_multiplier,
+    normalize, clamp_quad) -> delta, saving the seven tensors of SAVED_TENSOR_ORDER.  Backward
+    returns (None, None, d_mu, d_chol_raw, d_amp, None x 5).  Like the reference's, it only
+    freezes the signature; GaussianFieldCudaTrainFunction (runtime.py) implements it.
+    """
+
+    @staticmethod
+    def forward(ctx, row_coords, col_coords, mu, chol_raw, amp, tile_out, tile_in,
+                sigma_multiplier, normalize, clamp_quad):
+        raise NotImplementedError("Stage 0 signature skeleton only.")
+
+    @staticmethod
+    def backward(ctx, grad_delta):
+        raise NotImplementedError("Stage 0 signature skeleton only.")

@@ -139,6 +139,25 @@ def test_runtime_surface():
         assert callable(getattr(ext, name)), name
 
 
+# names exported by gaussian_peft/cuda_field/__init__.py:20-35
+REFERENCE_CUDA_FIELD_ALL = (
+    "CUDA_FIELD_EXTENSION_NAME", "CUDA_FIELD_REFERENCE_EXTENSION_NAME", "CUDA_FIELD_SOURCES",
+    "GaussianFieldCudaFunctionStage0", "NON_DIFFERENTIABLE_ARGS", "SAVED_TENSOR_SPEC",
+    "STAGE0_THRESHOLDS", "TENSOR_CONTRACT", "build_instructions", "gaussian_field_forward_reference",
+    "gaussian_field_reference", "gaussian_field_train", "get_source_paths", "load_extension",
+)
+
+
+def test_package_surface_covers_reference_names():
+    from guass_amd import cuda_field
+
+    missing = [n for n in REFERENCE_CUDA_FIELD_ALL if not hasattr(cuda_field, n)]
+    assert not missing, missing
+    assert set(REFERENCE_CUDA_FIELD_ALL) <= set(cuda_field.__all__)
+    with pytest.raises(NotImplementedError):
+        cuda_field.GaussianFieldCudaFunctionStage0.forward(None, *([None] * 10))
+
+
 def test_product_path_has_no_cpu_fallback(monkeypatch, tmp_path):
     """Without the built library the product path raises instead of computing anything."""
     monkeypatch.setattr(N, "_LIB", None)
