@@ -47,6 +47,11 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--kernel-reps", type=int, default=20, help="launches per per-kernel timing graph")
     ap.add_argument("--kernel-replays", type=int, default=25, help="timed replays per kernel graph")
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="first run one device-to-device copy of this many MiB (the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+    ap.add_argument("--traffic-file", default=str(ROOT / "profiles" / "cfg3_hbm_traffic.json"),
+                    help="per-kernel HBM bytes per launch measured with rocprofv3 --pmc")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -87,6 +92,20 @@ def roofline(bytes_: float, flops: float, seconds: float) -> dict:
             "frac": ach / (HBM_PEAK / 1e9)}
 
 
+def traffic_bytes(path: str, config: str, kernel: str):
+    """HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE, copy-calibrated) from the
+    committed rocprofv3 --pmc measurement, or None if there is none for this workload."""
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if data.get("config") != config:
+        return None
+    entry = data.get("kernels", {}).get(kernel)
+    return None if entry is None else float(entry["hbm_bytes_per_launch"])
+
+
 def cpu_baseline(problem, reps: int) -> dict:
     import torch
 
@@ -125,6 +144,14 @@ def main() -> int:
     from guass_amd.ops import FieldPlan
 
     dev = torch.device("cuda:0")
+    if args.calibrate_copy_mib > 0:
+        n = args.calibrate_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     prob = wl.CONFIGS[args.config](args.seed)
     q = prob.to(dev)
     M, N, K = prob.out_features, prob.in_features, prob.k
@@ -230,7 +257,8 @@ def main() -> int:
     }
     dominant = max(kernel_rooflines, key=lambda k: ph[k])
     roof = dict(kernel_rooflines[dominant])
-    roof.update({"kernel": dominant, "traffic": None, "duration_us": ph[dominant] * 1e3})
+    roof.update({"kernel": dominant, "traffic": traffic_bytes(args.traffic_file, args.config, dominant),
+                 "duration_us": ph[dominant] * 1e3})
     step_roof = roofline(counts["bytes_step"], counts["flops_fwd"] + counts["flops_bwd"],
                          ms_per_step / 1e3)
     out = {
