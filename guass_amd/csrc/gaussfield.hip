@@ -2,12 +2,12 @@
 //
 // Forward (reference forward.cu:372-569), three kernels:
 //   k_bin      one workgroup per field: bit-exact sigma-box tile rectangle of every Gaussian,
-//              its evaluation constants (kept in the workspace for the render and the
-//              backward), the pair total, per-tile Gaussian counts from row-wise difference
-//              arrays and their scan -> tile_ptr; every scan runs in LDS (DPP wave scans) and
-//              global memory is only written, coalesced.
-//   k_emit     one wave per Gaussian: a slot in each touched tile's range from a per-tile
-//              cursor (a counting sort on the tile key).
+//              the pair total, per-tile Gaussian counts from row-wise difference arrays and
+//              their scan -> tile_ptr; every scan runs in LDS (DPP wave scans) and global
+//              memory is only written, coalesced.
+//   k_emit     one wave per Gaussian: its evaluation constants (kept in the workspace for the
+//              render and the backward) and a slot in each touched tile's range from tile_ptr
+//              and a per-tile fill counter (a counting sort on the tile key).
 //   k_render16 one wave per 16x16 tile, four independent tiles per workgroup, no workgroup
 //              barriers: canonical (ascending gid) order of the tile's ids (written back),
 //              per-Gaussian constants loaded one Gaussian per lane and broadcast with
@@ -104,9 +104,10 @@ static_assert(sizeof(WsHeader) == 256, "workspace header must be 256 bytes");
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Forward workspace: header, per-Gaussian evaluation constants eval[K] (GaussEval), rect[K]
-// (int4 tile ranges), cursor[T] (next free slot of each tile's id segment).
+// (int4 tile ranges), cov[K] (float4: the fp32 covariance s00, s01, s11 and 0), fill[T]
+// (int32 ids emitted so far into each tile's segment).
 struct FwdLayout {
-  size_t eval, rect, cursor, total;
+  size_t eval, rect, cov, fill, total;
 };
 FwdLayout fwd_layout(int64_t K, int64_t T) {
   FwdLayout L;
@@ -115,8 +116,10 @@ FwdLayout fwd_layout(int64_t K, int64_t T) {
   o = align256(o + 32 * (size_t)K);
   L.rect = o;
   o = align256(o + sizeof(int4) * (size_t)K);
-  L.cursor = o;
-  o = align256(o + sizeof(int64_t) * (size_t)T);
+  L.cov = o;
+  o = align256(o + sizeof(float4) * (size_t)K);
+  L.fill = o;
+  o = align256(o + sizeof(int32_t) * (size_t)T);
   L.total = o;
   return L;
 }
@@ -370,6 +373,52 @@ __device__ inline void store_eval(GaussEval* ev, int64_t g, const GaussEval& v) 
 // registers between the phases of k_bin; the rest re-read it from the workspace.
 constexpr int kBinRectRegs = 4;
 
+// One wave scans whole rows of the band's difference array (lane l holds columns
+// j0 + l*V .. +V-1): counts are the inclusive prefix of the differences along the row, and
+// tile_ptr of a tile is its row's base plus the exclusive prefix of the counts.  Writes
+// tile_ptr and clears the tiles' fill counters directly.
+template <int V>
+__device__ inline void bin_scan_rows(const int32_t* lds, int32_t C, int32_t nb, int64_t b0,
+                                     const int64_t* rowbase, int64_t* __restrict__ tile_ptr,
+                                     int32_t* __restrict__ fill, int lane, int wid) {
+  for (int32_t row = wid; row < nb; row += kBinThreads / 64) {
+    const int32_t* rp = lds + row * C;
+    const int64_t out0 = (b0 + row) * (int64_t)C;
+    const int64_t base_off = rowbase[row];
+    int32_t carry_d = 0, carry_c = 0;
+    for (int32_t j0 = 0; j0 < C; j0 += 64 * V) {
+      const int32_t col0 = j0 + lane * V;
+      int32_t c[V];
+      int32_t run = 0;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        run += (col0 + v < C) ? rp[col0 + v] : 0;
+        c[v] = run;
+      }
+      const int32_t dinc = dpp_scan_i32(run);
+      const int32_t before = carry_d + dinc - run;  // count carried into this lane's first column
+      int32_t csum = 0;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        c[v] = (col0 + v < C) ? c[v] + before : 0;
+        csum += c[v];
+      }
+      const int32_t cinc = dpp_scan_i32(csum);
+      int32_t off = carry_c + cinc - csum;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        if (col0 + v < C) {
+          tile_ptr[out0 + col0 + v] = base_off + off;
+          fill[out0 + col0 + v] = 0;
+        }
+        off += c[v];
+      }
+      carry_d += __builtin_amdgcn_readlane(dinc, 63);
+      carry_c += __builtin_amdgcn_readlane(cinc, 63);
+    }
+  }
+}
+
 __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __restrict__ mu,
                                                      const float* __restrict__ chol_raw,
                                                      int64_t* __restrict__ tile_ptr,
@@ -377,27 +426,42 @@ __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __r
                                                      FwdLayout L) {
   __shared__ int32_t lds[kLdsDiffWords];
   __shared__ int64_t rowbase[kBinMaxBandRows + 1];
+  __shared__ int32_t rowdiff[kBinMaxBandRows + 1];
   __shared__ int64_t scan_lds[kBinThreads / 64 + 1];
+  __shared__ unsigned long long pairs_lds;
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
-  GaussEval* ev = reinterpret_cast<GaussEval*>(ws + L.eval);
   int4* rect = reinterpret_cast<int4*>(ws + L.rect);
-  int64_t* cursor = reinterpret_cast<int64_t*>(ws + L.cursor);
+  float4* covs = reinterpret_cast<float4*>(ws + L.cov);
+  int32_t* fill = reinterpret_cast<int32_t*>(ws + L.fill);
   const int64_t K = p.K, T = (int64_t)p.R * p.C;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  if (threadIdx.x == 0) hdr->status = 0u;
+  if (threadIdx.x == 0) {
+    hdr->status = 0u;
+    pairs_lds = 0ull;
+  }
 
-  // A: rectangles, pairs (tiles touched) and evaluation constants (the weight slot holds the
-  // normalisation; the render applies the amplitude).
+  // Per-tile counts go through LDS, band by band of whole tile rows, when the grid allows it.
+  const bool lds_path = p.C <= kLdsDiffWords && K * p.C < (int64_t)INT32_MAX;
+  const int32_t C = p.C;
+  const int32_t band_rows = lds_path ? min(kLdsDiffWords / C, kBinMaxBandRows) : 0;
+  auto clear_band = [&](int32_t nb) {
+    for (int32_t i = threadIdx.x; i < nb * C; i += kBinThreads) lds[i] = 0;
+    for (int32_t i = threadIdx.x; i <= nb; i += kBinThreads) rowdiff[i] = 0;
+  };
+  if (lds_path) clear_band(min(band_rows, p.R));
+
+  // A: tile rectangles, fp32 covariances and pairs (tiles touched); the first
+  // kBinRectRegs * kBinThreads Gaussians keep their rectangle in registers.  (Evaluation
+  // constants are computed from the stored covariances by k_emit, spread over the GPU.)
   int4 myrect[kBinRectRegs];
   int64_t my_pairs = 0;
   auto prep = [&](int64_t g) -> int4 {
     const GfChol Lc = gf_activate_cholesky(chol_raw[3 * g + 0], chol_raw[3 * g + 1], chol_raw[3 * g + 2]);
     const GfCov c = gf_cov_from_chol(Lc);
-    const float m0 = mu[2 * g + 0], m1 = mu[2 * g + 1];
     int32_t touched;
-    const int4 r = bin_rect(p, m0, m1, c, &touched);
+    const int4 r = bin_rect(p, mu[2 * g + 0], mu[2 * g + 1], c, &touched);
     rect[g] = r;
-    store_eval(ev, g, eval_from_cov(p, m0, m1, c, 1.0f));
+    covs[g] = make_float4(c.s00, c.s01, c.s11, 0.0f);
     my_pairs += touched;
     return r;
   };
@@ -408,75 +472,62 @@ __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __r
     if (g < K) myrect[i] = prep(g);
   }
   for (int64_t g = threadIdx.x + (int64_t)kBinRectRegs * kBinThreads; g < K; g += kBinThreads) prep(g);
+  // B: P = total pairs: wave sums, one LDS atomic per wave after the barrier that orders them
+  // behind the counter's initialisation; read by thread 0 after later barriers.
+  const int64_t wave_pairs = readlane_i64(wave_inclusive_scan(my_pairs), 63);
+  __syncthreads();
+  if (lane == 0) atomicAdd(&pairs_lds, (unsigned long long)wave_pairs);
 
-  // B: P = total pairs.
-  int64_t P;
-  (void)block_exclusive_scan<kBinThreads>(my_pairs, &P, scan_lds);
-
-  // C: per-tile counts and tile_ptr, band by band of whole tile rows.  Each covered row of each
-  // rectangle adds +1 at its first column and -1 after its last; one wave per row turns the
-  // differences into counts (inclusive scan) and the counts into row offsets (exclusive
-  // scan), the row totals are scanned, and tile_ptr / cursor are written coalesced.
+  // C: each covered row of each rectangle adds +1 at its first column and -1 after its last;
+  // the rectangle's width is added over its rows through a difference array over rows.  Wave
+  // 0 turns the row differences into row totals and row bases; then one wave per row scans
+  // the column differences into counts and the counts into tile_ptr (row base + exclusive
+  // prefix), written coalesced together with cleared fill counters.
   int64_t Pc = 0;
-  if (p.C <= kLdsDiffWords && K * p.C < (int64_t)INT32_MAX) {
-    const int64_t C = p.C;
-    int64_t band_rows = kLdsDiffWords / C;
-    if (band_rows > kBinMaxBandRows) band_rows = kBinMaxBandRows;
+  if (lds_path) {
     int64_t band_base = 0;
-    for (int64_t b0 = 0; b0 < p.R; b0 += band_rows) {
-      const int64_t nb = (p.R - b0) < band_rows ? (p.R - b0) : band_rows;
-      for (int64_t i = threadIdx.x; i < nb * C; i += kBinThreads) lds[i] = 0;
-      __syncthreads();
+    for (int32_t b0 = 0; b0 < p.R; b0 += band_rows) {
+      const int32_t nb = min(p.R - b0, band_rows);
+      if (b0 > 0) {
+        clear_band(nb);
+        __syncthreads();
+      }
       auto diff = [&](const int4 r) {
-        const int32_t rlo = r.x > (int32_t)b0 ? r.x : (int32_t)b0;
-        const int32_t rhi = r.y < (int32_t)(b0 + nb - 1) ? r.y : (int32_t)(b0 + nb - 1);
+        const int32_t rlo = max(r.x, b0), rhi = min(r.y, b0 + nb - 1);
+        if (rlo > rhi) return;
         for (int32_t row = rlo; row <= rhi; ++row) {
-          int32_t* d = lds + (row - (int32_t)b0) * (int32_t)C;
+          int32_t* d = lds + (row - b0) * C;
           atomicAdd(d + r.z, 1);
-          if (r.w + 1 < (int32_t)C) atomicAdd(d + r.w + 1, -1);
+          if (r.w + 1 < C) atomicAdd(d + r.w + 1, -1);
         }
+        const int32_t w = r.w - r.z + 1;
+        atomicAdd(rowdiff + (rlo - b0), w);
+        atomicAdd(rowdiff + (rhi + 1 - b0), -w);  // index <= nb
       };
 #pragma unroll
       for (int i = 0; i < kBinRectRegs; ++i) diff(myrect[i]);
       for (int64_t g = threadIdx.x + (int64_t)kBinRectRegs * kBinThreads; g < K; g += kBinThreads)
         diff(rect[g]);
       __syncthreads();
-      const int32_t Ci = (int32_t)C, nbi = (int32_t)nb;
-      for (int32_t row = wid; row < nbi; row += kBinThreads / 64) {
-        int32_t carry_d = 0, carry_c = 0;
-        for (int32_t j0 = 0; j0 < Ci; j0 += 64) {
-          const int32_t j = j0 + lane;
-          const int32_t dv = j < Ci ? lds[row * Ci + j] : 0;
-          const int32_t cnt = wave_inclusive_scan32(dv) + carry_d;
-          const int32_t cnt_in = j < Ci ? cnt : 0;
-          const int32_t inc = wave_inclusive_scan32(cnt_in);
-          if (j < Ci) lds[row * Ci + j] = carry_c + inc - cnt_in;  // exclusive offset in the row
-          carry_d = __builtin_amdgcn_readlane(cnt, 63);
-          carry_c += __builtin_amdgcn_readlane(inc, 63);
-        }
-        if (lane == 0) rowbase[row] = carry_c;  // row total (scanned below)
-      }
-      __syncthreads();
       if (wid == 0) {
         int64_t carry = 0;
-        for (int32_t r0 = 0; r0 < nbi; r0 += 64) {
+        int32_t carry_t = 0;
+        for (int32_t r0 = 0; r0 < nb; r0 += 64) {
           const int32_t r = r0 + lane;
-          const int64_t v = r < nbi ? rowbase[r] : 0;
-          const int64_t inc = wave_inclusive_scan(v);
-          if (r < nbi) rowbase[r] = band_base + carry + inc - v;
+          const int32_t dv = r < nb ? rowdiff[r] : 0;
+          const int32_t tinc = dpp_scan_i32(dv);
+          const int64_t tot = r < nb ? (int64_t)(carry_t + tinc) : 0;  // row total
+          const int64_t inc = wave_inclusive_scan(tot);
+          if (r < nb) rowbase[r] = band_base + carry + inc - tot;
           carry += readlane_i64(inc, 63);
+          carry_t += __builtin_amdgcn_readlane(tinc, 63);
         }
         if (lane == 0) rowbase[kBinMaxBandRows] = band_base + carry;
       }
       __syncthreads();
-      // 32-bit row/column split: the band holds at most kLdsDiffWords tiles.
-      const int32_t nbc = nbi * Ci;
-      for (int32_t i = threadIdx.x; i < nbc; i += kBinThreads) {
-        const int32_t row = (int32_t)((uint32_t)i / (uint32_t)Ci);
-        const int64_t v = rowbase[row] + lds[i];
-        tile_ptr[b0 * C + i] = v;
-        cursor[b0 * C + i] = v;
-      }
+      if (C <= 64) bin_scan_rows<1>(lds, C, nb, b0, rowbase, tile_ptr, fill, lane, wid);
+      else if (C <= 128) bin_scan_rows<2>(lds, C, nb, b0, rowbase, tile_ptr, fill, lane, wid);
+      else bin_scan_rows<4>(lds, C, nb, b0, rowbase, tile_ptr, fill, lane, wid);
       band_base = rowbase[kBinMaxBandRows];
       __syncthreads();
     }
@@ -494,12 +545,14 @@ __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __r
     for (int i = 0; i < kBinRectRegs; ++i) count(myrect[i]);
     for (int64_t g = threadIdx.x + (int64_t)kBinRectRegs * kBinThreads; g < K; g += kBinThreads)
       count(rect[g]);
+
     __threadfence();
     __syncthreads();
     Pc = block_scan_runs<kBinThreads>(tile_ptr, T, scan_lds);
-    for (int64_t t = threadIdx.x; t < T; t += kBinThreads) cursor[t] = tile_ptr[t];
+    for (int64_t t = threadIdx.x; t < T; t += kBinThreads) fill[t] = 0;
   }
   if (threadIdx.x == 0) {
+    const int64_t P = (int64_t)pairs_lds;
     tile_ptr[T] = Pc;
     *num_pairs = P;
     if (Pc != P) hdr->status |= GF_STATUS_COUNT_MISMATCH;
@@ -508,14 +561,16 @@ __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __r
 
 // ------------------------------------------------------------------------------------------
 // k_emit: one wave per Gaussian; the wave's lanes walk the Gaussian's tile rectangle row-major
-// and claim a slot of each tile's id segment with an atomic on the tile's cursor.  The order
+// and claim a slot of each tile's id segment, tile_ptr[t] + an atomic on the tile's fill count.  The order
 // inside a segment is fixed afterwards by the render, which sorts each segment.
 
-__global__ __launch_bounds__(kEmitThreads) void k_emit(Problem p, uint8_t* ws, FwdLayout L,
+__global__ __launch_bounds__(kEmitThreads) void k_emit(Problem p, const float* __restrict__ mu,
+                                                       uint8_t* ws, FwdLayout L,
+                                                       const int64_t* __restrict__ tile_ptr,
                                                        int64_t* __restrict__ ids, int64_t capacity) {
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   const int4* __restrict__ rect = reinterpret_cast<const int4*>(ws + L.rect);
-  unsigned long long* cursor = reinterpret_cast<unsigned long long*>(ws + L.cursor);
+  int32_t* fill = reinterpret_cast<int32_t*>(ws + L.fill);
   const int lane = threadIdx.x & 63;
   const int64_t g = (int64_t)blockIdx.x * (kEmitThreads / 64) +
                     __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
@@ -523,12 +578,37 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(Problem p, uint8_t* ws, F
   const int4 r = rect[g];
   const int32_t w = r.w - r.z + 1;
   const int32_t n = (r.y - r.x + 1) * w;
-  for (int32_t l = lane; l < n; l += 64) {
+  auto tile_of = [&](int32_t l) -> int64_t {
     const int32_t dr = (int32_t)((uint32_t)l / (uint32_t)w);
-    const int32_t tr = r.x + dr, tc = r.z + (l - dr * w);
-    const unsigned long long pos = atomicAdd(cursor + (int64_t)tr * p.C + tc, 1ull);
-    if ((int64_t)pos < capacity) ids[pos] = g;
+    return (int64_t)(r.x + dr) * p.C + (r.z + (l - dr * w));
+  };
+  auto place = [&](int64_t pos) {
+    if (pos < capacity) ids[pos] = g;
     else set_status(&hdr->status, GF_STATUS_CAPACITY);
+  };
+  // First round of slot atomics in flight while lane 0 computes the Gaussian's evaluation
+  // constants (the weight slot holds the normalisation; the render applies the amplitude);
+  // the returned slot is only combined with tile_ptr afterwards.
+  int64_t base0 = 0;
+  uint32_t slot0 = 0u;  // unsigned: widening it needs no instruction that would wait for it
+  if (lane < n) {
+    const int64_t t = tile_of(lane);
+    base0 = tile_ptr[t];
+    slot0 = atomicAdd(reinterpret_cast<uint32_t*>(fill) + t, 1u);
+  }
+  if (lane == 0) {
+    GaussEval* ev = reinterpret_cast<GaussEval*>(ws + L.eval);
+    const float4 c4 = reinterpret_cast<const float4*>(ws + L.cov)[g];
+    GfCov c;
+    c.s00 = c4.x;
+    c.s01 = c4.y;
+    c.s11 = c4.z;
+    store_eval(ev, g, eval_from_cov(p, mu[2 * g + 0], mu[2 * g + 1], c, 1.0f));
+  }
+  if (lane < n) place(base0 + (int64_t)slot0);
+  for (int32_t l = lane + 64; l < n; l += 64) {
+    const int64_t t = tile_of(l);
+    place(tile_ptr[t] + atomicAdd(fill + t, 1));
   }
 }
 
@@ -1261,8 +1341,8 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
 }
 
 int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                    int64_t* gaussian_ids_sorted, int64_t ids_capacity, void* workspace,
-                    size_t workspace_bytes, void* stream) {
+                    const float* mu, const int64_t* tile_ptr, int64_t* gaussian_ids_sorted,
+                    int64_t ids_capacity, void* workspace, size_t workspace_bytes, void* stream) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
@@ -1271,11 +1351,14 @@ int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in
     return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
   if (ids_capacity < 0 || (ids_capacity > 0 && !gaussian_ids_sorted))
     return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / ids_capacity invalid");
+  if (!tile_ptr) return set_err(GF_E_INVALID_ARGUMENT, "tile_ptr must not be NULL");
+  if (k > 0 && !mu) return set_err(GF_E_INVALID_ARGUMENT, "mu must not be NULL");
   if (k == 0) return GF_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t blocks = (k + kEmitThreads / 64 - 1) / (kEmitThreads / 64);
-  hipLaunchKernelGGL(k_emit, dim3((unsigned)blocks), dim3(kEmitThreads), 0, st, p,
-                     reinterpret_cast<uint8_t*>(workspace), L, gaussian_ids_sorted, ids_capacity);
+  hipLaunchKernelGGL(k_emit, dim3((unsigned)blocks), dim3(kEmitThreads), 0, st, p, mu,
+                     reinterpret_cast<uint8_t*>(workspace), L, tile_ptr, gaussian_ids_sorted,
+                     ids_capacity);
   GF_LAUNCH_CHECK("k_emit");
   return GF_OK;
 }

@@ -126,7 +126,8 @@ def forward_with_workspace(row_coords: Tensor, col_coords: Tensor, mu: Tensor, c
                                  ws.data_ptr(), ws_bytes, stream), "gaussian_field_forward (binning)")
         ids = torch.empty(P.value, dtype=torch.int64, device=dev)
         delta = torch.empty(M * Nf, dtype=torch.float32, device=dev)
-        N.check(L.gf_forward_emit(ctypes.byref(cfg), M, Nf, K, N.ptr(ids), P.value,
+        N.check(L.gf_forward_emit(ctypes.byref(cfg), M, Nf, K, N.ptr(mu), tile_ptr.data_ptr(),
+                                  N.ptr(ids), P.value,
                                   ws.data_ptr(), ws_bytes, stream), "gaussian_field_forward (emit)")
         N.check(L.gf_forward_render(ctypes.byref(cfg), M, Nf, K, row_coords.data_ptr(),
                                     col_coords.data_ptr(), N.ptr(amp), tile_ptr.data_ptr(),

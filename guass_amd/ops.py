@@ -57,14 +57,14 @@ class FieldPlan:
                                        self.num_pairs.data_ptr(), None, self.fwd_ws.data_ptr(),
                                        self.fwd_ws_bytes, self._stream()), "gf_forward_bin")
 
-    def emit(self) -> None:
-        N.check(N.lib().gf_forward_emit(ctypes.byref(self.cfg), self.M, self.N, self.K,
-                                        self.ids.data_ptr(), self.capacity, self.fwd_ws.data_ptr(),
-                                        self.fwd_ws_bytes, self._stream()),
+    def emit(self, mu) -> None:
+        N.check(N.lib().gf_forward_emit(ctypes.byref(self.cfg), self.M, self.N, self.K, N.ptr(mu),
+                                        self.tile_ptr.data_ptr(), self.ids.data_ptr(), self.capacity,
+                                        self.fwd_ws.data_ptr(), self.fwd_ws_bytes, self._stream()),
                 "gf_forward_emit")
 
     def render(self, row_coords, col_coords, amp) -> torch.Tensor:
-        """Renders from the Gaussian constants the last ``bin`` stored in the workspace."""
+        """Renders from the Gaussian constants the last ``emit`` stored in the workspace."""
         N.check(N.lib().gf_forward_render(ctypes.byref(self.cfg), self.M, self.N, self.K,
                                           row_coords.data_ptr(), col_coords.data_ptr(), N.ptr(amp),
                                           self.tile_ptr.data_ptr(), self.ids.data_ptr(), self.capacity,
@@ -76,7 +76,7 @@ class FieldPlan:
     def forward(self, row_coords, col_coords, mu, chol_raw, amp) -> torch.Tensor:
         """Bins and renders into ``self.delta`` (and ``tile_ptr`` / ``ids``); returns delta."""
         self.bin(mu, chol_raw)
-        self.emit()
+        self.emit(mu)
         return self.render(row_coords, col_coords, amp)
 
     def backward_reduce(self, grad, row_coords, col_coords, mu, chol_raw, num_pairs: int | None = None,

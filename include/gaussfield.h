@@ -70,8 +70,7 @@ size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, in
 
 /*
  * Forward phase 1 (binning): per-Gaussian geometry and sigma-box tile ranges, per-tile
- * Gaussian counts and their exclusive scan.  The workspace also receives each Gaussian's
- * evaluation constants, which gf_forward_render and (optionally) gf_backward reuse.
+ * Gaussian counts and their exclusive scan.
  *   tile_ptr        [T+1] int64 out: tile t owns gaussian_ids_sorted[tile_ptr[t] : tile_ptr[t+1]]
  *   num_pairs_dev   [1] int64 out: P = tile_ptr[T] = sum over Gaussians of tiles touched
  *   num_pairs_host  optional: if non-NULL the call synchronises `stream` and stores P here
@@ -85,13 +84,16 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
 
 /*
  * Forward phase 2 (emission): writes the (tile, gaussian) pairs into gaussian_ids_sorted,
- * each tile's ids inside its [tile_ptr[t], tile_ptr[t+1]) range (order fixed by phase 3).
- * Must follow gf_forward_bin on the same stream with the same workspace.
+ * each tile's ids inside its [tile_ptr[t], tile_ptr[t+1]) range (order fixed by phase 3),
+ * and stores each Gaussian's evaluation constants in the workspace (from the covariances
+ * gf_forward_bin left there), which gf_forward_render and (optionally) gf_backward reuse.
+ * Must follow gf_forward_bin on the same stream with the same workspace, tile_ptr and mu.
  *   gaussian_ids_sorted [ids_capacity] int64 out; pairs beyond the capacity are dropped and
  *                   GF_STATUS_CAPACITY is set
  * Replaces reference forward.cu:465-482 (emit_tile_pairs_kernel + radix sort on the tile key).
  */
 int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                    const float* mu, const int64_t* tile_ptr,
                     int64_t* gaussian_ids_sorted, int64_t ids_capacity,
                     void* workspace, size_t workspace_bytes, void* stream);
 
@@ -117,7 +119,7 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
  *   gaussian_ids    [num_pairs], int64 if ids_is_int64 else int32 (any order within a tile)
  *   d_mu [K,2], d_chol_raw [K,3], d_amp [K,1] fp32 out (fully written)
  *   forward_workspace  optional: the workspace of the gf_forward_bin call over the same
- *                   (mu, chol_raw) and config; its evaluation constants are reused instead of
+ *                   (mu, chol_raw) and config (after its gf_forward_emit); its evaluation constants are reused instead of
  *                   recomputed from mu / chol_raw.  NULL recomputes them.
  * Saved-state violations (non-monotone tile_ptr, tile_ptr[T] != num_pairs, ids outside
  * [0,K)) are detected on the device, the offending pairs skipped, and status bits set.

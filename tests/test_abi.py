@@ -69,9 +69,9 @@ def test_tile_grid_and_workspace_sizes():
     assert (R.value, C.value) == (6, 3)
     fwd = lib.gf_forward_workspace_bytes(1280, 1280, 1024, ctypes.byref(_cfg()))
     bwd = lib.gf_backward_workspace_bytes(1280, 1280, 1024, ctypes.byref(_cfg()))
-    # header + 32 B constants + 16 B rectangle per Gaussian + 8 B cursor per tile; 32 B per
-    # Gaussian of accumulators
-    assert fwd >= 256 + 48 * 1024 + 8 * 6400 and fwd % 256 == 0
+    # header + 32 B constants + 16 B rectangle per Gaussian + 4 B fill counter per tile; 32 B
+    # per Gaussian of accumulators
+    assert fwd >= 256 + 48 * 1024 + 4 * 6400 and fwd % 256 == 0
     assert bwd >= 256 + 32 * 1024 and bwd % 256 == 0
     assert lib.gf_forward_workspace_bytes(10, 10, 4, ctypes.byref(_cfg(tile_out=0))) == 0
 

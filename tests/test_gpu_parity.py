@@ -272,7 +272,8 @@ def test_plan_sync_free_and_capacity(device):
     fresh = [t.clone() for t in plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw,
                                               q.amp, num_pairs=P, reuse_forward=False)]
     for a, b in zip(fresh, ref[3:]):
-        grad_close(a, b, "plan without the forward's constants", rtol=1e-6)
+        # same arithmetic, different atomic accumulation order
+        grad_close(a, b, "plan without the forward's constants", rtol=1e-5)
     small = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=P // 2)
     small.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
     torch.cuda.synchronize()
