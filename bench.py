@@ -236,8 +236,8 @@ def main() -> int:
         return statistics.median(times)
 
     k_bin = lambda: plan.bin(q.mu, q.chol_raw)  # noqa: E731
-    k_emit = lambda: plan.emit(q.mu)  # noqa: E731
-    k_render = lambda: plan.render(q.row_coords, q.col_coords, q.amp)  # noqa: E731
+    k_emit = lambda: plan.emit(q.mu, q.amp)  # noqa: E731
+    k_render = lambda: plan.render(q.row_coords, q.col_coords)  # noqa: E731
     k_bwd = lambda: plan.backward_reduce(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, P)  # noqa: E731
     k_fin = lambda: plan.backward_finish(q.chol_raw, q.amp)  # noqa: E731
     ph = {"k_bin": graph_time_us([k_bin])}

@@ -17,6 +17,7 @@ import torch  # noqa: F401  (must precede the dlopen below)
 LIB_PATH = Path(__file__).resolve().with_name("libgaussfield.so")
 
 GF_OK = 0
+GF_PAIR_CONSTANT_BYTES = 32  # per pair, include/gaussfield.h
 GF_STATUS_CAPACITY = 0x1
 GF_STATUS_COUNT_MISMATCH = 0x2
 GF_STATUS_TILE_PTR_LAST = 0x4
@@ -75,7 +76,8 @@ def lib() -> ctypes.CDLL:
     L.gf_backward_workspace_bytes.argtypes = [c_int64, c_int64, c_int64, _CFG]
     L.gf_backward_workspace_bytes.restype = c_size_t
     L.gf_forward_bin.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_size_t, _P]
-    L.gf_forward_emit.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, c_int64, _P, c_size_t, _P]
+    L.gf_forward_emit.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, c_int64, _P,
+                                  c_size_t, _P]
     L.gf_forward_render.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P,
                                     c_int64, _P, _P, c_size_t, _P]
     L.gf_backward.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int32,

@@ -92,7 +92,8 @@ struct Problem {
 //   basis = 2^clamp(q') = exp(-q/2).
 struct __align__(16) GaussEval {
   float mu0, mu1, wa, wb, wc, w;  // w = amp * norm
-  float pad0, pad1;
+  int32_t gid;                    // the Gaussian's id (pair-ordered copies carry it)
+  float pad;
 };
 
 struct WsHeader {
@@ -191,7 +192,8 @@ __device__ inline GaussEval eval_from_cov(const Problem& p, float mu0, float mu1
     norm = gf_div_f32(1.0f, GF_TWO_PI_F32 * (sq < GF_FLT_EPS ? GF_FLT_EPS : sq));
   }
   v.w = amp * norm;
-  v.pad0 = v.pad1 = 0.0f;
+  v.gid = -1;
+  v.pad = 0.0f;
   return v;
 }
 
@@ -212,13 +214,15 @@ __device__ inline GaussEval load_eval(const GaussEval* __restrict__ ev, int64_t 
   v.wb = a.w;
   v.wc = b.x;
   v.w = b.y;
-  v.pad0 = v.pad1 = 0.0f;
+  v.gid = __float_as_int(b.z);
+  v.pad = 0.0f;
   return v;
 }
 
 __device__ inline GaussEval zero_eval() {
   GaussEval v;
-  v.mu0 = v.mu1 = v.wa = v.wb = v.wc = v.w = v.pad0 = v.pad1 = 0.0f;
+  v.mu0 = v.mu1 = v.wa = v.wb = v.wc = v.w = v.pad = 0.0f;
+  v.gid = -1;
   return v;
 }
 
@@ -363,10 +367,23 @@ __device__ int64_t bin_scan_lds_to_global(const int32_t* lds, int64_t n, int64_t
   return total;
 }
 
-__device__ inline void store_eval(GaussEval* ev, int64_t g, const GaussEval& v) {
-  float4* q = reinterpret_cast<float4*>(ev + g);
+__device__ inline void store_eval(GaussEval* ev, int64_t i, const GaussEval& v) {
+  float4* q = reinterpret_cast<float4*>(ev + i);
   q[0] = make_float4(v.mu0, v.mu1, v.wa, v.wb);
-  q[1] = make_float4(v.wc, v.w, 0.0f, 0.0f);
+  q[1] = make_float4(v.wc, v.w, __int_as_float(v.gid), 0.0f);
+}
+
+__device__ inline GaussEval readlane_eval(const GaussEval& v, int lane) {
+  GaussEval r;
+  r.mu0 = readlane_f(v.mu0, lane);
+  r.mu1 = readlane_f(v.mu1, lane);
+  r.wa = readlane_f(v.wa, lane);
+  r.wb = readlane_f(v.wb, lane);
+  r.wc = readlane_f(v.wc, lane);
+  r.w = readlane_f(v.w, lane);
+  r.gid = __builtin_amdgcn_readlane(v.gid, lane);
+  r.pad = 0.0f;
+  return r;
 }
 
 // Gaussians g = threadIdx.x + i * kBinThreads, i < kBinRectRegs, keep their tile rectangle in
@@ -565,9 +582,10 @@ __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __r
 // inside a segment is fixed afterwards by the render, which sorts each segment.
 
 __global__ __launch_bounds__(kEmitThreads) void k_emit(Problem p, const float* __restrict__ mu,
-                                                       uint8_t* ws, FwdLayout L,
-                                                       const int64_t* __restrict__ tile_ptr,
-                                                       int64_t* __restrict__ ids, int64_t capacity) {
+                                                       const float* __restrict__ amp, uint8_t* ws,
+                                                       FwdLayout L, const int64_t* __restrict__ tile_ptr,
+                                                       int64_t* __restrict__ ids,
+                                                       GaussEval* __restrict__ pair_ev, int64_t capacity) {
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   const int4* __restrict__ rect = reinterpret_cast<const int4*>(ws + L.rect);
   int32_t* fill = reinterpret_cast<int32_t*>(ws + L.fill);
@@ -582,13 +600,8 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(Problem p, const float* _
     const int32_t dr = (int32_t)((uint32_t)l / (uint32_t)w);
     return (int64_t)(r.x + dr) * p.C + (r.z + (l - dr * w));
   };
-  auto place = [&](int64_t pos) {
-    if (pos < capacity) ids[pos] = g;
-    else set_status(&hdr->status, GF_STATUS_CAPACITY);
-  };
   // First round of slot atomics in flight while lane 0 computes the Gaussian's evaluation
-  // constants (the weight slot holds the normalisation; the render applies the amplitude);
-  // the returned slot is only combined with tile_ptr afterwards.
+  // constants; the returned slot is only combined with tile_ptr afterwards.
   int64_t base0 = 0;
   uint32_t slot0 = 0u;  // unsigned: widening it needs no instruction that would wait for it
   if (lane < n) {
@@ -596,6 +609,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(Problem p, const float* _
     base0 = tile_ptr[t];
     slot0 = atomicAdd(reinterpret_cast<uint32_t*>(fill) + t, 1u);
   }
+  GaussEval mine = zero_eval();
   if (lane == 0) {
     GaussEval* ev = reinterpret_cast<GaussEval*>(ws + L.eval);
     const float4 c4 = reinterpret_cast<const float4*>(ws + L.cov)[g];
@@ -603,8 +617,19 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(Problem p, const float* _
     c.s00 = c4.x;
     c.s01 = c4.y;
     c.s11 = c4.z;
-    store_eval(ev, g, eval_from_cov(p, mu[2 * g + 0], mu[2 * g + 1], c, 1.0f));
+    mine = eval_from_cov(p, mu[2 * g + 0], mu[2 * g + 1], c, amp[g]);
+    mine.gid = (int32_t)g;
+    store_eval(ev, g, mine);
   }
+  const GaussEval v = readlane_eval(mine, 0);
+  auto place = [&](int64_t pos) {
+    if (pos < capacity) {
+      ids[pos] = g;
+      store_eval(pair_ev, pos, v);
+    } else {
+      set_status(&hdr->status, GF_STATUS_CAPACITY);
+    }
+  };
   if (lane < n) place(base0 + (int64_t)slot0);
   for (int32_t l = lane + 64; l < n; l += 64) {
     const int64_t t = tile_of(l);
@@ -815,27 +840,66 @@ __device__ inline void tile_range(const int64_t* __restrict__ tile_ptr, int64_t 
 // a time and broadcast with readlane while every lane accumulates its 4 pixels.
 __global__ __launch_bounds__(kTileThreads) void k_render16(
     Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
-    const GaussEval* __restrict__ ev, const float* __restrict__ amp,
-    const int64_t* __restrict__ tile_ptr, int64_t* ids, int64_t capacity, float* __restrict__ delta,
-    uint8_t* ws) {
+    const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids,
+    GaussEval* pair_ev, int64_t capacity, float* __restrict__ delta, uint8_t* ws) {
   __shared__ int32_t wkeys[kTileThreads / 64][kWaveSortKeys];
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
   const int64_t t = (int64_t)blockIdx.x * (kTileThreads / 64) + wid;
   if (t >= (int64_t)p.R * p.C) return;
   const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (t / p.C) * p.C);
   const int32_t pr = tr * 16 + (lane >> 2), pc = tc * 16 + ((lane & 3) << 2);
+  // coordinates first: they do not depend on the tile's segment
+  const float x = row_coords[min(pr, p.M - 1)];
+  float y[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) y[i] = col_coords[min(pc + i, p.N - 1)];
   int64_t s, n;
   tile_range(tile_ptr, t, capacity, &s, &n);
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  if (n > 0) {
+  auto accumulate = [&](const GaussEval& u) {
+    const float dx = x - u.mu0;
+    const float a = u.wa * dx;
+    const float A = a * a;
+    const float b = u.wb * dx;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float z = fmaf(u.wc, y[i] - u.mu1, b);
+      acc[i] = fmaf(u.w, basis_w(p, A, z), acc[i]);
+    }
+  };
+  if (n > 0 && n <= 64) {
+    // ids and their constants (emission order) in one round trip; rank sort by id; the
+    // constants follow their id to lane `rank` (ds_permute) and both go back sorted.
+    GaussEval my = zero_eval();
+    int32_t key = INT32_MAX;
+    if (lane < n) {
+      key = (int32_t)ids[s + lane];
+      my = load_eval(pair_ev, s + lane);
+    }
+    int rank = 0;
+    for (int j = 0; j < (int)n; ++j) rank += (__builtin_amdgcn_readlane(key, j) < key) ? 1 : 0;
+    const int addr = rank << 2;
+    GaussEval srt;
+    srt.mu0 = __int_as_float(__builtin_amdgcn_ds_permute(addr, __float_as_int(my.mu0)));
+    srt.mu1 = __int_as_float(__builtin_amdgcn_ds_permute(addr, __float_as_int(my.mu1)));
+    srt.wa = __int_as_float(__builtin_amdgcn_ds_permute(addr, __float_as_int(my.wa)));
+    srt.wb = __int_as_float(__builtin_amdgcn_ds_permute(addr, __float_as_int(my.wb)));
+    srt.wc = __int_as_float(__builtin_amdgcn_ds_permute(addr, __float_as_int(my.wc)));
+    srt.w = __int_as_float(__builtin_amdgcn_ds_permute(addr, __float_as_int(my.w)));
+    srt.gid = __builtin_amdgcn_ds_permute(addr, key);
+    srt.pad = 0.0f;
+    if (lane < n) {
+      if (srt.gid < 0 || srt.gid >= p.K) set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);
+      ids[s + lane] = srt.gid;
+      store_eval(pair_ev, s + lane, srt);
+    }
+    for (int j = 0; j < (int)n; ++j) accumulate(readlane_eval(srt, j));
+  } else if (n > 64) {
     int64_t* seg = ids + s;
     int32_t* keys = wkeys[wid];
     order_segment_wave(seg, n, p.K, keys, &hdr->status);
-    const float x = row_coords[min(pr, p.M - 1)];
-    float y[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) y[i] = col_coords[min(pc + i, p.N - 1)];
     for (int64_t j0 = 0; j0 < n; j0 += 64) {
       const int nj = (int)((n - j0) < 64 ? (n - j0) : 64);
       GaussEval my = zero_eval();
@@ -843,25 +907,12 @@ __global__ __launch_bounds__(kTileThreads) void k_render16(
         const int64_t g = (n <= kWaveSortKeys) ? (int64_t)keys[j0 + lane] : seg[j0 + lane];
         if (g >= 0 && g < p.K) {
           my = load_eval(ev, g);
-          my.w *= amp[g];
+          store_eval(pair_ev, s + j0 + lane, my);
         } else {
           set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);  // internal mismatch only
         }
       }
-      for (int j = 0; j < nj; ++j) {
-        const float mu0 = readlane_f(my.mu0, j), mu1 = readlane_f(my.mu1, j);
-        const float wa = readlane_f(my.wa, j), wb = readlane_f(my.wb, j);
-        const float wc = readlane_f(my.wc, j), w = readlane_f(my.w, j);
-        const float dx = x - mu0;
-        const float a = wa * dx;
-        const float A = a * a;
-        const float b = wb * dx;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float z = fmaf(wc, y[i] - mu1, b);
-          acc[i] = fmaf(w, basis_w(p, A, z), acc[i]);
-        }
-      }
+      for (int j = 0; j < nj; ++j) accumulate(readlane_eval(my, j));
     }
   }
   if (pr < p.M) {
@@ -879,9 +930,8 @@ __global__ __launch_bounds__(kTileThreads) void k_render16(
 // Any tile shape: each thread evaluates pixels p = tid, tid+256, ... of the tile.
 __global__ __launch_bounds__(kTileThreads) void k_render_any(
     Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
-    const GaussEval* __restrict__ ev, const float* __restrict__ amp,
-    const int64_t* __restrict__ tile_ptr, int64_t* ids, int64_t capacity, float* __restrict__ delta,
-    uint8_t* ws) {
+    const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids,
+    GaussEval* pair_ev, int64_t capacity, float* __restrict__ delta, uint8_t* ws) {
   __shared__ int32_t keys[kSortLdsWords];
   __shared__ int64_t small_lds[kTileThreads / 64 + 1];
   __shared__ GaussEval gl[kTileThreads];
@@ -893,6 +943,11 @@ __global__ __launch_bounds__(kTileThreads) void k_render_any(
   int64_t* seg = ids + s;
   order_segment(seg, n, p.K, keys, small_lds, &hdr->status);
   const bool keys_in_lds = n <= kSortLdsKeys;
+  // the pair-ordered constants follow the sorted ids
+  for (int64_t i = threadIdx.x; i < n; i += kTileThreads) {
+    const int64_t g = keys_in_lds ? (int64_t)keys[i] : seg[i];
+    if (g >= 0 && g < p.K) store_eval(pair_ev, s + i, load_eval(ev, g));
+  }
   const int32_t r0 = tr * p.tile_out, c0 = tc * p.tile_in;
   const int32_t r1 = min(r0 + p.tile_out, p.M), c1 = min(c0 + p.tile_in, p.N);
   const int32_t w = c1 - c0;
@@ -910,9 +965,7 @@ __global__ __launch_bounds__(kTileThreads) void k_render_any(
       if ((int)threadIdx.x < nj) {
         const int64_t g = keys_in_lds ? (int64_t)keys[j0 + threadIdx.x] : seg[j0 + threadIdx.x];
         if (g >= 0 && g < p.K) {
-          GaussEval v = load_eval(ev, g);
-          v.w *= amp[g];
-          gl[threadIdx.x] = v;
+          gl[threadIdx.x] = load_eval(ev, g);
         } else {
           gl[threadIdx.x] = zero_eval();
           set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);
@@ -961,7 +1014,7 @@ template <typename GIdx>
 __device__ inline void stage_gaussians(const Problem& p, const GIdx* __restrict__ gids, int64_t s,
                                        int64_t j0, int nj, const float* __restrict__ mu,
                                        const float* __restrict__ chol_raw,
-                                       const GaussEval* __restrict__ ev, GaussEval* gl,
+                                       const GaussEval* __restrict__ pair_ev, GaussEval* gl,
                                        int32_t* gid_lds, uint32_t* status) {
   if ((int)threadIdx.x < nj) {
     const int64_t g = (int64_t)gids[s + j0 + threadIdx.x];
@@ -970,7 +1023,7 @@ __device__ inline void stage_gaussians(const Problem& p, const GIdx* __restrict_
       gid_lds[threadIdx.x] = -1;
       gl[threadIdx.x] = zero_eval();
     } else {
-      gl[threadIdx.x] = ev ? load_eval(ev, g) : eval_geom(p, mu, chol_raw, nullptr, g);
+      gl[threadIdx.x] = pair_ev ? load_eval(pair_ev, s + j0 + threadIdx.x) : eval_geom(p, mu, chol_raw, nullptr, g);
       gid_lds[threadIdx.x] = (int32_t)g;
     }
   }
@@ -984,29 +1037,22 @@ template <typename TpIdx, typename GIdx>
 __global__ __launch_bounds__(kTileThreads) void k_bwd16(
     Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
-    const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
+    const float* __restrict__ chol_raw, const GaussEval* __restrict__ pair_ev,
     const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
     uint8_t* ws, BwdLayout L) {
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   float* acc = reinterpret_cast<float*>(ws + L.acc);
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
   const int64_t t = (int64_t)blockIdx.x * (kTileThreads / 64) + wid;
   const int64_t T = (int64_t)p.R * p.C;
   if (t >= T) return;
-  int64_t s = (int64_t)tile_ptr[t], e = (int64_t)tile_ptr[t + 1];
-  if (lane == 0) {
-    if (s < 0 || e < s || e > num_pairs) set_status(&hdr->status, GF_STATUS_TILE_PTR_ORDER);
-    if (t == T - 1 && e != num_pairs) set_status(&hdr->status, GF_STATUS_TILE_PTR_LAST);
-  }
-  if (s < 0) s = 0;
-  if (e > num_pairs) e = num_pairs;
-  const int64_t n = e > s ? e - s : 0;
-  if (n == 0) return;
   const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (t / p.C) * p.C);
   const int32_t r0 = tr * 16, c0 = tc * 16;
   const int slot = lane >> 4, row = lane & 15;
   const int32_t pr = r0 + row;
-  // this lane's row of dL/d(delta) (0 outside the matrix) and the tile's column coordinates
+  // This lane's row of dL/d(delta) (0 outside the matrix) and the tile's coordinates are
+  // requested before the segment bounds, on which they do not depend.
   float gv[16], yv[16];
   const float* grow = grad + (int64_t)min(pr, p.M - 1) * p.N + c0;
   if (pr < p.M && c0 + 15 < p.N && ((reinterpret_cast<uintptr_t>(grow) & 15) == 0)) {
@@ -1025,17 +1071,28 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd16(
 #pragma unroll
   for (int c = 0; c < 16; ++c) yv[c] = col_coords[min(c0 + c, p.N - 1)];
   const float x = row_coords[min(pr, p.M - 1)];
+  int64_t s = (int64_t)tile_ptr[t], e = (int64_t)tile_ptr[t + 1];
+  if (lane == 0) {
+    if (s < 0 || e < s || e > num_pairs) set_status(&hdr->status, GF_STATUS_TILE_PTR_ORDER);
+    if (t == T - 1 && e != num_pairs) set_status(&hdr->status, GF_STATUS_TILE_PTR_LAST);
+  }
+  if (s < 0) s = 0;
+  if (e > num_pairs) e = num_pairs;
+  const int64_t n = e > s ? e - s : 0;
+  if (n == 0) return;
 
   for (int64_t j0 = 0; j0 < n; j0 += 64) {
     const int nj = (int)((n - j0) < 64 ? (n - j0) : 64);
     GaussEval my = zero_eval();
     int32_t myg = -1;
     if (lane < nj) {
+      // the id and (when given) the pair's constants are independent loads
       const int64_t g = (int64_t)gids[s + j0 + lane];
+      const GaussEval pe = pair_ev ? load_eval(pair_ev, s + j0 + lane) : zero_eval();
       if (g < 0 || g >= p.K) {
         set_status(&hdr->status, g < 0 ? GF_STATUS_IDS_NEGATIVE : GF_STATUS_IDS_RANGE);
       } else {
-        my = ev ? load_eval(ev, g) : eval_geom(p, mu, chol_raw, nullptr, g);
+        my = pair_ev ? pe : eval_geom(p, mu, chol_raw, nullptr, g);
         myg = (int32_t)g;
       }
     }
@@ -1088,7 +1145,7 @@ template <typename TpIdx, typename GIdx>
 __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
     Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
-    const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
+    const float* __restrict__ chol_raw, const GaussEval* __restrict__ pair_ev,
     const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
     uint8_t* ws, BwdLayout L) {
   __shared__ GaussEval gl[kTileThreads];
@@ -1109,7 +1166,7 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
   for (int64_t j0 = 0; j0 < n; j0 += kTileThreads) {
     const int nj = (int)((n - j0) < kTileThreads ? (n - j0) : kTileThreads);
     __syncthreads();
-    stage_gaussians<GIdx>(p, gids, s, j0, nj, mu, chol_raw, ev, gl, gid_lds, &hdr->status);
+    stage_gaussians<GIdx>(p, gids, s, j0, nj, mu, chol_raw, pair_ev, gl, gid_lds, &hdr->status);
     __syncthreads();
     for (int j = 0; j < nj; ++j) {
       const int32_t g = gid_lds[j];
@@ -1266,15 +1323,15 @@ unsigned wave_tile_grid(int64_t T) { return (unsigned)((T + kTileThreads / 64 - 
 
 template <typename TP, typename GI>
 void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, const float* rc,
-                const float* cc, const float* mu, const float* raw, const GaussEval* ev,
+                const float* cc, const float* mu, const float* raw, const GaussEval* pev,
                 const void* tile_ptr, const void* gids, int64_t num_pairs, uint8_t* ws,
                 const BwdLayout& L) {
   if (fast16(p))
     hipLaunchKernelGGL((k_bwd16<TP, GI>), dim3(wave_tile_grid((int64_t)p.R * p.C)), dim3(kTileThreads), 0, st,
-                       p, grad, rc, cc, mu, raw, ev, reinterpret_cast<const TP*>(tile_ptr),
+                       p, grad, rc, cc, mu, raw, pev, reinterpret_cast<const TP*>(tile_ptr),
                        reinterpret_cast<const GI*>(gids), num_pairs, ws, L);
   else
-    hipLaunchKernelGGL((k_bwd_any<TP, GI>), grid, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw, ev,
+    hipLaunchKernelGGL((k_bwd_any<TP, GI>), grid, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw, pev,
                        reinterpret_cast<const TP*>(tile_ptr), reinterpret_cast<const GI*>(gids),
                        num_pairs, ws, L);
 }
@@ -1341,31 +1398,32 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
 }
 
 int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                    const float* mu, const int64_t* tile_ptr, int64_t* gaussian_ids_sorted,
-                    int64_t ids_capacity, void* workspace, size_t workspace_bytes, void* stream) {
+                    const float* mu, const float* amp, const int64_t* tile_ptr,
+                    int64_t* gaussian_ids_sorted, void* pair_constants, int64_t ids_capacity,
+                    void* workspace, size_t workspace_bytes, void* stream) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
   const FwdLayout L = fwd_layout(k, (int64_t)p.R * p.C);
   if (!workspace || workspace_bytes < L.total)
     return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
-  if (ids_capacity < 0 || (ids_capacity > 0 && !gaussian_ids_sorted))
-    return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / ids_capacity invalid");
+  if (ids_capacity < 0 || (ids_capacity > 0 && (!gaussian_ids_sorted || !pair_constants)))
+    return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / pair_constants / ids_capacity invalid");
   if (!tile_ptr) return set_err(GF_E_INVALID_ARGUMENT, "tile_ptr must not be NULL");
-  if (k > 0 && !mu) return set_err(GF_E_INVALID_ARGUMENT, "mu must not be NULL");
+  if (k > 0 && (!mu || !amp)) return set_err(GF_E_INVALID_ARGUMENT, "mu / amp must not be NULL");
   if (k == 0) return GF_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t blocks = (k + kEmitThreads / 64 - 1) / (kEmitThreads / 64);
-  hipLaunchKernelGGL(k_emit, dim3((unsigned)blocks), dim3(kEmitThreads), 0, st, p, mu,
+  hipLaunchKernelGGL(k_emit, dim3((unsigned)blocks), dim3(kEmitThreads), 0, st, p, mu, amp,
                      reinterpret_cast<uint8_t*>(workspace), L, tile_ptr, gaussian_ids_sorted,
-                     ids_capacity);
+                     reinterpret_cast<GaussEval*>(pair_constants), ids_capacity);
   GF_LAUNCH_CHECK("k_emit");
   return GF_OK;
 }
 
 int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                      const float* row_coords, const float* col_coords, const float* amp,
-                      const int64_t* tile_ptr, int64_t* gaussian_ids_sorted, int64_t ids_capacity,
+                      const float* row_coords, const float* col_coords, const int64_t* tile_ptr,
+                      int64_t* gaussian_ids_sorted, void* pair_constants, int64_t ids_capacity,
                       float* delta, void* workspace, size_t workspace_bytes, void* stream) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
@@ -1376,18 +1434,18 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
     return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
   if (!row_coords || !col_coords || !tile_ptr || !delta)
     return set_err(GF_E_INVALID_ARGUMENT, "coords / tile_ptr / delta must not be NULL");
-  if (ids_capacity < 0 || (ids_capacity > 0 && !gaussian_ids_sorted))
-    return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / ids_capacity invalid");
-  if (k > 0 && !amp) return set_err(GF_E_INVALID_ARGUMENT, "amp must not be NULL");
+  if (ids_capacity < 0 || (ids_capacity > 0 && (!gaussian_ids_sorted || !pair_constants)))
+    return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / pair_constants / ids_capacity invalid");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
   const GaussEval* ev = reinterpret_cast<const GaussEval*>(ws + L.eval);
+  GaussEval* pev = reinterpret_cast<GaussEval*>(pair_constants);
   if (fast16(p))
     hipLaunchKernelGGL(k_render16, dim3(wave_tile_grid(T)), dim3(kTileThreads), 0, st, p, row_coords,
-                       col_coords, ev, amp, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws);
+                       col_coords, ev, tile_ptr, gaussian_ids_sorted, pev, ids_capacity, delta, ws);
   else
     hipLaunchKernelGGL(k_render_any, dim3((unsigned)T), dim3(kTileThreads), 0, st, p, row_coords,
-                       col_coords, ev, amp, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws);
+                       col_coords, ev, tile_ptr, gaussian_ids_sorted, pev, ids_capacity, delta, ws);
   GF_LAUNCH_CHECK("k_render");
   return GF_OK;
 }
@@ -1396,7 +1454,7 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
                        const float* grad_delta, const float* row_coords, const float* col_coords,
                        const float* mu, const float* chol_raw, const void* tile_ptr,
                        int32_t tile_ptr_is_int64, const void* gaussian_ids, int32_t ids_is_int64,
-                       int64_t num_pairs, const void* forward_workspace, void* workspace,
+                       int64_t num_pairs, const void* pair_constants, void* workspace,
                        size_t workspace_bytes, void* stream) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
@@ -1412,9 +1470,7 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
   if (k > 0 && (!mu || !chol_raw)) return set_err(GF_E_INVALID_ARGUMENT, "mu / chol_raw must not be NULL");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
-  const GaussEval* ev = forward_workspace
-      ? reinterpret_cast<const GaussEval*>(reinterpret_cast<const uint8_t*>(forward_workspace) + fwd_layout(k, T).eval)
-      : nullptr;
+  const GaussEval* ev = reinterpret_cast<const GaussEval*>(pair_constants);
   const dim3 grid((unsigned)T);
   if (tile_ptr_is_int64 && ids_is_int64)
     launch_bwd<int64_t, int64_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs, ws, L);
@@ -1453,11 +1509,11 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
                 const float* mu, const float* chol_raw, const float* amp, const void* tile_ptr,
                 int32_t tile_ptr_is_int64, const void* gaussian_ids, int32_t ids_is_int64,
                 int64_t num_pairs, float* d_mu, float* d_chol_raw, float* d_amp,
-                const void* forward_workspace, void* workspace, size_t workspace_bytes, void* stream) {
+                const void* pair_constants, void* workspace, size_t workspace_bytes, void* stream) {
   if (k > 0 && !amp) return set_err(GF_E_INVALID_ARGUMENT, "amp must not be NULL");
   int rc = gf_backward_reduce(cfg, out_features, in_features, k, grad_delta, row_coords, col_coords,
                               mu, chol_raw, tile_ptr, tile_ptr_is_int64, gaussian_ids, ids_is_int64,
-                              num_pairs, forward_workspace, workspace, workspace_bytes, stream);
+                              num_pairs, pair_constants, workspace, workspace_bytes, stream);
   if (rc) return rc;
   return gf_backward_finish(cfg, out_features, in_features, k, chol_raw, amp, d_mu, d_chol_raw, d_amp,
                             workspace, workspace_bytes, stream);

@@ -41,6 +41,9 @@ class FieldPlan:
         self.tile_ptr = torch.empty(self.T + 1, dtype=torch.int64, device=dev)
         self.num_pairs = torch.empty(1, dtype=torch.int64, device=dev)
         self.ids = torch.empty(max(self.capacity, 1), dtype=torch.int64, device=dev)
+        # evaluation constants of each pair's Gaussian, in the order of ``ids``
+        self.pair_constants = torch.empty(max(self.capacity, 1) * N.GF_PAIR_CONSTANT_BYTES // 4,
+                                          dtype=torch.float32, device=dev)
         self.delta = torch.empty(self.M * self.N, dtype=torch.float32, device=dev)
         self.d_mu = torch.empty(self.K, 2, dtype=torch.float32, device=dev)
         self.d_chol_raw = torch.empty(self.K, 3, dtype=torch.float32, device=dev)
@@ -57,17 +60,19 @@ class FieldPlan:
                                        self.num_pairs.data_ptr(), None, self.fwd_ws.data_ptr(),
                                        self.fwd_ws_bytes, self._stream()), "gf_forward_bin")
 
-    def emit(self, mu) -> None:
+    def emit(self, mu, amp) -> None:
         N.check(N.lib().gf_forward_emit(ctypes.byref(self.cfg), self.M, self.N, self.K, N.ptr(mu),
-                                        self.tile_ptr.data_ptr(), self.ids.data_ptr(), self.capacity,
+                                        N.ptr(amp), self.tile_ptr.data_ptr(), self.ids.data_ptr(),
+                                        self.pair_constants.data_ptr(), self.capacity,
                                         self.fwd_ws.data_ptr(), self.fwd_ws_bytes, self._stream()),
                 "gf_forward_emit")
 
-    def render(self, row_coords, col_coords, amp) -> torch.Tensor:
-        """Renders from the Gaussian constants the last ``emit`` stored in the workspace."""
+    def render(self, row_coords, col_coords) -> torch.Tensor:
+        """Renders from the pair constants the last ``emit`` wrote (and sorts ids and constants)."""
         N.check(N.lib().gf_forward_render(ctypes.byref(self.cfg), self.M, self.N, self.K,
-                                          row_coords.data_ptr(), col_coords.data_ptr(), N.ptr(amp),
-                                          self.tile_ptr.data_ptr(), self.ids.data_ptr(), self.capacity,
+                                          row_coords.data_ptr(), col_coords.data_ptr(),
+                                          self.tile_ptr.data_ptr(), self.ids.data_ptr(),
+                                          self.pair_constants.data_ptr(), self.capacity,
                                           self.delta.data_ptr(), self.fwd_ws.data_ptr(),
                                           self.fwd_ws_bytes, self._stream()),
                 "gf_forward_render")
@@ -76,15 +81,15 @@ class FieldPlan:
     def forward(self, row_coords, col_coords, mu, chol_raw, amp) -> torch.Tensor:
         """Bins and renders into ``self.delta`` (and ``tile_ptr`` / ``ids``); returns delta."""
         self.bin(mu, chol_raw)
-        self.emit(mu)
-        return self.render(row_coords, col_coords, amp)
+        self.emit(mu, amp)
+        return self.render(row_coords, col_coords)
 
     def backward_reduce(self, grad, row_coords, col_coords, mu, chol_raw, num_pairs: int | None = None,
                         reuse_forward: bool = True):
-        """Per-tile moments.  With ``reuse_forward`` the Gaussian constants come from the last
-        forward's workspace (same mu / chol_raw), else they are recomputed from mu / chol_raw."""
+        """Per-tile moments.  With ``reuse_forward`` the Gaussian constants are the last forward's
+        pair constants (same mu / chol_raw), else they are recomputed from mu / chol_raw."""
         n = self.capacity if num_pairs is None else int(num_pairs)
-        fwd = self.fwd_ws.data_ptr() if reuse_forward else None
+        fwd = self.pair_constants.data_ptr() if reuse_forward else None
         N.check(N.lib().gf_backward_reduce(ctypes.byref(self.cfg), self.M, self.N, self.K,
                                            grad.data_ptr(), row_coords.data_ptr(), col_coords.data_ptr(),
                                            N.ptr(mu), N.ptr(chol_raw), self.tile_ptr.data_ptr(), 1,

@@ -82,32 +82,37 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
                    int64_t* tile_ptr, int64_t* num_pairs_dev, int64_t* num_pairs_host,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes per pair of the pair-constants buffer (evaluation constants of the pair's Gaussian,
+ * in the order of gaussian_ids_sorted). */
+#define GF_PAIR_CONSTANT_BYTES 32
+
 /*
  * Forward phase 2 (emission): writes the (tile, gaussian) pairs into gaussian_ids_sorted,
  * each tile's ids inside its [tile_ptr[t], tile_ptr[t+1]) range (order fixed by phase 3),
- * and stores each Gaussian's evaluation constants in the workspace (from the covariances
- * gf_forward_bin left there), which gf_forward_render and (optionally) gf_backward reuse.
- * Must follow gf_forward_bin on the same stream with the same workspace, tile_ptr and mu.
+ * and beside each id the evaluation constants of its Gaussian (from the covariance
+ * gf_forward_bin left in the workspace, with amp applied).  Must follow gf_forward_bin on the
+ * same stream with the same workspace, tile_ptr and mu.
  *   gaussian_ids_sorted [ids_capacity] int64 out; pairs beyond the capacity are dropped and
  *                   GF_STATUS_CAPACITY is set
+ *   pair_constants  [ids_capacity * GF_PAIR_CONSTANT_BYTES] out, same indexing as the ids
  * Replaces reference forward.cu:465-482 (emit_tile_pairs_kernel + radix sort on the tile key).
  */
 int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                    const float* mu, const int64_t* tile_ptr,
-                    int64_t* gaussian_ids_sorted, int64_t ids_capacity,
+                    const float* mu, const float* amp, const int64_t* tile_ptr,
+                    int64_t* gaussian_ids_sorted, void* pair_constants, int64_t ids_capacity,
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Forward phase 3 (render): puts every tile's ids in canonical order (gaussian id ascending;
- * with tile-major ranges this is the (tile, gaussian) order of a stable sort) and renders
- * delta-W.  Must follow gf_forward_emit on the same stream with the same workspace (the
- * Gaussian geometry comes from the constants gf_forward_bin stored there; amp is read here).
+ * with tile-major ranges this is the (tile, gaussian) order of a stable sort), the pair
+ * constants with them, and renders delta-W from the constants gf_forward_emit wrote.  Must
+ * follow gf_forward_emit on the same stream with the same workspace, ids and pair_constants.
  *   delta           [out_features*in_features] fp32 out, row-major; every element written
  * Replaces reference forward.cu:513-569 (tile_accumulate_kernel; delta needs no pre-zeroing).
  */
 int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                      const float* row_coords, const float* col_coords, const float* amp,
-                      const int64_t* tile_ptr, int64_t* gaussian_ids_sorted, int64_t ids_capacity,
+                      const float* row_coords, const float* col_coords, const int64_t* tile_ptr,
+                      int64_t* gaussian_ids_sorted, void* pair_constants, int64_t ids_capacity,
                       float* delta, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -118,9 +123,9 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
  *   tile_ptr        [T+1], int64 if tile_ptr_is_int64 else int32
  *   gaussian_ids    [num_pairs], int64 if ids_is_int64 else int32 (any order within a tile)
  *   d_mu [K,2], d_chol_raw [K,3], d_amp [K,1] fp32 out (fully written)
- *   forward_workspace  optional: the workspace of the gf_forward_bin call over the same
- *                   (mu, chol_raw) and config (after its gf_forward_emit); its evaluation constants are reused instead of
- *                   recomputed from mu / chol_raw.  NULL recomputes them.
+ *   pair_constants  optional: the pair constants of the forward (after its gf_forward_render)
+ *                   over the same (mu, chol_raw), config, tile_ptr and ids; read beside the
+ *                   ids instead of recomputing each Gaussian's constants.  NULL recomputes.
  * Saved-state violations (non-monotone tile_ptr, tile_ptr[T] != num_pairs, ids outside
  * [0,K)) are detected on the device, the offending pairs skipped, and status bits set.
  * Replaces reference backward.cu:541-716 (backward_pair_reduce_train).
@@ -130,7 +135,7 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
                 const float* mu, const float* chol_raw, const float* amp,
                 const void* tile_ptr, int32_t tile_ptr_is_int64,
                 const void* gaussian_ids, int32_t ids_is_int64, int64_t num_pairs,
-                float* d_mu, float* d_chol_raw, float* d_amp, const void* forward_workspace,
+                float* d_mu, float* d_chol_raw, float* d_amp, const void* pair_constants,
                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* First half of gf_backward (reference backward.cu:592-702: per-pair partials + reduce-by-key). */
@@ -139,7 +144,7 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
                        const float* mu, const float* chol_raw,
                        const void* tile_ptr, int32_t tile_ptr_is_int64,
                        const void* gaussian_ids, int32_t ids_is_int64, int64_t num_pairs,
-                       const void* forward_workspace, void* workspace, size_t workspace_bytes,
+                       const void* pair_constants, void* workspace, size_t workspace_bytes,
                        void* stream);
 
 /* Second half of gf_backward (reference backward.cu:436-496,704-715: cov -> chol_raw chain). */
