@@ -1,17 +1,23 @@
 #!/usr/bin/env python3
 """Benchmark: Gaussian-field delta-W elements/s for forward + backward on one MI355X.
 
-A step is one forward (binning + render) and one backward (gradient reduction + chain rule) of
-one layer's field, with inputs resident in HBM, issued through the sync-free C ABI path
-(guass_amd.ops.FieldPlan) and replayed from a HIP graph.  Workload
-("cfg3"), 1280x1280 fp32 delta-W from K=1024 Gaussians, 16x16 tiles, 3 sigma, clamp 80.
+A step is one forward (binning + render) and one backward (gradient reduction + chain rule),
+with inputs resident in HBM, issued through the sync-free C ABI path and replayed from a HIP
+graph.  Workloads:
+  cfg3 (default, the headline)  one 1280x1280 fp32 delta-W from K=1024 Gaussians
+                                (guass_amd.ops.FieldPlan: five launches per step)
+  cfg4                          all 128 attention linears of an SD1.5-shaped UNet, K=1024 each,
+                                as one batch (guass_amd.ops.FieldBatchPlan: five launches per
+                                step for all layers)
+  cfg1, cfg2, cfg5, cfg5c       single fields as cfg3
+All with 16x16 tiles, 3 sigma, clamp 80.
 
 Prints one JSON line (metric contract of the driver) with two extra objects:
   roofline      the dominant kernel's achieved throughput against MI355X peak; its duration is
                 measured live with HIP events on the launch stream around a graph of repeated
                 launches of that kernel (replay time / launch count);
   cpu_baseline  the CPU oracle (a from-scratch port of the reference's torch CPU path) timed on
-                this host on the same inputs.
+                this host on the same inputs (for cfg4, on a stated subset of the layers).
 """
 
 from __future__ import annotations
@@ -39,7 +45,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg5", "cfg5c"])
+    ap.add_argument("--config", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "cfg5c"])
+    ap.add_argument("--layers", type=int, default=None, help="cfg4: first N of the 128 layers")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of graph replay")
     ap.add_argument("--graph-steps", type=int, default=10,
@@ -47,12 +54,12 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--kernel-reps", type=int, default=20, help="launches per per-kernel timing graph")
     ap.add_argument("--kernel-replays", type=int, default=25, help="timed replays per kernel graph")
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB (the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     ap.add_argument("--traffic-file", default=str(ROOT / "profiles" / "cfg3_hbm_traffic.json"),
                     help="per-kernel HBM bytes per launch measured with rocprofv3 --pmc")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
 
@@ -68,6 +75,7 @@ def algorithmic_counts(tile_ptr, M: int, N: int, K: int, tile_out: int, tile_in:
     cols[-1] = N - (C - 1) * tile_in
     E = float((counts * rows.reshape(-1, 1) * cols.reshape(1, -1)).sum())
     return {
+        "elements": float(M * N),
         "pairs": int(tile_ptr[-1].item()),
         "evals": E,
         # per fwd+bwd: write delta + read dL/ddelta (4 B each per element), read 24 B and
@@ -78,6 +86,10 @@ def algorithmic_counts(tile_ptr, M: int, N: int, K: int, tile_out: int, tile_in:
         "flops_fwd": FWD_FLOPS_PER_EVAL * E,
         "flops_bwd": BWD_FLOPS_PER_EVAL * E,
     }
+
+
+def sum_counts(items: list[dict]) -> dict:
+    return {k: sum(c[k] for c in items) for k in items[0]}
 
 
 def roofline(bytes_: float, flops: float, seconds: float) -> dict:
@@ -106,16 +118,19 @@ def traffic_bytes(path: str, config: str, kernel: str):
     return None if entry is None else float(entry["hbm_bytes_per_launch"])
 
 
-def cpu_baseline(problem, reps: int) -> dict:
+def cpu_baseline(problems, reps: int, note: str) -> dict:
     import torch
 
     from oracle import field_oracle as fo  # CPU baseline leg only
 
     cores = min(len(os.sched_getaffinity(0)), 16)
     torch.set_num_threads(cores)
-    p = problem
-    run = lambda: fo.gaussian_field_fwd_bwd(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp,  # noqa: E731
-                                            p.grad, 16, 16, 3.0, False, 80.0)
+
+    def run():
+        for p in problems:
+            fo.gaussian_field_fwd_bwd(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad,
+                                      16, 16, 3.0, False, 80.0)
+
     run()  # warmup
     times = []
     for _ in range(reps):
@@ -123,10 +138,11 @@ def cpu_baseline(problem, reps: int) -> dict:
         run()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    return {"value": p.out_features * p.in_features / med, "unit": "ΔW elements/s",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"{p.name} seed {p.meta['seed']}: full layer fwd+bwd (per-tile loop + autograd), "
-                      f"1 warmup + median of {reps}, {med:.2f} s each"}
+    elements = sum(p.out_features * p.in_features for p in problems)
+    return {"value": elements / med, "unit": "ΔW elements/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{note}: fwd+bwd (per-tile loop + autograd), 1 warmup + median of {reps}, "
+                      f"{med:.2f} s each"}
 
 
 def main() -> int:
@@ -139,9 +155,10 @@ def main() -> int:
 
     import torch
 
+    from guass_amd import _native as Nat
     from guass_amd import workloads as wl
     from guass_amd.cuda_field import ext
-    from guass_amd.ops import FieldPlan
+    from guass_amd.ops import FieldBatchPlan, FieldPlan
 
     dev = torch.device("cuda:0")
     if args.calibrate_copy_mib > 0:
@@ -152,20 +169,49 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    prob = wl.CONFIGS[args.config](args.seed)
-    q = prob.to(dev)
-    M, N, K = prob.out_features, prob.in_features, prob.k
 
-    # Pair count of this input (one synchronising drop-in forward), then a sync-free plan.
-    _, tp0, _ = ext.gaussian_field_forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
-                                           16, 16, 3.0, False, 80.0)
-    counts = algorithmic_counts(tp0, M, N, K, 16, 16)
-    P = counts["pairs"]
-    plan = FieldPlan(M, N, K, dev, ids_capacity=P)
+    batched = args.config == "cfg4"
+    probs = wl.cfg4(args.seed, layers=args.layers) if batched else [wl.CONFIGS[args.config](args.seed)]
+    qs = [p.to(dev) for p in probs]
+    # Pair count of every field (one synchronising drop-in forward each), then sync-free plans.
+    counts = []
+    for p, q in zip(probs, qs):
+        _, tp0, _ = ext.gaussian_field_forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
+                                               16, 16, 3.0, False, 80.0)
+        counts.append(algorithmic_counts(tp0, p.out_features, p.in_features, p.k, 16, 16))
+    total = sum_counts(counts)
 
-    def step():
-        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
-        plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
+    if batched:
+        batch = FieldBatchPlan(qs, dev, capacities=[c["pairs"] for c in counts])
+
+        def step():
+            batch.forward()
+            batch.backward()
+
+        phases = {
+            "k_bin": [lambda: batch.forward(Nat.GF_PHASE_BIN)],
+            "k_emit+": [lambda: batch.forward(Nat.GF_PHASE_BIN | Nat.GF_PHASE_EMIT)],
+            "k_render": [lambda: batch.forward(Nat.GF_PHASE_RENDER)],
+            "k_bwd": [lambda: batch.backward(Nat.GF_PHASE_REDUCE)],
+            "k_bwd_finish": [lambda: batch.backward(Nat.GF_PHASE_FINISH)],
+        }
+        status = lambda: max(batch.status())  # noqa: E731
+    else:
+        q, P = qs[0], counts[0]["pairs"]
+        plan = FieldPlan(probs[0].out_features, probs[0].in_features, probs[0].k, dev, ids_capacity=P)
+
+        def step():
+            plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+            plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
+
+        phases = {
+            "k_bin": [lambda: plan.bin(q.mu, q.chol_raw)],
+            "k_emit+": [lambda: plan.bin(q.mu, q.chol_raw), lambda: plan.emit(q.mu, q.amp)],
+            "k_render": [lambda: plan.render(q.row_coords, q.col_coords)],
+            "k_bwd": [lambda: plan.backward_reduce(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, P)],
+            "k_bwd_finish": [lambda: plan.backward_finish(q.chol_raw, q.amp)],
+        }
+        status = plan.status
 
     stream = torch.cuda.Stream(dev)
     stream.wait_stream(torch.cuda.current_stream(dev))
@@ -201,16 +247,16 @@ def main() -> int:
     wall = time.perf_counter() - t0
     gpu_ms = ev0.elapsed_time(ev1)
     ms_per_step = 1e3 * wall / args.steps
-    status = plan.status()
-    if status:
-        print(f"device status bits {status:#x} after the timed run", file=sys.stderr)
+    st = status()
+    if st:
+        print(f"device status bits {st:#x} after the timed run", file=sys.stderr)
         return 1
 
     # Per-kernel durations: each kernel captured `--kernel-reps` times back to back in one HIP
     # graph, replayed on a side stream bracketed by HIP events recorded on that same stream; the
     # duration is the replay time over the launch count, which matches what rocprofv3's kernel
     # trace reports for the same launches (back-to-back kernels, no host gaps).  Every kernel is
-    # idempotent under repetition except k_emit (its tile cursors advance), so k_emit is timed
+    # idempotent under repetition except k_emit (its fill counters advance), so k_emit is timed
     # as (k_bin + k_emit) minus k_bin; repeated k_bwd only grows the accumulators, which the
     # trailing k_bwd_finish clears.
     def graph_time_us(fns) -> float:
@@ -235,32 +281,29 @@ def main() -> int:
         torch.cuda.synchronize()
         return statistics.median(times)
 
-    k_bin = lambda: plan.bin(q.mu, q.chol_raw)  # noqa: E731
-    k_emit = lambda: plan.emit(q.mu, q.amp)  # noqa: E731
-    k_render = lambda: plan.render(q.row_coords, q.col_coords)  # noqa: E731
-    k_bwd = lambda: plan.backward_reduce(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, P)  # noqa: E731
-    k_fin = lambda: plan.backward_finish(q.chol_raw, q.amp)  # noqa: E731
-    ph = {"k_bin": graph_time_us([k_bin])}
-    ph["k_emit"] = graph_time_us([k_bin, k_emit]) - ph["k_bin"]
-    ph["k_render"] = graph_time_us([k_render])
-    ph["k_bwd"] = graph_time_us([k_bwd])
-    ph["k_bwd_finish"] = graph_time_us([k_fin])
-    ph = {k: v / 1e3 for k, v in ph.items()}  # ms
-    # leave the plan in the state of one clean step
-    step()
+    ph = {name: graph_time_us(fns) for name, fns in phases.items()}
+    ph["k_emit"] = ph.pop("k_emit+") - ph["k_bin"]
+    ph = {k: ph[k] / 1e3 for k in ("k_bin", "k_emit", "k_render", "k_bwd", "k_bwd_finish")}  # ms
+    step()  # leave the plan in the state of one clean step
     torch.cuda.synchronize()
 
-    value = M * N / (ms_per_step / 1e3)
+    value = total["elements"] / (ms_per_step / 1e3)
     kernel_rooflines = {
-        "k_render": roofline(counts["bytes_fwd_render"], counts["flops_fwd"], ph["k_render"] / 1e3),
-        "k_bwd": roofline(counts["bytes_bwd"], counts["flops_bwd"], ph["k_bwd"] / 1e3),
+        "k_render": roofline(total["bytes_fwd_render"], total["flops_fwd"], ph["k_render"] / 1e3),
+        "k_bwd": roofline(total["bytes_bwd"], total["flops_bwd"], ph["k_bwd"] / 1e3),
     }
     dominant = max(kernel_rooflines, key=lambda k: ph[k])
     roof = dict(kernel_rooflines[dominant])
     roof.update({"kernel": dominant, "traffic": traffic_bytes(args.traffic_file, args.config, dominant),
                  "duration_us": ph[dominant] * 1e3})
-    step_roof = roofline(counts["bytes_step"], counts["flops_fwd"] + counts["flops_bwd"],
-                         ms_per_step / 1e3)
+    step_roof = roofline(total["bytes_step"], total["flops_fwd"] + total["flops_bwd"], ms_per_step / 1e3)
+    if batched:
+        workload = f"cfg4 SD1.5 attention linears x{len(probs)} (one batch) fwd+bwd, 16x16 tiles, 3 sigma, clamp 80"
+        shape = {"layers": len(probs), "sum_out_x_in": int(total["elements"]), "k_per_layer": 1024}
+    else:
+        p = probs[0]
+        workload = f"{p.name} fwd+bwd, 16x16 tiles, 3 sigma, clamp 80"
+        shape = {"out_features": p.out_features, "in_features": p.in_features, "k": p.k}
     out = {
         "metric": METRIC,
         "value": value,
@@ -274,9 +317,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded Gaussian field, BASELINE.json distribution)",
-        "config": {"workload": f"{prob.name} fwd+bwd, 16x16 tiles, 3 sigma, clamp 80",
-                   "out_features": M, "in_features": N, "k": K, "pairs": P,
-                   "pair_pixel_evals": counts["evals"],
+        "config": {"workload": workload, **shape, "pairs": int(total["pairs"]),
+                   "pair_pixel_evals": total["evals"],
                    "launch": (f"hip graph replay, {per_run} steps per graph" if graph is not None
                               else "eager")},
         "roofline": roof,
@@ -286,7 +328,14 @@ def main() -> int:
         "gpu_event_ms_per_step": gpu_ms / args.steps,
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(prob, args.cpu_reps)
+        if batched:
+            sub = probs[:2]
+            note = (f"cfg4 seed {args.seed}, first {len(sub)} of {len(probs)} layers "
+                    f"({'+'.join(f'{p.out_features}x{p.in_features}' for p in sub)})")
+        else:
+            sub = probs
+            note = f"{probs[0].name} seed {args.seed}, the full layer"
+        out["cpu_baseline"] = cpu_baseline(sub, args.cpu_reps, note)
     print(json.dumps(out), flush=True)
     return 0
 

@@ -17,7 +17,6 @@ import torch  # noqa: F401  (must precede the dlopen below)
 LIB_PATH = Path(__file__).resolve().with_name("libgaussfield.so")
 
 GF_OK = 0
-GF_PAIR_CONSTANT_BYTES = 32  # per pair, include/gaussfield.h
 GF_STATUS_CAPACITY = 0x1
 GF_STATUS_COUNT_MISMATCH = 0x2
 GF_STATUS_TILE_PTR_LAST = 0x4
@@ -30,8 +29,12 @@ EXPORTED = (
     "gf_version", "gf_last_error", "gf_tile_grid", "gf_forward_workspace_bytes",
     "gf_backward_workspace_bytes", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
     "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
-    "gf_selftest_softplus",
+    "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward",
 )
+
+GF_PHASE_BIN, GF_PHASE_EMIT, GF_PHASE_RENDER = 0x1, 0x2, 0x4
+GF_PHASE_REDUCE, GF_PHASE_FINISH = 0x1, 0x2
+GF_PHASE_ALL = 0xFF
 
 
 class GfFieldConfig(ctypes.Structure):
@@ -44,6 +47,29 @@ class GfFieldConfig(ctypes.Structure):
         ("normalize", c_int32),
         ("has_clamp_quad", c_int32),
         ("clamp_quad", c_double),
+    ]
+
+
+class GfLayer(ctypes.Structure):
+    """``gf_layer``: one field of a batch (device pointers)."""
+
+    _fields_ = [
+        ("out_features", c_int64), ("in_features", c_int64), ("k", c_int64),
+        ("row_coords", c_void_p), ("col_coords", c_void_p), ("mu", c_void_p),
+        ("chol_raw", c_void_p), ("amp", c_void_p), ("delta", c_void_p), ("tile_ptr", c_void_p),
+        ("num_pairs", c_void_p), ("gaussian_ids", c_void_p), ("ids_capacity", c_int64), ("forward_workspace", c_void_p),
+        ("forward_workspace_bytes", c_size_t), ("grad_delta", c_void_p), ("d_mu", c_void_p),
+        ("d_chol_raw", c_void_p), ("d_amp", c_void_p), ("backward_workspace", c_void_p),
+        ("backward_workspace_bytes", c_size_t),
+    ]
+
+
+class GfBatchInfo(ctypes.Structure):
+    """``gf_batch_info``."""
+
+    _fields_ = [
+        ("n_layers", c_int32), ("has_backward", c_int32), ("tile_blocks", c_int64),
+        ("emit_blocks", c_int64), ("finish_blocks", c_int64), ("plan_bytes", c_size_t),
     ]
 
 
@@ -76,9 +102,9 @@ def lib() -> ctypes.CDLL:
     L.gf_backward_workspace_bytes.argtypes = [c_int64, c_int64, c_int64, _CFG]
     L.gf_backward_workspace_bytes.restype = c_size_t
     L.gf_forward_bin.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_size_t, _P]
-    L.gf_forward_emit.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, c_int64, _P,
+    L.gf_forward_emit.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, c_int64, _P,
                                   c_size_t, _P]
-    L.gf_forward_render.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P,
+    L.gf_forward_render.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P,
                                     c_int64, _P, _P, c_size_t, _P]
     L.gf_backward.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int32,
                               _P, c_int32, c_int64, _P, _P, _P, _P, _P, c_size_t, _P]
@@ -86,10 +112,13 @@ def lib() -> ctypes.CDLL:
                                      _P, c_int32, c_int64, _P, _P, c_size_t, _P]
     L.gf_backward_finish.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_size_t, _P]
     L.gf_read_status.argtypes = [_P, c_int32, POINTER(c_uint32), _P]
+    L.gf_batch_plan.argtypes = [_CFG, POINTER(GfLayer), c_int32, _P, c_size_t, POINTER(GfBatchInfo), _P]
+    L.gf_batch_forward.argtypes = [_P, POINTER(GfBatchInfo), c_uint32, _P]
+    L.gf_batch_backward.argtypes = [_P, POINTER(GfBatchInfo), c_uint32, _P]
     L.gf_selftest_softplus.argtypes = [POINTER(c_uint64), _P]
     for name in ("gf_tile_grid", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
                  "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
-                 "gf_selftest_softplus"):
+                 "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward"):
         getattr(L, name).restype = c_int
     _LIB = L
     return L

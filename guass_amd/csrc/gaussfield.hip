@@ -30,6 +30,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <vector>
 
 #include "../../include/gaussfield.h"
 #include "geometry.h"
@@ -436,11 +437,16 @@ __device__ inline void bin_scan_rows(const int32_t* lds, int32_t C, int32_t nb, 
   }
 }
 
-__global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __restrict__ mu,
-                                                     const float* __restrict__ chol_raw,
-                                                     int64_t* __restrict__ tile_ptr,
-                                                     int64_t* __restrict__ num_pairs, uint8_t* ws,
-                                                     FwdLayout L) {
+// The binning of one field by one workgroup of kBinThreads threads.  With kEval it also
+// stores each Gaussian's evaluation constants (one Gaussian per thread: the batched path, where
+// every field has its own workgroup); otherwise k_emit computes them.
+template <bool kEval>
+__device__ __forceinline__ void bin_body(const Problem& p, const float* __restrict__ mu,
+                                         const float* __restrict__ chol_raw,
+                                         const float* __restrict__ amp,
+                                         int64_t* __restrict__ tile_ptr,
+                                         int64_t* __restrict__ num_pairs, uint8_t* ws,
+                                         const FwdLayout& L) {
   __shared__ int32_t lds[kLdsDiffWords];
   __shared__ int64_t rowbase[kBinMaxBandRows + 1];
   __shared__ int32_t rowdiff[kBinMaxBandRows + 1];
@@ -480,6 +486,11 @@ __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __r
     rect[g] = r;
     covs[g] = make_float4(c.s00, c.s01, c.s11, 0.0f);
     my_pairs += touched;
+    if (kEval) {
+      GaussEval v = eval_from_cov(p, mu[2 * g + 0], mu[2 * g + 1], c, amp[g]);
+      v.gid = (int32_t)g;
+      store_eval(reinterpret_cast<GaussEval*>(ws + L.eval), g, v);
+    }
     return r;
   };
 #pragma unroll
@@ -576,65 +587,112 @@ __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __r
   }
 }
 
+__global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __restrict__ mu,
+                                                     const float* __restrict__ chol_raw,
+                                                     int64_t* __restrict__ tile_ptr,
+                                                     int64_t* __restrict__ num_pairs, uint8_t* ws,
+                                                     FwdLayout L) {
+  bin_body<false>(p, mu, chol_raw, nullptr, tile_ptr, num_pairs, ws, L);
+}
+
 // ------------------------------------------------------------------------------------------
 // k_emit: one wave per Gaussian; the wave's lanes walk the Gaussian's tile rectangle row-major
 // and claim a slot of each tile's id segment, tile_ptr[t] + an atomic on the tile's fill count.  The order
 // inside a segment is fixed afterwards by the render, which sorts each segment.
 
-__global__ __launch_bounds__(kEmitThreads) void k_emit(Problem p, const float* __restrict__ mu,
-                                                       const float* __restrict__ amp, uint8_t* ws,
-                                                       FwdLayout L, const int64_t* __restrict__ tile_ptr,
-                                                       int64_t* __restrict__ ids,
-                                                       GaussEval* __restrict__ pair_ev, int64_t capacity) {
+// The emission of Gaussians g0 .. g0 + 64/SG - 1 of one field by one wave, SG lanes per
+// Gaussian; each lane keeps up to B slot atomics in flight before it uses their results.  With
+// kEval the first lane of a Gaussian's lanes also computes its evaluation constants
+// (overlapping the first atomics) and stores them (otherwise bin_body<true> did).
+template <bool kEval, int SG, int B>
+__device__ __forceinline__ void emit_body(const Problem& p, const float* __restrict__ mu,
+                                          const float* __restrict__ amp, uint8_t* ws,
+                                          const FwdLayout& L, const int64_t* __restrict__ tile_ptr,
+                                          int64_t* __restrict__ ids, int64_t capacity, int64_t g0) {
+  static_assert(SG >= 1 && SG <= 64 && (64 % SG) == 0, "sub-group size must divide 64");
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   const int4* __restrict__ rect = reinterpret_cast<const int4*>(ws + L.rect);
-  int32_t* fill = reinterpret_cast<int32_t*>(ws + L.fill);
+  uint32_t* fill = reinterpret_cast<uint32_t*>(ws + L.fill);
   const int lane = threadIdx.x & 63;
-  const int64_t g = (int64_t)blockIdx.x * (kEmitThreads / 64) +
-                    __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
-  if (g >= p.K) return;
-  const int4 r = rect[g];
+  const int sub = lane / SG, sl = lane - sub * SG;
+  const int64_t g = g0 + sub;
+  if (g0 >= p.K) return;
+  const bool valid = g < p.K;
+  const int4 r = valid ? rect[g] : make_int4(1, 0, 1, 0);
   const int32_t w = r.w - r.z + 1;
-  const int32_t n = (r.y - r.x + 1) * w;
+  const int32_t n = valid ? (r.y - r.x + 1) * w : 0;
   auto tile_of = [&](int32_t l) -> int64_t {
     const int32_t dr = (int32_t)((uint32_t)l / (uint32_t)w);
     return (int64_t)(r.x + dr) * p.C + (r.z + (l - dr * w));
   };
-  // First round of slot atomics in flight while lane 0 computes the Gaussian's evaluation
-  // constants; the returned slot is only combined with tile_ptr afterwards.
-  int64_t base0 = 0;
-  uint32_t slot0 = 0u;  // unsigned: widening it needs no instruction that would wait for it
-  if (lane < n) {
-    const int64_t t = tile_of(lane);
-    base0 = tile_ptr[t];
-    slot0 = atomicAdd(reinterpret_cast<uint32_t*>(fill) + t, 1u);
-  }
-  GaussEval mine = zero_eval();
-  if (lane == 0) {
-    GaussEval* ev = reinterpret_cast<GaussEval*>(ws + L.eval);
+  // Slots of pairs l = base + sl + j*SG (j < B): base from tile_ptr plus the tile's fill count.
+  // The unsigned slot widens without an instruction that would wait for the atomic early.
+  int64_t bases[B];
+  uint32_t slots[B];
+  auto claim = [&](int32_t lb) {
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const int32_t l = lb + sl + j * SG;
+      bases[j] = 0;
+      slots[j] = 0u;
+      if (l < n) {
+        const int64_t t = tile_of(l);
+        bases[j] = tile_ptr[t];
+        slots[j] = atomicAdd(fill + t, 1u);
+      }
+    }
+  };
+  claim(0);
+  if (kEval && sl == 0 && valid) {
     const float4 c4 = reinterpret_cast<const float4*>(ws + L.cov)[g];
     GfCov c;
     c.s00 = c4.x;
     c.s01 = c4.y;
     c.s11 = c4.z;
-    mine = eval_from_cov(p, mu[2 * g + 0], mu[2 * g + 1], c, amp[g]);
-    mine.gid = (int32_t)g;
-    store_eval(ev, g, mine);
+    GaussEval v = eval_from_cov(p, mu[2 * g + 0], mu[2 * g + 1], c, amp[g]);
+    v.gid = (int32_t)g;
+    store_eval(reinterpret_cast<GaussEval*>(ws + L.eval), g, v);
   }
-  const GaussEval v = readlane_eval(mine, 0);
-  auto place = [&](int64_t pos) {
-    if (pos < capacity) {
-      ids[pos] = g;
-      store_eval(pair_ev, pos, v);
-    } else {
-      set_status(&hdr->status, GF_STATUS_CAPACITY);
+  auto place = [&](int32_t lb) {
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      if (lb + sl + j * SG < n) {
+        const int64_t pos = bases[j] + (int64_t)slots[j];
+        if (pos < capacity) {
+          ids[pos] = g;
+        } else {
+          set_status(&hdr->status, GF_STATUS_CAPACITY);
+        }
+      }
     }
   };
-  if (lane < n) place(base0 + (int64_t)slot0);
-  for (int32_t l = lane + 64; l < n; l += 64) {
-    const int64_t t = tile_of(l);
-    place(tile_ptr[t] + atomicAdd(fill + t, 1));
+  place(0);
+  // Larger rectangles: further rounds of B*SG pairs per Gaussian while any of the wave's
+  // Gaussians has pairs left.
+  int32_t nmax = n;
+#pragma unroll
+  for (int k = 0; k < 64 / SG; ++k) nmax = max(nmax, __builtin_amdgcn_readlane(n, k * SG));
+  for (int32_t lb = B * SG; lb < nmax; lb += B * SG) {
+    claim(lb);
+    place(lb);
   }
+}
+
+// Gaussians per emission wave: the single-field kernel uses a whole wave per Gaussian (few
+// Gaussians, so latency matters); the batched one packs 4 Gaussians per wave (many Gaussians,
+// so the number of waves in flight matters).
+constexpr int kEmitLanesSingle = 64;
+constexpr int kEmitLanesBatch = 16;
+
+__device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6)); }
+
+__global__ __launch_bounds__(kEmitThreads) void k_emit(Problem p, const float* __restrict__ mu,
+                                                       const float* __restrict__ amp, uint8_t* ws,
+                                                       FwdLayout L, const int64_t* __restrict__ tile_ptr,
+                                                       int64_t* __restrict__ ids, int64_t capacity) {
+  emit_body<true, kEmitLanesSingle, 1>(
+      p, mu, amp, ws, L, tile_ptr, ids, capacity,
+      ((int64_t)blockIdx.x * (kEmitThreads / 64) + wave_id()) * (64 / kEmitLanesSingle));
 }
 
 
@@ -838,15 +896,15 @@ __device__ inline void tile_range(const int64_t* __restrict__ tile_ptr, int64_t 
 // 16x16 tiles, one wave per tile (tile blockIdx.x * 4 + wave).  Lane l covers tile row l/4,
 // columns 4*(l%4)..+3.  Gaussian constants are computed one per lane for up to 64 Gaussians at
 // a time and broadcast with readlane while every lane accumulates its 4 pixels.
-__global__ __launch_bounds__(kTileThreads) void k_render16(
-    Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
+// Tile t (16x16) of one field by one wave.
+__device__ __forceinline__ void render16_body(
+    const Problem& p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids,
-    GaussEval* pair_ev, int64_t capacity, float* __restrict__ delta, uint8_t* ws) {
+    int64_t capacity, float* __restrict__ delta, uint8_t* ws, int64_t t) {
   __shared__ int32_t wkeys[kTileThreads / 64][kWaveSortKeys];
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
-  const int64_t t = (int64_t)blockIdx.x * (kTileThreads / 64) + wid;
   if (t >= (int64_t)p.R * p.C) return;
   const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (t / p.C) * p.C);
   const int32_t pr = tr * 16 + (lane >> 2), pc = tc * 16 + ((lane & 3) << 2);
@@ -870,13 +928,13 @@ __global__ __launch_bounds__(kTileThreads) void k_render16(
     }
   };
   if (n > 0 && n <= 64) {
-    // ids and their constants (emission order) in one round trip; rank sort by id; the
-    // constants follow their id to lane `rank` (ds_permute) and both go back sorted.
+    // Rank sort of the ids (emission order); each lane gathers its Gaussian's constants while
+    // the ranks are computed, then they follow their id to lane `rank` (ds_permute).
     GaussEval my = zero_eval();
     int32_t key = INT32_MAX;
     if (lane < n) {
       key = (int32_t)ids[s + lane];
-      my = load_eval(pair_ev, s + lane);
+      if (key >= 0 && key < p.K) my = load_eval(ev, key);
     }
     int rank = 0;
     for (int j = 0; j < (int)n; ++j) rank += (__builtin_amdgcn_readlane(key, j) < key) ? 1 : 0;
@@ -888,12 +946,11 @@ __global__ __launch_bounds__(kTileThreads) void k_render16(
     srt.wb = __int_as_float(__builtin_amdgcn_ds_permute(addr, __float_as_int(my.wb)));
     srt.wc = __int_as_float(__builtin_amdgcn_ds_permute(addr, __float_as_int(my.wc)));
     srt.w = __int_as_float(__builtin_amdgcn_ds_permute(addr, __float_as_int(my.w)));
-    srt.gid = __builtin_amdgcn_ds_permute(addr, key);
+    srt.gid = __builtin_amdgcn_ds_permute(addr, key);  // key == my.gid for a valid id
     srt.pad = 0.0f;
     if (lane < n) {
       if (srt.gid < 0 || srt.gid >= p.K) set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);
-      ids[s + lane] = srt.gid;
-      store_eval(pair_ev, s + lane, srt);
+      if (srt.gid != key) ids[s + lane] = srt.gid;  // lanes whose id moved
     }
     for (int j = 0; j < (int)n; ++j) accumulate(readlane_eval(srt, j));
   } else if (n > 64) {
@@ -907,7 +964,6 @@ __global__ __launch_bounds__(kTileThreads) void k_render16(
         const int64_t g = (n <= kWaveSortKeys) ? (int64_t)keys[j0 + lane] : seg[j0 + lane];
         if (g >= 0 && g < p.K) {
           my = load_eval(ev, g);
-          store_eval(pair_ev, s + j0 + lane, my);
         } else {
           set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);  // internal mismatch only
         }
@@ -927,11 +983,19 @@ __global__ __launch_bounds__(kTileThreads) void k_render16(
   }
 }
 
+__global__ __launch_bounds__(kTileThreads) void k_render16(
+    Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
+    const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids,
+    int64_t capacity, float* __restrict__ delta, uint8_t* ws) {
+  render16_body(p, row_coords, col_coords, ev, tile_ptr, ids, capacity, delta, ws,
+                (int64_t)blockIdx.x * (kTileThreads / 64) + wave_id());
+}
+
 // Any tile shape: each thread evaluates pixels p = tid, tid+256, ... of the tile.
 __global__ __launch_bounds__(kTileThreads) void k_render_any(
     Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids,
-    GaussEval* pair_ev, int64_t capacity, float* __restrict__ delta, uint8_t* ws) {
+    int64_t capacity, float* __restrict__ delta, uint8_t* ws) {
   __shared__ int32_t keys[kSortLdsWords];
   __shared__ int64_t small_lds[kTileThreads / 64 + 1];
   __shared__ GaussEval gl[kTileThreads];
@@ -943,11 +1007,6 @@ __global__ __launch_bounds__(kTileThreads) void k_render_any(
   int64_t* seg = ids + s;
   order_segment(seg, n, p.K, keys, small_lds, &hdr->status);
   const bool keys_in_lds = n <= kSortLdsKeys;
-  // the pair-ordered constants follow the sorted ids
-  for (int64_t i = threadIdx.x; i < n; i += kTileThreads) {
-    const int64_t g = keys_in_lds ? (int64_t)keys[i] : seg[i];
-    if (g >= 0 && g < p.K) store_eval(pair_ev, s + i, load_eval(ev, g));
-  }
   const int32_t r0 = tr * p.tile_out, c0 = tc * p.tile_in;
   const int32_t r1 = min(r0 + p.tile_out, p.M), c1 = min(c0 + p.tile_in, p.N);
   const int32_t w = c1 - c0;
@@ -1014,7 +1073,7 @@ template <typename GIdx>
 __device__ inline void stage_gaussians(const Problem& p, const GIdx* __restrict__ gids, int64_t s,
                                        int64_t j0, int nj, const float* __restrict__ mu,
                                        const float* __restrict__ chol_raw,
-                                       const GaussEval* __restrict__ pair_ev, GaussEval* gl,
+                                       const GaussEval* __restrict__ ev, GaussEval* gl,
                                        int32_t* gid_lds, uint32_t* status) {
   if ((int)threadIdx.x < nj) {
     const int64_t g = (int64_t)gids[s + j0 + threadIdx.x];
@@ -1023,7 +1082,7 @@ __device__ inline void stage_gaussians(const Problem& p, const GIdx* __restrict_
       gid_lds[threadIdx.x] = -1;
       gl[threadIdx.x] = zero_eval();
     } else {
-      gl[threadIdx.x] = pair_ev ? load_eval(pair_ev, s + j0 + threadIdx.x) : eval_geom(p, mu, chol_raw, nullptr, g);
+      gl[threadIdx.x] = ev ? load_eval(ev, g) : eval_geom(p, mu, chol_raw, nullptr, g);
       gid_lds[threadIdx.x] = (int32_t)g;
     }
   }
@@ -1033,18 +1092,17 @@ __device__ inline void stage_gaussians(const Problem& p, const GIdx* __restrict_
 // l%16; per round the four slots take four Gaussians of the tile and each lane sums its row's
 // 16 pixels.  Gaussian constants are computed one per lane for up to 64 Gaussians at a time
 // and fetched by slot with a lane permute.
+// The moments of tile t (16x16) of one field by one wave.
 template <typename TpIdx, typename GIdx>
-__global__ __launch_bounds__(kTileThreads) void k_bwd16(
-    Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
+__device__ __forceinline__ void bwd16_body(
+    const Problem& p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
-    const float* __restrict__ chol_raw, const GaussEval* __restrict__ pair_ev,
+    const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
     const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
-    uint8_t* ws, BwdLayout L) {
+    uint8_t* ws, const BwdLayout& L, int64_t t) {
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   float* acc = reinterpret_cast<float*>(ws + L.acc);
   const int lane = threadIdx.x & 63;
-  const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
-  const int64_t t = (int64_t)blockIdx.x * (kTileThreads / 64) + wid;
   const int64_t T = (int64_t)p.R * p.C;
   if (t >= T) return;
   const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (t / p.C) * p.C);
@@ -1086,13 +1144,11 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd16(
     GaussEval my = zero_eval();
     int32_t myg = -1;
     if (lane < nj) {
-      // the id and (when given) the pair's constants are independent loads
       const int64_t g = (int64_t)gids[s + j0 + lane];
-      const GaussEval pe = pair_ev ? load_eval(pair_ev, s + j0 + lane) : zero_eval();
       if (g < 0 || g >= p.K) {
         set_status(&hdr->status, g < 0 ? GF_STATUS_IDS_NEGATIVE : GF_STATUS_IDS_RANGE);
       } else {
-        my = pair_ev ? pe : eval_geom(p, mu, chol_raw, nullptr, g);
+        my = ev ? load_eval(ev, g) : eval_geom(p, mu, chol_raw, nullptr, g);
         myg = (int32_t)g;
       }
     }
@@ -1134,6 +1190,17 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd16(
   }
 }
 
+template <typename TpIdx, typename GIdx>
+__global__ __launch_bounds__(kTileThreads) void k_bwd16(
+    Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
+    const float* __restrict__ col_coords, const float* __restrict__ mu,
+    const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
+    const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
+    uint8_t* ws, BwdLayout L) {
+  bwd16_body<TpIdx, GIdx>(p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gids,
+                          num_pairs, ws, L, (int64_t)blockIdx.x * (kTileThreads / 64) + wave_id());
+}
+
 __device__ inline float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -1145,7 +1212,7 @@ template <typename TpIdx, typename GIdx>
 __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
     Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
-    const float* __restrict__ chol_raw, const GaussEval* __restrict__ pair_ev,
+    const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
     const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
     uint8_t* ws, BwdLayout L) {
   __shared__ GaussEval gl[kTileThreads];
@@ -1166,7 +1233,7 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
   for (int64_t j0 = 0; j0 < n; j0 += kTileThreads) {
     const int nj = (int)((n - j0) < kTileThreads ? (n - j0) : kTileThreads);
     __syncthreads();
-    stage_gaussians<GIdx>(p, gids, s, j0, nj, mu, chol_raw, pair_ev, gl, gid_lds, &hdr->status);
+    stage_gaussians<GIdx>(p, gids, s, j0, nj, mu, chol_raw, ev, gl, gid_lds, &hdr->status);
     __syncthreads();
     for (int j = 0; j < nj; ++j) {
       const int32_t g = gid_lds[j];
@@ -1210,12 +1277,12 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
 //   G = dL/dcov = -A (dL/dA) A + dL/ddet det A;  dL/dL = (G + G^T) L;  softplus' on the diagonal.
 // A is the inverse of the fp32 covariance; the algebra follows torch's autograd of the
 // reference CPU path (linalg.inv, linalg.det, L L^T, softplus).
-__global__ __launch_bounds__(kTileThreads) void k_bwd_finish(
-    Problem p, const float* __restrict__ chol_raw, const float* __restrict__ amp,
+// The chain rule for Gaussian g of one field by one thread.
+__device__ __forceinline__ void finish_body(
+    const Problem& p, const float* __restrict__ chol_raw, const float* __restrict__ amp,
     float* __restrict__ d_mu, float* __restrict__ d_chol_raw, float* __restrict__ d_amp, uint8_t* ws,
-    BwdLayout L) {
+    const BwdLayout& L, int64_t g) {
   float* acc = reinterpret_cast<float*>(ws + L.acc);
-  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= p.K) return;
   const float4 a0 = reinterpret_cast<const float4*>(acc)[2 * g + 0];
   const float4 a1 = reinterpret_cast<const float4*>(acc)[2 * g + 1];
@@ -1256,6 +1323,14 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_finish(
   d_chol_raw[3 * g + 0] = (float)(dl11 * gf_softplus_grad(raw11));
   d_chol_raw[3 * g + 1] = (float)dl21;
   d_chol_raw[3 * g + 2] = (float)(dl22 * gf_softplus_grad(raw22));
+}
+
+__global__ __launch_bounds__(kTileThreads) void k_bwd_finish(
+    Problem p, const float* __restrict__ chol_raw, const float* __restrict__ amp,
+    float* __restrict__ d_mu, float* __restrict__ d_chol_raw, float* __restrict__ d_amp, uint8_t* ws,
+    BwdLayout L) {
+  finish_body(p, chol_raw, amp, d_mu, d_chol_raw, d_amp, ws, L,
+              (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
 // Self-test: order-independent checksum of gf_softplus_torch_cpu over all 2^32 inputs.
@@ -1321,17 +1396,118 @@ bool fast16(const Problem& p) { return p.tile_out == 16 && p.tile_in == 16; }
 
 unsigned wave_tile_grid(int64_t T) { return (unsigned)((T + kTileThreads / 64 - 1) / (kTileThreads / 64)); }
 
+
+// ------------------------------------------------------------------------------------------
+// Batched fields (one launch per phase for many layers).  The plan buffer holds a header,
+// one BatchLayer per field and, per kernel shape, a block -> field map:
+//   tile map    4 tiles per block (render, backward reduce)
+//   emit map    4 Gaussians per block
+//   finish map  256 Gaussians per block
+// Each field's blocks are contiguous, so block b of a kernel handles local index
+// (b - first block of its field) * per_block + wave / thread.
+
+struct BatchLayer {
+  Problem p;
+  FwdLayout fl;
+  BwdLayout bl;
+  const float* row_coords;
+  const float* col_coords;
+  const float* mu;
+  const float* chol_raw;
+  const float* amp;
+  const float* grad;
+  float* delta;
+  int64_t* tile_ptr;
+  int64_t* num_pairs;
+  int64_t* ids;
+  int64_t capacity;
+  uint8_t* fws;
+  uint8_t* bws;
+  float* d_mu;
+  float* d_chol_raw;
+  float* d_amp;
+  int64_t tile_block0, emit_block0, finish_block0;
+};
+
+struct BatchHeader {
+  int64_t n;
+  int64_t tile_blocks, emit_blocks, finish_blocks;
+  int64_t layers_off, tile_map_off, emit_map_off, finish_map_off;
+};
+
+__device__ inline const BatchLayer& batch_layer(const uint8_t* plan, int64_t map_off, int64_t* block0_sel,
+                                                int which) {
+  const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
+  const int32_t l = reinterpret_cast<const int32_t*>(plan + map_off)[blockIdx.x];
+  const BatchLayer& ly = reinterpret_cast<const BatchLayer*>(plan + h->layers_off)[l];
+  *block0_sel = which == 0 ? ly.tile_block0 : which == 1 ? ly.emit_block0 : ly.finish_block0;
+  return ly;
+}
+
+__global__ __launch_bounds__(kBinThreads) void k_bin_batch(const uint8_t* __restrict__ plan) {
+  const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
+  const BatchLayer& ly = reinterpret_cast<const BatchLayer*>(plan + h->layers_off)[blockIdx.x];
+  const Problem p = ly.p;
+  const FwdLayout L = ly.fl;
+  bin_body<true>(p, ly.mu, ly.chol_raw, ly.amp, ly.tile_ptr, ly.num_pairs, ly.fws, L);
+}
+
+__global__ __launch_bounds__(kEmitThreads) void k_emit_batch(const uint8_t* __restrict__ plan) {
+  const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
+  int64_t b0;
+  const BatchLayer& ly = batch_layer(plan, h->emit_map_off, &b0, 1);
+  const Problem p = ly.p;
+  const FwdLayout L = ly.fl;
+  emit_body<false, kEmitLanesBatch, 2>(
+      p, ly.mu, ly.amp, ly.fws, L, ly.tile_ptr, ly.ids, ly.capacity,
+      (((int64_t)blockIdx.x - b0) * (kEmitThreads / 64) + wave_id()) * (64 / kEmitLanesBatch));
+}
+
+__global__ __launch_bounds__(kTileThreads) void k_render16_batch(const uint8_t* __restrict__ plan) {
+  const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
+  int64_t b0;
+  const BatchLayer& ly = batch_layer(plan, h->tile_map_off, &b0, 0);
+  const Problem p = ly.p;
+  render16_body(p, ly.row_coords, ly.col_coords, reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
+                ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws,
+                ((int64_t)blockIdx.x - b0) * (kTileThreads / 64) + wave_id());
+}
+
+__global__ __launch_bounds__(kTileThreads) void k_bwd16_batch(const uint8_t* __restrict__ plan) {
+  const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
+  int64_t b0;
+  const BatchLayer& ly = batch_layer(plan, h->tile_map_off, &b0, 0);
+  const Problem p = ly.p;
+  const BwdLayout L = ly.bl;
+  const int64_t T = (int64_t)p.R * p.C;
+  const int64_t P = ly.tile_ptr[T];  // pairs beyond the id capacity were never emitted
+  bwd16_body<int64_t, int64_t>(p, ly.grad, ly.row_coords, ly.col_coords, ly.mu, ly.chol_raw,
+                               reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
+                               ly.tile_ptr, ly.ids, P < ly.capacity ? P : ly.capacity, ly.bws, L,
+                               ((int64_t)blockIdx.x - b0) * (kTileThreads / 64) + wave_id());
+}
+
+__global__ __launch_bounds__(kTileThreads) void k_finish_batch(const uint8_t* __restrict__ plan) {
+  const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
+  int64_t b0;
+  const BatchLayer& ly = batch_layer(plan, h->finish_map_off, &b0, 2);
+  const Problem p = ly.p;
+  const BwdLayout L = ly.bl;
+  finish_body(p, ly.chol_raw, ly.amp, ly.d_mu, ly.d_chol_raw, ly.d_amp, ly.bws, L,
+              ((int64_t)blockIdx.x - b0) * kTileThreads + threadIdx.x);
+}
+
 template <typename TP, typename GI>
 void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, const float* rc,
-                const float* cc, const float* mu, const float* raw, const GaussEval* pev,
+                const float* cc, const float* mu, const float* raw, const GaussEval* ev,
                 const void* tile_ptr, const void* gids, int64_t num_pairs, uint8_t* ws,
                 const BwdLayout& L) {
   if (fast16(p))
     hipLaunchKernelGGL((k_bwd16<TP, GI>), dim3(wave_tile_grid((int64_t)p.R * p.C)), dim3(kTileThreads), 0, st,
-                       p, grad, rc, cc, mu, raw, pev, reinterpret_cast<const TP*>(tile_ptr),
+                       p, grad, rc, cc, mu, raw, ev, reinterpret_cast<const TP*>(tile_ptr),
                        reinterpret_cast<const GI*>(gids), num_pairs, ws, L);
   else
-    hipLaunchKernelGGL((k_bwd_any<TP, GI>), grid, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw, pev,
+    hipLaunchKernelGGL((k_bwd_any<TP, GI>), grid, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw, ev,
                        reinterpret_cast<const TP*>(tile_ptr), reinterpret_cast<const GI*>(gids),
                        num_pairs, ws, L);
 }
@@ -1399,7 +1575,7 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
 
 int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                     const float* mu, const float* amp, const int64_t* tile_ptr,
-                    int64_t* gaussian_ids_sorted, void* pair_constants, int64_t ids_capacity,
+                    int64_t* gaussian_ids_sorted, int64_t ids_capacity,
                     void* workspace, size_t workspace_bytes, void* stream) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
@@ -1407,8 +1583,8 @@ int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in
   const FwdLayout L = fwd_layout(k, (int64_t)p.R * p.C);
   if (!workspace || workspace_bytes < L.total)
     return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
-  if (ids_capacity < 0 || (ids_capacity > 0 && (!gaussian_ids_sorted || !pair_constants)))
-    return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / pair_constants / ids_capacity invalid");
+  if (ids_capacity < 0 || (ids_capacity > 0 && !gaussian_ids_sorted))
+    return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / ids_capacity invalid");
   if (!tile_ptr) return set_err(GF_E_INVALID_ARGUMENT, "tile_ptr must not be NULL");
   if (k > 0 && (!mu || !amp)) return set_err(GF_E_INVALID_ARGUMENT, "mu / amp must not be NULL");
   if (k == 0) return GF_OK;
@@ -1416,14 +1592,14 @@ int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in
   const int64_t blocks = (k + kEmitThreads / 64 - 1) / (kEmitThreads / 64);
   hipLaunchKernelGGL(k_emit, dim3((unsigned)blocks), dim3(kEmitThreads), 0, st, p, mu, amp,
                      reinterpret_cast<uint8_t*>(workspace), L, tile_ptr, gaussian_ids_sorted,
-                     reinterpret_cast<GaussEval*>(pair_constants), ids_capacity);
+                     ids_capacity);
   GF_LAUNCH_CHECK("k_emit");
   return GF_OK;
 }
 
 int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                       const float* row_coords, const float* col_coords, const int64_t* tile_ptr,
-                      int64_t* gaussian_ids_sorted, void* pair_constants, int64_t ids_capacity,
+                      int64_t* gaussian_ids_sorted, int64_t ids_capacity,
                       float* delta, void* workspace, size_t workspace_bytes, void* stream) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
@@ -1434,18 +1610,17 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
     return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
   if (!row_coords || !col_coords || !tile_ptr || !delta)
     return set_err(GF_E_INVALID_ARGUMENT, "coords / tile_ptr / delta must not be NULL");
-  if (ids_capacity < 0 || (ids_capacity > 0 && (!gaussian_ids_sorted || !pair_constants)))
-    return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / pair_constants / ids_capacity invalid");
+  if (ids_capacity < 0 || (ids_capacity > 0 && !gaussian_ids_sorted))
+    return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / ids_capacity invalid");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
   const GaussEval* ev = reinterpret_cast<const GaussEval*>(ws + L.eval);
-  GaussEval* pev = reinterpret_cast<GaussEval*>(pair_constants);
   if (fast16(p))
     hipLaunchKernelGGL(k_render16, dim3(wave_tile_grid(T)), dim3(kTileThreads), 0, st, p, row_coords,
-                       col_coords, ev, tile_ptr, gaussian_ids_sorted, pev, ids_capacity, delta, ws);
+                       col_coords, ev, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws);
   else
     hipLaunchKernelGGL(k_render_any, dim3((unsigned)T), dim3(kTileThreads), 0, st, p, row_coords,
-                       col_coords, ev, tile_ptr, gaussian_ids_sorted, pev, ids_capacity, delta, ws);
+                       col_coords, ev, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws);
   GF_LAUNCH_CHECK("k_render");
   return GF_OK;
 }
@@ -1454,7 +1629,7 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
                        const float* grad_delta, const float* row_coords, const float* col_coords,
                        const float* mu, const float* chol_raw, const void* tile_ptr,
                        int32_t tile_ptr_is_int64, const void* gaussian_ids, int32_t ids_is_int64,
-                       int64_t num_pairs, const void* pair_constants, void* workspace,
+                       int64_t num_pairs, const void* forward_workspace, void* workspace,
                        size_t workspace_bytes, void* stream) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
@@ -1470,7 +1645,9 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
   if (k > 0 && (!mu || !chol_raw)) return set_err(GF_E_INVALID_ARGUMENT, "mu / chol_raw must not be NULL");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
-  const GaussEval* ev = reinterpret_cast<const GaussEval*>(pair_constants);
+  const GaussEval* ev = forward_workspace
+      ? reinterpret_cast<const GaussEval*>(reinterpret_cast<const uint8_t*>(forward_workspace) + fwd_layout(k, T).eval)
+      : nullptr;
   const dim3 grid((unsigned)T);
   if (tile_ptr_is_int64 && ids_is_int64)
     launch_bwd<int64_t, int64_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs, ws, L);
@@ -1509,14 +1686,154 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
                 const float* mu, const float* chol_raw, const float* amp, const void* tile_ptr,
                 int32_t tile_ptr_is_int64, const void* gaussian_ids, int32_t ids_is_int64,
                 int64_t num_pairs, float* d_mu, float* d_chol_raw, float* d_amp,
-                const void* pair_constants, void* workspace, size_t workspace_bytes, void* stream) {
+                const void* forward_workspace, void* workspace, size_t workspace_bytes, void* stream) {
   if (k > 0 && !amp) return set_err(GF_E_INVALID_ARGUMENT, "amp must not be NULL");
   int rc = gf_backward_reduce(cfg, out_features, in_features, k, grad_delta, row_coords, col_coords,
                               mu, chol_raw, tile_ptr, tile_ptr_is_int64, gaussian_ids, ids_is_int64,
-                              num_pairs, pair_constants, workspace, workspace_bytes, stream);
+                              num_pairs, forward_workspace, workspace, workspace_bytes, stream);
   if (rc) return rc;
   return gf_backward_finish(cfg, out_features, in_features, k, chol_raw, amp, d_mu, d_chol_raw, d_amp,
                             workspace, workspace_bytes, stream);
+}
+
+// ------------------------------------------------------------------------------------------
+// Batched fields.
+
+int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_layers, void* plan,
+                  size_t plan_bytes, gf_batch_info* info, void* stream) {
+  if (!cfg || !info || n_layers < 0 || (n_layers > 0 && !layers))
+    return set_err(GF_E_INVALID_ARGUMENT, "cfg / layers / info invalid");
+  if (cfg->tile_out != 16 || cfg->tile_in != 16)
+    return set_err(GF_E_INVALID_ARGUMENT, "batched fields need 16x16 tiles (got %lldx%lld)",
+                   (long long)cfg->tile_out, (long long)cfg->tile_in);
+  const size_t n = (size_t)n_layers;
+  BatchHeader h{};
+  h.n = n_layers;
+  h.layers_off = (int64_t)align256(sizeof(BatchHeader));
+  std::vector<BatchLayer> ls(n);
+  int64_t tile_blocks = 0, emit_blocks = 0, finish_blocks = 0;
+  bool has_backward = true;
+  for (size_t i = 0; i < n; ++i) {
+    const gf_layer& in = layers[i];
+    BatchLayer& ly = ls[i];
+    int rc = make_problem(cfg, in.out_features, in.in_features, in.k, &ly.p);
+    if (rc) {
+      char why[sizeof(g_err)];
+      std::snprintf(why, sizeof(why), "%s", g_err);
+      return set_err(rc, "layer %zu: %s", i, why);
+    }
+    const int64_t T = (int64_t)ly.p.R * ly.p.C, K = in.k;
+    ly.fl = fwd_layout(K, T);
+    ly.bl = bwd_layout(K);
+    if (!in.forward_workspace || in.forward_workspace_bytes < ly.fl.total)
+      return set_err(GF_E_WORKSPACE, "layer %zu: forward workspace needs %zu bytes", i, ly.fl.total);
+    if (!in.row_coords || !in.col_coords || !in.delta || !in.tile_ptr || !in.num_pairs)
+      return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: coords / delta / tile_ptr / num_pairs must not be NULL", i);
+    if (K > 0 && (!in.mu || !in.chol_raw || !in.amp))
+      return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: mu / chol_raw / amp must not be NULL", i);
+    if (in.ids_capacity < 0 || (in.ids_capacity > 0 && !in.gaussian_ids))
+      return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: gaussian_ids / ids_capacity invalid", i);
+    const bool bwd = in.grad_delta && in.backward_workspace &&
+                     in.backward_workspace_bytes >= ly.bl.total &&
+                     (K == 0 || (in.d_mu && in.d_chol_raw && in.d_amp));
+    has_backward = has_backward && bwd;
+    ly.row_coords = in.row_coords;
+    ly.col_coords = in.col_coords;
+    ly.mu = in.mu;
+    ly.chol_raw = in.chol_raw;
+    ly.amp = in.amp;
+    ly.grad = in.grad_delta;
+    ly.delta = in.delta;
+    ly.tile_ptr = in.tile_ptr;
+    ly.num_pairs = in.num_pairs;
+    ly.ids = in.gaussian_ids;
+    ly.capacity = in.ids_capacity;
+    ly.fws = reinterpret_cast<uint8_t*>(in.forward_workspace);
+    ly.bws = reinterpret_cast<uint8_t*>(in.backward_workspace);
+    ly.d_mu = in.d_mu;
+    ly.d_chol_raw = in.d_chol_raw;
+    ly.d_amp = in.d_amp;
+    ly.tile_block0 = tile_blocks;
+    ly.emit_block0 = emit_blocks;
+    ly.finish_block0 = finish_blocks;
+    tile_blocks += (T + kTileThreads / 64 - 1) / (kTileThreads / 64);
+    const int64_t per_emit_block = (kEmitThreads / 64) * (64 / kEmitLanesBatch);
+    emit_blocks += (K + per_emit_block - 1) / per_emit_block;
+    finish_blocks += (K + kTileThreads - 1) / kTileThreads;
+  }
+  if (tile_blocks >= INT32_MAX || emit_blocks >= INT32_MAX)
+    return set_err(GF_E_INVALID_ARGUMENT, "batch too large for one launch");
+  h.tile_blocks = tile_blocks;
+  h.emit_blocks = emit_blocks;
+  h.finish_blocks = finish_blocks;
+  h.tile_map_off = (int64_t)align256(h.layers_off + sizeof(BatchLayer) * n);
+  h.emit_map_off = (int64_t)align256(h.tile_map_off + sizeof(int32_t) * tile_blocks);
+  h.finish_map_off = (int64_t)align256(h.emit_map_off + sizeof(int32_t) * emit_blocks);
+  const size_t need = align256(h.finish_map_off + sizeof(int32_t) * finish_blocks);
+  info->n_layers = n_layers;
+  info->has_backward = has_backward ? 1 : 0;
+  info->tile_blocks = tile_blocks;
+  info->emit_blocks = emit_blocks;
+  info->finish_blocks = finish_blocks;
+  info->plan_bytes = need;
+  if (!plan) return GF_OK;  // size query
+  if (plan_bytes < need) return set_err(GF_E_WORKSPACE, "batch plan needs %zu bytes, got %zu", need, plan_bytes);
+  std::vector<uint8_t> host(need, 0);
+  std::memcpy(host.data(), &h, sizeof(h));
+  if (n) std::memcpy(host.data() + h.layers_off, ls.data(), sizeof(BatchLayer) * n);
+  int32_t* tm = reinterpret_cast<int32_t*>(host.data() + h.tile_map_off);
+  int32_t* em = reinterpret_cast<int32_t*>(host.data() + h.emit_map_off);
+  int32_t* fm = reinterpret_cast<int32_t*>(host.data() + h.finish_map_off);
+  for (size_t i = 0; i < n; ++i) {
+    const int64_t te = i + 1 < n ? ls[i + 1].tile_block0 : tile_blocks;
+    const int64_t ee = i + 1 < n ? ls[i + 1].emit_block0 : emit_blocks;
+    const int64_t fe = i + 1 < n ? ls[i + 1].finish_block0 : finish_blocks;
+    for (int64_t b = ls[i].tile_block0; b < te; ++b) tm[b] = (int32_t)i;
+    for (int64_t b = ls[i].emit_block0; b < ee; ++b) em[b] = (int32_t)i;
+    for (int64_t b = ls[i].finish_block0; b < fe; ++b) fm[b] = (int32_t)i;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  GF_HIP_CHECK(hipMemcpyAsync(plan, host.data(), need, hipMemcpyHostToDevice, st));
+  GF_HIP_CHECK(hipStreamSynchronize(st));  // the host staging buffer goes out of scope
+  return GF_OK;
+}
+
+int gf_batch_forward(const void* plan, const gf_batch_info* info, uint32_t phases, void* stream) {
+  if (!plan || !info) return set_err(GF_E_INVALID_ARGUMENT, "plan / info must not be NULL");
+  if (info->n_layers == 0) return GF_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const uint8_t* pl = reinterpret_cast<const uint8_t*>(plan);
+  if (phases & GF_PHASE_BIN) {
+    hipLaunchKernelGGL(k_bin_batch, dim3((unsigned)info->n_layers), dim3(kBinThreads), 0, st, pl);
+    GF_LAUNCH_CHECK("k_bin_batch");
+  }
+  if ((phases & GF_PHASE_EMIT) && info->emit_blocks > 0) {
+    hipLaunchKernelGGL(k_emit_batch, dim3((unsigned)info->emit_blocks), dim3(kEmitThreads), 0, st, pl);
+    GF_LAUNCH_CHECK("k_emit_batch");
+  }
+  if (phases & GF_PHASE_RENDER) {
+    hipLaunchKernelGGL(k_render16_batch, dim3((unsigned)info->tile_blocks), dim3(kTileThreads), 0, st, pl);
+    GF_LAUNCH_CHECK("k_render16_batch");
+  }
+  return GF_OK;
+}
+
+int gf_batch_backward(const void* plan, const gf_batch_info* info, uint32_t phases, void* stream) {
+  if (!plan || !info) return set_err(GF_E_INVALID_ARGUMENT, "plan / info must not be NULL");
+  if (!info->has_backward)
+    return set_err(GF_E_INVALID_ARGUMENT, "the batch plan was built without backward buffers");
+  if (info->n_layers == 0) return GF_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const uint8_t* pl = reinterpret_cast<const uint8_t*>(plan);
+  if (phases & GF_PHASE_REDUCE) {
+    hipLaunchKernelGGL(k_bwd16_batch, dim3((unsigned)info->tile_blocks), dim3(kTileThreads), 0, st, pl);
+    GF_LAUNCH_CHECK("k_bwd16_batch");
+  }
+  if ((phases & GF_PHASE_FINISH) && info->finish_blocks > 0) {
+    hipLaunchKernelGGL(k_finish_batch, dim3((unsigned)info->finish_blocks), dim3(kTileThreads), 0, st, pl);
+    GF_LAUNCH_CHECK("k_finish_batch");
+  }
+  return GF_OK;
 }
 
 int gf_read_status(void* workspace, int32_t clear, uint32_t* status_host, void* stream) {

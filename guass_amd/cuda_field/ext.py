@@ -91,19 +91,18 @@ def gaussian_field_forward(row_coords: Tensor, col_coords: Tensor, mu: Tensor, c
                            amp: Tensor, tile_out: int, tile_in: int, sigma_multiplier: float,
                            normalize: bool, clamp_quad: float | None):
     """Returns (delta f32[M*N], tile_ptr i64[T+1], gaussian_ids_sorted i64[P])."""
-    delta, tile_ptr, ids, _ = forward_with_pair_constants(row_coords, col_coords, mu, chol_raw, amp,
-                                                          tile_out, tile_in, sigma_multiplier,
-                                                          normalize, clamp_quad)
+    delta, tile_ptr, ids, _ = forward_with_workspace(row_coords, col_coords, mu, chol_raw, amp,
+                                                     tile_out, tile_in, sigma_multiplier, normalize,
+                                                     clamp_quad)
     return delta, tile_ptr, ids
 
 
-def forward_with_pair_constants(row_coords: Tensor, col_coords: Tensor, mu: Tensor,
-                                chol_raw: Tensor, amp: Tensor, tile_out: int, tile_in: int,
-                                sigma_multiplier: float, normalize: bool, clamp_quad: float | None):
-    """gaussian_field_forward plus its pair constants (f32[P * 8]: each pair's Gaussian
-    evaluation constants in the order of gaussian_ids_sorted); passing them to
-    gaussian_field_backward(pair_constants=...) with the same parameters and binning skips
-    recomputing them."""
+def forward_with_workspace(row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol_raw: Tensor,
+                           amp: Tensor, tile_out: int, tile_in: int, sigma_multiplier: float,
+                           normalize: bool, clamp_quad: float | None):
+    """gaussian_field_forward plus its forward workspace, which holds the Gaussians' evaluation
+    constants; passing it to gaussian_field_backward(forward_workspace=...) with the same
+    parameters skips recomputing them."""
     validate_forward_inputs(row_coords, col_coords, mu, chol_raw, amp)
     _check_config(tile_out, tile_in, sigma_multiplier)
     dev = _same_device(row_coords, col_coords, mu, chol_raw, amp)
@@ -126,17 +125,15 @@ def forward_with_pair_constants(row_coords: Tensor, col_coords: Tensor, mu: Tens
                                  tile_ptr.data_ptr(), num_pairs.data_ptr(), ctypes.byref(P),
                                  ws.data_ptr(), ws_bytes, stream), "gaussian_field_forward (binning)")
         ids = torch.empty(P.value, dtype=torch.int64, device=dev)
-        pair_constants = torch.empty(P.value * N.GF_PAIR_CONSTANT_BYTES // 4, dtype=torch.float32,
-                                     device=dev)
         delta = torch.empty(M * Nf, dtype=torch.float32, device=dev)
         N.check(L.gf_forward_emit(ctypes.byref(cfg), M, Nf, K, N.ptr(mu), N.ptr(amp),
-                                  tile_ptr.data_ptr(), N.ptr(ids), N.ptr(pair_constants), P.value,
-                                  ws.data_ptr(), ws_bytes, stream), "gaussian_field_forward (emit)")
+                                  tile_ptr.data_ptr(), N.ptr(ids), P.value, ws.data_ptr(), ws_bytes,
+                                  stream), "gaussian_field_forward (emit)")
         N.check(L.gf_forward_render(ctypes.byref(cfg), M, Nf, K, row_coords.data_ptr(),
-                                    col_coords.data_ptr(), tile_ptr.data_ptr(), N.ptr(ids),
-                                    N.ptr(pair_constants), P.value, delta.data_ptr(), ws.data_ptr(),
-                                    ws_bytes, stream), "gaussian_field_forward (render)")
-    return delta, tile_ptr, ids, pair_constants
+                                    col_coords.data_ptr(), tile_ptr.data_ptr(), N.ptr(ids), P.value,
+                                    delta.data_ptr(), ws.data_ptr(), ws_bytes, stream),
+                "gaussian_field_forward (render)")
+    return delta, tile_ptr, ids, ws
 
 
 # ------------------------------------------------------------------ backward
@@ -150,7 +147,7 @@ _SAVED_STATE_MESSAGES = (  # order of the reference checks, field_impl.cu:92-106
 
 
 def _backward(grad_delta, row_coords, col_coords, mu, chol_raw, amp, tile_ptr, gaussian_ids_sorted,
-              tile_out, tile_in, sigma_multiplier, normalize, clamp_quad, pair_constants):
+              tile_out, tile_in, sigma_multiplier, normalize, clamp_quad, forward_workspace):
     # validate_backward_inputs (field_impl.cu:73-84)
     _check_f32(grad_delta, "grad_delta")
     _check_f32(row_coords, "saved.row_coords")
@@ -190,12 +187,12 @@ def _backward(grad_delta, row_coords, col_coords, mu, chol_raw, amp, tile_ptr, g
         ws_bytes = L.gf_backward_workspace_bytes(M, Nf, K, ctypes.byref(cfg))
         ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
         fwd_ptr = None
-        if pair_constants is not None:
-            need = gaussian_ids_sorted.numel() * N.GF_PAIR_CONSTANT_BYTES
-            if (pair_constants.device != dev or not pair_constants.is_contiguous()
-                    or pair_constants.numel() * pair_constants.element_size() < need):
-                raise RuntimeError("pair_constants do not belong to this binning's forward")
-            fwd_ptr = pair_constants.data_ptr()
+        if forward_workspace is not None:
+            need = L.gf_forward_workspace_bytes(M, Nf, K, ctypes.byref(cfg))
+            if (forward_workspace.device != dev or forward_workspace.dtype != torch.uint8
+                    or forward_workspace.numel() < need):
+                raise RuntimeError("forward_workspace does not belong to this field's forward")
+            fwd_ptr = forward_workspace.data_ptr()
         d_mu = torch.empty(K, 2, dtype=torch.float32, device=dev)
         d_chol_raw = torch.empty(K, 3, dtype=torch.float32, device=dev)
         d_amp = torch.empty(K, 1, dtype=torch.float32, device=dev)
@@ -218,14 +215,14 @@ def gaussian_field_backward(grad_delta: Tensor, row_coords: Tensor, col_coords: 
                             chol_raw: Tensor, amp: Tensor, tile_ptr: Tensor,
                             gaussian_ids_sorted: Tensor, tile_out: int, tile_in: int,
                             sigma_multiplier: float, normalize: bool, clamp_quad: float | None,
-                            *, pair_constants: Tensor | None = None):
+                            *, forward_workspace: Tensor | None = None):
     """Returns [d_mu f32[K,2], d_chol_raw f32[K,3], d_amp f32[K,1]].
 
-    ``pair_constants`` (keyword, optional): from ``forward_with_pair_constants`` over the same
-    parameters and binning; the Gaussians' constants are then read instead of recomputed."""
+    ``forward_workspace`` (keyword, optional): the workspace from ``forward_with_workspace`` over
+    the same parameters, whose Gaussian constants are then reused."""
     return _backward(grad_delta, row_coords, col_coords, mu, chol_raw, amp, tile_ptr,
                      gaussian_ids_sorted, tile_out, tile_in, sigma_multiplier, normalize, clamp_quad,
-                     pair_constants)
+                     forward_workspace)
 
 
 def gaussian_field_backward_reference(grad_delta: Tensor, row_coords: Tensor, col_coords: Tensor,

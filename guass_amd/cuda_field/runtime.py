@@ -18,9 +18,9 @@ from guass_amd.cuda_field.loader import load_extension
 def _forward(ctx, row_coords, col_coords, mu, chol_raw, amp, tile_out, tile_in, sigma_multiplier,
              normalize, clamp_quad):
     ext = load_extension(verbose=False)
-    # The pair constants (each pair's Gaussian evaluation constants) ride along on ctx so the
-    # training backward reuses them; the saved tensors are the reference's seven.
-    delta, tile_ptr, gaussian_ids_sorted, ctx.pair_constants = ext.forward_with_pair_constants(
+    # The forward workspace (each Gaussian's evaluation constants) rides along on ctx so the
+    # training backward reuses it; the saved tensors are the reference's seven.
+    delta, tile_ptr, gaussian_ids_sorted, ctx.forward_workspace = ext.forward_with_workspace(
         row_coords, col_coords, mu, chol_raw, amp, tile_out, tile_in, sigma_multiplier, normalize,
         clamp_quad)
     ctx.save_for_backward(row_coords, col_coords, mu, chol_raw, amp, tile_ptr, gaussian_ids_sorted)
@@ -35,7 +35,7 @@ def _forward(ctx, row_coords, col_coords, mu, chol_raw, amp, tile_out, tile_in, 
 def _backward(ctx, grad_delta, entry: str):
     ext = load_extension(verbose=False)
     row_coords, col_coords, mu, chol_raw, amp, tile_ptr, gaussian_ids_sorted = ctx.saved_tensors
-    extra = {"pair_constants": ctx.pair_constants} if entry == "gaussian_field_backward" else {}
+    extra = {"forward_workspace": ctx.forward_workspace} if entry == "gaussian_field_backward" else {}
     d_mu, d_chol_raw, d_amp = getattr(ext, entry)(
         grad_delta.contiguous(), row_coords, col_coords, mu, chol_raw, amp, tile_ptr,
         gaussian_ids_sorted, ctx.tile_out, ctx.tile_in, ctx.sigma_multiplier, ctx.normalize,

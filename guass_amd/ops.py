@@ -41,9 +41,6 @@ class FieldPlan:
         self.tile_ptr = torch.empty(self.T + 1, dtype=torch.int64, device=dev)
         self.num_pairs = torch.empty(1, dtype=torch.int64, device=dev)
         self.ids = torch.empty(max(self.capacity, 1), dtype=torch.int64, device=dev)
-        # evaluation constants of each pair's Gaussian, in the order of ``ids``
-        self.pair_constants = torch.empty(max(self.capacity, 1) * N.GF_PAIR_CONSTANT_BYTES // 4,
-                                          dtype=torch.float32, device=dev)
         self.delta = torch.empty(self.M * self.N, dtype=torch.float32, device=dev)
         self.d_mu = torch.empty(self.K, 2, dtype=torch.float32, device=dev)
         self.d_chol_raw = torch.empty(self.K, 3, dtype=torch.float32, device=dev)
@@ -63,16 +60,15 @@ class FieldPlan:
     def emit(self, mu, amp) -> None:
         N.check(N.lib().gf_forward_emit(ctypes.byref(self.cfg), self.M, self.N, self.K, N.ptr(mu),
                                         N.ptr(amp), self.tile_ptr.data_ptr(), self.ids.data_ptr(),
-                                        self.pair_constants.data_ptr(), self.capacity,
-                                        self.fwd_ws.data_ptr(), self.fwd_ws_bytes, self._stream()),
+                                        self.capacity, self.fwd_ws.data_ptr(), self.fwd_ws_bytes,
+                                        self._stream()),
                 "gf_forward_emit")
 
     def render(self, row_coords, col_coords) -> torch.Tensor:
-        """Renders from the pair constants the last ``emit`` wrote (and sorts ids and constants)."""
+        """Renders from the Gaussian constants the last ``emit`` stored (and sorts the ids)."""
         N.check(N.lib().gf_forward_render(ctypes.byref(self.cfg), self.M, self.N, self.K,
                                           row_coords.data_ptr(), col_coords.data_ptr(),
-                                          self.tile_ptr.data_ptr(), self.ids.data_ptr(),
-                                          self.pair_constants.data_ptr(), self.capacity,
+                                          self.tile_ptr.data_ptr(), self.ids.data_ptr(), self.capacity,
                                           self.delta.data_ptr(), self.fwd_ws.data_ptr(),
                                           self.fwd_ws_bytes, self._stream()),
                 "gf_forward_render")
@@ -86,10 +82,10 @@ class FieldPlan:
 
     def backward_reduce(self, grad, row_coords, col_coords, mu, chol_raw, num_pairs: int | None = None,
                         reuse_forward: bool = True):
-        """Per-tile moments.  With ``reuse_forward`` the Gaussian constants are the last forward's
-        pair constants (same mu / chol_raw), else they are recomputed from mu / chol_raw."""
+        """Per-tile moments.  With ``reuse_forward`` the Gaussian constants come from the last
+        forward's workspace (same mu / chol_raw), else they are recomputed from mu / chol_raw."""
         n = self.capacity if num_pairs is None else int(num_pairs)
-        fwd = self.pair_constants.data_ptr() if reuse_forward else None
+        fwd = self.fwd_ws.data_ptr() if reuse_forward else None
         N.check(N.lib().gf_backward_reduce(ctypes.byref(self.cfg), self.M, self.N, self.K,
                                            grad.data_ptr(), row_coords.data_ptr(), col_coords.data_ptr(),
                                            N.ptr(mu), N.ptr(chol_raw), self.tile_ptr.data_ptr(), 1,
@@ -121,3 +117,60 @@ class FieldPlan:
         N.check(N.lib().gf_read_status(ws.data_ptr(), 0, ctypes.byref(st), self._stream()),
                 "gf_read_status")
         return st.value
+
+
+class FieldBatchPlan:
+    """Many fields (e.g. every adapted layer of a model) rendered and differentiated together:
+    each phase is one launch over all layers (``gf_batch_forward`` / ``gf_batch_backward``).
+
+    ``layers`` is a sequence of objects with device tensors ``row_coords``, ``col_coords``,
+    ``mu``, ``chol_raw``, ``amp`` and, for the backward, ``grad`` (dL/d(delta), read in place at
+    every ``backward()``).  The plan keeps references to them: their storage must stay put.
+    Each layer gets the buffers of a :class:`FieldPlan` (``self.plans[i]``: delta, tile_ptr,
+    ids, pair constants, gradients).  16x16 tiles only.
+    """
+
+    def __init__(self, layers, device, *, capacities, tile_out: int = 16, tile_in: int = 16,
+                 sigma_multiplier: float = 3.0, normalize: bool = False,
+                 clamp_quad: float | None = 80.0):
+        self.device = torch.device(device)
+        self.layers = list(layers)
+        self.cfg = N.make_config(tile_out, tile_in, sigma_multiplier, normalize, clamp_quad)
+        self.plans = [FieldPlan(int(ly.row_coords.numel()), int(ly.col_coords.numel()), int(ly.mu.shape[0]),
+                                self.device, tile_out=tile_out, tile_in=tile_in,
+                                sigma_multiplier=sigma_multiplier, normalize=normalize,
+                                clamp_quad=clamp_quad, ids_capacity=int(c))
+                      for ly, c in zip(self.layers, capacities)]
+        table = (N.GfLayer * max(len(self.plans), 1))()
+        for i, (ly, pl) in enumerate(zip(self.layers, self.plans)):
+            grad = getattr(ly, "grad", None)
+            table[i] = N.GfLayer(
+                pl.M, pl.N, pl.K, ly.row_coords.data_ptr(), ly.col_coords.data_ptr(), N.ptr(ly.mu),
+                N.ptr(ly.chol_raw), N.ptr(ly.amp), pl.delta.data_ptr(), pl.tile_ptr.data_ptr(),
+                pl.num_pairs.data_ptr(), pl.ids.data_ptr(), pl.capacity,
+                pl.fwd_ws.data_ptr(), pl.fwd_ws_bytes, None if grad is None else grad.data_ptr(),
+                N.ptr(pl.d_mu), N.ptr(pl.d_chol_raw), N.ptr(pl.d_amp), pl.bwd_ws.data_ptr(),
+                pl.bwd_ws_bytes)
+        self.info = N.GfBatchInfo()
+        L = N.lib()
+        n = len(self.plans)
+        N.check(L.gf_batch_plan(ctypes.byref(self.cfg), table, n, None, 0, ctypes.byref(self.info),
+                                self._stream()), "gf_batch_plan (size)")
+        self.plan = torch.empty(max(int(self.info.plan_bytes), 256), dtype=torch.uint8, device=self.device)
+        N.check(L.gf_batch_plan(ctypes.byref(self.cfg), table, n, self.plan.data_ptr(), self.plan.numel(),
+                                ctypes.byref(self.info), self._stream()), "gf_batch_plan")
+
+    def _stream(self) -> int:
+        return N.stream_handle(self.device)
+
+    def forward(self, phases: int = N.GF_PHASE_ALL) -> None:
+        N.check(N.lib().gf_batch_forward(self.plan.data_ptr(), ctypes.byref(self.info), phases,
+                                         self._stream()), "gf_batch_forward")
+
+    def backward(self, phases: int = N.GF_PHASE_ALL) -> None:
+        N.check(N.lib().gf_batch_backward(self.plan.data_ptr(), ctypes.byref(self.info), phases,
+                                          self._stream()), "gf_batch_backward")
+
+    def status(self) -> list[int]:
+        """Forward | backward GF_STATUS_* bits per layer (synchronises)."""
+        return [pl.status("forward") | pl.status("backward") for pl in self.plans]

@@ -82,37 +82,32 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
                    int64_t* tile_ptr, int64_t* num_pairs_dev, int64_t* num_pairs_host,
                    void* workspace, size_t workspace_bytes, void* stream);
 
-/* Bytes per pair of the pair-constants buffer (evaluation constants of the pair's Gaussian,
- * in the order of gaussian_ids_sorted). */
-#define GF_PAIR_CONSTANT_BYTES 32
-
 /*
  * Forward phase 2 (emission): writes the (tile, gaussian) pairs into gaussian_ids_sorted,
  * each tile's ids inside its [tile_ptr[t], tile_ptr[t+1]) range (order fixed by phase 3),
- * and beside each id the evaluation constants of its Gaussian (from the covariance
- * gf_forward_bin left in the workspace, with amp applied).  Must follow gf_forward_bin on the
- * same stream with the same workspace, tile_ptr and mu.
+ * and stores each Gaussian's evaluation constants in the workspace (from the covariance
+ * gf_forward_bin left there, with amp applied).  Must follow gf_forward_bin on the same stream
+ * with the same workspace, tile_ptr and mu.
  *   gaussian_ids_sorted [ids_capacity] int64 out; pairs beyond the capacity are dropped and
  *                   GF_STATUS_CAPACITY is set
- *   pair_constants  [ids_capacity * GF_PAIR_CONSTANT_BYTES] out, same indexing as the ids
  * Replaces reference forward.cu:465-482 (emit_tile_pairs_kernel + radix sort on the tile key).
  */
 int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                     const float* mu, const float* amp, const int64_t* tile_ptr,
-                    int64_t* gaussian_ids_sorted, void* pair_constants, int64_t ids_capacity,
+                    int64_t* gaussian_ids_sorted, int64_t ids_capacity,
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Forward phase 3 (render): puts every tile's ids in canonical order (gaussian id ascending;
- * with tile-major ranges this is the (tile, gaussian) order of a stable sort), the pair
- * constants with them, and renders delta-W from the constants gf_forward_emit wrote.  Must
- * follow gf_forward_emit on the same stream with the same workspace, ids and pair_constants.
+ * with tile-major ranges this is the (tile, gaussian) order of a stable sort) and renders
+ * delta-W from the Gaussian constants gf_forward_emit stored.  Must follow gf_forward_emit on
+ * the same stream with the same workspace and ids.
  *   delta           [out_features*in_features] fp32 out, row-major; every element written
  * Replaces reference forward.cu:513-569 (tile_accumulate_kernel; delta needs no pre-zeroing).
  */
 int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                       const float* row_coords, const float* col_coords, const int64_t* tile_ptr,
-                      int64_t* gaussian_ids_sorted, void* pair_constants, int64_t ids_capacity,
+                      int64_t* gaussian_ids_sorted, int64_t ids_capacity,
                       float* delta, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -123,9 +118,9 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
  *   tile_ptr        [T+1], int64 if tile_ptr_is_int64 else int32
  *   gaussian_ids    [num_pairs], int64 if ids_is_int64 else int32 (any order within a tile)
  *   d_mu [K,2], d_chol_raw [K,3], d_amp [K,1] fp32 out (fully written)
- *   pair_constants  optional: the pair constants of the forward (after its gf_forward_render)
- *                   over the same (mu, chol_raw), config, tile_ptr and ids; read beside the
- *                   ids instead of recomputing each Gaussian's constants.  NULL recomputes.
+ *   forward_workspace  optional: the workspace of the forward over the same (mu, chol_raw)
+ *                   and config (after its gf_forward_emit); the Gaussians' constants stored
+ *                   there are read instead of recomputed.  NULL recomputes them.
  * Saved-state violations (non-monotone tile_ptr, tile_ptr[T] != num_pairs, ids outside
  * [0,K)) are detected on the device, the offending pairs skipped, and status bits set.
  * Replaces reference backward.cu:541-716 (backward_pair_reduce_train).
@@ -135,7 +130,7 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
                 const float* mu, const float* chol_raw, const float* amp,
                 const void* tile_ptr, int32_t tile_ptr_is_int64,
                 const void* gaussian_ids, int32_t ids_is_int64, int64_t num_pairs,
-                float* d_mu, float* d_chol_raw, float* d_amp, const void* pair_constants,
+                float* d_mu, float* d_chol_raw, float* d_amp, const void* forward_workspace,
                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* First half of gf_backward (reference backward.cu:592-702: per-pair partials + reduce-by-key). */
@@ -144,7 +139,7 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
                        const float* mu, const float* chol_raw,
                        const void* tile_ptr, int32_t tile_ptr_is_int64,
                        const void* gaussian_ids, int32_t ids_is_int64, int64_t num_pairs,
-                       const void* pair_constants, void* workspace, size_t workspace_bytes,
+                       const void* forward_workspace, void* workspace, size_t workspace_bytes,
                        void* stream);
 
 /* Second half of gf_backward (reference backward.cu:436-496,704-715: cov -> chol_raw chain). */
@@ -152,6 +147,63 @@ int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t
                        const float* chol_raw, const float* amp,
                        float* d_mu, float* d_chol_raw, float* d_amp,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Batched fields (no single-call counterpart in the reference, which renders each adapted
+ * layer separately, gaussian_linear.py:162-220; this is the batched launch of BASELINE's
+ * SD1.5 configuration).  Every phase runs as one launch over all layers, each layer with the
+ * buffers its single-field calls would use.  16x16 tiles only; int64 ids.
+ */
+typedef struct gf_layer {
+  int64_t out_features, in_features, k;
+  const float* row_coords;       /* [out_features] */
+  const float* col_coords;       /* [in_features] */
+  const float* mu;               /* [k,2] */
+  const float* chol_raw;         /* [k,3] */
+  const float* amp;              /* [k,1] */
+  float* delta;                  /* [out_features*in_features] out */
+  int64_t* tile_ptr;             /* [T+1] out */
+  int64_t* num_pairs;            /* [1] out */
+  int64_t* gaussian_ids;         /* [ids_capacity] out */
+  int64_t ids_capacity;
+  void* forward_workspace;       /* gf_forward_workspace_bytes */
+  size_t forward_workspace_bytes;
+  const float* grad_delta;       /* backward only: [out_features*in_features] */
+  float* d_mu;                   /* backward only: [k,2] out */
+  float* d_chol_raw;             /* backward only: [k,3] out */
+  float* d_amp;                  /* backward only: [k,1] out */
+  void* backward_workspace;      /* backward only: gf_backward_workspace_bytes, zeroed once */
+  size_t backward_workspace_bytes;
+} gf_layer;
+
+typedef struct gf_batch_info {
+  int32_t n_layers;
+  int32_t has_backward;          /* every layer has its backward buffers */
+  int64_t tile_blocks, emit_blocks, finish_blocks;
+  size_t plan_bytes;             /* device bytes of the plan buffer */
+} gf_batch_info;
+
+/*
+ * Builds the device plan of a batch: call with plan == NULL to get info->plan_bytes, then
+ * with a device buffer of that size.  The second call copies the layer table to the device
+ * and synchronises `stream`.  The plan stays valid while the layers' buffers do.
+ */
+int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_layers, void* plan,
+                  size_t plan_bytes, gf_batch_info* info, void* stream);
+
+/* Phase selectors: GF_PHASE_ALL for a whole pass; single phases exist for timing. */
+#define GF_PHASE_BIN 0x1u
+#define GF_PHASE_EMIT 0x2u
+#define GF_PHASE_RENDER 0x4u
+#define GF_PHASE_REDUCE 0x1u
+#define GF_PHASE_FINISH 0x2u
+#define GF_PHASE_ALL 0xffu
+
+/* gf_forward_bin + gf_forward_emit + gf_forward_render of every layer: three launches. */
+int gf_batch_forward(const void* plan, const gf_batch_info* info, uint32_t phases, void* stream);
+
+/* gf_backward of every layer (with its pair constants): two launches. */
+int gf_batch_backward(const void* plan, const gf_batch_info* info, uint32_t phases, void* stream);
 
 /*
  * Reads (and, if clear != 0, resets) the device status word of a workspace produced by the

@@ -333,3 +333,89 @@ def test_golden_fixture_tiny_ragged(device):
     field_close(delta, torch.from_numpy(d["delta"]))
     for name, a in zip(("d_mu", "d_chol_raw", "d_amp"), grads):
         grad_close(a, torch.from_numpy(d[name]), name)
+
+
+def _single_layer(p, device):
+    """Forward + backward of one field through FieldPlan (sync-free path)."""
+    q = p.to(device)
+    ref = run_gpu(p, device)
+    P = int(ref[1][-1])
+    return ref, P
+
+
+def test_batch_matches_single_layers(device):
+    from guass_amd.ops import FieldBatchPlan
+
+    k0 = tiny_problem(40, 56, 1, 13)
+    k0.mu, k0.chol_raw, k0.amp = k0.mu[:0], k0.chol_raw[:0], k0.amp[:0]
+    probs = [wl.cfg1(3), wl.cfg2(4), tiny_problem(45, 70, 12, 12), k0, wl.cfg1(5)]
+    say("batch of " + ", ".join(f"{p.out_features}x{p.in_features}/K{p.k}" for p in probs))
+    singles = [run_gpu(p, device) for p in probs]
+    layers = [p.to(device) for p in probs]
+    caps = [int(s[1][-1]) for s in singles]
+    batch = FieldBatchPlan(layers, device, capacities=caps)
+    batch.forward()
+    batch.backward()
+    torch.cuda.synchronize()
+    assert batch.status() == [0] * len(probs)
+    for i, (pl, s) in enumerate(zip(batch.plans, singles)):
+        P = caps[i]
+        assert torch.equal(pl.tile_ptr, s[1]), f"layer {i}: tile_ptr"
+        assert torch.equal(pl.ids[:P], s[2]), f"layer {i}: ids"
+        assert torch.equal(pl.delta, s[0]), f"layer {i}: delta"
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), s[3:]):
+            grad_close(a, b, f"layer {i} {name}", rtol=1e-5)
+
+
+def test_batch_sd15_layers_against_oracle(device):
+    """Three SD1.5 attention layers of BASELINE cfg4 (320x320, 320x768 cross-attention key,
+    640x640) in one batch, against the CPU oracle."""
+    from guass_amd.ops import FieldBatchPlan
+
+    shapes = wl.sd15_attention_shapes()
+    pick = [0, 6, 40]
+    probs = [wl.make_problem(f"cfg4_{shapes[i][0]}", shapes[i][1], shapes[i][2], 1024, math.log(8.0), 0.6, i)
+             for i in pick]
+    refs = [oracle(p, batched=True) for p in probs]
+    layers = [p.to(device) for p in probs]
+    batch = FieldBatchPlan(layers, device, capacities=[int(r[1][-1]) for r in refs])
+    batch.forward()
+    batch.backward()
+    torch.cuda.synchronize()
+    assert batch.status() == [0, 0, 0]
+    for p, pl, r in zip(probs, batch.plans, refs):
+        say(f"  {p.name}: pairs={int(r[1][-1])}")
+        binning_equal(pl.tile_ptr, pl.ids[:int(r[1][-1])], r[1], r[2])
+        field_close(pl.delta, r[0])
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), r[3:]):
+            grad_close(a, b, name)
+
+
+def test_batch_graph_replay(device):
+    from guass_amd.ops import FieldBatchPlan
+
+    probs = [wl.cfg1(7), wl.cfg2(8)]
+    singles = [run_gpu(p, device) for p in probs]
+    layers = [p.to(device) for p in probs]
+    batch = FieldBatchPlan(layers, device, capacities=[int(s[1][-1]) for s in singles])
+    s = torch.cuda.Stream(device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(s):
+        batch.forward()
+        batch.backward()
+    torch.cuda.current_stream(device).wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        batch.forward()
+        batch.backward()
+    for rep in range(3):
+        for pl in batch.plans:
+            pl.delta.fill_(float("nan"))
+            pl.d_amp.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (pl, sg) in enumerate(zip(batch.plans, singles)):
+            assert torch.equal(pl.delta, sg[0]), f"replay {rep} layer {i}: delta"
+            grad_close(pl.d_amp, sg[5], f"replay {rep} layer {i}: d_amp", rtol=1e-5)
+        _ = sum(float(pl.delta.abs().sum()) for pl in batch.plans)  # eager work between replays
