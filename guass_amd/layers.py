@@ -1,0 +1,233 @@
+"""The adapted linear layer's use of the Gaussian-field path, on the MI355X runtime.
+
+``GaussianLinear`` has the surface of the reference layer (gaussian_peft/layers/gaussian_linear.py
+:19-280) for the two execution modes that run the field path:
+
+* ``cuda_field_train``             ``gaussian_field_train`` (autograd through the gfx950 kernels)
+* ``cuda_field_stage2_validation`` forward-only with the binning metadata
+
+``compute_delta_weight`` (gaussian_linear.py:162-220) takes mu = tanh(mu_raw), renders the field
+with the quadratic form clamped at 80, reshapes it to [out_features, in_features], records
+``delta_w_norm`` in ``last_forward_metadata`` and scales by ``adapter_scale``.  ``forward`` adds
+x @ delta-W^T to the frozen base linear in row chunks of the output (gaussian_linear.py:222-253).
+
+The reference layer itself runs unchanged on ``guass_amd.cuda_field`` (it imports only
+``gaussian_field_train`` and ``gaussian_field_cuda_field_stage2_validation`` from the runtime);
+this module serves users of this package that do not carry the reference.  Parameter
+initialisation supports ``uniform_grid`` and ``random_uniform`` (gaussian_linear.py:104-129);
+``grid_overlap`` belongs to the reference's initialiser package and is not built here -- load its
+parameters with ``load_adapter_state``.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+from guass_amd.cuda_field.runtime import (
+    gaussian_field_cuda_field_stage2_validation,
+    gaussian_field_train,
+)
+
+FIELD_EXECUTION_MODES = ("cuda_field_train", "cuda_field_stage2_validation")
+_MODE_ALIASES = {"cuda_field_stage3_custom": "cuda_field_train"}  # config/adapter.py:82-90
+CLAMP_QUAD = 80.0  # what the layer passes to the field (gaussian_linear.py:176,190)
+
+
+@dataclass(slots=True)
+class GaussianAdapterConfig:
+    """Adapter configuration (field names and defaults of config/adapter.py:8-29)."""
+
+    init_num_gaussians: int = 32
+    init_method: str = "random_uniform"
+    coord_norm: str = "minus_one_to_one"
+    covariance_type: str = "cholesky"
+    use_amp_scaling: bool = True
+    adapter_scale: float = 1.0
+    chunk_size: int | None = None
+    train_bias: bool = False
+    merge_weights: bool = False
+    normalize_gaussian: bool = False
+    compute_dtype: torch.dtype = torch.float32
+    eps: float = 1e-5
+    init_amp_scale: float = 1e-4
+    init_chol_scale_multiplier: float = 1.5
+    min_cov_diag: float = 1e-4
+    execution_mode: str = "cuda_field_train"
+    tile_out: int = 32
+    tile_in: int = 32
+    sigma_multiplier: float = 3.0
+
+    def validate(self) -> None:
+        """The checks of config/adapter.py:31-79 that concern the field path."""
+        if self.init_num_gaussians <= 0:
+            raise ValueError("init_num_gaussians must be positive")
+        if self.init_method not in ("uniform_grid", "random_uniform", "grid_overlap"):
+            raise ValueError(f"Unsupported init_method={self.init_method!r}.")
+        if self.coord_norm != "minus_one_to_one":
+            raise ValueError(f"Unsupported coord_norm={self.coord_norm!r}.")
+        if self.covariance_type != "cholesky":
+            raise ValueError(f"Unsupported covariance_type={self.covariance_type!r}.")
+        if self.eps <= 0:
+            raise ValueError("eps must be positive")
+        if self.min_cov_diag <= 0:
+            raise ValueError("min_cov_diag must be positive")
+        if self.init_amp_scale < 0:
+            raise ValueError("init_amp_scale must be non-negative")
+        if self.init_chol_scale_multiplier <= 0:
+            raise ValueError("init_chol_scale_multiplier must be positive")
+        if self.tile_out <= 0 or self.tile_in <= 0:
+            raise ValueError("tile_out and tile_in must be positive")
+        if self.sigma_multiplier <= 0:
+            raise ValueError("sigma_multiplier must be positive")
+        if self.merge_weights:
+            raise ValueError("merge_weights is disabled in the first implementation")
+        self.execution_mode = _MODE_ALIASES.get(self.execution_mode, self.execution_mode)
+        if self.execution_mode not in FIELD_EXECUTION_MODES:
+            raise ValueError(
+                f"execution_mode={self.execution_mode!r} is not a Gaussian-field mode; this "
+                f"package runs {FIELD_EXECUTION_MODES}")
+
+
+class GaussianLinear(nn.Linear):
+    """nn.Linear with a frozen base weight plus a Gaussian-field delta-W."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True, *,
+                 adapter_config: GaussianAdapterConfig, device=None, dtype=None) -> None:
+        super().__init__(in_features, out_features, bias=bias, device=device, dtype=dtype)
+        adapter_config.validate()
+        self.adapter_config = adapter_config
+        self.merged = False
+        self.weight.requires_grad = False
+        if self.bias is not None and not adapter_config.train_bias:
+            self.bias.requires_grad = False
+        # linspace(-1, 1) axes on the layer's device (kernels/coords.py:23-34)
+        self.register_buffer("row_coords", torch.linspace(-1.0, 1.0, out_features, device=self.weight.device),
+                             persistent=False)
+        self.register_buffer("col_coords", torch.linspace(-1.0, 1.0, in_features, device=self.weight.device),
+                             persistent=False)
+        self.last_forward_metadata: dict = {}
+        self.reset_gaussian_parameters()
+
+    @classmethod
+    def from_linear(cls, linear: nn.Linear, adapter_config: GaussianAdapterConfig) -> "GaussianLinear":
+        layer = cls(linear.in_features, linear.out_features, bias=linear.bias is not None,
+                    adapter_config=adapter_config, device=linear.weight.device,
+                    dtype=linear.weight.dtype)
+        with torch.no_grad():
+            layer.weight.copy_(linear.weight)
+            if linear.bias is not None:
+                layer.bias.copy_(linear.bias)
+        return layer
+
+    @property
+    def num_gaussians(self) -> int:
+        return int(self.mu_raw.shape[0])
+
+    # ---------------------------------------------------------------- parameters
+
+    def _parameter_dtype(self) -> torch.dtype:
+        dt = self.adapter_config.compute_dtype
+        return torch.float32 if dt in (torch.float16, torch.bfloat16) else dt
+
+    def reset_gaussian_parameters(self) -> None:
+        """uniform_grid / random_uniform initialisation (gaussian_linear.py:104-138)."""
+        cfg = self.adapter_config
+        if cfg.init_method == "grid_overlap":
+            raise NotImplementedError(
+                "init_method='grid_overlap' uses the reference's initialiser package, which is "
+                "not part of this build; initialise elsewhere and call load_adapter_state()")
+        k, dev, dt = cfg.init_num_gaussians, self.weight.device, self._parameter_dtype()
+        if cfg.init_method == "uniform_grid":
+            side = math.ceil(math.sqrt(k))
+            ax = torch.linspace(-1.0, 1.0, side, device=dev, dtype=dt)
+            gx, gy = torch.meshgrid(ax, ax, indexing="ij")
+            mu = torch.stack((gx, gy), dim=-1).reshape(-1, 2)[:k]
+        else:
+            mu = torch.empty(k, 2, device=dev, dtype=dt).uniform_(-1.0, 1.0)
+        scale = max(2.0 / math.sqrt(max(k, 1)) * cfg.init_chol_scale_multiplier, cfg.min_cov_diag ** 0.5)
+        chol_raw = torch.zeros(k, 3, device=dev, dtype=dt)
+        inv_sp = math.log(math.expm1(scale - cfg.eps))
+        chol_raw[:, 0] = inv_sp
+        chol_raw[:, 2] = inv_sp
+        amp = torch.zeros(k, 1, device=dev, dtype=dt)
+        if cfg.init_amp_scale > 0:
+            amp.normal_(mean=0.0, std=cfg.init_amp_scale)
+        self.mu_raw = nn.Parameter(torch.atanh(mu.clamp(-0.999999, 0.999999)))
+        self.chol_raw = nn.Parameter(chol_raw)
+        self.amp = nn.Parameter(amp)
+
+    def get_gaussian_parameters(self) -> dict[str, nn.Parameter]:
+        return {"mu_raw": self.mu_raw, "chol_raw": self.chol_raw, "amp": self.amp}
+
+    def get_adapter_state(self) -> dict[str, Tensor]:
+        return {k: v.detach().clone() for k, v in self.get_gaussian_parameters().items()}
+
+    def load_adapter_state(self, state: dict[str, Tensor]) -> None:
+        self.replace_gaussian_parameters_(mu_raw=state["mu_raw"], chol_raw=state["chol_raw"],
+                                          amp=state["amp"])
+
+    def replace_gaussian_parameters_(self, *, mu_raw: Tensor | None = None,
+                                     chol_raw: Tensor | None = None, amp: Tensor | None = None) -> None:
+        dev, dt = self.weight.device, self._parameter_dtype()
+        if mu_raw is not None:
+            self.mu_raw = nn.Parameter(mu_raw.to(device=dev, dtype=dt))
+        if chol_raw is not None:
+            self.chol_raw = nn.Parameter(chol_raw.to(device=dev, dtype=dt))
+        if amp is not None:
+            self.amp = nn.Parameter(amp.to(device=dev, dtype=dt))
+
+    def materialize_mu(self) -> Tensor:
+        return torch.tanh(self.mu_raw)
+
+    # ---------------------------------------------------------------- delta-W
+
+    def compute_delta_weight(self) -> Tensor:
+        cfg = self.adapter_config
+        ctx = torch.autocast(device_type="cuda", enabled=False) if self.weight.is_cuda else _null()
+        with ctx:
+            kwargs = dict(row_coords=self.row_coords, col_coords=self.col_coords,
+                          mu=self.materialize_mu().contiguous(), chol_raw=self.chol_raw,
+                          amp=self.amp, tile_out=cfg.tile_out, tile_in=cfg.tile_in,
+                          sigma_multiplier=cfg.sigma_multiplier, normalize=cfg.normalize_gaussian,
+                          clamp_quad=CLAMP_QUAD)
+            if cfg.execution_mode == "cuda_field_stage2_validation":
+                delta, metadata = gaussian_field_cuda_field_stage2_validation(**kwargs)
+            else:
+                delta = gaussian_field_train(**kwargs)
+                metadata = {"execution_mode": "cuda_field_train",
+                            "accumulate_backend": "cuda_field_train"}
+        delta_weight = delta.reshape(self.out_features, self.in_features)
+        metadata = dict(metadata)
+        metadata["delta_w_norm"] = float(delta_weight.detach().float().norm().item())
+        self.last_forward_metadata = metadata
+        return delta_weight * cfg.adapter_scale
+
+    def _delta_apply_row_chunk(self) -> int:
+        return min(self.out_features, max(max(1, int(self.adapter_config.tile_out)), 64))
+
+    def forward(self, input: Tensor) -> Tensor:
+        delta_weight = self.compute_delta_weight().to(dtype=self.weight.dtype)
+        base = F.linear(input, self.weight, self.bias)
+        chunk = self._delta_apply_row_chunk()
+        metadata = dict(self.last_forward_metadata)
+        metadata["linear_composition"] = "base_plus_delta_row_chunk_accumulate"
+        metadata["delta_apply_row_chunk"] = float(chunk)
+        self.last_forward_metadata = metadata
+        out = base.clone()
+        for r0 in range(0, self.out_features, chunk):
+            r1 = min(r0 + chunk, self.out_features)
+            out[..., r0:r1].add_(F.linear(input, delta_weight[r0:r1, :], None))
+        return out
+
+
+class _null:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False

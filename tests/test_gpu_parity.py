@@ -192,7 +192,7 @@ def test_int32_saved_state(device):
     g64 = run_gpu(p, device)
     g32 = run_gpu(p, device, index_dtype=torch.int32)
     for a, b in zip(g64[3:], g32[3:]):
-        grad_close(a, b, "int32 vs int64", rtol=1e-6)
+        grad_close(a, b, "int32 vs int64", rtol=1e-5)
 
 
 @pytest.mark.parametrize("kind", ["last", "order", "negative", "range"])
@@ -266,8 +266,9 @@ def test_plan_sync_free_and_capacity(device):
     assert plan.status() == 0 and plan.pairs() == P
     assert torch.equal(plan.delta, ref[0]) and torch.equal(plan.tile_ptr, ref[1])
     assert torch.equal(plan.ids[:P], ref[2])
+    # same arithmetic; fp32 atomics accumulate the tiles in a run-dependent order
     for a, b in zip((plan.d_mu, plan.d_chol_raw, plan.d_amp), ref[3:]):
-        grad_close(a, b, "plan", rtol=1e-6)
+        grad_close(a, b, "plan", rtol=1e-5)
     # Gaussian constants recomputed from mu / chol_raw instead of reused from the forward.
     fresh = [t.clone() for t in plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw,
                                               q.amp, num_pairs=P, reuse_forward=False)]
@@ -312,7 +313,7 @@ def test_graph_replay_matches_eager(device):
         assert torch.equal(plan.delta, eager[0]), f"replay {rep}: delta"
         assert torch.equal(plan.ids[:P], eager[2]), f"replay {rep}: ids"
         for a, b in zip((plan.d_mu, plan.d_chol_raw, plan.d_amp), eager[3:]):
-            grad_close(a, b, f"replay {rep}", rtol=1e-6)
+            grad_close(a, b, f"replay {rep}", rtol=1e-5)
         _ = (eager[0] * 2.0).sum().item()  # eager work between replays
 
 
@@ -419,3 +420,48 @@ def test_batch_graph_replay(device):
             assert torch.equal(pl.delta, sg[0]), f"replay {rep} layer {i}: delta"
             grad_close(pl.d_amp, sg[5], f"replay {rep} layer {i}: d_amp", rtol=1e-5)
         _ = sum(float(pl.delta.abs().sum()) for pl in batch.plans)  # eager work between replays
+
+
+@pytest.mark.parametrize("tile", [16, 32])
+def test_gaussian_linear_layer(device, tile):
+    """GaussianLinear.compute_delta_weight / forward (gaussian_linear.py:162-253): delta-W and the
+    gradients of mu_raw (through tanh), chol_raw and amp against the oracle; the row-chunked
+    forward against the dense x (W + delta-W)^T + b."""
+    import torch.nn.functional as F
+
+    from guass_amd.layers import GaussianAdapterConfig, GaussianLinear
+
+    say(f"GaussianLinear 96->80, K=48, tiles {tile}x{tile}")
+    gen = torch.Generator().manual_seed(tile)
+    cfg = GaussianAdapterConfig(init_num_gaussians=48, init_method="random_uniform", tile_out=tile,
+                                tile_in=tile, adapter_scale=0.5, init_amp_scale=1e-2)
+    base = torch.nn.Linear(96, 80, device=device)
+    layer = GaussianLinear.from_linear(base, cfg)
+    with torch.no_grad():  # varied sizes (sigma ~ 1.5-8 px) and orientations, well conditioned
+        raw = torch.randn(48, 3, generator=gen)
+        raw[:, 0] = raw[:, 0] * 0.5 - 2.5
+        raw[:, 2] = raw[:, 2] * 0.5 - 2.5
+        raw[:, 1] = raw[:, 1] * 0.03
+        layer.chol_raw.copy_(raw.to(device))
+    dW = layer.compute_delta_weight()
+    G = torch.randn(80, 96, generator=gen).to(device)
+    (dW * G).sum().backward()
+    torch.cuda.synchronize()
+    mu = layer.materialize_mu().detach().cpu()  # the same fp32 means the layer rendered
+    ref = fo.gaussian_field_fwd_bwd(layer.row_coords.cpu(), layer.col_coords.cpu(), mu,
+                                    layer.chol_raw.detach().cpu(), layer.amp.detach().cpu(),
+                                    (0.5 * G).reshape(-1).cpu(), tile, tile, 3.0, False, 80.0)
+    field_close(dW.detach().reshape(-1) / 0.5, ref[0])
+    grad_close(layer.mu_raw.grad, ref[3] * (1.0 - mu * mu), "d_mu_raw")
+    grad_close(layer.chol_raw.grad, ref[4], "d_chol_raw")
+    grad_close(layer.amp.grad, ref[5], "d_amp")
+    meta = layer.last_forward_metadata
+    assert meta["execution_mode"] == "cuda_field_train"
+    assert abs(meta["delta_w_norm"] - float(ref[0].double().norm())) <= 1e-5 * meta["delta_w_norm"]
+    x = torch.randn(5, 96, generator=gen).to(device)
+    with torch.no_grad():
+        y = layer(x)
+        assert layer.last_forward_metadata["delta_apply_row_chunk"] == float(min(80, max(tile, 64)))
+        assert layer.last_forward_metadata["linear_composition"] == "base_plus_delta_row_chunk_accumulate"
+        want = F.linear(x, layer.weight + layer.compute_delta_weight(), layer.bias)
+    assert float((y - want).abs().max()) <= 1e-5 * float(want.abs().max())

@@ -1,0 +1,36 @@
+"""GaussianLinear's field path (reference gaussian_linear.py:162-253) without a GPU: config
+validation, initialisation and the reference's error on non-CUDA tensors."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from guass_amd.layers import GaussianAdapterConfig, GaussianLinear
+
+
+def test_config_validation_and_aliases():
+    cfg = GaussianAdapterConfig(execution_mode="cuda_field_stage3_custom")
+    cfg.validate()
+    assert cfg.execution_mode == "cuda_field_train"
+    for bad in (dict(execution_mode="dense_reference"), dict(tile_out=0), dict(sigma_multiplier=0.0),
+                dict(init_num_gaussians=0), dict(merge_weights=True), dict(eps=0.0)):
+        with pytest.raises(ValueError):
+            GaussianAdapterConfig(**bad).validate()
+    with pytest.raises(NotImplementedError):
+        GaussianLinear(8, 8, adapter_config=GaussianAdapterConfig(init_method="grid_overlap"))
+
+
+def test_layer_parameters_and_cpu_error():
+    torch.manual_seed(0)
+    cfg = GaussianAdapterConfig(init_num_gaussians=10, init_method="uniform_grid")
+    layer = GaussianLinear(24, 16, adapter_config=cfg)
+    assert layer.num_gaussians == 10 and layer.chol_raw.shape == (10, 3) and layer.amp.shape == (10, 1)
+    assert not layer.weight.requires_grad and not layer.bias.requires_grad
+    mu = layer.materialize_mu().detach()
+    assert float(mu.abs().max()) <= 1.0 and torch.allclose(mu[0], torch.tensor([-1.0, -1.0]), atol=1e-5)
+    state = layer.get_adapter_state()
+    layer.load_adapter_state({k: v + 0.0 for k, v in state.items()})
+    assert torch.equal(layer.amp, state["amp"])
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        layer.compute_delta_weight()
