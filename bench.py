@@ -205,8 +205,8 @@ def main() -> int:
             plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
 
         phases = {
-            "k_bin": [lambda: plan.bin(q.mu, q.chol_raw)],
-            "k_emit+": [lambda: plan.bin(q.mu, q.chol_raw), lambda: plan.emit(q.mu, q.amp)],
+            "k_bin": [lambda: plan.bin(q.mu, q.chol_raw, q.amp)],
+            "k_emit+": [lambda: plan.bin(q.mu, q.chol_raw, q.amp), lambda: plan.emit(q.mu, q.amp)],
             "k_render": [lambda: plan.render(q.row_coords, q.col_coords)],
             "k_bwd": [lambda: plan.backward_reduce(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, P)],
             "k_bwd_finish": [lambda: plan.backward_finish(q.chol_raw, q.amp)],

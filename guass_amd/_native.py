@@ -101,7 +101,7 @@ def lib() -> ctypes.CDLL:
     L.gf_forward_workspace_bytes.restype = c_size_t
     L.gf_backward_workspace_bytes.argtypes = [c_int64, c_int64, c_int64, _CFG]
     L.gf_backward_workspace_bytes.restype = c_size_t
-    L.gf_forward_bin.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_size_t, _P]
+    L.gf_forward_bin.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_size_t, _P]
     L.gf_forward_emit.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, c_int64, _P,
                                   c_size_t, _P]
     L.gf_forward_render.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P,

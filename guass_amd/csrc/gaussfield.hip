@@ -1,17 +1,21 @@
 // gaussfield.hip - gfx950 kernels and C ABI of libgaussfield.so.
 //
-// Forward (reference forward.cu:372-569), three kernels:
+// Forward (reference forward.cu:372-569), two kernels on the mask path (16x16 tiles, K <= 8192),
+// three otherwise:
 //   k_bin      one workgroup per field: bit-exact sigma-box tile rectangle of every Gaussian,
 //              the pair total, per-tile Gaussian counts from row-wise difference arrays and
 //              their scan -> tile_ptr; every scan runs in LDS (DPP wave scans) and global
-//              memory is only written, coalesced.
-//   k_emit     one wave per Gaussian: its evaluation constants (kept in the workspace for the
-//              render and the backward) and a slot in each touched tile's range from tile_ptr
-//              and a per-tile fill counter (a counting sort on the tile key).
+//              memory is only written, coalesced.  Mask path (k_bin_masks): also each
+//              Gaussian's evaluation constants and, per tile row and tile column, a bitmask of
+//              the Gaussians whose tile range covers it.
+//   k_emit     (emission path) one wave per Gaussian: its evaluation constants (kept in the
+//              workspace for the render and the backward) and a slot in each touched tile's
+//              range from tile_ptr and a per-tile fill counter (a counting sort on the tile key).
 //   k_render16 one wave per 16x16 tile, four independent tiles per workgroup, no workgroup
-//              barriers: canonical (ascending gid) order of the tile's ids (written back),
-//              per-Gaussian constants loaded one Gaussian per lane and broadcast with
-//              readlane, 4 pixels per lane with per-row terms hoisted.
+//              barriers: the tile's ids in canonical (ascending gid) order -- the set bits of
+//              rowmask & colmask (mask path) or k_emit's segment sorted -- written to the
+//              tile's segment, per-Gaussian constants loaded one Gaussian per lane and broadcast
+//              with readlane, 4 pixels per lane with per-row terms hoisted.
 //   (k_render_any handles other tile shapes.)
 // Backward (reference backward.cu:541-716), two kernels:
 //   k_bwd16    one wave per 16x16 tile: lanes are (Gaussian slot, tile row); each lane sums
@@ -44,6 +48,15 @@ constexpr int kTileThreads = 256;
 constexpr int kEmitThreads = 256;
 constexpr int kLdsDiffWords = 12288;  // 48 KiB row-difference band in k_bin
 constexpr int kBinMaxBandRows = 1024; // row totals kept in LDS per band in k_bin
+constexpr int kMaskLdsWords = 16384;  // 64 KiB band of tile-row / tile-column masks in k_bin
+constexpr int64_t kMaskMaxK = 8192;   // mask path up to this many Gaussians (256 words a mask)
+constexpr int64_t kMaskMaxWords = int64_t(1) << 24;  // and up to (R + C) * W mask words
+
+// k_bin counts a tile grid of C columns in LDS bands (int32 row sums) when this holds;
+// otherwise through global memory.
+__host__ __device__ inline bool bin_counts_in_lds(int64_t C, int64_t K) {
+  return (C | 1) <= kLdsDiffWords && K * C < (int64_t)INT32_MAX;
+}
 constexpr int kSortLdsKeys = 2048;    // (any-shape kernels) segments up to this length in LDS
 constexpr int kBitmapMaxK = 131072;   // (any-shape kernels) longer segments: K-bit bitmap
 constexpr int kSortLdsWords = (kSortLdsKeys > kBitmapMaxK / 32) ? kSortLdsKeys : kBitmapMaxK / 32;
@@ -86,6 +99,7 @@ struct Problem {
   float sigma;
   float q_lo, q_hi;  // clamp range of the scaled quadratic form q * kHalfLog2e
   int32_t normalize;
+  int32_t W;  // words per tile-row / tile-column mask (0: the ids are emitted by k_emit)
 };
 
 // Per-Gaussian constants of the tile kernels: with dx = x - mu0, dy = y - mu1,
@@ -107,11 +121,14 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Forward workspace: header, per-Gaussian evaluation constants eval[K] (GaussEval), rect[K]
 // (int4 tile ranges), cov[K] (float4: the fp32 covariance s00, s01, s11 and 0), fill[T]
-// (int32 ids emitted so far into each tile's segment).
+// (int32 ids emitted so far into each tile's segment; emission path), rowmask[R][W] and
+// colmask[C][W] (mask path: bit g%32 of word g/32 is set when Gaussian g's tile rectangle covers
+// the tile row / column).
 struct FwdLayout {
-  size_t eval, rect, cov, fill, total;
+  size_t eval, rect, cov, fill, rowmask, colmask, total;
 };
-FwdLayout fwd_layout(int64_t K, int64_t T) {
+FwdLayout fwd_layout(const Problem& p) {
+  const int64_t K = p.K, T = (int64_t)p.R * p.C;
   FwdLayout L;
   size_t o = sizeof(WsHeader);
   L.eval = o;
@@ -122,6 +139,10 @@ FwdLayout fwd_layout(int64_t K, int64_t T) {
   o = align256(o + sizeof(float4) * (size_t)K);
   L.fill = o;
   o = align256(o + sizeof(int32_t) * (size_t)T);
+  L.rowmask = o;
+  o = align256(o + sizeof(uint32_t) * (size_t)p.R * (size_t)p.W);
+  L.colmask = o;
+  o = align256(o + sizeof(uint32_t) * (size_t)p.C * (size_t)p.W);
   L.total = o;
   return L;
 }
@@ -396,11 +417,12 @@ constexpr int kBinRectRegs = 4;
 // tile_ptr of a tile is its row's base plus the exclusive prefix of the counts.  Writes
 // tile_ptr and clears the tiles' fill counters directly.
 template <int V>
-__device__ inline void bin_scan_rows(const int32_t* lds, int32_t C, int32_t nb, int64_t b0,
+__device__ inline void bin_scan_rows(const int32_t* lds, int32_t stride, int32_t C, int32_t nb, int64_t b0,
                                      const int64_t* rowbase, int64_t* __restrict__ tile_ptr,
                                      int32_t* __restrict__ fill, int lane, int wid) {
+  // fill == nullptr: no emission follows (mask path), nothing to clear
   for (int32_t row = wid; row < nb; row += kBinThreads / 64) {
-    const int32_t* rp = lds + row * C;
+    const int32_t* rp = lds + row * stride;
     const int64_t out0 = (b0 + row) * (int64_t)C;
     const int64_t base_off = rowbase[row];
     int32_t carry_d = 0, carry_c = 0;
@@ -427,7 +449,7 @@ __device__ inline void bin_scan_rows(const int32_t* lds, int32_t C, int32_t nb, 
       for (int v = 0; v < V; ++v) {
         if (col0 + v < C) {
           tile_ptr[out0 + col0 + v] = base_off + off;
-          fill[out0 + col0 + v] = 0;
+          if (fill) fill[out0 + col0 + v] = 0;
         }
         off += c[v];
       }
@@ -438,15 +460,16 @@ __device__ inline void bin_scan_rows(const int32_t* lds, int32_t C, int32_t nb, 
 }
 
 // The binning of one field by one workgroup of kBinThreads threads.  With kEval it also
-// stores each Gaussian's evaluation constants (one Gaussian per thread: the batched path, where
-// every field has its own workgroup); otherwise k_emit computes them.
+// stores each Gaussian's evaluation constants (one Gaussian per thread); otherwise k_emit
+// computes them.  With p.W > 0 (mlds: kMaskLdsWords of LDS) it also writes the tile-row and
+// tile-column masks, from which the render reads each tile's ids (no emission).
 template <bool kEval>
 __device__ __forceinline__ void bin_body(const Problem& p, const float* __restrict__ mu,
                                          const float* __restrict__ chol_raw,
                                          const float* __restrict__ amp,
                                          int64_t* __restrict__ tile_ptr,
                                          int64_t* __restrict__ num_pairs, uint8_t* ws,
-                                         const FwdLayout& L) {
+                                         const FwdLayout& L, uint32_t* mlds) {
   __shared__ int32_t lds[kLdsDiffWords];
   __shared__ int64_t rowbase[kBinMaxBandRows + 1];
   __shared__ int32_t rowdiff[kBinMaxBandRows + 1];
@@ -456,26 +479,42 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
   int4* rect = reinterpret_cast<int4*>(ws + L.rect);
   float4* covs = reinterpret_cast<float4*>(ws + L.cov);
   int32_t* fill = reinterpret_cast<int32_t*>(ws + L.fill);
+  uint32_t* rowmask = reinterpret_cast<uint32_t*>(ws + L.rowmask);
+  uint32_t* colmask = reinterpret_cast<uint32_t*>(ws + L.colmask);
   const int64_t K = p.K, T = (int64_t)p.R * p.C;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int32_t W = mlds ? p.W : 0;  // mask words (the host only sets p.W where masks fit)
   if (threadIdx.x == 0) {
     hdr->status = 0u;
     pairs_lds = 0ull;
   }
 
   // Per-tile counts go through LDS, band by band of whole tile rows, when the grid allows it.
-  const bool lds_path = p.C <= kLdsDiffWords && K * p.C < (int64_t)INT32_MAX;
+  const bool lds_path = bin_counts_in_lds(p.C, K);
   const int32_t C = p.C;
-  const int32_t band_rows = lds_path ? min(kLdsDiffWords / C, kBinMaxBandRows) : 0;
+  // LDS rows of masks are Wp = W | 1 words apart: with an odd stride, the same word of
+  // different rows falls in different LDS banks (the lanes of a wave share a word index).
+  const int32_t Wp = W > 0 ? (W | 1) : 0;  // no masks: no mask rows (mlds may be NULL)
+  // Count rows likewise Cp = C | 1 apart (the first columns of clustered rectangles coincide).
+  const int32_t Cp = C | 1;
+  int32_t band_rows = lds_path ? min(kLdsDiffWords / Cp, kBinMaxBandRows) : 0;
+  if (W > 0) band_rows = min(band_rows, kMaskLdsWords / Wp);
   auto clear_band = [&](int32_t nb) {
-    for (int32_t i = threadIdx.x; i < nb * C; i += kBinThreads) lds[i] = 0;
+    for (int32_t i = threadIdx.x; i < nb * Cp; i += kBinThreads) lds[i] = 0;
     for (int32_t i = threadIdx.x; i <= nb; i += kBinThreads) rowdiff[i] = 0;
+    for (int32_t i = threadIdx.x; i < nb * Wp; i += kBinThreads) mlds[i] = 0u;
+  };
+  // n mask rows of LDS (stride Wp) -> global rows of W words, by threads t0, t0 + nt, ...
+  auto copy_masks = [&](uint32_t* out, int32_t n, int32_t t0, int32_t nt) {
+    for (int32_t i = t0; i < n * W; i += nt) {
+      const int32_t r = i / W;
+      out[i] = mlds[r * Wp + (i - r * W)];
+    }
   };
   if (lds_path) clear_band(min(band_rows, p.R));
 
   // A: tile rectangles, fp32 covariances and pairs (tiles touched); the first
-  // kBinRectRegs * kBinThreads Gaussians keep their rectangle in registers.  (Evaluation
-  // constants are computed from the stored covariances by k_emit, spread over the GPU.)
+  // kBinRectRegs * kBinThreads Gaussians keep their rectangle in registers.
   int4 myrect[kBinRectRegs];
   int64_t my_pairs = 0;
   auto prep = [&](int64_t g) -> int4 {
@@ -507,10 +546,12 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
   if (lane == 0) atomicAdd(&pairs_lds, (unsigned long long)wave_pairs);
 
   // C: each covered row of each rectangle adds +1 at its first column and -1 after its last;
-  // the rectangle's width is added over its rows through a difference array over rows.  Wave
-  // 0 turns the row differences into row totals and row bases; then one wave per row scans
-  // the column differences into counts and the counts into tile_ptr (row base + exclusive
-  // prefix), written coalesced together with cleared fill counters.
+  // the rectangle's width is added over its rows through a difference array over rows (and,
+  // with masks, the Gaussian's bit is set in each covered row's mask).  Wave 0 turns the row
+  // differences into row totals and row bases while the other waves copy out the band's row
+  // masks; then one wave per row scans the column differences into counts and the counts into
+  // tile_ptr (row base + exclusive prefix), written coalesced together with cleared fill
+  // counters (emission path).
   int64_t Pc = 0;
   if (lds_path) {
     int64_t band_base = 0;
@@ -520,22 +561,25 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
         clear_band(nb);
         __syncthreads();
       }
-      auto diff = [&](const int4 r) {
+      auto diff = [&](const int4 r, int64_t g) {
         const int32_t rlo = max(r.x, b0), rhi = min(r.y, b0 + nb - 1);
         if (rlo > rhi) return;
+        const uint32_t bit = 1u << (g & 31);
+        const int32_t word = (int32_t)(g >> 5);
         for (int32_t row = rlo; row <= rhi; ++row) {
-          int32_t* d = lds + (row - b0) * C;
+          int32_t* d = lds + (row - b0) * Cp;
           atomicAdd(d + r.z, 1);
           if (r.w + 1 < C) atomicAdd(d + r.w + 1, -1);
+          if (W > 0) atomicOr(mlds + (row - b0) * Wp + word, bit);
         }
         const int32_t w = r.w - r.z + 1;
         atomicAdd(rowdiff + (rlo - b0), w);
         atomicAdd(rowdiff + (rhi + 1 - b0), -w);  // index <= nb
       };
 #pragma unroll
-      for (int i = 0; i < kBinRectRegs; ++i) diff(myrect[i]);
+      for (int i = 0; i < kBinRectRegs; ++i) diff(myrect[i], threadIdx.x + (int64_t)i * kBinThreads);
       for (int64_t g = threadIdx.x + (int64_t)kBinRectRegs * kBinThreads; g < K; g += kBinThreads)
-        diff(rect[g]);
+        diff(rect[g], g);
       __syncthreads();
       if (wid == 0) {
         int64_t carry = 0;
@@ -551,15 +595,40 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
           carry_t += __builtin_amdgcn_readlane(tinc, 63);
         }
         if (lane == 0) rowbase[kBinMaxBandRows] = band_base + carry;
+      } else if (W > 0) {
+        copy_masks(rowmask + (int64_t)b0 * W, nb, threadIdx.x - 64, kBinThreads - 64);
       }
       __syncthreads();
-      if (C <= 64) bin_scan_rows<1>(lds, C, nb, b0, rowbase, tile_ptr, fill, lane, wid);
-      else if (C <= 128) bin_scan_rows<2>(lds, C, nb, b0, rowbase, tile_ptr, fill, lane, wid);
-      else bin_scan_rows<4>(lds, C, nb, b0, rowbase, tile_ptr, fill, lane, wid);
+      int32_t* fl = W > 0 ? nullptr : fill;
+      if (C <= 64) bin_scan_rows<1>(lds, Cp, C, nb, b0, rowbase, tile_ptr, fl, lane, wid);
+      else if (C <= 128) bin_scan_rows<2>(lds, Cp, C, nb, b0, rowbase, tile_ptr, fl, lane, wid);
+      else bin_scan_rows<4>(lds, Cp, C, nb, b0, rowbase, tile_ptr, fl, lane, wid);
       band_base = rowbase[kBinMaxBandRows];
       __syncthreads();
     }
     Pc = band_base;
+    // D (masks): the column masks, band by band of tile columns.
+    if (W > 0) {
+      const int32_t band_cols = kMaskLdsWords / Wp;
+      for (int32_t cb0 = 0; cb0 < C; cb0 += band_cols) {
+        const int32_t nc = min(C - cb0, band_cols);
+        for (int32_t i = threadIdx.x; i < nc * Wp; i += kBinThreads) mlds[i] = 0u;
+        __syncthreads();
+        auto colset = [&](const int4 r, int64_t g) {
+          const int32_t lo = max(r.z, cb0), hi = min(r.w, cb0 + nc - 1);
+          const uint32_t bit = 1u << (g & 31);
+          uint32_t* m = mlds + (g >> 5);
+          for (int32_t c = lo; c <= hi; ++c) atomicOr(m + (c - cb0) * Wp, bit);
+        };
+#pragma unroll
+        for (int i = 0; i < kBinRectRegs; ++i) colset(myrect[i], threadIdx.x + (int64_t)i * kBinThreads);
+        for (int64_t g = threadIdx.x + (int64_t)kBinRectRegs * kBinThreads; g < K; g += kBinThreads)
+          colset(rect[g], g);
+        __syncthreads();
+        copy_masks(colmask + (int64_t)cb0 * W, nc, threadIdx.x, kBinThreads);
+        __syncthreads();
+      }
+    }
   } else {
     // Very wide tile grids (> kLdsDiffWords tile columns): counts through global memory.
     for (int64_t i = threadIdx.x; i < T; i += kBinThreads) tile_ptr[i] = 0;
@@ -587,12 +656,24 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
   }
 }
 
+// Emission path: rectangles, counts and tile_ptr (k_emit computes the Gaussians' constants).
 __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __restrict__ mu,
                                                      const float* __restrict__ chol_raw,
                                                      int64_t* __restrict__ tile_ptr,
                                                      int64_t* __restrict__ num_pairs, uint8_t* ws,
                                                      FwdLayout L) {
-  bin_body<false>(p, mu, chol_raw, nullptr, tile_ptr, num_pairs, ws, L);
+  bin_body<false>(p, mu, chol_raw, nullptr, tile_ptr, num_pairs, ws, L, nullptr);
+}
+
+// Mask path: also the Gaussians' constants and the tile-row / tile-column masks.
+__global__ __launch_bounds__(kBinThreads) void k_bin_masks(Problem p, const float* __restrict__ mu,
+                                                           const float* __restrict__ chol_raw,
+                                                           const float* __restrict__ amp,
+                                                           int64_t* __restrict__ tile_ptr,
+                                                           int64_t* __restrict__ num_pairs, uint8_t* ws,
+                                                           FwdLayout L) {
+  __shared__ uint32_t mlds[kMaskLdsWords];
+  bin_body<true>(p, mu, chol_raw, amp, tile_ptr, num_pairs, ws, L, mlds);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -894,13 +975,16 @@ __device__ inline void tile_range(const int64_t* __restrict__ tile_ptr, int64_t 
 }
 
 // 16x16 tiles, one wave per tile (tile blockIdx.x * 4 + wave).  Lane l covers tile row l/4,
-// columns 4*(l%4)..+3.  Gaussian constants are computed one per lane for up to 64 Gaussians at
+// columns 4*(l%4)..+3.  Gaussian constants are loaded one per lane for up to 64 Gaussians at
 // a time and broadcast with readlane while every lane accumulates its 4 pixels.
-// Tile t (16x16) of one field by one wave.
+// Tile t (16x16) of one field by one wave.  The tile's ids come from the masks (p.W > 0: the
+// set bits of rowmask[tr] & colmask[tc], in ascending order, written to the tile's segment) or
+// from k_emit's segment (ordered here by a rank sort and written back where they moved).
 __device__ __forceinline__ void render16_body(
     const Problem& p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids,
-    int64_t capacity, float* __restrict__ delta, uint8_t* ws, int64_t t) {
+    int64_t capacity, float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
+    const uint32_t* __restrict__ colmask, int64_t t) {
   __shared__ int32_t wkeys[kTileThreads / 64][kWaveSortKeys];
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   const int lane = threadIdx.x & 63;
@@ -913,8 +997,6 @@ __device__ __forceinline__ void render16_body(
   float y[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) y[i] = col_coords[min(pc + i, p.N - 1)];
-  int64_t s, n;
-  tile_range(tile_ptr, t, capacity, &s, &n);
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   auto accumulate = [&](const GaussEval& u) {
     const float dx = x - u.mu0;
@@ -927,6 +1009,57 @@ __device__ __forceinline__ void render16_body(
       acc[i] = fmaf(u.w, basis_w(p, A, z), acc[i]);
     }
   };
+  int64_t s, n;
+  if (p.W > 0) {
+    // The tile's segment [s, s + count) from tile_ptr; ids past the capacity are not stored.
+    s = tile_ptr[t];
+    const int64_t count = tile_ptr[t + 1] - s;
+    const int64_t room = capacity - s < count ? (capacity - s > 0 ? capacity - s : 0) : count;
+    const uint32_t* rm = rowmask + (int64_t)tr * p.W;
+    const uint32_t* cm = colmask + (int64_t)tc * p.W;
+    int32_t* keys = wkeys[wid];
+    int64_t done = 0;
+    for (int32_t w0 = 0; w0 < p.W; w0 += 64) {
+      const int32_t w = w0 + lane;
+      const uint32_t m = w < p.W ? (rm[w] & cm[w]) : 0u;
+      const int32_t cnt = __popc(m);
+      const int32_t inc = dpp_scan_i32(cnt);
+      const int32_t tot = __builtin_amdgcn_readlane(inc, 63);
+      // Expand the set bits in order, kWaveSortKeys positions at a time.
+      for (int32_t base = 0; base < tot; base += kWaveSortKeys) {
+        uint32_t mm = m;
+        int32_t pos = inc - cnt;
+        while (mm != 0u && pos < base + kWaveSortKeys) {
+          const int32_t bit = __builtin_ctz(mm);
+          mm &= mm - 1u;
+          if (pos >= base) keys[pos - base] = (w << 5) + bit;
+          ++pos;
+        }
+        wave_sync();
+        const int32_t nwin = min(kWaveSortKeys, tot - base);
+        for (int32_t j0 = 0; j0 < nwin; j0 += 64) {
+          const int nj = min(64, nwin - j0);
+          GaussEval my = zero_eval();
+          if (lane < nj) {
+            const int32_t g = keys[j0 + lane];
+            my = load_eval(ev, g);
+            const int64_t slot = done + j0 + lane;
+            if (slot < room) ids[s + slot] = g;
+          }
+          for (int j = 0; j < nj; ++j) accumulate(readlane_eval(my, j));
+        }
+        done += nwin;
+        wave_sync();
+      }
+    }
+    if (lane == 0) {
+      if (done != count) set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);
+      if (room < count) set_status(&hdr->status, GF_STATUS_CAPACITY);
+    }
+    n = 0;  // rendered
+  } else {
+    tile_range(tile_ptr, t, capacity, &s, &n);
+  }
   if (n > 0 && n <= 64) {
     // Rank sort of the ids (emission order); each lane gathers its Gaussian's constants while
     // the ranks are computed, then they follow their id to lane `rank` (ds_permute).
@@ -986,8 +1119,9 @@ __device__ __forceinline__ void render16_body(
 __global__ __launch_bounds__(kTileThreads) void k_render16(
     Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids,
-    int64_t capacity, float* __restrict__ delta, uint8_t* ws) {
-  render16_body(p, row_coords, col_coords, ev, tile_ptr, ids, capacity, delta, ws,
+    int64_t capacity, float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
+    const uint32_t* __restrict__ colmask) {
+  render16_body(p, row_coords, col_coords, ev, tile_ptr, ids, capacity, delta, ws, rowmask, colmask,
                 (int64_t)blockIdx.x * (kTileThreads / 64) + wave_id());
 }
 
@@ -1389,6 +1523,13 @@ int make_problem(const gf_field_config* cfg, int64_t M, int64_t N, int64_t K, Pr
     p->q_hi = INFINITY;
   }
   p->normalize = cfg->normalize ? 1 : 0;
+  // Mask path (no emission kernel): 16x16 tiles, 1 <= K <= kMaskMaxK, a tile grid k_bin bins in
+  // LDS, and masks of a bounded total size.
+  p->W = 0;
+  if (p->tile_out == 16 && p->tile_in == 16 && K >= 1 && K <= kMaskMaxK && bin_counts_in_lds(C, K)) {
+    const int64_t W = (K + 31) / 32;
+    if ((R + C) * W <= kMaskMaxWords) p->W = (int32_t)W;
+  }
   return GF_OK;
 }
 
@@ -1449,7 +1590,8 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_batch(const uint8_t* __rest
   const BatchLayer& ly = reinterpret_cast<const BatchLayer*>(plan + h->layers_off)[blockIdx.x];
   const Problem p = ly.p;
   const FwdLayout L = ly.fl;
-  bin_body<true>(p, ly.mu, ly.chol_raw, ly.amp, ly.tile_ptr, ly.num_pairs, ly.fws, L);
+  __shared__ uint32_t mlds[kMaskLdsWords];
+  bin_body<true>(p, ly.mu, ly.chol_raw, ly.amp, ly.tile_ptr, ly.num_pairs, ly.fws, L, mlds);
 }
 
 __global__ __launch_bounds__(kEmitThreads) void k_emit_batch(const uint8_t* __restrict__ plan) {
@@ -1470,6 +1612,8 @@ __global__ __launch_bounds__(kTileThreads) void k_render16_batch(const uint8_t* 
   const Problem p = ly.p;
   render16_body(p, ly.row_coords, ly.col_coords, reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
                 ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws,
+                reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.rowmask),
+                reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.colmask),
                 ((int64_t)blockIdx.x - b0) * (kTileThreads / 64) + wave_id());
 }
 
@@ -1536,7 +1680,7 @@ size_t gf_forward_workspace_bytes(int64_t out_features, int64_t in_features, int
                                   const gf_field_config* cfg) {
   Problem p;
   if (make_problem(cfg, out_features, in_features, k, &p)) return 0;
-  return fwd_layout(k, (int64_t)p.R * p.C).total;
+  return fwd_layout(p).total;
 }
 
 size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, int64_t k,
@@ -1547,20 +1691,26 @@ size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, in
 }
 
 int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                   const float* mu, const float* chol_raw, int64_t* tile_ptr,
+                   const float* mu, const float* chol_raw, const float* amp, int64_t* tile_ptr,
                    int64_t* num_pairs_dev, int64_t* num_pairs_host, void* workspace,
                    size_t workspace_bytes, void* stream) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
-  const FwdLayout L = fwd_layout(k, (int64_t)p.R * p.C);
+  const FwdLayout L = fwd_layout(p);
   if (!workspace || workspace_bytes < L.total)
     return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
   if (!tile_ptr || !num_pairs_dev) return set_err(GF_E_INVALID_ARGUMENT, "tile_ptr / num_pairs_dev must not be NULL");
   if (k > 0 && (!mu || !chol_raw)) return set_err(GF_E_INVALID_ARGUMENT, "mu / chol_raw must not be NULL");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(k_bin, dim3(1), dim3(kBinThreads), 0, st, p, mu, chol_raw, tile_ptr,
-                     num_pairs_dev, reinterpret_cast<uint8_t*>(workspace), L);
+  if (p.W > 0) {
+    if (!amp) return set_err(GF_E_INVALID_ARGUMENT, "amp must not be NULL");
+    hipLaunchKernelGGL(k_bin_masks, dim3(1), dim3(kBinThreads), 0, st, p, mu, chol_raw, amp, tile_ptr,
+                       num_pairs_dev, reinterpret_cast<uint8_t*>(workspace), L);
+  } else {
+    hipLaunchKernelGGL(k_bin, dim3(1), dim3(kBinThreads), 0, st, p, mu, chol_raw, tile_ptr,
+                       num_pairs_dev, reinterpret_cast<uint8_t*>(workspace), L);
+  }
   GF_LAUNCH_CHECK("k_bin");
   if (num_pairs_host) {
     uint32_t status = 0;
@@ -1580,14 +1730,14 @@ int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
-  const FwdLayout L = fwd_layout(k, (int64_t)p.R * p.C);
+  const FwdLayout L = fwd_layout(p);
   if (!workspace || workspace_bytes < L.total)
     return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
   if (ids_capacity < 0 || (ids_capacity > 0 && !gaussian_ids_sorted))
     return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / ids_capacity invalid");
   if (!tile_ptr) return set_err(GF_E_INVALID_ARGUMENT, "tile_ptr must not be NULL");
   if (k > 0 && (!mu || !amp)) return set_err(GF_E_INVALID_ARGUMENT, "mu / amp must not be NULL");
-  if (k == 0) return GF_OK;
+  if (k == 0 || p.W > 0) return GF_OK;  // mask path: the render reads the ids from the masks
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t blocks = (k + kEmitThreads / 64 - 1) / (kEmitThreads / 64);
   hipLaunchKernelGGL(k_emit, dim3((unsigned)blocks), dim3(kEmitThreads), 0, st, p, mu, amp,
@@ -1605,7 +1755,7 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
   const int64_t T = (int64_t)p.R * p.C;
-  const FwdLayout L = fwd_layout(k, T);
+  const FwdLayout L = fwd_layout(p);
   if (!workspace || workspace_bytes < L.total)
     return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
   if (!row_coords || !col_coords || !tile_ptr || !delta)
@@ -1617,7 +1767,9 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
   const GaussEval* ev = reinterpret_cast<const GaussEval*>(ws + L.eval);
   if (fast16(p))
     hipLaunchKernelGGL(k_render16, dim3(wave_tile_grid(T)), dim3(kTileThreads), 0, st, p, row_coords,
-                       col_coords, ev, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws);
+                       col_coords, ev, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws,
+                       reinterpret_cast<const uint32_t*>(ws + L.rowmask),
+                       reinterpret_cast<const uint32_t*>(ws + L.colmask));
   else
     hipLaunchKernelGGL(k_render_any, dim3((unsigned)T), dim3(kTileThreads), 0, st, p, row_coords,
                        col_coords, ev, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws);
@@ -1646,7 +1798,7 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
   const GaussEval* ev = forward_workspace
-      ? reinterpret_cast<const GaussEval*>(reinterpret_cast<const uint8_t*>(forward_workspace) + fwd_layout(k, T).eval)
+      ? reinterpret_cast<const GaussEval*>(reinterpret_cast<const uint8_t*>(forward_workspace) + fwd_layout(p).eval)
       : nullptr;
   const dim3 grid((unsigned)T);
   if (tile_ptr_is_int64 && ids_is_int64)
@@ -1723,7 +1875,7 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
       return set_err(rc, "layer %zu: %s", i, why);
     }
     const int64_t T = (int64_t)ly.p.R * ly.p.C, K = in.k;
-    ly.fl = fwd_layout(K, T);
+    ly.fl = fwd_layout(ly.p);
     ly.bl = bwd_layout(K);
     if (!in.forward_workspace || in.forward_workspace_bytes < ly.fl.total)
       return set_err(GF_E_WORKSPACE, "layer %zu: forward workspace needs %zu bytes", i, ly.fl.total);
@@ -1758,7 +1910,7 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
     ly.finish_block0 = finish_blocks;
     tile_blocks += (T + kTileThreads / 64 - 1) / (kTileThreads / 64);
     const int64_t per_emit_block = (kEmitThreads / 64) * (64 / kEmitLanesBatch);
-    emit_blocks += (K + per_emit_block - 1) / per_emit_block;
+    if (ly.p.W == 0) emit_blocks += (K + per_emit_block - 1) / per_emit_block;  // emission path
     finish_blocks += (K + kTileThreads - 1) / kTileThreads;
   }
   if (tile_blocks >= INT32_MAX || emit_blocks >= INT32_MAX)

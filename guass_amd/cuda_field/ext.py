@@ -121,7 +121,7 @@ def forward_with_workspace(row_coords: Tensor, col_coords: Tensor, mu: Tensor, c
         tile_ptr = torch.empty(T + 1, dtype=torch.int64, device=dev)
         num_pairs = torch.empty(1, dtype=torch.int64, device=dev)
         P = ctypes.c_int64(0)
-        N.check(L.gf_forward_bin(ctypes.byref(cfg), M, Nf, K, N.ptr(mu), N.ptr(chol_raw),
+        N.check(L.gf_forward_bin(ctypes.byref(cfg), M, Nf, K, N.ptr(mu), N.ptr(chol_raw), N.ptr(amp),
                                  tile_ptr.data_ptr(), num_pairs.data_ptr(), ctypes.byref(P),
                                  ws.data_ptr(), ws_bytes, stream), "gaussian_field_forward (binning)")
         ids = torch.empty(P.value, dtype=torch.int64, device=dev)

@@ -51,9 +51,9 @@ class FieldPlan:
 
     # The three forward phases and two backward phases are exposed separately so that each
     # kernel can be timed on its own; forward() / backward() run them in order.
-    def bin(self, mu, chol_raw) -> None:
+    def bin(self, mu, chol_raw, amp) -> None:
         N.check(N.lib().gf_forward_bin(ctypes.byref(self.cfg), self.M, self.N, self.K, N.ptr(mu),
-                                       N.ptr(chol_raw), self.tile_ptr.data_ptr(),
+                                       N.ptr(chol_raw), N.ptr(amp), self.tile_ptr.data_ptr(),
                                        self.num_pairs.data_ptr(), None, self.fwd_ws.data_ptr(),
                                        self.fwd_ws_bytes, self._stream()), "gf_forward_bin")
 
@@ -76,7 +76,7 @@ class FieldPlan:
 
     def forward(self, row_coords, col_coords, mu, chol_raw, amp) -> torch.Tensor:
         """Bins and renders into ``self.delta`` (and ``tile_ptr`` / ``ids``); returns delta."""
-        self.bin(mu, chol_raw)
+        self.bin(mu, chol_raw, amp)
         self.emit(mu, amp)
         return self.render(row_coords, col_coords)
 

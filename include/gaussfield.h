@@ -70,7 +70,11 @@ size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, in
 
 /*
  * Forward phase 1 (binning): per-Gaussian geometry and sigma-box tile ranges, per-tile
- * Gaussian counts and their exclusive scan.
+ * Gaussian counts and their exclusive scan.  For 16x16 tiles with 1 <= k <= 8192 (the mask
+ * path) it also stores every Gaussian's evaluation constants and, per tile row and tile column,
+ * a bitmask of the Gaussians whose tile range covers it; the render then reads each tile's ids
+ * from those masks and gf_forward_emit has nothing to do.
+ *   amp             [K,1] fp32 (read on the mask path; may be NULL otherwise)
  *   tile_ptr        [T+1] int64 out: tile t owns gaussian_ids_sorted[tile_ptr[t] : tile_ptr[t+1]]
  *   num_pairs_dev   [1] int64 out: P = tile_ptr[T] = sum over Gaussians of tiles touched
  *   num_pairs_host  optional: if non-NULL the call synchronises `stream` and stores P here
@@ -78,16 +82,16 @@ size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, in
  * Replaces reference forward.cu:372-511 (preprocess_geometry + build_binning_state up to tile_ptr).
  */
 int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                   const float* mu, const float* chol_raw,
+                   const float* mu, const float* chol_raw, const float* amp,
                    int64_t* tile_ptr, int64_t* num_pairs_dev, int64_t* num_pairs_host,
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Forward phase 2 (emission): writes the (tile, gaussian) pairs into gaussian_ids_sorted,
- * each tile's ids inside its [tile_ptr[t], tile_ptr[t+1]) range (order fixed by phase 3),
- * and stores each Gaussian's evaluation constants in the workspace (from the covariance
- * gf_forward_bin left there, with amp applied).  Must follow gf_forward_bin on the same stream
- * with the same workspace, tile_ptr and mu.
+ * Forward phase 2 (emission; returns at once on the mask path): writes the (tile, gaussian)
+ * pairs into gaussian_ids_sorted, each tile's ids inside its [tile_ptr[t], tile_ptr[t+1]) range
+ * (order fixed by phase 3), and stores each Gaussian's evaluation constants in the workspace
+ * (from the covariance gf_forward_bin left there, with amp applied).  Must follow
+ * gf_forward_bin on the same stream with the same workspace, tile_ptr and mu.
  *   gaussian_ids_sorted [ids_capacity] int64 out; pairs beyond the capacity are dropped and
  *                   GF_STATUS_CAPACITY is set
  * Replaces reference forward.cu:465-482 (emit_tile_pairs_kernel + radix sort on the tile key).
@@ -100,8 +104,9 @@ int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in
 /*
  * Forward phase 3 (render): puts every tile's ids in canonical order (gaussian id ascending;
  * with tile-major ranges this is the (tile, gaussian) order of a stable sort) and renders
- * delta-W from the Gaussian constants gf_forward_emit stored.  Must follow gf_forward_emit on
- * the same stream with the same workspace and ids.
+ * delta-W from the Gaussian constants stored by gf_forward_emit (or, on the mask path,
+ * gf_forward_bin, in which case the render writes the ids itself from the masks).  Must follow
+ * gf_forward_emit on the same stream with the same workspace and ids.
  *   delta           [out_features*in_features] fp32 out, row-major; every element written
  * Replaces reference forward.cu:513-569 (tile_accumulate_kernel; delta needs no pre-zeroing).
  */

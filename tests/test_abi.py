@@ -87,7 +87,7 @@ def test_invalid_config_is_rejected_before_device_work(kw, msg):
     assert msg in lib.gf_last_error().decode()
     # the same check guards every entry point that takes a config
     rc = lib.gf_forward_bin(ctypes.byref(_cfg(**kw)), 64, 64, 4, None, None, None, None, None,
-                            None, 0, None)
+                            None, None, 0, None)
     assert rc == GF_E_INVALID_ARGUMENT and msg in lib.gf_last_error().decode()
 
 
@@ -95,7 +95,7 @@ def test_workspace_and_pointer_checks():
     lib = N.lib()
     cfg = _cfg()
     need = lib.gf_forward_workspace_bytes(64, 64, 4, ctypes.byref(cfg))
-    rc = lib.gf_forward_bin(ctypes.byref(cfg), 64, 64, 4, None, None, None, None, None, None,
+    rc = lib.gf_forward_bin(ctypes.byref(cfg), 64, 64, 4, None, None, None, None, None, None, None,
                             need - 1, None)
     assert rc == GF_E_WORKSPACE and "workspace" in lib.gf_last_error().decode()
     rc = lib.gf_tile_grid(0, 64, ctypes.byref(cfg), None, None)
