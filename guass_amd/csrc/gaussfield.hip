@@ -100,6 +100,7 @@ struct Problem {
   float q_lo, q_hi;  // clamp range of the scaled quadratic form q * kHalfLog2e
   int32_t normalize;
   int32_t W;  // words per tile-row / tile-column mask (0: the ids are emitted by k_emit)
+  int32_t S;  // backward accumulator stripes (power of two): tile t adds into stripe t % S
 };
 
 // Per-Gaussian constants of the tile kernels: with dx = x - mu0, dy = y - mu1,
@@ -147,17 +148,18 @@ FwdLayout fwd_layout(const Problem& p) {
   return L;
 }
 
-// Backward workspace: header + eight fp32 accumulators per Gaussian.  It must be zero before
-// the first backward; every backward leaves it zero again (k_bwd_finish clears what it reads),
-// so a workspace kept across calls is zeroed once.
+// Backward workspace: header + S stripes of eight fp32 accumulators per Gaussian
+// (acc[g][s][8]: the tiles of a Gaussian spread their atomics over S addresses per moment).
+// It must be zero before the first backward; every backward leaves it zero again
+// (k_bwd_finish clears what it reads), so a workspace kept across calls is zeroed once.
 struct BwdLayout {
   size_t acc, total;
 };
-BwdLayout bwd_layout(int64_t K) {
+BwdLayout bwd_layout(const Problem& p) {
   BwdLayout L;
   size_t o = sizeof(WsHeader);
   L.acc = o;
-  o = align256(o + sizeof(float) * 8 * (size_t)K);
+  o = align256(o + sizeof(float) * 8 * (size_t)p.S * (size_t)p.K);
   L.total = o;
   return L;
 }
@@ -1318,7 +1320,7 @@ __device__ __forceinline__ void bwd16_body(
       if (g >= 0 && row >= 10) {
         const int k = row - 10;
         const float val = k == 0 ? v0 : k == 1 ? v1 : k == 2 ? v2 : k == 3 ? v3 : k == 4 ? v4 : m[5];
-        unsafeAtomicAdd(acc + 8 * (int64_t)g + k, val);
+        unsafeAtomicAdd(acc + 8 * ((int64_t)g * p.S + (t & (p.S - 1))) + k, val);
       }
     }
   }
@@ -1398,7 +1400,7 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
         float tot = 0.f;
 #pragma unroll
         for (int q = 0; q < kTileThreads / 64; ++q) tot += red[q][threadIdx.x];
-        unsafeAtomicAdd(acc + 8 * (int64_t)g + threadIdx.x, tot);
+        unsafeAtomicAdd(acc + 8 * ((int64_t)g * p.S + (t & (p.S - 1))) + threadIdx.x, tot);
       }
       __syncthreads();
     }
@@ -1411,22 +1413,40 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
 //   G = dL/dcov = -A (dL/dA) A + dL/ddet det A;  dL/dL = (G + G^T) L;  softplus' on the diagonal.
 // A is the inverse of the fp32 covariance; the algebra follows torch's autograd of the
 // reference CPU path (linalg.inv, linalg.det, L L^T, softplus).
-// The chain rule for Gaussian g of one field by one thread.
+// The chain rule for the Gaussians of one field, S = p.S threads per Gaussian: thread idx
+// takes stripe idx % S of Gaussian idx / S (loads it and clears it), the S threads (adjacent
+// lanes of one wave) sum the six moments with xor shuffles, and the first applies the chain
+// rule.  Every lane of the wave must call it (the shuffles).
 __device__ __forceinline__ void finish_body(
     const Problem& p, const float* __restrict__ chol_raw, const float* __restrict__ amp,
     float* __restrict__ d_mu, float* __restrict__ d_chol_raw, float* __restrict__ d_amp, uint8_t* ws,
-    const BwdLayout& L, int64_t g) {
+    const BwdLayout& L, int64_t idx) {
   float* acc = reinterpret_cast<float*>(ws + L.acc);
-  if (g >= p.K) return;
-  const float4 a0 = reinterpret_cast<const float4*>(acc)[2 * g + 0];
-  const float4 a1 = reinterpret_cast<const float4*>(acc)[2 * g + 1];
-  reinterpret_cast<float4*>(acc)[2 * g + 0] = make_float4(0.f, 0.f, 0.f, 0.f);
-  reinterpret_cast<float4*>(acc)[2 * g + 1] = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int64_t g = idx / p.S;
+  const int32_t st = (int32_t)(idx & (p.S - 1));
+  float m[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (g < p.K) {
+    float4* ag = reinterpret_cast<float4*>(acc) + 2 * (g * p.S + st);
+    const float4 b0 = ag[0], b1 = ag[1];
+    ag[0] = make_float4(0.f, 0.f, 0.f, 0.f);
+    ag[1] = make_float4(0.f, 0.f, 0.f, 0.f);
+    m[0] = b0.x;
+    m[1] = b0.y;
+    m[2] = b0.z;
+    m[3] = b0.w;
+    m[4] = b1.x;
+    m[5] = b1.y;
+  }
+  for (int32_t o = 1; o < p.S; o <<= 1) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) m[k] += __shfl_xor(m[k], o, 64);
+  }
+  if (g >= p.K || st != 0) return;
   const float raw11 = chol_raw[3 * g + 0], raw21 = chol_raw[3 * g + 1], raw22 = chol_raw[3 * g + 2];
   const GfChol Lc = gf_activate_cholesky(raw11, raw21, raw22);
   const GfCov cov = gf_cov_from_chol(Lc);
   const GfRenderGeom rg = gf_render_geom(cov, p.normalize);
-  const double S0 = a0.x, S1 = a0.y, S2 = a0.z, S3 = a0.w, S4 = a1.x, S5 = a1.y;
+  const double S0 = m[0], S1 = m[1], S2 = m[2], S3 = m[3], S4 = m[4], S5 = m[5];
   const double a = (double)amp[g];
   const double nrm = (double)rg.norm;
   const double an = a * nrm;
@@ -1491,6 +1511,14 @@ __global__ __launch_bounds__(256) void k_selftest_softplus(unsigned long long* o
 // ------------------------------------------------------------------------------------------
 // Host helpers.
 
+// Accumulator stripes of the backward: tile grids large enough to hold Gaussians that touch
+// thousands of tiles (whose atomics on one address serialise) get 4 or 16 stripes; the finish
+// then reads and clears K * S * 32 bytes (one thread per stripe).
+int32_t backward_stripes(int64_t K, int64_t T) {
+  (void)K;
+  return T >= 16384 ? 16 : (T >= 8192 ? 4 : 1);
+}
+
 int make_problem(const gf_field_config* cfg, int64_t M, int64_t N, int64_t K, Problem* p) {
   if (!cfg) return set_err(GF_E_INVALID_ARGUMENT, "config must not be NULL");
   if (cfg->tile_out <= 0) return set_err(GF_E_INVALID_ARGUMENT, "tile_out must be positive");
@@ -1523,6 +1551,7 @@ int make_problem(const gf_field_config* cfg, int64_t M, int64_t N, int64_t K, Pr
     p->q_hi = INFINITY;
   }
   p->normalize = cfg->normalize ? 1 : 0;
+  p->S = backward_stripes(K, R * C);
   // Mask path (no emission kernel): 16x16 tiles, 1 <= K <= kMaskMaxK, a tile grid k_bin bins in
   // LDS, and masks of a bounded total size.
   p->W = 0;
@@ -1687,7 +1716,7 @@ size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, in
                                    const gf_field_config* cfg) {
   Problem p;
   if (make_problem(cfg, out_features, in_features, k, &p)) return 0;
-  return bwd_layout(k).total;
+  return bwd_layout(p).total;
 }
 
 int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
@@ -1787,7 +1816,7 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
   const int64_t T = (int64_t)p.R * p.C;
-  const BwdLayout L = bwd_layout(k);
+  const BwdLayout L = bwd_layout(p);
   if (!workspace || workspace_bytes < L.total)
     return set_err(GF_E_WORKSPACE, "backward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
   if (num_pairs < 0) return set_err(GF_E_INVALID_ARGUMENT, "num_pairs must be non-negative");
@@ -1819,14 +1848,14 @@ int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
-  const BwdLayout L = bwd_layout(k);
+  const BwdLayout L = bwd_layout(p);
   if (!workspace || workspace_bytes < L.total)
     return set_err(GF_E_WORKSPACE, "backward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
   if (k == 0) return GF_OK;
   if (!chol_raw || !amp || !d_mu || !d_chol_raw || !d_amp)
     return set_err(GF_E_INVALID_ARGUMENT, "parameter / gradient pointers must not be NULL");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const unsigned blocks = (unsigned)((k + kTileThreads - 1) / kTileThreads);
+  const unsigned blocks = (unsigned)((k * p.S + kTileThreads - 1) / kTileThreads);
   hipLaunchKernelGGL(k_bwd_finish, dim3(blocks), dim3(kTileThreads), 0, st, p, chol_raw, amp, d_mu,
                      d_chol_raw, d_amp, reinterpret_cast<uint8_t*>(workspace), L);
   GF_LAUNCH_CHECK("k_bwd_finish");
@@ -1876,7 +1905,7 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
     }
     const int64_t T = (int64_t)ly.p.R * ly.p.C, K = in.k;
     ly.fl = fwd_layout(ly.p);
-    ly.bl = bwd_layout(K);
+    ly.bl = bwd_layout(ly.p);
     if (!in.forward_workspace || in.forward_workspace_bytes < ly.fl.total)
       return set_err(GF_E_WORKSPACE, "layer %zu: forward workspace needs %zu bytes", i, ly.fl.total);
     if (!in.row_coords || !in.col_coords || !in.delta || !in.tile_ptr || !in.num_pairs)
@@ -1911,7 +1940,7 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
     tile_blocks += (T + kTileThreads / 64 - 1) / (kTileThreads / 64);
     const int64_t per_emit_block = (kEmitThreads / 64) * (64 / kEmitLanesBatch);
     if (ly.p.W == 0) emit_blocks += (K + per_emit_block - 1) / per_emit_block;  // emission path
-    finish_blocks += (K + kTileThreads - 1) / kTileThreads;
+    finish_blocks += (K * ly.p.S + kTileThreads - 1) / kTileThreads;
   }
   if (tile_blocks >= INT32_MAX || emit_blocks >= INT32_MAX)
     return set_err(GF_E_INVALID_ARGUMENT, "batch too large for one launch");

@@ -281,6 +281,28 @@ def test_plan_sync_free_and_capacity(device):
     assert small.status() & _native.GF_STATUS_CAPACITY
 
 
+def test_backward_stripes(device):
+    """Tile grids of >= 8192 tiles spread each Gaussian's accumulators over 4 stripes (>= 16384:
+    16): a 1280x1792 field (8960 tiles) against the oracle, alone and as a batch layer next to a
+    one-stripe layer (the batched finish maps K * stripes threads per layer)."""
+    from guass_amd.ops import FieldBatchPlan
+
+    p = wl.make_problem("stripes4_1280x1792_k512", 1280, 1792, 512, math.log(8.0), 0.6, 21)
+    g, r = check(p, device)
+    small = wl.cfg2(22)
+    singles = [run_gpu(small, device), g]
+    batch = FieldBatchPlan([small.to(device), p.to(device)], device,
+                           capacities=[int(sg[1][-1]) for sg in singles])
+    batch.forward()
+    batch.backward()
+    torch.cuda.synchronize()
+    assert batch.status() == [0, 0]
+    for i, (pl, sg) in enumerate(zip(batch.plans, singles)):
+        assert torch.equal(pl.delta, sg[0]), f"layer {i}: delta"
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), sg[3:]):
+            grad_close(a, b, f"layer {i} {name}", rtol=1e-5)
+
+
 def test_deterministic_forward(device):
     p = wl.cfg3(1)
     a = run_gpu(p, device)
