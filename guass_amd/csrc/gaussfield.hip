@@ -49,6 +49,8 @@ constexpr int kEmitThreads = 256;
 constexpr int kLdsDiffWords = 12288;  // 48 KiB row-difference band in k_bin
 constexpr int kBinMaxBandRows = 1024; // row totals kept in LDS per band in k_bin
 constexpr int kMaskLdsWords = 16384;  // 64 KiB band of tile-row / tile-column masks in k_bin
+constexpr int kLongSpan = 32;         // k_bin: rectangles spanning more rows / columns than this
+constexpr int kLongMax = 256;         //   go to a list of up to kLongMax spread over the workgroup
 constexpr int64_t kMaskMaxK = 8192;   // mask path up to this many Gaussians (256 words a mask)
 constexpr int64_t kMaskMaxWords = int64_t(1) << 24;  // and up to (R + C) * W mask words
 
@@ -477,6 +479,11 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
   __shared__ int32_t rowdiff[kBinMaxBandRows + 1];
   __shared__ int64_t scan_lds[kBinThreads / 64 + 1];
   __shared__ unsigned long long pairs_lds;
+  // rectangles with long row / column spans: Gaussian, first row / column in the band, span,
+  // columns (row spans), and the prefix of the spans
+  __shared__ int32_t long_g[kLongMax], long_lo[kLongMax], long_n[kLongMax];
+  __shared__ int32_t long_c0[kLongMax], long_c1[kLongMax], long_off[kLongMax + 1];
+  __shared__ uint32_t nlong;
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   int4* rect = reinterpret_cast<int4*>(ws + L.rect);
   float4* covs = reinterpret_cast<float4*>(ws + L.cov);
@@ -489,6 +496,7 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
   if (threadIdx.x == 0) {
     hdr->status = 0u;
     pairs_lds = 0ull;
+    nlong = 0u;
   }
 
   // Per-tile counts go through LDS, band by band of whole tile rows, when the grid allows it.
@@ -514,21 +522,77 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
     }
   };
   if (lds_path) clear_band(min(band_rows, p.R));
+  // The nl listed long spans, item by item (entry e covers long_n[e] rows / columns from
+  // long_lo[e]): wave 0 scans the spans, then thread t takes a contiguous run of the items.
+  // Every thread must call it (barriers); it ends with a barrier.
+  auto run_long = [&](int32_t nl, auto&& item) {
+    if (wid == 0) {
+      int32_t carry = 0;
+      for (int32_t e0 = 0; e0 < nl; e0 += 64) {
+        const int32_t e = e0 + lane;
+        const int32_t v = e < nl ? long_n[e] : 0;
+        const int32_t inc = dpp_scan_i32(v);
+        if (e < nl) long_off[e] = carry + inc - v;
+        carry += __builtin_amdgcn_readlane(inc, 63);
+      }
+      if (lane == 0) long_off[nl] = carry;
+    }
+    __syncthreads();
+    const int32_t total = long_off[nl];
+    const int32_t per = (total + kBinThreads - 1) / kBinThreads;
+    int32_t i = (int32_t)threadIdx.x * per;
+    const int32_t iend = min(i + per, total);
+    if (i < iend) {
+      int32_t lo = 0, hi = nl;  // long_off[lo] <= i < long_off[hi]
+      while (hi - lo > 1) {
+        const int32_t mid = (lo + hi) >> 1;
+        if (long_off[mid] <= i) lo = mid;
+        else hi = mid;
+      }
+      int32_t e = lo, k = i - long_off[lo];
+      for (; i < iend; ++i, ++k) {
+        while (k >= long_n[e]) {  // spans are >= 1
+          k -= long_n[e];
+          ++e;
+        }
+        item(e, long_lo[e] + k);
+      }
+    }
+    __syncthreads();
+  };
+  // Appends a long span to the list; false when the list is full (the caller loops itself).
+  auto push_long = [&](int64_t g, int32_t lo, int32_t n, int32_t c0, int32_t c1) -> bool {
+    const uint32_t slot = atomicAdd(&nlong, 1u);
+    if (slot >= (uint32_t)kLongMax) return false;
+    long_g[slot] = (int32_t)g;
+    long_lo[slot] = lo;
+    long_n[slot] = n;
+    long_c0[slot] = c0;
+    long_c1[slot] = c1;
+    return true;
+  };
 
   // A: tile rectangles, fp32 covariances and pairs (tiles touched); the first
   // kBinRectRegs * kBinThreads Gaussians keep their rectangle in registers.
   int4 myrect[kBinRectRegs];
   int64_t my_pairs = 0;
-  auto prep = [&](int64_t g) -> int4 {
-    const GfChol Lc = gf_activate_cholesky(chol_raw[3 * g + 0], chol_raw[3 * g + 1], chol_raw[3 * g + 2]);
+  struct PrepIn {
+    float mu0, mu1, r11, r21, r22, amp;
+  };
+  auto load_in = [&](int64_t g) -> PrepIn {
+    return PrepIn{mu[2 * g + 0], mu[2 * g + 1], chol_raw[3 * g + 0], chol_raw[3 * g + 1],
+                  chol_raw[3 * g + 2], kEval ? amp[g] : 0.0f};
+  };
+  auto prep = [&](int64_t g, const PrepIn& in) -> int4 {
+    const GfChol Lc = gf_activate_cholesky(in.r11, in.r21, in.r22);
     const GfCov c = gf_cov_from_chol(Lc);
     int32_t touched;
-    const int4 r = bin_rect(p, mu[2 * g + 0], mu[2 * g + 1], c, &touched);
+    const int4 r = bin_rect(p, in.mu0, in.mu1, c, &touched);
     rect[g] = r;
     covs[g] = make_float4(c.s00, c.s01, c.s11, 0.0f);
     my_pairs += touched;
     if (kEval) {
-      GaussEval v = eval_from_cov(p, mu[2 * g + 0], mu[2 * g + 1], c, amp[g]);
+      GaussEval v = eval_from_cov(p, in.mu0, in.mu1, c, in.amp);
       v.gid = (int32_t)g;
       store_eval(reinterpret_cast<GaussEval*>(ws + L.eval), g, v);
     }
@@ -538,9 +602,10 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
   for (int i = 0; i < kBinRectRegs; ++i) {
     const int64_t g = threadIdx.x + (int64_t)i * kBinThreads;
     myrect[i] = make_int4(1, 0, 1, 0);  // empty
-    if (g < K) myrect[i] = prep(g);
+    if (g < K) myrect[i] = prep(g, load_in(g));
   }
-  for (int64_t g = threadIdx.x + (int64_t)kBinRectRegs * kBinThreads; g < K; g += kBinThreads) prep(g);
+  for (int64_t g = threadIdx.x + (int64_t)kBinRectRegs * kBinThreads; g < K; g += kBinThreads)
+    prep(g, load_in(g));
   // B: P = total pairs: wave sums, one LDS atomic per wave after the barrier that orders them
   // behind the counter's initialisation; read by thread 0 after later barriers.
   const int64_t wave_pairs = readlane_i64(wave_inclusive_scan(my_pairs), 63);
@@ -563,26 +628,31 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
         clear_band(nb);
         __syncthreads();
       }
+      auto row_item = [&](int32_t row, int32_t c0, int32_t c1, int64_t g) {
+        int32_t* d = lds + (row - b0) * Cp;
+        atomicAdd(d + c0, 1);
+        if (c1 + 1 < C) atomicAdd(d + c1 + 1, -1);
+        if (W > 0) atomicOr(mlds + (row - b0) * Wp + (int32_t)(g >> 5), 1u << (g & 31));
+      };
       auto diff = [&](const int4 r, int64_t g) {
         const int32_t rlo = max(r.x, b0), rhi = min(r.y, b0 + nb - 1);
         if (rlo > rhi) return;
-        const uint32_t bit = 1u << (g & 31);
-        const int32_t word = (int32_t)(g >> 5);
-        for (int32_t row = rlo; row <= rhi; ++row) {
-          int32_t* d = lds + (row - b0) * Cp;
-          atomicAdd(d + r.z, 1);
-          if (r.w + 1 < C) atomicAdd(d + r.w + 1, -1);
-          if (W > 0) atomicOr(mlds + (row - b0) * Wp + word, bit);
-        }
         const int32_t w = r.w - r.z + 1;
         atomicAdd(rowdiff + (rlo - b0), w);
         atomicAdd(rowdiff + (rhi + 1 - b0), -w);  // index <= nb
+        if (rhi - rlo >= kLongSpan && push_long(g, rlo, rhi - rlo + 1, r.z, r.w)) return;
+        for (int32_t row = rlo; row <= rhi; ++row) row_item(row, r.z, r.w, g);
       };
 #pragma unroll
       for (int i = 0; i < kBinRectRegs; ++i) diff(myrect[i], threadIdx.x + (int64_t)i * kBinThreads);
       for (int64_t g = threadIdx.x + (int64_t)kBinRectRegs * kBinThreads; g < K; g += kBinThreads)
         diff(rect[g], g);
       __syncthreads();
+      const int32_t nl = (int32_t)min(nlong, (uint32_t)kLongMax);
+      if (nl > 0) {
+        run_long(nl, [&](int32_t e, int32_t row) { row_item(row, long_c0[e], long_c1[e], long_g[e]); });
+        if (threadIdx.x == 0) nlong = 0u;  // every thread read it before run_long's barriers
+      }
       if (wid == 0) {
         int64_t carry = 0;
         int32_t carry_t = 0;
@@ -616,17 +686,25 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
         const int32_t nc = min(C - cb0, band_cols);
         for (int32_t i = threadIdx.x; i < nc * Wp; i += kBinThreads) mlds[i] = 0u;
         __syncthreads();
+        auto col_item = [&](int32_t c, int64_t g) {
+          atomicOr(mlds + (c - cb0) * Wp + (int32_t)(g >> 5), 1u << (g & 31));
+        };
         auto colset = [&](const int4 r, int64_t g) {
           const int32_t lo = max(r.z, cb0), hi = min(r.w, cb0 + nc - 1);
-          const uint32_t bit = 1u << (g & 31);
-          uint32_t* m = mlds + (g >> 5);
-          for (int32_t c = lo; c <= hi; ++c) atomicOr(m + (c - cb0) * Wp, bit);
+          if (lo > hi) return;
+          if (hi - lo >= kLongSpan && push_long(g, lo, hi - lo + 1, 0, 0)) return;
+          for (int32_t c = lo; c <= hi; ++c) col_item(c, g);
         };
 #pragma unroll
         for (int i = 0; i < kBinRectRegs; ++i) colset(myrect[i], threadIdx.x + (int64_t)i * kBinThreads);
         for (int64_t g = threadIdx.x + (int64_t)kBinRectRegs * kBinThreads; g < K; g += kBinThreads)
           colset(rect[g], g);
         __syncthreads();
+        const int32_t nl = (int32_t)min(nlong, (uint32_t)kLongMax);
+        if (nl > 0) {
+          run_long(nl, [&](int32_t e, int32_t c) { col_item(c, long_g[e]); });
+          if (threadIdx.x == 0) nlong = 0u;
+        }
         copy_masks(colmask + (int64_t)cb0 * W, nc, threadIdx.x, kBinThreads);
         __syncthreads();
       }
