@@ -10,6 +10,10 @@ graph.  Workloads:
                                 as one batch (guass_amd.ops.FieldBatchPlan: five launches per
                                 step for all layers)
   cfg1, cfg2, cfg5, cfg5c       single fields as cfg3
+  cfg4-model                    the cfg4 layers as GaussianLinear modules through autograd: one
+                                training step's fields via GaussianFieldBatch.render() (one
+                                batched launch per phase) against every layer rendering its own
+                                through the drop-in gaussian_field_train (eager, both)
 All with 16x16 tiles, 3 sigma, clamp 80.
 
 Prints one JSON line (metric contract of the driver) with two extra objects:
@@ -45,7 +49,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "cfg5c"])
+    ap.add_argument("--config", default="cfg3",
+                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "cfg5c", "cfg4-model"])
     ap.add_argument("--layers", type=int, default=None, help="cfg4: first N of the 128 layers")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of graph replay")
@@ -145,6 +150,73 @@ def cpu_baseline(problems, reps: int, note: str) -> dict:
                       f"{med:.2f} s each"}
 
 
+def model_bench(args) -> int:
+    """cfg4-model: one training step's Gaussian fields of the 128 SD1.5 attention layers through
+    the layer API and autograd (dL/d(delta-W) fed to autograd directly, no model around them)."""
+    import torch
+
+    from guass_amd import workloads as wl
+    from guass_amd.cuda_field.runtime import gaussian_field_train
+    from guass_amd.layers import GaussianAdapterConfig, GaussianFieldBatch, GaussianLinear
+
+    dev = torch.device("cuda:0")
+    probs = wl.cfg4(args.seed, layers=args.layers)
+    layers = []
+    for p in probs:
+        cfg = GaussianAdapterConfig(init_num_gaussians=p.k, tile_out=16, tile_in=16)
+        ly = GaussianLinear(p.in_features, p.out_features, adapter_config=cfg, device=dev)
+        with torch.no_grad():
+            ly.row_coords.copy_(p.row_coords.to(dev))
+            ly.col_coords.copy_(p.col_coords.to(dev))
+        ly.load_adapter_state({"mu_raw": torch.atanh(p.mu.clamp(-0.999999, 0.999999)),
+                               "chol_raw": p.chol_raw, "amp": p.amp})
+        layers.append(ly)
+    grads = [p.grad.to(dev).reshape(p.out_features, p.in_features) for p in probs]
+    params = [t for ly in layers for t in (ly.mu_raw, ly.chol_raw, ly.amp)]
+    fb = GaussianFieldBatch(layers)
+
+    def batched():
+        torch.autograd.backward(fb.render(), grads)
+
+    def per_layer():
+        deltas = [gaussian_field_train(row_coords=ly.row_coords, col_coords=ly.col_coords,
+                                       mu=ly.materialize_mu(), chol_raw=ly.chol_raw, amp=ly.amp,
+                                       tile_out=16, tile_in=16, sigma_multiplier=3.0, normalize=False,
+                                       clamp_quad=80.0).reshape(ly.out_features, ly.in_features)
+                  for ly in layers]
+        torch.autograd.backward(deltas, grads)
+
+    def timed(fn, steps: int, warmup: int) -> float:
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            for t in params:
+                t.grad = None
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
+    t_batch = timed(batched, args.steps, args.warmup)
+    t_single = timed(per_layer, max(1, args.steps // 5), max(1, args.warmup // 5))
+    elements = float(sum(p.out_features * p.in_features for p in probs))
+    out = {
+        "metric": "ΔW elements/sec fwd+bwd of the SD1.5 attention layers through the layer API",
+        "value": elements / t_batch, "unit": "ΔW elements/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": t_batch * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded Gaussian fields, BASELINE.json cfg4 distribution)",
+        "config": {"workload": f"cfg4 x{len(probs)} GaussianLinear layers, GaussianFieldBatch.render + "
+                               "autograd backward (eager)", "layers": len(probs),
+                   "sum_out_x_in": int(elements), "k_per_layer": 1024},
+        "per_layer_ms_per_step": t_single * 1e3,
+        "speedup_vs_per_layer": t_single / t_batch,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -152,6 +224,8 @@ def main() -> int:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
               "this build has no multi-GPU path to time.", file=sys.stderr)
         return 2
+    if args.config == "cfg4-model":
+        return model_bench(args)
 
     import torch
 

@@ -30,6 +30,7 @@ EXPORTED = (
     "gf_backward_workspace_bytes", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
     "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
     "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward",
+    "gf_batch_set_grads", "gf_batch_read",
 )
 
 GF_PHASE_BIN, GF_PHASE_EMIT, GF_PHASE_RENDER = 0x1, 0x2, 0x4
@@ -70,6 +71,7 @@ class GfBatchInfo(ctypes.Structure):
     _fields_ = [
         ("n_layers", c_int32), ("has_backward", c_int32), ("tile_blocks", c_int64),
         ("emit_blocks", c_int64), ("finish_blocks", c_int64), ("plan_bytes", c_size_t),
+        ("backward_buffers", c_int32), ("reserved", c_int32),
     ]
 
 
@@ -115,10 +117,13 @@ def lib() -> ctypes.CDLL:
     L.gf_batch_plan.argtypes = [_CFG, POINTER(GfLayer), c_int32, _P, c_size_t, POINTER(GfBatchInfo), _P]
     L.gf_batch_forward.argtypes = [_P, POINTER(GfBatchInfo), c_uint32, _P]
     L.gf_batch_backward.argtypes = [_P, POINTER(GfBatchInfo), c_uint32, _P]
+    L.gf_batch_set_grads.argtypes = [_P, POINTER(GfBatchInfo), POINTER(c_void_p), _P]
+    L.gf_batch_read.argtypes = [_P, POINTER(GfBatchInfo), c_int32, POINTER(c_uint32), POINTER(c_int64), _P]
     L.gf_selftest_softplus.argtypes = [POINTER(c_uint64), _P]
     for name in ("gf_tile_grid", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
                  "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
-                 "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward"):
+                 "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward",
+                 "gf_batch_set_grads", "gf_batch_read"):
         getattr(L, name).restype = c_int
     _LIB = L
     return L

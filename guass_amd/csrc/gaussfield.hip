@@ -1663,7 +1663,6 @@ struct BatchLayer {
   const float* mu;
   const float* chol_raw;
   const float* amp;
-  const float* grad;
   float* delta;
   int64_t* tile_ptr;
   int64_t* num_pairs;
@@ -1677,18 +1676,44 @@ struct BatchLayer {
   int64_t tile_block0, emit_block0, finish_block0;
 };
 
+// Plan regions after the header: layers, the tile / emission / finish block maps, the
+// dL/d(delta) pointer of every layer (rewritten by gf_batch_set_grads) and a read-back area
+// (per layer: status bits, pair count).
 struct BatchHeader {
   int64_t n;
   int64_t tile_blocks, emit_blocks, finish_blocks;
-  int64_t layers_off, tile_map_off, emit_map_off, finish_map_off;
+  int64_t layers_off, tile_map_off, emit_map_off, finish_map_off, grad_table_off, readback_off, total;
 };
 
+struct BatchReadback {
+  uint32_t status;
+  uint32_t pad;
+  int64_t pairs;
+};
+
+BatchHeader batch_header(int64_t n, int64_t tile_blocks, int64_t emit_blocks, int64_t finish_blocks) {
+  BatchHeader h{};
+  h.n = n;
+  h.tile_blocks = tile_blocks;
+  h.emit_blocks = emit_blocks;
+  h.finish_blocks = finish_blocks;
+  h.layers_off = (int64_t)align256(sizeof(BatchHeader));
+  h.tile_map_off = (int64_t)align256(h.layers_off + sizeof(BatchLayer) * n);
+  h.emit_map_off = (int64_t)align256(h.tile_map_off + sizeof(int32_t) * tile_blocks);
+  h.finish_map_off = (int64_t)align256(h.emit_map_off + sizeof(int32_t) * emit_blocks);
+  h.grad_table_off = (int64_t)align256(h.finish_map_off + sizeof(int32_t) * finish_blocks);
+  h.readback_off = (int64_t)align256(h.grad_table_off + sizeof(void*) * n);
+  h.total = (int64_t)align256(h.readback_off + sizeof(BatchReadback) * n);
+  return h;
+}
+
 __device__ inline const BatchLayer& batch_layer(const uint8_t* plan, int64_t map_off, int64_t* block0_sel,
-                                                int which) {
+                                                int which, int32_t* index = nullptr) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
   const int32_t l = reinterpret_cast<const int32_t*>(plan + map_off)[blockIdx.x];
   const BatchLayer& ly = reinterpret_cast<const BatchLayer*>(plan + h->layers_off)[l];
   *block0_sel = which == 0 ? ly.tile_block0 : which == 1 ? ly.emit_block0 : ly.finish_block0;
+  if (index) *index = l;
   return ly;
 }
 
@@ -1727,15 +1752,50 @@ __global__ __launch_bounds__(kTileThreads) void k_render16_batch(const uint8_t* 
 __global__ __launch_bounds__(kTileThreads) void k_bwd16_batch(const uint8_t* __restrict__ plan) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
   int64_t b0;
-  const BatchLayer& ly = batch_layer(plan, h->tile_map_off, &b0, 0);
+  int32_t l;
+  const BatchLayer& ly = batch_layer(plan, h->tile_map_off, &b0, 0, &l);
   const Problem p = ly.p;
   const BwdLayout L = ly.bl;
   const int64_t T = (int64_t)p.R * p.C;
   const int64_t P = ly.tile_ptr[T];  // pairs beyond the id capacity were never emitted
-  bwd16_body<int64_t, int64_t>(p, ly.grad, ly.row_coords, ly.col_coords, ly.mu, ly.chol_raw,
+  const float* grad = reinterpret_cast<const float* const*>(plan + h->grad_table_off)[l];
+  bwd16_body<int64_t, int64_t>(p, grad, ly.row_coords, ly.col_coords, ly.mu, ly.chol_raw,
                                reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
                                ly.tile_ptr, ly.ids, P < ly.capacity ? P : ly.capacity, ly.bws, L,
                                ((int64_t)blockIdx.x - b0) * (kTileThreads / 64) + wave_id());
+}
+
+// dL/d(delta) pointers of layers base .. base + count - 1 (count <= kPtrChunk), passed by value.
+constexpr int kPtrChunk = 256;
+struct PtrChunk {
+  const float* p[kPtrChunk];
+};
+
+__global__ __launch_bounds__(kPtrChunk) void k_batch_set_grads(uint8_t* plan, PtrChunk chunk, int32_t base,
+                                                               int32_t count) {
+  const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
+  if ((int32_t)threadIdx.x < count)
+    reinterpret_cast<const float**>(plan + h->grad_table_off)[base + threadIdx.x] = chunk.p[threadIdx.x];
+}
+
+// Per layer: forward | backward status bits and the pair count, into the read-back area;
+// clear != 0 resets the status words.
+__global__ __launch_bounds__(256) void k_batch_read(uint8_t* plan, int32_t clear) {
+  const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
+  const int64_t l = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (l >= h->n) return;
+  const BatchLayer& ly = reinterpret_cast<const BatchLayer*>(plan + h->layers_off)[l];
+  WsHeader* fh = reinterpret_cast<WsHeader*>(ly.fws);
+  WsHeader* bh = reinterpret_cast<WsHeader*>(ly.bws);
+  BatchReadback r;
+  r.status = fh->status | (bh ? bh->status : 0u);
+  r.pad = 0u;
+  r.pairs = *ly.num_pairs;
+  reinterpret_cast<BatchReadback*>(plan + h->readback_off)[l] = r;
+  if (clear) {
+    fh->status = 0u;
+    if (bh) bh->status = 0u;
+  }
 }
 
 __global__ __launch_bounds__(kTileThreads) void k_finish_batch(const uint8_t* __restrict__ plan) {
@@ -1967,11 +2027,9 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
                    (long long)cfg->tile_out, (long long)cfg->tile_in);
   const size_t n = (size_t)n_layers;
   BatchHeader h{};
-  h.n = n_layers;
-  h.layers_off = (int64_t)align256(sizeof(BatchHeader));
   std::vector<BatchLayer> ls(n);
   int64_t tile_blocks = 0, emit_blocks = 0, finish_blocks = 0;
-  bool has_backward = true;
+  bool backward_buffers = true, grads_set = true;
   for (size_t i = 0; i < n; ++i) {
     const gf_layer& in = layers[i];
     BatchLayer& ly = ls[i];
@@ -1992,16 +2050,15 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
       return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: mu / chol_raw / amp must not be NULL", i);
     if (in.ids_capacity < 0 || (in.ids_capacity > 0 && !in.gaussian_ids))
       return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: gaussian_ids / ids_capacity invalid", i);
-    const bool bwd = in.grad_delta && in.backward_workspace &&
-                     in.backward_workspace_bytes >= ly.bl.total &&
-                     (K == 0 || (in.d_mu && in.d_chol_raw && in.d_amp));
-    has_backward = has_backward && bwd;
+    const bool bufs = in.backward_workspace && in.backward_workspace_bytes >= ly.bl.total &&
+                      (K == 0 || (in.d_mu && in.d_chol_raw && in.d_amp));
+    backward_buffers = backward_buffers && bufs;
+    grads_set = grads_set && in.grad_delta;
     ly.row_coords = in.row_coords;
     ly.col_coords = in.col_coords;
     ly.mu = in.mu;
     ly.chol_raw = in.chol_raw;
     ly.amp = in.amp;
-    ly.grad = in.grad_delta;
     ly.delta = in.delta;
     ly.tile_ptr = in.tile_ptr;
     ly.num_pairs = in.num_pairs;
@@ -2022,15 +2079,11 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
   }
   if (tile_blocks >= INT32_MAX || emit_blocks >= INT32_MAX)
     return set_err(GF_E_INVALID_ARGUMENT, "batch too large for one launch");
-  h.tile_blocks = tile_blocks;
-  h.emit_blocks = emit_blocks;
-  h.finish_blocks = finish_blocks;
-  h.tile_map_off = (int64_t)align256(h.layers_off + sizeof(BatchLayer) * n);
-  h.emit_map_off = (int64_t)align256(h.tile_map_off + sizeof(int32_t) * tile_blocks);
-  h.finish_map_off = (int64_t)align256(h.emit_map_off + sizeof(int32_t) * emit_blocks);
-  const size_t need = align256(h.finish_map_off + sizeof(int32_t) * finish_blocks);
+  h = batch_header(n_layers, tile_blocks, emit_blocks, finish_blocks);
+  const size_t need = (size_t)h.total;
   info->n_layers = n_layers;
-  info->has_backward = has_backward ? 1 : 0;
+  info->backward_buffers = backward_buffers ? 1 : 0;
+  info->has_backward = backward_buffers && grads_set ? 1 : 0;
   info->tile_blocks = tile_blocks;
   info->emit_blocks = emit_blocks;
   info->finish_blocks = finish_blocks;
@@ -2043,6 +2096,8 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
   int32_t* tm = reinterpret_cast<int32_t*>(host.data() + h.tile_map_off);
   int32_t* em = reinterpret_cast<int32_t*>(host.data() + h.emit_map_off);
   int32_t* fm = reinterpret_cast<int32_t*>(host.data() + h.finish_map_off);
+  const float** gt = reinterpret_cast<const float**>(host.data() + h.grad_table_off);
+  for (size_t i = 0; i < n; ++i) gt[i] = layers[i].grad_delta;
   for (size_t i = 0; i < n; ++i) {
     const int64_t te = i + 1 < n ? ls[i + 1].tile_block0 : tile_blocks;
     const int64_t ee = i + 1 < n ? ls[i + 1].emit_block0 : emit_blocks;
@@ -2077,10 +2132,51 @@ int gf_batch_forward(const void* plan, const gf_batch_info* info, uint32_t phase
   return GF_OK;
 }
 
+int gf_batch_set_grads(void* plan, gf_batch_info* info, const float* const* grad_delta, void* stream) {
+  if (!plan || !info || (info->n_layers > 0 && !grad_delta))
+    return set_err(GF_E_INVALID_ARGUMENT, "plan / info / grad_delta must not be NULL");
+  bool all = true;
+  for (int32_t i = 0; i < info->n_layers; ++i) all = all && grad_delta[i];
+  if (!all) return set_err(GF_E_INVALID_ARGUMENT, "every layer needs a dL/d(delta) pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  uint8_t* pl = reinterpret_cast<uint8_t*>(plan);
+  for (int32_t b = 0; b < info->n_layers; b += kPtrChunk) {
+    PtrChunk c{};
+    const int32_t cnt = std::min<int32_t>(kPtrChunk, info->n_layers - b);
+    for (int32_t i = 0; i < cnt; ++i) c.p[i] = grad_delta[b + i];
+    hipLaunchKernelGGL(k_batch_set_grads, dim3(1), dim3(kPtrChunk), 0, st, pl, c, b, cnt);
+    GF_LAUNCH_CHECK("k_batch_set_grads");
+  }
+  info->has_backward = info->backward_buffers;
+  return GF_OK;
+}
+
+int gf_batch_read(void* plan, const gf_batch_info* info, int32_t clear, uint32_t* status_host,
+                  int64_t* pairs_host, void* stream) {
+  if (!plan || !info) return set_err(GF_E_INVALID_ARGUMENT, "plan / info must not be NULL");
+  const int32_t n = info->n_layers;
+  if (n == 0) return GF_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  uint8_t* pl = reinterpret_cast<uint8_t*>(plan);
+  hipLaunchKernelGGL(k_batch_read, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, pl, clear);
+  GF_LAUNCH_CHECK("k_batch_read");
+  const BatchHeader h = batch_header(n, info->tile_blocks, info->emit_blocks, info->finish_blocks);
+  std::vector<BatchReadback> rb((size_t)n);
+  GF_HIP_CHECK(hipMemcpyAsync(rb.data(), pl + h.readback_off, sizeof(BatchReadback) * (size_t)n,
+                              hipMemcpyDeviceToHost, st));
+  GF_HIP_CHECK(hipStreamSynchronize(st));
+  for (int32_t i = 0; i < n; ++i) {
+    if (status_host) status_host[i] = rb[(size_t)i].status;
+    if (pairs_host) pairs_host[i] = rb[(size_t)i].pairs;
+  }
+  return GF_OK;
+}
+
 int gf_batch_backward(const void* plan, const gf_batch_info* info, uint32_t phases, void* stream) {
   if (!plan || !info) return set_err(GF_E_INVALID_ARGUMENT, "plan / info must not be NULL");
   if (!info->has_backward)
-    return set_err(GF_E_INVALID_ARGUMENT, "the batch plan was built without backward buffers");
+    return set_err(GF_E_INVALID_ARGUMENT,
+                   "the batch plan has no backward buffers or no dL/d(delta) pointers (gf_batch_set_grads)");
   if (info->n_layers == 0) return GF_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const uint8_t* pl = reinterpret_cast<const uint8_t*>(plan);

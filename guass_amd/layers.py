@@ -111,6 +111,7 @@ class GaussianLinear(nn.Linear):
         self.register_buffer("col_coords", torch.linspace(-1.0, 1.0, in_features, device=self.weight.device),
                              persistent=False)
         self.last_forward_metadata: dict = {}
+        self._batched_delta: Tensor | None = None
         self.reset_gaussian_parameters()
 
     @classmethod
@@ -188,6 +189,15 @@ class GaussianLinear(nn.Linear):
 
     def compute_delta_weight(self) -> Tensor:
         cfg = self.adapter_config
+        pending = self._batched_delta
+        if pending is not None:
+            # rendered for this step by GaussianFieldBatch.render(); used once
+            self._batched_delta = None
+            delta_weight = pending
+            metadata = {"execution_mode": cfg.execution_mode, "accumulate_backend": "batched_fields"}
+            metadata["delta_w_norm"] = float(delta_weight.detach().float().norm().item())
+            self.last_forward_metadata = metadata
+            return delta_weight * cfg.adapter_scale
         ctx = torch.autocast(device_type="cuda", enabled=False) if self.weight.is_cuda else _null()
         with ctx:
             kwargs = dict(row_coords=self.row_coords, col_coords=self.col_coords,
@@ -231,3 +241,169 @@ class _null:
 
     def __exit__(self, *exc):
         return False
+
+
+class _BatchedFieldFunction(torch.autograd.Function):
+    """Autograd node of GaussianFieldBatch.render(): inputs (mu_raw, chol_raw, amp) of every
+    layer, outputs every layer's delta-W [out_features, in_features].  mu = tanh(mu_raw)
+    (gaussian_linear.py:153-154) is taken inside, for all layers in one multi-tensor launch, and
+    its derivative 1 - mu^2 is applied the same way in the backward."""
+
+    @staticmethod
+    def forward(ctx, fb: "GaussianFieldBatch", *params: Tensor):
+        ctx.fb = fb
+        deltas, ctx.mus = fb._run_forward(params)
+        return tuple(deltas)
+
+    @staticmethod
+    def backward(ctx, *grads: Tensor):
+        fb: GaussianFieldBatch = ctx.fb
+        return (None, *fb._run_backward(grads, ctx.mus))
+
+
+class GaussianFieldBatch:
+    """The delta-W of many GaussianLinear layers rendered together: one launch per forward phase
+    for all layers at the start of a step, and one launch per backward phase for all their
+    dL/d(delta-W) (the reference renders each layer inside its own forward,
+    gaussian_linear.py:178-190).
+
+    Per training step::
+
+        fb = GaussianFieldBatch(layers)   # once
+        fb.render()                       # step start: every layer's delta-W, with autograd
+        loss = model(x); loss.backward()  # each layer's forward uses its rendered delta-W once
+
+    A layer whose forward does not run in the step contributes a zero dL/d(delta-W).  The
+    rendered delta-W tensors are the plan's own buffers: they hold until the next render().
+    The forward reads back every layer's status and pair count once (one host synchronisation
+    per step, where the reference synchronises per layer); a pair count past a layer's id
+    capacity grows the capacities and renders again.  All layers must share the tile shape
+    (16x16: the batched kernels), sigma multiplier and normalisation.
+    """
+
+    def __init__(self, layers, *, headroom: float = 1.25):
+        from guass_amd import _native as Nat
+
+        self._Nat = Nat
+        self.layers = list(layers)
+        if not self.layers:
+            raise ValueError("GaussianFieldBatch needs at least one layer")
+        for i, ly in enumerate(self.layers):
+            if not isinstance(ly, GaussianLinear):
+                raise TypeError(f"layer {i} is not a GaussianLinear")
+        cfgs = [ly.adapter_config for ly in self.layers]
+        c0 = cfgs[0]
+        for i, c in enumerate(cfgs):
+            if c.tile_out != 16 or c.tile_in != 16:
+                raise ValueError(f"layer {i}: batched fields need 16x16 tiles (got {c.tile_out}x{c.tile_in})")
+            if c.sigma_multiplier != c0.sigma_multiplier or c.normalize_gaussian != c0.normalize_gaussian:
+                raise ValueError(f"layer {i}: sigma_multiplier / normalize_gaussian differ from layer 0")
+        self.device = self.layers[0].weight.device
+        if any(ly.weight.device != self.device for ly in self.layers):
+            raise ValueError("all layers must live on one device")
+        self.headroom = float(headroom)
+        self._plan = None
+        self._key = None
+        self._caps = [ly.num_gaussians * 32 for ly in self.layers]  # grown from the read-back
+        self._zero_grads: dict[int, Tensor] = {}
+
+    # ---------------------------------------------------------------- plan
+
+    def _param_key(self):
+        return tuple((ly.num_gaussians, ly.chol_raw.data_ptr(), ly.amp.data_ptr()) for ly in self.layers)
+
+    def _build(self) -> None:
+        from guass_amd.ops import FieldBatchPlan
+
+        class _View:
+            pass
+
+        views, self._mu_bufs = [], []
+        for ly in self.layers:
+            v = _View()
+            v.row_coords, v.col_coords = ly.row_coords, ly.col_coords
+            v.mu = torch.empty_like(ly.mu_raw, dtype=torch.float32).contiguous()
+            v.chol_raw, v.amp = ly.chol_raw, ly.amp
+            v.grad = None
+            self._mu_bufs.append(v.mu)
+            views.append(v)
+        c0 = self.layers[0].adapter_config
+        self._plan = FieldBatchPlan(views, self.device, capacities=self._caps,
+                                    sigma_multiplier=c0.sigma_multiplier,
+                                    normalize=c0.normalize_gaussian, clamp_quad=CLAMP_QUAD)
+        self._key = self._param_key()
+
+    # ---------------------------------------------------------------- passes
+
+    def render(self) -> list[Tensor]:
+        """Renders every layer's delta-W for this step (autograd-tracked) and hands each layer
+        its own for its next forward; returns them."""
+        for i, ly in enumerate(self.layers):
+            for name in ("chol_raw", "amp"):
+                t = getattr(ly, name)
+                if t.dtype != torch.float32 or not t.is_contiguous():
+                    raise ValueError(f"layer {i}: {name} must be contiguous float32")
+        ctx = torch.autocast(device_type="cuda", enabled=False) if self.device.type == "cuda" else _null()
+        with ctx:
+            params = []
+            for ly in self.layers:
+                params += [ly.mu_raw, ly.chol_raw, ly.amp]
+            deltas = _BatchedFieldFunction.apply(self, *params)
+        for ly, d in zip(self.layers, deltas):
+            ly._batched_delta = d
+        return list(deltas)
+
+    def _run_forward(self, params) -> tuple[list[Tensor], list[Tensor]]:
+        Nat = self._Nat
+        if self._plan is None or self._key != self._param_key():
+            self._build()
+        mus = torch._foreach_tanh([t.detach() for t in params[0::3]])
+        for _ in range(8):
+            torch._foreach_copy_(self._mu_bufs, mus)
+            self._plan.forward()
+            status, pairs = self._plan.read(clear=True)
+            over = [i for i, st in enumerate(status) if st & Nat.GF_STATUS_CAPACITY]
+            bad = [(i, st) for i, st in enumerate(status) if st & ~Nat.GF_STATUS_CAPACITY]
+            if bad:
+                raise RuntimeError(f"batched fields: device status {bad} (layer, GF_STATUS_* bits)")
+            if not over:
+                self._pairs = pairs
+                return [pl.delta.view(pl.M, pl.N) for pl in self._plan.plans], mus
+            for i in over:
+                self._caps[i] = max(int(pairs[i] * self.headroom) + 1, self._caps[i] * 2)
+            self._build()
+        raise RuntimeError("batched fields: id capacities did not settle")
+
+    def _zero_grad(self, i: int) -> Tensor:
+        pl = self._plan.plans[i]
+        z = self._zero_grads.get(i)
+        if z is None or z.numel() != pl.M * pl.N:
+            z = torch.zeros(pl.M * pl.N, dtype=torch.float32, device=self.device)
+            self._zero_grads[i] = z
+        return z
+
+    def _run_backward(self, grads, mus) -> list[Tensor | None]:
+        gs = []
+        for i, g in enumerate(grads):
+            gs.append(self._zero_grad(i) if g is None else g.to(torch.float32).contiguous().view(-1))
+        self._plan.set_grads(gs)
+        self._plan.backward()
+        # one copy of every layer's gradients (the plan's buffer is rewritten by the next
+        # backward), then d mu_raw = d mu * (1 - mu^2)
+        flat = self._plan.grad_flat.clone()
+        d_mu, d_chol, d_amp = [], [], []
+        o = 0
+        for pl in self._plan.plans:
+            K = pl.K
+            d_mu.append(flat[o:o + 2 * K].view(K, 2))
+            d_chol.append(flat[o + 2 * K:o + 5 * K].view(K, 3))
+            d_amp.append(flat[o + 5 * K:o + 6 * K].view(K, 1))
+            o += 6 * K
+        one_minus = torch._foreach_mul(mus, mus)
+        torch._foreach_neg_(one_minus)
+        torch._foreach_add_(one_minus, 1.0)
+        d_mu_raw = torch._foreach_mul(d_mu, one_minus)
+        out: list[Tensor | None] = []
+        for a, b, c in zip(d_mu_raw, d_chol, d_amp):
+            out += [a, b, c]
+        return out

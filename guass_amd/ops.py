@@ -141,6 +141,17 @@ class FieldBatchPlan:
                                 sigma_multiplier=sigma_multiplier, normalize=normalize,
                                 clamp_quad=clamp_quad, ids_capacity=int(c))
                       for ly, c in zip(self.layers, capacities)]
+        # Every layer's gradients in one buffer (per layer: d_mu [K,2], d_chol_raw [K,3],
+        # d_amp [K,1]), so that they can be copied out with one launch.
+        self.grad_flat = torch.empty(max(sum(6 * pl.K for pl in self.plans), 1), dtype=torch.float32,
+                                     device=self.device)
+        o = 0
+        for pl in self.plans:
+            K = pl.K
+            pl.d_mu = self.grad_flat[o:o + 2 * K].view(K, 2)
+            pl.d_chol_raw = self.grad_flat[o + 2 * K:o + 5 * K].view(K, 3)
+            pl.d_amp = self.grad_flat[o + 5 * K:o + 6 * K].view(K, 1)
+            o += 6 * K
         table = (N.GfLayer * max(len(self.plans), 1))()
         for i, (ly, pl) in enumerate(zip(self.layers, self.plans)):
             grad = getattr(ly, "grad", None)
@@ -171,6 +182,32 @@ class FieldBatchPlan:
         N.check(N.lib().gf_batch_backward(self.plan.data_ptr(), ctypes.byref(self.info), phases,
                                           self._stream()), "gf_batch_backward")
 
+    def set_grads(self, grads) -> None:
+        """dL/d(delta) of every layer for the next ``backward()`` (contiguous fp32 device tensors
+        of M*N elements, kept alive by the plan until replaced); no host synchronisation."""
+        grads = list(grads)
+        if len(grads) != len(self.plans):
+            raise ValueError(f"expected {len(self.plans)} gradients, got {len(grads)}")
+        for i, (g, pl) in enumerate(zip(grads, self.plans)):
+            if (g.dtype != torch.float32 or not g.is_contiguous() or g.numel() != pl.M * pl.N
+                    or g.device != self.device):
+                raise ValueError(f"layer {i}: dL/d(delta) must be a contiguous float32 tensor of "
+                                 f"{pl.M * pl.N} elements on {self.device}")
+        ptrs = (ctypes.c_void_p * max(len(grads), 1))(*[g.data_ptr() for g in grads])
+        N.check(N.lib().gf_batch_set_grads(self.plan.data_ptr(), ctypes.byref(self.info), ptrs,
+                                           self._stream()), "gf_batch_set_grads")
+        self._grads = grads
+
+    def read(self, clear: bool = False) -> tuple[list[int], list[int]]:
+        """(GF_STATUS_* bits, pair count) of every layer's last pass, in one read-back
+        (synchronises)."""
+        n = len(self.plans)
+        st = (ctypes.c_uint32 * max(n, 1))()
+        pairs = (ctypes.c_int64 * max(n, 1))()
+        N.check(N.lib().gf_batch_read(self.plan.data_ptr(), ctypes.byref(self.info), 1 if clear else 0, st,
+                                      pairs, self._stream()), "gf_batch_read")
+        return [int(st[i]) for i in range(n)], [int(pairs[i]) for i in range(n)]
+
     def status(self) -> list[int]:
         """Forward | backward GF_STATUS_* bits per layer (synchronises)."""
-        return [pl.status("forward") | pl.status("backward") for pl in self.plans]
+        return self.read()[0]

@@ -183,9 +183,11 @@ typedef struct gf_layer {
 
 typedef struct gf_batch_info {
   int32_t n_layers;
-  int32_t has_backward;          /* every layer has its backward buffers */
+  int32_t has_backward;          /* backward_buffers and every layer's grad_delta is set */
   int64_t tile_blocks, emit_blocks, finish_blocks;
   size_t plan_bytes;             /* device bytes of the plan buffer */
+  int32_t backward_buffers;      /* every layer has its backward workspace and gradient outputs */
+  int32_t reserved;
 } gf_batch_info;
 
 /*
@@ -204,11 +206,29 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
 #define GF_PHASE_FINISH 0x2u
 #define GF_PHASE_ALL 0xffu
 
-/* gf_forward_bin + gf_forward_emit + gf_forward_render of every layer: three launches. */
+/* gf_forward_bin + gf_forward_emit + gf_forward_render of every layer: three launches (two
+ * when every layer is on the mask path). */
 int gf_batch_forward(const void* plan, const gf_batch_info* info, uint32_t phases, void* stream);
 
 /* gf_backward of every layer (with its pair constants): two launches. */
 int gf_batch_backward(const void* plan, const gf_batch_info* info, uint32_t phases, void* stream);
+
+/*
+ * Replaces every layer's dL/d(delta) pointer in a batch plan (grad_delta: n_layers device
+ * pointers, none NULL), e.g. with the gradients an autograd engine allocated for this step.
+ * Asynchronous on `stream` (the pointers travel as kernel arguments; no host
+ * synchronisation) and sets info->has_backward when the layers have their backward buffers.
+ * A plan built with every gf_layer.grad_delta set needs no call.
+ */
+int gf_batch_set_grads(void* plan, gf_batch_info* info, const float* const* grad_delta, void* stream);
+
+/*
+ * Per layer of a batch plan: the forward | backward GF_STATUS_* bits (status_host) and the pair
+ * count of the last forward (pairs_host), either may be NULL; clear != 0 resets the status
+ * words.  One small kernel and one device-to-host copy; synchronises `stream`.
+ */
+int gf_batch_read(void* plan, const gf_batch_info* info, int32_t clear, uint32_t* status_host,
+                  int64_t* pairs_host, void* stream);
 
 /*
  * Reads (and, if clear != 0, resets) the device status word of a workspace produced by the

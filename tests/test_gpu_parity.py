@@ -487,3 +487,61 @@ def test_gaussian_linear_layer(device, tile):
         assert layer.last_forward_metadata["linear_composition"] == "base_plus_delta_row_chunk_accumulate"
         want = F.linear(x, layer.weight + layer.compute_delta_weight(), layer.bias)
     assert float((y - want).abs().max()) <= 1e-5 * float(want.abs().max())
+
+
+def test_gaussian_field_batch_matches_per_layer(device):
+    """GaussianFieldBatch.render() (one batched launch per phase for every layer, autograd
+    through it) against each GaussianLinear rendering its own delta-W, over two training steps
+    (parameters updated in between) with layers of different shapes and one layer whose forward
+    does not run in the second step (zero dL/d(delta-W))."""
+    import copy
+
+    from guass_amd.layers import GaussianAdapterConfig, GaussianFieldBatch, GaussianLinear
+
+    torch.manual_seed(7)
+    shapes = [(96, 80, 48), (64, 64, 24), (120, 40, 36)]  # (in, out, K)
+    layers_a, layers_b = [], []
+    for i, (n_in, n_out, k) in enumerate(shapes):
+        cfg = GaussianAdapterConfig(init_num_gaussians=k, tile_out=16, tile_in=16, adapter_scale=0.5,
+                                    init_amp_scale=1e-2)
+        la = GaussianLinear(n_in, n_out, adapter_config=cfg, device=device)
+        with torch.no_grad():
+            la.chol_raw.add_(torch.randn_like(la.chol_raw) * 0.2)
+        layers_a.append(la)
+        layers_b.append(copy.deepcopy(la))
+    say("GaussianFieldBatch over 3 layers vs per-layer rendering, 2 steps")
+    fb = GaussianFieldBatch(layers_b)
+    xs = [torch.randn(6, n_in, device=device) for (n_in, _, _) in shapes]
+    for step in range(2):
+        used = [0, 1, 2] if step == 0 else [0, 2]
+        for ls in (layers_a, layers_b):
+            for ly in ls:
+                for p in (ly.mu_raw, ly.chol_raw, ly.amp):
+                    p.grad = None
+        loss_a = sum((layers_a[i](xs[i]) ** 2).sum() for i in used)
+        loss_a.backward()
+        fb.render()
+        outs_b = {i: layers_b[i](xs[i]) for i in used}
+        loss_b = sum((outs_b[i] ** 2).sum() for i in used)
+        loss_b.backward()
+        torch.cuda.synchronize()
+        for i in used:
+            assert layers_b[i].last_forward_metadata["accumulate_backend"] == "batched_fields"
+            with torch.no_grad():
+                ya = layers_a[i](xs[i])
+            assert torch.equal(outs_b[i].detach(), ya), f"step {step} layer {i}: output"
+        for i in range(3):
+            for name in ("mu_raw", "chol_raw", "amp"):
+                ga = getattr(layers_a[i], name).grad
+                gb = getattr(layers_b[i], name).grad
+                if i not in used:
+                    assert ga is None and gb is not None and float(gb.abs().max()) == 0.0
+                    continue
+                grad_close(gb, ga, f"step {step} layer {i} {name}", rtol=1e-5)
+        with torch.no_grad():  # an optimiser step, then the same parameters on both copies
+            for la, lb in zip(layers_a, layers_b):  # (the gradients agree to atomic order only)
+                for name in ("mu_raw", "chol_raw", "amp"):
+                    pa, pb = getattr(la, name), getattr(lb, name)
+                    if pa.grad is not None:
+                        pa.add_(pa.grad, alpha=-0.05)
+                    pb.copy_(pa)

@@ -34,3 +34,21 @@ def test_layer_parameters_and_cpu_error():
     assert torch.equal(layer.amp, state["amp"])
     with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
         layer.compute_delta_weight()
+
+
+def test_field_batch_checks_layer_configs():
+    """GaussianFieldBatch needs 16x16 tiles and one sigma / normalisation for all layers; the
+    checks run before any device work."""
+    from guass_amd.layers import GaussianFieldBatch
+
+    ok = GaussianAdapterConfig(init_num_gaussians=4, tile_out=16, tile_in=16)
+    a = GaussianLinear(32, 32, adapter_config=ok)
+    with pytest.raises(ValueError, match="16x16"):
+        GaussianFieldBatch([a, GaussianLinear(32, 32, adapter_config=GaussianAdapterConfig(init_num_gaussians=4))])
+    other = GaussianAdapterConfig(init_num_gaussians=4, tile_out=16, tile_in=16, sigma_multiplier=2.5)
+    with pytest.raises(ValueError, match="sigma_multiplier"):
+        GaussianFieldBatch([a, GaussianLinear(32, 32, adapter_config=other)])
+    with pytest.raises(ValueError, match="at least one"):
+        GaussianFieldBatch([])
+    with pytest.raises(TypeError):
+        GaussianFieldBatch([torch.nn.Linear(4, 4)])
