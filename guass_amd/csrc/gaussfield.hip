@@ -34,6 +34,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/gaussfield.h"
@@ -106,12 +107,16 @@ struct Problem {
 };
 
 // Per-Gaussian constants of the tile kernels: with dx = x - mu0, dy = y - mu1,
-//   a = wa dx,  z = wb dx + wc dy,  q' = -(a^2 + z^2) = kHalfLog2e * (d^T cov^-1 d),
-//   basis = 2^clamp(q') = exp(-q/2).
+//   a = wa dx,  z = wb dx + wc dy,  q' = kHalfLog2e * (d^T cov^-1 d),
+//   basis = 2^clamp(q') = exp(-q/2) with q clamped to [0, clamp]:
+//   gen == 0 (positive-definite fp32 covariance): q' = -(a^2 + z^2);
+//   gen != 0 (the fp32 covariance lost positive definiteness in rounding, det < 0):
+//     q' = z^2 - a^2, the exact inverse of that indefinite matrix; its negative forms the clamp
+//     maps to q = 0 (basis 1), as the reference's torch path does.
 struct __align__(16) GaussEval {
   float mu0, mu1, wa, wb, wc, w;  // w = amp * norm
   int32_t gid;                    // the Gaussian's id (pair-ordered copies carry it)
-  float pad;
+  float gen;                      // 0: whitened form, 1: general form
 };
 
 struct WsHeader {
@@ -201,13 +206,17 @@ __device__ inline int4 bin_rect(const Problem& p, float mu0, float mu1, GfCov c,
 __device__ inline GaussEval eval_from_cov(const Problem& p, float mu0, float mu1, GfCov c, float amp) {
   const double a = (double)c.s00, b = (double)c.s01, d = (double)c.s11;
   double det = a * d - b * b;  // exact products, one rounding
-  if (!(det > 0.0)) det = 1e-300;  // singular fp32 covariance: a (numerically) degenerate line
-  const double r00 = 1.0 / sqrt(a);
-  const double r11 = sqrt(a / det);  // 1 / l22 with l22 = sqrt(det / a)
-  const double r10 = -(b / a) * r11;  // -l21 / (l11 l22)
   GaussEval v;
   v.mu0 = mu0;
   v.mu1 = mu1;
+  // d^T cov^-1 d = dx^2 / a + (a / det) (dy - (b / a) dx)^2 for any det != 0 (a > 0): the
+  // second coefficient takes the sign of det, so an indefinite matrix only flips that term.
+  v.gen = det < 0.0 ? 1.0f : 0.0f;
+  det = fabs(det);
+  if (!(det > 0.0)) det = 1e-300;  // exactly singular fp32 covariance: a degenerate line
+  const double r00 = 1.0 / sqrt(a);
+  const double r11 = sqrt(a / det);  // 1 / l22 with l22 = sqrt(det / a)
+  const double r10 = -(b / a) * r11;  // -l21 / (l11 l22)
   v.wa = (float)(kSqrtHalfLog2e * r00);
   v.wb = (float)(kSqrtHalfLog2e * r10);
   v.wc = (float)(kSqrtHalfLog2e * r11);
@@ -219,7 +228,6 @@ __device__ inline GaussEval eval_from_cov(const Problem& p, float mu0, float mu1
   }
   v.w = amp * norm;
   v.gid = -1;
-  v.pad = 0.0f;
   return v;
 }
 
@@ -241,13 +249,13 @@ __device__ inline GaussEval load_eval(const GaussEval* __restrict__ ev, int64_t 
   v.wc = b.x;
   v.w = b.y;
   v.gid = __float_as_int(b.z);
-  v.pad = 0.0f;
+  v.gen = b.w;
   return v;
 }
 
 __device__ inline GaussEval zero_eval() {
   GaussEval v;
-  v.mu0 = v.mu1 = v.wa = v.wb = v.wc = v.w = v.pad = 0.0f;
+  v.mu0 = v.mu1 = v.wa = v.wb = v.wc = v.w = v.gen = 0.0f;
   v.gid = -1;
   return v;
 }
@@ -255,6 +263,17 @@ __device__ inline GaussEval zero_eval() {
 // 2^clamp(q'), q' = -(A + z^2).
 __device__ inline float basis_w(const Problem& p, float A, float z) {
   const float q = -fmaf(z, z, A);
+  return __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(q, p.q_lo, p.q_hi));
+}
+
+// q' of a pixel for either form of GaussEval.
+__device__ inline float quad_form(const GaussEval& u, float dx, float dy) {
+  const float a = u.wa * dx;
+  const float z = fmaf(u.wc, dy, u.wb * dx);
+  return u.gen != 0.0f ? fmaf(z, z, -(a * a)) : -fmaf(z, z, a * a);
+}
+
+__device__ inline float basis_q(const Problem& p, float q) {
   return __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(q, p.q_lo, p.q_hi));
 }
 
@@ -396,7 +415,7 @@ __device__ int64_t bin_scan_lds_to_global(const int32_t* lds, int64_t n, int64_t
 __device__ inline void store_eval(GaussEval* ev, int64_t i, const GaussEval& v) {
   float4* q = reinterpret_cast<float4*>(ev + i);
   q[0] = make_float4(v.mu0, v.mu1, v.wa, v.wb);
-  q[1] = make_float4(v.wc, v.w, __int_as_float(v.gid), 0.0f);
+  q[1] = make_float4(v.wc, v.w, __int_as_float(v.gid), v.gen);
 }
 
 __device__ inline GaussEval readlane_eval(const GaussEval& v, int lane) {
@@ -408,7 +427,7 @@ __device__ inline GaussEval readlane_eval(const GaussEval& v, int lane) {
   r.wc = readlane_f(v.wc, lane);
   r.w = readlane_f(v.w, lane);
   r.gid = __builtin_amdgcn_readlane(v.gid, lane);
-  r.pad = 0.0f;
+  r.gen = readlane_f(v.gen, lane);
   return r;
 }
 
@@ -1078,8 +1097,19 @@ __device__ __forceinline__ void render16_body(
 #pragma unroll
   for (int i = 0; i < 4; ++i) y[i] = col_coords[min(pc + i, p.N - 1)];
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  auto accumulate = [&](const GaussEval& u) {
+  auto accumulate = [&](const GaussEval& u, auto general) {
     const float dx = x - u.mu0;
+    if (general && u.gen != 0.0f) {  // indefinite form (uniform: u is broadcast)
+      const float a = u.wa * dx;
+      const float nA = -(a * a);
+      const float b = u.wb * dx;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float z = fmaf(u.wc, y[i] - u.mu1, b);
+        acc[i] = fmaf(u.w, basis_q(p, fmaf(z, z, nA)), acc[i]);
+      }
+      return;
+    }
     const float a = u.wa * dx;
     const float A = a * a;
     const float b = u.wb * dx;
@@ -1087,6 +1117,15 @@ __device__ __forceinline__ void render16_body(
     for (int i = 0; i < 4; ++i) {
       const float z = fmaf(u.wc, y[i] - u.mu1, b);
       acc[i] = fmaf(u.w, basis_w(p, A, z), acc[i]);
+    }
+  };
+  // Gaussians 0 .. nj-1 of a chunk (lane j holds Gaussian j), broadcast in order; one ballot
+  // per chunk picks the loop that handles general-form Gaussians.
+  auto run_chunk = [&](const GaussEval& my, int nj) {
+    if (__builtin_amdgcn_ballot_w64(lane < nj && my.gen != 0.0f) == 0) {
+      for (int j = 0; j < nj; ++j) accumulate(readlane_eval(my, j), std::false_type{});
+    } else {
+      for (int j = 0; j < nj; ++j) accumulate(readlane_eval(my, j), std::true_type{});
     }
   };
   int64_t s, n;
@@ -1126,7 +1165,7 @@ __device__ __forceinline__ void render16_body(
             const int64_t slot = done + j0 + lane;
             if (slot < room) ids[s + slot] = g;
           }
-          for (int j = 0; j < nj; ++j) accumulate(readlane_eval(my, j));
+          run_chunk(my, nj);
         }
         done += nwin;
         wave_sync();
@@ -1160,12 +1199,12 @@ __device__ __forceinline__ void render16_body(
     srt.wc = __int_as_float(__builtin_amdgcn_ds_permute(addr, __float_as_int(my.wc)));
     srt.w = __int_as_float(__builtin_amdgcn_ds_permute(addr, __float_as_int(my.w)));
     srt.gid = __builtin_amdgcn_ds_permute(addr, key);  // key == my.gid for a valid id
-    srt.pad = 0.0f;
+    srt.gen = __int_as_float(__builtin_amdgcn_ds_permute(addr, __float_as_int(my.gen)));
     if (lane < n) {
       if (srt.gid < 0 || srt.gid >= p.K) set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);
       if (srt.gid != key) ids[s + lane] = srt.gid;  // lanes whose id moved
     }
-    for (int j = 0; j < (int)n; ++j) accumulate(readlane_eval(srt, j));
+    run_chunk(srt, (int)n);
   } else if (n > 64) {
     int64_t* seg = ids + s;
     int32_t* keys = wkeys[wid];
@@ -1181,7 +1220,7 @@ __device__ __forceinline__ void render16_body(
           set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);  // internal mismatch only
         }
       }
-      for (int j = 0; j < nj; ++j) accumulate(readlane_eval(my, j));
+      run_chunk(my, nj);
     }
   }
   if (pr < p.M) {
@@ -1247,9 +1286,7 @@ __global__ __launch_bounds__(kTileThreads) void k_render_any(
       __syncthreads();
       for (int j = 0; j < nj; ++j) {
         const GaussEval v = gl[j];
-        const float dx = x - v.mu0, dy = y - v.mu1;
-        const float a = v.wa * dx;
-        acc = fmaf(v.w, basis_w(p, a * a, fmaf(v.wc, dy, v.wb * dx)), acc);
+        acc = fmaf(v.w, basis_q(p, quad_form(v, x - v.mu0, y - v.mu1)), acc);
       }
     }
     if (have) delta[(int64_t)r * p.N + c] = acc;
@@ -1353,6 +1390,7 @@ __device__ __forceinline__ void bwd16_body(
   const int64_t n = e > s ? e - s : 0;
   if (n == 0) return;
 
+  bool tile_general = false;
   for (int64_t j0 = 0; j0 < n; j0 += 64) {
     const int nj = (int)((n - j0) < 64 ? (n - j0) : 64);
     GaussEval my = zero_eval();
@@ -1366,18 +1404,21 @@ __device__ __forceinline__ void bwd16_body(
         myg = (int32_t)g;
       }
     }
+    const bool chunk_general = __builtin_amdgcn_ballot_w64(lane < nj && my.gen != 0.0f) != 0;
     for (int jb = 0; jb < nj; jb += 4) {
       const int j = jb + slot;
       const int src = j < nj ? j : 0;
       const float mu0 = __shfl(my.mu0, src, 64), mu1 = __shfl(my.mu1, src, 64);
       const float wa = __shfl(my.wa, src, 64), wb = __shfl(my.wb, src, 64);
       const float wc = __shfl(my.wc, src, 64);
+      const float gen = chunk_general ? __shfl(my.gen, src, 64) : 0.0f;
       int32_t g = __shfl(myg, src, 64);
       if (j >= nj) g = -1;
       const float dx = x - mu0;
       const float a = wa * dx;
       const float A = a * a;
       const float b = wb * dx;
+      if (chunk_general && gen != 0.0f) g = -1;  // indefinite form: the pass below
       float t0 = 0.f, t2 = 0.f, t3 = 0.f;
 #pragma unroll
       for (int c = 0; c < 16; ++c) {
@@ -1401,11 +1442,71 @@ __device__ __forceinline__ void bwd16_body(
         unsafeAtomicAdd(acc + 8 * ((int64_t)g * p.S + (t & (p.S - 1))) + k, val);
       }
     }
+    tile_general = tile_general || chunk_general;
+  }
+  // Indefinite-form Gaussians of the tile (q' = z^2 - a^2; rare), after the rounds above so
+  // that the row registers are free: lanes 0..15 take one tile row each, the pixels one at a
+  // time from memory, and the clamped pixels (q < 0 or q > clamp) add nothing to the
+  // quadratic-form moments.
+  if (tile_general) {
+    for (int64_t j0 = 0; j0 < n; j0 += 64) {
+      const int nj = (int)((n - j0) < 64 ? (n - j0) : 64);
+      GaussEval my = zero_eval();
+      int32_t myg = -1;
+      if (lane < nj) {
+        const int64_t g = (int64_t)gids[s + j0 + lane];
+        if (g >= 0 && g < p.K) {
+          my = ev ? load_eval(ev, g) : eval_geom(p, mu, chol_raw, nullptr, g);
+          myg = (int32_t)g;
+        }
+      }
+      uint64_t gm = __builtin_amdgcn_ballot_w64(lane < nj && my.gen != 0.0f);
+      while (gm) {
+        const int j = __builtin_ctzll(gm);
+        gm &= gm - 1;
+        const GaussEval u = readlane_eval(my, j);
+        const int32_t gj = __builtin_amdgcn_readlane(myg, j);
+        float mm[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        const int32_t pr2 = r0 + lane;
+        if (lane < 16 && pr2 < p.M) {
+          const float dx2 = row_coords[pr2] - u.mu0;
+          const float a2 = u.wa * dx2;
+          const float nA2 = -(a2 * a2);
+          const float b2 = u.wb * dx2;
+          const float* grow2 = grad + (int64_t)pr2 * p.N;
+#pragma unroll 1
+          for (int c = 0; c < 16 && c0 + c < p.N; ++c) {
+            const float dy = col_coords[c0 + c] - u.mu1;
+            const float z = fmaf(u.wc, dy, b2);
+            const float q = fmaf(z, z, nA2);
+            const float qc = __builtin_amdgcn_fmed3f(q, p.q_lo, p.q_hi);
+            const float ge = grow2[c0 + c] * __builtin_amdgcn_exp2f(qc);
+            mm[0] += ge;
+            if (qc == q) {
+              mm[1] += ge * dx2;
+              mm[2] += ge * dy;
+              mm[3] += ge * dx2 * dx2;
+              mm[4] += ge * dx2 * dy;
+              mm[5] += ge * dy * dy;
+            }
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 6; ++k) mm[k] = dpp_row_sum_f32(mm[k]);  // row 0: lanes 0..15
+        if (lane == 15 && gj >= 0) {
+#pragma unroll
+          for (int k = 0; k < 6; ++k)
+            unsafeAtomicAdd(acc + 8 * ((int64_t)gj * p.S + (t & (p.S - 1))) + k, mm[k]);
+        }
+      }
+    }
   }
 }
 
+// Seven waves per SIMD (72 VGPRs): the rarely taken indefinite-form pass would otherwise
+// raise the register count and cost the common path occupancy.
 template <typename TpIdx, typename GIdx>
-__global__ __launch_bounds__(kTileThreads) void k_bwd16(
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_bwd16(
     Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
     const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
@@ -1458,14 +1559,16 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
         const int32_t r = r0 + px / w, c = c0 + (px - (px / w) * w);
         const float gr = grad[(int64_t)r * p.N + c];
         const float dx = row_coords[r] - v.mu0, dy = col_coords[c] - v.mu1;
-        const float a = v.wa * dx;
-        const float ge = gr * basis_w(p, a * a, fmaf(v.wc, dy, v.wb * dx));
+        const float q = quad_form(v, dx, dy);
+        const float ge = gr * basis_q(p, q);
         m[0] += ge;
-        m[1] += ge * dx;
-        m[2] += ge * dy;
-        m[3] += ge * dx * dx;
-        m[4] += ge * dx * dy;
-        m[5] += ge * dy * dy;
+        // clamped pixels of a general-form Gaussian carry no quadratic-form gradient
+        const float gq = (v.gen != 0.0f && !(q >= p.q_lo && q <= p.q_hi)) ? 0.f : ge;
+        m[1] += gq * dx;
+        m[2] += gq * dy;
+        m[3] += gq * dx * dx;
+        m[4] += gq * dx * dy;
+        m[5] += gq * dy * dy;
       }
 #pragma unroll
       for (int k = 0; k < 6; ++k) m[k] = wave_sum(m[k]);
@@ -1749,7 +1852,7 @@ __global__ __launch_bounds__(kTileThreads) void k_render16_batch(const uint8_t* 
                 ((int64_t)blockIdx.x - b0) * (kTileThreads / 64) + wave_id());
 }
 
-__global__ __launch_bounds__(kTileThreads) void k_bwd16_batch(const uint8_t* __restrict__ plan) {
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_bwd16_batch(const uint8_t* __restrict__ plan) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
   int64_t b0;
   int32_t l;

@@ -545,3 +545,74 @@ def test_gaussian_field_batch_matches_per_layer(device):
                     if pa.grad is not None:
                         pa.add_(pa.grad, alpha=-0.05)
                     pb.copy_(pa)
+
+
+def test_adapter_checkpoint_delta_w(device, tmp_path):
+    """A trained adapter (a few SGD steps on the GPU) saved in the gaussian-peft-adapter format
+    and loaded into a fresh model: its delta-W equals the trained layer's bit for bit and the
+    oracle's at the field tolerance (checkpoints/io.py:18-39; scripts/sample_eval_10751.py:231-239
+    loads adapters this way for sampling)."""
+    from guass_amd.checkpoints import load_adapter_checkpoint, save_adapter_checkpoint
+    from guass_amd.layers import GaussianAdapterConfig, GaussianLinear
+
+    torch.manual_seed(3)
+    cfg = GaussianAdapterConfig(init_num_gaussians=40, tile_out=16, tile_in=16, init_amp_scale=1e-2)
+    model = torch.nn.ModuleDict({"to_k": GaussianLinear(96, 80, adapter_config=cfg, device=device)})
+    layer = model["to_k"]
+    opt = torch.optim.SGD([layer.mu_raw, layer.chol_raw, layer.amp], lr=1e-3)
+    x = torch.randn(8, 96, device=device)
+    say("adapter checkpoint: 3 SGD steps, save, load, delta-W")
+    before = [t.detach().clone() for t in (layer.mu_raw, layer.chol_raw, layer.amp)]
+    for _ in range(3):
+        opt.zero_grad()
+        (layer(x) ** 2).mean().backward()
+        opt.step()
+    for b0, t in zip(before, (layer.mu_raw, layer.chol_raw, layer.amp)):
+        assert not torch.equal(b0, t.detach())  # trained: every parameter moved
+    path = str(tmp_path / "adapter.pt")
+    save_adapter_checkpoint(path, model, ["to_k"], cfg, step=3)
+    fresh = torch.nn.ModuleDict({"to_k": GaussianLinear(96, 80, adapter_config=cfg, device=device)})
+    load_adapter_checkpoint(path, fresh)
+    with torch.no_grad():
+        want = layer.compute_delta_weight()
+        got = fresh["to_k"].compute_delta_weight()
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    ly = fresh["to_k"]
+    ref = fo.gaussian_field_fwd_bwd(ly.row_coords.cpu(), ly.col_coords.cpu(), ly.materialize_mu().detach().cpu(),
+                                    ly.chol_raw.detach().cpu(), ly.amp.detach().cpu(),
+                                    torch.zeros(80 * 96), 16, 16, 3.0, False, 80.0)
+    field_close(got.reshape(-1), ref[0])
+
+
+def _indefinite_problem(M: int, N: int, seed: int, n_normal: int = 24, n_bad: int = 6):
+    """Ordinary Gaussians plus extremely elongated ones whose fp32 covariance L L^T is no longer
+    positive definite after rounding (det < 0: l11, l22 at the softplus floor, |l21| ~ 100).
+    The reference's torch path inverts such a matrix exactly; the negative quadratic forms its
+    clamp maps to q = 0 give the Gaussian its full amplitude there."""
+    p = tiny_problem(M, N, n_normal, seed)
+    gen = torch.Generator().manual_seed(seed)
+    found = []
+    while len(found) < n_bad:
+        raw = torch.empty(64, 3)
+        raw[:, 0] = -100.0 - 100.0 * torch.rand(64, generator=gen)
+        raw[:, 1] = (50.0 + 100.0 * torch.rand(64, generator=gen)) * torch.sign(torch.randn(64, generator=gen))
+        raw[:, 2] = -100.0 - 100.0 * torch.rand(64, generator=gen)
+        cov = fo.activate_cholesky(raw)
+        cov = cov @ cov.transpose(-1, -2)  # fp32, as the reference forms it
+        c64 = cov.double()
+        det = c64[:, 0, 0] * c64[:, 1, 1] - c64[:, 0, 1] * c64[:, 1, 0]
+        found += [raw[i] for i in range(64) if det[i] < 0][: n_bad - len(found)]
+    bad = torch.stack(found)
+    mu_bad = (torch.rand(n_bad, 2, generator=gen) * 1.6 - 0.8)
+    amp_bad = torch.randn(n_bad, 1, generator=gen) * 1e-2
+    p.mu = torch.cat([p.mu, mu_bad])
+    p.chol_raw = torch.cat([p.chol_raw, bad])
+    p.amp = torch.cat([p.amp, amp_bad])
+    return p
+
+
+@pytest.mark.parametrize("tile", [16, 32])
+def test_indefinite_fp32_covariances(device, tile):
+    p = _indefinite_problem(80, 96, 31 + tile)
+    check(p, device, tile_out=tile, tile_in=tile)
