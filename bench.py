@@ -10,6 +10,9 @@ graph.  Workloads:
                                 as one batch (guass_amd.ops.FieldBatchPlan: five launches per
                                 step for all layers)
   cfg1, cfg2, cfg5, cfg5c       single fields as cfg3
+  delta-apply                   the layer's composition with delta-W over the cfg4 shapes (x of
+                                --tokens rows, fp32, forward + backward into delta-W): the
+                                reference's row-chunked composition against one merged GEMM
   cfg4-model                    the cfg4 layers as GaussianLinear modules through autograd: one
                                 training step's fields via GaussianFieldBatch.render() (one
                                 batched launch per phase) against every layer rendering its own
@@ -50,7 +53,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="cfg3",
-                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "cfg5c", "cfg4-model"])
+                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "cfg5c", "cfg4-model", "delta-apply"])
+    ap.add_argument("--tokens", type=int, default=4096, help="delta-apply: rows of x per layer")
     ap.add_argument("--layers", type=int, default=None, help="cfg4: first N of the 128 layers")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of graph replay")
@@ -217,6 +221,68 @@ def model_bench(args) -> int:
     return 0
 
 
+def delta_apply_bench(args) -> int:
+    """delta-apply: forward + backward (into delta-W and x) of y = x (W + delta-W)^T + b over the
+    SD1.5 attention shapes, composed as the reference layer does (base GEMM, output clone,
+    delta-W GEMMs in row chunks, gaussian_linear.py:222-253) and as one merged GEMM."""
+    import torch
+    import torch.nn.functional as F
+
+    from guass_amd import workloads as wl
+
+    dev = torch.device("cuda:0")
+    shapes = wl.sd15_attention_shapes()[: args.layers]
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    layers = []
+    for _, m, n in shapes:
+        W = torch.randn(m, n, device=dev, generator=gen) * 0.02
+        b = torch.zeros(m, device=dev)
+        dW = (torch.randn(m, n, device=dev, generator=gen) * 1e-3).requires_grad_(True)
+        x = torch.randn(args.tokens, n, device=dev, generator=gen).requires_grad_(True)
+        layers.append((W, b, dW, x, torch.randn(args.tokens, m, device=dev, generator=gen)))
+
+    def row_chunk(W, b, dW, x):
+        chunk = min(W.shape[0], 64)
+        out = F.linear(x, W, b).clone()
+        for r0 in range(0, W.shape[0], chunk):
+            out[..., r0:r0 + chunk].add_(F.linear(x, dW[r0:r0 + chunk, :], None))
+        return out
+
+    def merged(W, b, dW, x):
+        return F.linear(x, W + dW, b)
+
+    def step(fn):
+        for W, b, dW, x, g in layers:
+            dW.grad = None
+            x.grad = None
+            fn(W, b, dW, x).backward(g)
+
+    def timed(fn) -> float:
+        for _ in range(max(1, args.warmup // 10)):
+            step(fn)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        n = max(1, args.steps // 10)
+        for _ in range(n):
+            step(fn)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n
+
+    t_chunk, t_merged = timed(row_chunk), timed(merged)
+    flops = sum(6.0 * args.tokens * m * n for _, m, n in shapes)  # fwd + two backward GEMMs
+    out = {
+        "metric": "delta-W composition, forward + backward over the SD1.5 attention shapes",
+        "value": flops / t_merged / 1e12, "unit": "TFLOP/s (merged)", "n_gpus": 1,
+        "steps": max(1, args.steps // 10), "warmup": max(1, args.warmup // 10),
+        "ms_per_step": t_merged * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"{len(shapes)} SD1.5 attention linears, x of {args.tokens} rows"},
+        "row_chunk_ms_per_step": t_chunk * 1e3, "speedup_vs_row_chunk": t_chunk / t_merged,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -226,6 +292,8 @@ def main() -> int:
         return 2
     if args.config == "cfg4-model":
         return model_bench(args)
+    if args.config == "delta-apply":
+        return delta_apply_bench(args)
 
     import torch
 

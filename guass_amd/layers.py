@@ -61,6 +61,10 @@ class GaussianAdapterConfig:
     tile_out: int = 32
     tile_in: int = 32
     sigma_multiplier: float = 3.0
+    # How forward composes the base linear with delta-W (no counterpart field in the reference,
+    # whose layer always does "row_chunk", gaussian_linear.py:222-253): "merged" runs one GEMM on
+    # W + delta-W instead of the base GEMM plus row-chunked delta GEMMs and an output clone.
+    delta_apply: str = "row_chunk"
 
     def validate(self) -> None:
         """The checks of config/adapter.py:31-79 that concern the field path."""
@@ -84,6 +88,8 @@ class GaussianAdapterConfig:
             raise ValueError("tile_out and tile_in must be positive")
         if self.sigma_multiplier <= 0:
             raise ValueError("sigma_multiplier must be positive")
+        if self.delta_apply not in ("row_chunk", "merged"):
+            raise ValueError(f"Unsupported delta_apply={self.delta_apply!r}.")
         if self.merge_weights:
             raise ValueError("merge_weights is disabled in the first implementation")
         self.execution_mode = _MODE_ALIASES.get(self.execution_mode, self.execution_mode)
@@ -222,6 +228,11 @@ class GaussianLinear(nn.Linear):
 
     def forward(self, input: Tensor) -> Tensor:
         delta_weight = self.compute_delta_weight().to(dtype=self.weight.dtype)
+        if self.adapter_config.delta_apply == "merged":
+            metadata = dict(self.last_forward_metadata)
+            metadata["linear_composition"] = "merged_weight"
+            self.last_forward_metadata = metadata
+            return F.linear(input, self.weight + delta_weight, self.bias)
         base = F.linear(input, self.weight, self.bias)
         chunk = self._delta_apply_row_chunk()
         metadata = dict(self.last_forward_metadata)

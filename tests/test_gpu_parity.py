@@ -616,3 +616,30 @@ def _indefinite_problem(M: int, N: int, seed: int, n_normal: int = 24, n_bad: in
 def test_indefinite_fp32_covariances(device, tile):
     p = _indefinite_problem(80, 96, 31 + tile)
     check(p, device, tile_out=tile, tile_in=tile)
+
+
+def test_delta_apply_merged_matches_row_chunk(device):
+    """delta_apply="merged" (one GEMM on W + delta-W) against the reference's row-chunked
+    composition (gaussian_linear.py:222-253): outputs and gradients at fp32 GEMM tolerance."""
+    import copy
+
+    from guass_amd.layers import GaussianAdapterConfig, GaussianLinear
+
+    torch.manual_seed(11)
+    cfg = GaussianAdapterConfig(init_num_gaussians=32, tile_out=16, tile_in=16, init_amp_scale=1e-2,
+                                adapter_scale=0.7)
+    a = GaussianLinear(96, 200, adapter_config=cfg, device=device)
+    b = copy.deepcopy(a)
+    b.adapter_config = copy.copy(cfg)
+    b.adapter_config.delta_apply = "merged"
+    x = torch.randn(3, 7, 96, device=device)
+    ya, yb = a(x), b(x)
+    (ya.square().sum()).backward()
+    (yb.square().sum()).backward()
+    torch.cuda.synchronize()
+    assert a.last_forward_metadata["linear_composition"] == "base_plus_delta_row_chunk_accumulate"
+    assert b.last_forward_metadata["linear_composition"] == "merged_weight"
+    ya, yb = ya.detach(), yb.detach()
+    assert float((ya - yb).abs().max()) <= 1e-5 * float(ya.abs().max())
+    for name in ("mu_raw", "chol_raw", "amp"):
+        grad_close(getattr(b, name).grad, getattr(a, name).grad, name, rtol=1e-4)
