@@ -17,7 +17,7 @@ graph.  Workloads:
                                 training step's fields via GaussianFieldBatch.render() (one
                                 batched launch per phase) against every layer rendering its own
                                 through the drop-in gaussian_field_train (eager, both)
-All with 16x16 tiles, 3 sigma, clamp 80.
+All with 16x16 tiles (--tile 32: the reference's training configs' 32x32), 3 sigma, clamp 80.
 
 Prints one JSON line (metric contract of the driver) with two extra objects:
   roofline      the dominant kernel's achieved throughput against MI355X peak; its duration is
@@ -55,6 +55,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--config", default="cfg3",
                     choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "cfg5c", "cfg4-model", "delta-apply"])
     ap.add_argument("--tokens", type=int, default=4096, help="delta-apply: rows of x per layer")
+    ap.add_argument("--tile", type=int, default=16, choices=[16, 32],
+                    help="square tile size (the headline metric is quoted on 16x16 tiles)")
     ap.add_argument("--layers", type=int, default=None, help="cfg4: first N of the 128 layers")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of graph replay")
@@ -127,7 +129,7 @@ def traffic_bytes(path: str, config: str, kernel: str):
     return None if entry is None else float(entry["hbm_bytes_per_launch"])
 
 
-def cpu_baseline(problems, reps: int, note: str) -> dict:
+def cpu_baseline(problems, reps: int, note: str, tile: int = 16) -> dict:
     import torch
 
     from oracle import field_oracle as fo  # CPU baseline leg only
@@ -138,7 +140,7 @@ def cpu_baseline(problems, reps: int, note: str) -> dict:
     def run():
         for p in problems:
             fo.gaussian_field_fwd_bwd(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad,
-                                      16, 16, 3.0, False, 80.0)
+                                      tile, tile, 3.0, False, 80.0)
 
     run()  # warmup
     times = []
@@ -319,12 +321,13 @@ def main() -> int:
     counts = []
     for p, q in zip(probs, qs):
         _, tp0, _ = ext.gaussian_field_forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
-                                               16, 16, 3.0, False, 80.0)
-        counts.append(algorithmic_counts(tp0, p.out_features, p.in_features, p.k, 16, 16))
+                                               args.tile, args.tile, 3.0, False, 80.0)
+        counts.append(algorithmic_counts(tp0, p.out_features, p.in_features, p.k, args.tile, args.tile))
     total = sum_counts(counts)
 
     if batched:
-        batch = FieldBatchPlan(qs, dev, capacities=[c["pairs"] for c in counts])
+        batch = FieldBatchPlan(qs, dev, capacities=[c["pairs"] for c in counts], tile_out=args.tile,
+                               tile_in=args.tile)
 
         def step():
             batch.forward()
@@ -340,7 +343,8 @@ def main() -> int:
         status = lambda: max(batch.status())  # noqa: E731
     else:
         q, P = qs[0], counts[0]["pairs"]
-        plan = FieldPlan(probs[0].out_features, probs[0].in_features, probs[0].k, dev, ids_capacity=P)
+        plan = FieldPlan(probs[0].out_features, probs[0].in_features, probs[0].k, dev, ids_capacity=P,
+                         tile_out=args.tile, tile_in=args.tile)
 
         def step():
             plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
@@ -440,11 +444,12 @@ def main() -> int:
                  "duration_us": ph[dominant] * 1e3})
     step_roof = roofline(total["bytes_step"], total["flops_fwd"] + total["flops_bwd"], ms_per_step / 1e3)
     if batched:
-        workload = f"cfg4 SD1.5 attention linears x{len(probs)} (one batch) fwd+bwd, 16x16 tiles, 3 sigma, clamp 80"
+        workload = (f"cfg4 SD1.5 attention linears x{len(probs)} (one batch) fwd+bwd, {args.tile}x{args.tile} "
+                    "tiles, 3 sigma, clamp 80")
         shape = {"layers": len(probs), "sum_out_x_in": int(total["elements"]), "k_per_layer": 1024}
     else:
         p = probs[0]
-        workload = f"{p.name} fwd+bwd, 16x16 tiles, 3 sigma, clamp 80"
+        workload = f"{p.name} fwd+bwd, {args.tile}x{args.tile} tiles, 3 sigma, clamp 80"
         shape = {"out_features": p.out_features, "in_features": p.in_features, "k": p.k}
     out = {
         "metric": METRIC,
@@ -477,7 +482,7 @@ def main() -> int:
         else:
             sub = probs
             note = f"{probs[0].name} seed {args.seed}, the full layer"
-        out["cpu_baseline"] = cpu_baseline(sub, args.cpu_reps, note)
+        out["cpu_baseline"] = cpu_baseline(sub, args.cpu_reps, note, args.tile)
     print(json.dumps(out), flush=True)
     return 0
 

@@ -1079,18 +1079,43 @@ __device__ inline void tile_range(const int64_t* __restrict__ tile_ptr, int64_t 
 // Tile t (16x16) of one field by one wave.  The tile's ids come from the masks (p.W > 0: the
 // set bits of rowmask[tr] & colmask[tc], in ascending order, written to the tile's segment) or
 // from k_emit's segment (ordered here by a rank sort and written back where they moved).
+// The 16x16 block of pixels one wave of the tile kernels handles.  16x16 tiles: tile
+// idx * 4 + wave.  32x32 tiles (tile_out == tile_in == 32): tile idx, quadrant `wave` (pixel
+// rows / columns 16 * (wave >> 1), 16 * (wave & 1) of the tile), all four from the tile's own
+// id list.  sidx numbers the blocks for the backward's accumulator stripes.
+struct SubTile {
+  int64_t t;
+  int32_t r0, c0;
+  int32_t quad;
+  int64_t sidx;
+};
+
+__device__ inline SubTile sub_tile(const Problem& p, int64_t idx, int wave) {
+  SubTile st;
+  const bool q32 = p.tile_out == 32;
+  st.t = q32 ? idx : idx * 4 + wave;
+  st.quad = q32 ? wave : 0;
+  const int64_t tr = st.t / p.C, tc = st.t - (st.t / p.C) * p.C;
+  st.r0 = (int32_t)tr * p.tile_out + 16 * (st.quad >> 1);
+  st.c0 = (int32_t)tc * p.tile_in + 16 * (st.quad & 1);
+  st.sidx = q32 ? idx * 4 + wave : st.t;
+  return st;
+}
+
 __device__ __forceinline__ void render16_body(
     const Problem& p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids,
     int64_t capacity, float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
-    const uint32_t* __restrict__ colmask, int64_t t) {
+    const uint32_t* __restrict__ colmask, const SubTile& st) {
   __shared__ int32_t wkeys[kTileThreads / 64][kWaveSortKeys];
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
+  const int64_t t = st.t;
   if (t >= (int64_t)p.R * p.C) return;
   const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (t / p.C) * p.C);
-  const int32_t pr = tr * 16 + (lane >> 2), pc = tc * 16 + ((lane & 3) << 2);
+  const bool write_ids = st.quad == 0;  // one wave of a 32x32 tile writes its ids
+  const int32_t pr = st.r0 + (lane >> 2), pc = st.c0 + ((lane & 3) << 2);
   // coordinates first: they do not depend on the tile's segment
   const float x = row_coords[min(pr, p.M - 1)];
   float y[4];
@@ -1163,7 +1188,7 @@ __device__ __forceinline__ void render16_body(
             const int32_t g = keys[j0 + lane];
             my = load_eval(ev, g);
             const int64_t slot = done + j0 + lane;
-            if (slot < room) ids[s + slot] = g;
+            if (write_ids && slot < room) ids[s + slot] = g;
           }
           run_chunk(my, nj);
         }
@@ -1171,7 +1196,7 @@ __device__ __forceinline__ void render16_body(
         wave_sync();
       }
     }
-    if (lane == 0) {
+    if (lane == 0 && write_ids) {
       if (done != count) set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);
       if (room < count) set_status(&hdr->status, GF_STATUS_CAPACITY);
     }
@@ -1241,7 +1266,7 @@ __global__ __launch_bounds__(kTileThreads) void k_render16(
     int64_t capacity, float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
     const uint32_t* __restrict__ colmask) {
   render16_body(p, row_coords, col_coords, ev, tile_ptr, ids, capacity, delta, ws, rowmask, colmask,
-                (int64_t)blockIdx.x * (kTileThreads / 64) + wave_id());
+                sub_tile(p, blockIdx.x, wave_id()));
 }
 
 // Any tile shape: each thread evaluates pixels p = tid, tid+256, ... of the tile.
@@ -1350,14 +1375,15 @@ __device__ __forceinline__ void bwd16_body(
     const float* __restrict__ col_coords, const float* __restrict__ mu,
     const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
     const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
-    uint8_t* ws, const BwdLayout& L, int64_t t) {
+    uint8_t* ws, const BwdLayout& L, const SubTile& st) {
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   float* acc = reinterpret_cast<float*>(ws + L.acc);
   const int lane = threadIdx.x & 63;
   const int64_t T = (int64_t)p.R * p.C;
+  const int64_t t = st.t;
   if (t >= T) return;
-  const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (t / p.C) * p.C);
-  const int32_t r0 = tr * 16, c0 = tc * 16;
+  const int32_t r0 = st.r0, c0 = st.c0;
+  const int64_t stripe = st.sidx & (p.S - 1);
   const int slot = lane >> 4, row = lane & 15;
   const int32_t pr = r0 + row;
   // This lane's row of dL/d(delta) (0 outside the matrix) and the tile's coordinates are
@@ -1439,7 +1465,7 @@ __device__ __forceinline__ void bwd16_body(
       if (g >= 0 && row >= 10) {
         const int k = row - 10;
         const float val = k == 0 ? v0 : k == 1 ? v1 : k == 2 ? v2 : k == 3 ? v3 : k == 4 ? v4 : m[5];
-        unsafeAtomicAdd(acc + 8 * ((int64_t)g * p.S + (t & (p.S - 1))) + k, val);
+        unsafeAtomicAdd(acc + 8 * ((int64_t)g * p.S + stripe) + k, val);
       }
     }
     tile_general = tile_general || chunk_general;
@@ -1496,7 +1522,7 @@ __device__ __forceinline__ void bwd16_body(
         if (lane == 15 && gj >= 0) {
 #pragma unroll
           for (int k = 0; k < 6; ++k)
-            unsafeAtomicAdd(acc + 8 * ((int64_t)gj * p.S + (t & (p.S - 1))) + k, mm[k]);
+            unsafeAtomicAdd(acc + 8 * ((int64_t)gj * p.S + stripe) + k, mm[k]);
         }
       }
     }
@@ -1513,7 +1539,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
     const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
     uint8_t* ws, BwdLayout L) {
   bwd16_body<TpIdx, GIdx>(p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gids,
-                          num_pairs, ws, L, (int64_t)blockIdx.x * (kTileThreads / 64) + wave_id());
+                          num_pairs, ws, L, sub_tile(p, blockIdx.x, wave_id()));
 }
 
 __device__ inline float wave_sum(float v) {
@@ -1733,19 +1759,30 @@ int make_problem(const gf_field_config* cfg, int64_t M, int64_t N, int64_t K, Pr
   }
   p->normalize = cfg->normalize ? 1 : 0;
   p->S = backward_stripes(K, R * C);
-  // Mask path (no emission kernel): 16x16 tiles, 1 <= K <= kMaskMaxK, a tile grid k_bin bins in
-  // LDS, and masks of a bounded total size.
+  // Mask path (no emission kernel): 16x16 or 32x32 tiles, 1 <= K <= kMaskMaxK, a tile grid
+  // k_bin bins in LDS, and masks of a bounded total size.
   p->W = 0;
-  if (p->tile_out == 16 && p->tile_in == 16 && K >= 1 && K <= kMaskMaxK && bin_counts_in_lds(C, K)) {
+  if (((p->tile_out == 16 && p->tile_in == 16) || (p->tile_out == 32 && p->tile_in == 32)) && K >= 1 &&
+      K <= kMaskMaxK && bin_counts_in_lds(C, K)) {
     const int64_t W = (K + 31) / 32;
     if ((R + C) * W <= kMaskMaxWords) p->W = (int32_t)W;
   }
   return GF_OK;
 }
 
-bool fast16(const Problem& p) { return p.tile_out == 16 && p.tile_in == 16; }
+// The 16x16-block tile kernels (k_render16 / k_bwd16 and their batched forms) run 16x16
+// tiles, and 32x32 tiles as four 16x16 quadrants; the render only on the mask path for 32x32
+// (its emission path sorts each tile's ids in place, which four waves cannot share).
+bool quad_tiles(const Problem& p) {
+  return (p.tile_out == 16 && p.tile_in == 16) || (p.tile_out == 32 && p.tile_in == 32);
+}
+bool quad_render(const Problem& p) { return quad_tiles(p) && (p.tile_out == 16 || p.W > 0); }
 
-unsigned wave_tile_grid(int64_t T) { return (unsigned)((T + kTileThreads / 64 - 1) / (kTileThreads / 64)); }
+// Workgroups of the 16x16-block tile kernels: four 16x16 tiles or one 32x32 tile each.
+int64_t quad_grid(const Problem& p) {
+  const int64_t T = (int64_t)p.R * p.C;
+  return p.tile_out == 32 ? T : (T + kTileThreads / 64 - 1) / (kTileThreads / 64);
+}
 
 
 // ------------------------------------------------------------------------------------------
@@ -1849,7 +1886,7 @@ __global__ __launch_bounds__(kTileThreads) void k_render16_batch(const uint8_t* 
                 ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws,
                 reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.rowmask),
                 reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.colmask),
-                ((int64_t)blockIdx.x - b0) * (kTileThreads / 64) + wave_id());
+                sub_tile(p, (int64_t)blockIdx.x - b0, wave_id()));
 }
 
 __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_bwd16_batch(const uint8_t* __restrict__ plan) {
@@ -1865,7 +1902,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
   bwd16_body<int64_t, int64_t>(p, grad, ly.row_coords, ly.col_coords, ly.mu, ly.chol_raw,
                                reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
                                ly.tile_ptr, ly.ids, P < ly.capacity ? P : ly.capacity, ly.bws, L,
-                               ((int64_t)blockIdx.x - b0) * (kTileThreads / 64) + wave_id());
+                               sub_tile(p, (int64_t)blockIdx.x - b0, wave_id()));
 }
 
 // dL/d(delta) pointers of layers base .. base + count - 1 (count <= kPtrChunk), passed by value.
@@ -1916,8 +1953,8 @@ void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, 
                 const float* cc, const float* mu, const float* raw, const GaussEval* ev,
                 const void* tile_ptr, const void* gids, int64_t num_pairs, uint8_t* ws,
                 const BwdLayout& L) {
-  if (fast16(p))
-    hipLaunchKernelGGL((k_bwd16<TP, GI>), dim3(wave_tile_grid((int64_t)p.R * p.C)), dim3(kTileThreads), 0, st,
+  if (quad_tiles(p))
+    hipLaunchKernelGGL((k_bwd16<TP, GI>), dim3((unsigned)quad_grid(p)), dim3(kTileThreads), 0, st,
                        p, grad, rc, cc, mu, raw, ev, reinterpret_cast<const TP*>(tile_ptr),
                        reinterpret_cast<const GI*>(gids), num_pairs, ws, L);
   else
@@ -2035,8 +2072,8 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
   const GaussEval* ev = reinterpret_cast<const GaussEval*>(ws + L.eval);
-  if (fast16(p))
-    hipLaunchKernelGGL(k_render16, dim3(wave_tile_grid(T)), dim3(kTileThreads), 0, st, p, row_coords,
+  if (quad_render(p))
+    hipLaunchKernelGGL(k_render16, dim3((unsigned)quad_grid(p)), dim3(kTileThreads), 0, st, p, row_coords,
                        col_coords, ev, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws,
                        reinterpret_cast<const uint32_t*>(ws + L.rowmask),
                        reinterpret_cast<const uint32_t*>(ws + L.colmask));
@@ -2125,8 +2162,9 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
                   size_t plan_bytes, gf_batch_info* info, void* stream) {
   if (!cfg || !info || n_layers < 0 || (n_layers > 0 && !layers))
     return set_err(GF_E_INVALID_ARGUMENT, "cfg / layers / info invalid");
-  if (cfg->tile_out != 16 || cfg->tile_in != 16)
-    return set_err(GF_E_INVALID_ARGUMENT, "batched fields need 16x16 tiles (got %lldx%lld)",
+  const bool t32 = cfg->tile_out == 32 && cfg->tile_in == 32;
+  if (!(cfg->tile_out == 16 && cfg->tile_in == 16) && !t32)
+    return set_err(GF_E_INVALID_ARGUMENT, "batched fields need 16x16 or 32x32 tiles (got %lldx%lld)",
                    (long long)cfg->tile_out, (long long)cfg->tile_in);
   const size_t n = (size_t)n_layers;
   BatchHeader h{};
@@ -2143,6 +2181,10 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
       return set_err(rc, "layer %zu: %s", i, why);
     }
     const int64_t T = (int64_t)ly.p.R * ly.p.C, K = in.k;
+    if (t32 && !quad_render(ly.p))
+      return set_err(GF_E_INVALID_ARGUMENT,
+                     "layer %zu: batched 32x32 tiles need the mask path (1 <= k <= %lld, tile columns within LDS)",
+                     i, (long long)kMaskMaxK);
     ly.fl = fwd_layout(ly.p);
     ly.bl = bwd_layout(ly.p);
     if (!in.forward_workspace || in.forward_workspace_bytes < ly.fl.total)
@@ -2175,7 +2217,7 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
     ly.tile_block0 = tile_blocks;
     ly.emit_block0 = emit_blocks;
     ly.finish_block0 = finish_blocks;
-    tile_blocks += (T + kTileThreads / 64 - 1) / (kTileThreads / 64);
+    tile_blocks += quad_grid(ly.p);
     const int64_t per_emit_block = (kEmitThreads / 64) * (64 / kEmitLanesBatch);
     if (ly.p.W == 0) emit_blocks += (K + per_emit_block - 1) / per_emit_block;  // emission path
     finish_blocks += (K * ly.p.S + kTileThreads - 1) / kTileThreads;

@@ -289,7 +289,7 @@ class GaussianFieldBatch:
     The forward reads back every layer's status and pair count once (one host synchronisation
     per step, where the reference synchronises per layer); a pair count past a layer's id
     capacity grows the capacities and renders again.  All layers must share the tile shape
-    (16x16: the batched kernels), sigma multiplier and normalisation.
+    (16x16 or 32x32: the batched kernels), sigma multiplier and normalisation.
     """
 
     def __init__(self, layers, *, headroom: float = 1.25):
@@ -305,10 +305,13 @@ class GaussianFieldBatch:
         cfgs = [ly.adapter_config for ly in self.layers]
         c0 = cfgs[0]
         for i, c in enumerate(cfgs):
-            if c.tile_out != 16 or c.tile_in != 16:
-                raise ValueError(f"layer {i}: batched fields need 16x16 tiles (got {c.tile_out}x{c.tile_in})")
-            if c.sigma_multiplier != c0.sigma_multiplier or c.normalize_gaussian != c0.normalize_gaussian:
-                raise ValueError(f"layer {i}: sigma_multiplier / normalize_gaussian differ from layer 0")
+            if (c.tile_out, c.tile_in) not in ((16, 16), (32, 32)):
+                raise ValueError(f"layer {i}: batched fields need 16x16 or 32x32 tiles "
+                                 f"(got {c.tile_out}x{c.tile_in})")
+            if (c.tile_out != c0.tile_out or c.sigma_multiplier != c0.sigma_multiplier
+                    or c.normalize_gaussian != c0.normalize_gaussian):
+                raise ValueError(f"layer {i}: tile shape / sigma_multiplier / normalize_gaussian differ "
+                                 "from layer 0")
         self.device = self.layers[0].weight.device
         if any(ly.weight.device != self.device for ly in self.layers):
             raise ValueError("all layers must live on one device")
@@ -339,8 +342,8 @@ class GaussianFieldBatch:
             self._mu_bufs.append(v.mu)
             views.append(v)
         c0 = self.layers[0].adapter_config
-        self._plan = FieldBatchPlan(views, self.device, capacities=self._caps,
-                                    sigma_multiplier=c0.sigma_multiplier,
+        self._plan = FieldBatchPlan(views, self.device, capacities=self._caps, tile_out=c0.tile_out,
+                                    tile_in=c0.tile_in, sigma_multiplier=c0.sigma_multiplier,
                                     normalize=c0.normalize_gaussian, clamp_quad=CLAMP_QUAD)
         self._key = self._param_key()
 

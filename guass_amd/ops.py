@@ -127,7 +127,7 @@ class FieldBatchPlan:
     ``mu``, ``chol_raw``, ``amp`` and, for the backward, ``grad`` (dL/d(delta), read in place at
     every ``backward()``).  The plan keeps references to them: their storage must stay put.
     Each layer gets the buffers of a :class:`FieldPlan` (``self.plans[i]``: delta, tile_ptr,
-    ids, pair constants, gradients).  16x16 tiles only.
+    ids, pair constants, gradients).  16x16 or 32x32 tiles (32x32: every layer's K <= 8192).
     """
 
     def __init__(self, layers, device, *, capacities, tile_out: int = 16, tile_in: int = 16,

@@ -155,9 +155,10 @@ int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t
 
 /*
  * Batched fields (no single-call counterpart in the reference, which renders each adapted
- * layer separately, gaussian_linear.py:162-220; this is the batched launch of BASELINE's
- * SD1.5 configuration).  Every phase runs as one launch over all layers, each layer with the
- * buffers its single-field calls would use.  16x16 tiles only; int64 ids.
+ * layer separately, gaussian_linear.py:162-220; this is the batched launch of an SD1.5
+ * UNet's adapted attention layers).  Every phase runs as one launch over all layers, each layer with the
+ * buffers its single-field calls would use.  16x16 or 32x32 tiles (32x32 needs every layer on the
+ * mask path: K <= 8192); int64 ids.
  */
 typedef struct gf_layer {
   int64_t out_features, in_features, k;

@@ -125,6 +125,40 @@ def test_tiles_32x32(device):
     check(wl.cfg1(0), device, tile_out=32, tile_in=32)
 
 
+@pytest.mark.parametrize("which", ["cfg3", "ragged", "cfg2"])
+def test_tiles_32x32_quadrants(device, which):
+    """32x32 tiles (the reference's training configs, configs/dreambooth_sd*.yaml:27-28): four
+    16x16 quadrant waves per tile on the mask path."""
+    p = {"cfg3": lambda: wl.cfg3(4), "ragged": lambda: tiny_problem(100, 90, 40, 14),
+         "cfg2": lambda: wl.cfg2(6)}[which]()
+    check(p, device, tile_out=32, tile_in=32)
+
+
+def test_tiles_32x32_emission_path(device):
+    # K > 8192: emission path; the render stays on the any-shape kernel, the backward on quadrants
+    p = tiny_problem(96, 112, 9000, 15, log_scale_px=-1.0, spread=0.3)
+    check(p, device, batched=True, tile_out=32, tile_in=32)
+
+
+def test_batch_32x32_tiles(device):
+    from guass_amd.ops import FieldBatchPlan
+
+    probs = [wl.cfg1(3), wl.cfg2(4), tiny_problem(45, 70, 12, 12)]
+    singles = [run_gpu(p, device, tile_out=32, tile_in=32) for p in probs]
+    batch = FieldBatchPlan([p.to(device) for p in probs], device, capacities=[int(s[1][-1]) for s in singles],
+                           tile_out=32, tile_in=32)
+    batch.forward()
+    batch.backward()
+    torch.cuda.synchronize()
+    assert batch.status() == [0] * len(probs)
+    for i, (pl, sg) in enumerate(zip(batch.plans, singles)):
+        P = int(sg[1][-1])
+        assert torch.equal(pl.tile_ptr, sg[1]) and torch.equal(pl.ids[:P], sg[2]), f"layer {i}: binning"
+        assert torch.equal(pl.delta, sg[0]), f"layer {i}: delta"
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), sg[3:]):
+            grad_close(a, b, f"layer {i} {name}", rtol=1e-5)
+
+
 def test_tiles_8x24(device):
     check(tiny_problem(100, 90, 40, 5), device, tile_out=8, tile_in=24)
 
@@ -489,7 +523,8 @@ def test_gaussian_linear_layer(device, tile):
     assert float((y - want).abs().max()) <= 1e-5 * float(want.abs().max())
 
 
-def test_gaussian_field_batch_matches_per_layer(device):
+@pytest.mark.parametrize("tile", [16, 32])
+def test_gaussian_field_batch_matches_per_layer(device, tile):
     """GaussianFieldBatch.render() (one batched launch per phase for every layer, autograd
     through it) against each GaussianLinear rendering its own delta-W, over two training steps
     (parameters updated in between) with layers of different shapes and one layer whose forward
@@ -502,7 +537,7 @@ def test_gaussian_field_batch_matches_per_layer(device):
     shapes = [(96, 80, 48), (64, 64, 24), (120, 40, 36)]  # (in, out, K)
     layers_a, layers_b = [], []
     for i, (n_in, n_out, k) in enumerate(shapes):
-        cfg = GaussianAdapterConfig(init_num_gaussians=k, tile_out=16, tile_in=16, adapter_scale=0.5,
+        cfg = GaussianAdapterConfig(init_num_gaussians=k, tile_out=tile, tile_in=tile, adapter_scale=0.5,
                                     init_amp_scale=1e-2)
         la = GaussianLinear(n_in, n_out, adapter_config=cfg, device=device)
         with torch.no_grad():

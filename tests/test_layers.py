@@ -43,7 +43,10 @@ def test_field_batch_checks_layer_configs():
 
     ok = GaussianAdapterConfig(init_num_gaussians=4, tile_out=16, tile_in=16)
     a = GaussianLinear(32, 32, adapter_config=ok)
-    with pytest.raises(ValueError, match="16x16"):
+    with pytest.raises(ValueError, match="16x16 or 32x32"):
+        GaussianFieldBatch([a, GaussianLinear(32, 32, adapter_config=GaussianAdapterConfig(
+            init_num_gaussians=4, tile_out=8, tile_in=8))])
+    with pytest.raises(ValueError, match="tile shape"):  # 32x32 next to 16x16
         GaussianFieldBatch([a, GaussianLinear(32, 32, adapter_config=GaussianAdapterConfig(init_num_gaussians=4))])
     other = GaussianAdapterConfig(init_num_gaussians=4, tile_out=16, tile_in=16, sigma_multiplier=2.5)
     with pytest.raises(ValueError, match="sigma_multiplier"):
