@@ -179,7 +179,7 @@ def model_bench(args) -> int:
         layers.append(ly)
     grads = [p.grad.to(dev).reshape(p.out_features, p.in_features) for p in probs]
     params = [t for ly in layers for t in (ly.mu_raw, ly.chol_raw, ly.amp)]
-    fb = GaussianFieldBatch(layers)
+    fb = GaussianFieldBatch(layers, k_capacity=2 * max(p.k for p in probs))
 
     def batched():
         torch.autograd.backward(fb.render(), grads)
@@ -206,6 +206,7 @@ def model_bench(args) -> int:
 
     t_batch = timed(batched, args.steps, args.warmup)
     t_single = timed(per_layer, max(1, args.steps // 5), max(1, args.warmup // 5))
+    densify = densify_costs(fb, layers, batched, params)
     elements = float(sum(p.out_features * p.in_features for p in probs))
     out = {
         "metric": "ΔW elements/sec fwd+bwd of the SD1.5 attention layers through the layer API",
@@ -218,9 +219,46 @@ def model_bench(args) -> int:
                    "sum_out_x_in": int(elements), "k_per_layer": 1024},
         "per_layer_ms_per_step": t_single * 1e3,
         "speedup_vs_per_layer": t_single / t_batch,
+        "densify": densify,
     }
     print(json.dumps(out), flush=True)
     return 0
+
+
+def densify_costs(fb, layers, step, params) -> dict:
+    """Cost of a densification event (the reference clones up to max_new_gaussians_per_step = 2
+    Gaussians per layer every 50 steps, configs/dreambooth_sd_k*_densify.yaml:55-62): every
+    layer's parameters replaced by tensors with two more Gaussians, then the in-place re-plan,
+    the first step after it, and a plan built from scratch for comparison."""
+    import torch
+
+    from guass_amd.layers import GaussianFieldBatch
+
+    allocs = sum(pl.allocations for pl in fb._plan.plans)
+    for ly in layers:
+        idx = torch.tensor([0, 1], device=ly.mu_raw.device)
+        p = ly.get_gaussian_parameters()
+        ly.replace_gaussian_parameters_(mu_raw=torch.cat([p["mu_raw"].detach(), p["mu_raw"].detach()[idx]]),
+                                        chol_raw=torch.cat([p["chol_raw"].detach(), p["chol_raw"].detach()[idx]]),
+                                        amp=torch.cat([p["amp"].detach(), p["amp"].detach()[idx]]))
+    params[:] = [t for ly in layers for t in (ly.mu_raw, ly.chol_raw, ly.amp)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    fb._build()
+    torch.cuda.synchronize()
+    replan = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    step()
+    torch.cuda.synchronize()
+    first = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    fresh = GaussianFieldBatch(layers, k_capacity=fb._kcaps)
+    fresh._build()
+    torch.cuda.synchronize()
+    rebuild = time.perf_counter() - t0
+    return {"replan_in_place_ms": replan * 1e3, "first_step_after_ms": first * 1e3,
+            "plan_from_scratch_ms": rebuild * 1e3,
+            "buffers_reallocated": sum(pl.allocations for pl in fb._plan.plans) - allocs}
 
 
 def delta_apply_bench(args) -> int:

@@ -1871,6 +1871,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_batch(const uint8_t* __re
   int64_t b0;
   const BatchLayer& ly = batch_layer(plan, h->emit_map_off, &b0, 1);
   const Problem p = ly.p;
+  if (p.W > 0) return;  // blocks kept for a capacity on the emission path; k is on the mask path
   const FwdLayout L = ly.fl;
   emit_body<false, kEmitLanesBatch, 2>(
       p, ly.mu, ly.amp, ly.fws, L, ly.tile_ptr, ly.ids, ly.capacity,
@@ -2181,6 +2182,12 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
       return set_err(rc, "layer %zu: %s", i, why);
     }
     const int64_t T = (int64_t)ly.p.R * ly.p.C, K = in.k;
+    if (in.k_capacity < 0) return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: k_capacity < 0", i);
+    // Grids for the capacity: a layer on the emission path at any k <= kc keeps its emit blocks.
+    const int64_t kc = std::max<int64_t>(K, in.k_capacity);
+    Problem pc;
+    rc = make_problem(cfg, in.out_features, in.in_features, kc, &pc);
+    if (rc) return set_err(rc, "layer %zu: k_capacity %lld invalid", i, (long long)kc);
     if (t32 && !quad_render(ly.p))
       return set_err(GF_E_INVALID_ARGUMENT,
                      "layer %zu: batched 32x32 tiles need the mask path (1 <= k <= %lld, tile columns within LDS)",
@@ -2219,8 +2226,8 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
     ly.finish_block0 = finish_blocks;
     tile_blocks += quad_grid(ly.p);
     const int64_t per_emit_block = (kEmitThreads / 64) * (64 / kEmitLanesBatch);
-    if (ly.p.W == 0) emit_blocks += (K + per_emit_block - 1) / per_emit_block;  // emission path
-    finish_blocks += (K * ly.p.S + kTileThreads - 1) / kTileThreads;
+    if (ly.p.W == 0 || pc.W == 0) emit_blocks += (kc + per_emit_block - 1) / per_emit_block;  // emission path
+    finish_blocks += (kc * ly.p.S + kTileThreads - 1) / kTileThreads;
   }
   if (tile_blocks >= INT32_MAX || emit_blocks >= INT32_MAX)
     return set_err(GF_E_INVALID_ARGUMENT, "batch too large for one launch");

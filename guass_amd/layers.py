@@ -290,9 +290,15 @@ class GaussianFieldBatch:
     per step, where the reference synchronises per layer); a pair count past a layer's id
     capacity grows the capacities and renders again.  All layers must share the tile shape
     (16x16 or 32x32: the batched kernels), sigma multiplier and normalisation.
+
+    Densification (the reference trainer's clone / prune, base_trainer.py:126-220) replaces a
+    layer's Gaussian parameters with tensors of another K; the next render() re-plans in place.
+    ``k_capacity`` (an int for every layer, or one per layer; e.g. the densify config's
+    ``max_gaussians_per_layer``) sizes the buffers so that K changes up to it allocate nothing;
+    past it a layer's capacity doubles.
     """
 
-    def __init__(self, layers, *, headroom: float = 1.25):
+    def __init__(self, layers, *, headroom: float = 1.25, k_capacity=None):
         from guass_amd import _native as Nat
 
         self._Nat = Nat
@@ -319,7 +325,16 @@ class GaussianFieldBatch:
         self._plan = None
         self._key = None
         self._caps = [ly.num_gaussians * 32 for ly in self.layers]  # grown from the read-back
+        if k_capacity is None or isinstance(k_capacity, int):
+            kc = [max(int(k_capacity or 0), ly.num_gaussians) for ly in self.layers]
+        else:
+            kc = [max(int(c), ly.num_gaussians) for c, ly in zip(k_capacity, self.layers, strict=True)]
+        self._kcaps = kc
+        self._ks = [ly.num_gaussians for ly in self.layers]
+        self._pairs = None
+        self._mu_store: list[Tensor] = []
         self._zero_grads: dict[int, Tensor] = {}
+        self.replans = 0  # re-plans after the first plan (parameter tensors or K changed)
 
     # ---------------------------------------------------------------- plan
 
@@ -327,24 +342,45 @@ class GaussianFieldBatch:
         return tuple((ly.num_gaussians, ly.chol_raw.data_ptr(), ly.amp.data_ptr()) for ly in self.layers)
 
     def _build(self) -> None:
+        """Plans, or re-plans in place, for the layers' current K and parameter tensors."""
         from guass_amd.ops import FieldBatchPlan
 
         class _View:
             pass
 
-        views, self._mu_bufs = [], []
-        for ly in self.layers:
+        for i, ly in enumerate(self.layers):
+            K = ly.num_gaussians
+            if K > self._kcaps[i]:
+                self._kcaps[i] = max(K, 2 * self._kcaps[i])
+            if K != self._ks[i] and self._pairs is not None and self._ks[i] > 0:
+                # pairs scale with K: grow the id capacity with it rather than by a retry
+                self._caps[i] = max(self._caps[i], int(self._pairs[i] * K / self._ks[i] * self.headroom) + 1)
+            self._ks[i] = K
+        views = []
+        for i, ly in enumerate(self.layers):
+            K = ly.num_gaussians
+            if i == len(self._mu_store) or self._mu_store[i].shape[0] < K:
+                store = torch.empty(self._kcaps[i], 2, dtype=torch.float32, device=self.device)
+                if i == len(self._mu_store):
+                    self._mu_store.append(store)
+                else:
+                    self._mu_store[i] = store
             v = _View()
             v.row_coords, v.col_coords = ly.row_coords, ly.col_coords
-            v.mu = torch.empty_like(ly.mu_raw, dtype=torch.float32).contiguous()
+            v.mu = self._mu_store[i][:K]
             v.chol_raw, v.amp = ly.chol_raw, ly.amp
             v.grad = None
-            self._mu_bufs.append(v.mu)
             views.append(v)
-        c0 = self.layers[0].adapter_config
-        self._plan = FieldBatchPlan(views, self.device, capacities=self._caps, tile_out=c0.tile_out,
-                                    tile_in=c0.tile_in, sigma_multiplier=c0.sigma_multiplier,
-                                    normalize=c0.normalize_gaussian, clamp_quad=CLAMP_QUAD)
+        self._mu_bufs = [v.mu for v in views]
+        if self._plan is None:
+            c0 = self.layers[0].adapter_config
+            self._plan = FieldBatchPlan(views, self.device, capacities=self._caps, k_capacities=self._kcaps,
+                                        tile_out=c0.tile_out, tile_in=c0.tile_in,
+                                        sigma_multiplier=c0.sigma_multiplier,
+                                        normalize=c0.normalize_gaussian, clamp_quad=CLAMP_QUAD)
+        else:
+            self._plan.update(views, capacities=self._caps, k_capacities=self._kcaps)
+            self.replans += 1
         self._key = self._param_key()
 
     # ---------------------------------------------------------------- passes
@@ -404,7 +440,7 @@ class GaussianFieldBatch:
         self._plan.backward()
         # one copy of every layer's gradients (the plan's buffer is rewritten by the next
         # backward), then d mu_raw = d mu * (1 - mu^2)
-        flat = self._plan.grad_flat.clone()
+        flat = self._plan.grad_flat[:self._plan.grad_numel].clone()
         d_mu, d_chol, d_amp = [], [], []
         o = 0
         for pl in self._plan.plans:

@@ -18,10 +18,16 @@ from guass_amd import _native as N
 
 
 class FieldPlan:
+    """Device buffers of one field's forward and backward, sized for ``k_capacity`` Gaussians
+    (default ``k``): :meth:`resize` moves to another K (densification clones and prunes
+    Gaussians, reference controllers/clone.py:31-56, prune.py:34-45) and allocates only when a
+    buffer must grow, so K changes within the capacity allocate nothing."""
+
     def __init__(self, out_features: int, in_features: int, k: int, device, *, tile_out: int = 16,
                  tile_in: int = 16, sigma_multiplier: float = 3.0, normalize: bool = False,
-                 clamp_quad: float | None = 80.0, ids_capacity: int | None = None):
-        self.M, self.N, self.K = int(out_features), int(in_features), int(k)
+                 clamp_quad: float | None = 80.0, ids_capacity: int | None = None,
+                 k_capacity: int | None = None, grads: bool = True):
+        self.M, self.N = int(out_features), int(in_features)
         self.device = torch.device(device)
         self.cfg = N.make_config(tile_out, tile_in, sigma_multiplier, normalize, clamp_quad)
         L = N.lib()
@@ -30,21 +36,61 @@ class FieldPlan:
                                ctypes.byref(C)), "gf_tile_grid")
         self.num_tile_rows, self.num_tile_cols = R.value, C.value
         self.T = R.value * C.value
-        if ids_capacity is None:
-            ids_capacity = self.K * self.T  # every Gaussian on every tile
-        self.capacity = int(ids_capacity)
         dev = self.device
-        self.fwd_ws_bytes = L.gf_forward_workspace_bytes(self.M, self.N, self.K, ctypes.byref(self.cfg))
-        self.bwd_ws_bytes = L.gf_backward_workspace_bytes(self.M, self.N, self.K, ctypes.byref(self.cfg))
-        self.fwd_ws = torch.empty(self.fwd_ws_bytes, dtype=torch.uint8, device=dev)
-        self.bwd_ws = torch.zeros(self.bwd_ws_bytes, dtype=torch.uint8, device=dev)  # self-cleaning
         self.tile_ptr = torch.empty(self.T + 1, dtype=torch.int64, device=dev)
         self.num_pairs = torch.empty(1, dtype=torch.int64, device=dev)
-        self.ids = torch.empty(max(self.capacity, 1), dtype=torch.int64, device=dev)
         self.delta = torch.empty(self.M * self.N, dtype=torch.float32, device=dev)
-        self.d_mu = torch.empty(self.K, 2, dtype=torch.float32, device=dev)
-        self.d_chol_raw = torch.empty(self.K, 3, dtype=torch.float32, device=dev)
-        self.d_amp = torch.empty(self.K, 1, dtype=torch.float32, device=dev)
+        self._own_grads = bool(grads)
+        self.K = self.k_capacity = self.capacity = 0
+        self.fwd_ws_bytes = self.bwd_ws_bytes = 0
+        self.fwd_ws = self.bwd_ws = self.ids = None
+        self._d_mu = self._d_chol_raw = self._d_amp = None
+        self.allocations = 0  # buffer (re)allocations made by resize()
+        if ids_capacity is None:
+            ids_capacity = int(k) * self.T  # every Gaussian on every tile
+        self.resize(k, ids_capacity=ids_capacity, k_capacity=k_capacity)
+
+    def resize(self, k: int, *, ids_capacity: int | None = None, k_capacity: int | None = None) -> bool:
+        """Moves the plan to ``k`` Gaussians (and at least ``ids_capacity`` gaussian ids); the
+        capacities only grow.  Returns True when a buffer was reallocated."""
+        k = int(k)
+        if k < 0:
+            raise ValueError("k must be >= 0")
+        L = N.lib()
+        kc = max(k, int(k_capacity or 0), self.k_capacity)
+        dev, grew = self.device, False
+
+        def need(fn, kk):
+            return int(fn(self.M, self.N, kk, ctypes.byref(self.cfg)))
+
+        fwd = need(L.gf_forward_workspace_bytes, k)
+        if self.fwd_ws is None or self.fwd_ws.numel() < fwd:
+            self.fwd_ws = torch.empty(max(fwd, need(L.gf_forward_workspace_bytes, kc)), dtype=torch.uint8,
+                                      device=dev)
+            grew = True
+        bwd = need(L.gf_backward_workspace_bytes, k)
+        if self.bwd_ws is None or self.bwd_ws.numel() < bwd:
+            # zeroed once: every backward leaves its accumulators zero again
+            self.bwd_ws = torch.zeros(max(bwd, need(L.gf_backward_workspace_bytes, kc)), dtype=torch.uint8,
+                                      device=dev)
+            grew = True
+        ids = max(int(ids_capacity if ids_capacity is not None else self.capacity), 1)
+        if self.ids is None or self.ids.numel() < ids:
+            self.ids = torch.empty(ids, dtype=torch.int64, device=dev)
+            grew = True
+        if self._own_grads and (self._d_mu is None or self._d_mu.shape[0] < k):
+            rows = max(k, kc)
+            self._d_mu = torch.empty(rows, 2, dtype=torch.float32, device=dev)
+            self._d_chol_raw = torch.empty(rows, 3, dtype=torch.float32, device=dev)
+            self._d_amp = torch.empty(rows, 1, dtype=torch.float32, device=dev)
+            grew = True
+        if self._own_grads:
+            self.d_mu, self.d_chol_raw, self.d_amp = self._d_mu[:k], self._d_chol_raw[:k], self._d_amp[:k]
+        self.K, self.k_capacity = k, kc
+        self.fwd_ws_bytes, self.bwd_ws_bytes = self.fwd_ws.numel(), self.bwd_ws.numel()
+        self.capacity = self.ids.numel()
+        self.allocations += int(grew)
+        return grew
 
     def _stream(self) -> int:
         return N.stream_handle(self.device)
@@ -125,26 +171,62 @@ class FieldBatchPlan:
 
     ``layers`` is a sequence of objects with device tensors ``row_coords``, ``col_coords``,
     ``mu``, ``chol_raw``, ``amp`` and, for the backward, ``grad`` (dL/d(delta), read in place at
-    every ``backward()``).  The plan keeps references to them: their storage must stay put.
-    Each layer gets the buffers of a :class:`FieldPlan` (``self.plans[i]``: delta, tile_ptr,
-    ids, pair constants, gradients).  16x16 or 32x32 tiles (32x32: every layer's K <= 8192).
+    every ``backward()``).  The plan keeps references to them: their storage must stay put until
+    the next :meth:`update`.  Each layer gets the buffers of a :class:`FieldPlan`
+    (``self.plans[i]``: delta, tile_ptr, ids, pair constants, gradients).  16x16 or 32x32 tiles
+    (32x32: every layer's K <= 8192).
+
+    ``k_capacities`` sizes each layer's buffers and the launch grids for that many Gaussians:
+    after a layer's K or tensors change (densification), :meth:`update` re-plans in place, and
+    for K within the capacities the launch grids and the plan buffer stay the same, so
+    launches captured in a graph remain valid.
     """
 
-    def __init__(self, layers, device, *, capacities, tile_out: int = 16, tile_in: int = 16,
-                 sigma_multiplier: float = 3.0, normalize: bool = False,
+    def __init__(self, layers, device, *, capacities, k_capacities=None, tile_out: int = 16,
+                 tile_in: int = 16, sigma_multiplier: float = 3.0, normalize: bool = False,
                  clamp_quad: float | None = 80.0):
         self.device = torch.device(device)
-        self.layers = list(layers)
         self.cfg = N.make_config(tile_out, tile_in, sigma_multiplier, normalize, clamp_quad)
-        self.plans = [FieldPlan(int(ly.row_coords.numel()), int(ly.col_coords.numel()), int(ly.mu.shape[0]),
-                                self.device, tile_out=tile_out, tile_in=tile_in,
-                                sigma_multiplier=sigma_multiplier, normalize=normalize,
-                                clamp_quad=clamp_quad, ids_capacity=int(c))
-                      for ly, c in zip(self.layers, capacities)]
+        self._plan_kwargs = dict(tile_out=tile_out, tile_in=tile_in, sigma_multiplier=sigma_multiplier,
+                                 normalize=normalize, clamp_quad=clamp_quad)
+        self.plans: list[FieldPlan] = []
+        self.plan = None
+        self.info = None
+        self.grad_flat = None
+        self.update(layers, capacities=capacities, k_capacities=k_capacities)
+
+    def update(self, layers=None, *, capacities=None, k_capacities=None) -> bool:
+        """Re-plans for ``layers`` (default: the current ones, re-read): each layer's K and
+        tensors, with at least ``capacities`` gaussian ids and ``k_capacities`` Gaussians per
+        layer.  Buffers grow only when they must.  Returns True when the launch grids and the
+        plan buffer are unchanged (graphs captured over forward() / backward() stay valid).
+        Synchronises the stream (the plan is uploaded from host memory)."""
+        if layers is not None:
+            layers = list(layers)
+            if self.plans and len(layers) != len(self.plans):
+                raise ValueError(f"expected {len(self.plans)} layers, got {len(layers)}")
+            self.layers = layers
+        n = len(self.layers)
+        caps = list(capacities) if capacities is not None else [None] * n
+        kcs = list(k_capacities) if k_capacities is not None else [None] * n
+        if len(caps) != n or len(kcs) != n:
+            raise ValueError("capacities / k_capacities need one entry per layer")
+        for i, ly in enumerate(self.layers):
+            M, Nf, K = int(ly.row_coords.numel()), int(ly.col_coords.numel()), int(ly.mu.shape[0])
+            if i < len(self.plans):
+                pl = self.plans[i]
+                if (pl.M, pl.N) != (M, Nf):
+                    raise ValueError(f"layer {i}: shape {M}x{Nf} differs from the planned {pl.M}x{pl.N}")
+                pl.resize(K, ids_capacity=caps[i], k_capacity=kcs[i])
+            else:
+                self.plans.append(FieldPlan(M, Nf, K, self.device, ids_capacity=caps[i],
+                                            k_capacity=kcs[i], grads=False, **self._plan_kwargs))
         # Every layer's gradients in one buffer (per layer: d_mu [K,2], d_chol_raw [K,3],
         # d_amp [K,1]), so that they can be copied out with one launch.
-        self.grad_flat = torch.empty(max(sum(6 * pl.K for pl in self.plans), 1), dtype=torch.float32,
-                                     device=self.device)
+        self.grad_numel = sum(6 * pl.K for pl in self.plans)
+        if self.grad_flat is None or self.grad_flat.numel() < self.grad_numel:
+            self.grad_flat = torch.empty(max(sum(6 * pl.k_capacity for pl in self.plans), 1),
+                                         dtype=torch.float32, device=self.device)
         o = 0
         for pl in self.plans:
             K = pl.K
@@ -152,7 +234,7 @@ class FieldBatchPlan:
             pl.d_chol_raw = self.grad_flat[o + 2 * K:o + 5 * K].view(K, 3)
             pl.d_amp = self.grad_flat[o + 5 * K:o + 6 * K].view(K, 1)
             o += 6 * K
-        table = (N.GfLayer * max(len(self.plans), 1))()
+        table = (N.GfLayer * max(n, 1))()
         for i, (ly, pl) in enumerate(zip(self.layers, self.plans)):
             grad = getattr(ly, "grad", None)
             table[i] = N.GfLayer(
@@ -161,15 +243,21 @@ class FieldBatchPlan:
                 pl.num_pairs.data_ptr(), pl.ids.data_ptr(), pl.capacity,
                 pl.fwd_ws.data_ptr(), pl.fwd_ws_bytes, None if grad is None else grad.data_ptr(),
                 N.ptr(pl.d_mu), N.ptr(pl.d_chol_raw), N.ptr(pl.d_amp), pl.bwd_ws.data_ptr(),
-                pl.bwd_ws_bytes)
-        self.info = N.GfBatchInfo()
+                pl.bwd_ws_bytes, pl.k_capacity)
+        info = N.GfBatchInfo()
         L = N.lib()
-        n = len(self.plans)
-        N.check(L.gf_batch_plan(ctypes.byref(self.cfg), table, n, None, 0, ctypes.byref(self.info),
+        N.check(L.gf_batch_plan(ctypes.byref(self.cfg), table, n, None, 0, ctypes.byref(info),
                                 self._stream()), "gf_batch_plan (size)")
-        self.plan = torch.empty(max(int(self.info.plan_bytes), 256), dtype=torch.uint8, device=self.device)
+        old, old_plan = self.info, self.plan
+        if self.plan is None or self.plan.numel() < int(info.plan_bytes):
+            self.plan = torch.empty(max(int(info.plan_bytes), 256), dtype=torch.uint8, device=self.device)
         N.check(L.gf_batch_plan(ctypes.byref(self.cfg), table, n, self.plan.data_ptr(), self.plan.numel(),
-                                ctypes.byref(self.info), self._stream()), "gf_batch_plan")
+                                ctypes.byref(info), self._stream()), "gf_batch_plan")
+        self.info = info
+        self._grads = None
+        return (old is not None and self.plan is old_plan and
+                (old.tile_blocks, old.emit_blocks, old.finish_blocks) ==
+                (info.tile_blocks, info.emit_blocks, info.finish_blocks))
 
     def _stream(self) -> int:
         return N.stream_handle(self.device)

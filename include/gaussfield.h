@@ -180,6 +180,12 @@ typedef struct gf_layer {
   float* d_amp;                  /* backward only: [k,1] out */
   void* backward_workspace;      /* backward only: gf_backward_workspace_bytes, zeroed once */
   size_t backward_workspace_bytes;
+  /* Launch grids and block maps are sized for max(k, k_capacity) Gaussians (0: k).  Densified
+   * adapters change k every few hundred steps (reference controllers/clone.py:31-56,
+   * prune.py:34-45); re-planned for any k <= k_capacity into the same plan buffer, the plan keeps
+   * its gf_batch_info, so launches captured in a graph stay valid.  The buffers above must be
+   * sized for the current k only. */
+  int64_t k_capacity;
 } gf_layer;
 
 typedef struct gf_batch_info {

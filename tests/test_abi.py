@@ -164,3 +164,53 @@ def test_product_path_has_no_cpu_fallback(monkeypatch, tmp_path):
     monkeypatch.setattr(N, "LIB_PATH", tmp_path / "missing.so")
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         N.lib()
+
+
+def _batch_info(layers_mnk, *, tile=16, k_capacity=0):
+    """gf_batch_plan's size query (host only: no device memory is touched) for layers of the
+    given (out, in, k); the pointer fields hold placeholder addresses."""
+    lib = N.lib()
+    cfg = _cfg(tile_out=tile, tile_in=tile)
+    fake = 0x10000
+    table = (N.GfLayer * len(layers_mnk))()
+    for i, (m, n, k) in enumerate(layers_mnk):
+        fwd = lib.gf_forward_workspace_bytes(m, n, k, ctypes.byref(cfg))
+        bwd = lib.gf_backward_workspace_bytes(m, n, k, ctypes.byref(cfg))
+        table[i] = N.GfLayer(m, n, k, fake, fake, fake, fake, fake, fake, fake, fake, fake, 1, fake, fwd,
+                             None, fake, fake, fake, fake, bwd, k_capacity)
+    info = N.GfBatchInfo()
+    rc = lib.gf_batch_plan(ctypes.byref(cfg), table, len(layers_mnk), None, 0, ctypes.byref(info), None)
+    assert rc == 0, lib.gf_last_error().decode()
+    return (info.tile_blocks, info.emit_blocks, info.finish_blocks, info.plan_bytes)
+
+
+@pytest.mark.parametrize("tile", [16, 32])
+def test_batch_plan_grids_fixed_within_k_capacity(tile):
+    """Densification changes K (reference controllers/clone.py:31-56, prune.py:34-45): with
+    k_capacity the launch grids and the plan size do not depend on K up to the capacity, so a
+    plan re-written in place keeps graph-captured launches valid; without it they follow K."""
+    shapes = [(320, 320), (320, 768), (1280, 1280)]
+    ref = _batch_info([(m, n, 1024) for m, n in shapes], tile=tile, k_capacity=1024)
+    for ks in ([256, 257, 1000], [1, 1024, 513], [1024, 1024, 1024]):
+        got = _batch_info([(m, n, k) for (m, n), k in zip(shapes, ks)], tile=tile, k_capacity=1024)
+        assert got == ref, ks
+    small = _batch_info([(m, n, 256) for m, n in shapes], tile=tile)
+    assert small[2] < ref[2]  # finish blocks follow K without a capacity
+    assert small[0] == ref[0]  # tile blocks depend on the tile grid only
+
+
+def test_batch_plan_reserves_emission_blocks_for_capacity():
+    """A layer whose capacity lies past the mask path (K > 8192) keeps emit blocks while its
+    current K is on the mask path; their workgroups return at once (k_emit_batch)."""
+    mask = _batch_info([(320, 320, 4096)])
+    assert mask[1] == 0
+    reserved = _batch_info([(320, 320, 4096)], k_capacity=16384)
+    emitting = _batch_info([(320, 320, 16384)], k_capacity=16384)
+    assert reserved[1] > 0 and reserved == emitting
+    lib = N.lib()
+    cfg = _cfg()
+    table = (N.GfLayer * 1)()
+    table[0] = N.GfLayer(64, 64, 4, *([0x10000] * 9), 1, 0x10000, 1 << 20, None, *([0x10000] * 4), 1 << 20, -1)
+    info = N.GfBatchInfo()
+    rc = lib.gf_batch_plan(ctypes.byref(cfg), table, 1, None, 0, ctypes.byref(info), None)
+    assert rc == GF_E_INVALID_ARGUMENT and "k_capacity" in lib.gf_last_error().decode()

@@ -582,6 +582,169 @@ def test_gaussian_field_batch_matches_per_layer(device, tile):
                     pb.copy_(pa)
 
 
+def _densify_clone(layer, idx, noise):
+    """The reference's clone (controllers/clone.py:31-56): the selected Gaussians are appended
+    with mu_raw + noise, and the originals and the clones each keep half the amplitude."""
+    mu, chol, amp = layer.mu_raw.detach(), layer.chol_raw.detach(), layer.amp.detach()
+    idx = torch.as_tensor(idx, dtype=torch.long, device=mu.device)
+    new_amp = amp.clone()
+    new_amp[idx] = new_amp[idx] * 0.5
+    layer.replace_gaussian_parameters_(mu_raw=torch.cat([mu, mu.index_select(0, idx) + noise]),
+                                       chol_raw=torch.cat([chol, chol.index_select(0, idx)]),
+                                       amp=torch.cat([new_amp, amp.index_select(0, idx) * 0.5]))
+
+
+def _densify_prune(layer, keep):
+    """The reference's prune (controllers/prune.py:38-45): rows of the keep mask."""
+    keep = keep.to(layer.mu_raw.device)
+    layer.replace_gaussian_parameters_(mu_raw=layer.mu_raw.detach()[keep], chol_raw=layer.chol_raw.detach()[keep],
+                                       amp=layer.amp.detach()[keep])
+
+
+@pytest.mark.parametrize("tile", [16, 32])
+def test_gaussian_field_batch_densification(device, tile):
+    """Densification between training steps (reference base_trainer.py:126-220: clone and prune
+    replace a layer's parameters with tensors of another K): GaussianFieldBatch re-plans in
+    place and keeps matching per-layer rendering; K changes within k_capacity reuse every
+    workspace and the plan buffer, and a layer grown past it gets larger buffers."""
+    import copy
+
+    from guass_amd.layers import GaussianAdapterConfig, GaussianFieldBatch, GaussianLinear
+
+    torch.manual_seed(11)
+    shapes = [(96, 80, 48), (64, 64, 24), (120, 40, 36)]  # (in, out, K)
+    layers_a, layers_b = [], []
+    for n_in, n_out, k in shapes:
+        cfg = GaussianAdapterConfig(init_num_gaussians=k, tile_out=tile, tile_in=tile, adapter_scale=0.5,
+                                    init_amp_scale=1e-2)
+        la = GaussianLinear(n_in, n_out, adapter_config=cfg, device=device)
+        with torch.no_grad():
+            la.chol_raw.add_(torch.randn_like(la.chol_raw) * 0.2)
+        layers_a.append(la)
+        layers_b.append(copy.deepcopy(la))
+    fb = GaussianFieldBatch(layers_b, k_capacity=64)
+    xs = [torch.randn(5, n_in, device=device) for (n_in, _, _) in shapes]
+
+    def buffers():
+        return [(pl.fwd_ws.data_ptr(), pl.bwd_ws.data_ptr()) for pl in fb._plan.plans], fb._plan.plan.data_ptr()
+
+    g = torch.Generator(device="cpu").manual_seed(5)
+    events = [  # (layer, "clone" indices | "prune" keep count) after each step
+        [(0, "clone", 6), (1, "prune", 20)],
+        [(2, "clone", 10)],
+        [(1, "clone", 50)],  # 20 -> 70: past the capacity of 64
+        [(0, "prune", 30)],
+    ]
+    prev = None
+    for step in range(len(events) + 1):
+        for ls in (layers_a, layers_b):
+            for ly in ls:
+                for q in (ly.mu_raw, ly.chol_raw, ly.amp):
+                    q.grad = None
+        ks = [ly.num_gaussians for ly in layers_b]
+        say(f"densification step {step}: K={ks} tile {tile}")
+        loss_a = sum((ly(x) ** 2).sum() for ly, x in zip(layers_a, xs))
+        loss_a.backward()
+        fb.render()
+        outs_b = [ly(x) for ly, x in zip(layers_b, xs)]
+        sum((o ** 2).sum() for o in outs_b).backward()
+        torch.cuda.synchronize()
+        for i in range(3):
+            with torch.no_grad():
+                ya = layers_a[i](xs[i])
+            assert torch.equal(outs_b[i].detach(), ya), f"step {step} layer {i}: output"
+            for name in ("mu_raw", "chol_raw", "amp"):
+                grad_close(getattr(layers_b[i], name).grad, getattr(layers_a[i], name).grad,
+                           f"step {step} layer {i} {name}", rtol=1e-5)
+        now = buffers()
+        if prev is not None:
+            grown = {i for i, k in enumerate(ks) if k > 64 and prev_ks[i] <= 64}
+            for i in range(3):
+                if i in grown:
+                    assert now[0][i] != prev[0][i], f"step {step} layer {i}: buffers should have grown"
+                else:
+                    assert now[0][i] == prev[0][i], f"step {step} layer {i}: workspace reallocated"
+            if not grown:
+                assert now[1] == prev[1], f"step {step}: plan buffer reallocated"
+        prev, prev_ks = now, ks
+        if step == len(events):
+            break
+        with torch.no_grad():  # an Adam-sized step (lr * sign), then the same parameters on both copies
+            for la, lb in zip(layers_a, layers_b):
+                for name in ("mu_raw", "chol_raw", "amp"):
+                    pa, pb = getattr(la, name), getattr(lb, name)
+                    pa.add_(pa.grad.sign(), alpha=-1e-3)
+                    pb.copy_(pa)
+        for i, kind, n in events[step]:
+            K = layers_a[i].num_gaussians
+            if kind == "clone":
+                idx = torch.randint(0, K, (n,), generator=g)
+                noise = (torch.randn(n, 2, generator=g) * 1e-2).to(device)
+                for ls in (layers_a, layers_b):
+                    _densify_clone(ls[i], idx, noise)
+            else:
+                keep = torch.zeros(K, dtype=torch.bool)
+                keep[torch.randperm(K, generator=g)[:n]] = True
+                for ls in (layers_a, layers_b):
+                    _densify_prune(ls[i], keep)
+    assert fb.replans >= len(events)
+
+
+@pytest.mark.parametrize("tile", [16, 32])
+def test_batch_plan_update_keeps_captured_graph_valid(device, tile):
+    """A graph captured over gf_batch_forward + gf_batch_backward before every layer's K and
+    parameter tensors change (densification) replays correctly after FieldBatchPlan.update()
+    re-plans in place within k_capacity: binning, delta-W and gradients as the single-field
+    path gives for the new fields, and no buffer reallocated."""
+    from guass_amd.ops import FieldBatchPlan
+
+    before = [wl.cfg1(6), wl.make_problem("cfg2_k256_s7", 320, 768, 256, math.log(6.0), 0.7, 7),
+              tiny_problem(80, 96, 40, 8)]
+    after = [wl.make_problem("cfg1_k150_s9", 320, 320, 150, math.log(4.0), 0.5, 9),
+             wl.make_problem("cfg2_k190_s10", 320, 768, 190, math.log(6.0), 0.7, 10),
+             tiny_problem(80, 96, 96, 11)]
+    singles = {}
+    for name, probs in (("before", before), ("after", after)):
+        singles[name] = [run_gpu(p, device, tile_out=tile, tile_in=tile) for p in probs]
+    caps = [max(int(a[1][-1]), int(b[1][-1])) for a, b in zip(singles["before"], singles["after"])]
+    qa = [p.to(device) for p in before]
+    batch = FieldBatchPlan(qa, device, capacities=caps, k_capacities=[256] * 3, tile_out=tile, tile_in=tile)
+    bufs = ([(pl.fwd_ws.data_ptr(), pl.bwd_ws.data_ptr(), pl.ids.data_ptr()) for pl in batch.plans],
+            batch.plan.data_ptr(), batch.grad_flat.data_ptr())
+    s = torch.cuda.Stream(device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(s):
+        batch.forward()
+        batch.backward()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            batch.forward()
+            batch.backward()
+    torch.cuda.current_stream(device).wait_stream(s)
+    torch.cuda.synchronize()
+
+    def verify(name):
+        assert batch.status() == [0] * 3, name
+        for i, (pl, sg) in enumerate(zip(batch.plans, singles[name])):
+            P = int(sg[1][-1])
+            assert torch.equal(pl.tile_ptr, sg[1]) and torch.equal(pl.ids[:P], sg[2]), f"{name} {i}: binning"
+            assert torch.equal(pl.delta, sg[0]), f"{name} {i}: delta"
+            for gname, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), sg[3:]):
+                grad_close(a, b, f"{name} layer {i} {gname}", rtol=1e-5)
+
+    for name, probs in (("before", None), ("after", after)):
+        if probs is not None:
+            say(f"re-plan in place: K {[p.k for p in before]} -> {[p.k for p in probs]} tile {tile}")
+            qb = [p.to(device) for p in probs]
+            assert batch.update(qb), "launch grids changed within k_capacity"
+            now = ([(pl.fwd_ws.data_ptr(), pl.bwd_ws.data_ptr(), pl.ids.data_ptr()) for pl in batch.plans],
+                   batch.plan.data_ptr(), batch.grad_flat.data_ptr())
+            assert now == bufs, "a buffer was reallocated within the capacities"
+        graph.replay()
+        torch.cuda.synchronize()
+        verify(name)
+
+
 def test_adapter_checkpoint_delta_w(device, tmp_path):
     """A trained adapter (a few SGD steps on the GPU) saved in the gaussian-peft-adapter format
     and loaded into a fresh model: its delta-W equals the trained layer's bit for bit and the
