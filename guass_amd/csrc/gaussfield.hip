@@ -1,18 +1,24 @@
 // gaussfield.hip - gfx950 kernels and C ABI of libgaussfield.so.
 //
-// Forward (reference forward.cu:372-569), two kernels on the mask path (16x16 tiles, K <= 8192),
-// three otherwise:
-//   k_bin      one workgroup per field: bit-exact sigma-box tile rectangle of every Gaussian,
-//              the pair total, per-tile Gaussian counts from row-wise difference arrays and
-//              their scan -> tile_ptr; every scan runs in LDS (DPP wave scans) and global
-//              memory is only written, coalesced.  Mask path (k_bin_masks): also each
-//              Gaussian's evaluation constants and, per tile row and tile column, a bitmask of
-//              the Gaussians whose tile range covers it.
+// Forward (reference forward.cu:372-569).  Mask path (16x16 or 32x32 tiles, K <= 8192), three
+// kernels:
+//   k_prep     one thread per Gaussian: bit-exact sigma-box tile rectangle, fp32 covariance
+//              and evaluation constants.
+//   k_bin_tiles one workgroup per tile row and per tile column, none waiting for another: the
+//              row's or column's bitmask of the Gaussians whose tile range covers it (wave
+//              ballots), and per tile row the tile_ptr of its tiles (a closed-form count of
+//              the pairs in earlier rows plus a scan of the row's column differences).
+//   k_render16 (below).
+// Emission path, three kernels:
+//   k_bin      one workgroup per field: rectangles, the pair total, per-tile Gaussian counts
+//              from row-wise difference arrays and their scan -> tile_ptr; every scan runs in
+//              LDS (DPP wave scans) and global memory is only written, coalesced.  (The
+//              batched form, k_bin_batch, one workgroup per field, also builds the masks.)
 //   k_emit     (emission path) one wave per Gaussian: its evaluation constants (kept in the
 //              workspace for the render and the backward) and a slot in each touched tile's
 //              range from tile_ptr and a per-tile fill counter (a counting sort on the tile key).
-//   k_render16 one wave per 16x16 tile, four independent tiles per workgroup, no workgroup
-//              barriers: the tile's ids in canonical (ascending gid) order -- the set bits of
+//   k_render16 one wave per 16x16 tile (or 16x16 quadrant of a 32x32 tile), four per
+//              workgroup, no workgroup barriers: the tile's ids in canonical (ascending gid) order -- the set bits of
 //              rowmask & colmask (mask path) or k_emit's segment sorted -- written to the
 //              tile's segment, per-Gaussian constants loaded one Gaussian per lane and broadcast
 //              with readlane, 4 pixels per lane with per-row terms hoisted.
@@ -764,15 +770,148 @@ __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __r
   bin_body<false>(p, mu, chol_raw, nullptr, tile_ptr, num_pairs, ws, L, nullptr);
 }
 
-// Mask path: also the Gaussians' constants and the tile-row / tile-column masks.
-__global__ __launch_bounds__(kBinThreads) void k_bin_masks(Problem p, const float* __restrict__ mu,
-                                                           const float* __restrict__ chol_raw,
-                                                           const float* __restrict__ amp,
-                                                           int64_t* __restrict__ tile_ptr,
-                                                           int64_t* __restrict__ num_pairs, uint8_t* ws,
-                                                           FwdLayout L) {
-  __shared__ uint32_t mlds[kMaskLdsWords];
-  bin_body<true>(p, mu, chol_raw, amp, tile_ptr, num_pairs, ws, L, mlds);
+// ------------------------------------------------------------------------------------------
+// Parallel binning (mask path).  Workgroup b < R takes tile row b: its row mask and the
+// tile_ptr of its C tiles; workgroup R + c takes tile column c: its column mask.  Every
+// workgroup sees every Gaussian's tile rectangle, so none waits for another:
+//   tile_ptr[r*C + c] = rowbase[r] + sum_{c' < c} count(r, c'),
+//   rowbase[r] = sum_g w_g * clamp(r - x_g, 0, h_g)   (g's tiles in rows before r),
+// with the row's counts from a difference array over its columns.  A mask word pair is one
+// wave's ballot over 64 consecutive Gaussians.  k_prep, launched before, stores each
+// Gaussian's rectangle, covariance and evaluation constants (one thread per Gaussian).
+constexpr int kTilesThreads = 256;
+
+struct PrepOut {
+  int4 rect;
+  GfCov cov;
+  float mu0, mu1;
+};
+
+struct PrepLoad {
+  float mu0, mu1, r11, r21, r22;
+};
+
+__device__ inline PrepLoad prep_load(const float* __restrict__ mu, const float* __restrict__ chol_raw,
+                                     int64_t g) {
+  return PrepLoad{mu[2 * g + 0], mu[2 * g + 1], chol_raw[3 * g + 0], chol_raw[3 * g + 1], chol_raw[3 * g + 2]};
+}
+
+__device__ inline PrepOut prep_rect(const Problem& p, const PrepLoad& in) {
+  PrepOut o;
+  o.mu0 = in.mu0;
+  o.mu1 = in.mu1;
+  o.cov = gf_cov_from_chol(gf_activate_cholesky(in.r11, in.r21, in.r22));
+  int32_t touched;
+  o.rect = bin_rect(p, o.mu0, o.mu1, o.cov, &touched);
+  return o;
+}
+
+__device__ inline void store_prep(const Problem& p, const PrepOut& o, float amp, int64_t g, uint8_t* ws,
+                                  const FwdLayout& L) {
+  reinterpret_cast<int4*>(ws + L.rect)[g] = o.rect;
+  reinterpret_cast<float4*>(ws + L.cov)[g] = make_float4(o.cov.s00, o.cov.s01, o.cov.s11, 0.0f);
+  GaussEval v = eval_from_cov(p, o.mu0, o.mu1, o.cov, amp);
+  v.gid = (int32_t)g;
+  store_eval(reinterpret_cast<GaussEval*>(ws + L.eval), g, v);
+}
+
+// One thread per Gaussian: rectangle, covariance and evaluation constants.
+__global__ __launch_bounds__(kTilesThreads) void k_prep(Problem p, const float* __restrict__ mu,
+                                                        const float* __restrict__ chol_raw,
+                                                        const float* __restrict__ amp, uint8_t* ws,
+                                                        FwdLayout L) {
+  const int64_t g = (int64_t)blockIdx.x * kTilesThreads + threadIdx.x;
+  if (g < p.K) store_prep(p, prep_rect(p, prep_load(mu, chol_raw, g)), amp[g], g, ws, L);
+}
+
+__global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t* __restrict__ tile_ptr,
+                                                             int64_t* __restrict__ num_pairs, uint8_t* ws,
+                                                             FwdLayout L) {
+  __shared__ int32_t diff[kLdsDiffWords];  // tile-row workgroups: the row's column differences
+  const int64_t K = p.K;
+  const int32_t R = p.R, C = p.C, W = p.W;
+  const int32_t b = (int32_t)blockIdx.x;
+  const bool is_row = b < R;
+  const int32_t line = is_row ? b : b - R;
+  const int lane = threadIdx.x & 63;
+  const int4* __restrict__ rect = reinterpret_cast<const int4*>(ws + L.rect);
+  uint32_t* out = reinterpret_cast<uint32_t*>(ws + (is_row ? L.rowmask : L.colmask)) + (int64_t)line * W;
+  if (is_row)
+    for (int32_t i = threadIdx.x; i <= C; i += kTilesThreads) diff[i] = 0;
+  __syncthreads();
+  int64_t before = 0, pairs = 0;
+  for (int64_t g0 = threadIdx.x & ~63; g0 < K; g0 += kTilesThreads) {  // wave-uniform
+    const int64_t g = g0 + lane;
+    bool covers = false;
+    if (g < K) {
+      const int4 r = rect[g];
+      if (is_row) {
+        const int32_t h = r.y - r.x + 1, w = r.w - r.z + 1;
+        before += (int64_t)w * clamp_i32(line - r.x, 0, h);
+        pairs += (int64_t)w * h;
+        covers = r.x <= line && line <= r.y;
+        if (covers) {
+          atomicAdd(diff + r.z, 1);
+          atomicAdd(diff + r.w + 1, -1);  // r.w + 1 <= C
+        }
+      } else {
+        covers = r.z <= line && line <= r.w;
+      }
+    }
+    const uint64_t bits = __builtin_amdgcn_ballot_w64(covers);
+    const int64_t w0 = g0 >> 5;  // even: words w0, w0 + 1 hold Gaussians g0 .. g0 + 63
+    if (lane == 0) out[w0] = (uint32_t)bits;
+    if (lane == 1 && w0 + 1 < W) out[w0 + 1] = (uint32_t)(bits >> 32);
+  }
+  if (!is_row) return;
+  __syncthreads();  // the row's differences are complete
+  // tile_ptr[line*C + c] = rowbase + sum_{c' < c} diff[c'] * (c - c') = rowbase + c*D(c) - E(c),
+  // with D, E the exclusive prefixes of diff[c] and c*diff[c]: one scan of two sums, with
+  // rowbase and the pair total as plain sums beside it.  Thread t owns columns
+  // [t*per, t*per + per).
+  constexpr int kWaves = kTilesThreads / 64;
+  __shared__ int64_t wsum[4][kWaves];
+  const int wid = threadIdx.x >> 6;
+  const int32_t per = (C + kTilesThreads - 1) / kTilesThreads;
+  const int32_t cb = (int32_t)threadIdx.x * per, ce = min(cb + per, C);
+  int64_t d = 0, e = 0;
+  for (int32_t c = cb; c < ce; ++c) {
+    d += diff[c];
+    e += (int64_t)c * diff[c];
+  }
+  const int64_t di = wave_inclusive_scan(d), ei = wave_inclusive_scan(e);
+  const int64_t bi = wave_inclusive_scan(before), pi = wave_inclusive_scan(pairs);
+  if (lane == 63) {
+    wsum[0][wid] = di;
+    wsum[1][wid] = ei;
+    wsum[2][wid] = bi;
+    wsum[3][wid] = pi;
+  }
+  __syncthreads();
+  int64_t D = di - d, E = ei - e, Dt = 0, Et = 0, rowbase = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    if (w < wid) {
+      D += wsum[0][w];
+      E += wsum[1][w];
+    }
+    Dt += wsum[0][w];
+    Et += wsum[1][w];
+    rowbase += wsum[2][w];
+    total += wsum[3][w];
+  }
+  int64_t* tp = tile_ptr + (int64_t)line * C;
+  for (int32_t c = cb; c < ce; ++c) {
+    tp[c] = rowbase + (int64_t)c * D - E;
+    D += diff[c];
+    E += (int64_t)c * diff[c];
+  }
+  if (line == R - 1 && threadIdx.x == 0) {
+    const int64_t P = rowbase + (int64_t)C * Dt - Et;
+    tile_ptr[(int64_t)R * C] = P;
+    *num_pairs = P;
+    reinterpret_cast<WsHeader*>(ws)->status = P == total ? 0u : GF_STATUS_COUNT_MISMATCH;
+  }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -2013,8 +2152,12 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (p.W > 0) {
     if (!amp) return set_err(GF_E_INVALID_ARGUMENT, "amp must not be NULL");
-    hipLaunchKernelGGL(k_bin_masks, dim3(1), dim3(kBinThreads), 0, st, p, mu, chol_raw, amp, tile_ptr,
-                       num_pairs_dev, reinterpret_cast<uint8_t*>(workspace), L);
+    uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+    const unsigned lines = (unsigned)(p.R + p.C);
+    hipLaunchKernelGGL(k_prep, dim3((unsigned)((k + kTilesThreads - 1) / kTilesThreads)), dim3(kTilesThreads), 0,
+                       st, p, mu, chol_raw, amp, ws, L);
+    GF_LAUNCH_CHECK("k_prep");
+    hipLaunchKernelGGL(k_bin_tiles, dim3(lines), dim3(kTilesThreads), 0, st, p, tile_ptr, num_pairs_dev, ws, L);
   } else {
     hipLaunchKernelGGL(k_bin, dim3(1), dim3(kBinThreads), 0, st, p, mu, chol_raw, tile_ptr,
                        num_pairs_dev, reinterpret_cast<uint8_t*>(workspace), L);
