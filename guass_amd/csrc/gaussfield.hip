@@ -127,7 +127,9 @@ struct __align__(16) GaussEval {
 
 struct WsHeader {
   uint32_t status;
-  uint32_t pad[63];
+  uint32_t pad0;
+  int64_t* num_pairs;  // forward, tiles binned in the render: where the render stores P
+  uint32_t pad[60];
 };
 static_assert(sizeof(WsHeader) == 256, "workspace header must be 256 bytes");
 
@@ -819,8 +821,13 @@ __device__ inline void store_prep(const Problem& p, const PrepOut& o, float amp,
 __global__ __launch_bounds__(kTilesThreads) void k_prep(Problem p, const float* __restrict__ mu,
                                                         const float* __restrict__ chol_raw,
                                                         const float* __restrict__ amp, uint8_t* ws,
-                                                        FwdLayout L) {
+                                                        FwdLayout L, int64_t* num_pairs) {
   const int64_t g = (int64_t)blockIdx.x * kTilesThreads + threadIdx.x;
+  if (g == 0) {
+    WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
+    hdr->status = 0u;
+    hdr->num_pairs = num_pairs;
+  }
   if (g < p.K) store_prep(p, prep_rect(p, prep_load(mu, chol_raw, g)), amp[g], g, ws, L);
 }
 
@@ -912,6 +919,22 @@ __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t*
     *num_pairs = P;
     reinterpret_cast<WsHeader*>(ws)->status = P == total ? 0u : GF_STATUS_COUNT_MISMATCH;
   }
+}
+
+// P = sum_g h_g * w_g from the stored rectangles, for a host read-back right after binning
+// when the render bins the tiles (tiles_in_render).
+__global__ __launch_bounds__(kTilesThreads) void k_pairs(Problem p, int64_t* __restrict__ num_pairs,
+                                                         const uint8_t* __restrict__ ws, FwdLayout L) {
+  __shared__ int64_t scan_lds[kTilesThreads / 64 + 1];
+  const int4* __restrict__ rect = reinterpret_cast<const int4*>(ws + L.rect);
+  int64_t s = 0;
+  for (int64_t g = threadIdx.x; g < p.K; g += kTilesThreads) {
+    const int4 r = rect[g];
+    s += (int64_t)(r.y - r.x + 1) * (r.w - r.z + 1);
+  }
+  int64_t total;
+  (void)block_exclusive_scan<kTilesThreads>(s, &total, scan_lds);
+  if (threadIdx.x == 0) *num_pairs = total;
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1245,12 +1268,64 @@ __device__ __forceinline__ void render16_body(
     const Problem& p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids,
     int64_t capacity, float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
-    const uint32_t* __restrict__ colmask, const SubTile& st) {
+    const uint32_t* __restrict__ colmask, const SubTile& st, const int4* __restrict__ rects = nullptr,
+    int64_t* __restrict__ tile_ptr_out = nullptr) {
   __shared__ int32_t wkeys[kTileThreads / 64][kWaveSortKeys];
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
   const int64_t t = st.t;
+  // Tiles binned here (tiles_in_render, mask path): the workgroup's tiles -- four 16x16 tiles
+  // or one 32x32 tile -- get their mask words (one ballot per 64 Gaussians), pair counts and
+  // segment starts from the K rectangles, each wave taking every fourth run of 64 Gaussians for
+  // all of them.  A segment start is the pairs of every Gaussian in earlier tiles (row-major):
+  //   w_g * clamp(tr - x_g, 0, h_g) + [x_g <= tr <= y_g] * clamp(tc - z_g, 0, w_g).
+  __shared__ uint32_t bin_mask[kTileThreads / 64][kMaskMaxK / 32];
+  __shared__ int64_t bin_part[kTileThreads / 64][kTileThreads / 64];
+  __shared__ int64_t bin_cnt[kTileThreads / 64][kTileThreads / 64];
+  if (rects) {
+    const int64_t T = (int64_t)p.R * p.C;
+    const int ntiles = p.tile_out == 32 ? 1 : kTileThreads / 64;
+    const int64_t tbase = p.tile_out == 32 ? t : t - wid;
+    int32_t btr[kTileThreads / 64], btc[kTileThreads / 64];
+    int64_t before[kTileThreads / 64], cnt[kTileThreads / 64];
+#pragma unroll
+    for (int jj = 0; jj < kTileThreads / 64; ++jj) {
+      const int64_t tj = tbase + jj < T ? tbase + jj : T - 1;
+      btr[jj] = (int32_t)(tj / p.C);
+      btc[jj] = (int32_t)(tj - (tj / p.C) * p.C);
+      before[jj] = 0;
+      cnt[jj] = 0;
+    }
+    for (int64_t g0 = (int64_t)wid * 64; g0 < p.K; g0 += kTileThreads) {  // wave-uniform
+      const int64_t g = g0 + lane;
+      const int4 r = g < p.K ? rects[g] : make_int4(1, 0, 1, 0);  // empty
+      const int32_t h = r.y - r.x + 1, wd = r.w - r.z + 1;
+      const int32_t w0 = (int32_t)(g0 >> 5);
+#pragma unroll
+      for (int jj = 0; jj < kTileThreads / 64; ++jj) {
+        if (jj < ntiles) {
+          const bool in_row = r.x <= btr[jj] && btr[jj] <= r.y;
+          if (g < p.K)
+            before[jj] += (int64_t)wd * clamp_i32(btr[jj] - r.x, 0, h) +
+                          (in_row ? clamp_i32(btc[jj] - r.z, 0, wd) : 0);
+          const uint64_t bits = __builtin_amdgcn_ballot_w64(in_row && r.z <= btc[jj] && btc[jj] <= r.w);
+          cnt[jj] += __popcll(bits);
+          if (lane == 0) bin_mask[jj][w0] = (uint32_t)bits;
+          if (lane == 1 && w0 + 1 < p.W) bin_mask[jj][w0 + 1] = (uint32_t)(bits >> 32);
+        }
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < kTileThreads / 64; ++jj) {
+      const int64_t tot = readlane_i64(wave_inclusive_scan(before[jj]), 63);
+      if (lane == 0) {
+        bin_part[wid][jj] = tot;
+        bin_cnt[wid][jj] = cnt[jj];
+      }
+    }
+    __syncthreads();
+  }
   if (t >= (int64_t)p.R * p.C) return;
   const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (t / p.C) * p.C);
   const bool write_ids = st.quad == 0;  // one wave of a 32x32 tile writes its ids
@@ -1294,9 +1369,27 @@ __device__ __forceinline__ void render16_body(
   };
   int64_t s, n;
   if (p.W > 0) {
-    // The tile's segment [s, s + count) from tile_ptr; ids past the capacity are not stored.
-    s = tile_ptr[t];
-    const int64_t count = tile_ptr[t + 1] - s;
+    // The tile's segment [s, s + count); ids past the capacity are not stored.
+    int64_t count;
+    const uint32_t* own = nullptr;
+    if (rects) {
+      // Binned above (tiles_in_render).
+      const int j = p.tile_out == 32 ? 0 : wid;
+      s = bin_part[0][j] + bin_part[1][j] + bin_part[2][j] + bin_part[3][j];
+      count = bin_cnt[0][j] + bin_cnt[1][j] + bin_cnt[2][j] + bin_cnt[3][j];
+      if (write_ids && lane == 0) {
+        tile_ptr_out[t] = s;
+        const int64_t T = (int64_t)p.R * p.C;
+        if (t == T - 1) {
+          tile_ptr_out[T] = s + count;
+          *hdr->num_pairs = s + count;
+        }
+      }
+      own = bin_mask[j];
+    } else {
+      s = tile_ptr[t];
+      count = tile_ptr[t + 1] - s;
+    }
     const int64_t room = capacity - s < count ? (capacity - s > 0 ? capacity - s : 0) : count;
     const uint32_t* rm = rowmask + (int64_t)tr * p.W;
     const uint32_t* cm = colmask + (int64_t)tc * p.W;
@@ -1304,7 +1397,7 @@ __device__ __forceinline__ void render16_body(
     int64_t done = 0;
     for (int32_t w0 = 0; w0 < p.W; w0 += 64) {
       const int32_t w = w0 + lane;
-      const uint32_t m = w < p.W ? (rm[w] & cm[w]) : 0u;
+      const uint32_t m = w < p.W ? (own ? own[w] : (rm[w] & cm[w])) : 0u;
       const int32_t cnt = __popc(m);
       const int32_t inc = dpp_scan_i32(cnt);
       const int32_t tot = __builtin_amdgcn_readlane(inc, 63);
@@ -1403,9 +1496,9 @@ __global__ __launch_bounds__(kTileThreads) void k_render16(
     Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids,
     int64_t capacity, float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
-    const uint32_t* __restrict__ colmask) {
+    const uint32_t* __restrict__ colmask, const int4* __restrict__ rects, int64_t* __restrict__ tile_ptr_out) {
   render16_body(p, row_coords, col_coords, ev, tile_ptr, ids, capacity, delta, ws, rowmask, colmask,
-                sub_tile(p, blockIdx.x, wave_id()));
+                sub_tile(p, blockIdx.x, wave_id()), rects, tile_ptr_out);
 }
 
 // Any tile shape: each thread evaluates pixels p = tid, tid+256, ... of the tile.
@@ -1917,6 +2010,15 @@ bool quad_tiles(const Problem& p) {
 }
 bool quad_render(const Problem& p) { return quad_tiles(p) && (p.tile_out == 16 || p.W > 0); }
 
+// Small fields on the mask path bin their tiles in the render, which saves the k_bin_tiles
+// launch (about 4 us) at the price of K rectangle tests per tile in the render: a gain up to
+// K * T of about 2^20 (cfg1 17.0 -> 16.1 us, cfg2 19.2 -> 18.2 us), a loss beyond (cfg3 at
+// 6.5M tests: 29.3 -> 34.1 us).
+constexpr int64_t kTilesInRenderMaxTests = int64_t(1) << 20;
+bool tiles_in_render(const Problem& p) {
+  return p.W > 0 && quad_render(p) && (int64_t)p.R * p.C * p.K <= kTilesInRenderMaxTests;
+}
+
 // Workgroups of the 16x16-block tile kernels: four 16x16 tiles or one 32x32 tile each.
 int64_t quad_grid(const Problem& p) {
   const int64_t T = (int64_t)p.R * p.C;
@@ -2155,9 +2257,12 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
     const unsigned lines = (unsigned)(p.R + p.C);
     hipLaunchKernelGGL(k_prep, dim3((unsigned)((k + kTilesThreads - 1) / kTilesThreads)), dim3(kTilesThreads), 0,
-                       st, p, mu, chol_raw, amp, ws, L);
+                       st, p, mu, chol_raw, amp, ws, L, num_pairs_dev);
     GF_LAUNCH_CHECK("k_prep");
-    hipLaunchKernelGGL(k_bin_tiles, dim3(lines), dim3(kTilesThreads), 0, st, p, tile_ptr, num_pairs_dev, ws, L);
+    if (!tiles_in_render(p))
+      hipLaunchKernelGGL(k_bin_tiles, dim3(lines), dim3(kTilesThreads), 0, st, p, tile_ptr, num_pairs_dev, ws, L);
+    else if (num_pairs_host)
+      hipLaunchKernelGGL(k_pairs, dim3(1), dim3(kTilesThreads), 0, st, p, num_pairs_dev, ws, L);
   } else {
     hipLaunchKernelGGL(k_bin, dim3(1), dim3(kBinThreads), 0, st, p, mu, chol_raw, tile_ptr,
                        num_pairs_dev, reinterpret_cast<uint8_t*>(workspace), L);
@@ -2199,7 +2304,7 @@ int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in
 }
 
 int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                      const float* row_coords, const float* col_coords, const int64_t* tile_ptr,
+                      const float* row_coords, const float* col_coords, int64_t* tile_ptr,
                       int64_t* gaussian_ids_sorted, int64_t ids_capacity,
                       float* delta, void* workspace, size_t workspace_bytes, void* stream) {
   Problem p;
@@ -2216,11 +2321,15 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
   const GaussEval* ev = reinterpret_cast<const GaussEval*>(ws + L.eval);
-  if (quad_render(p))
+  if (quad_render(p)) {
+    const bool binned_here = tiles_in_render(p);
     hipLaunchKernelGGL(k_render16, dim3((unsigned)quad_grid(p)), dim3(kTileThreads), 0, st, p, row_coords,
                        col_coords, ev, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws,
                        reinterpret_cast<const uint32_t*>(ws + L.rowmask),
-                       reinterpret_cast<const uint32_t*>(ws + L.colmask));
+                       reinterpret_cast<const uint32_t*>(ws + L.colmask),
+                       binned_here ? reinterpret_cast<const int4*>(ws + L.rect) : nullptr,
+                       binned_here ? tile_ptr : nullptr);
+  }
   else
     hipLaunchKernelGGL(k_render_any, dim3((unsigned)T), dim3(kTileThreads), 0, st, p, row_coords,
                        col_coords, ev, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws);

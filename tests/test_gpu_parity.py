@@ -179,21 +179,24 @@ def test_sigma_multiplier_2_5(device):
     check(wl.cfg2(1), device, sigma=2.5)
 
 
+@pytest.mark.parametrize("shape", [(100, 200), (1250, 700)])
 @pytest.mark.parametrize("tile", [16, 32])
 @pytest.mark.parametrize("k", [1, 31, 32, 33, 63, 64, 65, 127, 129, 257, 1000, 8192])
-def test_mask_path_binning_k_boundaries(device, k, tile):
-    """The mask path's binning (a workgroup per tile row and per tile column; mask word pairs
-    from 64-Gaussian ballots; tile_ptr in closed form) at K around the ballot groups and at the
-    path's largest K, with Gaussians spanning the whole grid and Gaussians in the last, partial
-    tile row and column: tile_ptr and ids bit-exact against the oracle's binning
-    (bounds.py:24-75, tile_index.py:51-99), delta-W at the field tolerance."""
-    p = tiny_problem(100, 200, k, 40 + k, log_scale_px=1.5, spread=0.9)
+def test_mask_path_binning_k_boundaries(device, k, tile, shape):
+    """The mask path's binning at K around the 64-Gaussian ballot groups (a mask word pair each)
+    and at the path's largest K, with Gaussians spanning the whole grid and Gaussians in the
+    last, partial tile row and column.  The small grid bins in the render (K * T <= 2^20), the
+    large one mostly in k_bin_tiles (a workgroup per tile row and column): tile_ptr and ids
+    bit-exact against the oracle's binning (bounds.py:24-75, tile_index.py:51-99), delta-W at
+    the field tolerance on the small grid."""
+    M, N = shape
+    p = tiny_problem(M, N, k, 40 + k, log_scale_px=1.5 if M < 1000 else 3.0, spread=0.9)
     g = torch.Generator().manual_seed(k)
     huge = torch.arange(0, k, 7)
     p.chol_raw[huge] = torch.tensor([3.0, 0.2, 3.0])  # sigma boxes past the matrix
     corner = torch.arange(k)[3::11]
     p.mu[corner] = torch.tensor([0.98, 0.99]) + 0.01 * torch.rand(len(corner), 2, generator=g)
-    say(f"mask-path binning K={k} tile {tile}")
+    say(f"mask-path binning {M}x{N} K={k} tile {tile}")
     q = p.to(device)
     delta, tp, ids = ext.gaussian_field_forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
                                                 tile, tile, 3.0, False, 80.0)
@@ -201,7 +204,7 @@ def test_mask_path_binning_k_boundaries(device, k, tile):
     chol = fo.activate_cholesky(p.chol_raw)
     ti = fo.build_tile_index(fo.tile_bounds(p.mu, chol, p.out_features, p.in_features, tile, tile, 3.0))
     binning_equal(tp, ids, ti.tile_ptr, ti.gaussian_ids)
-    if k <= 1000:
+    if k <= 1000 and M < 1000:
         ref = fo.gaussian_field_forward(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, tile, tile,
                                         3.0, False, 80.0)[0]
         field_close(delta, ref)
