@@ -1275,57 +1275,6 @@ __device__ __forceinline__ void render16_body(
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
   const int64_t t = st.t;
-  // Tiles binned here (tiles_in_render, mask path): the workgroup's tiles -- four 16x16 tiles
-  // or one 32x32 tile -- get their mask words (one ballot per 64 Gaussians), pair counts and
-  // segment starts from the K rectangles, each wave taking every fourth run of 64 Gaussians for
-  // all of them.  A segment start is the pairs of every Gaussian in earlier tiles (row-major):
-  //   w_g * clamp(tr - x_g, 0, h_g) + [x_g <= tr <= y_g] * clamp(tc - z_g, 0, w_g).
-  __shared__ uint32_t bin_mask[kTileThreads / 64][kMaskMaxK / 32];
-  __shared__ int64_t bin_part[kTileThreads / 64][kTileThreads / 64];
-  __shared__ int64_t bin_cnt[kTileThreads / 64][kTileThreads / 64];
-  if (rects) {
-    const int64_t T = (int64_t)p.R * p.C;
-    const int ntiles = p.tile_out == 32 ? 1 : kTileThreads / 64;
-    const int64_t tbase = p.tile_out == 32 ? t : t - wid;
-    int32_t btr[kTileThreads / 64], btc[kTileThreads / 64];
-    int64_t before[kTileThreads / 64], cnt[kTileThreads / 64];
-#pragma unroll
-    for (int jj = 0; jj < kTileThreads / 64; ++jj) {
-      const int64_t tj = tbase + jj < T ? tbase + jj : T - 1;
-      btr[jj] = (int32_t)(tj / p.C);
-      btc[jj] = (int32_t)(tj - (tj / p.C) * p.C);
-      before[jj] = 0;
-      cnt[jj] = 0;
-    }
-    for (int64_t g0 = (int64_t)wid * 64; g0 < p.K; g0 += kTileThreads) {  // wave-uniform
-      const int64_t g = g0 + lane;
-      const int4 r = g < p.K ? rects[g] : make_int4(1, 0, 1, 0);  // empty
-      const int32_t h = r.y - r.x + 1, wd = r.w - r.z + 1;
-      const int32_t w0 = (int32_t)(g0 >> 5);
-#pragma unroll
-      for (int jj = 0; jj < kTileThreads / 64; ++jj) {
-        if (jj < ntiles) {
-          const bool in_row = r.x <= btr[jj] && btr[jj] <= r.y;
-          if (g < p.K)
-            before[jj] += (int64_t)wd * clamp_i32(btr[jj] - r.x, 0, h) +
-                          (in_row ? clamp_i32(btc[jj] - r.z, 0, wd) : 0);
-          const uint64_t bits = __builtin_amdgcn_ballot_w64(in_row && r.z <= btc[jj] && btc[jj] <= r.w);
-          cnt[jj] += __popcll(bits);
-          if (lane == 0) bin_mask[jj][w0] = (uint32_t)bits;
-          if (lane == 1 && w0 + 1 < p.W) bin_mask[jj][w0 + 1] = (uint32_t)(bits >> 32);
-        }
-      }
-    }
-#pragma unroll
-    for (int jj = 0; jj < kTileThreads / 64; ++jj) {
-      const int64_t tot = readlane_i64(wave_inclusive_scan(before[jj]), 63);
-      if (lane == 0) {
-        bin_part[wid][jj] = tot;
-        bin_cnt[wid][jj] = cnt[jj];
-      }
-    }
-    __syncthreads();
-  }
   if (t >= (int64_t)p.R * p.C) return;
   const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (t / p.C) * p.C);
   const bool write_ids = st.quad == 0;  // one wave of a 32x32 tile writes its ids
@@ -1373,10 +1322,32 @@ __device__ __forceinline__ void render16_body(
     int64_t count;
     const uint32_t* own = nullptr;
     if (rects) {
-      // Binned above (tiles_in_render).
-      const int j = p.tile_out == 32 ? 0 : wid;
-      s = bin_part[0][j] + bin_part[1][j] + bin_part[2][j] + bin_part[3][j];
-      count = bin_cnt[0][j] + bin_cnt[1][j] + bin_cnt[2][j] + bin_cnt[3][j];
+      // Tiles binned here (tiles_in_render): the tile's mask words, one ballot per 64
+      // Gaussians, into the wave's LDS, its count, and its segment start in closed form -- the
+      // pairs of every Gaussian in earlier tiles, row-major:
+      //   w_g * clamp(tr - x_g, 0, h_g) + [x_g <= tr <= y_g] * clamp(tc - z_g, 0, w_g).
+      __shared__ uint32_t wmask[kTileThreads / 64][kMaskMaxK / 32];
+      uint32_t* mw = wmask[wid];
+      int64_t before = 0, cnt = 0;
+#pragma unroll 4
+      for (int64_t g0 = 0; g0 < p.K; g0 += 64) {
+        const int64_t g = g0 + lane;
+        bool covers = false;
+        if (g < p.K) {
+          const int4 r = rects[g];
+          const int32_t h = r.y - r.x + 1, wd = r.w - r.z + 1;
+          const bool in_row = r.x <= tr && tr <= r.y;
+          before += (int64_t)wd * clamp_i32(tr - r.x, 0, h) + (in_row ? clamp_i32(tc - r.z, 0, wd) : 0);
+          covers = in_row && r.z <= tc && tc <= r.w;
+        }
+        const uint64_t bits = __builtin_amdgcn_ballot_w64(covers);
+        cnt += __popcll(bits);
+        const int32_t w0 = (int32_t)(g0 >> 5);
+        if (lane == 0) mw[w0] = (uint32_t)bits;
+        if (lane == 1 && w0 + 1 < p.W) mw[w0 + 1] = (uint32_t)(bits >> 32);
+      }
+      s = readlane_i64(wave_inclusive_scan(before), 63);
+      count = cnt;
       if (write_ids && lane == 0) {
         tile_ptr_out[t] = s;
         const int64_t T = (int64_t)p.R * p.C;
@@ -1385,7 +1356,8 @@ __device__ __forceinline__ void render16_body(
           *hdr->num_pairs = s + count;
         }
       }
-      own = bin_mask[j];
+      wave_sync();
+      own = mw;
     } else {
       s = tile_ptr[t];
       count = tile_ptr[t + 1] - s;
@@ -2010,13 +1982,15 @@ bool quad_tiles(const Problem& p) {
 }
 bool quad_render(const Problem& p) { return quad_tiles(p) && (p.tile_out == 16 || p.W > 0); }
 
-// Small fields on the mask path bin their tiles in the render, which saves the k_bin_tiles
-// launch (about 4 us) at the price of K rectangle tests per tile in the render: a gain up to
-// K * T of about 2^20 (cfg1 17.0 -> 16.1 us, cfg2 19.2 -> 18.2 us), a loss beyond (cfg3 at
-// 6.5M tests: 29.3 -> 34.1 us).
-constexpr int64_t kTilesInRenderMaxTests = int64_t(1) << 20;
+// Fields with few Gaussians bin their tiles in the render, which saves the k_bin_tiles launch
+// (about 4 us): each wave reads the K rectangles for its own tile's mask words and segment
+// start, K/64 dependent rounds of loads.  Measured over SD1.5 shapes (320..1280 square and
+// 320x768), this gains 0.4-2.3 us for K <= 256 and loses 3 us or more at K = 1024.
+constexpr int64_t kTilesInRenderMaxK = 256;
+constexpr int64_t kTilesInRenderMaxTests = int64_t(1) << 23;
 bool tiles_in_render(const Problem& p) {
-  return p.W > 0 && quad_render(p) && (int64_t)p.R * p.C * p.K <= kTilesInRenderMaxTests;
+  return p.W > 0 && quad_render(p) && p.K <= kTilesInRenderMaxK &&
+         (int64_t)p.R * p.C * p.K <= kTilesInRenderMaxTests;
 }
 
 // Workgroups of the 16x16-block tile kernels: four 16x16 tiles or one 32x32 tile each.

@@ -74,7 +74,7 @@ size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, in
  * mask path) it also stores every Gaussian's evaluation constants and, per tile row and tile
  * column, a bitmask of the Gaussians whose tile range covers it; the render then reads each
  * tile's ids from those masks and gf_forward_emit has nothing to do.  On the mask path with
- * k * T <= 2^20 the render bins each tile itself: tile_ptr and num_pairs_dev are then written by
+ * k <= 256 (and k * T <= 2^23) the render bins each tile itself: tile_ptr and num_pairs_dev are then written by
  * gf_forward_render (num_pairs_dev here too when num_pairs_host is given).
  *   amp             [K,1] fp32 (read on the mask path; may be NULL otherwise)
  *   tile_ptr        [T+1] int64 out: tile t owns gaussian_ids_sorted[tile_ptr[t] : tile_ptr[t+1]]
@@ -110,7 +110,7 @@ int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in
  * gf_forward_bin, in which case the render writes the ids itself from the masks).  Must follow
  * gf_forward_emit on the same stream with the same workspace and ids.
  *   tile_ptr        [T+1] int64, from gf_forward_bin; written here instead on the mask path with
- *                   k * T <= 2^20 (with P to gf_forward_bin's num_pairs_dev)
+ *                   k <= 256 and k * T <= 2^23 (with P to gf_forward_bin's num_pairs_dev)
  *   delta           [out_features*in_features] fp32 out, row-major; every element written
  * Replaces reference forward.cu:513-569 (tile_accumulate_kernel; delta needs no pre-zeroing).
  */

@@ -185,10 +185,9 @@ def test_sigma_multiplier_2_5(device):
 def test_mask_path_binning_k_boundaries(device, k, tile, shape):
     """The mask path's binning at K around the 64-Gaussian ballot groups (a mask word pair each)
     and at the path's largest K, with Gaussians spanning the whole grid and Gaussians in the
-    last, partial tile row and column.  The small grid bins in the render (K * T <= 2^20), the
-    large one mostly in k_bin_tiles (a workgroup per tile row and column): tile_ptr and ids
-    bit-exact against the oracle's binning (bounds.py:24-75, tile_index.py:51-99), delta-W at
-    the field tolerance on the small grid."""
+    last, partial tile row and column.  K <= 256 bins in the render, larger K in k_bin_tiles (a
+    workgroup per tile row and column): tile_ptr and ids bit-exact against the oracle's binning
+    (bounds.py:24-75, tile_index.py:51-99), delta-W at the field tolerance on the small grid."""
     M, N = shape
     p = tiny_problem(M, N, k, 40 + k, log_scale_px=1.5 if M < 1000 else 3.0, spread=0.9)
     g = torch.Generator().manual_seed(k)
