@@ -270,8 +270,10 @@ __device__ inline GaussEval zero_eval() {
 
 // 2^clamp(q'), q' = -(A + z^2).
 __device__ inline float basis_w(const Problem& p, float A, float z) {
+  // q' <= 0 for the definite form, so the upper clamp (p.q_hi: 0, or +inf without a clamp)
+  // is the literal 0: an inline constant, which leaves med3 its one scalar operand for q_lo.
   const float q = -fmaf(z, z, A);
-  return __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(q, p.q_lo, p.q_hi));
+  return __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(q, p.q_lo, 0.0f));
 }
 
 // q' of a pixel for either form of GaussEval.
@@ -1307,14 +1309,35 @@ __device__ __forceinline__ void render16_body(
       acc[i] = fmaf(u.w, basis_w(p, A, z), acc[i]);
     }
   };
-  // Gaussians 0 .. nj-1 of a chunk (lane j holds Gaussian j), broadcast in order; one ballot
-  // per chunk picks the loop that handles general-form Gaussians.
+  // Gaussians 0 .. nj-1 of a chunk (lane j holds Gaussian j), staged in the wave's LDS and
+  // read back in order with broadcast loads (two ds_read_b128 per Gaussian instead of a
+  // v_readlane per constant); one ballot per chunk picks the loop that handles general-form
+  // Gaussians.
+  __shared__ float4 wevals[kTileThreads / 64][128];
+  float4* ew = wevals[wid];
   auto run_chunk = [&](const GaussEval& my, int nj) {
+    ew[2 * lane] = make_float4(my.mu0, my.mu1, my.wa, my.wb);
+    ew[2 * lane + 1] = make_float4(my.wc, my.w, __int_as_float(my.gid), my.gen);
+    wave_sync();
+    auto at = [&](int j) {
+      const float4 a = ew[2 * j], b = ew[2 * j + 1];
+      GaussEval u;
+      u.mu0 = a.x;
+      u.mu1 = a.y;
+      u.wa = a.z;
+      u.wb = a.w;
+      u.wc = b.x;
+      u.w = b.y;
+      u.gid = __float_as_int(b.z);
+      u.gen = b.w;
+      return u;
+    };
     if (__builtin_amdgcn_ballot_w64(lane < nj && my.gen != 0.0f) == 0) {
-      for (int j = 0; j < nj; ++j) accumulate(readlane_eval(my, j), std::false_type{});
+      for (int j = 0; j < nj; ++j) accumulate(at(j), std::false_type{});
     } else {
-      for (int j = 0; j < nj; ++j) accumulate(readlane_eval(my, j), std::true_type{});
+      for (int j = 0; j < nj; ++j) accumulate(at(j), std::true_type{});
     }
+    wave_sync();  // every lane has read the slots before the next chunk rewrites them
   };
   int64_t s, n;
   if (p.W > 0) {
@@ -1385,15 +1408,16 @@ __device__ __forceinline__ void render16_body(
         }
         wave_sync();
         const int32_t nwin = min(kWaveSortKeys, tot - base);
+        if (write_ids) {
+          for (int32_t j = lane; j < nwin; j += 64) {
+            const int64_t slot = done + j;
+            if (slot < room) ids[s + slot] = keys[j];
+          }
+        }
         for (int32_t j0 = 0; j0 < nwin; j0 += 64) {
           const int nj = min(64, nwin - j0);
           GaussEval my = zero_eval();
-          if (lane < nj) {
-            const int32_t g = keys[j0 + lane];
-            my = load_eval(ev, g);
-            const int64_t slot = done + j0 + lane;
-            if (write_ids && slot < room) ids[s + slot] = g;
-          }
+          if (lane < nj) my = load_eval(ev, keys[j0 + lane]);
           run_chunk(my, nj);
         }
         done += nwin;
