@@ -1612,6 +1612,8 @@ __device__ __forceinline__ void bwd16_body(
   if (t >= T) return;
   const int32_t r0 = st.r0, c0 = st.c0;
   const int64_t stripe = st.sidx & (p.S - 1);
+  float* const acc_s = acc + 8 * stripe;       // this tile's stripe of Gaussian 0's accumulators
+  const uint64_t stride8 = 8u * (uint32_t)p.S;  // floats from one Gaussian's stripes to the next's
   const int slot = lane >> 4, row = lane & 15;
   const int32_t pr = r0 + row;
   // This lane's row of dL/d(delta) (0 outside the matrix) and the tile's coordinates are
@@ -1661,12 +1663,13 @@ __device__ __forceinline__ void bwd16_body(
     const bool chunk_general = __builtin_amdgcn_ballot_w64(lane < nj && my.gen != 0.0f) != 0;
     for (int jb = 0; jb < nj; jb += 4) {
       const int j = jb + slot;
-      const int src = j < nj ? j : 0;
-      const float mu0 = __shfl(my.mu0, src, 64), mu1 = __shfl(my.mu1, src, 64);
-      const float wa = __shfl(my.wa, src, 64), wb = __shfl(my.wb, src, 64);
-      const float wc = __shfl(my.wc, src, 64);
-      const float gen = chunk_general ? __shfl(my.gen, src, 64) : 0.0f;
-      int32_t g = __shfl(myg, src, 64);
+      const int addr = j < nj ? j << 2 : 0;  // ds_bpermute byte address of the slot's lane
+      auto from = [&](float v) { return __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(v))); };
+      const float mu0 = from(my.mu0), mu1 = from(my.mu1);
+      const float wa = from(my.wa), wb = from(my.wb);
+      const float wc = from(my.wc);
+      const float gen = chunk_general ? from(my.gen) : 0.0f;
+      int32_t g = __builtin_amdgcn_ds_bpermute(addr, myg);
       if (j >= nj) g = -1;
       const float dx = x - mu0;
       const float a = wa * dx;
@@ -1693,7 +1696,7 @@ __device__ __forceinline__ void bwd16_body(
       if (g >= 0 && row >= 10) {
         const int k = row - 10;
         const float val = k == 0 ? v0 : k == 1 ? v1 : k == 2 ? v2 : k == 3 ? v3 : k == 4 ? v4 : m[5];
-        unsafeAtomicAdd(acc + 8 * ((int64_t)g * p.S + stripe) + k, val);
+        unsafeAtomicAdd(acc_s + ((uint64_t)(uint32_t)g * stride8 + (uint32_t)k), val);
       }
     }
     tile_general = tile_general || chunk_general;
