@@ -1597,7 +1597,7 @@ __device__ inline void stage_gaussians(const Problem& p, const GIdx* __restrict_
 // 16 pixels.  Gaussian constants are computed one per lane for up to 64 Gaussians at a time
 // and fetched by slot with a lane permute.
 // The moments of tile t (16x16) of one field by one wave.
-template <typename TpIdx, typename GIdx>
+template <typename TpIdx, typename GIdx, bool kTransposeSums>
 __device__ __forceinline__ void bwd16_body(
     const Problem& p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
@@ -1614,6 +1614,8 @@ __device__ __forceinline__ void bwd16_body(
   const int64_t stripe = st.sidx & (p.S - 1);
   float* const acc_s = acc + 8 * stripe;       // this tile's stripe of Gaussian 0's accumulators
   const uint64_t stride8 = 8u * (uint32_t)p.S;  // floats from one Gaussian's stripes to the next's
+  const bool hb3 = (lane & 8) != 0, hb2 = (lane & 4) != 0, hb1 = (lane & 2) != 0;
+  const bool atomic_lane = (lane & 1) == 0 && (lane & 15) < 12;
   const int slot = lane >> 4, row = lane & 15;
   const int32_t pr = r0 + row;
   // This lane's row of dL/d(delta) (0 outside the matrix) and the tile's coordinates are
@@ -1686,18 +1688,36 @@ __device__ __forceinline__ void bwd16_body(
         t2 += tt;
         t3 = fmaf(tt, dy, t3);
       }
-      float m[6] = {t0, dx * t0, t2, dx * dx * t0, dx * t2, t3};
-#pragma unroll
-      for (int k = 0; k < 6; ++k) m[k] = dpp_row_sum_f32(m[k]);
-      // Lane 15 of each 16-lane row holds the six sums; moment k moves to lane 10 + k
-      // (row_shl by 5 - k) and lanes 10..15 issue one atomic each.
-      const float v0 = dpp_f32<0x105>(m[0]), v1 = dpp_f32<0x104>(m[1]), v2 = dpp_f32<0x103>(m[2]);
-      const float v3 = dpp_f32<0x102>(m[3]), v4 = dpp_f32<0x101>(m[4]);
-      if (g >= 0 && row >= 10) {
-        const int k = row - 10;
-        const float val = k == 0 ? v0 : k == 1 ? v1 : k == 2 ? v2 : k == 3 ? v3 : k == 4 ? v4 : m[5];
-        unsafeAtomicAdd(acc_s + ((uint64_t)(uint32_t)g * stride8 + (uint32_t)k), val);
+      const float m0 = t0, m1 = dx * t0, m2 = t2, m3 = dx * dx * t0, m4 = dx * t2, m5 = t3;
+      if (!kTransposeSums) {
+        // Six independent row sums (the shorter dependency chain: single-field launches, where
+        // a wave makes few rounds).  Lane 15 of the slot's row holds the sums; moment k moves
+        // to lane 10 + k (row_shl by 5 - k) and lanes 10..15 add one each.
+        const float s0 = dpp_row_sum_f32(m0), s1 = dpp_row_sum_f32(m1), s2 = dpp_row_sum_f32(m2);
+        const float s3 = dpp_row_sum_f32(m3), s4 = dpp_row_sum_f32(m4), s5 = dpp_row_sum_f32(m5);
+        const float v0 = dpp_f32<0x105>(s0), v1 = dpp_f32<0x104>(s1), v2 = dpp_f32<0x103>(s2);
+        const float v3 = dpp_f32<0x102>(s3), v4 = dpp_f32<0x101>(s4);
+        if (g >= 0 && row >= 10) {
+          const int k = row - 10;
+          const float val = k == 0 ? v0 : k == 1 ? v1 : k == 2 ? v2 : k == 3 ? v3 : k == 4 ? v4 : s5;
+          unsafeAtomicAdd(acc_s + ((uint64_t)(uint32_t)g * stride8 + (uint32_t)k), val);
+        }
+        continue;
       }
+      // Batches (many rounds per wave): fewer instructions.  The six moments summed over the
+      // slot's 16 lanes by recursive halving: each step keeps
+      // half of a lane's values, sends the other half to its partner (lane ^ 15, ^ 7, ^ 2, ^ 1:
+      // row_mirror, row_half_mirror, two quad_perms) and adds what it receives.  Lane r ends
+      // with moment r >> 1 (moments 6, 7 are zero padding); even lanes 0..10 add it atomically.
+      const float a0 = (hb3 ? m4 : m0) + dpp_f32<0x140>(hb3 ? m0 : m4);
+      const float a1 = (hb3 ? m5 : m1) + dpp_f32<0x140>(hb3 ? m1 : m5);
+      const float a2 = (hb3 ? 0.0f : m2) + dpp_f32<0x140>(hb3 ? m2 : 0.0f);
+      const float a3 = (hb3 ? 0.0f : m3) + dpp_f32<0x140>(hb3 ? m3 : 0.0f);
+      const float c0 = (hb2 ? a2 : a0) + dpp_f32<0x141>(hb2 ? a0 : a2);
+      const float c1 = (hb2 ? a3 : a1) + dpp_f32<0x141>(hb2 ? a1 : a3);
+      float d = (hb1 ? c1 : c0) + dpp_f32<0x4e>(hb1 ? c0 : c1);
+      d += dpp_f32<0xb1>(d);
+      if (g >= 0 && atomic_lane) unsafeAtomicAdd(acc_s + ((uint64_t)(uint32_t)g * stride8 + (uint32_t)(row >> 1)), d);
     }
     tile_general = tile_general || chunk_general;
   }
@@ -1769,7 +1789,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
     const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
     const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
     uint8_t* ws, BwdLayout L) {
-  bwd16_body<TpIdx, GIdx>(p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gids,
+  bwd16_body<TpIdx, GIdx, false>(p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gids,
                           num_pairs, ws, L, sub_tile(p, blockIdx.x, wave_id()));
 }
 
@@ -2142,7 +2162,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
   const int64_t T = (int64_t)p.R * p.C;
   const int64_t P = ly.tile_ptr[T];  // pairs beyond the id capacity were never emitted
   const float* grad = reinterpret_cast<const float* const*>(plan + h->grad_table_off)[l];
-  bwd16_body<int64_t, int64_t>(p, grad, ly.row_coords, ly.col_coords, ly.mu, ly.chol_raw,
+  bwd16_body<int64_t, int64_t, true>(p, grad, ly.row_coords, ly.col_coords, ly.mu, ly.chol_raw,
                                reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
                                ly.tile_ptr, ly.ids, P < ly.capacity ? P : ly.capacity, ly.bws, L,
                                sub_tile(p, (int64_t)blockIdx.x - b0, wave_id()));
