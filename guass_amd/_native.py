@@ -61,7 +61,8 @@ class GfLayer(ctypes.Structure):
         ("num_pairs", c_void_p), ("gaussian_ids", c_void_p), ("ids_capacity", c_int64), ("forward_workspace", c_void_p),
         ("forward_workspace_bytes", c_size_t), ("grad_delta", c_void_p), ("d_mu", c_void_p),
         ("d_chol_raw", c_void_p), ("d_amp", c_void_p), ("backward_workspace", c_void_p),
-        ("backward_workspace_bytes", c_size_t), ("k_capacity", c_int64),
+        ("backward_workspace_bytes", c_size_t), ("k_capacity", c_int64), ("mu_tanh", c_int32),
+        ("reserved", c_int32),
     ]
 
 

@@ -110,7 +110,15 @@ struct Problem {
   int32_t normalize;
   int32_t W;  // words per tile-row / tile-column mask (0: the ids are emitted by k_emit)
   int32_t S;  // backward accumulator stripes (power of two): tile t adds into stripe t % S
+  int32_t mu_tanh;  // batched layers: mu holds mu_raw, the kernels use tanh(mu_raw) and d_mu
+                    // receives dL/d(mu_raw) (GaussianLinear.materialize_mu)
 };
+
+// A Gaussian's mean coordinate i (0: row, 1: column) as the field uses it.
+__device__ inline float mu_at(const Problem& p, const float* __restrict__ mu, int64_t i) {
+  const float v = mu[i];
+  return p.mu_tanh ? tanhf(v) : v;
+}
 
 // Per-Gaussian constants of the tile kernels: with dx = x - mu0, dy = y - mu1,
 //   a = wa dx,  z = wb dx + wc dy,  q' = kHalfLog2e * (d^T cov^-1 d),
@@ -243,7 +251,8 @@ __device__ inline GaussEval eval_geom(const Problem& p, const float* __restrict_
                                       const float* __restrict__ chol_raw,
                                       const float* __restrict__ amp, int64_t g) {
   const GfChol L = gf_activate_cholesky(chol_raw[3 * g + 0], chol_raw[3 * g + 1], chol_raw[3 * g + 2]);
-  return eval_from_cov(p, mu[2 * g + 0], mu[2 * g + 1], gf_cov_from_chol(L), amp ? amp[g] : 0.0f);
+  return eval_from_cov(p, mu_at(p, mu, 2 * g + 0), mu_at(p, mu, 2 * g + 1), gf_cov_from_chol(L),
+                       amp ? amp[g] : 0.0f);
 }
 
 __device__ inline GaussEval load_eval(const GaussEval* __restrict__ ev, int64_t g) {
@@ -609,7 +618,7 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
     float mu0, mu1, r11, r21, r22, amp;
   };
   auto load_in = [&](int64_t g) -> PrepIn {
-    return PrepIn{mu[2 * g + 0], mu[2 * g + 1], chol_raw[3 * g + 0], chol_raw[3 * g + 1],
+    return PrepIn{mu_at(p, mu, 2 * g + 0), mu_at(p, mu, 2 * g + 1), chol_raw[3 * g + 0], chol_raw[3 * g + 1],
                   chol_raw[3 * g + 2], kEval ? amp[g] : 0.0f};
   };
   auto prep = [&](int64_t g, const PrepIn& in) -> int4 {
@@ -993,7 +1002,7 @@ __device__ __forceinline__ void emit_body(const Problem& p, const float* __restr
     c.s00 = c4.x;
     c.s01 = c4.y;
     c.s11 = c4.z;
-    GaussEval v = eval_from_cov(p, mu[2 * g + 0], mu[2 * g + 1], c, amp[g]);
+    GaussEval v = eval_from_cov(p, mu_at(p, mu, 2 * g + 0), mu_at(p, mu, 2 * g + 1), c, amp[g]);
     v.gid = (int32_t)g;
     store_eval(reinterpret_cast<GaussEval*>(ws + L.eval), g, v);
   }
@@ -1878,7 +1887,7 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
 __device__ __forceinline__ void finish_body(
     const Problem& p, const float* __restrict__ chol_raw, const float* __restrict__ amp,
     float* __restrict__ d_mu, float* __restrict__ d_chol_raw, float* __restrict__ d_amp, uint8_t* ws,
-    const BwdLayout& L, int64_t idx) {
+    const BwdLayout& L, int64_t idx, const float* __restrict__ mu = nullptr) {
   float* acc = reinterpret_cast<float*>(ws + L.acc);
   const int64_t g = idx / p.S;
   const int32_t st = (int32_t)(idx & (p.S - 1));
@@ -1909,8 +1918,15 @@ __device__ __forceinline__ void finish_body(
   const double nrm = (double)rg.norm;
   const double an = a * nrm;
   d_amp[g] = (float)(nrm * S0);
-  d_mu[2 * g + 0] = (float)(an * (rg.i00 * S1 + rg.i01 * S2));
-  d_mu[2 * g + 1] = (float)(an * (rg.i01 * S1 + rg.i11 * S2));
+  float dm0 = (float)(an * (rg.i00 * S1 + rg.i01 * S2));
+  float dm1 = (float)(an * (rg.i01 * S1 + rg.i11 * S2));
+  if (p.mu_tanh) {  // dL/d(mu_raw) = dL/d(mu) * (1 - tanh(mu_raw)^2), as torch's tanh backward
+    const float y0 = tanhf(mu[2 * g + 0]), y1 = tanhf(mu[2 * g + 1]);
+    dm0 = dm0 * (1.0f - y0 * y0);
+    dm1 = dm1 * (1.0f - y1 * y1);
+  }
+  d_mu[2 * g + 0] = dm0;
+  d_mu[2 * g + 1] = dm1;
   const double G00 = -0.5 * an * S3, G01 = -0.5 * an * S4, G11 = -0.5 * an * S5;
   const double ag00 = rg.i00 * G00 + rg.i01 * G01, ag01 = rg.i00 * G01 + rg.i01 * G11;
   const double ag10 = rg.i01 * G00 + rg.i11 * G01, ag11 = rg.i01 * G01 + rg.i11 * G11;
@@ -2010,6 +2026,7 @@ int make_problem(const gf_field_config* cfg, int64_t M, int64_t N, int64_t K, Pr
   }
   p->normalize = cfg->normalize ? 1 : 0;
   p->S = backward_stripes(K, R * C);
+  p->mu_tanh = 0;
   // Mask path (no emission kernel): 16x16 or 32x32 tiles, 1 <= K <= kMaskMaxK, a tile grid
   // k_bin bins in LDS, and masks of a bounded total size.
   p->W = 0;
@@ -2208,7 +2225,7 @@ __global__ __launch_bounds__(kTileThreads) void k_finish_batch(const uint8_t* __
   const Problem p = ly.p;
   const BwdLayout L = ly.bl;
   finish_body(p, ly.chol_raw, ly.amp, ly.d_mu, ly.d_chol_raw, ly.d_amp, ly.bws, L,
-              ((int64_t)blockIdx.x - b0) * kTileThreads + threadIdx.x);
+              ((int64_t)blockIdx.x - b0) * kTileThreads + threadIdx.x, ly.mu);
 }
 
 template <typename TP, typename GI>
@@ -2454,6 +2471,8 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
       std::snprintf(why, sizeof(why), "%s", g_err);
       return set_err(rc, "layer %zu: %s", i, why);
     }
+    if (in.mu_tanh != 0 && in.mu_tanh != 1) return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: mu_tanh must be 0 or 1", i);
+    ly.p.mu_tanh = in.mu_tanh;
     const int64_t T = (int64_t)ly.p.R * ly.p.C, K = in.k;
     if (in.k_capacity < 0) return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: k_capacity < 0", i);
     // Grids for the capacity: a layer on the emission path at any k <= kc keeps its emit blocks.

@@ -256,20 +256,18 @@ class _null:
 
 class _BatchedFieldFunction(torch.autograd.Function):
     """Autograd node of GaussianFieldBatch.render(): inputs (mu_raw, chol_raw, amp) of every
-    layer, outputs every layer's delta-W [out_features, in_features].  mu = tanh(mu_raw)
-    (gaussian_linear.py:153-154) is taken inside, for all layers in one multi-tensor launch, and
-    its derivative 1 - mu^2 is applied the same way in the backward."""
+    layer, outputs every layer's delta-W [out_features, in_features].  The batched kernels take
+    mu = tanh(mu_raw) (gaussian_linear.py:153-154) themselves and return dL/d(mu_raw)."""
 
     @staticmethod
     def forward(ctx, fb: "GaussianFieldBatch", *params: Tensor):
         ctx.fb = fb
-        deltas, ctx.mus = fb._run_forward(params)
-        return tuple(deltas)
+        return tuple(fb._run_forward())
 
     @staticmethod
     def backward(ctx, *grads: Tensor):
         fb: GaussianFieldBatch = ctx.fb
-        return (None, *fb._run_backward(grads, ctx.mus))
+        return (None, *fb._run_backward(grads))
 
 
 class GaussianFieldBatch:
@@ -332,23 +330,29 @@ class GaussianFieldBatch:
         self._kcaps = kc
         self._ks = [ly.num_gaussians for ly in self.layers]
         self._pairs = None
-        self._mu_store: list[Tensor] = []
         self._zero_grads: dict[int, Tensor] = {}
         self.replans = 0  # re-plans after the first plan (parameter tensors or K changed)
 
     # ---------------------------------------------------------------- plan
 
     def _param_key(self):
-        return tuple((ly.num_gaussians, ly.chol_raw.data_ptr(), ly.amp.data_ptr()) for ly in self.layers)
+        return tuple((ly.num_gaussians, ly.mu_raw.data_ptr(), ly.chol_raw.data_ptr(), ly.amp.data_ptr())
+                     for ly in self.layers)
 
     def _build(self) -> None:
-        """Plans, or re-plans in place, for the layers' current K and parameter tensors."""
+        """Plans, or re-plans in place, for the layers' current K and parameter tensors (which
+        the kernels read in place: mu_raw, chol_raw and amp as contiguous float32)."""
         from guass_amd.ops import FieldBatchPlan
 
         class _View:
             pass
 
+        views = []
         for i, ly in enumerate(self.layers):
+            for name in ("mu_raw", "chol_raw", "amp"):
+                t = getattr(ly, name)
+                if t.dtype != torch.float32 or not t.is_contiguous():
+                    raise ValueError(f"layer {i}: {name} must be contiguous float32")
             K = ly.num_gaussians
             if K > self._kcaps[i]:
                 self._kcaps[i] = max(K, 2 * self._kcaps[i])
@@ -356,22 +360,12 @@ class GaussianFieldBatch:
                 # pairs scale with K: grow the id capacity with it rather than by a retry
                 self._caps[i] = max(self._caps[i], int(self._pairs[i] * K / self._ks[i] * self.headroom) + 1)
             self._ks[i] = K
-        views = []
-        for i, ly in enumerate(self.layers):
-            K = ly.num_gaussians
-            if i == len(self._mu_store) or self._mu_store[i].shape[0] < K:
-                store = torch.empty(self._kcaps[i], 2, dtype=torch.float32, device=self.device)
-                if i == len(self._mu_store):
-                    self._mu_store.append(store)
-                else:
-                    self._mu_store[i] = store
             v = _View()
             v.row_coords, v.col_coords = ly.row_coords, ly.col_coords
-            v.mu = self._mu_store[i][:K]
-            v.chol_raw, v.amp = ly.chol_raw, ly.amp
+            v.mu, v.chol_raw, v.amp = ly.mu_raw, ly.chol_raw, ly.amp
+            v.mu_tanh = True
             v.grad = None
             views.append(v)
-        self._mu_bufs = [v.mu for v in views]
         if self._plan is None:
             c0 = self.layers[0].adapter_config
             self._plan = FieldBatchPlan(views, self.device, capacities=self._caps, k_capacities=self._kcaps,
@@ -381,6 +375,11 @@ class GaussianFieldBatch:
         else:
             self._plan.update(views, capacities=self._caps, k_capacities=self._kcaps)
             self.replans += 1
+        pl = self._plan
+        self._deltas = [q.delta.view(q.M, q.N) for q in pl.plans]
+        # the gradient buffer split per parameter: d_mu_raw [K,2], d_chol_raw [K,3], d_amp [K,1]
+        self._grad_sizes = [n for q in pl.plans for n in (2 * q.K, 3 * q.K, q.K)]
+        self._grad_shapes = [sh for q in pl.plans for sh in ((q.K, 2), (q.K, 3), (q.K, 1))]
         self._key = self._param_key()
 
     # ---------------------------------------------------------------- passes
@@ -388,11 +387,6 @@ class GaussianFieldBatch:
     def render(self) -> list[Tensor]:
         """Renders every layer's delta-W for this step (autograd-tracked) and hands each layer
         its own for its next forward; returns them."""
-        for i, ly in enumerate(self.layers):
-            for name in ("chol_raw", "amp"):
-                t = getattr(ly, name)
-                if t.dtype != torch.float32 or not t.is_contiguous():
-                    raise ValueError(f"layer {i}: {name} must be contiguous float32")
         ctx = torch.autocast(device_type="cuda", enabled=False) if self.device.type == "cuda" else _null()
         with ctx:
             params = []
@@ -403,13 +397,11 @@ class GaussianFieldBatch:
             ly._batched_delta = d
         return list(deltas)
 
-    def _run_forward(self, params) -> tuple[list[Tensor], list[Tensor]]:
+    def _run_forward(self) -> list[Tensor]:
         Nat = self._Nat
         if self._plan is None or self._key != self._param_key():
             self._build()
-        mus = torch._foreach_tanh([t.detach() for t in params[0::3]])
         for _ in range(8):
-            torch._foreach_copy_(self._mu_bufs, mus)
             self._plan.forward()
             status, pairs = self._plan.read(clear=True)
             over = [i for i, st in enumerate(status) if st & Nat.GF_STATUS_CAPACITY]
@@ -418,7 +410,7 @@ class GaussianFieldBatch:
                 raise RuntimeError(f"batched fields: device status {bad} (layer, GF_STATUS_* bits)")
             if not over:
                 self._pairs = pairs
-                return [pl.delta.view(pl.M, pl.N) for pl in self._plan.plans], mus
+                return self._deltas
             for i in over:
                 self._caps[i] = max(int(pairs[i] * self.headroom) + 1, self._caps[i] * 2)
             self._build()
@@ -432,28 +424,17 @@ class GaussianFieldBatch:
             self._zero_grads[i] = z
         return z
 
-    def _run_backward(self, grads, mus) -> list[Tensor | None]:
+    def _run_backward(self, grads) -> list[Tensor | None]:
         gs = []
         for i, g in enumerate(grads):
-            gs.append(self._zero_grad(i) if g is None else g.to(torch.float32).contiguous().view(-1))
-        self._plan.set_grads(gs)
+            if g is None:
+                g = self._zero_grad(i)
+            elif g.dtype != torch.float32 or not g.is_contiguous():
+                g = g.to(torch.float32).contiguous()
+            gs.append(g)
+        self._plan.set_grads(gs, check=False)
         self._plan.backward()
         # one copy of every layer's gradients (the plan's buffer is rewritten by the next
-        # backward), then d mu_raw = d mu * (1 - mu^2)
+        # backward), split into the parameters' shapes
         flat = self._plan.grad_flat[:self._plan.grad_numel].clone()
-        d_mu, d_chol, d_amp = [], [], []
-        o = 0
-        for pl in self._plan.plans:
-            K = pl.K
-            d_mu.append(flat[o:o + 2 * K].view(K, 2))
-            d_chol.append(flat[o + 2 * K:o + 5 * K].view(K, 3))
-            d_amp.append(flat[o + 5 * K:o + 6 * K].view(K, 1))
-            o += 6 * K
-        one_minus = torch._foreach_mul(mus, mus)
-        torch._foreach_neg_(one_minus)
-        torch._foreach_add_(one_minus, 1.0)
-        d_mu_raw = torch._foreach_mul(d_mu, one_minus)
-        out: list[Tensor | None] = []
-        for a, b, c in zip(d_mu_raw, d_chol, d_amp):
-            out += [a, b, c]
-        return out
+        return [t.view(sh) for t, sh in zip(flat.split(self._grad_sizes), self._grad_shapes)]

@@ -171,7 +171,8 @@ class FieldBatchPlan:
 
     ``layers`` is a sequence of objects with device tensors ``row_coords``, ``col_coords``,
     ``mu``, ``chol_raw``, ``amp`` and, for the backward, ``grad`` (dL/d(delta), read in place at
-    every ``backward()``).  The plan keeps references to them: their storage must stay put until
+    every ``backward()``); a true ``mu_tanh`` attribute marks ``mu`` as GaussianLinear's mu_raw
+    (the kernels take tanh and ``d_mu`` receives dL/d(mu_raw)).  The plan keeps references to them: their storage must stay put until
     the next :meth:`update`.  Each layer gets the buffers of a :class:`FieldPlan`
     (``self.plans[i]``: delta, tile_ptr, ids, pair constants, gradients).  16x16 or 32x32 tiles
     (32x32: every layer's K <= 8192).
@@ -243,7 +244,7 @@ class FieldBatchPlan:
                 pl.num_pairs.data_ptr(), pl.ids.data_ptr(), pl.capacity,
                 pl.fwd_ws.data_ptr(), pl.fwd_ws_bytes, None if grad is None else grad.data_ptr(),
                 N.ptr(pl.d_mu), N.ptr(pl.d_chol_raw), N.ptr(pl.d_amp), pl.bwd_ws.data_ptr(),
-                pl.bwd_ws_bytes, pl.k_capacity)
+                pl.bwd_ws_bytes, pl.k_capacity, 1 if getattr(ly, "mu_tanh", False) else 0, 0)
         info = N.GfBatchInfo()
         L = N.lib()
         N.check(L.gf_batch_plan(ctypes.byref(self.cfg), table, n, None, 0, ctypes.byref(info),
@@ -270,13 +271,14 @@ class FieldBatchPlan:
         N.check(N.lib().gf_batch_backward(self.plan.data_ptr(), ctypes.byref(self.info), phases,
                                           self._stream()), "gf_batch_backward")
 
-    def set_grads(self, grads) -> None:
+    def set_grads(self, grads, check: bool = True) -> None:
         """dL/d(delta) of every layer for the next ``backward()`` (contiguous fp32 device tensors
-        of M*N elements, kept alive by the plan until replaced); no host synchronisation."""
+        of M*N elements, kept alive by the plan until replaced); no host synchronisation.
+        ``check=False`` skips the per-tensor checks for callers that guarantee them."""
         grads = list(grads)
         if len(grads) != len(self.plans):
             raise ValueError(f"expected {len(self.plans)} gradients, got {len(grads)}")
-        for i, (g, pl) in enumerate(zip(grads, self.plans)):
+        for i, (g, pl) in enumerate(zip(grads, self.plans) if check else ()):
             if (g.dtype != torch.float32 or not g.is_contiguous() or g.numel() != pl.M * pl.N
                     or g.device != self.device):
                 raise ValueError(f"layer {i}: dL/d(delta) must be a contiguous float32 tensor of "

@@ -190,6 +190,11 @@ typedef struct gf_layer {
    * its gf_batch_info, so launches captured in a graph stay valid.  The buffers above must be
    * sized for the current k only. */
   int64_t k_capacity;
+  /* 1: mu holds GaussianLinear's mu_raw (gaussian_linear.py:153-154 takes mu = tanh(mu_raw));
+   * the kernels use tanh(mu_raw) (the device tanhf torch's GPU tanh uses) and d_mu receives
+   * dL/d(mu_raw).  0: mu is used as given. */
+  int32_t mu_tanh;
+  int32_t reserved;
 } gf_layer;
 
 typedef struct gf_batch_info {
