@@ -412,25 +412,6 @@ __device__ int64_t block_scan_runs(int64_t* data, int64_t n, int64_t* lds) {
 // ------------------------------------------------------------------------------------------
 // k_bin: one workgroup.
 
-__device__ inline int32_t wave_inclusive_scan32(int32_t x) { return dpp_scan_i32(x); }
-
-// Exclusive scan of the int32 values lds[0..n) by the workgroup (each thread owns a contiguous
-// run), written to out[0..n) as int64; returns the total.
-__device__ int64_t bin_scan_lds_to_global(const int32_t* lds, int64_t n, int64_t* out, int64_t* scan_lds) {
-  const int64_t per = (n + kBinThreads - 1) / kBinThreads;
-  const int64_t b = (int64_t)threadIdx.x * per;
-  const int64_t e = b + per < n ? b + per : n;
-  int64_t s = 0;
-  for (int64_t i = b; i < e; ++i) s += lds[i];
-  int64_t total;
-  int64_t run = block_exclusive_scan<kBinThreads>(s, &total, scan_lds);
-  for (int64_t i = b; i < e; ++i) {
-    out[i] = run;
-    run += lds[i];
-  }
-  return total;
-}
-
 __device__ inline void store_eval(GaussEval* ev, int64_t i, const GaussEval& v) {
   float4* q = reinterpret_cast<float4*>(ev + i);
   q[0] = make_float4(v.mu0, v.mu1, v.wa, v.wb);
@@ -1361,7 +1342,6 @@ __device__ __forceinline__ void render16_body(
       __shared__ uint32_t wmask[kTileThreads / 64][kMaskMaxK / 32];
       uint32_t* mw = wmask[wid];
       int64_t before = 0, cnt = 0;
-#pragma unroll 4
       for (int64_t g0 = 0; g0 < p.K; g0 += 64) {
         const int64_t g = g0 + lane;
         bool covers = false;
@@ -2473,7 +2453,7 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
     }
     if (in.mu_tanh != 0 && in.mu_tanh != 1) return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: mu_tanh must be 0 or 1", i);
     ly.p.mu_tanh = in.mu_tanh;
-    const int64_t T = (int64_t)ly.p.R * ly.p.C, K = in.k;
+    const int64_t K = in.k;
     if (in.k_capacity < 0) return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: k_capacity < 0", i);
     // Grids for the capacity: a layer on the emission path at any k <= kc keeps its emit blocks.
     const int64_t kc = std::max<int64_t>(K, in.k_capacity);
