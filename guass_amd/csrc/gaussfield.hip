@@ -1679,8 +1679,8 @@ __device__ __forceinline__ void bwd16_body(
       }
       const float m0 = t0, m1 = dx * t0, m2 = t2, m3 = dx * dx * t0, m4 = dx * t2, m5 = t3;
       if (!kTransposeSums) {
-        // Six independent row sums (the shorter dependency chain: single-field launches, where
-        // a wave makes few rounds).  Lane 15 of the slot's row holds the sums; moment k moves
+        // Six independent row sums (the shorter dependency chain, for sparse tiles where a wave
+        // makes few rounds).  Lane 15 of the slot's row holds the sums; moment k moves
         // to lane 10 + k (row_shl by 5 - k) and lanes 10..15 add one each.
         const float s0 = dpp_row_sum_f32(m0), s1 = dpp_row_sum_f32(m1), s2 = dpp_row_sum_f32(m2);
         const float s3 = dpp_row_sum_f32(m3), s4 = dpp_row_sum_f32(m4), s5 = dpp_row_sum_f32(m5);
@@ -1693,7 +1693,7 @@ __device__ __forceinline__ void bwd16_body(
         }
         continue;
       }
-      // Batches (many rounds per wave): fewer instructions.  The six moments summed over the
+      // Dense tiles and batches (many rounds per wave): fewer instructions.  The six moments summed over the
       // slot's 16 lanes by recursive halving: each step keeps
       // half of a lane's values, sends the other half to its partner (lane ^ 15, ^ 7, ^ 2, ^ 1:
       // row_mirror, row_half_mirror, two quad_perms) and adds what it receives.  Lane r ends
@@ -1771,15 +1771,15 @@ __device__ __forceinline__ void bwd16_body(
 
 // Seven waves per SIMD (72 VGPRs): the rarely taken indefinite-form pass would otherwise
 // raise the register count and cost the common path occupancy.
-template <typename TpIdx, typename GIdx>
+template <typename TpIdx, typename GIdx, bool kTransposeSums>
 __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_bwd16(
     Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
     const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
     const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
     uint8_t* ws, BwdLayout L) {
-  bwd16_body<TpIdx, GIdx, false>(p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gids,
-                          num_pairs, ws, L, sub_tile(p, blockIdx.x, wave_id()));
+  bwd16_body<TpIdx, GIdx, kTransposeSums>(p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr,
+                                          gids, num_pairs, ws, L, sub_tile(p, blockIdx.x, wave_id()));
 }
 
 __device__ inline float wave_sum(float v) {
@@ -2213,8 +2213,15 @@ void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, 
                 const float* cc, const float* mu, const float* raw, const GaussEval* ev,
                 const void* tile_ptr, const void* gids, int64_t num_pairs, uint8_t* ws,
                 const BwdLayout& L) {
-  if (quad_tiles(p))
-    hipLaunchKernelGGL((k_bwd16<TP, GI>), dim3((unsigned)quad_grid(p)), dim3(kTileThreads), 0, st,
+  // Tiles of many Gaussians (a wave makes >= 4 rounds on average) take the transposing
+  // moment reduction (fewer instructions); sparse ones the row sums (shorter chain).
+  const bool dense = num_pairs >= 16 * (int64_t)p.R * p.C;
+  if (quad_tiles(p) && dense)
+    hipLaunchKernelGGL((k_bwd16<TP, GI, true>), dim3((unsigned)quad_grid(p)), dim3(kTileThreads), 0, st,
+                       p, grad, rc, cc, mu, raw, ev, reinterpret_cast<const TP*>(tile_ptr),
+                       reinterpret_cast<const GI*>(gids), num_pairs, ws, L);
+  else if (quad_tiles(p))
+    hipLaunchKernelGGL((k_bwd16<TP, GI, false>), dim3((unsigned)quad_grid(p)), dim3(kTileThreads), 0, st,
                        p, grad, rc, cc, mu, raw, ev, reinterpret_cast<const TP*>(tile_ptr),
                        reinterpret_cast<const GI*>(gids), num_pairs, ws, L);
   else

@@ -209,6 +209,15 @@ def test_mask_path_binning_k_boundaries(device, k, tile, shape):
         field_close(delta, ref)
 
 
+@pytest.mark.parametrize("tile", [16, 32])
+def test_dense_tiles_backward(device, tile):
+    """Tiles of many Gaussians (P >= 16 T: the single-field backward takes the transposing
+    moment reduction) against the oracle."""
+    p = tiny_problem(256, 256, 2048, 21, log_scale_px=2.5)
+    g, r = check(p, device, batched=True, tile_out=tile, tile_in=tile)
+    assert int(r[1][-1]) >= 16 * (256 // tile) ** 2, "not dense enough for the transposing reduction"
+
+
 def test_k1_corner_and_huge(device):
     # one Gaussian at the top-left corner, one covering the whole matrix
     p = tiny_problem(70, 90, 2, 7)
