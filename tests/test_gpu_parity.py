@@ -729,6 +729,34 @@ def test_gaussian_field_batch_densification(device, tile):
     assert fb.replans >= len(events)
 
 
+def test_field_plan_resize_within_capacity(device):
+    """A single-field FieldPlan moved between K values (densification: clone and prune,
+    reference controllers/clone.py:31-56, prune.py:34-45) within its k_capacity: forward and
+    backward against the oracle at every K, with no buffer reallocated; past the capacity its
+    buffers grow."""
+    plan = FieldPlan(320, 768, 64, device, ids_capacity=1 << 18, k_capacity=512)
+    bufs = (plan.fwd_ws.data_ptr(), plan.bwd_ws.data_ptr(), plan.ids.data_ptr(), plan._d_mu.data_ptr())
+    for k, seed in ((64, 1), (300, 2), (512, 3), (100, 4), (700, 5)):
+        p = wl.make_problem(f"resize_k{k}", 320, 768, k, math.log(6.0), 0.7, seed)
+        grew = plan.resize(k)
+        say(f"FieldPlan.resize to K={k}: grew={grew}")
+        assert grew == (k > 512), f"K={k}: reallocation {grew}"
+        if k <= 512:
+            assert (plan.fwd_ws.data_ptr(), plan.bwd_ws.data_ptr(), plan.ids.data_ptr(),
+                    plan._d_mu.data_ptr()) == bufs
+        q = p.to(device)
+        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+        d_mu, d_chol, d_amp = plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+        torch.cuda.synchronize()
+        assert plan.status() == 0
+        r = oracle(p)
+        P = int(r[1][-1])
+        binning_equal(plan.tile_ptr, plan.ids[:P], r[1], r[2])
+        field_close(plan.delta, r[0])
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (d_mu, d_chol, d_amp), r[3:]):
+            grad_close(a, b, f"K={k} {name}")
+
+
 @pytest.mark.parametrize("tile", [16, 32])
 def test_batch_plan_update_keeps_captured_graph_valid(device, tile):
     """A graph captured over gf_batch_forward + gf_batch_backward before every layer's K and
