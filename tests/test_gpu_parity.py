@@ -218,6 +218,30 @@ def test_dense_tiles_backward(device, tile):
     assert int(r[1][-1]) >= 16 * (256 // tile) ** 2, "not dense enough for the transposing reduction"
 
 
+def _random_cases(n: int, seed: int):
+    g = torch.Generator().manual_seed(seed)
+    tiles = [(16, 16), (32, 32), (16, 16), (8, 24), (32, 16), (4, 4)]
+    for i in range(n):
+        M = int(torch.randint(1, 140, (1,), generator=g))
+        N = int(torch.randint(1, 140, (1,), generator=g))
+        K = int(torch.randint(0, 300, (1,), generator=g))
+        to, ti = tiles[i % len(tiles)]
+        log_scale = float(torch.empty(1).uniform_(0.0, 3.0, generator=g))
+        sigma = float(torch.empty(1).uniform_(1.5, 3.5, generator=g))
+        clamp = None if i % 5 == 4 else float(torch.empty(1).uniform_(20.0, 100.0, generator=g))
+        yield i, M, N, K, to, ti, log_scale, sigma, clamp, i % 7 == 3
+
+
+@pytest.mark.parametrize("case", list(_random_cases(40, 2026)), ids=lambda c: f"r{c[0]}")
+def test_random_fields(device, case):
+    """Seeded random fields over sizes (ragged and tiny), K (including 0), tile shapes (the
+    mask path's 16x16 / 32x32, the emission path's others), sigma multiplier, clamp (or none)
+    and normalisation: binning bit-exact, delta-W and gradients at the parity bars."""
+    i, M, N, K, to, ti, log_scale, sigma, clamp, normalize = case
+    p = wl.make_problem(f"rand{i}", M, N, K, log_scale, 0.6, 100 + i)
+    check(p, device, tile_out=to, tile_in=ti, sigma=sigma, clamp=clamp, normalize=normalize)
+
+
 def test_k1_corner_and_huge(device):
     # one Gaussian at the top-left corner, one covering the whole matrix
     p = tiny_problem(70, 90, 2, 7)
