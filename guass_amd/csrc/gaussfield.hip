@@ -112,6 +112,8 @@ struct Problem {
   int32_t S;  // backward accumulator stripes (power of two): tile t adds into stripe t % S
   int32_t mu_tanh;  // batched layers: mu holds mu_raw, the kernels use tanh(mu_raw) and d_mu
                     // receives dL/d(mu_raw) (GaussianLinear.materialize_mu)
+  int32_t mask_clamp;  // clamp_quad < 80: the backward drops clamped pixels from the quadratic-
+                       // form moments (at 80 and above their terms are below e^-40)
 };
 
 // A Gaussian's mean coordinate i (0: row, 1: column) as the field uses it.
@@ -1586,7 +1588,7 @@ __device__ inline void stage_gaussians(const Problem& p, const GIdx* __restrict_
 // 16 pixels.  Gaussian constants are computed one per lane for up to 64 Gaussians at a time
 // and fetched by slot with a lane permute.
 // The moments of tile t (16x16) of one field by one wave.
-template <typename TpIdx, typename GIdx, bool kTransposeSums>
+template <typename TpIdx, typename GIdx, bool kTransposeSums, bool kMaskClamp>
 __device__ __forceinline__ void bwd16_body(
     const Problem& p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
@@ -1667,17 +1669,32 @@ __device__ __forceinline__ void bwd16_body(
       const float A = a * a;
       const float b = wb * dx;
       if (chunk_general && gen != 0.0f) g = -1;  // indefinite form: the pass below
-      float t0 = 0.f, t2 = 0.f, t3 = 0.f;
+      float t0 = 0.f, t2 = 0.f, t3 = 0.f, tq = 0.f;
 #pragma unroll
       for (int c = 0; c < 16; ++c) {
         const float dy = yv[c] - mu1;
-        const float ge = gv[c] * basis_w(p, A, fmaf(wc, dy, b));
-        t0 += ge;
-        const float tt = ge * dy;
-        t2 += tt;
-        t3 = fmaf(tt, dy, t3);
+        if (kMaskClamp) {
+          // clamped pixels (q > clamp_quad) carry no quadratic-form gradient (the reference's
+          // clamp mask, backward.cu:316-320,336-338): they add to S0 only
+          const float z = fmaf(wc, dy, b);
+          const float qv = -fmaf(z, z, A);
+          const float ge = gv[c] * __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(qv, p.q_lo, 0.0f));
+          t0 += ge;
+          const float gq = qv < p.q_lo ? 0.0f : ge;
+          tq += gq;
+          const float tt = gq * dy;
+          t2 += tt;
+          t3 = fmaf(tt, dy, t3);
+        } else {
+          const float ge = gv[c] * basis_w(p, A, fmaf(wc, dy, b));
+          t0 += ge;
+          const float tt = ge * dy;
+          t2 += tt;
+          t3 = fmaf(tt, dy, t3);
+        }
       }
-      const float m0 = t0, m1 = dx * t0, m2 = t2, m3 = dx * dx * t0, m4 = dx * t2, m5 = t3;
+      const float t0q = kMaskClamp ? tq : t0;  // the quadratic-form moments' share of S0
+      const float m0 = t0, m1 = dx * t0q, m2 = t2, m3 = dx * dx * t0q, m4 = dx * t2, m5 = t3;
       if (!kTransposeSums) {
         // Six independent row sums (the shorter dependency chain, for sparse tiles where a wave
         // makes few rounds).  Lane 15 of the slot's row holds the sums; moment k moves
@@ -1771,14 +1788,14 @@ __device__ __forceinline__ void bwd16_body(
 
 // Seven waves per SIMD (72 VGPRs): the rarely taken indefinite-form pass would otherwise
 // raise the register count and cost the common path occupancy.
-template <typename TpIdx, typename GIdx, bool kTransposeSums>
+template <typename TpIdx, typename GIdx, bool kTransposeSums, bool kMaskClamp>
 __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_bwd16(
     Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
     const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
     const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
     uint8_t* ws, BwdLayout L) {
-  bwd16_body<TpIdx, GIdx, kTransposeSums>(p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr,
+  bwd16_body<TpIdx, GIdx, kTransposeSums, kMaskClamp>(p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr,
                                           gids, num_pairs, ws, L, sub_tile(p, blockIdx.x, wave_id()));
 }
 
@@ -1828,8 +1845,8 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
         const float q = quad_form(v, dx, dy);
         const float ge = gr * basis_q(p, q);
         m[0] += ge;
-        // clamped pixels of a general-form Gaussian carry no quadratic-form gradient
-        const float gq = (v.gen != 0.0f && !(q >= p.q_lo && q <= p.q_hi)) ? 0.f : ge;
+        // clamped pixels carry no quadratic-form gradient (backward.cu:316-320,336-338)
+        const float gq = !(q >= p.q_lo && q <= p.q_hi) ? 0.f : ge;
         m[1] += gq * dx;
         m[2] += gq * dy;
         m[3] += gq * dx * dx;
@@ -2007,6 +2024,7 @@ int make_problem(const gf_field_config* cfg, int64_t M, int64_t N, int64_t K, Pr
   p->normalize = cfg->normalize ? 1 : 0;
   p->S = backward_stripes(K, R * C);
   p->mu_tanh = 0;
+  p->mask_clamp = (cfg->has_clamp_quad && cfg->clamp_quad < 80.0) ? 1 : 0;
   // Mask path (no emission kernel): 16x16 or 32x32 tiles, 1 <= K <= kMaskMaxK, a tile grid
   // k_bin bins in LDS, and masks of a bounded total size.
   p->W = 0;
@@ -2149,6 +2167,7 @@ __global__ __launch_bounds__(kTileThreads) void k_render16_batch(const uint8_t* 
                 sub_tile(p, (int64_t)blockIdx.x - b0, wave_id()));
 }
 
+template <bool kMaskClamp>
 __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_bwd16_batch(const uint8_t* __restrict__ plan) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
   int64_t b0;
@@ -2159,7 +2178,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
   const int64_t T = (int64_t)p.R * p.C;
   const int64_t P = ly.tile_ptr[T];  // pairs beyond the id capacity were never emitted
   const float* grad = reinterpret_cast<const float* const*>(plan + h->grad_table_off)[l];
-  bwd16_body<int64_t, int64_t, true>(p, grad, ly.row_coords, ly.col_coords, ly.mu, ly.chol_raw,
+  bwd16_body<int64_t, int64_t, true, kMaskClamp>(p, grad, ly.row_coords, ly.col_coords, ly.mu, ly.chol_raw,
                                reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
                                ly.tile_ptr, ly.ids, P < ly.capacity ? P : ly.capacity, ly.bws, L,
                                sub_tile(p, (int64_t)blockIdx.x - b0, wave_id()));
@@ -2216,15 +2235,23 @@ void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, 
   // Tiles of many Gaussians (a wave makes >= 4 rounds on average) take the transposing
   // moment reduction (fewer instructions); sparse ones the row sums (shorter chain).
   const bool dense = num_pairs >= 16 * (int64_t)p.R * p.C;
-  if (quad_tiles(p) && dense)
-    hipLaunchKernelGGL((k_bwd16<TP, GI, true>), dim3((unsigned)quad_grid(p)), dim3(kTileThreads), 0, st,
-                       p, grad, rc, cc, mu, raw, ev, reinterpret_cast<const TP*>(tile_ptr),
-                       reinterpret_cast<const GI*>(gids), num_pairs, ws, L);
-  else if (quad_tiles(p))
-    hipLaunchKernelGGL((k_bwd16<TP, GI, false>), dim3((unsigned)quad_grid(p)), dim3(kTileThreads), 0, st,
-                       p, grad, rc, cc, mu, raw, ev, reinterpret_cast<const TP*>(tile_ptr),
-                       reinterpret_cast<const GI*>(gids), num_pairs, ws, L);
-  else
+  const dim3 qg((unsigned)quad_grid(p));
+  const TP* tp = reinterpret_cast<const TP*>(tile_ptr);
+  const GI* gi = reinterpret_cast<const GI*>(gids);
+  if (quad_tiles(p)) {
+    if (p.mask_clamp && dense)
+      hipLaunchKernelGGL((k_bwd16<TP, GI, true, true>), qg, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw,
+                         ev, tp, gi, num_pairs, ws, L);
+    else if (p.mask_clamp)
+      hipLaunchKernelGGL((k_bwd16<TP, GI, false, true>), qg, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw,
+                         ev, tp, gi, num_pairs, ws, L);
+    else if (dense)
+      hipLaunchKernelGGL((k_bwd16<TP, GI, true, false>), qg, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw,
+                         ev, tp, gi, num_pairs, ws, L);
+    else
+      hipLaunchKernelGGL((k_bwd16<TP, GI, false, false>), qg, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu,
+                         raw, ev, tp, gi, num_pairs, ws, L);
+  } else
     hipLaunchKernelGGL((k_bwd_any<TP, GI>), grid, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw, ev,
                        reinterpret_cast<const TP*>(tile_ptr), reinterpret_cast<const GI*>(gids),
                        num_pairs, ws, L);
@@ -2513,6 +2540,7 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
   h = batch_header(n_layers, tile_blocks, emit_blocks, finish_blocks);
   const size_t need = (size_t)h.total;
   info->n_layers = n_layers;
+  info->mask_clamp = (cfg->has_clamp_quad && cfg->clamp_quad < 80.0) ? 1 : 0;
   info->backward_buffers = backward_buffers ? 1 : 0;
   info->has_backward = backward_buffers && grads_set ? 1 : 0;
   info->tile_blocks = tile_blocks;
@@ -2612,7 +2640,10 @@ int gf_batch_backward(const void* plan, const gf_batch_info* info, uint32_t phas
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const uint8_t* pl = reinterpret_cast<const uint8_t*>(plan);
   if (phases & GF_PHASE_REDUCE) {
-    hipLaunchKernelGGL(k_bwd16_batch, dim3((unsigned)info->tile_blocks), dim3(kTileThreads), 0, st, pl);
+    if (info->mask_clamp)
+      hipLaunchKernelGGL(k_bwd16_batch<true>, dim3((unsigned)info->tile_blocks), dim3(kTileThreads), 0, st, pl);
+    else
+      hipLaunchKernelGGL(k_bwd16_batch<false>, dim3((unsigned)info->tile_blocks), dim3(kTileThreads), 0, st, pl);
     GF_LAUNCH_CHECK("k_bwd16_batch");
   }
   if ((phases & GF_PHASE_FINISH) && info->finish_blocks > 0) {

@@ -203,7 +203,8 @@ typedef struct gf_batch_info {
   int64_t tile_blocks, emit_blocks, finish_blocks;
   size_t plan_bytes;             /* device bytes of the plan buffer */
   int32_t backward_buffers;      /* every layer has its backward workspace and gradient outputs */
-  int32_t reserved;
+  int32_t mask_clamp;            /* clamp_quad < 80: the backward drops clamped pixels from the
+                                    quadratic-form moments (at 80 and above they are below e^-40) */
 } gf_batch_info;
 
 /*

@@ -242,6 +242,31 @@ def test_random_fields(device, case):
     check(p, device, tile_out=to, tile_in=ti, sigma=sigma, clamp=clamp, normalize=normalize)
 
 
+@pytest.mark.parametrize("tile", [16, 32])
+def test_low_clamp_backward(device, tile):
+    """clamp_quad below 80: pixels with q > clamp carry no quadratic-form gradient (the
+    reference's clamp mask, backward.cu:316-320,336-338), for the single-field backward (sparse
+    and dense tiles) and the batched one, against the oracle."""
+    from guass_amd.ops import FieldBatchPlan
+
+    sparse = wl.make_problem("clamp_sparse", 320, 320, 200, math.log(5.0), 0.6, 31)
+    dense = tiny_problem(128, 128, 800, 32, log_scale_px=2.5)
+    for p in (sparse, dense):
+        check(p, device, tile_out=tile, tile_in=tile, clamp=22.0)
+    refs = [oracle(p, tile_out=tile, tile_in=tile, clamp=22.0) for p in (sparse, dense)]
+    batch = FieldBatchPlan([p.to(device) for p in (sparse, dense)], device,
+                           capacities=[int(r[1][-1]) for r in refs], tile_out=tile, tile_in=tile, clamp_quad=22.0)
+    assert batch.info.mask_clamp == 1
+    batch.forward()
+    batch.backward()
+    torch.cuda.synchronize()
+    assert batch.status() == [0, 0]
+    for i, (pl, r) in enumerate(zip(batch.plans, refs)):
+        field_close(pl.delta, r[0])
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), r[3:]):
+            grad_close(a, b, f"batch layer {i} {name}")
+
+
 def test_k1_corner_and_huge(device):
     # one Gaussian at the top-left corner, one covering the whole matrix
     p = tiny_problem(70, 90, 2, 7)
