@@ -223,7 +223,8 @@ __device__ inline int4 bin_rect(const Problem& p, float mu0, float mu1, GfCov c,
 // R = L'^-1 in double (R^T R = cov^-1), scaled by sqrt(log2(e)/2) and rounded once.
 __device__ inline GaussEval eval_from_cov(const Problem& p, float mu0, float mu1, GfCov c, float amp) {
   const double a = (double)c.s00, b = (double)c.s01, d = (double)c.s11;
-  double det = a * d - b * b;  // exact products, one rounding
+  const double det_signed = a * d - b * b;  // exact products, one rounding
+  double det = det_signed;
   GaussEval v;
   v.mu0 = mu0;
   v.mu1 = mu1;
@@ -241,7 +242,9 @@ __device__ inline GaussEval eval_from_cov(const Problem& p, float mu0, float mu1
   float norm = 1.0f;
   if (p.normalize) {
 #pragma clang fp contract(off)
-    const float sq = gf_sqrt_rn((float)det);
+    // 1 / (2 pi max(sqrt(det), eps)) on the signed det: an indefinite covariance gives NaN, as
+    // torch.clamp keeps the NaN of sqrt(det < 0) in the reference (gaussian_core.py:55-82)
+    const float sq = gf_sqrt_rn((float)det_signed);
     norm = gf_div_f32(1.0f, GF_TWO_PI_F32 * (sq < GF_FLT_EPS ? GF_FLT_EPS : sq));
   }
   v.w = amp * norm;
