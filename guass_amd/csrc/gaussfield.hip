@@ -173,8 +173,9 @@ FwdLayout fwd_layout(const Problem& p) {
   return L;
 }
 
-// Backward workspace: header + S stripes of eight fp32 accumulators per Gaussian
-// (acc[g][s][8]: the tiles of a Gaussian spread their atomics over S addresses per moment).
+// Backward workspace: header + S stripes of eight fp32 accumulators per Gaussian, stripe-major
+// (acc[s][g][8], see acc_slot): the tiles of a Gaussian spread their atomics over S addresses
+// per moment, on S different cache lines.
 // It must be zero before the first backward; every backward leaves it zero again
 // (k_bwd_finish clears what it reads), so a workspace kept across calls is zeroed once.
 struct BwdLayout {
@@ -190,6 +191,12 @@ BwdLayout bwd_layout(const Problem& p) {
 }
 
 __device__ inline void set_status(uint32_t* status, uint32_t bit) { atomicOr(status, bit); }
+
+// Accumulator slot (eight floats) of stripe st of Gaussian g.  Stripe-major: atomics on one
+// cache line serialise where they are performed, so a Gaussian that touches thousands of
+// tiles must not keep its S stripes on one or two lines (Gaussian-major, 128-byte lines hold
+// four 32-byte slots).
+__device__ inline int64_t acc_slot(const Problem& p, int64_t g, int64_t st) { return st * p.K + g; }
 
 __device__ inline int32_t clamp_i32(int32_t v, int32_t lo, int32_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
@@ -1606,8 +1613,7 @@ __device__ __forceinline__ void bwd16_body(
   if (t >= T) return;
   const int32_t r0 = st.r0, c0 = st.c0;
   const int64_t stripe = st.sidx & (p.S - 1);
-  float* const acc_s = acc + 8 * stripe;       // this tile's stripe of Gaussian 0's accumulators
-  const uint64_t stride8 = 8u * (uint32_t)p.S;  // floats from one Gaussian's stripes to the next's
+  float* const acc_s = acc + 8 * acc_slot(p, 0, stripe);  // Gaussian 0's slot in this tile's stripe
   const bool hb3 = (lane & 8) != 0, hb2 = (lane & 4) != 0, hb1 = (lane & 2) != 0;
   const bool atomic_lane = (lane & 1) == 0 && (lane & 15) < 12;
   const int slot = lane >> 4, row = lane & 15;
@@ -1709,7 +1715,7 @@ __device__ __forceinline__ void bwd16_body(
         if (g >= 0 && row >= 10) {
           const int k = row - 10;
           const float val = k == 0 ? v0 : k == 1 ? v1 : k == 2 ? v2 : k == 3 ? v3 : k == 4 ? v4 : s5;
-          unsafeAtomicAdd(acc_s + ((uint64_t)(uint32_t)g * stride8 + (uint32_t)k), val);
+          unsafeAtomicAdd(acc_s + (8u * (uint64_t)(uint32_t)g + (uint32_t)k), val);
         }
         continue;
       }
@@ -1726,7 +1732,7 @@ __device__ __forceinline__ void bwd16_body(
       const float c1 = (hb2 ? a3 : a1) + dpp_f32<0x141>(hb2 ? a1 : a3);
       float d = (hb1 ? c1 : c0) + dpp_f32<0x4e>(hb1 ? c0 : c1);
       d += dpp_f32<0xb1>(d);
-      if (g >= 0 && atomic_lane) unsafeAtomicAdd(acc_s + ((uint64_t)(uint32_t)g * stride8 + (uint32_t)(row >> 1)), d);
+      if (g >= 0 && atomic_lane) unsafeAtomicAdd(acc_s + (8u * (uint64_t)(uint32_t)g + (uint32_t)(row >> 1)), d);
     }
     tile_general = tile_general || chunk_general;
   }
@@ -1782,7 +1788,7 @@ __device__ __forceinline__ void bwd16_body(
         if (lane == 15 && gj >= 0) {
 #pragma unroll
           for (int k = 0; k < 6; ++k)
-            unsafeAtomicAdd(acc + 8 * ((int64_t)gj * p.S + stripe) + k, mm[k]);
+            unsafeAtomicAdd(acc + 8 * acc_slot(p, gj, stripe) + k, mm[k]);
         }
       }
     }
@@ -1867,7 +1873,7 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
         float tot = 0.f;
 #pragma unroll
         for (int q = 0; q < kTileThreads / 64; ++q) tot += red[q][threadIdx.x];
-        unsafeAtomicAdd(acc + 8 * ((int64_t)g * p.S + (t & (p.S - 1))) + threadIdx.x, tot);
+        unsafeAtomicAdd(acc + 8 * acc_slot(p, g, t & (p.S - 1)) + threadIdx.x, tot);
       }
       __syncthreads();
     }
@@ -1893,7 +1899,7 @@ __device__ __forceinline__ void finish_body(
   const int32_t st = (int32_t)(idx & (p.S - 1));
   float m[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (g < p.K) {
-    float4* ag = reinterpret_cast<float4*>(acc) + 2 * (g * p.S + st);
+    float4* ag = reinterpret_cast<float4*>(acc) + 2 * acc_slot(p, g, st);
     const float4 b0 = ag[0], b1 = ag[1];
     ag[0] = make_float4(0.f, 0.f, 0.f, 0.f);
     ag[1] = make_float4(0.f, 0.f, 0.f, 0.f);

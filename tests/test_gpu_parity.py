@@ -856,15 +856,20 @@ def test_gaussian_field_batch_densification(device, tile):
     assert fb.replans >= len(events)
 
 
-def test_field_plan_resize_within_capacity(device):
+@pytest.mark.parametrize("shape", [(320, 768), (1280, 1792)], ids=["320x768", "1280x1792_stripes4"])
+def test_field_plan_resize_within_capacity(device, shape):
     """A single-field FieldPlan moved between K values (densification: clone and prune,
     reference controllers/clone.py:31-56, prune.py:34-45) within its k_capacity: forward and
     backward against the oracle at every K, with no buffer reallocated; past the capacity its
-    buffers grow."""
-    plan = FieldPlan(320, 768, 64, device, ids_capacity=1 << 18, k_capacity=512)
+    buffers grow.  The 1280x1792 field (8960 tiles) has four accumulator stripes, laid out
+    stripe-major by the current K, so the backward after each K change reads slots the previous
+    K's layout left zeroed."""
+    M, N = shape
+    plan = FieldPlan(M, N, 64, device, ids_capacity=1 << 18, k_capacity=512)
     bufs = (plan.fwd_ws.data_ptr(), plan.bwd_ws.data_ptr(), plan.ids.data_ptr(), plan._d_mu.data_ptr())
-    for k, seed in ((64, 1), (300, 2), (512, 3), (100, 4), (700, 5)):
-        p = wl.make_problem(f"resize_k{k}", 320, 768, k, math.log(6.0), 0.7, seed)
+    ks = ((64, 1), (300, 2), (512, 3), (100, 4), (700, 5)) if M == 320 else ((200, 1), (512, 3), (100, 4))
+    for k, seed in ks:
+        p = wl.make_problem(f"resize_{M}x{N}_k{k}", M, N, k, math.log(6.0), 0.7, seed)
         grew = plan.resize(k)
         say(f"FieldPlan.resize to K={k}: grew={grew}")
         assert grew == (k > 512), f"K={k}: reallocation {grew}"
