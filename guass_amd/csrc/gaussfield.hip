@@ -69,7 +69,8 @@ __host__ __device__ inline bool bin_counts_in_lds(int64_t C, int64_t K) {
 constexpr int kSortLdsKeys = 2048;    // (any-shape kernels) segments up to this length in LDS
 constexpr int kBitmapMaxK = 131072;   // (any-shape kernels) longer segments: K-bit bitmap
 constexpr int kSortLdsWords = (kSortLdsKeys > kBitmapMaxK / 32) ? kSortLdsKeys : kBitmapMaxK / 32;
-constexpr int kWaveSortKeys = 512;    // (16x16 kernels) per-wave LDS keys / bitmap words
+constexpr int kWaveSortKeys = 512;
+constexpr int kHeavyChunk = 16;       // Gaussians per chunk of a heavy tile's four waves    // (16x16 kernels) per-wave LDS keys / bitmap words
 // exp(-q/2) = 2^(q * kHalfLog2e); the clamp q in [0, clamp] maps to [clamp * kHalfLog2e, 0].
 constexpr float kHalfLog2e = -0.72134752044448170368f;
 constexpr double kSqrtHalfLog2e = 0.84932180028801904272;  // sqrt(-kHalfLog2e)
@@ -114,6 +115,8 @@ struct Problem {
                     // receives dL/d(mu_raw) (GaussianLinear.materialize_mu)
   int32_t mask_clamp;  // clamp_quad < 80: the backward drops clamped pixels from the quadratic-
                        // form moments (at 80 and above their terms are below e^-40)
+  int32_t heavy;  // > 0 (single fields on the k_bin_tiles path): tiles of more than `heavy`
+                  // Gaussians are listed by k_bin_tiles and rendered / reduced by four waves
 };
 
 // A Gaussian's mean coordinate i (0: row, 1: column) as the field uses it.
@@ -137,7 +140,7 @@ struct __align__(16) GaussEval {
 
 struct WsHeader {
   uint32_t status;
-  uint32_t pad0;
+  uint32_t heavy;      // forward, heavy-tile mode: tiles in the heavy-tile list
   int64_t* num_pairs;  // forward, tiles binned in the render: where the render stores P
   uint32_t pad[60];
 };
@@ -163,7 +166,7 @@ FwdLayout fwd_layout(const Problem& p) {
   o = align256(o + sizeof(int4) * (size_t)K);
   L.cov = o;
   o = align256(o + sizeof(float4) * (size_t)K);
-  L.fill = o;
+  L.fill = o;  // emission path: per-tile fill counts; mask path: the heavy-tile list
   o = align256(o + sizeof(int32_t) * (size_t)T);
   L.rowmask = o;
   o = align256(o + sizeof(uint32_t) * (size_t)p.R * (size_t)p.W);
@@ -830,6 +833,7 @@ __global__ __launch_bounds__(kTilesThreads) void k_prep(Problem p, const float* 
   if (g == 0) {
     WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
     hdr->status = 0u;
+    hdr->heavy = 0u;
     hdr->num_pairs = num_pairs;
   }
   if (g < p.K) store_prep(p, prep_rect(p, prep_load(mu, chol_raw, g)), amp[g], g, ws, L);
@@ -912,10 +916,13 @@ __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t*
     total += wsum[3][w];
   }
   int64_t* tp = tile_ptr + (int64_t)line * C;
+  int32_t* heavy_list = reinterpret_cast<int32_t*>(ws + L.fill);
   for (int32_t c = cb; c < ce; ++c) {
     tp[c] = rowbase + (int64_t)c * D - E;
-    D += diff[c];
+    D += diff[c];  // the count of tile (line, c)
     E += (int64_t)c * diff[c];
+    if (p.heavy > 0 && D > p.heavy)
+      heavy_list[atomicAdd(&reinterpret_cast<WsHeader*>(ws)->heavy, 1u)] = line * C + c;
   }
   if (line == R - 1 && threadIdx.x == 0) {
     const int64_t P = rowbase + (int64_t)C * Dt - Et;
@@ -1256,6 +1263,56 @@ struct SubTile {
   int64_t sidx;
 };
 
+// 16x16 tile t as a whole (heavy-tile workgroups).
+__device__ inline SubTile tile16(const Problem& p, int64_t t) {
+  SubTile st;
+  st.t = t;
+  st.quad = 0;
+  const int64_t tr = t / p.C, tc = t - (t / p.C) * p.C;
+  st.r0 = (int32_t)tr * 16;
+  st.c0 = (int32_t)tc * 16;
+  st.sidx = t;
+  return st;
+}
+
+__device__ inline SubTile sub_tile(const Problem& p, int64_t idx, int wave);
+
+// The work of workgroup blockIdx.x in a 16x16-block tile kernel with heavy-tile workgroups:
+// the first nh = (tiles k_bin_tiles listed) workgroups take one listed tile each, four waves
+// sharing it (q = wave, F = 4); the rest take four tiles each in tile order, one per wave, and
+// skip listed tiles.  The grid has xh workgroups beyond the one-per-four-tiles ones; xh bounds
+// nh (nh > xh only when the pairs exceed the id capacity: status CAPACITY), and the workgroups
+// past the tiles, at the end of the grid, return.
+struct HeavyItem {
+  SubTile st;
+  int q, F;
+};
+__device__ inline HeavyItem heavy_item(const Problem& p, const int32_t* __restrict__ heavy_list,
+                                       const uint32_t* heavy_count, int32_t xh, uint32_t* status) {
+  HeavyItem it;
+  it.q = 0;
+  it.F = 1;
+  const int64_t b = blockIdx.x;
+  int64_t nh = 0;
+  if (xh > 0) {
+    const int64_t T = (int64_t)p.R * p.C;
+    nh = (int64_t)*heavy_count;
+    if (nh > xh) {
+      if (b == 0 && threadIdx.x == 0) atomicOr(status, GF_STATUS_CAPACITY);
+      nh = xh;
+    }
+    if (b < nh) {
+      const int64_t t = heavy_list[b];
+      it.st = tile16(p, t < 0 || t >= T ? T : t);  // t == T: nothing to do
+      it.q = wave_id();
+      it.F = kTileThreads / 64;
+      return it;
+    }
+  }
+  it.st = sub_tile(p, b - nh, wave_id());
+  return it;
+}
+
 __device__ inline SubTile sub_tile(const Problem& p, int64_t idx, int wave) {
   SubTile st;
   const bool q32 = p.tile_out == 32;
@@ -1268,20 +1325,29 @@ __device__ inline SubTile sub_tile(const Problem& p, int64_t idx, int wave) {
   return st;
 }
 
+// LDS of the 16x16 render, at namespace scope so that both instantiations of render16_body in
+// one kernel share one allocation: per wave, sort / expansion keys and a chunk's constants.
+__shared__ int32_t r16_wkeys[kTileThreads / 64][kWaveSortKeys];
+__shared__ float4 r16_wevals[kTileThreads / 64][128];
+
 __device__ __forceinline__ void render16_body(
     const Problem& p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids,
     int64_t capacity, float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
     const uint32_t* __restrict__ colmask, const SubTile& st, const int4* __restrict__ rects = nullptr,
-    int64_t* __restrict__ tile_ptr_out = nullptr) {
-  __shared__ int32_t wkeys[kTileThreads / 64][kWaveSortKeys];
+    int64_t* __restrict__ tile_ptr_out = nullptr, int q = 0, int F = 1) {
+  // F > 1 (heavy tiles, mask path only): the F = 4 waves of the workgroup share tile st, wave q
+  // taking chunks q, q + F, ... of kHeavyChunk Gaussians; wave 0 adds the others' partial sums
+  // in wave order and writes the tile.  Every wave must call it (two workgroup barriers).
+  const int cs = F > 1 ? kHeavyChunk : 64;
+  auto& wkeys = r16_wkeys;
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
   const int64_t t = st.t;
   if (t >= (int64_t)p.R * p.C) return;
   const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (t / p.C) * p.C);
-  const bool write_ids = st.quad == 0;  // one wave of a 32x32 tile writes its ids
+  const bool write_ids = st.quad == 0 && q == 0;  // one wave of a tile writes its ids
   const int32_t pr = st.r0 + (lane >> 2), pc = st.c0 + ((lane & 3) << 2);
   // coordinates first: they do not depend on the tile's segment
   const float x = row_coords[min(pr, p.M - 1)];
@@ -1315,7 +1381,7 @@ __device__ __forceinline__ void render16_body(
   // read back in order with broadcast loads (two ds_read_b128 per Gaussian instead of a
   // v_readlane per constant); one ballot per chunk picks the loop that handles general-form
   // Gaussians.
-  __shared__ float4 wevals[kTileThreads / 64][128];
+  auto& wevals = r16_wevals;
   float4* ew = wevals[wid];
   auto run_chunk = [&](const GaussEval& my, int nj) {
     ew[2 * lane] = make_float4(my.mu0, my.mu1, my.wa, my.wb);
@@ -1385,6 +1451,7 @@ __device__ __forceinline__ void render16_body(
     } else {
       s = tile_ptr[t];
       count = tile_ptr[t + 1] - s;
+      if (F == 1 && p.heavy > 0 && count > p.heavy) return;  // a heavy-tile workgroup's
     }
     const int64_t room = capacity - s < count ? (capacity - s > 0 ? capacity - s : 0) : count;
     const uint32_t* rm = rowmask + (int64_t)tr * p.W;
@@ -1415,8 +1482,8 @@ __device__ __forceinline__ void render16_body(
             if (slot < room) ids[s + slot] = keys[j];
           }
         }
-        for (int32_t j0 = 0; j0 < nwin; j0 += 64) {
-          const int nj = min(64, nwin - j0);
+        for (int32_t j0 = q * cs; j0 < nwin; j0 += F * cs) {
+          const int nj = min(cs, nwin - j0);
           GaussEval my = zero_eval();
           if (lane < nj) my = load_eval(ev, keys[j0 + lane]);
           run_chunk(my, nj);
@@ -1477,6 +1544,21 @@ __device__ __forceinline__ void render16_body(
       run_chunk(my, nj);
     }
   }
+  if (F > 1) {
+    if (wid != 0) ew[lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    __syncthreads();
+    if (wid == 0) {
+      for (int w = 1; w < F; ++w) {
+        const float4 v = wevals[w][lane];
+        acc[0] += v.x;
+        acc[1] += v.y;
+        acc[2] += v.z;
+        acc[3] += v.w;
+      }
+    }
+    __syncthreads();  // the partial sums are read before the slots are reused
+    if (wid != 0) return;
+  }
   if (pr < p.M) {
     float* out = delta + (int64_t)pr * p.N + pc;
     if (pc + 3 < p.N && ((reinterpret_cast<uintptr_t>(out) & 15) == 0)) {
@@ -1489,13 +1571,24 @@ __device__ __forceinline__ void render16_body(
   }
 }
 
+template <bool kHeavy>
 __global__ __launch_bounds__(kTileThreads) void k_render16(
     Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids,
     int64_t capacity, float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
-    const uint32_t* __restrict__ colmask, const int4* __restrict__ rects, int64_t* __restrict__ tile_ptr_out) {
-  render16_body(p, row_coords, col_coords, ev, tile_ptr, ids, capacity, delta, ws, rowmask, colmask,
-                sub_tile(p, blockIdx.x, wave_id()), rects, tile_ptr_out);
+    const uint32_t* __restrict__ colmask, const int4* __restrict__ rects, int64_t* __restrict__ tile_ptr_out,
+    const int32_t* __restrict__ heavy_list, int32_t xh) {
+  HeavyItem it;
+  if constexpr (kHeavy) {
+    it = heavy_item(p, heavy_list, &reinterpret_cast<const WsHeader*>(ws)->heavy, xh,
+                    &reinterpret_cast<WsHeader*>(ws)->status);
+  } else {
+    it.st = sub_tile(p, blockIdx.x, wave_id());
+    it.q = 0;
+    it.F = 1;
+  }
+  render16_body(p, row_coords, col_coords, ev, tile_ptr, ids, capacity, delta, ws, rowmask, colmask, it.st,
+                rects, tile_ptr_out, it.q, it.F);
 }
 
 // Any tile shape: each thread evaluates pixels p = tid, tid+256, ... of the tile.
@@ -1604,7 +1697,10 @@ __device__ __forceinline__ void bwd16_body(
     const float* __restrict__ col_coords, const float* __restrict__ mu,
     const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
     const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
-    uint8_t* ws, const BwdLayout& L, const SubTile& st) {
+    uint8_t* ws, const BwdLayout& L, const SubTile& st, int q = 0, int F = 1) {
+  // F > 1 (heavy tiles): the F = 4 waves of the workgroup share tile st, wave q taking chunks
+  // q, q + F, ... of kHeavyChunk Gaussians (and their indefinite-form pass).
+  const int cs = F > 1 ? kHeavyChunk : 64;
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   float* acc = reinterpret_cast<float*>(ws + L.acc);
   const int lane = threadIdx.x & 63;
@@ -1647,10 +1743,11 @@ __device__ __forceinline__ void bwd16_body(
   if (e > num_pairs) e = num_pairs;
   const int64_t n = e > s ? e - s : 0;
   if (n == 0) return;
+  if (F == 1 && p.heavy > 0 && n > p.heavy) return;  // a heavy-tile workgroup's
 
   bool tile_general = false;
-  for (int64_t j0 = 0; j0 < n; j0 += 64) {
-    const int nj = (int)((n - j0) < 64 ? (n - j0) : 64);
+  for (int64_t j0 = q * cs; j0 < n; j0 += F * cs) {
+    const int nj = (int)((n - j0) < cs ? (n - j0) : cs);
     GaussEval my = zero_eval();
     int32_t myg = -1;
     if (lane < nj) {
@@ -1741,8 +1838,8 @@ __device__ __forceinline__ void bwd16_body(
   // time from memory, and the clamped pixels (q < 0 or q > clamp) add nothing to the
   // quadratic-form moments.
   if (tile_general) {
-    for (int64_t j0 = 0; j0 < n; j0 += 64) {
-      const int nj = (int)((n - j0) < 64 ? (n - j0) : 64);
+    for (int64_t j0 = q * cs; j0 < n; j0 += F * cs) {
+      const int nj = (int)((n - j0) < cs ? (n - j0) : cs);
       GaussEval my = zero_eval();
       int32_t myg = -1;
       if (lane < nj) {
@@ -1797,15 +1894,24 @@ __device__ __forceinline__ void bwd16_body(
 
 // Seven waves per SIMD (72 VGPRs): the rarely taken indefinite-form pass would otherwise
 // raise the register count and cost the common path occupancy.
-template <typename TpIdx, typename GIdx, bool kTransposeSums, bool kMaskClamp>
+template <typename TpIdx, typename GIdx, bool kTransposeSums, bool kMaskClamp, bool kHeavy>
 __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_bwd16(
     Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
     const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
     const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
-    uint8_t* ws, BwdLayout L) {
+    uint8_t* ws, BwdLayout L, const int32_t* __restrict__ heavy_list,
+    const uint32_t* __restrict__ heavy_count, int32_t xh) {
+  HeavyItem it;
+  if constexpr (kHeavy) {
+    it = heavy_item(p, heavy_list, heavy_count, xh, &reinterpret_cast<WsHeader*>(ws)->status);
+  } else {
+    it.st = sub_tile(p, blockIdx.x, wave_id());
+    it.q = 0;
+    it.F = 1;
+  }
   bwd16_body<TpIdx, GIdx, kTransposeSums, kMaskClamp>(p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr,
-                                          gids, num_pairs, ws, L, sub_tile(p, blockIdx.x, wave_id()));
+                                                      gids, num_pairs, ws, L, it.st, it.q, it.F);
 }
 
 __device__ inline float wave_sum(float v) {
@@ -2034,6 +2140,7 @@ int make_problem(const gf_field_config* cfg, int64_t M, int64_t N, int64_t K, Pr
   p->S = backward_stripes(K, R * C);
   p->mu_tanh = 0;
   p->mask_clamp = (cfg->has_clamp_quad && cfg->clamp_quad < 80.0) ? 1 : 0;
+  p->heavy = 0;  // set per launch (heavy_threshold)
   // Mask path (no emission kernel): 16x16 or 32x32 tiles, 1 <= K <= kMaskMaxK, a tile grid
   // k_bin bins in LDS, and masks of a bounded total size.
   p->W = 0;
@@ -2062,6 +2169,35 @@ constexpr int64_t kTilesInRenderMaxTests = int64_t(1) << 23;
 bool tiles_in_render(const Problem& p) {
   return p.W > 0 && quad_render(p) && p.K <= kTilesInRenderMaxK &&
          (int64_t)p.R * p.C * p.K <= kTilesInRenderMaxTests;
+}
+
+// Heavy tiles.  One wave per tile leaves a tile of many Gaussians as the tail of the render
+// and the backward: at cfg5 (clustered, up to 166 Gaussians per tile) the 364 tiles of more
+// than 64 Gaussians, 12% of the pairs, cost the render 12 us of 42 and the backward 19 us of
+// 67.  Single 16x16 fields on the k_bin_tiles path therefore list those tiles while binning;
+// the render and backward give each listed tile a workgroup of four waves, dispatched before
+// the one-wave-per-tile workgroups, which skip them (heavy_item).  K <= 64 cannot make a
+// heavy tile.
+constexpr int32_t kHeavyTile = 64;
+int32_t heavy_threshold(const Problem& p) {
+  return p.W > 0 && p.tile_out == 16 && p.tile_in == 16 && !tiles_in_render(p) && p.K > kHeavyTile
+             ? kHeavyTile : 0;
+}
+// The kernels with heavy-tile workgroups (kHeavy) run about 1 us slower than the plain ones
+// at cfg3, which has no heavy tile: the four-wave path changes the code of the one-wave path.
+// They are launched for fields of many Gaussians (K >= 2048, where densification has
+// clustered them) or many pairs per tile (>= 8 on average); cfg5c, clustered at 2 pairs per
+// tile, has 271 heavy tiles.  Return: their extra workgroups (0: the plain kernels).  At most
+// min(T, pairs / 65) tiles hold more than 64 Gaussians, for pairs <= pair_bound (the id
+// capacity, or P); the workgroups not needed return at the end of the grid.
+constexpr int64_t kHeavyMinK = 2048;
+constexpr int64_t kHeavyMinPairsPerTile = 8;
+int32_t heavy_grid(const Problem& p, int64_t pair_bound) {
+  const int64_t T = (int64_t)p.R * p.C;
+  if (heavy_threshold(p) <= 0 || pair_bound <= 0) return 0;
+  if (p.K < kHeavyMinK && pair_bound < kHeavyMinPairsPerTile * T) return 0;
+  const int64_t n = pair_bound / (kHeavyTile + 1);
+  return (int32_t)(n < T ? n : T);
 }
 
 // Workgroups of the 16x16-block tile kernels: four 16x16 tiles or one 32x32 tile each.
@@ -2236,30 +2372,54 @@ __global__ __launch_bounds__(kTileThreads) void k_finish_batch(const uint8_t* __
               ((int64_t)blockIdx.x - b0) * kTileThreads + threadIdx.x, ly.mu);
 }
 
+template <typename TP, typename GI, bool kTS, bool kMC>
+void launch_bwd16(const Problem& p, int32_t xh, hipStream_t st, const float* grad, const float* rc,
+                  const float* cc, const float* mu, const float* raw, const GaussEval* ev, const TP* tp,
+                  const GI* gi, int64_t num_pairs, uint8_t* ws, const BwdLayout& L, const int32_t* heavy_list,
+                  const uint32_t* heavy_count) {
+  // heavy-tile kernels for the int64 saved state (FieldPlan, the autograd functions)
+  constexpr bool kCanHeavy = std::is_same<TP, int64_t>::value && std::is_same<GI, int64_t>::value;
+  if constexpr (kCanHeavy) {
+    if (xh > 0) {
+      Problem q = p;
+      q.heavy = kHeavyTile;
+      hipLaunchKernelGGL((k_bwd16<TP, GI, kTS, kMC, true>), dim3((unsigned)(xh + quad_grid(p))),
+                         dim3(kTileThreads), 0, st, q, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L,
+                         heavy_list, heavy_count, xh);
+      return;
+    }
+  }
+  Problem q = p;
+  q.heavy = 0;
+  hipLaunchKernelGGL((k_bwd16<TP, GI, kTS, kMC, false>), dim3((unsigned)quad_grid(p)), dim3(kTileThreads), 0, st,
+                     q, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L, heavy_list, heavy_count, 0);
+}
+
 template <typename TP, typename GI>
 void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, const float* rc,
                 const float* cc, const float* mu, const float* raw, const GaussEval* ev,
                 const void* tile_ptr, const void* gids, int64_t num_pairs, uint8_t* ws,
-                const BwdLayout& L) {
+                const BwdLayout& L, const int32_t* heavy_list, const uint32_t* heavy_count) {
   // Tiles of many Gaussians (a wave makes >= 4 rounds on average) take the transposing
   // moment reduction (fewer instructions); sparse ones the row sums (shorter chain).
   const bool dense = num_pairs >= 16 * (int64_t)p.R * p.C;
-  const dim3 qg((unsigned)quad_grid(p));
+  // heavy-tile workgroups only with the forward's tile list (the forward workspace)
+  const int32_t xh = heavy_list ? heavy_grid(p, num_pairs) : 0;
   const TP* tp = reinterpret_cast<const TP*>(tile_ptr);
   const GI* gi = reinterpret_cast<const GI*>(gids);
   if (quad_tiles(p)) {
     if (p.mask_clamp && dense)
-      hipLaunchKernelGGL((k_bwd16<TP, GI, true, true>), qg, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw,
-                         ev, tp, gi, num_pairs, ws, L);
+      launch_bwd16<TP, GI, true, true>(p, xh, st, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L, heavy_list,
+                                       heavy_count);
     else if (p.mask_clamp)
-      hipLaunchKernelGGL((k_bwd16<TP, GI, false, true>), qg, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw,
-                         ev, tp, gi, num_pairs, ws, L);
+      launch_bwd16<TP, GI, false, true>(p, xh, st, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L, heavy_list,
+                                        heavy_count);
     else if (dense)
-      hipLaunchKernelGGL((k_bwd16<TP, GI, true, false>), qg, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw,
-                         ev, tp, gi, num_pairs, ws, L);
+      launch_bwd16<TP, GI, true, false>(p, xh, st, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L, heavy_list,
+                                        heavy_count);
     else
-      hipLaunchKernelGGL((k_bwd16<TP, GI, false, false>), qg, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu,
-                         raw, ev, tp, gi, num_pairs, ws, L);
+      launch_bwd16<TP, GI, false, false>(p, xh, st, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L,
+                                         heavy_list, heavy_count);
   } else
     hipLaunchKernelGGL((k_bwd_any<TP, GI>), grid, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw, ev,
                        reinterpret_cast<const TP*>(tile_ptr), reinterpret_cast<const GI*>(gids),
@@ -2320,6 +2480,7 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
     hipLaunchKernelGGL(k_prep, dim3((unsigned)((k + kTilesThreads - 1) / kTilesThreads)), dim3(kTilesThreads), 0,
                        st, p, mu, chol_raw, amp, ws, L, num_pairs_dev);
     GF_LAUNCH_CHECK("k_prep");
+    p.heavy = heavy_threshold(p);
     if (!tiles_in_render(p))
       hipLaunchKernelGGL(k_bin_tiles, dim3(lines), dim3(kTilesThreads), 0, st, p, tile_ptr, num_pairs_dev, ws, L);
     else if (num_pairs_host)
@@ -2384,12 +2545,14 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
   const GaussEval* ev = reinterpret_cast<const GaussEval*>(ws + L.eval);
   if (quad_render(p)) {
     const bool binned_here = tiles_in_render(p);
-    hipLaunchKernelGGL(k_render16, dim3((unsigned)quad_grid(p)), dim3(kTileThreads), 0, st, p, row_coords,
-                       col_coords, ev, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws,
-                       reinterpret_cast<const uint32_t*>(ws + L.rowmask),
+    const int32_t xh = heavy_grid(p, ids_capacity);
+    p.heavy = xh > 0 ? kHeavyTile : 0;
+    hipLaunchKernelGGL(xh > 0 ? k_render16<true> : k_render16<false>, dim3((unsigned)(xh + quad_grid(p))),
+                       dim3(kTileThreads), 0, st, p, row_coords, col_coords, ev, tile_ptr, gaussian_ids_sorted,
+                       ids_capacity, delta, ws, reinterpret_cast<const uint32_t*>(ws + L.rowmask),
                        reinterpret_cast<const uint32_t*>(ws + L.colmask),
                        binned_here ? reinterpret_cast<const int4*>(ws + L.rect) : nullptr,
-                       binned_here ? tile_ptr : nullptr);
+                       binned_here ? tile_ptr : nullptr, reinterpret_cast<const int32_t*>(ws + L.fill), xh);
   }
   else
     hipLaunchKernelGGL(k_render_any, dim3((unsigned)T), dim3(kTileThreads), 0, st, p, row_coords,
@@ -2418,18 +2581,20 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
   if (k > 0 && (!mu || !chol_raw)) return set_err(GF_E_INVALID_ARGUMENT, "mu / chol_raw must not be NULL");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
-  const GaussEval* ev = forward_workspace
-      ? reinterpret_cast<const GaussEval*>(reinterpret_cast<const uint8_t*>(forward_workspace) + fwd_layout(p).eval)
-      : nullptr;
+  const uint8_t* fws = reinterpret_cast<const uint8_t*>(forward_workspace);
+  const GaussEval* ev = fws ? reinterpret_cast<const GaussEval*>(fws + fwd_layout(p).eval) : nullptr;
+  // The heavy-tile list comes with the forward workspace of the forward that binned these tiles.
+  const int32_t* heavy_list = fws ? reinterpret_cast<const int32_t*>(fws + fwd_layout(p).fill) : nullptr;
+  const uint32_t* heavy_count = fws ? &reinterpret_cast<const WsHeader*>(fws)->heavy : nullptr;
   const dim3 grid((unsigned)T);
   if (tile_ptr_is_int64 && ids_is_int64)
-    launch_bwd<int64_t, int64_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs, ws, L);
+    launch_bwd<int64_t, int64_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs, ws, L, heavy_list, heavy_count);
   else if (tile_ptr_is_int64)
-    launch_bwd<int64_t, int32_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs, ws, L);
+    launch_bwd<int64_t, int32_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs, ws, L, heavy_list, heavy_count);
   else if (ids_is_int64)
-    launch_bwd<int32_t, int64_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs, ws, L);
+    launch_bwd<int32_t, int64_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs, ws, L, heavy_list, heavy_count);
   else
-    launch_bwd<int32_t, int32_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs, ws, L);
+    launch_bwd<int32_t, int32_t>(p, grid, st, grad_delta, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs, ws, L, heavy_list, heavy_count);
   GF_LAUNCH_CHECK("k_bwd");
   return GF_OK;
 }

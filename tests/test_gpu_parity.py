@@ -889,6 +889,105 @@ def test_field_plan_resize_within_capacity(device, shape):
             grad_close(a, b, f"K={k} {name}")
 
 
+def run_plan(p: wl.FieldProblem, device, capacity: int, **cfg):
+    """The sync-free FieldPlan path: the forward workspace (and its heavy-tile list) reaches the
+    backward, as in GaussianFieldCudaTrainFunction."""
+    q = p.to(device)
+    plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=capacity, **cfg)
+    plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+    grads = plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+    torch.cuda.synchronize()
+    P = int(plan.tile_ptr[-1])
+    return plan, (plan.delta.clone(), plan.tile_ptr.clone(), plan.ids[:min(P, capacity)].clone(),
+                  *(t.clone() for t in grads))
+
+
+def _clustered_problem(name, M, N, K, seed, clusters, cluster_sigma_px, log_scale_px, n_bad=0):
+    p = wl.make_problem(name, M, N, K, log_scale_px, 0.3, seed, clusters=clusters,
+                        cluster_sigma_px=cluster_sigma_px)
+    if n_bad:
+        bad = _indefinite_problem(M, N, seed, n_normal=1, n_bad=n_bad)
+        # elongated indefinite Gaussians through the first cluster's heavy tiles
+        centre = p.mu[: K // clusters].mean(0)
+        p.mu = torch.cat([p.mu, centre + 0.02 * torch.randn(n_bad, 2, generator=torch.Generator().manual_seed(seed))])
+        p.chol_raw = torch.cat([p.chol_raw, bad.chol_raw[1:]])
+        p.amp = torch.cat([p.amp, bad.amp[1:]])
+    return p
+
+
+def _heavy_tiles(tile_ptr) -> int:
+    return int(((tile_ptr[1:] - tile_ptr[:-1]) > 64).sum())
+
+
+HEAVY_CASES = {
+    # dense (pairs >= 16 per tile: transposing sums), clusters of 2048 Gaussians
+    "dense": dict(M=192, N=256, K=2048, clusters=2, cluster_sigma_px=14.0, log_scale_px=math.log(4.0)),
+    # sparse (row sums), one tight cluster in a large field
+    "sparse": dict(M=640, N=640, K=2048, clusters=1, cluster_sigma_px=10.0, log_scale_px=math.log(2.0)),
+    # clamp below 80 (masked moments), normalisation, indefinite Gaussians inside heavy tiles
+    "clamp24": dict(M=192, N=256, K=2048, clusters=2, cluster_sigma_px=14.0, log_scale_px=math.log(4.0),
+                    cfg=dict(clamp_quad=24.0)),
+    "normalize": dict(M=256, N=192, K=2100, clusters=3, cluster_sigma_px=12.0, log_scale_px=math.log(3.0),
+                      cfg=dict(normalize=True)),
+    "indefinite": dict(M=256, N=192, K=2100, clusters=3, cluster_sigma_px=12.0, log_scale_px=math.log(3.0),
+                       n_bad=6),
+}
+
+
+@pytest.mark.parametrize("case", list(HEAVY_CASES))
+def test_heavy_tiles_plan(device, case):
+    """Tiles of more than 64 Gaussians (k_bin_tiles lists them; the render and backward give each
+    a workgroup of four waves) through the sync-free plan, against the oracle: binning bit-exact,
+    field and gradients at the parity bars."""
+    c = dict(HEAVY_CASES[case])
+    cfg = c.pop("cfg", {})
+    p = _clustered_problem(f"heavy_{case}", seed=40, **c)
+    kw = dict(normalize=cfg.get("normalize", False), clamp=cfg.get("clamp_quad", 80.0))
+    say(f"{p.name} M={p.out_features} N={p.in_features} K={p.k} {cfg}")
+    r = oracle(p, batched=True, **kw)
+    P = int(r[1][-1])
+    heavy = _heavy_tiles(r[1])
+    say(f"  pairs={P} tiles={r[1].numel() - 1} heavy tiles={heavy}")
+    assert heavy > 0
+    plan, g = run_plan(p, device, P, **cfg)
+    assert plan.status() == 0 and plan.status("backward") == 0
+    binning_equal(g[1], g[2], r[1], r[2])
+    field_close(g[0], r[0])
+    for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), g[3:], r[3:]):
+        grad_close(a, b, name)
+
+
+def test_heavy_tiles_cfg5c_plan_and_determinism(device):
+    """cfg5c (clustered: 271 heavy tiles, up to 151 Gaussians per tile) through the sync-free plan
+    against the oracle, and a second forward bit-identical to the first (the heavy tiles' partial
+    sums are added in wave order, whichever workgroup takes the tile)."""
+    p = wl.cfg5c(0)
+    r = oracle(p, batched=True)
+    P = int(r[1][-1])
+    assert _heavy_tiles(r[1]) > 200
+    plan, g = run_plan(p, device, P)
+    assert plan.status() == 0
+    binning_equal(g[1], g[2], r[1], r[2])
+    field_close(g[0], r[0])
+    for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), g[3:], r[3:]):
+        grad_close(a, b, name)
+    q = p.to(device)
+    plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+    torch.cuda.synchronize()
+    assert torch.equal(plan.delta, g[0]) and torch.equal(plan.ids[:P], g[2])
+
+
+def test_heavy_tiles_capacity_overflow(device):
+    """An id capacity below the pair count on a field with heavy tiles: GF_STATUS_CAPACITY, and
+    every kernel returns (the heavy-tile grid is sized from the capacity)."""
+    c = dict(HEAVY_CASES["dense"])
+    p = _clustered_problem("heavy_overflow", seed=41, **c)
+    r = oracle(p, batched=True)
+    P = int(r[1][-1])
+    plan, _ = run_plan(p, device, P // 3)
+    assert plan.status() & _native.GF_STATUS_CAPACITY
+
+
 @pytest.mark.parametrize("tile", [16, 32])
 def test_batch_plan_update_keeps_captured_graph_valid(device, tile):
     """A graph captured over gf_batch_forward + gf_batch_backward before every layer's K and
