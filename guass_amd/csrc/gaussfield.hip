@@ -2174,11 +2174,12 @@ bool tiles_in_render(const Problem& p) {
 // Heavy tiles.  One wave per tile leaves a tile of many Gaussians as the tail of the render
 // and the backward: at cfg5 (clustered, up to 166 Gaussians per tile) the 364 tiles of more
 // than 64 Gaussians, 12% of the pairs, cost the render 12 us of 42 and the backward 19 us of
-// 67.  Single 16x16 fields on the k_bin_tiles path therefore list those tiles while binning;
-// the render and backward give each listed tile a workgroup of four waves, dispatched before
-// the one-wave-per-tile workgroups, which skip them (heavy_item).  K <= 64 cannot make a
-// heavy tile.
-constexpr int32_t kHeavyTile = 64;
+// 67.  Single 16x16 fields on the k_bin_tiles path therefore list the tiles of more than
+// kHeavyTile Gaussians while binning; the render and backward give each listed tile a
+// workgroup of four waves, dispatched before the one-wave-per-tile workgroups, which skip them
+// (heavy_item).  Thresholds 24..64 measured at cfg5 / cfg5c: 32 is best for cfg5 (100 us; 64:
+// 107 us) and within 1.5 us of the best for cfg5c.  K <= kHeavyTile cannot make a heavy tile.
+constexpr int32_t kHeavyTile = 32;
 int32_t heavy_threshold(const Problem& p) {
   return p.W > 0 && p.tile_out == 16 && p.tile_in == 16 && !tiles_in_render(p) && p.K > kHeavyTile
              ? kHeavyTile : 0;
@@ -2188,7 +2189,7 @@ int32_t heavy_threshold(const Problem& p) {
 // They are launched for fields of many Gaussians (K >= 2048, where densification has
 // clustered them) or many pairs per tile (>= 8 on average); cfg5c, clustered at 2 pairs per
 // tile, has 271 heavy tiles.  Return: their extra workgroups (0: the plain kernels).  At most
-// min(T, pairs / 65) tiles hold more than 64 Gaussians, for pairs <= pair_bound (the id
+// min(T, pairs / (kHeavyTile + 1)) tiles are heavy, for pairs <= pair_bound (the id
 // capacity, or P); the workgroups not needed return at the end of the grid.
 constexpr int64_t kHeavyMinK = 2048;
 constexpr int64_t kHeavyMinPairsPerTile = 8;

@@ -916,7 +916,7 @@ def _clustered_problem(name, M, N, K, seed, clusters, cluster_sigma_px, log_scal
 
 
 def _heavy_tiles(tile_ptr) -> int:
-    return int(((tile_ptr[1:] - tile_ptr[:-1]) > 64).sum())
+    return int(((tile_ptr[1:] - tile_ptr[:-1]) > 32).sum())
 
 
 HEAVY_CASES = {
@@ -936,7 +936,7 @@ HEAVY_CASES = {
 
 @pytest.mark.parametrize("case", list(HEAVY_CASES))
 def test_heavy_tiles_plan(device, case):
-    """Tiles of more than 64 Gaussians (k_bin_tiles lists them; the render and backward give each
+    """Tiles of more than 32 Gaussians (k_bin_tiles lists them; the render and backward give each
     a workgroup of four waves) through the sync-free plan, against the oracle: binning bit-exact,
     field and gradients at the parity bars."""
     c = dict(HEAVY_CASES[case])
