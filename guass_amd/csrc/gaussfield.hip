@@ -1351,29 +1351,35 @@ __device__ __forceinline__ void render16_body(
   const int32_t pr = st.r0 + (lane >> 2), pc = st.c0 + ((lane & 3) << 2);
   // coordinates first: they do not depend on the tile's segment
   const float x = row_coords[min(pr, p.M - 1)];
-  float y[4];
+  // The lane's four columns as y0 and offsets from it: z of column i is z0 + wc (y_i - y0), one
+  // FMA, with y_i - y0 exact for neighbouring coordinates.
+  float y0, yd[4];
+  {
+    float y[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) y[i] = col_coords[min(pc + i, p.N - 1)];
+    for (int i = 0; i < 4; ++i) y[i] = col_coords[min(pc + i, p.N - 1)];
+    y0 = y[0];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) yd[i] = y[i] - y0;
+  }
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   auto accumulate = [&](const GaussEval& u, auto general) {
     const float dx = x - u.mu0;
+    const float a = u.wa * dx;
+    const float z0 = fmaf(u.wc, y0 - u.mu1, u.wb * dx);
     if (general && u.gen != 0.0f) {  // indefinite form (uniform: u is broadcast)
-      const float a = u.wa * dx;
       const float nA = -(a * a);
-      const float b = u.wb * dx;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float z = fmaf(u.wc, y[i] - u.mu1, b);
+        const float z = i == 0 ? z0 : fmaf(u.wc, yd[i], z0);
         acc[i] = fmaf(u.w, basis_q(p, fmaf(z, z, nA)), acc[i]);
       }
       return;
     }
-    const float a = u.wa * dx;
     const float A = a * a;
-    const float b = u.wb * dx;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float z = fmaf(u.wc, y[i] - u.mu1, b);
+      const float z = i == 0 ? z0 : fmaf(u.wc, yd[i], z0);
       acc[i] = fmaf(u.w, basis_w(p, A, z), acc[i]);
     }
   };
