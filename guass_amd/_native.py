@@ -113,7 +113,7 @@ def lib() -> ctypes.CDLL:
                               _P, c_int32, c_int64, _P, _P, _P, _P, _P, c_size_t, _P]
     L.gf_backward_reduce.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int32,
                                      _P, c_int32, c_int64, _P, _P, c_size_t, _P]
-    L.gf_backward_finish.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_size_t, _P]
+    L.gf_backward_finish.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_size_t, _P]
     L.gf_read_status.argtypes = [_P, c_int32, POINTER(c_uint32), _P]
     L.gf_batch_plan.argtypes = [_CFG, POINTER(GfLayer), c_int32, _P, c_size_t, POINTER(GfBatchInfo), _P]
     L.gf_batch_forward.argtypes = [_P, POINTER(GfBatchInfo), c_uint32, _P]

@@ -154,7 +154,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // colmask[C][W] (mask path: bit g%32 of word g/32 is set when Gaussian g's tile rectangle covers
 // the tile row / column).
 struct FwdLayout {
-  size_t eval, rect, cov, fill, rowmask, colmask, total;
+  size_t eval, rect, cov, lfac, fill, rowmask, colmask, total;
 };
 FwdLayout fwd_layout(const Problem& p) {
   const int64_t K = p.K, T = (int64_t)p.R * p.C;
@@ -166,6 +166,8 @@ FwdLayout fwd_layout(const Problem& p) {
   o = align256(o + sizeof(int4) * (size_t)K);
   L.cov = o;
   o = align256(o + sizeof(float4) * (size_t)K);
+  L.lfac = o;  // (l11, l22) of each Gaussian's Cholesky factor, for the backward's finish
+  o = align256(o + sizeof(float2) * (size_t)K);
   L.fill = o;  // emission path: per-tile fill counts; mask path: the heavy-tile list
   o = align256(o + sizeof(int32_t) * (size_t)T);
   L.rowmask = o;
@@ -624,6 +626,7 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
     const int4 r = bin_rect(p, in.mu0, in.mu1, c, &touched);
     rect[g] = r;
     covs[g] = make_float4(c.s00, c.s01, c.s11, 0.0f);
+    reinterpret_cast<float2*>(ws + L.lfac)[g] = make_float2(Lc.l11, Lc.l22);
     my_pairs += touched;
     if (kEval) {
       GaussEval v = eval_from_cov(p, in.mu0, in.mu1, c, in.amp);
@@ -794,6 +797,7 @@ struct PrepOut {
   int4 rect;
   GfCov cov;
   float mu0, mu1;
+  float l11, l22;
 };
 
 struct PrepLoad {
@@ -809,7 +813,10 @@ __device__ inline PrepOut prep_rect(const Problem& p, const PrepLoad& in) {
   PrepOut o;
   o.mu0 = in.mu0;
   o.mu1 = in.mu1;
-  o.cov = gf_cov_from_chol(gf_activate_cholesky(in.r11, in.r21, in.r22));
+  const GfChol Lc = gf_activate_cholesky(in.r11, in.r21, in.r22);
+  o.cov = gf_cov_from_chol(Lc);
+  o.l11 = Lc.l11;
+  o.l22 = Lc.l22;
   int32_t touched;
   o.rect = bin_rect(p, o.mu0, o.mu1, o.cov, &touched);
   return o;
@@ -819,6 +826,7 @@ __device__ inline void store_prep(const Problem& p, const PrepOut& o, float amp,
                                   const FwdLayout& L) {
   reinterpret_cast<int4*>(ws + L.rect)[g] = o.rect;
   reinterpret_cast<float4*>(ws + L.cov)[g] = make_float4(o.cov.s00, o.cov.s01, o.cov.s11, 0.0f);
+  reinterpret_cast<float2*>(ws + L.lfac)[g] = make_float2(o.l11, o.l22);
   GaussEval v = eval_from_cov(p, o.mu0, o.mu1, o.cov, amp);
   v.gid = (int32_t)g;
   store_eval(reinterpret_cast<GaussEval*>(ws + L.eval), g, v);
@@ -1992,6 +2000,15 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
   }
 }
 
+// d softplus / dx as torch's softplus backward: x > 20 ? 1 : e^x / (e^x + 1).  In fp32 with the
+// hardware exp2, within 2e-6 relative of the exact value (the argument x log2(e) <= 28.9 is
+// rounded once); the finish's gradients are held to 1e-4.
+__device__ inline float softplus_grad_f32(float x) {
+  if (x > 20.0f) return 1.0f;
+  const float e = __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+  return e / (e + 1.0f);
+}
+
 // Chain rule from the six moments of Gaussian g to (d_mu, d_chol_raw, d_amp), in double:
 //   d_amp = norm S0;  d_mu = amp norm A (S1, S2);  dL/dA = -amp norm / 2 [[S3,S4],[S4,S5]];
 //   dL/ddet = amp S0 (-norm / (2 det)) if normalize and sqrt(det) >= eps (else 0);
@@ -2005,7 +2022,8 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
 __device__ __forceinline__ void finish_body(
     const Problem& p, const float* __restrict__ chol_raw, const float* __restrict__ amp,
     float* __restrict__ d_mu, float* __restrict__ d_chol_raw, float* __restrict__ d_amp, uint8_t* ws,
-    const BwdLayout& L, int64_t idx, const float* __restrict__ mu = nullptr) {
+    const BwdLayout& L, int64_t idx, const float* __restrict__ mu = nullptr,
+    const float4* __restrict__ fwd_cov = nullptr, const float2* __restrict__ fwd_lfac = nullptr) {
   float* acc = reinterpret_cast<float*>(ws + L.acc);
   const int64_t g = idx / p.S;
   const int32_t st = (int32_t)(idx & (p.S - 1));
@@ -2028,8 +2046,21 @@ __device__ __forceinline__ void finish_body(
   }
   if (g >= p.K || st != 0) return;
   const float raw11 = chol_raw[3 * g + 0], raw21 = chol_raw[3 * g + 1], raw22 = chol_raw[3 * g + 2];
-  const GfChol Lc = gf_activate_cholesky(raw11, raw21, raw22);
-  const GfCov cov = gf_cov_from_chol(Lc);
+  GfChol Lc;
+  GfCov cov;
+  if (fwd_cov) {  // the forward's factor and covariance (the same functions of chol_raw)
+    const float2 lf = fwd_lfac[g];
+    const float4 c4 = fwd_cov[g];
+    Lc.l11 = lf.x;
+    Lc.l21 = raw21;
+    Lc.l22 = lf.y;
+    cov.s00 = c4.x;
+    cov.s01 = c4.y;
+    cov.s11 = c4.z;
+  } else {
+    Lc = gf_activate_cholesky(raw11, raw21, raw22);
+    cov = gf_cov_from_chol(Lc);
+  }
   const GfRenderGeom rg = gf_render_geom(cov, p.normalize);
   const double S0 = m[0], S1 = m[1], S2 = m[2], S3 = m[3], S4 = m[4], S5 = m[5];
   const double a = (double)amp[g];
@@ -2066,17 +2097,17 @@ __device__ __forceinline__ void finish_body(
   const double dl11 = 2.0 * c00 * l11 + (c01 + c10) * l21;
   const double dl21 = (c10 + c01) * l11 + 2.0 * c11 * l21;
   const double dl22 = 2.0 * c11 * l22;
-  d_chol_raw[3 * g + 0] = (float)(dl11 * gf_softplus_grad(raw11));
+  d_chol_raw[3 * g + 0] = (float)(dl11 * softplus_grad_f32(raw11));
   d_chol_raw[3 * g + 1] = (float)dl21;
-  d_chol_raw[3 * g + 2] = (float)(dl22 * gf_softplus_grad(raw22));
+  d_chol_raw[3 * g + 2] = (float)(dl22 * softplus_grad_f32(raw22));
 }
 
 __global__ __launch_bounds__(kTileThreads) void k_bwd_finish(
     Problem p, const float* __restrict__ chol_raw, const float* __restrict__ amp,
     float* __restrict__ d_mu, float* __restrict__ d_chol_raw, float* __restrict__ d_amp, uint8_t* ws,
-    BwdLayout L) {
+    BwdLayout L, const float4* __restrict__ fwd_cov, const float2* __restrict__ fwd_lfac) {
   finish_body(p, chol_raw, amp, d_mu, d_chol_raw, d_amp, ws, L,
-              (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+              (int64_t)blockIdx.x * blockDim.x + threadIdx.x, nullptr, fwd_cov, fwd_lfac);
 }
 
 // Self-test: order-independent checksum of gf_softplus_torch_cpu over all 2^32 inputs.
@@ -2376,7 +2407,8 @@ __global__ __launch_bounds__(kTileThreads) void k_finish_batch(const uint8_t* __
   const Problem p = ly.p;
   const BwdLayout L = ly.bl;
   finish_body(p, ly.chol_raw, ly.amp, ly.d_mu, ly.d_chol_raw, ly.d_amp, ly.bws, L,
-              ((int64_t)blockIdx.x - b0) * kTileThreads + threadIdx.x, ly.mu);
+              ((int64_t)blockIdx.x - b0) * kTileThreads + threadIdx.x, ly.mu,
+              reinterpret_cast<const float4*>(ly.fws + ly.fl.cov), reinterpret_cast<const float2*>(ly.fws + ly.fl.lfac));
 }
 
 template <typename TP, typename GI, bool kTS, bool kMC>
@@ -2608,7 +2640,8 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
 
 int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                        const float* chol_raw, const float* amp, float* d_mu, float* d_chol_raw,
-                       float* d_amp, void* workspace, size_t workspace_bytes, void* stream) {
+                       float* d_amp, const void* forward_workspace, void* workspace, size_t workspace_bytes,
+                       void* stream) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
@@ -2620,8 +2653,12 @@ int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t
     return set_err(GF_E_INVALID_ARGUMENT, "parameter / gradient pointers must not be NULL");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const unsigned blocks = (unsigned)((k * p.S + kTileThreads - 1) / kTileThreads);
+  const uint8_t* fws = reinterpret_cast<const uint8_t*>(forward_workspace);
+  const FwdLayout FL = fwd_layout(p);
   hipLaunchKernelGGL(k_bwd_finish, dim3(blocks), dim3(kTileThreads), 0, st, p, chol_raw, amp, d_mu,
-                     d_chol_raw, d_amp, reinterpret_cast<uint8_t*>(workspace), L);
+                     d_chol_raw, d_amp, reinterpret_cast<uint8_t*>(workspace), L,
+                     fws ? reinterpret_cast<const float4*>(fws + FL.cov) : nullptr,
+                     fws ? reinterpret_cast<const float2*>(fws + FL.lfac) : nullptr);
   GF_LAUNCH_CHECK("k_bwd_finish");
   return GF_OK;
 }
@@ -2638,7 +2675,7 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
                               num_pairs, forward_workspace, workspace, workspace_bytes, stream);
   if (rc) return rc;
   return gf_backward_finish(cfg, out_features, in_features, k, chol_raw, amp, d_mu, d_chol_raw, d_amp,
-                            workspace, workspace_bytes, stream);
+                            forward_workspace, workspace, workspace_bytes, stream);
 }
 
 // ------------------------------------------------------------------------------------------

@@ -138,10 +138,13 @@ class FieldPlan:
                                            self.ids.data_ptr(), 1, n, fwd, self.bwd_ws.data_ptr(),
                                            self.bwd_ws_bytes, self._stream()), "gf_backward_reduce")
 
-    def backward_finish(self, chol_raw, amp):
+    def backward_finish(self, chol_raw, amp, reuse_forward: bool = True):
+        """Chain rule into ``d_mu``, ``d_chol_raw``, ``d_amp``.  With ``reuse_forward`` the
+        Cholesky factors and covariances come from the last forward's workspace."""
+        fwd = self.fwd_ws.data_ptr() if reuse_forward else None
         N.check(N.lib().gf_backward_finish(ctypes.byref(self.cfg), self.M, self.N, self.K,
                                            N.ptr(chol_raw), N.ptr(amp), N.ptr(self.d_mu),
-                                           N.ptr(self.d_chol_raw), N.ptr(self.d_amp),
+                                           N.ptr(self.d_chol_raw), N.ptr(self.d_amp), fwd,
                                            self.bwd_ws.data_ptr(), self.bwd_ws_bytes, self._stream()),
                 "gf_backward_finish")
         return self.d_mu, self.d_chol_raw, self.d_amp
@@ -150,7 +153,7 @@ class FieldPlan:
                  reuse_forward: bool = True):
         """Gradients into ``d_mu``, ``d_chol_raw``, ``d_amp`` from the last forward's binning."""
         self.backward_reduce(grad, row_coords, col_coords, mu, chol_raw, num_pairs, reuse_forward)
-        return self.backward_finish(chol_raw, amp)
+        return self.backward_finish(chol_raw, amp, reuse_forward)
 
     def pairs(self) -> int:
         """Pair count of the last forward (synchronises)."""

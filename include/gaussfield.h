@@ -128,8 +128,10 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
  *   gaussian_ids    [num_pairs], int64 if ids_is_int64 else int32 (any order within a tile)
  *   d_mu [K,2], d_chol_raw [K,3], d_amp [K,1] fp32 out (fully written)
  *   forward_workspace  optional: the workspace of the forward over the same (mu, chol_raw)
- *                   and config (after its gf_forward_emit); the Gaussians' constants stored
- *                   there are read instead of recomputed.  NULL recomputes them.
+ *                   and config (after its gf_forward_emit); the Gaussians' constants and
+ *                   Cholesky factors stored there are read instead of recomputed, and the
+ *                   forward's list of heavy tiles lets the reduction split them over
+ *                   workgroups.  NULL recomputes them.
  * Saved-state violations (non-monotone tile_ptr, tile_ptr[T] != num_pairs, ids outside
  * [0,K)) are detected on the device, the offending pairs skipped, and status bits set.
  * Replaces reference backward.cu:541-716 (backward_pair_reduce_train).
@@ -151,10 +153,12 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
                        const void* forward_workspace, void* workspace, size_t workspace_bytes,
                        void* stream);
 
-/* Second half of gf_backward (reference backward.cu:436-496,704-715: cov -> chol_raw chain). */
+/* Second half of gf_backward (reference backward.cu:436-496,704-715: cov -> chol_raw chain).
+ * forward_workspace as for gf_backward_reduce: optional; the forward's Cholesky factor and
+ * covariance are read instead of recomputed from chol_raw. */
 int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                        const float* chol_raw, const float* amp,
-                       float* d_mu, float* d_chol_raw, float* d_amp,
+                       float* d_mu, float* d_chol_raw, float* d_amp, const void* forward_workspace,
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /*
