@@ -863,28 +863,42 @@ __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t*
     for (int32_t i = threadIdx.x; i <= C; i += kTilesThreads) diff[i] = 0;
   __syncthreads();
   int64_t before = 0, pairs = 0;
-  for (int64_t g0 = threadIdx.x & ~63; g0 < K; g0 += kTilesThreads) {  // wave-uniform
-    const int64_t g = g0 + lane;
-    bool covers = false;
-    if (g < K) {
-      const int4 r = rect[g];
-      if (is_row) {
-        const int32_t h = r.y - r.x + 1, w = r.w - r.z + 1;
-        before += (int64_t)w * clamp_i32(line - r.x, 0, h);
-        pairs += (int64_t)w * h;
-        covers = r.x <= line && line <= r.y;
-        if (covers) {
-          atomicAdd(diff + r.z, 1);
-          atomicAdd(diff + r.w + 1, -1);  // r.w + 1 <= C
-        }
-      } else {
-        covers = r.z <= line && line <= r.w;
-      }
+  // The rectangles are loaded kBinPrefetch rounds at a time, so that the rounds do not each wait
+  // for their own load (4 rounds at cfg3).
+  constexpr int kBinPrefetch = 8;
+  for (int64_t gb = threadIdx.x & ~63; gb < K; gb += kBinPrefetch * kTilesThreads) {  // wave-uniform
+    int4 rr[kBinPrefetch];
+#pragma unroll
+    for (int i = 0; i < kBinPrefetch; ++i) {
+      const int64_t g = gb + (int64_t)i * kTilesThreads + lane;
+      rr[i] = g < K ? rect[g] : make_int4(0, -1, 0, -1);
     }
-    const uint64_t bits = __builtin_amdgcn_ballot_w64(covers);
-    const int64_t w0 = g0 >> 5;  // even: words w0, w0 + 1 hold Gaussians g0 .. g0 + 63
-    if (lane == 0) out[w0] = (uint32_t)bits;
-    if (lane == 1 && w0 + 1 < W) out[w0 + 1] = (uint32_t)(bits >> 32);
+#pragma unroll
+    for (int i = 0; i < kBinPrefetch; ++i) {
+      const int64_t g0 = gb + (int64_t)i * kTilesThreads;
+      if (g0 >= K) break;
+      const int64_t g = g0 + lane;
+      bool covers = false;
+      if (g < K) {
+        const int4 r = rr[i];
+        if (is_row) {
+          const int32_t h = r.y - r.x + 1, w = r.w - r.z + 1;
+          before += (int64_t)w * clamp_i32(line - r.x, 0, h);
+          pairs += (int64_t)w * h;
+          covers = r.x <= line && line <= r.y;
+          if (covers) {
+            atomicAdd(diff + r.z, 1);
+            atomicAdd(diff + r.w + 1, -1);  // r.w + 1 <= C
+          }
+        } else {
+          covers = r.z <= line && line <= r.w;
+        }
+      }
+      const uint64_t bits = __builtin_amdgcn_ballot_w64(covers);
+      const int64_t w0 = g0 >> 5;  // even: words w0, w0 + 1 hold Gaussians g0 .. g0 + 63
+      if (lane == 0) out[w0] = (uint32_t)bits;
+      if (lane == 1 && w0 + 1 < W) out[w0 + 1] = (uint32_t)(bits >> 32);
+    }
   }
   if (!is_row) return;
   __syncthreads();  // the row's differences are complete
