@@ -1448,21 +1448,33 @@ __device__ __forceinline__ void render16_body(
       __shared__ uint32_t wmask[kTileThreads / 64][kMaskMaxK / 32];
       uint32_t* mw = wmask[wid];
       int64_t before = 0, cnt = 0;
-      for (int64_t g0 = 0; g0 < p.K; g0 += 64) {
-        const int64_t g = g0 + lane;
-        bool covers = false;
-        if (g < p.K) {
-          const int4 r = rects[g];
-          const int32_t h = r.y - r.x + 1, wd = r.w - r.z + 1;
-          const bool in_row = r.x <= tr && tr <= r.y;
-          before += (int64_t)wd * clamp_i32(tr - r.x, 0, h) + (in_row ? clamp_i32(tc - r.z, 0, wd) : 0);
-          covers = in_row && r.z <= tc && tc <= r.w;
+      constexpr int kPre = 4;  // rounds of rectangle loads in flight (K <= 256: all of them)
+      for (int64_t gb = 0; gb < p.K; gb += kPre * 64) {
+        int4 rr[kPre];
+#pragma unroll
+        for (int i = 0; i < kPre; ++i) {
+          const int64_t g = gb + 64 * i + lane;
+          rr[i] = g < p.K ? rects[g] : make_int4(0, -1, 0, -1);
         }
-        const uint64_t bits = __builtin_amdgcn_ballot_w64(covers);
-        cnt += __popcll(bits);
-        const int32_t w0 = (int32_t)(g0 >> 5);
-        if (lane == 0) mw[w0] = (uint32_t)bits;
-        if (lane == 1 && w0 + 1 < p.W) mw[w0 + 1] = (uint32_t)(bits >> 32);
+#pragma unroll
+        for (int i = 0; i < kPre; ++i) {
+          const int64_t g0 = gb + 64 * i;
+          if (g0 >= p.K) break;
+          const int64_t g = g0 + lane;
+          bool covers = false;
+          if (g < p.K) {
+            const int4 r = rr[i];
+            const int32_t h = r.y - r.x + 1, wd = r.w - r.z + 1;
+            const bool in_row = r.x <= tr && tr <= r.y;
+            before += (int64_t)wd * clamp_i32(tr - r.x, 0, h) + (in_row ? clamp_i32(tc - r.z, 0, wd) : 0);
+            covers = in_row && r.z <= tc && tc <= r.w;
+          }
+          const uint64_t bits = __builtin_amdgcn_ballot_w64(covers);
+          cnt += __popcll(bits);
+          const int32_t w0 = (int32_t)(g0 >> 5);
+          if (lane == 0) mw[w0] = (uint32_t)bits;
+          if (lane == 1 && w0 + 1 < p.W) mw[w0 + 1] = (uint32_t)(bits >> 32);
+        }
       }
       s = readlane_i64(wave_inclusive_scan(before), 63);
       count = cnt;
