@@ -977,6 +977,31 @@ def test_heavy_tiles_cfg5c_plan_and_determinism(device):
     assert torch.equal(plan.delta, g[0]) and torch.equal(plan.ids[:P], g[2])
 
 
+@pytest.mark.parametrize("case", ["dense", "indefinite"])
+def test_heavy_tiles_autograd_train_function(device, case):
+    """Heavy tiles through the reference's autograd entry point (runtime.gaussian_field_train,
+    runtime.py:273-297): its backward receives the forward workspace kept on ctx, so the
+    reduction takes the heavy-tile kernels; gradients against the oracle."""
+    c = dict(HEAVY_CASES[case])
+    c.pop("cfg", None)
+    p = _clustered_problem(f"heavy_autograd_{case}", seed=42, **c)
+    q = p.to(device)
+    mu = q.mu.clone().requires_grad_(True)
+    raw = q.chol_raw.clone().requires_grad_(True)
+    amp = q.amp.clone().requires_grad_(True)
+    delta = runtime.gaussian_field_train(row_coords=q.row_coords, col_coords=q.col_coords, mu=mu,
+                                         chol_raw=raw, amp=amp, tile_out=16, tile_in=16,
+                                         sigma_multiplier=3.0, normalize=False, clamp_quad=80.0)
+    (delta * q.grad.view_as(delta)).sum().backward()
+    torch.cuda.synchronize()
+    r = oracle(p, batched=True)
+    assert _heavy_tiles(r[1]) > 0
+    field_close(delta, r[0])
+    grad_close(mu.grad, r[3], "mu.grad")
+    grad_close(raw.grad, r[4], "chol_raw.grad")
+    grad_close(amp.grad, r[5], "amp.grad")
+
+
 def test_heavy_tiles_capacity_overflow(device):
     """An id capacity below the pair count on a field with heavy tiles: GF_STATUS_CAPACITY, and
     every kernel returns (the heavy-tile grid is sized from the capacity)."""
