@@ -1002,6 +1002,31 @@ def test_heavy_tiles_autograd_train_function(device, case):
     grad_close(amp.grad, r[5], "amp.grad")
 
 
+def test_one_layer_batch_survives_k_changes(device):
+    """A single layer that must keep a captured graph across densification runs as a batch of
+    one: re-planned for K = 200, 480, 90 within k_capacity 512, its launch grids and plan size
+    stay the same and every K matches the oracle."""
+    from guass_amd.ops import FieldBatchPlan
+
+    p0 = wl.make_problem("one_layer_k200", 320, 768, 200, math.log(6.0), 0.7, 1)
+    batch = FieldBatchPlan([p0.to(device)], device, capacities=[1 << 16], k_capacities=[512])
+    first = (batch.info.tile_blocks, batch.info.emit_blocks, batch.info.finish_blocks, batch.info.plan_bytes)
+    for k, seed in ((200, 1), (480, 2), (90, 3)):
+        p = wl.make_problem(f"one_layer_k{k}", 320, 768, k, math.log(6.0), 0.7, seed)
+        assert batch.update([p.to(device)]), f"K={k}: re-planned with new grids"
+        batch.forward()
+        batch.backward()
+        torch.cuda.synchronize()
+        assert (batch.info.tile_blocks, batch.info.emit_blocks, batch.info.finish_blocks,
+                batch.info.plan_bytes) == first
+        r = oracle(p)
+        pl = batch.plans[0]
+        binning_equal(pl.tile_ptr, pl.ids[:int(r[1][-1])], r[1], r[2])
+        field_close(pl.delta, r[0])
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), r[3:]):
+            grad_close(a, b, f"K={k} {name}")
+
+
 def test_heavy_tiles_capacity_overflow(device):
     """An id capacity below the pair count on a field with heavy tiles: GF_STATUS_CAPACITY, and
     every kernel returns (the heavy-tile grid is sized from the capacity)."""
