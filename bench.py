@@ -60,7 +60,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--layers", type=int, default=None, help="cfg4: first N of the 128 layers")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of graph replay")
-    ap.add_argument("--graph-steps", type=int, default=10,
+    ap.add_argument("--graph-steps", type=int, default=100,
                     help="steps captured per HIP graph (replay overhead is paid once per graph)")
     ap.add_argument("--kernel-reps", type=int, default=20, help="launches per per-kernel timing graph")
     ap.add_argument("--kernel-replays", type=int, default=25, help="timed replays per kernel graph")
@@ -129,13 +129,26 @@ def traffic_bytes(path: str, config: str, kernel: str):
     return None if entry is None else float(entry["hbm_bytes_per_launch"])
 
 
+def cgroup_cpu_quota() -> float | None:
+    """CPUs the cgroup v2 quota allows (cpu.max "quota period"), or None when unlimited."""
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+    except (OSError, ValueError):
+        return None
+    return None if quota == "max" else float(quota) / float(period)
+
+
 def cpu_baseline(problems, reps: int, note: str, tile: int = 16) -> dict:
     import torch
 
     from oracle import field_oracle as fo  # CPU baseline leg only
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
-    torch.set_num_threads(cores)
+    affinity = len(os.sched_getaffinity(0))
+    quota = cgroup_cpu_quota()
+    # every core the process may run on; a cgroup CPU quota below that would only time-slice
+    # the extra threads, so it caps the count
+    threads = affinity if quota is None else max(1, min(affinity, int(quota)))
+    torch.set_num_threads(threads)
 
     def run():
         for p in problems:
@@ -151,7 +164,7 @@ def cpu_baseline(problems, reps: int, note: str, tile: int = 16) -> dict:
     med = statistics.median(times)
     elements = sum(p.out_features * p.in_features for p in problems)
     return {"value": elements / med, "unit": "ΔW elements/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "affinity_cores": affinity, "cgroup_cpu_quota": quota, "kind": "port",
             "sample": f"{note}: fwd+bwd (per-tile loop + autograd), 1 warmup + median of {reps}, "
                       f"{med:.2f} s each"}
 
@@ -379,6 +392,7 @@ def main() -> int:
             "k_bwd_finish": [lambda: batch.backward(Nat.GF_PHASE_FINISH)],
         }
         status = lambda: max(batch.status())  # noqa: E731
+        emits = batch.info.emit_blocks > 0
     else:
         q, P = qs[0], counts[0]["pairs"]
         plan = FieldPlan(probs[0].out_features, probs[0].in_features, probs[0].k, dev, ids_capacity=P,
@@ -396,6 +410,7 @@ def main() -> int:
             "k_bwd_finish": [lambda: plan.backward_finish(q.chol_raw, q.amp)],
         }
         status = plan.status
+        emits = probs[0].k > 8192 or args.tile not in (16, 32)  # the emission path (no masks)
 
     stream = torch.cuda.Stream(dev)
     stream.wait_stream(torch.cuda.current_stream(dev))
@@ -465,9 +480,12 @@ def main() -> int:
         torch.cuda.synchronize()
         return statistics.median(times)
 
+    if not emits:  # the mask path launches no emission kernel
+        phases.pop("k_emit+")
     ph = {name: graph_time_us(fns) for name, fns in phases.items()}
-    ph["k_emit"] = ph.pop("k_emit+") - ph["k_bin"]
-    ph = {k: ph[k] / 1e3 for k in ("k_bin", "k_emit", "k_render", "k_bwd", "k_bwd_finish")}  # ms
+    if emits:
+        ph["k_emit"] = ph.pop("k_emit+") - ph["k_bin"]
+    ph = {k: ph[k] / 1e3 for k in ("k_bin", "k_emit", "k_render", "k_bwd", "k_bwd_finish") if k in ph}  # ms
     step()  # leave the plan in the state of one clean step
     torch.cuda.synchronize()
 

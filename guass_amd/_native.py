@@ -27,7 +27,7 @@ GF_STATUS_IDS_RANGE = 0x20
 # Symbols include/gaussfield.h declares.
 EXPORTED = (
     "gf_version", "gf_last_error", "gf_tile_grid", "gf_forward_workspace_bytes",
-    "gf_backward_workspace_bytes", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
+    "gf_forward_workspace_bytes_max", "gf_backward_workspace_bytes", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
     "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
     "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward",
     "gf_batch_set_grads", "gf_batch_read",
@@ -102,6 +102,8 @@ def lib() -> ctypes.CDLL:
     L.gf_tile_grid.argtypes = [c_int64, c_int64, _CFG, POINTER(c_int64), POINTER(c_int64)]
     L.gf_forward_workspace_bytes.argtypes = [c_int64, c_int64, c_int64, _CFG]
     L.gf_forward_workspace_bytes.restype = c_size_t
+    L.gf_forward_workspace_bytes_max.argtypes = [c_int64, c_int64, c_int64, _CFG]
+    L.gf_forward_workspace_bytes_max.restype = c_size_t
     L.gf_backward_workspace_bytes.argtypes = [c_int64, c_int64, c_int64, _CFG]
     L.gf_backward_workspace_bytes.restype = c_size_t
     L.gf_forward_bin.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_size_t, _P]

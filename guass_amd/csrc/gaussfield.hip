@@ -2518,6 +2518,30 @@ size_t gf_forward_workspace_bytes(int64_t out_features, int64_t in_features, int
   return fwd_layout(p).total;
 }
 
+size_t gf_forward_workspace_bytes_max(int64_t out_features, int64_t in_features, int64_t k_capacity,
+                                      const gf_field_config* cfg) {
+  // Every condition of the mask path is an upper bound on K, so the mask path holds exactly for
+  // 1 <= K <= K*; the bytes grow with K on either side of K*, and the largest need over
+  // [0, k_capacity] is that of k_capacity or of min(k_capacity, K*).
+  Problem p;
+  if (k_capacity < 0 || make_problem(cfg, out_features, in_features, k_capacity, &p)) return 0;
+  size_t most = fwd_layout(p).total;
+  int64_t lo = 0, hi = std::min<int64_t>(k_capacity, kMaskMaxK);  // largest K on the mask path
+  while (lo < hi) {
+    const int64_t mid = lo + (hi - lo + 1) / 2;
+    Problem q;
+    if (make_problem(cfg, out_features, in_features, mid, &q) == GF_OK && q.W > 0)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  if (lo > 0) {
+    Problem q;
+    if (make_problem(cfg, out_features, in_features, lo, &q) == GF_OK) most = std::max(most, fwd_layout(q).total);
+  }
+  return most;
+}
+
 size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, int64_t k,
                                    const gf_field_config* cfg) {
   Problem p;

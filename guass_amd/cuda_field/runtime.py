@@ -45,7 +45,8 @@ def _backward(ctx, grad_delta, entry: str):
 
 class GaussianFieldCudaReferenceFunction(torch.autograd.Function):
     """Validation entry (reference runtime.py:11-104): same forward; backward through the
-    extension's reference entry, which returns the training gradients."""
+    extension's reference entry, which returns the training gradients.  The one-time warning
+    text is the reference's (runtime.py:66-73)."""
 
     _backward_warning_emitted = False
 
@@ -59,8 +60,9 @@ class GaussianFieldCudaReferenceFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_delta: Tensor):
         if not GaussianFieldCudaReferenceFunction._backward_warning_emitted:
-            warnings.warn("gaussian_field_reference backward is a validation entry point; use "
-                          "gaussian_field_train for training.", stacklevel=2)
+            warnings.warn("gaussian_field_reference backward is a validation-only reference replay path. "
+                          "Use it only for numerical alignment checks, not for training or performance "
+                          "measurements.", stacklevel=2)
             GaussianFieldCudaReferenceFunction._backward_warning_emitted = True
         return _backward(ctx, grad_delta, "gaussian_field_backward_reference")
 

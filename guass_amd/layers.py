@@ -158,9 +158,12 @@ class GaussianLinear(nn.Linear):
             mu = torch.empty(k, 2, device=dev, dtype=dt).uniform_(-1.0, 1.0)
         scale = max(2.0 / math.sqrt(max(k, 1)) * cfg.init_chol_scale_multiplier, cfg.min_cov_diag ** 0.5)
         chol_raw = torch.zeros(k, 3, device=dev, dtype=dt)
-        inv_sp = math.log(math.expm1(scale - cfg.eps))
-        chol_raw[:, 0] = inv_sp
-        chol_raw[:, 2] = inv_sp
+        # inverse softplus in the parameter dtype on the layer's device, as the reference
+        # computes it (gaussian_linear.py:115-125,286-288); a float64 evaluation rounded once
+        # differs from it by an ulp for some K
+        target_diag = torch.full((k, 2), scale, device=dev, dtype=dt)
+        chol_raw[:, 0] = torch.log(torch.expm1(target_diag[:, 0] - cfg.eps))
+        chol_raw[:, 2] = torch.log(torch.expm1(target_diag[:, 1] - cfg.eps))
         amp = torch.zeros(k, 1, device=dev, dtype=dt)
         if cfg.init_amp_scale > 0:
             amp.normal_(mean=0.0, std=cfg.init_amp_scale)

@@ -65,7 +65,8 @@ class FieldPlan:
 
         fwd = need(L.gf_forward_workspace_bytes, k)
         if self.fwd_ws is None or self.fwd_ws.numel() < fwd:
-            self.fwd_ws = torch.empty(max(fwd, need(L.gf_forward_workspace_bytes, kc)), dtype=torch.uint8,
+            # the largest need of any K up to the capacity (the bytes are not monotone in K)
+            self.fwd_ws = torch.empty(max(fwd, need(L.gf_forward_workspace_bytes_max, kc)), dtype=torch.uint8,
                                       device=dev)
             grew = True
         bwd = need(L.gf_backward_workspace_bytes, k)
@@ -203,8 +204,10 @@ class FieldBatchPlan:
         """Re-plans for ``layers`` (default: the current ones, re-read): each layer's K and
         tensors, with at least ``capacities`` gaussian ids and ``k_capacities`` Gaussians per
         layer.  Buffers grow only when they must.  Returns True when the launch grids and the
-        plan buffer are unchanged (graphs captured over forward() / backward() stay valid).
-        Synchronises the stream (the plan is uploaded from host memory)."""
+        plan buffer are unchanged (graphs captured over forward() / backward() stay valid: the
+        kernels read every layer's buffers from the plan).  ``self.reallocated`` tells whether a
+        layer buffer or the gradient buffer had to grow.  Synchronises the stream (the plan is
+        uploaded from host memory)."""
         if layers is not None:
             layers = list(layers)
             if self.plans and len(layers) != len(self.plans):
@@ -215,13 +218,14 @@ class FieldBatchPlan:
         kcs = list(k_capacities) if k_capacities is not None else [None] * n
         if len(caps) != n or len(kcs) != n:
             raise ValueError("capacities / k_capacities need one entry per layer")
+        grew = False
         for i, ly in enumerate(self.layers):
             M, Nf, K = int(ly.row_coords.numel()), int(ly.col_coords.numel()), int(ly.mu.shape[0])
             if i < len(self.plans):
                 pl = self.plans[i]
                 if (pl.M, pl.N) != (M, Nf):
                     raise ValueError(f"layer {i}: shape {M}x{Nf} differs from the planned {pl.M}x{pl.N}")
-                pl.resize(K, ids_capacity=caps[i], k_capacity=kcs[i])
+                grew |= pl.resize(K, ids_capacity=caps[i], k_capacity=kcs[i])
             else:
                 self.plans.append(FieldPlan(M, Nf, K, self.device, ids_capacity=caps[i],
                                             k_capacity=kcs[i], grads=False, **self._plan_kwargs))
@@ -229,8 +233,10 @@ class FieldBatchPlan:
         # d_amp [K,1]), so that they can be copied out with one launch.
         self.grad_numel = sum(6 * pl.K for pl in self.plans)
         if self.grad_flat is None or self.grad_flat.numel() < self.grad_numel:
+            grew = grew or self.grad_flat is not None
             self.grad_flat = torch.empty(max(sum(6 * pl.k_capacity for pl in self.plans), 1),
                                          dtype=torch.float32, device=self.device)
+        self.reallocated = grew
         o = 0
         for pl in self.plans:
             K = pl.K

@@ -67,6 +67,13 @@ size_t gf_forward_workspace_bytes(int64_t out_features, int64_t in_features, int
                                   const gf_field_config* cfg);
 size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, int64_t k,
                                    const gf_field_config* cfg);
+/* The largest gf_forward_workspace_bytes over every k in [0, k_capacity] (it is not monotone in
+ * k: past the mask path's limit the coverage masks drop out).  A workspace of this size serves
+ * any k up to the capacity, so densified fields (reference controllers/clone.py:31-56,
+ * prune.py:34-45) change k without reallocating.  No reference counterpart (the reference
+ * allocates its workspaces per call, field_impl.cu:110-133); 0 on an invalid argument. */
+size_t gf_forward_workspace_bytes_max(int64_t out_features, int64_t in_features, int64_t k_capacity,
+                                      const gf_field_config* cfg);
 
 /*
  * Forward phase 1 (binning): per-Gaussian geometry and sigma-box tile ranges, per-tile

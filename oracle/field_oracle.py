@@ -16,6 +16,8 @@ CPU/torch path for this kernel (paths are under ``/root/reference/gaussian_peft`
                              cuda_field/csrc/field_impl.cu:135-163 returns
 * ``gaussian_field_fwd_bwd`` forward + torch autograd backward, the gradient definition the
                              reference's training backward (backward.cu:541-716) implements
+* ``gaussian_linear_fwd_bwd`` the layer's use of it: mu = tanh(mu_raw), autograd through the tanh
+                             (layers/gaussian_linear.py:153-154,162-220)
 
 Deliberate difference: the reference sorts pair keys with ``torch.argsort`` (default
 ``stable=False``, tile_index.py:86), whose within-tile order is implementation-defined.  The
@@ -401,21 +403,26 @@ def dense_field(row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol_raw: Te
     return (amp.reshape(-1, 1) * basis).sum(dim=0)
 
 
-def tile_stats(tile_ptr: Tensor, out_features: int, in_features: int, tile_out: int,
-               tile_in: int) -> dict:
-    """Pairs P, pair-pixel evaluations E = sum_t count_t * pixels_t, per-tile max/mean."""
-    n_tr = (out_features + tile_out - 1) // tile_out
-    n_tc = (in_features + tile_in - 1) // tile_in
-    counts = (tile_ptr[1:] - tile_ptr[:-1]).reshape(n_tr, n_tc).to(torch.float64)
-    rows = torch.full((n_tr,), float(tile_out), dtype=torch.float64)
-    rows[-1] = out_features - (n_tr - 1) * tile_out
-    cols = torch.full((n_tc,), float(tile_in), dtype=torch.float64)
-    cols[-1] = in_features - (n_tc - 1) * tile_in
-    pixels = rows.reshape(-1, 1) * cols.reshape(1, -1)
-    return {
-        "pairs": int(tile_ptr[-1].item()),
-        "evals": int((counts * pixels).sum().item()),
-        "max_count": int(counts.max().item()),
-        "mean_count": float(counts.mean().item()),
-        "empty_tiles": int((counts == 0).sum().item()),
-    }
+
+def gaussian_linear_fwd_bwd(row_coords: Tensor, col_coords: Tensor, mu_raw: Tensor, chol_raw: Tensor,
+                            amp: Tensor, grad_delta: Tensor, tile_out: int, tile_in: int,
+                            sigma_multiplier: float, normalize: bool = False,
+                            clamp_quad: float | None = 80.0, *, mu_values: Tensor | None = None,
+                            batched: bool = False, exact_linalg: bool = True):
+    """The field of ``GaussianLinear.compute_delta_weight`` (layers/gaussian_linear.py:153-154,
+    162-220): mu = tanh(mu_raw), the field program on it, and autograd back through the tanh.
+
+    ``mu_values`` (optional, fp32 [K,2]) substitutes the forward value of tanh(mu_raw) -- e.g. the
+    device's tanh, which may differ from the CPU's in the last ulp and so move a sigma box across
+    a tile edge -- while the gradient still flows through ``torch.tanh``'s autograd.
+    Returns (delta, tile_ptr, gaussian_ids_sorted, d_mu_raw[K,2], d_chol_raw[K,3], d_amp[K,1]).
+    """
+    raw_leaf = mu_raw.detach().clone().requires_grad_(True)
+    mu = torch.tanh(raw_leaf)
+    if mu_values is not None:
+        mu = mu + (mu_values.to(mu.dtype) - mu).detach()
+    fn = gaussian_field_fwd_bwd_batched if batched else gaussian_field_fwd_bwd
+    out = fn(row_coords, col_coords, mu.detach(), chol_raw, amp, grad_delta, tile_out, tile_in,
+             sigma_multiplier, normalize, clamp_quad, exact_linalg=exact_linalg)
+    (d_mu_raw,) = torch.autograd.grad(mu, raw_leaf, grad_outputs=out[3])
+    return out[0], out[1], out[2], d_mu_raw, out[4], out[5]

@@ -76,6 +76,22 @@ def test_tile_grid_and_workspace_sizes():
     assert lib.gf_forward_workspace_bytes(10, 10, 4, ctypes.byref(_cfg(tile_out=0))) == 0
 
 
+@pytest.mark.parametrize("shape,kc", [((1280, 1280), 9000), ((320, 768), 8500), ((96, 80), 300),
+                                      ((1280, 1280), 5000)])
+def test_forward_workspace_bytes_max_is_worst_case(shape, kc):
+    """gf_forward_workspace_bytes_max(kc) = the largest gf_forward_workspace_bytes over every
+    K in [0, kc], by brute force.  Past K = 8192 the masks drop out and the need falls, so for
+    kc > 8192 the worst case is an interior K, not kc."""
+    lib = N.lib()
+    cfg = ctypes.byref(_cfg())
+    M, Nf = shape
+    need = [lib.gf_forward_workspace_bytes(M, Nf, k, cfg) for k in range(kc + 1)]
+    assert lib.gf_forward_workspace_bytes_max(M, Nf, kc, cfg) == max(need)
+    if kc > 8192:
+        assert max(need) > need[kc]
+    assert lib.gf_forward_workspace_bytes_max(M, Nf, -1, cfg) == 0
+
+
 @pytest.mark.parametrize("kw,msg", [({"tile_out": 0}, "tile_out must be positive"),
                                     ({"tile_in": -2}, "tile_in must be positive"),
                                     ({"sigma_multiplier": 0.0}, "sigma_multiplier must be positive")])

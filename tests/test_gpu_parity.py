@@ -39,16 +39,17 @@ def run_gpu(p: wl.FieldProblem, device, tile_out=16, tile_in=16, sigma=3.0, norm
 
 
 def oracle(p: wl.FieldProblem, tile_out=16, tile_in=16, sigma=3.0, normalize=False, clamp=80.0,
-           batched=False):
+           batched=False, exact_linalg=True):
     fn = fo.gaussian_field_fwd_bwd_batched if batched else fo.gaussian_field_fwd_bwd
     return fn(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad, tile_out, tile_in, sigma,
-              normalize, clamp)
+              normalize, clamp, exact_linalg=exact_linalg)
 
 
-def check(p: wl.FieldProblem, device, batched=False, **kw):
-    say(f"{p.name} M={p.out_features} N={p.in_features} K={p.k} {kw}")
+def check(p: wl.FieldProblem, device, batched=False, exact_linalg=True, **kw):
+    say(f"{p.name} M={p.out_features} N={p.in_features} K={p.k} {kw}"
+        + ("" if exact_linalg else " (oracle: fp32 linalg.inv/det)"))
     g = run_gpu(p, device, **kw)
-    r = oracle(p, batched=batched, **kw)
+    r = oracle(p, batched=batched, exact_linalg=exact_linalg, **kw)
     binning_equal(g[1], g[2], r[1], r[2])
     errs = {"delta": field_close(g[0], r[0])}
     for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), g[3:], r[3:]):
@@ -124,6 +125,14 @@ def ctypes_u64():
 @pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3"])
 def test_parity_baseline_configs(cfg, device):
     check(wl.CONFIGS[cfg](0), device)
+
+
+@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3"])
+def test_parity_reference_fp32_linalg(cfg, device):
+    """The same configs against the oracle with the reference CPU path's literal fp32
+    torch.linalg.inv / det (kernels/covariance.py:35-38, gaussian_core.py:42-44) instead of the
+    exact inverse of the same fp32 covariance: the kernels meet the bars against both."""
+    check(wl.CONFIGS[cfg](0), device, exact_linalg=False)
 
 
 @pytest.mark.parametrize("seed", [1, 2, 3])
@@ -590,28 +599,187 @@ def test_batch_matches_single_layers(device):
             grad_close(a, b, f"layer {i} {name}", rtol=1e-5)
 
 
+# One cfg4 layer of each of the six distinct SD1.5 attention shapes (index into
+# wl.sd15_attention_shapes(): block 0 attn1.to_q 320x320, block 0 attn2.to_k 320x768, block 2
+# attn1.to_q 640x640, block 2 attn2.to_k 640x768, block 4 attn1.to_q 1280x1280, block 4
+# attn2.to_k 1280x768).
+SD15_SHAPE_PICK = [0, 5, 16, 21, 32, 37]
+
+
+def _cfg4_layer(i: int) -> wl.FieldProblem:
+    """Layer i of wl.cfg4(0) (same seed, distribution and K = 1024) without drawing the others."""
+    name, m, n = wl.sd15_attention_shapes()[i]
+    return wl.make_problem(f"cfg4_{name}", m, n, 1024, math.log(8.0), 0.6, i)
+
+
 def test_batch_sd15_layers_against_oracle(device):
-    """Three SD1.5 attention layers of BASELINE cfg4 (320x320, 320x768 cross-attention key,
-    640x640) in one batch, against the CPU oracle."""
+    """One BASELINE cfg4 layer of each of the six SD1.5 attention shapes (320x320, 320x768,
+    640x640, 640x768, 1280x1280, 1280x768; K = 1024 each) in one batch, against the CPU
+    oracle."""
     from guass_amd.ops import FieldBatchPlan
 
-    shapes = wl.sd15_attention_shapes()
-    pick = [0, 6, 40]
-    probs = [wl.make_problem(f"cfg4_{shapes[i][0]}", shapes[i][1], shapes[i][2], 1024, math.log(8.0), 0.6, i)
-             for i in pick]
-    refs = [oracle(p, batched=True) for p in probs]
+    probs = [_cfg4_layer(i) for i in SD15_SHAPE_PICK]
+    assert sorted({(p.out_features, p.in_features) for p in probs}) == sorted(
+        {(m, n) for _, m, n in wl.sd15_attention_shapes()})
+    refs = []
+    for p in probs:
+        say(f"  oracle {p.name} {p.out_features}x{p.in_features}")
+        refs.append(oracle(p, batched=True))
     layers = [p.to(device) for p in probs]
     batch = FieldBatchPlan(layers, device, capacities=[int(r[1][-1]) for r in refs])
     batch.forward()
     batch.backward()
     torch.cuda.synchronize()
-    assert batch.status() == [0, 0, 0]
+    assert batch.status() == [0] * len(probs)
     for p, pl, r in zip(probs, batch.plans, refs):
-        say(f"  {p.name}: pairs={int(r[1][-1])}")
+        say(f"  {p.name} {p.out_features}x{p.in_features}: pairs={int(r[1][-1])}")
         binning_equal(pl.tile_ptr, pl.ids[:int(r[1][-1])], r[1], r[2])
         field_close(pl.delta, r[0])
         for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), r[3:]):
             grad_close(a, b, name)
+
+
+def test_cfg4_full_batch_matches_single_fields(device):
+    """BASELINE cfg4 at its workload: all 128 SD1.5 attention layers (K = 1024 each) as one
+    FieldBatchPlan, forward and backward, against each layer's own single-field run (the drop-in
+    ext path; reference: each adapted layer renders its own delta-W, gaussian_linear.py:162-220).
+    Binning is bit-equal for every layer.  delta-W is bit-equal where the single-field render
+    has no heavy-tile workgroups; a field of >= 8 pairs per tile (the 320- and 640-wide layers,
+    12-53 pairs per tile) renders its tiles of more than 32 Gaussians with four waves whose
+    partial sums wave 0 adds, a different fp32 summation order from the batch's one wave per
+    tile, so there delta-W agrees to 1e-6 of the field's peak.  Gradients agree to the atomics'
+    summation order."""
+    from guass_amd.ops import FieldBatchPlan
+
+    probs = wl.cfg4(0)
+    assert len(probs) == 128
+    say(f"cfg4: 128 layers, sum M*N = {sum(p.out_features * p.in_features for p in probs)}")
+    singles = []
+    for i, p in enumerate(probs):
+        singles.append(run_gpu(p, device))
+        if i % 32 == 31:
+            say(f"  single-field runs: {i + 1}/128")
+    layers = [p.to(device) for p in probs]
+    caps = [int(s[1][-1]) for s in singles]
+    batch = FieldBatchPlan(layers, device, capacities=caps)
+    tiles = [(-(-p.out_features // 16)) * (-(-p.in_features // 16)) for p in probs]
+    assert batch.info.tile_blocks == sum(-(-t // 4) for t in tiles)  # four 16x16 tiles a workgroup
+    batch.forward()
+    batch.backward()
+    torch.cuda.synchronize()
+    st, pairs = batch.read()
+    assert st == [0] * 128, [(i, x) for i, x in enumerate(st) if x]
+    assert pairs == caps
+    say(f"  batch done: {sum(caps)} pairs")
+    exact = heavy = 0
+    worst = 0.0
+    for i, (pl, sg, t) in enumerate(zip(batch.plans, singles, tiles)):
+        P = caps[i]
+        assert torch.equal(pl.tile_ptr, sg[1]), f"layer {i}: tile_ptr"
+        assert torch.equal(pl.ids[:P], sg[2]), f"layer {i}: ids"
+        if P >= 8 * t:  # the single-field render split its heavy tiles over four waves
+            heavy += 1
+            worst = max(worst, field_close(pl.delta, sg[0], rtol=1e-6))
+        else:
+            exact += 1
+            assert torch.equal(pl.delta, sg[0]), f"layer {i}: delta"
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), sg[3:]):
+            grad_close(a, b, f"layer {i} {name}", rtol=1e-5)
+    say(f"  every layer matches its single-field run: {exact} bit-equal, {heavy} heavy-tile layers "
+        f"within {worst:.1e} of the peak")
+    assert exact >= 48 and heavy >= 48
+
+
+def _layers_from_problems(probs, device, tile=16):
+    """GaussianLinear layers (K of each problem) holding the problems' parameters: mu_raw =
+    atanh(mu) as the layer stores it, and the problems' CPU linspace axes."""
+    from guass_amd.layers import GaussianAdapterConfig, GaussianLinear
+
+    layers = []
+    for p in probs:
+        cfg = GaussianAdapterConfig(init_num_gaussians=p.k, tile_out=tile, tile_in=tile)
+        ly = GaussianLinear(p.in_features, p.out_features, adapter_config=cfg, device=device)
+        with torch.no_grad():
+            ly.row_coords.copy_(p.row_coords.to(device))
+            ly.col_coords.copy_(p.col_coords.to(device))
+        ly.load_adapter_state({"mu_raw": torch.atanh(p.mu.clamp(-0.999999, 0.999999)),
+                               "chol_raw": p.chol_raw, "amp": p.amp})
+        layers.append(ly)
+    return layers
+
+
+def test_gaussian_field_batch_against_oracle(device):
+    """GaussianFieldBatch.render() + autograd (the batched kernels take mu = tanh(mu_raw) and
+    return dL/d(mu_raw)) against the CPU oracle's autograd through torch.tanh
+    (gaussian_linear.py:153-154,178-190), on a cfg2 layer and a 1280x1280 cfg4 layer in one
+    batch.  The oracle's forward uses the device's tanh values (torch's GPU tanh, the function
+    the kernels call), which are checked against the CPU's to 1 ulp."""
+    from guass_amd.layers import GaussianFieldBatch
+
+    probs = [wl.cfg2(0), _cfg4_layer(32)]
+    layers = _layers_from_problems(probs, device)
+    fb = GaussianFieldBatch(layers)
+    deltas = fb.render()
+    torch.autograd.backward(deltas, [p.grad.to(device).view(p.out_features, p.in_features) for p in probs])
+    torch.cuda.synchronize()
+    for p, ly, d in zip(probs, layers, deltas):
+        say(f"  {p.name} {p.out_features}x{p.in_features} K={p.k}: batched render vs oracle through tanh")
+        mu_raw = ly.mu_raw.detach().cpu()
+        mu_dev = torch.tanh(ly.mu_raw.detach()).cpu()
+        ulp = (mu_dev.view(torch.int32) - torch.tanh(mu_raw).view(torch.int32)).abs().max()
+        assert int(ulp) <= 1, f"device tanh {int(ulp)} ulp from the CPU's"
+        r = fo.gaussian_linear_fwd_bwd(ly.row_coords.cpu(), ly.col_coords.cpu(), mu_raw, ly.chol_raw.detach().cpu(),
+                                       ly.amp.detach().cpu(), p.grad, 16, 16, 3.0, False, 80.0,
+                                       mu_values=mu_dev, batched=p.k > 256)
+        pl = fb._plan.plans[layers.index(ly)]
+        binning_equal(pl.tile_ptr, pl.ids[:int(r[1][-1])], r[1], r[2])
+        field_close(d.detach().reshape(-1), r[0])
+        for name, got, want in zip(("d_mu_raw", "d_chol_raw", "d_amp"), (ly.mu_raw.grad, ly.chol_raw.grad, ly.amp.grad),
+                                   r[3:]):
+            grad_close(got, want, name)
+
+
+def test_gaussian_field_reference_entry(device):
+    """The validation entry gaussian_field_reference (runtime.py:236-270) with
+    allow_reference_backward=True and the extension's gaussian_field_backward_reference
+    (ext.cpp:73-110) at cfg2: delta-W and gradients against the oracle, the one-time warning of
+    its backward (runtime.py:66-73), and the guard's RuntimeError without the flag."""
+    import warnings
+
+    p = wl.cfg2(0)
+    q = p.to(device)
+    r = oracle(p)
+    mu = q.mu.clone().requires_grad_(True)
+    raw = q.chol_raw.clone().requires_grad_(True)
+    amp = q.amp.clone().requires_grad_(True)
+    kw = dict(row_coords=q.row_coords, col_coords=q.col_coords, tile_out=16, tile_in=16, sigma_multiplier=3.0,
+              normalize=False, clamp_quad=80.0)
+    with pytest.raises(RuntimeError, match="gaussian_field_reference is validation-only"):
+        runtime.gaussian_field_reference(mu=mu, chol_raw=raw, amp=amp, **kw)
+    runtime.GaussianFieldCudaReferenceFunction._backward_warning_emitted = False
+    for attempt in range(2):
+        for t in (mu, raw, amp):
+            t.grad = None
+        delta = runtime.gaussian_field_reference(mu=mu, chol_raw=raw, amp=amp, allow_reference_backward=True, **kw)
+        with warnings.catch_warnings(record=True) as caught:
+            warnings.simplefilter("always")
+            (delta * q.grad).sum().backward()
+        torch.cuda.synchronize()
+        msgs = [str(w.message) for w in caught if "validation-only reference replay" in str(w.message)]
+        assert len(msgs) == (1 if attempt == 0 else 0), msgs
+        say(f"  gaussian_field_reference attempt {attempt}: warnings {len(msgs)}")
+        field_close(delta, r[0])
+        grad_close(mu.grad, r[3], "d_mu")
+        grad_close(raw.grad, r[4], "d_chol_raw")
+        grad_close(amp.grad, r[5], "d_amp")
+    # the extension's entry directly, on int32 saved state
+    _, tp, ids = ext.gaussian_field_forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, 16, 16, 3.0,
+                                            False, 80.0)
+    got = ext.gaussian_field_backward_reference(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
+                                                tp.to(torch.int32), ids.to(torch.int32), 16, 16, 3.0, False, 80.0)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), got, r[3:]):
+        grad_close(a, b, f"backward_reference {name}")
 
 
 def test_batch_graph_replay(device):
@@ -1004,23 +1172,44 @@ def test_heavy_tiles_autograd_train_function(device, case):
 
 def test_one_layer_batch_survives_k_changes(device):
     """A single layer that must keep a captured graph across densification runs as a batch of
-    one: re-planned for K = 200, 480, 90 within k_capacity 512, its launch grids and plan size
-    stay the same and every K matches the oracle."""
+    one: a graph captured over forward + backward at K = 200 is replayed after update()
+    re-plans the same plan for K = 480 and 90 (k_capacity 512).  No buffer or plan pointer
+    changes, and every replay matches the oracle for the current K."""
     from guass_amd.ops import FieldBatchPlan
 
     p0 = wl.make_problem("one_layer_k200", 320, 768, 200, math.log(6.0), 0.7, 1)
     batch = FieldBatchPlan([p0.to(device)], device, capacities=[1 << 16], k_capacities=[512])
+    pl = batch.plans[0]
+
+    def pointers():
+        return (pl.fwd_ws.data_ptr(), pl.bwd_ws.data_ptr(), pl.ids.data_ptr(), pl.delta.data_ptr(),
+                batch.plan.data_ptr(), batch.grad_flat.data_ptr())
+
     first = (batch.info.tile_blocks, batch.info.emit_blocks, batch.info.finish_blocks, batch.info.plan_bytes)
+    ptrs = pointers()
+    s = torch.cuda.Stream(device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(s):
+        batch.forward()
+        batch.backward()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            batch.forward()
+            batch.backward()
+    torch.cuda.current_stream(device).wait_stream(s)
+    torch.cuda.synchronize()
     for k, seed in ((200, 1), (480, 2), (90, 3)):
         p = wl.make_problem(f"one_layer_k{k}", 320, 768, k, math.log(6.0), 0.7, seed)
         assert batch.update([p.to(device)]), f"K={k}: re-planned with new grids"
-        batch.forward()
-        batch.backward()
-        torch.cuda.synchronize()
+        assert not batch.reallocated and pointers() == ptrs, f"K={k}: a buffer was reallocated"
         assert (batch.info.tile_blocks, batch.info.emit_blocks, batch.info.finish_blocks,
                 batch.info.plan_bytes) == first
+        pl.delta.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        say(f"  K={k}: graph replayed after the re-plan")
+        assert batch.status() == [0]
         r = oracle(p)
-        pl = batch.plans[0]
         binning_equal(pl.tile_ptr, pl.ids[:int(r[1][-1])], r[1], r[2])
         field_close(pl.delta, r[0])
         for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), r[3:]):

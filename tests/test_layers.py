@@ -55,3 +55,21 @@ def test_field_batch_checks_layer_configs():
         GaussianFieldBatch([])
     with pytest.raises(TypeError):
         GaussianFieldBatch([torch.nn.Linear(4, 4)])
+
+
+@pytest.mark.parametrize("k", [8, 32, 128, 512])
+def test_init_chol_raw_matches_reference_arithmetic(k):
+    """Initial chol_raw diagonal = log(expm1(target - eps)) evaluated by torch in the parameter
+    dtype (reference gaussian_linear.py:115-125,286-288).  For these K the float64 value rounded
+    once to fp32 is an ulp away, so the check tells the two evaluations apart."""
+    import math
+
+    cfg = GaussianAdapterConfig(init_num_gaussians=k, init_method="uniform_grid")
+    layer = GaussianLinear(16, 16, adapter_config=cfg)
+    scale = max(2.0 / math.sqrt(k) * cfg.init_chol_scale_multiplier, cfg.min_cov_diag ** 0.5)
+    fp32 = torch.log(torch.expm1(torch.full((k,), scale, dtype=torch.float32) - cfg.eps))
+    f64_rounded = torch.full((k,), math.log(math.expm1(scale - cfg.eps)), dtype=torch.float32)
+    assert not torch.equal(fp32, f64_rounded)
+    raw = layer.chol_raw.detach()
+    assert torch.equal(raw[:, 0], fp32) and torch.equal(raw[:, 2], fp32)
+    assert float(raw[:, 1].abs().max()) == 0.0

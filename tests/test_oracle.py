@@ -356,7 +356,7 @@ def _close(a, b, rtol):
     return float((a - b).abs().max()) <= rtol * float(b.abs().max()) + 1e-30
 
 
-@pytest.mark.parametrize("cfg", ["cfg1", "cfg2"])
+@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3"])
 def test_batched_and_fp64_variants_match_loop(cfg):
     p = wl.CONFIGS[cfg](0)
     args = (p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad, 16, 16, 3.0, False, 80.0)
@@ -369,6 +369,38 @@ def test_batched_and_fp64_variants_match_loop(cfg):
         assert _close(other[0], loop[0], ftol)
         for a, b in zip(other[3:], loop[3:]):
             assert _close(a, b, gtol)
+
+
+def test_gaussian_linear_oracle_chains_through_tanh():
+    """gaussian_linear_fwd_bwd (mu = tanh(mu_raw), autograd back through the tanh) against the
+    field oracle at tanh(mu_raw) with d/dx tanh = 1 - tanh^2 applied in float64; a substituted
+    forward value (mu_values) changes the field but keeps the derivative at tanh(mu_raw)."""
+    p = wl.make_problem("tanh_chain", 48, 72, 20, math.log(3.0), 0.4, 21)
+    mu_raw = torch.atanh(p.mu.clamp(-0.999999, 0.999999)) + 0.05
+    args = (p.row_coords, p.col_coords)
+    tail = (p.chol_raw, p.amp, p.grad, 16, 16, 3.0, False, 80.0)
+    got = fo.gaussian_linear_fwd_bwd(*args, mu_raw, *tail)
+    mu = torch.tanh(mu_raw)
+    ref = fo.gaussian_field_fwd_bwd(*args, mu, *tail)
+    assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1]) and torch.equal(got[2], ref[2])
+    t = torch.tanh(mu_raw.double())
+
+    def chained(d_mu, d_mu_raw):
+        # autograd forms 1 - y^2 from the fp32 tanh y: an absolute error of about 2^-23 in the
+        # factor, i.e. relative 1e-5 where |tanh| is near 1 (mu_raw up to 3 here)
+        want = d_mu.double() * (1.0 - t * t)
+        err = (d_mu_raw.double() - want).abs()
+        return bool((err <= 1e-6 * want.abs() + 3e-7 * d_mu.double().abs()).all())
+
+    assert chained(ref[3], got[3])
+    assert torch.equal(got[4], ref[4]) and torch.equal(got[5], ref[5])
+    shifted = mu + 1e-3
+    sub = fo.gaussian_linear_fwd_bwd(*args, mu_raw, *tail, mu_values=shifted)
+    ref2 = fo.gaussian_field_fwd_bwd(*args, shifted, *tail)
+    assert torch.equal(sub[0], ref2[0])
+    assert chained(ref2[3], sub[3])
+    batched = fo.gaussian_linear_fwd_bwd(*args, mu_raw, *tail, batched=True)
+    assert _close(batched[0], got[0], 1e-6) and _close(batched[3], got[3], 1e-5)
 
 
 # ------------------------------------------------------------------------------ fixtures
