@@ -30,7 +30,7 @@ EXPORTED = (
     "gf_forward_workspace_bytes_max", "gf_backward_workspace_bytes", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
     "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
     "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward",
-    "gf_batch_set_grads", "gf_batch_read",
+    "gf_batch_set_grads", "gf_batch_read", "gf_backward_noalloc",
 )
 
 GF_PHASE_BIN, GF_PHASE_EMIT, GF_PHASE_RENDER = 0x1, 0x2, 0x4
@@ -116,6 +116,8 @@ def lib() -> ctypes.CDLL:
     L.gf_backward_reduce.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int32,
                                      _P, c_int32, c_int64, _P, _P, c_size_t, _P]
     L.gf_backward_finish.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_size_t, _P]
+    L.gf_backward_noalloc.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int32,
+                                      _P, c_int32, c_int64, _P, _P, _P, _P, _P]
     L.gf_read_status.argtypes = [_P, c_int32, POINTER(c_uint32), _P]
     L.gf_batch_plan.argtypes = [_CFG, POINTER(GfLayer), c_int32, _P, c_size_t, POINTER(GfBatchInfo), _P]
     L.gf_batch_forward.argtypes = [_P, POINTER(GfBatchInfo), c_uint32, _P]
@@ -126,7 +128,7 @@ def lib() -> ctypes.CDLL:
     for name in ("gf_tile_grid", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
                  "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
                  "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward",
-                 "gf_batch_set_grads", "gf_batch_read"):
+                 "gf_batch_set_grads", "gf_batch_read", "gf_backward_noalloc"):
         getattr(L, name).restype = c_int
     _LIB = L
     return L

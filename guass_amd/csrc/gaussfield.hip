@@ -40,6 +40,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <type_traits>
 #include <vector>
 
@@ -2491,6 +2492,54 @@ void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, 
                        num_pairs, ws, L);
 }
 
+// ------------------------------------------------------------------------------------------
+// Allocation-free backward (gf_backward_noalloc).  Its workspace -- the header with the status
+// word and the S x K accumulator slots -- lives in this static device array, one copy per GPU,
+// held until the process ends.  4 MiB: K up to 131,064 Gaussians for S = 1 (fewer than 8192 tiles),
+// 32,760 for S = 4 and 8,184 for S = 16.
+constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;
+
+// Clears n 16-byte words (a fill kernel rather than hipMemsetAsync, which must not be recorded
+// into the HIP graphs a caller of the allocation-free entry may capture).
+__global__ __launch_bounds__(256) void k_fill_zero(uint4* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Copies a workspace's status word to the caller's device word.
+__global__ __launch_bounds__(64) void k_copy_status(const uint32_t* __restrict__ status, uint32_t* __restrict__ out) {
+  if (threadIdx.x == 0) *out = *status;
+}
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+// The device address of `scratch` on the current device, looked up once per device with that
+// device current (each GPU holds its own copy of the array at its own address).  In host code
+// the name `scratch` is only a host-side stand-in: kernels get this address instead.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];
+
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  GF_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return set_err(GF_E_HIP, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return set_err(GF_E_HIP, "hipGetSymbolAddress(scratch) on device %d failed: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return GF_OK;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------------------------------
@@ -2917,6 +2966,43 @@ int gf_batch_backward(const void* plan, const gf_batch_info* info, uint32_t phas
   if ((phases & GF_PHASE_FINISH) && info->finish_blocks > 0) {
     hipLaunchKernelGGL(k_finish_batch, dim3((unsigned)info->finish_blocks), dim3(kTileThreads), 0, st, pl);
     GF_LAUNCH_CHECK("k_finish_batch");
+  }
+  return GF_OK;
+}
+
+int gf_backward_noalloc(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                        const float* grad_delta, const float* row_coords, const float* col_coords,
+                        const float* mu, const float* chol_raw, const float* amp, const void* tile_ptr,
+                        int32_t tile_ptr_is_int64, const void* gaussian_ids, int32_t ids_is_int64,
+                        int64_t num_pairs, float* d_mu, float* d_chol_raw, float* d_amp, uint32_t* status_dev,
+                        void* stream) {
+  Problem p;
+  int rc = make_problem(cfg, out_features, in_features, k, &p);
+  if (rc) return rc;
+  const BwdLayout L = bwd_layout(p);
+  if (L.total > kNoAllocScratchBytes)
+    return set_err(GF_E_WORKSPACE,
+                   "gf_backward_noalloc: this field needs %zu bytes of backward workspace; the static scratch "
+                   "holds %zu (K <= %lld for %d accumulator stripes); use gf_backward with a workspace",
+                   L.total, kNoAllocScratchBytes,
+                   (long long)((kNoAllocScratchBytes - sizeof(WsHeader)) / (32 * (size_t)p.S)), (int)p.S);
+  if (k > 0 && !amp) return set_err(GF_E_INVALID_ARGUMENT, "amp must not be NULL");
+  void* ws = nullptr;
+  rc = scratch_for_current_device(&ws);
+  if (rc) return rc;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // the header (status word) and this call's accumulator slots start at zero
+  const int64_t words = (int64_t)(L.total / 16);
+  hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)std::min<int64_t>((words + 255) / 256, 1024)), dim3(256), 0, st,
+                     reinterpret_cast<uint4*>(ws), words);
+  GF_LAUNCH_CHECK("k_fill_zero");
+  rc = gf_backward(cfg, out_features, in_features, k, grad_delta, row_coords, col_coords, mu, chol_raw, amp,
+                   tile_ptr, tile_ptr_is_int64, gaussian_ids, ids_is_int64, num_pairs, d_mu, d_chol_raw, d_amp,
+                   nullptr, ws, L.total, stream);
+  if (rc) return rc;
+  if (status_dev) {
+    hipLaunchKernelGGL(k_copy_status, dim3(1), dim3(64), 0, st, reinterpret_cast<const uint32_t*>(ws), status_dev);
+    GF_LAUNCH_CHECK("k_copy_status");
   }
   return GF_OK;
 }

@@ -259,6 +259,29 @@ int gf_batch_read(void* plan, const gf_batch_info* info, int32_t clear, uint32_t
                   int64_t* pairs_host, void* stream);
 
 /*
+ * Allocation-free gf_backward.  No counterpart in the reference (whose backward allocates its
+ * buffers on every call, backward.cu:541-716); it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and gradients as gf_backward with forward_workspace = NULL (the Gaussians'
+ * constants are recomputed from mu / chol_raw), but the backward workspace is a static device
+ * array of 4 MiB held by the library on each GPU it runs on until the process ends; the call
+ * makes no hipMalloc / hipFree and allocates nothing else.  It covers fields whose workspace
+ * (gf_backward_workspace_bytes) fits 4 MiB: K <= 131,064 below 8192 tiles (K <= 32,760 below
+ * 16,384 tiles, K <= 8,184 above); larger fields are rejected with GF_E_WORKSPACE before any
+ * device work.  Each call clears the part of the array it uses (a kernel, no memset), so it
+ * needs no set-up; every call on one GPU shares that GPU's array, so calls that overlap on one
+ * GPU (different streams or threads without ordering) race and must be serialised by the caller.
+ *   status_dev      optional [1] uint32 out (device): the call's GF_STATUS_* bits (saved-state
+ *                   violations), written on `stream`; NULL skips it.
+ */
+int gf_backward_noalloc(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                        const float* grad_delta, const float* row_coords, const float* col_coords,
+                        const float* mu, const float* chol_raw, const float* amp,
+                        const void* tile_ptr, int32_t tile_ptr_is_int64,
+                        const void* gaussian_ids, int32_t ids_is_int64, int64_t num_pairs,
+                        float* d_mu, float* d_chol_raw, float* d_amp, uint32_t* status_dev, void* stream);
+
+/*
  * Reads (and, if clear != 0, resets) the device status word of a workspace produced by the
  * calls above.  Synchronises `stream`.  *status_host receives GF_STATUS_* bits.
  */

@@ -1,0 +1,79 @@
+"""gf_backward_noalloc: the backward with its workspace in the library's static device scratch.
+
+Called through the C ABI and checked against the existing entry point gf_backward (same
+kernels, a caller-allocated workspace) and against the CPU oracle, on consecutive calls of
+shrinking size: a field with four accumulator stripes, then cfg2, then cfg1.  Each call clears
+only what it uses, so a smaller call after a larger one must not see the larger one's state.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import pytest
+import torch
+
+from guass_amd import _native as N
+from guass_amd import workloads as wl
+from guass_amd.cuda_field import ext
+from oracle import field_oracle as fo
+from tests.parity import grad_close
+
+GF_E_WORKSPACE = 2
+SCRATCH_BYTES = 4 << 20
+
+
+def _cfg():
+    return N.make_config(16, 16, 3.0, False, 80.0)
+
+
+def test_noalloc_rejects_fields_beyond_the_scratch():
+    """A workspace past 4 MiB is refused with GF_E_WORKSPACE before any device work (safe
+    without a GPU); gf_backward_workspace_bytes tells where the limit falls."""
+    L = N.lib()
+    cfg = ctypes.byref(_cfg())
+    assert L.gf_backward_workspace_bytes(320, 768, 131064, cfg) == SCRATCH_BYTES
+    assert L.gf_backward_workspace_bytes(320, 768, 131065, cfg) > SCRATCH_BYTES
+    d = ctypes.c_void_p(16)  # never dereferenced: the size check comes first
+    rc = L.gf_backward_noalloc(cfg, 320, 768, 131065, d, d, d, d, d, d, d, 1, d, 1, 1, d, d, d, None, None)
+    assert rc == GF_E_WORKSPACE
+    msg = L.gf_last_error().decode()
+    assert "static scratch" in msg and "131064" in msg
+
+
+def _noalloc(q, tp, ids, device):
+    K = q.k
+    out = [torch.full((K, n), float("nan"), dtype=torch.float32, device=device) for n in (2, 3, 1)]
+    status = torch.full((1,), -1, dtype=torch.int32, device=device)
+    N.check(N.lib().gf_backward_noalloc(
+        ctypes.byref(_cfg()), q.out_features, q.in_features, K, q.grad.data_ptr(), q.row_coords.data_ptr(),
+        q.col_coords.data_ptr(), q.mu.data_ptr(), q.chol_raw.data_ptr(), q.amp.data_ptr(), tp.data_ptr(),
+        int(tp.dtype == torch.int64), ids.data_ptr(), int(ids.dtype == torch.int64), ids.numel(),
+        out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(), status.data_ptr(),
+        N.stream_handle(device)), "gf_backward_noalloc")
+    return out, status
+
+
+@pytest.mark.gpu
+def test_noalloc_backward_matches_gf_backward(device):
+    probs = [wl.make_problem("stripes4_1280x1792_k512", 1280, 1792, 512, math.log(8.0), 0.6, 3),
+             wl.cfg2(0), wl.cfg1(0)]
+    for i, p in enumerate(probs):
+        print(f"[gpu-test] gf_backward_noalloc call {i}: {p.name} M={p.out_features} N={p.in_features} K={p.k}",
+              flush=True)
+        q = p.to(device)
+        _, tp, ids = ext.gaussian_field_forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, 16, 16, 3.0,
+                                                False, 80.0)
+        if i == 2:  # int32 saved state on the last call
+            tp, ids = tp.to(torch.int32), ids.to(torch.int32)
+        want = ext.gaussian_field_backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, tp, ids,
+                                           16, 16, 3.0, False, 80.0)
+        got, status = _noalloc(q, tp, ids, device)
+        torch.cuda.synchronize()
+        assert int(status.item()) == 0
+        ref = fo.gaussian_field_fwd_bwd_batched(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad,
+                                                16, 16, 3.0, False, 80.0)
+        for name, a, b, r in zip(("d_mu", "d_chol_raw", "d_amp"), got, want, ref[3:]):
+            grad_close(a, b, f"call {i} {name} vs gf_backward", rtol=1e-5)
+            grad_close(a, r, f"call {i} {name} vs oracle")
