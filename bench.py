@@ -13,10 +13,11 @@ graph.  Workloads:
   delta-apply                   the layer's composition with delta-W over the cfg4 shapes (x of
                                 --tokens rows, fp32, forward + backward into delta-W): the
                                 reference's row-chunked composition against one merged GEMM
-  cfg4-model                    the cfg4 layers as GaussianLinear modules through autograd: one
-                                training step's fields via GaussianFieldBatch.render() (one
-                                batched launch per phase) against every layer rendering its own
-                                through the drop-in gaussian_field_train (eager, both)
+  cfg4-model                    the cfg4 layers as GaussianLinear modules: one training step
+                                (delta-W, every layer's forward on --model-tokens rows, autograd
+                                backward) with GaussianFieldBatch.render() (one batched launch
+                                per phase, one host read-back) against every layer rendering
+                                its own through the drop-in gaussian_field_train (eager, both)
 All with 16x16 tiles (--tile 32: the reference's training configs' 32x32), 3 sigma, clamp 80.
 
 Prints one JSON line (metric contract of the driver) with two extra objects:
@@ -55,6 +56,11 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--config", default="cfg3",
                     choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "cfg5c", "cfg4-model", "delta-apply"])
     ap.add_argument("--tokens", type=int, default=4096, help="delta-apply: rows of x per layer")
+    ap.add_argument("--model-tokens", type=int, default=64, help="cfg4-model: rows of x per layer")
+    ap.add_argument("--delta-apply", default="merged", choices=["merged", "row_chunk"],
+                    help="cfg4-model: how each layer composes its base weight with delta-W")
+    ap.add_argument("--skip-per-layer", action="store_true",
+                    help="cfg4-model: time the batched step only (no per-layer comparison)")
     ap.add_argument("--tile", type=int, default=16, choices=[16, 32],
                     help="square tile size (the headline metric is quoted on 16x16 tiles)")
     ap.add_argument("--layers", type=int, default=None, help="cfg4: first N of the 128 layers")
@@ -170,19 +176,20 @@ def cpu_baseline(problems, reps: int, note: str, tile: int = 16) -> dict:
 
 
 def model_bench(args) -> int:
-    """cfg4-model: one training step's Gaussian fields of the 128 SD1.5 attention layers through
-    the layer API and autograd (dL/d(delta-W) fed to autograd directly, no model around them)."""
+    """cfg4-model: one training step of the 128 SD1.5 attention layers as GaussianLinear
+    modules: every layer's delta-W (GaussianFieldBatch.render(), or each layer rendering its own
+    through gaussian_field_train inside its forward, as the reference does), every layer's
+    forward on --model-tokens rows of input, and autograd's backward through them."""
     import torch
 
     from guass_amd import workloads as wl
-    from guass_amd.cuda_field.runtime import gaussian_field_train
     from guass_amd.layers import GaussianAdapterConfig, GaussianFieldBatch, GaussianLinear
 
     dev = torch.device("cuda:0")
     probs = wl.cfg4(args.seed, layers=args.layers)
     layers = []
     for p in probs:
-        cfg = GaussianAdapterConfig(init_num_gaussians=p.k, tile_out=16, tile_in=16)
+        cfg = GaussianAdapterConfig(init_num_gaussians=p.k, tile_out=16, tile_in=16, delta_apply=args.delta_apply)
         ly = GaussianLinear(p.in_features, p.out_features, adapter_config=cfg, device=dev)
         with torch.no_grad():
             ly.row_coords.copy_(p.row_coords.to(dev))
@@ -190,20 +197,18 @@ def model_bench(args) -> int:
         ly.load_adapter_state({"mu_raw": torch.atanh(p.mu.clamp(-0.999999, 0.999999)),
                                "chol_raw": p.chol_raw, "amp": p.amp})
         layers.append(ly)
-    grads = [p.grad.to(dev).reshape(p.out_features, p.in_features) for p in probs]
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    xs = [torch.randn(args.model_tokens, p.in_features, device=dev, generator=gen) for p in probs]
+    gys = [torch.randn(args.model_tokens, p.out_features, device=dev, generator=gen) for p in probs]
     params = [t for ly in layers for t in (ly.mu_raw, ly.chol_raw, ly.amp)]
     fb = GaussianFieldBatch(layers, k_capacity=2 * max(p.k for p in probs))
 
     def batched():
-        torch.autograd.backward(fb.render(), grads)
+        fb.render()  # every layer's delta-W, one read-back; each layer's forward consumes its own
+        torch.autograd.backward([ly(x) for ly, x in zip(layers, xs)], gys)
 
-    def per_layer():
-        deltas = [gaussian_field_train(row_coords=ly.row_coords, col_coords=ly.col_coords,
-                                       mu=ly.materialize_mu(), chol_raw=ly.chol_raw, amp=ly.amp,
-                                       tile_out=16, tile_in=16, sigma_multiplier=3.0, normalize=False,
-                                       clamp_quad=80.0).reshape(ly.out_features, ly.in_features)
-                  for ly in layers]
-        torch.autograd.backward(deltas, grads)
+    def per_layer():  # the reference's step: each layer renders its delta-W in its forward
+        torch.autograd.backward([ly(x) for ly, x in zip(layers, xs)], gys)
 
     def timed(fn, steps: int, warmup: int) -> float:
         for _ in range(warmup):
@@ -218,6 +223,10 @@ def model_bench(args) -> int:
         return (time.perf_counter() - t0) / steps
 
     t_batch = timed(batched, args.steps, args.warmup)
+    if args.skip_per_layer:  # e.g. to trace the batched steps alone
+        print(json.dumps({"config": "cfg4-model", "batched_ms_per_step": t_batch * 1e3,
+                          "steps": args.steps, "warmup": args.warmup}), flush=True)
+        return 0
     t_single = timed(per_layer, max(1, args.steps // 5), max(1, args.warmup // 5))
     densify = densify_costs(fb, layers, batched, params)
     elements = float(sum(p.out_features * p.in_features for p in probs))
@@ -227,9 +236,10 @@ def model_bench(args) -> int:
         "warmup": args.warmup, "ms_per_step": t_batch * 1e3, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded Gaussian fields, BASELINE.json cfg4 distribution)",
-        "config": {"workload": f"cfg4 x{len(probs)} GaussianLinear layers, GaussianFieldBatch.render + "
-                               "autograd backward (eager)", "layers": len(probs),
-                   "sum_out_x_in": int(elements), "k_per_layer": 1024},
+        "config": {"workload": f"cfg4 x{len(probs)} GaussianLinear layers: GaussianFieldBatch.render, every "
+                               f"layer's forward on {args.model_tokens} rows, autograd backward (eager)",
+                   "layers": len(probs), "sum_out_x_in": int(elements), "k_per_layer": 1024,
+                   "tokens_per_layer": args.model_tokens, "delta_apply": args.delta_apply},
         "per_layer_ms_per_step": t_single * 1e3,
         "speedup_vs_per_layer": t_single / t_batch,
         "densify": densify,

@@ -123,7 +123,8 @@ def lib() -> ctypes.CDLL:
     L.gf_batch_forward.argtypes = [_P, POINTER(GfBatchInfo), c_uint32, _P]
     L.gf_batch_backward.argtypes = [_P, POINTER(GfBatchInfo), c_uint32, _P]
     L.gf_batch_set_grads.argtypes = [_P, POINTER(GfBatchInfo), POINTER(c_void_p), _P]
-    L.gf_batch_read.argtypes = [_P, POINTER(GfBatchInfo), c_int32, POINTER(c_uint32), POINTER(c_int64), _P]
+    L.gf_batch_read.argtypes = [_P, POINTER(GfBatchInfo), c_int32, POINTER(c_uint32), POINTER(c_int64),
+                                POINTER(c_double), _P]
     L.gf_selftest_softplus.argtypes = [POINTER(c_uint64), _P]
     for name in ("gf_tile_grid", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
                  "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",

@@ -36,6 +36,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -153,9 +154,10 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // (int4 tile ranges), cov[K] (float4: the fp32 covariance s00, s01, s11 and 0), fill[T]
 // (int32 ids emitted so far into each tile's segment; emission path), rowmask[R][W] and
 // colmask[C][W] (mask path: bit g%32 of word g/32 is set when Gaussian g's tile rectangle covers
-// the tile row / column).
+// the tile row / column), bsq[blocks] (fp32 sum of delta-W^2 over each 16x16 block, written by
+// the batched render for the layer's norm).
 struct FwdLayout {
-  size_t eval, rect, cov, lfac, fill, rowmask, colmask, total;
+  size_t eval, rect, cov, lfac, fill, rowmask, colmask, bsq, total;
 };
 FwdLayout fwd_layout(const Problem& p) {
   const int64_t K = p.K, T = (int64_t)p.R * p.C;
@@ -175,6 +177,8 @@ FwdLayout fwd_layout(const Problem& p) {
   o = align256(o + sizeof(uint32_t) * (size_t)p.R * (size_t)p.W);
   L.colmask = o;
   o = align256(o + sizeof(uint32_t) * (size_t)p.C * (size_t)p.W);
+  L.bsq = o;  // batched render: sum of squares of delta-W over each 16x16 block (block index sidx)
+  o = align256(o + sizeof(float) * (size_t)T * (p.tile_out == 32 && p.tile_in == 32 ? 4 : 1));
   L.total = o;
   return L;
 }
@@ -1358,7 +1362,7 @@ __device__ __forceinline__ void render16_body(
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids,
     int64_t capacity, float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
     const uint32_t* __restrict__ colmask, const SubTile& st, const int4* __restrict__ rects = nullptr,
-    int64_t* __restrict__ tile_ptr_out = nullptr, int q = 0, int F = 1) {
+    int64_t* __restrict__ tile_ptr_out = nullptr, int q = 0, int F = 1, float* __restrict__ blk_sq = nullptr) {
   // F > 1 (heavy tiles, mask path only): the F = 4 waves of the workgroup share tile st, wave q
   // taking chunks q, q + F, ... of kHeavyChunk Gaussians; wave 0 adds the others' partial sums
   // in wave order and writes the tile.  Every wave must call it (two workgroup barriers).
@@ -1599,6 +1603,17 @@ __device__ __forceinline__ void render16_body(
     }
     __syncthreads();  // the partial sums are read before the slots are reused
     if (wid != 0) return;
+  }
+  if (blk_sq) {  // the block's sum of squares (the layer's ||delta-W||, reduced by k_batch_read)
+    float sq = 0.f;
+    if (pr < p.M) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (pc + i < p.N) sq = fmaf(acc[i], acc[i], sq);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
+    if (lane == 0) blk_sq[st.sidx] = sq;
   }
   if (pr < p.M) {
     float* out = delta + (int64_t)pr * p.N + pc;
@@ -2316,6 +2331,8 @@ struct BatchReadback {
   uint32_t status;
   uint32_t pad;
   int64_t pairs;
+  double delta_sumsq;  // sum of delta-W^2 of the last forward
+  double pad2;
 };
 
 BatchHeader batch_header(int64_t n, int64_t tile_blocks, int64_t emit_blocks, int64_t finish_blocks) {
@@ -2374,7 +2391,8 @@ __global__ __launch_bounds__(kTileThreads) void k_render16_batch(const uint8_t* 
                 ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws,
                 reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.rowmask),
                 reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.colmask),
-                sub_tile(p, (int64_t)blockIdx.x - b0, wave_id()));
+                sub_tile(p, (int64_t)blockIdx.x - b0, wave_id()), nullptr, nullptr, 0, 1,
+                reinterpret_cast<float*>(ly.fws + ly.fl.bsq));
 }
 
 template <bool kMaskClamp>
@@ -2407,19 +2425,35 @@ __global__ __launch_bounds__(kPtrChunk) void k_batch_set_grads(uint8_t* plan, Pt
     reinterpret_cast<const float**>(plan + h->grad_table_off)[base + threadIdx.x] = chunk.p[threadIdx.x];
 }
 
-// Per layer: forward | backward status bits and the pair count, into the read-back area;
-// clear != 0 resets the status words.
+// One workgroup per layer: forward | backward status bits, the pair count and the sum of
+// delta-W^2 over the render's 16x16 blocks (in double, a fixed order: thread-strided sums, then
+// a tree), into the read-back area; clear != 0 resets the status words.
 __global__ __launch_bounds__(256) void k_batch_read(uint8_t* plan, int32_t clear) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
-  const int64_t l = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t l = blockIdx.x;
   if (l >= h->n) return;
   const BatchLayer& ly = reinterpret_cast<const BatchLayer*>(plan + h->layers_off)[l];
+  const Problem& p = ly.p;
+  const int64_t nb = (int64_t)p.R * p.C * (p.tile_out == 32 ? 4 : 1);
+  const float* bsq = reinterpret_cast<const float*>(ly.fws + ly.fl.bsq);
+  double v = 0.0;
+  for (int64_t i = threadIdx.x; i < nb; i += blockDim.x) v += (double)bsq[i];
+  __shared__ double part[256];
+  part[threadIdx.x] = v;
+  __syncthreads();
+  for (int o = 128; o >= 1; o >>= 1) {
+    if ((int)threadIdx.x < o) part[threadIdx.x] += part[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x != 0) return;
   WsHeader* fh = reinterpret_cast<WsHeader*>(ly.fws);
   WsHeader* bh = reinterpret_cast<WsHeader*>(ly.bws);
   BatchReadback r;
   r.status = fh->status | (bh ? bh->status : 0u);
   r.pad = 0u;
   r.pairs = *ly.num_pairs;
+  r.delta_sumsq = part[0];
+  r.pad2 = 0.0;
   reinterpret_cast<BatchReadback*>(plan + h->readback_off)[l] = r;
   if (clear) {
     fh->status = 0u;
@@ -2928,13 +2962,13 @@ int gf_batch_set_grads(void* plan, gf_batch_info* info, const float* const* grad
 }
 
 int gf_batch_read(void* plan, const gf_batch_info* info, int32_t clear, uint32_t* status_host,
-                  int64_t* pairs_host, void* stream) {
+                  int64_t* pairs_host, double* delta_norm_host, void* stream) {
   if (!plan || !info) return set_err(GF_E_INVALID_ARGUMENT, "plan / info must not be NULL");
   const int32_t n = info->n_layers;
   if (n == 0) return GF_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* pl = reinterpret_cast<uint8_t*>(plan);
-  hipLaunchKernelGGL(k_batch_read, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, pl, clear);
+  hipLaunchKernelGGL(k_batch_read, dim3((unsigned)n), dim3(256), 0, st, pl, clear);
   GF_LAUNCH_CHECK("k_batch_read");
   const BatchHeader h = batch_header(n, info->tile_blocks, info->emit_blocks, info->finish_blocks);
   std::vector<BatchReadback> rb((size_t)n);
@@ -2944,6 +2978,7 @@ int gf_batch_read(void* plan, const gf_batch_info* info, int32_t clear, uint32_t
   for (int32_t i = 0; i < n; ++i) {
     if (status_host) status_host[i] = rb[(size_t)i].status;
     if (pairs_host) pairs_host[i] = rb[(size_t)i].pairs;
+    if (delta_norm_host) delta_norm_host[i] = std::sqrt(rb[(size_t)i].delta_sumsq);
   }
   return GF_OK;
 }

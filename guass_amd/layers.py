@@ -117,7 +117,7 @@ class GaussianLinear(nn.Linear):
         self.register_buffer("col_coords", torch.linspace(-1.0, 1.0, in_features, device=self.weight.device),
                              persistent=False)
         self.last_forward_metadata: dict = {}
-        self._batched_delta: Tensor | None = None
+        self._batched_delta: tuple[Tensor, float] | None = None  # (delta-W, its norm) from GaussianFieldBatch
         self.reset_gaussian_parameters()
 
     @classmethod
@@ -200,11 +200,12 @@ class GaussianLinear(nn.Linear):
         cfg = self.adapter_config
         pending = self._batched_delta
         if pending is not None:
-            # rendered for this step by GaussianFieldBatch.render(); used once
+            # rendered for this step by GaussianFieldBatch.render(), with its norm from the
+            # batch's one read-back (no per-layer synchronisation); used once
             self._batched_delta = None
-            delta_weight = pending
-            metadata = {"execution_mode": cfg.execution_mode, "accumulate_backend": "batched_fields"}
-            metadata["delta_w_norm"] = float(delta_weight.detach().float().norm().item())
+            delta_weight, norm = pending
+            metadata = {"execution_mode": cfg.execution_mode, "accumulate_backend": "batched_fields",
+                        "delta_w_norm": norm}
             self.last_forward_metadata = metadata
             return delta_weight * cfg.adapter_scale
         ctx = torch.autocast(device_type="cuda", enabled=False) if self.weight.is_cuda else _null()
@@ -287,9 +288,10 @@ class GaussianFieldBatch:
 
     A layer whose forward does not run in the step contributes a zero dL/d(delta-W).  The
     rendered delta-W tensors are the plan's own buffers: they hold until the next render().
-    The forward reads back every layer's status and pair count once (one host synchronisation
-    per step, where the reference synchronises per layer); a pair count past a layer's id
-    capacity grows the capacities and renders again.  All layers must share the tile shape
+    The forward reads back every layer's status, pair count and ||delta-W|| (the layer's
+    ``delta_w_norm`` metadata) at once: one host synchronisation per step, where the reference
+    synchronises per layer (gaussian_linear.py:218).  A pair count past a layer's id capacity
+    grows the capacities and renders again.  All layers must share the tile shape
     (16x16 or 32x32: the batched kernels), sigma multiplier and normalisation.
 
     Densification (the reference trainer's clone / prune, base_trainer.py:126-220) replaces a
@@ -396,8 +398,8 @@ class GaussianFieldBatch:
             for ly in self.layers:
                 params += [ly.mu_raw, ly.chol_raw, ly.amp]
             deltas = _BatchedFieldFunction.apply(self, *params)
-        for ly, d in zip(self.layers, deltas):
-            ly._batched_delta = d
+        for ly, d, nrm in zip(self.layers, deltas, self._norms):
+            ly._batched_delta = (d, nrm)
         return list(deltas)
 
     def _run_forward(self) -> list[Tensor]:
@@ -406,7 +408,7 @@ class GaussianFieldBatch:
             self._build()
         for _ in range(8):
             self._plan.forward()
-            status, pairs = self._plan.read(clear=True)
+            status, pairs, self._norms = self._plan.read(clear=True, norms=True)
             over = [i for i, st in enumerate(status) if st & Nat.GF_STATUS_CAPACITY]
             bad = [(i, st) for i, st in enumerate(status) if st & ~Nat.GF_STATUS_CAPACITY]
             if bad:

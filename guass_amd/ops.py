@@ -297,15 +297,18 @@ class FieldBatchPlan:
                                            self._stream()), "gf_batch_set_grads")
         self._grads = grads
 
-    def read(self, clear: bool = False) -> tuple[list[int], list[int]]:
-        """(GF_STATUS_* bits, pair count) of every layer's last pass, in one read-back
+    def read(self, clear: bool = False, norms: bool = False):
+        """(GF_STATUS_* bits, pair count) of every layer's last pass -- plus, with ``norms``, the
+        Frobenius norm of every layer's delta-W from the last forward -- in one read-back
         (synchronises)."""
         n = len(self.plans)
         st = (ctypes.c_uint32 * max(n, 1))()
         pairs = (ctypes.c_int64 * max(n, 1))()
+        nrm = (ctypes.c_double * max(n, 1))()
         N.check(N.lib().gf_batch_read(self.plan.data_ptr(), ctypes.byref(self.info), 1 if clear else 0, st,
-                                      pairs, self._stream()), "gf_batch_read")
-        return [int(st[i]) for i in range(n)], [int(pairs[i]) for i in range(n)]
+                                      pairs, nrm if norms else None, self._stream()), "gf_batch_read")
+        out = ([int(st[i]) for i in range(n)], [int(pairs[i]) for i in range(n)])
+        return out + ([float(nrm[i]) for i in range(n)],) if norms else out
 
     def status(self) -> list[int]:
         """Forward | backward GF_STATUS_* bits per layer (synchronises)."""

@@ -251,12 +251,15 @@ int gf_batch_backward(const void* plan, const gf_batch_info* info, uint32_t phas
 int gf_batch_set_grads(void* plan, gf_batch_info* info, const float* const* grad_delta, void* stream);
 
 /*
- * Per layer of a batch plan: the forward | backward GF_STATUS_* bits (status_host) and the pair
- * count of the last forward (pairs_host), either may be NULL; clear != 0 resets the status
+ * Per layer of a batch plan: the forward | backward GF_STATUS_* bits (status_host), the pair
+ * count of the last forward (pairs_host) and the Frobenius norm of its delta-W
+ * (delta_norm_host, from per-block sums of squares the batched render leaves in the forward
+ * workspace, added in double in a fixed order; the reference reads it per layer with a
+ * blocking .item(), gaussian_linear.py:218); any may be NULL; clear != 0 resets the status
  * words.  One small kernel and one device-to-host copy; synchronises `stream`.
  */
 int gf_batch_read(void* plan, const gf_batch_info* info, int32_t clear, uint32_t* status_host,
-                  int64_t* pairs_host, void* stream);
+                  int64_t* pairs_host, double* delta_norm_host, void* stream);
 
 /*
  * Allocation-free gf_backward.  No counterpart in the reference (whose backward allocates its

@@ -739,6 +739,55 @@ def test_gaussian_field_batch_against_oracle(device):
             grad_close(got, want, name)
 
 
+def test_batched_step_reads_back_once(device, monkeypatch):
+    """A training step through GaussianFieldBatch -- render(), every layer's forward, autograd's
+    backward -- makes one host read-back (FieldBatchPlan.read, which returns every layer's
+    status, pair count and ||delta-W||) and no synchronising torch call (CUDA sync debug mode
+    "error"); the reference synchronises per layer for delta_w_norm (gaussian_linear.py:218).
+    Each layer's delta_w_norm metadata equals the norm of its delta-W to 1e-6."""
+    from guass_amd.layers import GaussianFieldBatch
+    from guass_amd.ops import FieldBatchPlan
+
+    probs = [wl.cfg2(1), wl.cfg1(2), _cfg4_layer(16)]
+    layers = _layers_from_problems(probs, device)
+    fb = GaussianFieldBatch(layers)
+    gen = torch.Generator(device=device).manual_seed(4)
+    xs = [torch.randn(9, p.in_features, device=device, generator=gen) for p in probs]
+    gys = [torch.randn(9, p.out_features, device=device, generator=gen) for p in probs]
+
+    def step():
+        fb.render()
+        torch.autograd.backward([ly(x) for ly, x in zip(layers, xs)], gys)
+
+    step()  # plans (uploading the plan synchronises)
+    torch.cuda.synchronize()
+    reads = []
+    real_read = FieldBatchPlan.read
+
+    def counting_read(self, *a, **kw):
+        reads.append(kw)
+        return real_read(self, *a, **kw)
+
+    monkeypatch.setattr(FieldBatchPlan, "read", counting_read)
+    for ly in layers:
+        for t in (ly.mu_raw, ly.chol_raw, ly.amp):
+            t.grad = None
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        step()
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    torch.cuda.synchronize()
+    say(f"  one step: {len(reads)} read-back(s)")
+    assert len(reads) == 1
+    for i, (ly, pl) in enumerate(zip(layers, fb._plan.plans)):
+        meta = ly.last_forward_metadata
+        assert meta["accumulate_backend"] == "batched_fields"
+        want = float(pl.delta.double().norm())
+        assert abs(meta["delta_w_norm"] - want) <= 1e-6 * want, (i, meta["delta_w_norm"], want)
+        assert ly.amp.grad is not None and float(ly.amp.grad.abs().max()) > 0.0
+
+
 def test_gaussian_field_reference_entry(device):
     """The validation entry gaussian_field_reference (runtime.py:236-270) with
     allow_reference_backward=True and the extension's gaussian_field_backward_reference
@@ -896,6 +945,9 @@ def test_gaussian_field_batch_matches_per_layer(device, tile):
         torch.cuda.synchronize()
         for i in used:
             assert layers_b[i].last_forward_metadata["accumulate_backend"] == "batched_fields"
+            na = layers_a[i].last_forward_metadata["delta_w_norm"]  # torch's norm().item()
+            nb = layers_b[i].last_forward_metadata["delta_w_norm"]  # the batch's read-back
+            assert abs(nb - na) <= 1e-6 * na, (step, i, na, nb)
             with torch.no_grad():
                 ya = layers_a[i](xs[i])
             assert torch.equal(outs_b[i].detach(), ya), f"step {step} layer {i}: output"
