@@ -30,7 +30,7 @@ EXPORTED = (
     "gf_forward_workspace_bytes_max", "gf_backward_workspace_bytes", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
     "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
     "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward",
-    "gf_batch_set_grads", "gf_batch_read", "gf_backward_noalloc",
+    "gf_batch_set_grads", "gf_batch_read", "gf_backward_noalloc", "gf_forward",
 )
 
 GF_PHASE_BIN, GF_PHASE_EMIT, GF_PHASE_RENDER = 0x1, 0x2, 0x4
@@ -111,6 +111,8 @@ def lib() -> ctypes.CDLL:
                                   c_size_t, _P]
     L.gf_forward_render.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P,
                                     c_int64, _P, _P, c_size_t, _P]
+    L.gf_forward.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, _P, _P,
+                             c_size_t, _P]
     L.gf_backward.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int32,
                               _P, c_int32, c_int64, _P, _P, _P, _P, _P, c_size_t, _P]
     L.gf_backward_reduce.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int32,
@@ -129,7 +131,7 @@ def lib() -> ctypes.CDLL:
     for name in ("gf_tile_grid", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
                  "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
                  "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward",
-                 "gf_batch_set_grads", "gf_batch_read", "gf_backward_noalloc"):
+                 "gf_batch_set_grads", "gf_batch_read", "gf_backward_noalloc", "gf_forward"):
         getattr(L, name).restype = c_int
     _LIB = L
     return L

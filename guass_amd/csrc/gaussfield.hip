@@ -2733,6 +2733,20 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
   return GF_OK;
 }
 
+int gf_forward(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+               const float* row_coords, const float* col_coords, const float* mu, const float* chol_raw,
+               const float* amp, int64_t* tile_ptr, int64_t* num_pairs_dev, int64_t* gaussian_ids_sorted,
+               int64_t ids_capacity, float* delta, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = gf_forward_bin(cfg, out_features, in_features, k, mu, chol_raw, amp, tile_ptr, num_pairs_dev, nullptr,
+                          workspace, workspace_bytes, stream);
+  if (rc) return rc;
+  rc = gf_forward_emit(cfg, out_features, in_features, k, mu, amp, tile_ptr, gaussian_ids_sorted, ids_capacity,
+                       workspace, workspace_bytes, stream);
+  if (rc) return rc;
+  return gf_forward_render(cfg, out_features, in_features, k, row_coords, col_coords, tile_ptr,
+                           gaussian_ids_sorted, ids_capacity, delta, workspace, workspace_bytes, stream);
+}
+
 int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                        const float* grad_delta, const float* row_coords, const float* col_coords,
                        const float* mu, const float* chol_raw, const void* tile_ptr,

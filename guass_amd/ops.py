@@ -122,7 +122,17 @@ class FieldPlan:
         return self.delta
 
     def forward(self, row_coords, col_coords, mu, chol_raw, amp) -> torch.Tensor:
-        """Bins and renders into ``self.delta`` (and ``tile_ptr`` / ``ids``); returns delta."""
+        """Bins and renders into ``self.delta`` (and ``tile_ptr`` / ``ids``); returns delta.
+        One call (gf_forward) running the three phases."""
+        N.check(N.lib().gf_forward(ctypes.byref(self.cfg), self.M, self.N, self.K, row_coords.data_ptr(),
+                                   col_coords.data_ptr(), N.ptr(mu), N.ptr(chol_raw), N.ptr(amp),
+                                   self.tile_ptr.data_ptr(), self.num_pairs.data_ptr(), self.ids.data_ptr(),
+                                   self.capacity, self.delta.data_ptr(), self.fwd_ws.data_ptr(),
+                                   self.fwd_ws_bytes, self._stream()), "gf_forward")
+        return self.delta
+
+    def forward_phases(self, row_coords, col_coords, mu, chol_raw, amp) -> torch.Tensor:
+        """The forward as its three phases (bin, emit, render): the same outputs as forward()."""
         self.bin(mu, chol_raw, amp)
         self.emit(mu, amp)
         return self.render(row_coords, col_coords)

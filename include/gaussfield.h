@@ -127,6 +127,18 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
                       float* delta, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * The whole forward in one call, without a host synchronisation: gf_forward_bin +
+ * gf_forward_emit + gf_forward_render into a gaussian-id buffer of fixed capacity (pairs past it
+ * are dropped and GF_STATUS_CAPACITY is set; P goes to num_pairs_dev), for callers that keep
+ * their buffers, e.g. under HIP graph capture.  Replaces reference field_impl.cu:135-163
+ * (gaussian_field_forward, which reads P back to size its id buffer).
+ */
+int gf_forward(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+               const float* row_coords, const float* col_coords, const float* mu, const float* chol_raw,
+               const float* amp, int64_t* tile_ptr, int64_t* num_pairs_dev, int64_t* gaussian_ids_sorted,
+               int64_t ids_capacity, float* delta, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Backward: reduces dL/d(delta) into per-Gaussian gradients through the saved binning.
  * gf_backward = gf_backward_reduce (per-tile moments, atomics into the workspace) followed by
  * gf_backward_finish (chain rule, clears the workspace accumulators).

@@ -490,6 +490,88 @@ def test_plan_sync_free_and_capacity(device):
     assert small.status() & _native.GF_STATUS_CAPACITY
 
 
+def _random_forward_problem(i: int):
+    """Seeded 16x16-tile fields with 1 <= K <= 1024, most below 8 pairs per tile: ragged sizes,
+    sub-pixel to whole-matrix Gaussians, indefinite covariances, normalisation, clamps, sigma."""
+    g = torch.Generator().manual_seed(1000 + i)
+    K = [1, 2, 63, 64, 65, 255, 256, 257, 511, 700, 1023, 1024][i % 12]
+    lo, hi = (1, 300) if K <= 256 else (250, 720)  # more Gaussians on larger fields: < 8 pairs a tile
+    M = int(torch.randint(lo, hi, (1,), generator=g))
+    N = int(torch.randint(lo, hi, (1,), generator=g))
+    log_px = float(torch.empty(1).uniform_(-1.0, 2.5, generator=g))
+    spread = float(torch.empty(1).uniform_(0.0, 1.2, generator=g))
+    p = wl.make_problem(f"rand_fwd_{i}_{M}x{N}_k{K}", M, N, K, log_px, spread, 2000 + i)
+    if i % 5 == 3:  # elongated Gaussians whose fp32 covariance is indefinite
+        nb = min(K, 3)
+        bad = _indefinite_problem(max(M, 2), max(N, 2), 3000 + i, n_normal=1, n_bad=nb)
+        p.chol_raw[:nb] = bad.chol_raw[1:]
+    if i % 7 == 2:  # a few Gaussians covering the whole matrix
+        p.chol_raw[: min(K, 5), 0] = 4.0
+        p.chol_raw[: min(K, 5), 2] = 4.0
+    cfg = dict(sigma=[3.0, 2.5, 1.5, 3.5][i % 4], normalize=i % 6 == 5, clamp=[80.0, 24.0, None, 200.0][i % 4])
+    return p, cfg
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_gf_forward_random_fields(device, i):
+    """FieldPlan.forward (the one-call gf_forward) against the float64 evaluation and, bit for
+    bit, against the forward called phase by phase (gf_forward_bin / _emit / _render): tile_ptr,
+    ids, delta-W, the constants the backward reads, and the backward's gradients; then an id
+    capacity below the pair count."""
+    p, cfg = _random_forward_problem(i)
+    r = fo.gaussian_field_fwd_bwd_batched(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad, 16, 16,
+                                          cfg["sigma"], cfg["normalize"], cfg["clamp"])
+    P = int(r[1][-1])
+    T = (-(-p.out_features // 16)) * (-(-p.in_features // 16))
+    cap = max(P, 1)
+    say(f"{p.name} P={P} T={T} {cfg}")
+    q = p.to(device)
+    kw = dict(sigma_multiplier=cfg["sigma"], normalize=cfg["normalize"], clamp_quad=cfg["clamp"])
+    one = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=cap, **kw)
+    phased = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=cap, **kw)
+    one.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+    phased.forward_phases(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+    gf = [t.clone() for t in one.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)]
+    gp = [t.clone() for t in phased.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
+                                             num_pairs=P)]
+    torch.cuda.synchronize()
+    assert one.status() == 0 and one.pairs() == P
+    binning_equal(one.tile_ptr, one.ids[:P], r[1], r[2])
+    assert torch.equal(one.tile_ptr, phased.tile_ptr) and torch.equal(one.ids[:P], phased.ids[:P])
+    assert torch.equal(one.delta, phased.delta), "delta-W differs from the three-phase forward"
+    n = 8 * p.k  # the constants the backward reads: eval[K] (32 B each) in both workspaces
+    assert torch.equal(one.fwd_ws[256:256 + 4 * n], phased.fwd_ws[256:256 + 4 * n])
+    # Random sizes and spreads give covariance condition numbers in the thousands, where no two
+    # fp32 evaluation orders agree to 1e-5 (the fp32 oracle is itself up to 1.6e-5 from the
+    # float64 evaluation); the yardstick is float64: at least as close to it as the oracle.
+    r64 = fo.gaussian_field_fwd_bwd_fp64(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad, 16, 16,
+                                         cfg["sigma"], cfg["normalize"], cfg["clamp"])
+    finite = torch.isfinite(r64[0])
+    assert torch.equal(torch.isfinite(one.delta.cpu()), finite)  # NaN: normalised indefinite Gaussians
+    if bool(finite.any()):
+        scale = max(float(r64[0][finite].abs().max()), 1e-30)
+        err_g = float((one.delta.cpu().double() - r64[0])[finite].abs().max()) / scale
+        err_o = float((r[0].double() - r64[0])[finite].abs().max()) / scale
+        assert err_g <= err_o + 1e-5, (err_g, err_o)
+    for name, a, b, c, o in zip(("d_mu", "d_chol_raw", "d_amp"), gf, gp, r64[3:], r[3:]):
+        fin = torch.isfinite(c)
+        if not bool(fin.all()):
+            continue
+        grad_close(a, b, f"{name} vs three-phase", rtol=1e-5)
+        cn = float(c.norm())
+        if cn > 0.0:
+            eg = float((a.cpu().double() - c).norm()) / cn
+            eo = float((o.double() - c).norm()) / cn
+            assert eg <= eo + 1e-4, (name, eg, eo)
+    if P > 1:  # an id capacity below the pair count: ids truncated, the rest unchanged
+        small = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=P // 2, **kw)
+        small.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+        torch.cuda.synchronize()
+        assert small.status() & _native.GF_STATUS_CAPACITY and small.pairs() == P
+        assert torch.equal(small.tile_ptr, one.tile_ptr) and torch.equal(small.delta, one.delta)
+        assert torch.equal(small.ids[:P // 2], one.ids[:P // 2])
+
+
 def test_backward_stripes(device):
     """Tile grids of >= 8192 tiles spread each Gaussian's accumulators over 4 stripes (>= 16384:
     16): a 1280x1792 field (8960 tiles) against the oracle, alone and as a batch layer next to a
