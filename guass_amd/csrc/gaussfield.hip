@@ -375,6 +375,18 @@ __device__ inline float dpp_f32(float v) {
   return __int_as_float(dpp_i32<CTRL, 0xf>(__float_as_int(v)));
 }
 
+// Inclusive scan over the 64 lanes in fp32 (the order of dpp_scan_i32): lane 63 holds the
+// wave's sum, in a fixed order.
+__device__ inline float dpp_scan_f32(float v) {
+  v += __int_as_float(dpp_i32<0x111, 0xf>(__float_as_int(v)));
+  v += __int_as_float(dpp_i32<0x112, 0xf>(__float_as_int(v)));
+  v += __int_as_float(dpp_i32<0x114, 0xf>(__float_as_int(v)));
+  v += __int_as_float(dpp_i32<0x118, 0xf>(__float_as_int(v)));
+  v += __int_as_float(dpp_i32<0x142, 0xa>(__float_as_int(v)));
+  v += __int_as_float(dpp_i32<0x143, 0xc>(__float_as_int(v)));
+  return v;
+}
+
 // Sum over each row of 16 lanes, left in lane 15 of the row (other lanes hold partial sums).
 __device__ inline float dpp_row_sum_f32(float v) {
   v += __int_as_float(dpp_i32<0x111, 0xf>(__float_as_int(v)));
@@ -1390,6 +1402,21 @@ __device__ __forceinline__ void render16_body(
     for (int i = 0; i < 4; ++i) yd[i] = y[i] - y0;
   }
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  // With clamp_quad >= 80 (or none) the clamp only floors positive-definite bases below e^-40:
+  // the third loop of run_chunk leaves them at their value, a difference below e^-40 |amp| per
+  // Gaussian and pixel, and saves the v_med3 of every pixel.
+  const bool floor_free = !p.mask_clamp;
+  auto accumulate_free = [&](const GaussEval& u) {
+    const float dx = x - u.mu0;
+    const float a = u.wa * dx;
+    const float z0 = fmaf(u.wc, y0 - u.mu1, u.wb * dx);
+    const float A = a * a;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float z = i == 0 ? z0 : fmaf(u.wc, yd[i], z0);
+      acc[i] = fmaf(u.w, __builtin_amdgcn_exp2f(-fmaf(z, z, A)), acc[i]);
+    }
+  };
   auto accumulate = [&](const GaussEval& u, auto general) {
     const float dx = x - u.mu0;
     const float a = u.wa * dx;
@@ -1434,7 +1461,10 @@ __device__ __forceinline__ void render16_body(
       return u;
     };
     if (__builtin_amdgcn_ballot_w64(lane < nj && my.gen != 0.0f) == 0) {
-      for (int j = 0; j < nj; ++j) accumulate(at(j), std::false_type{});
+      if (floor_free)
+        for (int j = 0; j < nj; ++j) accumulate_free(at(j));
+      else
+        for (int j = 0; j < nj; ++j) accumulate(at(j), std::false_type{});
     } else {
       for (int j = 0; j < nj; ++j) accumulate(at(j), std::true_type{});
     }
@@ -1611,9 +1641,8 @@ __device__ __forceinline__ void render16_body(
       for (int i = 0; i < 4; ++i)
         if (pc + i < p.N) sq = fmaf(acc[i], acc[i], sq);
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
-    if (lane == 0) blk_sq[st.sidx] = sq;
+    sq = dpp_scan_f32(sq);
+    if (lane == 63) blk_sq[st.sidx] = sq;
   }
   if (pr < p.M) {
     float* out = delta + (int64_t)pr * p.N + pc;
