@@ -1395,8 +1395,16 @@ __device__ __forceinline__ void render16_body(
   float y0, yd[4];
   {
     float y[4];
+    if (pc + 3 < p.N && ((reinterpret_cast<uintptr_t>(col_coords + pc) & 15) == 0)) {
+      const float4 v = *reinterpret_cast<const float4*>(col_coords + pc);
+      y[0] = v.x;
+      y[1] = v.y;
+      y[2] = v.z;
+      y[3] = v.w;
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) y[i] = col_coords[min(pc + i, p.N - 1)];
+      for (int i = 0; i < 4; ++i) y[i] = col_coords[min(pc + i, p.N - 1)];
+    }
     y0 = y[0];
 #pragma unroll
     for (int i = 0; i < 4; ++i) yd[i] = y[i] - y0;
@@ -1816,8 +1824,21 @@ __device__ __forceinline__ void bwd16_body(
 #pragma unroll
     for (int c = 0; c < 16; ++c) gv[c] = (pr < p.M && c0 + c < p.N) ? grow[c] : 0.0f;
   }
+  // (the same 16 addresses in every lane: inside the matrix, four aligned float4 from one base)
+  if (c0 + 15 < p.N && ((reinterpret_cast<uintptr_t>(col_coords + c0) & 15) == 0)) {
+    const float4* yq = reinterpret_cast<const float4*>(col_coords + c0);
 #pragma unroll
-  for (int c = 0; c < 16; ++c) yv[c] = col_coords[min(c0 + c, p.N - 1)];
+    for (int c = 0; c < 4; ++c) {
+      const float4 v = yq[c];
+      yv[4 * c] = v.x;
+      yv[4 * c + 1] = v.y;
+      yv[4 * c + 2] = v.z;
+      yv[4 * c + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) yv[c] = col_coords[min(c0 + c, p.N - 1)];
+  }
   const float x = row_coords[min(pr, p.M - 1)];
   int64_t s = (int64_t)tile_ptr[t], e = (int64_t)tile_ptr[t + 1];
   if (lane == 0) {
