@@ -72,7 +72,7 @@ class GfBatchInfo(ctypes.Structure):
     _fields_ = [
         ("n_layers", c_int32), ("has_backward", c_int32), ("tile_blocks", c_int64),
         ("emit_blocks", c_int64), ("finish_blocks", c_int64), ("plan_bytes", c_size_t),
-        ("backward_buffers", c_int32), ("mask_clamp", c_int32),
+        ("backward_buffers", c_int32), ("mask_clamp", c_int32), ("render_blocks", c_int64),
     ]
 
 

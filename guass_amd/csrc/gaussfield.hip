@@ -328,11 +328,38 @@ __device__ inline int64_t readlane_i64(int64_t v, int lane) {
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-// Orders the memory operations of one wave (its lanes exchange data through LDS / global).
+// Orders the memory operations of one wave whose lanes exchange data through LDS: release /
+// acquire fences at wavefront scope (the LDS performs one wave's operations in issue order, so
+// they cost no wait instruction; rocPRIM's wave_barrier is the same) and a wave barrier that
+// keeps the compiler from moving code across.
 __device__ inline void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The same where lanes exchange data through global memory (rare paths): a workgroup-scope
+// fence, which waits for the wave's outstanding memory operations.
+__device__ inline void wave_sync_global() {
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   __builtin_amdgcn_wave_barrier();
 }
+
+// Streaming access to delta-W (written once by the render) and dL/d(delta-W) (read once by the
+// backward): the nontemporal hint keeps those bytes from evicting the L2 lines the tile kernels
+// reuse (masks, Gaussian constants, coordinates, accumulators).
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ inline void store4_stream(float* q, float a, float b, float c, float d) {
+  const f32x4_t v = {a, b, c, d};
+  __builtin_nontemporal_store(v, reinterpret_cast<f32x4_t*>(q));
+}
+__device__ inline void store_stream(float* q, float v) { __builtin_nontemporal_store(v, q); }
+__device__ inline float4 load4_stream(const float* q) {
+  const f32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(q));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ inline float load_stream(const float* q) { return __builtin_nontemporal_load(q); }
+
 
 // ------------------------------------------------------------------------------------------
 // DPP wave primitives (gfx9 row_shr / row_bcast; no LDS traffic).
@@ -1249,7 +1276,7 @@ __device__ void order_segment_wave(int64_t* seg, int64_t n, int64_t K, int32_t* 
         ++pos;
       }
     }
-    wave_sync();
+    wave_sync_global();  // the caller reads seg
     return;
   }
   // In place in global memory (segments longer than kWaveSortKeys with K > 16384).
@@ -1268,7 +1295,7 @@ __device__ void order_segment_wave(int64_t* seg, int64_t n, int64_t K, int32_t* 
           }
         }
       }
-      wave_sync();
+      wave_sync_global();
     }
   }
 }
@@ -1442,7 +1469,10 @@ __device__ __forceinline__ void render16_body(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float z = i == 0 ? z0 : fmaf(u.wc, yd[i], z0);
-      acc[i] = fmaf(u.w, basis_w(p, A, z), acc[i]);
+      // definite forms as in accumulate_free whenever the floor is dropped, so that a pixel's
+      // value does not depend on which loop its chunk took
+      const float e = floor_free ? __builtin_amdgcn_exp2f(-fmaf(z, z, A)) : basis_w(p, A, z);
+      acc[i] = fmaf(u.w, e, acc[i]);
     }
   };
   // Gaussians 0 .. nj-1 of a chunk (lane j holds Gaussian j), staged in the wave's LDS and
@@ -1452,11 +1482,12 @@ __device__ __forceinline__ void render16_body(
   auto& wevals = r16_wevals;
   float4* ew = wevals[wid];
   auto run_chunk = [&](const GaussEval& my, int nj) {
-    ew[2 * lane] = make_float4(my.mu0, my.mu1, my.wa, my.wb);
-    ew[2 * lane + 1] = make_float4(my.wc, my.w, __int_as_float(my.gid), my.gen);
+    // two arrays of 64 float4 (conflict-free writes, broadcast reads)
+    ew[lane] = make_float4(my.mu0, my.mu1, my.wa, my.wb);
+    ew[64 + lane] = make_float4(my.wc, my.w, __int_as_float(my.gid), my.gen);
     wave_sync();
     auto at = [&](int j) {
-      const float4 a = ew[2 * j], b = ew[2 * j + 1];
+      const float4 a = ew[j], b = ew[64 + j];
       GaussEval u;
       u.mu0 = a.x;
       u.mu1 = a.y;
@@ -1655,11 +1686,215 @@ __device__ __forceinline__ void render16_body(
   if (pr < p.M) {
     float* out = delta + (int64_t)pr * p.N + pc;
     if (pc + 3 < p.N && ((reinterpret_cast<uintptr_t>(out) & 15) == 0)) {
-      *reinterpret_cast<float4*>(out) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      store4_stream(out, acc[0], acc[1], acc[2], acc[3]);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (pc + i < p.N) out[i] = acc[i];
+        if (pc + i < p.N) store_stream(out + i, acc[i]);
+    }
+  }
+}
+
+// Two horizontally adjacent 16x16 tiles of one field by one wave, on the mask path (p.W > 0):
+// tiles (tr, tc) and (tr, tc + 1), the second absent when tc + 1 == p.C.  Lane l covers tile row
+// l/4, columns 4*(l%4)..+3 of both tiles.  The wave expands the union of the two tiles' mask
+// bits once and stages each Gaussian of the union once, with a zero amplitude for a tile that
+// does not list it: for a definite form the basis is finite, so fma(0, e, acc) == acc exactly,
+// and indefinite forms are skipped per tile.  Every pixel thus sums its own tile's Gaussians in
+// ascending id order with the arithmetic of render16_body, bit for bit, while the per-tile
+// work (mask loads, scans, gathers, waits) is shared by twice the pixels.  Each tile's ids are
+// written to its own segment chunk by chunk.
+constexpr int32_t kPairInA = 1 << 14, kPairInB = 1 << 15, kPairIdMask = kPairInA - 1;  // ids < kMaskMaxK
+static_assert(kMaskMaxK <= kPairInA, "pair keys hold the id below the tile flags");
+
+__device__ __forceinline__ void render16x2_body(
+    const Problem& p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
+    const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* __restrict__ ids,
+    int64_t capacity, float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
+    const uint32_t* __restrict__ colmask, int32_t tr, int32_t tc, float* __restrict__ blk_sq) {
+  WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
+  const bool has_b = tc + 1 < p.C;
+  const int64_t ta = (int64_t)tr * p.C + tc;
+  const int32_t pr = tr * 16 + (lane >> 2);
+  const int32_t pc0 = tc * 16 + ((lane & 3) << 2);
+  const float x = row_coords[min(pr, p.M - 1)];
+  float y0[2], yd[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int32_t pc = pc0 + 16 * h;
+    float y[4];
+    if (pc + 3 < p.N && ((reinterpret_cast<uintptr_t>(col_coords + pc) & 15) == 0)) {
+      const float4 v = *reinterpret_cast<const float4*>(col_coords + pc);
+      y[0] = v.x;
+      y[1] = v.y;
+      y[2] = v.z;
+      y[3] = v.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] = col_coords[min(pc + i, p.N - 1)];
+    }
+    y0[h] = y[0];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) yd[h][i] = y[i] - y[0];
+  }
+  float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  const bool floor_free = !p.mask_clamp;
+  // The two segments are adjacent: [sa, sb) and [sb, se).
+  const int64_t sa = tile_ptr[ta], sb = tile_ptr[ta + 1], se = has_b ? tile_ptr[ta + 2] : sb;
+  const int64_t cnt_a = sb - sa, cnt_b = se - sb;
+  auto room_of = [&](int64_t s, int64_t count) {
+    return capacity - s < count ? (capacity - s > 0 ? capacity - s : 0) : count;
+  };
+  const int64_t room_a = room_of(sa, cnt_a), room_b = room_of(sb, cnt_b);
+  const uint32_t* rm = rowmask + (int64_t)tr * p.W;
+  const uint32_t* cma = colmask + (int64_t)tc * p.W;
+  const uint32_t* cmb = cma + p.W;  // read only when has_b
+  int32_t* keys = r16_wkeys[wid];
+  float4* ew = r16_wevals[wid];
+
+  // One chunk of nj <= 64 union Gaussians (key kf in lane j < nj): each tile's ids go to its
+  // segment at the lane's rank among the chunk's keys of that tile; lane j stages Gaussian j
+  // (constants, each tile's amplitude, flags: 1 tile A, 2 tile B, 4 indefinite form) and every
+  // lane adds its 8 pixels.
+  int32_t done_a = 0, done_b = 0;  // ids of each tile so far (< K)
+  auto run_chunk = [&](int32_t kf, int nj) {
+    const bool in_a = lane < nj && (kf & kPairInA) != 0, in_b = lane < nj && (kf & kPairInB) != 0;
+    const uint64_t bal_a = __builtin_amdgcn_ballot_w64(in_a), bal_b = __builtin_amdgcn_ballot_w64(in_b);
+    const int32_t id = kf & kPairIdMask;
+    if (in_a) {
+      const int32_t r = done_a + (int32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal_a >> 32),
+                                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)bal_a, 0u));
+      if (r < room_a) ids[sa + r] = id;
+    }
+    if (in_b) {
+      const int32_t r = done_b + (int32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal_b >> 32),
+                                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)bal_b, 0u));
+      if (r < room_b) ids[sb + r] = id;
+    }
+    done_a += __popcll(bal_a);
+    done_b += __popcll(bal_b);
+    GaussEval my = zero_eval();
+    if (lane < nj) my = load_eval(ev, id);
+    const int32_t fl = (in_a ? 1 : 0) | (in_b ? 2 : 0) | (my.gen != 0.0f ? 4 : 0);
+    // two arrays of 64 float4 (conflict-free writes, broadcast reads)
+    ew[lane] = make_float4(my.mu0, my.mu1, my.wa, my.wb);
+    ew[64 + lane] = make_float4(my.wc, in_a ? my.w : 0.0f, in_b ? my.w : 0.0f, __int_as_float(fl));
+    const bool general = __builtin_amdgcn_ballot_w64((fl & 4) != 0) != 0;
+    wave_sync();
+    auto definite = [&](const float4& a, const float4& b, auto free_form) {
+      const float dx = x - a.x;
+      const float aa = a.z * dx;
+      const float bb = a.w * dx;
+      const float A = aa * aa;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float wh = h == 0 ? b.y : b.z;
+        const float z0 = fmaf(b.x, y0[h] - a.y, bb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float z = i == 0 ? z0 : fmaf(b.x, yd[h][i], z0);
+          const float e = free_form ? __builtin_amdgcn_exp2f(-fmaf(z, z, A)) : basis_w(p, A, z);
+          acc[h][i] = fmaf(wh, e, acc[h][i]);
+        }
+      }
+    };
+    if (!general) {
+      if (floor_free)
+        for (int j = 0; j < nj; ++j) definite(ew[j], ew[64 + j], std::true_type{});
+      else
+        for (int j = 0; j < nj; ++j) definite(ew[j], ew[64 + j], std::false_type{});
+    } else {
+      for (int j = 0; j < nj; ++j) {
+        const float4 a = ew[j], b = ew[64 + j];
+        const int32_t f = __builtin_amdgcn_readfirstlane(__float_as_int(b.w));
+        if ((f & 4) == 0) {
+          if (floor_free)
+            definite(a, b, std::true_type{});
+          else
+            definite(a, b, std::false_type{});
+          continue;
+        }
+        // indefinite form (q' = z^2 - a^2), only on the tiles that list it
+        const float dx = x - a.x;
+        const float aa = a.z * dx;
+        const float nA = -(aa * aa);
+        const float bb = a.w * dx;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if ((f & (1 << h)) == 0) continue;
+          const float wh = h == 0 ? b.y : b.z;
+          const float z0 = fmaf(b.x, y0[h] - a.y, bb);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float z = i == 0 ? z0 : fmaf(b.x, yd[h][i], z0);
+            acc[h][i] = fmaf(wh, basis_q(p, fmaf(z, z, nA)), acc[h][i]);
+          }
+        }
+      }
+    }
+    wave_sync();  // every lane has read the slots before the next chunk rewrites them
+  };
+
+  for (int32_t w0 = 0; w0 < p.W; w0 += 64) {
+    const int32_t w = w0 + lane;
+    uint32_t ma = 0u, mb = 0u;
+    if (w < p.W) {
+      const uint32_t r = rm[w];
+      ma = r & cma[w];
+      if (has_b) mb = r & cmb[w];
+    }
+    const uint32_t u = ma | mb;
+    const int32_t cu = __popc(u);
+    const int32_t inc_u = dpp_scan_i32(cu);
+    const int32_t tot_u = __builtin_amdgcn_readlane(inc_u, 63);
+    for (int32_t base = 0; base < tot_u; base += kWaveSortKeys) {
+      uint32_t mm = u;
+      int32_t pos = inc_u - cu;
+      while (mm != 0u && pos < base + kWaveSortKeys) {
+        const int32_t bit = __builtin_ctz(mm);
+        mm &= mm - 1u;
+        if (pos >= base)
+          keys[pos - base] = ((w << 5) + bit) | (int32_t)(((ma >> bit) & 1u) << 14) | (int32_t)(((mb >> bit) & 1u) << 15);
+        ++pos;
+      }
+      wave_sync();
+      const int32_t nwin = min(kWaveSortKeys, tot_u - base);
+      for (int32_t j0 = 0; j0 < nwin; j0 += 64) {
+        const int nj = min(64, nwin - j0);
+        run_chunk(lane < nj ? keys[j0 + lane] : 0, nj);
+      }
+      wave_sync();
+    }
+  }
+  if (lane == 0) {
+    if (done_a != cnt_a || done_b != cnt_b) set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);
+    if (room_a < cnt_a || room_b < cnt_b) set_status(&hdr->status, GF_STATUS_CAPACITY);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (h == 1 && !has_b) break;
+    const int32_t pc = pc0 + 16 * h;
+    if (blk_sq) {  // as in render16_body
+      float sq = 0.f;
+      if (pr < p.M) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (pc + i < p.N) sq = fmaf(acc[h][i], acc[h][i], sq);
+      }
+      sq = dpp_scan_f32(sq);
+      if (lane == 63) blk_sq[ta + h] = sq;
+    }
+    if (pr < p.M) {
+      float* out = delta + (int64_t)pr * p.N + pc;
+      if (pc + 3 < p.N && ((reinterpret_cast<uintptr_t>(out) & 15) == 0)) {
+        store4_stream(out, acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (pc + i < p.N) store_stream(out + i, acc[h][i]);
+      }
     }
   }
 }
@@ -1729,7 +1964,7 @@ __global__ __launch_bounds__(kTileThreads) void k_render_any(
         acc = fmaf(v.w, basis_q(p, quad_form(v, x - v.mu0, y - v.mu1)), acc);
       }
     }
-    if (have) delta[(int64_t)r * p.N + c] = acc;
+    if (have) store_stream(delta + (int64_t)r * p.N + c, acc);
   }
 }
 
@@ -1808,21 +2043,38 @@ __device__ __forceinline__ void bwd16_body(
   const int slot = lane >> 4, row = lane & 15;
   const int32_t pr = r0 + row;
   // This lane's row of dL/d(delta) (0 outside the matrix) and the tile's coordinates are
-  // requested before the segment bounds, on which they do not depend.
+  // requested before the segment bounds, on which they do not depend.  The wave reads the 16x16
+  // block of dL/d(delta) once, a float4 per lane with the nontemporal hint (the bytes are read
+  // once, and keeping them out of L2 keeps the accumulator and constant lines there), and each
+  // lane takes its row from LDS (row stride 20 floats: the 16 rows' float4 reads fall in
+  // distinct banks).
   float gv[16], yv[16];
-  const float* grow = grad + (int64_t)min(pr, p.M - 1) * p.N + c0;
-  if (pr < p.M && c0 + 15 < p.N && ((reinterpret_cast<uintptr_t>(grow) & 15) == 0)) {
+  {
+    __shared__ float gtile[kTileThreads / 64][16 * 20];
+    float* gt = gtile[__builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6))];
+    const int32_t lr = r0 + (lane >> 2), lc = c0 + ((lane & 3) << 2);
+    const float* gp = grad + (int64_t)min(lr, p.M - 1) * p.N + lc;
+    float4 g4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (lr < p.M) {
+      if (lc + 3 < p.N && ((reinterpret_cast<uintptr_t>(gp) & 15) == 0)) {
+        g4 = load4_stream(gp);
+      } else {
+        g4.x = lc < p.N ? load_stream(gp) : 0.f;
+        g4.y = lc + 1 < p.N ? load_stream(gp + 1) : 0.f;
+        g4.z = lc + 2 < p.N ? load_stream(gp + 2) : 0.f;
+        g4.w = lc + 3 < p.N ? load_stream(gp + 3) : 0.f;
+      }
+    }
+    *reinterpret_cast<float4*>(gt + (lane >> 2) * 20 + ((lane & 3) << 2)) = g4;
+    wave_sync();
 #pragma unroll
     for (int c = 0; c < 16; c += 4) {
-      const float4 g4 = *reinterpret_cast<const float4*>(grow + c);
-      gv[c] = g4.x;
-      gv[c + 1] = g4.y;
-      gv[c + 2] = g4.z;
-      gv[c + 3] = g4.w;
+      const float4 v = *reinterpret_cast<const float4*>(gt + row * 20 + c);
+      gv[c] = v.x;
+      gv[c + 1] = v.y;
+      gv[c + 2] = v.z;
+      gv[c + 3] = v.w;
     }
-  } else {
-#pragma unroll
-    for (int c = 0; c < 16; ++c) gv[c] = (pr < p.M && c0 + c < p.N) ? grow[c] : 0.0f;
   }
   // (the same 16 addresses in every lane: inside the matrix, four aligned float4 from one base)
   if (c0 + 15 < p.N && ((reinterpret_cast<uintptr_t>(col_coords + c0) & 15) == 0)) {
@@ -2340,9 +2592,10 @@ int64_t quad_grid(const Problem& p) {
 // ------------------------------------------------------------------------------------------
 // Batched fields (one launch per phase for many layers).  The plan buffer holds a header,
 // one BatchLayer per field and, per kernel shape, a block -> field map:
-//   tile map    4 tiles per block (render, backward reduce)
+//   tile map    4 tiles per block (backward reduce)
 //   emit map    4 Gaussians per block
 //   finish map  256 Gaussians per block
+//   render map  4 pairs of 16x16 tiles (or one 32x32 tile) per block
 // Each field's blocks are contiguous, so block b of a kernel handles local index
 // (b - first block of its field) * per_block + wave / thread.
 
@@ -2365,7 +2618,7 @@ struct BatchLayer {
   float* d_mu;
   float* d_chol_raw;
   float* d_amp;
-  int64_t tile_block0, emit_block0, finish_block0;
+  int64_t tile_block0, emit_block0, finish_block0, render_block0;
 };
 
 // Plan regions after the header: layers, the tile / emission / finish block maps, the
@@ -2373,8 +2626,9 @@ struct BatchLayer {
 // (per layer: status bits, pair count).
 struct BatchHeader {
   int64_t n;
-  int64_t tile_blocks, emit_blocks, finish_blocks;
-  int64_t layers_off, tile_map_off, emit_map_off, finish_map_off, grad_table_off, readback_off, total;
+  int64_t tile_blocks, emit_blocks, finish_blocks, render_blocks;
+  int64_t layers_off, tile_map_off, emit_map_off, finish_map_off, render_map_off, grad_table_off, readback_off,
+      total;
 };
 
 struct BatchReadback {
@@ -2385,35 +2639,73 @@ struct BatchReadback {
   double pad2;
 };
 
-BatchHeader batch_header(int64_t n, int64_t tile_blocks, int64_t emit_blocks, int64_t finish_blocks) {
+BatchHeader batch_header(int64_t n, int64_t tile_blocks, int64_t emit_blocks, int64_t finish_blocks,
+                         int64_t render_blocks) {
   BatchHeader h{};
   h.n = n;
   h.tile_blocks = tile_blocks;
   h.emit_blocks = emit_blocks;
   h.finish_blocks = finish_blocks;
+  h.render_blocks = render_blocks;
   h.layers_off = (int64_t)align256(sizeof(BatchHeader));
   h.tile_map_off = (int64_t)align256(h.layers_off + sizeof(BatchLayer) * n);
   h.emit_map_off = (int64_t)align256(h.tile_map_off + sizeof(int32_t) * tile_blocks);
   h.finish_map_off = (int64_t)align256(h.emit_map_off + sizeof(int32_t) * emit_blocks);
-  h.grad_table_off = (int64_t)align256(h.finish_map_off + sizeof(int32_t) * finish_blocks);
+  h.render_map_off = (int64_t)align256(h.finish_map_off + sizeof(int32_t) * finish_blocks);
+  h.grad_table_off = (int64_t)align256(h.render_map_off + sizeof(int32_t) * render_blocks);
   h.readback_off = (int64_t)align256(h.grad_table_off + sizeof(void*) * n);
   h.total = (int64_t)align256(h.readback_off + sizeof(BatchReadback) * n);
   return h;
 }
 
-__device__ inline const BatchLayer& batch_layer(const uint8_t* plan, int64_t map_off, int64_t* block0_sel,
-                                                int which, int32_t* index = nullptr) {
+// A pointer the kernel read from memory (the plan) is generic to the compiler, which then emits
+// flat loads and stores; flat operations count against the LDS wait counter as well, so every
+// wait for an LDS read also waits for the outstanding global ones.  A cast to the global address
+// space (kept opaque, so that the compiler does not fold it with the cast back) lets the
+// compiler emit global instructions.  For pointers that are uniform across the wave.
+template <typename T>
+__device__ inline T* glob(T* q) {
+  __attribute__((address_space(1))) T* g = (__attribute__((address_space(1))) T*)q;
+  asm("" : "+s"(g));
+  return (T*)g;
+}
+
+// Layer l of the plan with its pointers marked global (all of them address device memory).
+__device__ inline BatchLayer global_layer(const BatchLayer& src) {
+  BatchLayer ly = src;
+  ly.row_coords = glob(ly.row_coords);
+  ly.col_coords = glob(ly.col_coords);
+  ly.mu = glob(ly.mu);
+  ly.chol_raw = glob(ly.chol_raw);
+  ly.amp = glob(ly.amp);
+  ly.delta = glob(ly.delta);
+  ly.tile_ptr = glob(ly.tile_ptr);
+  ly.num_pairs = glob(ly.num_pairs);
+  ly.ids = glob(ly.ids);
+  ly.fws = glob(ly.fws);
+  ly.bws = glob(ly.bws);
+  ly.d_mu = glob(ly.d_mu);
+  ly.d_chol_raw = glob(ly.d_chol_raw);
+  ly.d_amp = glob(ly.d_amp);
+  return ly;
+}
+
+__device__ inline BatchLayer batch_layer(const uint8_t* plan, int64_t map_off, int64_t* block0_sel, int which,
+                                         int32_t* index = nullptr) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
   const int32_t l = reinterpret_cast<const int32_t*>(plan + map_off)[blockIdx.x];
   const BatchLayer& ly = reinterpret_cast<const BatchLayer*>(plan + h->layers_off)[l];
-  *block0_sel = which == 0 ? ly.tile_block0 : which == 1 ? ly.emit_block0 : ly.finish_block0;
+  *block0_sel = which == 0   ? ly.tile_block0
+                : which == 1 ? ly.emit_block0
+                : which == 2 ? ly.finish_block0
+                             : ly.render_block0;
   if (index) *index = l;
-  return ly;
+  return global_layer(ly);
 }
 
 __global__ __launch_bounds__(kBinThreads) void k_bin_batch(const uint8_t* __restrict__ plan) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
-  const BatchLayer& ly = reinterpret_cast<const BatchLayer*>(plan + h->layers_off)[blockIdx.x];
+  const BatchLayer ly = global_layer(reinterpret_cast<const BatchLayer*>(plan + h->layers_off)[blockIdx.x]);
   const Problem p = ly.p;
   const FwdLayout L = ly.fl;
   __shared__ uint32_t mlds[kMaskLdsWords];
@@ -2423,7 +2715,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_batch(const uint8_t* __rest
 __global__ __launch_bounds__(kEmitThreads) void k_emit_batch(const uint8_t* __restrict__ plan) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
   int64_t b0;
-  const BatchLayer& ly = batch_layer(plan, h->emit_map_off, &b0, 1);
+  const BatchLayer ly = batch_layer(plan, h->emit_map_off, &b0, 1);
   const Problem p = ly.p;
   if (p.W > 0) return;  // blocks kept for a capacity on the emission path; k is on the mask path
   const FwdLayout L = ly.fl;
@@ -2435,14 +2727,32 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_batch(const uint8_t* __re
 __global__ __launch_bounds__(kTileThreads) void k_render16_batch(const uint8_t* __restrict__ plan) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
   int64_t b0;
-  const BatchLayer& ly = batch_layer(plan, h->tile_map_off, &b0, 0);
+  const BatchLayer ly = batch_layer(plan, h->render_map_off, &b0, 3);
   const Problem p = ly.p;
-  render16_body(p, ly.row_coords, ly.col_coords, reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
-                ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws,
-                reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.rowmask),
-                reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.colmask),
-                sub_tile(p, (int64_t)blockIdx.x - b0, wave_id()), nullptr, nullptr, 0, 1,
-                reinterpret_cast<float*>(ly.fws + ly.fl.bsq));
+  const GaussEval* ev = reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval);
+  const uint32_t* rowmask = reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.rowmask);
+  const uint32_t* colmask = reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.colmask);
+  float* bsq = reinterpret_cast<float*>(ly.fws + ly.fl.bsq);
+  const int64_t idx = (int64_t)blockIdx.x - b0;
+  if (p.tile_out == 32) {  // one 32x32 tile a workgroup, a quadrant a wave
+    render16_body(p, ly.row_coords, ly.col_coords, ev, ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws, rowmask,
+                  colmask, sub_tile(p, idx, wave_id()), nullptr, nullptr, 0, 1, bsq);
+    return;
+  }
+  // 16x16 tiles: a pair of horizontally adjacent tiles a wave, (R x ceil(C / 2)) pairs row-major
+  const int32_t cp = (p.C + 1) / 2;
+  const int64_t pi = idx * (kTileThreads / 64) + wave_id();
+  if (pi >= (int64_t)p.R * cp) return;
+  const int32_t tr = (int32_t)pi / cp, tc = 2 * ((int32_t)pi - tr * cp);
+  if (p.W > 0) {
+    render16x2_body(p, ly.row_coords, ly.col_coords, ev, ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws,
+                    rowmask, colmask, tr, tc, bsq);
+    return;
+  }
+  // emission path (k beyond the masks): the two tiles one after the other
+  for (int32_t c = tc; c < tc + 2 && c < p.C; ++c)
+    render16_body(p, ly.row_coords, ly.col_coords, ev, ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws, rowmask,
+                  colmask, tile16(p, (int64_t)tr * p.C + c), nullptr, nullptr, 0, 1, bsq);
 }
 
 template <bool kMaskClamp>
@@ -2450,12 +2760,12 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
   int64_t b0;
   int32_t l;
-  const BatchLayer& ly = batch_layer(plan, h->tile_map_off, &b0, 0, &l);
+  const BatchLayer ly = batch_layer(plan, h->tile_map_off, &b0, 0, &l);
   const Problem p = ly.p;
   const BwdLayout L = ly.bl;
   const int64_t T = (int64_t)p.R * p.C;
   const int64_t P = ly.tile_ptr[T];  // pairs beyond the id capacity were never emitted
-  const float* grad = reinterpret_cast<const float* const*>(plan + h->grad_table_off)[l];
+  const float* grad = glob(reinterpret_cast<const float* const*>(plan + h->grad_table_off)[l]);
   bwd16_body<int64_t, int64_t, true, kMaskClamp>(p, grad, ly.row_coords, ly.col_coords, ly.mu, ly.chol_raw,
                                reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
                                ly.tile_ptr, ly.ids, P < ly.capacity ? P : ly.capacity, ly.bws, L,
@@ -2514,7 +2824,7 @@ __global__ __launch_bounds__(256) void k_batch_read(uint8_t* plan, int32_t clear
 __global__ __launch_bounds__(kTileThreads) void k_finish_batch(const uint8_t* __restrict__ plan) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
   int64_t b0;
-  const BatchLayer& ly = batch_layer(plan, h->finish_map_off, &b0, 2);
+  const BatchLayer ly = batch_layer(plan, h->finish_map_off, &b0, 2);
   const Problem p = ly.p;
   const BwdLayout L = ly.bl;
   finish_body(p, ly.chol_raw, ly.amp, ly.d_mu, ly.d_chol_raw, ly.d_amp, ly.bws, L,
@@ -2889,7 +3199,7 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
   const size_t n = (size_t)n_layers;
   BatchHeader h{};
   std::vector<BatchLayer> ls(n);
-  int64_t tile_blocks = 0, emit_blocks = 0, finish_blocks = 0;
+  int64_t tile_blocks = 0, emit_blocks = 0, finish_blocks = 0, render_blocks = 0;
   bool backward_buffers = true, grads_set = true;
   for (size_t i = 0; i < n; ++i) {
     const gf_layer& in = layers[i];
@@ -2945,14 +3255,17 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
     ly.tile_block0 = tile_blocks;
     ly.emit_block0 = emit_blocks;
     ly.finish_block0 = finish_blocks;
+    ly.render_block0 = render_blocks;
     tile_blocks += quad_grid(ly.p);
+    render_blocks += t32 ? quad_grid(ly.p)
+                         : ((int64_t)ly.p.R * ((ly.p.C + 1) / 2) + kTileThreads / 64 - 1) / (kTileThreads / 64);
     const int64_t per_emit_block = (kEmitThreads / 64) * (64 / kEmitLanesBatch);
     if (ly.p.W == 0 || pc.W == 0) emit_blocks += (kc + per_emit_block - 1) / per_emit_block;  // emission path
     finish_blocks += (kc * ly.p.S + kTileThreads - 1) / kTileThreads;
   }
-  if (tile_blocks >= INT32_MAX || emit_blocks >= INT32_MAX)
+  if (tile_blocks >= INT32_MAX || emit_blocks >= INT32_MAX || render_blocks >= INT32_MAX)
     return set_err(GF_E_INVALID_ARGUMENT, "batch too large for one launch");
-  h = batch_header(n_layers, tile_blocks, emit_blocks, finish_blocks);
+  h = batch_header(n_layers, tile_blocks, emit_blocks, finish_blocks, render_blocks);
   const size_t need = (size_t)h.total;
   info->n_layers = n_layers;
   info->mask_clamp = (cfg->has_clamp_quad && cfg->clamp_quad < 80.0) ? 1 : 0;
@@ -2961,6 +3274,7 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
   info->tile_blocks = tile_blocks;
   info->emit_blocks = emit_blocks;
   info->finish_blocks = finish_blocks;
+  info->render_blocks = render_blocks;
   info->plan_bytes = need;
   if (!plan) return GF_OK;  // size query
   if (plan_bytes < need) return set_err(GF_E_WORKSPACE, "batch plan needs %zu bytes, got %zu", need, plan_bytes);
@@ -2970,15 +3284,18 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
   int32_t* tm = reinterpret_cast<int32_t*>(host.data() + h.tile_map_off);
   int32_t* em = reinterpret_cast<int32_t*>(host.data() + h.emit_map_off);
   int32_t* fm = reinterpret_cast<int32_t*>(host.data() + h.finish_map_off);
+  int32_t* rmap = reinterpret_cast<int32_t*>(host.data() + h.render_map_off);
   const float** gt = reinterpret_cast<const float**>(host.data() + h.grad_table_off);
   for (size_t i = 0; i < n; ++i) gt[i] = layers[i].grad_delta;
   for (size_t i = 0; i < n; ++i) {
     const int64_t te = i + 1 < n ? ls[i + 1].tile_block0 : tile_blocks;
     const int64_t ee = i + 1 < n ? ls[i + 1].emit_block0 : emit_blocks;
     const int64_t fe = i + 1 < n ? ls[i + 1].finish_block0 : finish_blocks;
+    const int64_t re = i + 1 < n ? ls[i + 1].render_block0 : render_blocks;
     for (int64_t b = ls[i].tile_block0; b < te; ++b) tm[b] = (int32_t)i;
     for (int64_t b = ls[i].emit_block0; b < ee; ++b) em[b] = (int32_t)i;
     for (int64_t b = ls[i].finish_block0; b < fe; ++b) fm[b] = (int32_t)i;
+    for (int64_t b = ls[i].render_block0; b < re; ++b) rmap[b] = (int32_t)i;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   GF_HIP_CHECK(hipMemcpyAsync(plan, host.data(), need, hipMemcpyHostToDevice, st));
@@ -3000,7 +3317,7 @@ int gf_batch_forward(const void* plan, const gf_batch_info* info, uint32_t phase
     GF_LAUNCH_CHECK("k_emit_batch");
   }
   if (phases & GF_PHASE_RENDER) {
-    hipLaunchKernelGGL(k_render16_batch, dim3((unsigned)info->tile_blocks), dim3(kTileThreads), 0, st, pl);
+    hipLaunchKernelGGL(k_render16_batch, dim3((unsigned)info->render_blocks), dim3(kTileThreads), 0, st, pl);
     GF_LAUNCH_CHECK("k_render16_batch");
   }
   return GF_OK;
@@ -3034,7 +3351,7 @@ int gf_batch_read(void* plan, const gf_batch_info* info, int32_t clear, uint32_t
   uint8_t* pl = reinterpret_cast<uint8_t*>(plan);
   hipLaunchKernelGGL(k_batch_read, dim3((unsigned)n), dim3(256), 0, st, pl, clear);
   GF_LAUNCH_CHECK("k_batch_read");
-  const BatchHeader h = batch_header(n, info->tile_blocks, info->emit_blocks, info->finish_blocks);
+  const BatchHeader h = batch_header(n, info->tile_blocks, info->emit_blocks, info->finish_blocks, info->render_blocks);
   std::vector<BatchReadback> rb((size_t)n);
   GF_HIP_CHECK(hipMemcpyAsync(rb.data(), pl + h.readback_off, sizeof(BatchReadback) * (size_t)n,
                               hipMemcpyDeviceToHost, st));

@@ -228,6 +228,8 @@ typedef struct gf_batch_info {
   int32_t backward_buffers;      /* every layer has its backward workspace and gradient outputs */
   int32_t mask_clamp;            /* clamp_quad < 80: the backward drops clamped pixels from the
                                     quadratic-form moments (at 80 and above they are below e^-40) */
+  int64_t render_blocks;         /* workgroups of the render: 4 pairs of 16x16 tiles or one 32x32
+                                    tile each */
 } gf_batch_info;
 
 /*

@@ -681,6 +681,64 @@ def test_batch_matches_single_layers(device):
             grad_close(a, b, f"layer {i} {name}", rtol=1e-5)
 
 
+def test_batch_tile_pairs_match_single_fields(device):
+    """The batched render takes two horizontally adjacent 16x16 tiles a wave: the union of their
+    Gaussians, staged once, with a zero amplitude on the tile that does not list one.  Per field
+    configuration, a batch of the 24 seeded random fields (ragged sizes, odd tile-column counts,
+    indefinite forms, clamps, normalisation, sub-pixel to whole-matrix Gaussians) plus two fields
+    on the emission path (K > 8192; odd and even tile columns), against each field's
+    single-field run: tile_ptr and ids bit for bit; delta-W bit for bit where no tile holds more
+    than 32 Gaussians (beyond that the single-field render may split a tile over four waves, a
+    different fp32 summation order: 1e-6 of the peak); the delta-W norm of the read-back; the
+    gradients to the atomics' order."""
+    from guass_amd.ops import FieldBatchPlan
+
+    groups: dict = {}
+    for i in range(24):
+        p, cfg = _random_forward_problem(i)
+        groups.setdefault((cfg["sigma"], cfg["normalize"], cfg["clamp"]), []).append(p)
+    first = next(iter(groups))
+    groups[first] += [tiny_problem(45, 70, 8300, 8), tiny_problem(60, 96, 9000, 9)]
+    exact = odd = 0
+    for (sigma, normalize, clamp), probs in groups.items():
+        kw = dict(sigma=sigma, normalize=normalize, clamp=clamp)
+        say(f"batch of {len(probs)} fields {kw}: " + ", ".join(f"{p.out_features}x{p.in_features}/K{p.k}"
+                                                              for p in probs))
+        singles = [run_gpu(p, device, **kw) for p in probs]
+        caps = [max(int(sg[1][-1]), 1) for sg in singles]
+        batch = FieldBatchPlan([p.to(device) for p in probs], device, capacities=caps, sigma_multiplier=sigma,
+                               normalize=normalize, clamp_quad=clamp)
+        batch.forward()
+        batch.backward()
+        st, pairs, norms = batch.read(norms=True)
+        assert st == [0] * len(probs), st
+        for i, (p, pl, sg) in enumerate(zip(probs, batch.plans, singles)):
+            P = int(sg[1][-1])
+            assert pairs[i] == P, f"{p.name}: pairs"
+            assert torch.equal(pl.tile_ptr, sg[1]), f"{p.name}: tile_ptr"
+            assert torch.equal(pl.ids[:P], sg[2]), f"{p.name}: ids"
+            odd += (-(-p.in_features // 16)) % 2
+            if int((sg[1][1:] - sg[1][:-1]).max()) <= 32:
+                exact += 1
+                assert torch.equal(pl.delta.nan_to_num(7.0), sg[0].nan_to_num(7.0)), f"{p.name}: delta"
+            else:
+                # indefinite forms without a clamp overflow to +-inf in both renders, at the same pixels
+                fin = torch.isfinite(sg[0])
+                assert torch.equal(pl.delta[~fin].nan_to_num(7.0), sg[0][~fin].nan_to_num(7.0)), f"{p.name}: inf"
+                field_close(pl.delta[fin], sg[0][fin], rtol=1e-6)
+            want = float(torch.linalg.vector_norm(sg[0].double()))
+            if math.isfinite(want):
+                assert abs(norms[i] - want) <= 1e-6 * max(want, 1e-30), f"{p.name}: norm {norms[i]} vs {want}"
+            else:
+                assert not math.isfinite(norms[i]), f"{p.name}: norm {norms[i]} vs {want}"
+            for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), sg[3:]):
+                fin = torch.isfinite(b)
+                assert torch.equal(torch.isfinite(a), fin), f"{p.name} {name}: non-finite entries differ"
+                grad_close(a[fin], b[fin], f"{p.name} {name}", rtol=1e-5)
+    say(f"  {exact} of 26 fields bit-equal, {odd} with an odd tile-column count")
+    assert exact >= 20 and odd >= 6
+
+
 # One cfg4 layer of each of the six distinct SD1.5 attention shapes (index into
 # wl.sd15_attention_shapes(): block 0 attn1.to_q 320x320, block 0 attn2.to_k 320x768, block 2
 # attn1.to_q 640x640, block 2 attn2.to_k 640x768, block 4 attn1.to_q 1280x1280, block 4
@@ -746,6 +804,8 @@ def test_cfg4_full_batch_matches_single_fields(device):
     batch = FieldBatchPlan(layers, device, capacities=caps)
     tiles = [(-(-p.out_features // 16)) * (-(-p.in_features // 16)) for p in probs]
     assert batch.info.tile_blocks == sum(-(-t // 4) for t in tiles)  # four 16x16 tiles a workgroup
+    pairs_of = [(-(-p.out_features // 16)) * -(-(-(-p.in_features // 16)) // 2) for p in probs]
+    assert batch.info.render_blocks == sum(-(-t // 4) for t in pairs_of)  # four tile pairs a workgroup
     batch.forward()
     batch.backward()
     torch.cuda.synchronize()
@@ -1319,7 +1379,8 @@ def test_one_layer_batch_survives_k_changes(device):
         return (pl.fwd_ws.data_ptr(), pl.bwd_ws.data_ptr(), pl.ids.data_ptr(), pl.delta.data_ptr(),
                 batch.plan.data_ptr(), batch.grad_flat.data_ptr())
 
-    first = (batch.info.tile_blocks, batch.info.emit_blocks, batch.info.finish_blocks, batch.info.plan_bytes)
+    first = (batch.info.tile_blocks, batch.info.emit_blocks, batch.info.finish_blocks, batch.info.render_blocks,
+             batch.info.plan_bytes)
     ptrs = pointers()
     s = torch.cuda.Stream(device)
     s.wait_stream(torch.cuda.current_stream(device))
@@ -1336,7 +1397,7 @@ def test_one_layer_batch_survives_k_changes(device):
         p = wl.make_problem(f"one_layer_k{k}", 320, 768, k, math.log(6.0), 0.7, seed)
         assert batch.update([p.to(device)]), f"K={k}: re-planned with new grids"
         assert not batch.reallocated and pointers() == ptrs, f"K={k}: a buffer was reallocated"
-        assert (batch.info.tile_blocks, batch.info.emit_blocks, batch.info.finish_blocks,
+        assert (batch.info.tile_blocks, batch.info.emit_blocks, batch.info.finish_blocks, batch.info.render_blocks,
                 batch.info.plan_bytes) == first
         pl.delta.fill_(float("nan"))
         graph.replay()
