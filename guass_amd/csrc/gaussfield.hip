@@ -2091,6 +2091,14 @@ __device__ __forceinline__ void bwd16_body(
 #pragma unroll
     for (int c = 0; c < 16; ++c) yv[c] = col_coords[min(c0 + c, p.N - 1)];
   }
+  // Dense tiles without the clamp mask: columns as offsets from the tile's first one (uniform:
+  // scalar registers), for the moments about that column below (32 instructions a tile, repaid
+  // by 32 a round on tiles of several rounds).
+  constexpr bool kShifted = !kMaskClamp && kTransposeSums;
+  float yd[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c)
+    yd[c] = kShifted ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(yv[c] - yv[0]))) : 0.0f;
   const float x = row_coords[min(pr, p.M - 1)];
   int64_t s = (int64_t)tile_ptr[t], e = (int64_t)tile_ptr[t + 1];
   if (lane == 0) {
@@ -2134,12 +2142,12 @@ __device__ __forceinline__ void bwd16_body(
       const float b = wb * dx;
       if (chunk_general && gen != 0.0f) g = -1;  // indefinite form: the pass below
       float t0 = 0.f, t2 = 0.f, t3 = 0.f, tq = 0.f;
+      if (kMaskClamp) {
 #pragma unroll
-      for (int c = 0; c < 16; ++c) {
-        const float dy = yv[c] - mu1;
-        if (kMaskClamp) {
+        for (int c = 0; c < 16; ++c) {
           // clamped pixels (q > clamp_quad) carry no quadratic-form gradient (the reference's
           // clamp mask, backward.cu:316-320,336-338): they add to S0 only
+          const float dy = yv[c] - mu1;
           const float z = fmaf(wc, dy, b);
           const float qv = -fmaf(z, z, A);
           const float ge = gv[c] * __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(qv, p.q_lo, 0.0f));
@@ -2149,8 +2157,32 @@ __device__ __forceinline__ void bwd16_body(
           const float tt = gq * dy;
           t2 += tt;
           t3 = fmaf(tt, dy, t3);
-        } else {
-          const float ge = gv[c] * basis_w(p, A, fmaf(wc, dy, b));
+        }
+      } else if (kShifted) {
+        // Moments about the tile's first column y0: with dy = yd_c + dl, dl = y0 - mu1,
+        //   S(ge dy) = S(ge yd) + dl S(ge),  S(ge dy^2) = S(ge yd^2) + dl (2 S(ge yd) + dl S(ge)),
+        // and z = wc dy + b = wc yd_c + z0 with z0 = wc dl + b.  With clamp_quad >= 80 (or none)
+        // the clamp only floors bases below e^-40 (a difference below e^-40 |g| per pixel), so
+        // the floor is dropped here and below, as in the render.
+        const float dl = yv[0] - mu1;
+        const float z0 = fmaf(wc, dl, b);
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+          const float z = c == 0 ? z0 : fmaf(wc, yd[c], z0);
+          const float ge = gv[c] * __builtin_amdgcn_exp2f(-fmaf(z, z, A));
+          t0 += ge;
+          const float tt = ge * yd[c];
+          t2 += tt;
+          t3 = fmaf(tt, yd[c], t3);
+        }
+        t3 = fmaf(dl, fmaf(dl, t0, 2.0f * t2), t3);
+        t2 = fmaf(dl, t0, t2);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+          const float dy = yv[c] - mu1;
+          const float z = fmaf(wc, dy, b);
+          const float ge = gv[c] * __builtin_amdgcn_exp2f(-fmaf(z, z, A));
           t0 += ge;
           const float tt = ge * dy;
           t2 += tt;
@@ -2691,9 +2723,9 @@ __device__ inline BatchLayer global_layer(const BatchLayer& src) {
 }
 
 __device__ inline BatchLayer batch_layer(const uint8_t* plan, int64_t map_off, int64_t* block0_sel, int which,
-                                         int32_t* index = nullptr) {
+                                         uint32_t blk, int32_t* index = nullptr) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
-  const int32_t l = reinterpret_cast<const int32_t*>(plan + map_off)[blockIdx.x];
+  const int32_t l = reinterpret_cast<const int32_t*>(plan + map_off)[blk];
   const BatchLayer& ly = reinterpret_cast<const BatchLayer*>(plan + h->layers_off)[l];
   *block0_sel = which == 0   ? ly.tile_block0
                 : which == 1 ? ly.emit_block0
@@ -2715,7 +2747,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_batch(const uint8_t* __rest
 __global__ __launch_bounds__(kEmitThreads) void k_emit_batch(const uint8_t* __restrict__ plan) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
   int64_t b0;
-  const BatchLayer ly = batch_layer(plan, h->emit_map_off, &b0, 1);
+  const BatchLayer ly = batch_layer(plan, h->emit_map_off, &b0, 1, blockIdx.x);
   const Problem p = ly.p;
   if (p.W > 0) return;  // blocks kept for a capacity on the emission path; k is on the mask path
   const FwdLayout L = ly.fl;
@@ -2727,13 +2759,14 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_batch(const uint8_t* __re
 __global__ __launch_bounds__(kTileThreads) void k_render16_batch(const uint8_t* __restrict__ plan) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
   int64_t b0;
-  const BatchLayer ly = batch_layer(plan, h->render_map_off, &b0, 3);
+  const uint32_t blk = blockIdx.x;
+  const BatchLayer ly = batch_layer(plan, h->render_map_off, &b0, 3, blk);
   const Problem p = ly.p;
   const GaussEval* ev = reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval);
   const uint32_t* rowmask = reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.rowmask);
   const uint32_t* colmask = reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.colmask);
   float* bsq = reinterpret_cast<float*>(ly.fws + ly.fl.bsq);
-  const int64_t idx = (int64_t)blockIdx.x - b0;
+  const int64_t idx = (int64_t)blk - b0;
   if (p.tile_out == 32) {  // one 32x32 tile a workgroup, a quadrant a wave
     render16_body(p, ly.row_coords, ly.col_coords, ev, ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws, rowmask,
                   colmask, sub_tile(p, idx, wave_id()), nullptr, nullptr, 0, 1, bsq);
@@ -2760,7 +2793,8 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
   int64_t b0;
   int32_t l;
-  const BatchLayer ly = batch_layer(plan, h->tile_map_off, &b0, 0, &l);
+  const uint32_t blk = blockIdx.x;
+  const BatchLayer ly = batch_layer(plan, h->tile_map_off, &b0, 0, blk, &l);
   const Problem p = ly.p;
   const BwdLayout L = ly.bl;
   const int64_t T = (int64_t)p.R * p.C;
@@ -2769,7 +2803,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
   bwd16_body<int64_t, int64_t, true, kMaskClamp>(p, grad, ly.row_coords, ly.col_coords, ly.mu, ly.chol_raw,
                                reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
                                ly.tile_ptr, ly.ids, P < ly.capacity ? P : ly.capacity, ly.bws, L,
-                               sub_tile(p, (int64_t)blockIdx.x - b0, wave_id()));
+                               sub_tile(p, (int64_t)blk - b0, wave_id()));
 }
 
 // dL/d(delta) pointers of layers base .. base + count - 1 (count <= kPtrChunk), passed by value.
@@ -2824,7 +2858,7 @@ __global__ __launch_bounds__(256) void k_batch_read(uint8_t* plan, int32_t clear
 __global__ __launch_bounds__(kTileThreads) void k_finish_batch(const uint8_t* __restrict__ plan) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
   int64_t b0;
-  const BatchLayer ly = batch_layer(plan, h->finish_map_off, &b0, 2);
+  const BatchLayer ly = batch_layer(plan, h->finish_map_off, &b0, 2, blockIdx.x);
   const Problem p = ly.p;
   const BwdLayout L = ly.bl;
   finish_body(p, ly.chol_raw, ly.amp, ly.d_mu, ly.d_chol_raw, ly.d_amp, ly.bws, L,

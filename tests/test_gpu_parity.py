@@ -690,7 +690,8 @@ def test_batch_tile_pairs_match_single_fields(device):
     single-field run: tile_ptr and ids bit for bit; delta-W bit for bit where no tile holds more
     than 32 Gaussians (beyond that the single-field render may split a tile over four waves, a
     different fp32 summation order: 1e-6 of the peak); the delta-W norm of the read-back; the
-    gradients to the atomics' order."""
+    gradients to 1e-4 of each other, each batch gradient at least as close to the float64
+    evaluation as the single field's (+ 1e-5)."""
     from guass_amd.ops import FieldBatchPlan
 
     groups: dict = {}
@@ -700,6 +701,7 @@ def test_batch_tile_pairs_match_single_fields(device):
     first = next(iter(groups))
     groups[first] += [tiny_problem(45, 70, 8300, 8), tiny_problem(60, 96, 9000, 9)]
     exact = odd = 0
+    worst_gap = 0.0
     for (sigma, normalize, clamp), probs in groups.items():
         kw = dict(sigma=sigma, normalize=normalize, clamp=clamp)
         say(f"batch of {len(probs)} fields {kw}: " + ", ".join(f"{p.out_features}x{p.in_features}/K{p.k}"
@@ -731,10 +733,22 @@ def test_batch_tile_pairs_match_single_fields(device):
                 assert abs(norms[i] - want) <= 1e-6 * max(want, 1e-30), f"{p.name}: norm {norms[i]} vs {want}"
             else:
                 assert not math.isfinite(norms[i]), f"{p.name}: norm {norms[i]} vs {want}"
-            for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), sg[3:]):
+            # gradients: the batch reduces its dense tiles with moments about each tile's first
+            # column, the single field's sparse tiles about the Gaussian's centre -- two fp32
+            # evaluations, each held to the float64 one
+            r64 = fo.gaussian_field_fwd_bwd_fp64(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad,
+                                                 16, 16, sigma, normalize, clamp)
+            for name, a, b, c in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), sg[3:],
+                                     r64[3:]):
                 fin = torch.isfinite(b)
                 assert torch.equal(torch.isfinite(a), fin), f"{p.name} {name}: non-finite entries differ"
-                grad_close(a[fin], b[fin], f"{p.name} {name}", rtol=1e-5)
+                grad_close(a[fin], b[fin], f"{p.name} {name}", rtol=1e-4)
+                if bool(torch.isfinite(c).all()) and float(c.norm()) > 0.0:
+                    eb = float((a.cpu().double() - c).norm()) / float(c.norm())
+                    es = float((b.cpu().double() - c).norm()) / float(c.norm())
+                    worst_gap = max(worst_gap, eb - es)
+                    assert eb <= es + 1e-5, (p.name, name, eb, es)
+    say(f"  batch gradients at most {worst_gap:.1e} further from float64 than the single fields'")
     say(f"  {exact} of 26 fields bit-equal, {odd} with an odd tile-column count")
     assert exact >= 20 and odd >= 6
 
