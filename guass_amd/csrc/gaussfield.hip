@@ -1899,6 +1899,21 @@ __device__ __forceinline__ void render16x2_body(
   }
 }
 
+// Single 16x16 fields on the mask path without heavy tiles: a pair of horizontally adjacent
+// tiles a wave, four pairs (R x ceil(C / 2), row-major) a workgroup.
+__global__ __launch_bounds__(kTileThreads) void k_render16x2(
+    Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
+    const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids, int64_t capacity,
+    float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
+    const uint32_t* __restrict__ colmask) {
+  const int32_t cp = (p.C + 1) / 2;
+  const int64_t pi = (int64_t)blockIdx.x * (kTileThreads / 64) + wave_id();
+  if (pi >= (int64_t)p.R * cp) return;
+  const int32_t tr = (int32_t)pi / cp, tc = 2 * ((int32_t)pi - tr * cp);
+  render16x2_body(p, row_coords, col_coords, ev, tile_ptr, ids, capacity, delta, ws, rowmask, colmask, tr, tc,
+                  nullptr);
+}
+
 template <bool kHeavy>
 __global__ __launch_bounds__(kTileThreads) void k_render16(
     Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
@@ -3113,6 +3128,15 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
     const bool binned_here = tiles_in_render(p);
     const int32_t xh = heavy_grid(p, ids_capacity);
     p.heavy = xh > 0 ? kHeavyTile : 0;
+    if (p.tile_out == 16 && p.tile_in == 16 && p.W > 0 && !binned_here && xh == 0) {
+      const int64_t pairs = (int64_t)p.R * ((p.C + 1) / 2);
+      hipLaunchKernelGGL(k_render16x2, dim3((unsigned)((pairs + kTileThreads / 64 - 1) / (kTileThreads / 64))),
+                         dim3(kTileThreads), 0, st, p, row_coords, col_coords, ev, tile_ptr, gaussian_ids_sorted,
+                         ids_capacity, delta, ws, reinterpret_cast<const uint32_t*>(ws + L.rowmask),
+                         reinterpret_cast<const uint32_t*>(ws + L.colmask));
+      GF_LAUNCH_CHECK("k_render16x2");
+      return GF_OK;
+    }
     hipLaunchKernelGGL(xh > 0 ? k_render16<true> : k_render16<false>, dim3((unsigned)(xh + quad_grid(p))),
                        dim3(kTileThreads), 0, st, p, row_coords, col_coords, ev, tile_ptr, gaussian_ids_sorted,
                        ids_capacity, delta, ws, reinterpret_cast<const uint32_t*>(ws + L.rowmask),
