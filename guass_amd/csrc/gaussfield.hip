@@ -2063,10 +2063,17 @@ __device__ __forceinline__ void bwd16_body(
   // once, and keeping them out of L2 keeps the accumulator and constant lines there), and each
   // lane takes its row from LDS (row stride 20 floats: the 16 rows' float4 reads fall in
   // distinct banks).
+  // Dense tiles without the clamp mask (kShifted) take their moments about the tile's first
+  // column y0 (below): each lane also stages g (y - y0) and g (y - y0)^2 for its four columns, so
+  // that a round weights one exponential with three FMAs.  LDS row stride: 52 floats there (g,
+  // g yd, g yd^2 and pad), 20 otherwise; either way the 16 rows' float4 reads fall in distinct
+  // banks.
+  constexpr bool kShifted = !kMaskClamp && kTransposeSums;
+  constexpr int kGs = kShifted ? 52 : 20;
+  __shared__ float gtile[kTileThreads / 64][16 * 52];
+  float* gt = gtile[__builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6))];
   float gv[16], yv[16];
   {
-    __shared__ float gtile[kTileThreads / 64][16 * 20];
-    float* gt = gtile[__builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6))];
     const int32_t lr = r0 + (lane >> 2), lc = c0 + ((lane & 3) << 2);
     const float* gp = grad + (int64_t)min(lr, p.M - 1) * p.N + lc;
     float4 g4 = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -2080,15 +2087,28 @@ __device__ __forceinline__ void bwd16_body(
         g4.w = lc + 3 < p.N ? load_stream(gp + 3) : 0.f;
       }
     }
-    *reinterpret_cast<float4*>(gt + (lane >> 2) * 20 + ((lane & 3) << 2)) = g4;
-    wave_sync();
+    float* gw = gt + (lane >> 2) * kGs + ((lane & 3) << 2);
+    *reinterpret_cast<float4*>(gw) = g4;
+    if (kShifted) {
+      // the lane's four column offsets, as the scalar yd[] below computes them
+      const float yf = col_coords[c0];
+      float ydl[4];
 #pragma unroll
-    for (int c = 0; c < 16; c += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(gt + row * 20 + c);
-      gv[c] = v.x;
-      gv[c + 1] = v.y;
-      gv[c + 2] = v.z;
-      gv[c + 3] = v.w;
+      for (int i = 0; i < 4; ++i) ydl[i] = col_coords[min(lc + i, p.N - 1)] - yf;
+      const float4 gy = make_float4(g4.x * ydl[0], g4.y * ydl[1], g4.z * ydl[2], g4.w * ydl[3]);
+      *reinterpret_cast<float4*>(gw + 16) = gy;
+      *reinterpret_cast<float4*>(gw + 32) = make_float4(gy.x * ydl[0], gy.y * ydl[1], gy.z * ydl[2], gy.w * ydl[3]);
+    }
+    wave_sync();
+    if (!kShifted) {
+#pragma unroll
+      for (int c = 0; c < 16; c += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(gt + row * kGs + c);
+        gv[c] = v.x;
+        gv[c + 1] = v.y;
+        gv[c + 2] = v.z;
+        gv[c + 3] = v.w;
+      }
     }
   }
   // (the same 16 addresses in every lane: inside the matrix, four aligned float4 from one base)
@@ -2108,8 +2128,7 @@ __device__ __forceinline__ void bwd16_body(
   }
   // Dense tiles without the clamp mask: columns as offsets from the tile's first one (uniform:
   // scalar registers), for the moments about that column below (32 instructions a tile, repaid
-  // by 32 a round on tiles of several rounds).
-  constexpr bool kShifted = !kMaskClamp && kTransposeSums;
+  // on tiles of several rounds).
   float yd[16];
 #pragma unroll
   for (int c = 0; c < 16; ++c)
@@ -2182,13 +2201,24 @@ __device__ __forceinline__ void bwd16_body(
         const float dl = yv[0] - mu1;
         const float z0 = fmaf(wc, dl, b);
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
-          const float z = c == 0 ? z0 : fmaf(wc, yd[c], z0);
-          const float ge = gv[c] * __builtin_amdgcn_exp2f(-fmaf(z, z, A));
-          t0 += ge;
-          const float tt = ge * yd[c];
-          t2 += tt;
-          t3 = fmaf(tt, yd[c], t3);
+        for (int c4 = 0; c4 < 4; ++c4) {
+          const float4 g4 = *reinterpret_cast<const float4*>(gt + row * kGs + 4 * c4);
+          const float4 gy4 = *reinterpret_cast<const float4*>(gt + row * kGs + 16 + 4 * c4);
+          const float4 gyy4 = *reinterpret_cast<const float4*>(gt + row * kGs + 32 + 4 * c4);
+          const float gq[4] = {g4.x, g4.y, g4.z, g4.w}, gyq[4] = {gy4.x, gy4.y, gy4.z, gy4.w};
+          const float gyyq[4] = {gyy4.x, gyy4.y, gyy4.z, gyy4.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int c = 4 * c4 + i;
+            const float z = c == 0 ? z0 : fmaf(wc, yd[c], z0);
+            const float e = __builtin_amdgcn_exp2f(-fmaf(z, z, A));
+            t0 = fmaf(gq[i], e, t0);
+            t2 = fmaf(gyq[i], e, t2);
+            t3 = fmaf(gyyq[i], e, t3);
+          }
+          // keep each group's three LDS reads beside their use (hoisted, the twelve of a round
+          // would hold 48 registers)
+          __builtin_amdgcn_sched_barrier(0);
         }
         t3 = fmaf(dl, fmaf(dl, t0, 2.0f * t2), t3);
         t2 = fmaf(dl, t0, t2);
