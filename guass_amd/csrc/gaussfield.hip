@@ -2034,7 +2034,7 @@ __device__ inline void stage_gaussians(const Problem& p, const GIdx* __restrict_
 // 16 pixels.  Gaussian constants are computed one per lane for up to 64 Gaussians at a time
 // and fetched by slot with a lane permute.
 // The moments of tile t (16x16) of one field by one wave.
-template <typename TpIdx, typename GIdx, bool kTransposeSums, bool kMaskClamp>
+template <typename TpIdx, typename GIdx, bool kTransposeSums, bool kMaskClamp, bool kManyRounds = kTransposeSums>
 __device__ __forceinline__ void bwd16_body(
     const Problem& p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
@@ -2063,12 +2063,13 @@ __device__ __forceinline__ void bwd16_body(
   // once, and keeping them out of L2 keeps the accumulator and constant lines there), and each
   // lane takes its row from LDS (row stride 20 floats: the 16 rows' float4 reads fall in
   // distinct banks).
-  // Dense tiles without the clamp mask (kShifted) take their moments about the tile's first
-  // column y0 (below): each lane also stages g (y - y0) and g (y - y0)^2 for its four columns, so
-  // that a round weights one exponential with three FMAs.  LDS row stride: 52 floats there (g,
-  // g yd, g yd^2 and pad), 20 otherwise; either way the 16 rows' float4 reads fall in distinct
-  // banks.
-  constexpr bool kShifted = !kMaskClamp && kTransposeSums;
+  // Tiles of several rounds (kManyRounds: dense fields, batches, heavy-tile kernels) without
+  // the clamp mask (kShifted) take their moments about the tile's middle column y8 (below): each
+  // lane also stages g (y - y8) and g (y - y8)^2 for its four columns, so that a round weights
+  // one exponential with three FMAs.  The per-tile set-up is repaid over several rounds (at
+  // cfg3's one round a tile it is not).  LDS row stride: 52 floats there (g, g yd, g yd^2 and
+  // pad), 20 otherwise; either way the 16 rows' float4 reads fall in distinct banks.
+  constexpr bool kShifted = !kMaskClamp && kManyRounds;
   constexpr int kGs = kShifted ? 52 : 20;
   __shared__ float gtile[kTileThreads / 64][16 * 52];
   float* gt = gtile[__builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6))];
@@ -2091,7 +2092,7 @@ __device__ __forceinline__ void bwd16_body(
     *reinterpret_cast<float4*>(gw) = g4;
     if (kShifted) {
       // the lane's four column offsets, as the scalar yd[] below computes them
-      const float yf = col_coords[c0];
+      const float yf = col_coords[min(c0 + 8, p.N - 1)];
       float ydl[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) ydl[i] = col_coords[min(lc + i, p.N - 1)] - yf;
@@ -2126,13 +2127,12 @@ __device__ __forceinline__ void bwd16_body(
 #pragma unroll
     for (int c = 0; c < 16; ++c) yv[c] = col_coords[min(c0 + c, p.N - 1)];
   }
-  // Dense tiles without the clamp mask: columns as offsets from the tile's first one (uniform:
-  // scalar registers), for the moments about that column below (32 instructions a tile, repaid
-  // on tiles of several rounds).
+  // kShifted: columns as offsets from the tile's middle one, column 8 (uniform: scalar
+  // registers), for the moments about that column below.
   float yd[16];
 #pragma unroll
   for (int c = 0; c < 16; ++c)
-    yd[c] = kShifted ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(yv[c] - yv[0]))) : 0.0f;
+    yd[c] = kShifted ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(yv[c] - yv[8]))) : 0.0f;
   const float x = row_coords[min(pr, p.M - 1)];
   int64_t s = (int64_t)tile_ptr[t], e = (int64_t)tile_ptr[t + 1];
   if (lane == 0) {
@@ -2193,12 +2193,13 @@ __device__ __forceinline__ void bwd16_body(
           t3 = fmaf(tt, dy, t3);
         }
       } else if (kShifted) {
-        // Moments about the tile's first column y0: with dy = yd_c + dl, dl = y0 - mu1,
+        // Moments about the tile's middle column y8: with dy = yd_c + dl, dl = y8 - mu1,
         //   S(ge dy) = S(ge yd) + dl S(ge),  S(ge dy^2) = S(ge yd^2) + dl (2 S(ge yd) + dl S(ge)),
-        // and z = wc dy + b = wc yd_c + z0 with z0 = wc dl + b.  With clamp_quad >= 80 (or none)
+        // and z = wc dy + b = wc yd_c + z0 with z0 = wc dl + b.  The shift cancels by up to
+        // (offset / width)^2, so the origin sits mid-tile (offsets of -8..7 pixels).  With clamp_quad >= 80 (or none)
         // the clamp only floors bases below e^-40 (a difference below e^-40 |g| per pixel), so
         // the floor is dropped here and below, as in the render.
-        const float dl = yv[0] - mu1;
+        const float dl = yv[8] - mu1;
         const float z0 = fmaf(wc, dl, b);
 #pragma unroll
         for (int c4 = 0; c4 < 4; ++c4) {
@@ -2210,7 +2211,7 @@ __device__ __forceinline__ void bwd16_body(
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int c = 4 * c4 + i;
-            const float z = c == 0 ? z0 : fmaf(wc, yd[c], z0);
+            const float z = c == 8 ? z0 : fmaf(wc, yd[c], z0);
             const float e = __builtin_amdgcn_exp2f(-fmaf(z, z, A));
             t0 = fmaf(gq[i], e, t0);
             t2 = fmaf(gyq[i], e, t2);
@@ -2345,7 +2346,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
     it.q = 0;
     it.F = 1;
   }
-  bwd16_body<TpIdx, GIdx, kTransposeSums, kMaskClamp>(p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr,
+  bwd16_body<TpIdx, GIdx, kTransposeSums, kMaskClamp, kTransposeSums || kHeavy>(p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr,
                                                       gids, num_pairs, ws, L, it.st, it.q, it.F);
 }
 
