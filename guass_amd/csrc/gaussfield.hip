@@ -2034,7 +2034,10 @@ __device__ inline void stage_gaussians(const Problem& p, const GIdx* __restrict_
 // 16 pixels.  Gaussian constants are computed one per lane for up to 64 Gaussians at a time
 // and fetched by slot with a lane permute.
 // The moments of tile t (16x16) of one field by one wave.
-template <typename TpIdx, typename GIdx, bool kTransposeSums, bool kMaskClamp, bool kManyRounds = kTransposeSums>
+// kEvalGiven: ev is never null (batches), so the per-Gaussian recomputation from mu / chol_raw
+// (the exact softplus chain) is left out of the kernel, with its registers.
+template <typename TpIdx, typename GIdx, bool kTransposeSums, bool kMaskClamp, bool kManyRounds = kTransposeSums,
+          bool kEvalGiven = false>
 __device__ __forceinline__ void bwd16_body(
     const Problem& p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
@@ -2155,7 +2158,7 @@ __device__ __forceinline__ void bwd16_body(
       if (g < 0 || g >= p.K) {
         set_status(&hdr->status, g < 0 ? GF_STATUS_IDS_NEGATIVE : GF_STATUS_IDS_RANGE);
       } else {
-        my = ev ? load_eval(ev, g) : eval_geom(p, mu, chol_raw, nullptr, g);
+        my = (kEvalGiven || ev) ? load_eval(ev, g) : eval_geom(p, mu, chol_raw, nullptr, g);
         myg = (int32_t)g;
       }
     }
@@ -2281,7 +2284,7 @@ __device__ __forceinline__ void bwd16_body(
       if (lane < nj) {
         const int64_t g = (int64_t)gids[s + j0 + lane];
         if (g >= 0 && g < p.K) {
-          my = ev ? load_eval(ev, g) : eval_geom(p, mu, chol_raw, nullptr, g);
+          my = (kEvalGiven || ev) ? load_eval(ev, g) : eval_geom(p, mu, chol_raw, nullptr, g);
           myg = (int32_t)g;
         }
       }
@@ -2848,7 +2851,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(8)
   const int64_t T = (int64_t)p.R * p.C;
   const int64_t P = ly.tile_ptr[T];  // pairs beyond the id capacity were never emitted
   const float* grad = glob(reinterpret_cast<const float* const*>(plan + h->grad_table_off)[l]);
-  bwd16_body<int64_t, int64_t, true, kMaskClamp>(p, grad, ly.row_coords, ly.col_coords, ly.mu, ly.chol_raw,
+  bwd16_body<int64_t, int64_t, true, kMaskClamp, true, true>(p, grad, ly.row_coords, ly.col_coords, ly.mu, ly.chol_raw,
                                reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
                                ly.tile_ptr, ly.ids, P < ly.capacity ? P : ly.capacity, ly.bws, L,
                                sub_tile(p, (int64_t)blk - b0, wave_id()));
