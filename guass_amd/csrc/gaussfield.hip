@@ -2333,7 +2333,9 @@ __device__ __forceinline__ void bwd16_body(
 
 // Seven waves per SIMD (72 VGPRs): the rarely taken indefinite-form pass would otherwise
 // raise the register count and cost the common path occupancy.
-template <typename TpIdx, typename GIdx, bool kTransposeSums, bool kMaskClamp, bool kHeavy>
+// kEvalGiven: launched with the forward's constants (ev != null); the heavy-tile kernels always
+// are, since their tile list lives in the same workspace.
+template <typename TpIdx, typename GIdx, bool kTransposeSums, bool kMaskClamp, bool kHeavy, bool kEvalGiven = kHeavy>
 __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_bwd16(
     Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
@@ -2349,8 +2351,8 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
     it.q = 0;
     it.F = 1;
   }
-  bwd16_body<TpIdx, GIdx, kTransposeSums, kMaskClamp, kTransposeSums || kHeavy>(p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr,
-                                                      gids, num_pairs, ws, L, it.st, it.q, it.F);
+  bwd16_body<TpIdx, GIdx, kTransposeSums, kMaskClamp, kTransposeSums || kHeavy, kEvalGiven>(
+      p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gids, num_pairs, ws, L, it.st, it.q, it.F);
 }
 
 __device__ inline float wave_sum(float v) {
@@ -2936,6 +2938,13 @@ void launch_bwd16(const Problem& p, int32_t xh, hipStream_t st, const float* gra
   }
   Problem q = p;
   q.heavy = 0;
+  if constexpr (kCanHeavy) {
+    if (ev) {  // the forward's constants (FieldPlan, the autograd functions)
+      hipLaunchKernelGGL((k_bwd16<TP, GI, kTS, kMC, false, true>), dim3((unsigned)quad_grid(p)), dim3(kTileThreads),
+                         0, st, q, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L, heavy_list, heavy_count, 0);
+      return;
+    }
+  }
   hipLaunchKernelGGL((k_bwd16<TP, GI, kTS, kMC, false>), dim3((unsigned)quad_grid(p)), dim3(kTileThreads), 0, st,
                      q, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L, heavy_list, heavy_count, 0);
 }
