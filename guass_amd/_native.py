@@ -73,6 +73,7 @@ class GfBatchInfo(ctypes.Structure):
         ("n_layers", c_int32), ("has_backward", c_int32), ("tile_blocks", c_int64),
         ("emit_blocks", c_int64), ("finish_blocks", c_int64), ("plan_bytes", c_size_t),
         ("backward_buffers", c_int32), ("mask_clamp", c_int32), ("render_blocks", c_int64),
+        ("tile_render", c_int32), ("reserved", c_int32),
     ]
 
 

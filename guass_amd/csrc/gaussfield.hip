@@ -2675,10 +2675,10 @@ int64_t quad_grid(const Problem& p) {
 // ------------------------------------------------------------------------------------------
 // Batched fields (one launch per phase for many layers).  The plan buffer holds a header,
 // one BatchLayer per field and, per kernel shape, a block -> field map:
-//   tile map    4 tiles per block (backward reduce)
+//   tile map    4 tiles per block (backward reduce; render of the layers without tile pairs)
 //   emit map    4 Gaussians per block
 //   finish map  256 Gaussians per block
-//   render map  4 pairs of 16x16 tiles (or one 32x32 tile) per block
+//   render map  4 pairs of 16x16 tiles per block (layers rendered by tile pairs)
 // Each field's blocks are contiguous, so block b of a kernel handles local index
 // (b - first block of its field) * per_block + wave / thread.
 
@@ -2702,6 +2702,8 @@ struct BatchLayer {
   float* d_chol_raw;
   float* d_amp;
   int64_t tile_block0, emit_block0, finish_block0, render_block0;
+  int32_t pair_render;  // rendered by tile pairs (render map); else tile by tile (tile map)
+  int32_t pad;
 };
 
 // Plan regions after the header: layers, the tile / emission / finish block maps, the
@@ -2807,36 +2809,41 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_batch(const uint8_t* __re
       (((int64_t)blockIdx.x - b0) * (kEmitThreads / 64) + wave_id()) * (64 / kEmitLanesBatch));
 }
 
+// Layers rendered tile by tile (BatchLayer::pair_render == 0: 32x32 tiles, or 16x16 tiles whose
+// capacity reaches the emission path), over the tile map; the other layers' blocks return.
 __global__ __launch_bounds__(kTileThreads) void k_render16_batch(const uint8_t* __restrict__ plan) {
+  const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
+  int64_t b0;
+  const uint32_t blk = blockIdx.x;
+  const BatchLayer ly = batch_layer(plan, h->tile_map_off, &b0, 0, blk);
+  if (ly.pair_render) return;
+  const Problem p = ly.p;
+  render16_body(p, ly.row_coords, ly.col_coords, reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
+                ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws,
+                reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.rowmask),
+                reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.colmask),
+                sub_tile(p, (int64_t)blk - b0, wave_id()), nullptr, nullptr, 0, 1,
+                reinterpret_cast<float*>(ly.fws + ly.fl.bsq));
+}
+
+// Layers rendered by tile pairs (16x16 tiles on the mask path at every k up to the capacity):
+// a pair of horizontally adjacent tiles a wave, R x ceil(C / 2) pairs row-major, over the
+// render map (which lists only these layers).
+__global__ __launch_bounds__(kTileThreads) void k_render16x2_batch(const uint8_t* __restrict__ plan) {
   const BatchHeader* h = reinterpret_cast<const BatchHeader*>(plan);
   int64_t b0;
   const uint32_t blk = blockIdx.x;
   const BatchLayer ly = batch_layer(plan, h->render_map_off, &b0, 3, blk);
   const Problem p = ly.p;
-  const GaussEval* ev = reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval);
-  const uint32_t* rowmask = reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.rowmask);
-  const uint32_t* colmask = reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.colmask);
-  float* bsq = reinterpret_cast<float*>(ly.fws + ly.fl.bsq);
-  const int64_t idx = (int64_t)blk - b0;
-  if (p.tile_out == 32) {  // one 32x32 tile a workgroup, a quadrant a wave
-    render16_body(p, ly.row_coords, ly.col_coords, ev, ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws, rowmask,
-                  colmask, sub_tile(p, idx, wave_id()), nullptr, nullptr, 0, 1, bsq);
-    return;
-  }
-  // 16x16 tiles: a pair of horizontally adjacent tiles a wave, (R x ceil(C / 2)) pairs row-major
   const int32_t cp = (p.C + 1) / 2;
-  const int64_t pi = idx * (kTileThreads / 64) + wave_id();
+  const int64_t pi = ((int64_t)blk - b0) * (kTileThreads / 64) + wave_id();
   if (pi >= (int64_t)p.R * cp) return;
   const int32_t tr = (int32_t)pi / cp, tc = 2 * ((int32_t)pi - tr * cp);
-  if (p.W > 0) {
-    render16x2_body(p, ly.row_coords, ly.col_coords, ev, ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws,
-                    rowmask, colmask, tr, tc, bsq);
-    return;
-  }
-  // emission path (k beyond the masks): the two tiles one after the other
-  for (int32_t c = tc; c < tc + 2 && c < p.C; ++c)
-    render16_body(p, ly.row_coords, ly.col_coords, ev, ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws, rowmask,
-                  colmask, tile16(p, (int64_t)tr * p.C + c), nullptr, nullptr, 0, 1, bsq);
+  render16x2_body(p, ly.row_coords, ly.col_coords, reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
+                  ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws,
+                  reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.rowmask),
+                  reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.colmask), tr, tc,
+                  reinterpret_cast<float*>(ly.fws + ly.fl.bsq));
 }
 
 // Eight waves per SIMD: the batch's dense-tile body fits 64 VGPRs without spilling, and the
@@ -3303,7 +3310,7 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
   BatchHeader h{};
   std::vector<BatchLayer> ls(n);
   int64_t tile_blocks = 0, emit_blocks = 0, finish_blocks = 0, render_blocks = 0;
-  bool backward_buffers = true, grads_set = true;
+  bool backward_buffers = true, grads_set = true, tile_render = false;
   for (size_t i = 0; i < n; ++i) {
     const gf_layer& in = layers[i];
     BatchLayer& ly = ls[i];
@@ -3360,8 +3367,14 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
     ly.finish_block0 = finish_blocks;
     ly.render_block0 = render_blocks;
     tile_blocks += quad_grid(ly.p);
-    render_blocks += t32 ? quad_grid(ly.p)
-                         : ((int64_t)ly.p.R * ((ly.p.C + 1) / 2) + kTileThreads / 64 - 1) / (kTileThreads / 64);
+    // Tile pairs for 16x16 layers that stay on the mask path at every k up to the capacity (the
+    // grids must not change with k); the others render tile by tile over the tile map.
+    ly.pair_render = (!t32 && kc <= kMaskMaxK) ? 1 : 0;
+    ly.pad = 0;
+    if (ly.pair_render)
+      render_blocks += ((int64_t)ly.p.R * ((ly.p.C + 1) / 2) + kTileThreads / 64 - 1) / (kTileThreads / 64);
+    else
+      tile_render = true;
     const int64_t per_emit_block = (kEmitThreads / 64) * (64 / kEmitLanesBatch);
     if (ly.p.W == 0 || pc.W == 0) emit_blocks += (kc + per_emit_block - 1) / per_emit_block;  // emission path
     finish_blocks += (kc * ly.p.S + kTileThreads - 1) / kTileThreads;
@@ -3378,6 +3391,8 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
   info->emit_blocks = emit_blocks;
   info->finish_blocks = finish_blocks;
   info->render_blocks = render_blocks;
+  info->tile_render = tile_render ? 1 : 0;
+  info->reserved = 0;
   info->plan_bytes = need;
   if (!plan) return GF_OK;  // size query
   if (plan_bytes < need) return set_err(GF_E_WORKSPACE, "batch plan needs %zu bytes, got %zu", need, plan_bytes);
@@ -3420,8 +3435,14 @@ int gf_batch_forward(const void* plan, const gf_batch_info* info, uint32_t phase
     GF_LAUNCH_CHECK("k_emit_batch");
   }
   if (phases & GF_PHASE_RENDER) {
-    hipLaunchKernelGGL(k_render16_batch, dim3((unsigned)info->render_blocks), dim3(kTileThreads), 0, st, pl);
-    GF_LAUNCH_CHECK("k_render16_batch");
+    if (info->render_blocks > 0) {
+      hipLaunchKernelGGL(k_render16x2_batch, dim3((unsigned)info->render_blocks), dim3(kTileThreads), 0, st, pl);
+      GF_LAUNCH_CHECK("k_render16x2_batch");
+    }
+    if (info->tile_render) {
+      hipLaunchKernelGGL(k_render16_batch, dim3((unsigned)info->tile_blocks), dim3(kTileThreads), 0, st, pl);
+      GF_LAUNCH_CHECK("k_render16_batch");
+    }
   }
   return GF_OK;
 }

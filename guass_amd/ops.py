@@ -276,8 +276,8 @@ class FieldBatchPlan:
         self.info = info
         self._grads = None
         return (old is not None and self.plan is old_plan and
-                (old.tile_blocks, old.emit_blocks, old.finish_blocks, old.render_blocks) ==
-                (info.tile_blocks, info.emit_blocks, info.finish_blocks, info.render_blocks))
+                (old.tile_blocks, old.emit_blocks, old.finish_blocks, old.render_blocks, old.tile_render) ==
+                (info.tile_blocks, info.emit_blocks, info.finish_blocks, info.render_blocks, info.tile_render))
 
     def _stream(self) -> int:
         return N.stream_handle(self.device)

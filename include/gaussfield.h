@@ -228,8 +228,10 @@ typedef struct gf_batch_info {
   int32_t backward_buffers;      /* every layer has its backward workspace and gradient outputs */
   int32_t mask_clamp;            /* clamp_quad < 80: the backward drops clamped pixels from the
                                     quadratic-form moments (at 80 and above they are below e^-40) */
-  int64_t render_blocks;         /* workgroups of the render: 4 pairs of 16x16 tiles or one 32x32
-                                    tile each */
+  int64_t render_blocks;         /* workgroups of the tile-pair render: 4 pairs of 16x16 tiles each */
+  int32_t tile_render;           /* 1: some layer renders tile by tile (32x32 tiles, or a k capacity
+                                    past the masks), a second launch over the tile map */
+  int32_t reserved;
 } gf_batch_info;
 
 /*

@@ -197,7 +197,8 @@ def _batch_info(layers_mnk, *, tile=16, k_capacity=0):
     info = N.GfBatchInfo()
     rc = lib.gf_batch_plan(ctypes.byref(cfg), table, len(layers_mnk), None, 0, ctypes.byref(info), None)
     assert rc == 0, lib.gf_last_error().decode()
-    return (info.tile_blocks, info.emit_blocks, info.finish_blocks, info.render_blocks, info.plan_bytes)
+    return (info.tile_blocks, info.emit_blocks, info.finish_blocks, info.render_blocks, info.tile_render,
+            info.plan_bytes)
 
 
 @pytest.mark.parametrize("tile", [16, 32])

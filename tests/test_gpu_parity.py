@@ -820,6 +820,7 @@ def test_cfg4_full_batch_matches_single_fields(device):
     assert batch.info.tile_blocks == sum(-(-t // 4) for t in tiles)  # four 16x16 tiles a workgroup
     pairs_of = [(-(-p.out_features // 16)) * -(-(-(-p.in_features // 16)) // 2) for p in probs]
     assert batch.info.render_blocks == sum(-(-t // 4) for t in pairs_of)  # four tile pairs a workgroup
+    assert batch.info.tile_render == 0  # every layer renders by tile pairs
     batch.forward()
     batch.backward()
     torch.cuda.synchronize()
@@ -1393,7 +1394,7 @@ def test_one_layer_batch_survives_k_changes(device):
         return (pl.fwd_ws.data_ptr(), pl.bwd_ws.data_ptr(), pl.ids.data_ptr(), pl.delta.data_ptr(),
                 batch.plan.data_ptr(), batch.grad_flat.data_ptr())
 
-    first = (batch.info.tile_blocks, batch.info.emit_blocks, batch.info.finish_blocks, batch.info.render_blocks,
+    first = (batch.info.tile_blocks, batch.info.emit_blocks, batch.info.finish_blocks, batch.info.render_blocks, batch.info.tile_render,
              batch.info.plan_bytes)
     ptrs = pointers()
     s = torch.cuda.Stream(device)
@@ -1411,7 +1412,7 @@ def test_one_layer_batch_survives_k_changes(device):
         p = wl.make_problem(f"one_layer_k{k}", 320, 768, k, math.log(6.0), 0.7, seed)
         assert batch.update([p.to(device)]), f"K={k}: re-planned with new grids"
         assert not batch.reallocated and pointers() == ptrs, f"K={k}: a buffer was reallocated"
-        assert (batch.info.tile_blocks, batch.info.emit_blocks, batch.info.finish_blocks, batch.info.render_blocks,
+        assert (batch.info.tile_blocks, batch.info.emit_blocks, batch.info.finish_blocks, batch.info.render_blocks, batch.info.tile_render,
                 batch.info.plan_bytes) == first
         pl.delta.fill_(float("nan"))
         graph.replay()
