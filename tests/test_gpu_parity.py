@@ -753,6 +753,54 @@ def test_batch_tile_pairs_match_single_fields(device):
     assert exact >= 20 and odd >= 6
 
 
+def test_dense_tiles_narrow_gaussians_against_float64(device):
+    """Dense tiles (>= 16 pairs a tile), whose backward takes its moments about the tile's middle
+    column and shifts them to the Gaussian's centre, on sub-pixel Gaussians (sigma 0.2-0.6 px):
+    the shift cancels by up to (offset / sigma)^2, largest for narrow Gaussians near a tile's
+    edge.  Random centres and centres on tile edges; the single-field kernel (P >= 16 T) and the
+    batched one, each against the float64 evaluation of the reference program: at most 1e-5
+    further from it than the fp32 oracle (measured: 1.3e-6 further; the gradient bar is 1e-4)."""
+    from guass_amd.ops import FieldBatchPlan
+
+    probs = []
+    for seed, edges in ((71, False), (72, True)):
+        p = wl.make_problem(f"narrow_dense_s{seed}{'_edges' if edges else ''}", 256, 256, 6000, math.log(0.35), 0.3,
+                            seed)
+        if edges:  # column centres half a pixel inside a tile's first or last column
+            g = torch.Generator().manual_seed(seed)
+            tcol = torch.randint(0, 16, (p.k,), generator=g).to(torch.float64)
+            side = torch.randint(0, 2, (p.k,), generator=g).to(torch.float64)
+            px = 16.0 * tcol + 0.5 + 14.0 * side
+            p.mu[:, 1] = (2.0 * px / (p.in_features - 1) - 1.0).to(torch.float32)
+        probs.append(p)
+    worst = 0.0
+    for p in probs:
+        r = oracle(p, batched=True)
+        P = int(r[1][-1])
+        T = (-(-p.out_features // 16)) * (-(-p.in_features // 16))
+        say(f"{p.name}: P={P} ({P / T:.1f} pairs a tile)")
+        assert P >= 16 * T
+        r64 = fo.gaussian_field_fwd_bwd_fp64(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad, 16, 16, 3.0,
+                                             False, 80.0)
+        single = run_gpu(p, device)
+        batch = FieldBatchPlan([p.to(device)], device, capacities=[P])
+        batch.forward()
+        batch.backward()
+        torch.cuda.synchronize()
+        assert batch.status() == [0]
+        pl = batch.plans[0]
+        for name, a, b, c, o in zip(("d_mu", "d_chol_raw", "d_amp"), single[3:], (pl.d_mu, pl.d_chol_raw, pl.d_amp),
+                                    r64[3:], r[3:]):
+            cn = float(c.norm())
+            eo = float((o.double() - c).norm()) / cn
+            es = float((a.cpu().double() - c).norm()) / cn
+            eb = float((b.cpu().double() - c).norm()) / cn
+            say(f"  {name}: oracle {eo:.2e}, single field {es:.2e}, batch {eb:.2e} from float64")
+            worst = max(worst, es - eo, eb - eo)
+            assert es <= eo + 1e-5 and eb <= eo + 1e-5, (p.name, name, eo, es, eb)
+    say(f"  at most {worst:.1e} further from float64 than the oracle")
+
+
 # One cfg4 layer of each of the six distinct SD1.5 attention shapes (index into
 # wl.sd15_attention_shapes(): block 0 attn1.to_q 320x320, block 0 attn2.to_k 320x768, block 2
 # attn1.to_q 640x640, block 2 attn2.to_k 640x768, block 4 attn1.to_q 1280x1280, block 4
