@@ -1707,6 +1707,7 @@ __device__ __forceinline__ void render16_body(
 constexpr int32_t kPairInA = 1 << 14, kPairInB = 1 << 15, kPairIdMask = kPairInA - 1;  // ids < kMaskMaxK
 static_assert(kMaskMaxK <= kPairInA, "pair keys hold the id below the tile flags");
 
+template <bool kSkipHalves>
 __device__ __forceinline__ void render16x2_body(
     const Problem& p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* __restrict__ ids,
@@ -1783,13 +1784,20 @@ __device__ __forceinline__ void render16x2_body(
     ew[64 + lane] = make_float4(my.wc, in_a ? my.w : 0.0f, in_b ? my.w : 0.0f, __int_as_float(fl));
     const bool general = __builtin_amdgcn_ballot_w64((fl & 4) != 0) != 0;
     wave_sync();
+    // kSkipHalves (batches): a Gaussian of one tile only (a third of the union at cfg4) skips the
+    // other tile's half: the flags are the same in every lane (one Gaussian at a time), so the
+    // branch is scalar, and skipping the zero-amplitude half leaves acc as the no-op fma would.
+    // Single fields of larger Gaussians (cfg3: nearly all in both tiles) do not repay the
+    // readfirstlane and branches.
     auto definite = [&](const float4& a, const float4& b, auto free_form) {
+      const int32_t f = kSkipHalves ? __builtin_amdgcn_readfirstlane(__float_as_int(b.w)) : 3;
       const float dx = x - a.x;
       const float aa = a.z * dx;
       const float bb = a.w * dx;
       const float A = aa * aa;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
+        if ((f & (1 << h)) == 0) continue;
         const float wh = h == 0 ? b.y : b.z;
         const float z0 = fmaf(b.x, y0[h] - a.y, bb);
 #pragma unroll
@@ -1910,8 +1918,8 @@ __global__ __launch_bounds__(kTileThreads) void k_render16x2(
   const int64_t pi = (int64_t)blockIdx.x * (kTileThreads / 64) + wave_id();
   if (pi >= (int64_t)p.R * cp) return;
   const int32_t tr = (int32_t)pi / cp, tc = 2 * ((int32_t)pi - tr * cp);
-  render16x2_body(p, row_coords, col_coords, ev, tile_ptr, ids, capacity, delta, ws, rowmask, colmask, tr, tc,
-                  nullptr);
+  render16x2_body<false>(p, row_coords, col_coords, ev, tile_ptr, ids, capacity, delta, ws, rowmask, colmask, tr,
+                         tc, nullptr);
 }
 
 template <bool kHeavy>
@@ -2839,7 +2847,7 @@ __global__ __launch_bounds__(kTileThreads) void k_render16x2_batch(const uint8_t
   const int64_t pi = ((int64_t)blk - b0) * (kTileThreads / 64) + wave_id();
   if (pi >= (int64_t)p.R * cp) return;
   const int32_t tr = (int32_t)pi / cp, tc = 2 * ((int32_t)pi - tr * cp);
-  render16x2_body(p, ly.row_coords, ly.col_coords, reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
+  render16x2_body<true>(p, ly.row_coords, ly.col_coords, reinterpret_cast<const GaussEval*>(ly.fws + ly.fl.eval),
                   ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws,
                   reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.rowmask),
                   reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.colmask), tr, tc,
