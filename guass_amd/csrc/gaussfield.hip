@@ -2110,6 +2110,9 @@ __device__ __forceinline__ void bwd16_body(
       const float4 gy = make_float4(g4.x * ydl[0], g4.y * ydl[1], g4.z * ydl[2], g4.w * ydl[3]);
       *reinterpret_cast<float4*>(gw + 16) = gy;
       *reinterpret_cast<float4*>(gw + 32) = make_float4(gy.x * ydl[0], gy.y * ydl[1], gy.z * ydl[2], gy.w * ydl[3]);
+      // the 16 column offsets, a float4 per column group in the pad of rows 0..3, for the split
+      // rounds below (whose lanes take different columns)
+      if (lane < 4) *reinterpret_cast<float4*>(gt + lane * kGs + 48) = make_float4(ydl[0], ydl[1], ydl[2], ydl[3]);
     }
     wave_sync();
     if (!kShifted) {
@@ -2171,8 +2174,19 @@ __device__ __forceinline__ void bwd16_body(
       }
     }
     const bool chunk_general = __builtin_amdgcn_ballot_w64(lane < nj && my.gen != 0.0f) != 0;
-    for (int jb = 0; jb < nj; jb += 4) {
-      const int j = jb + slot;
+    // kShifted: a last round of one or two Gaussians splits their columns over the four slots
+    // (two slots of eight columns each, or four of four) instead of leaving slots empty, and the
+    // slots' partial moments are added before the atomics.  That round is the second pass of
+    // the unrolled loop below (split is a constant in each copy), so that the full rounds carry
+    // none of its work.
+    const int tail = kShifted && ((nj & 3) == 1 || (nj & 3) == 2) ? (nj & 3) : 0;
+#pragma unroll
+    for (int pass = 0; pass < (kShifted ? 2 : 1); ++pass) {
+    const bool split = pass == 1;
+    for (int jb = split ? nj - tail : 0; jb < (split ? nj : nj - tail); jb += 4) {
+      const int rem = nj - jb;  // wave-uniform
+      const int j = split ? jb + (rem == 2 ? slot >> 1 : 0) : jb + slot;
+      const int part = split ? (rem == 2 ? slot & 1 : slot) : 0;
       const int addr = j < nj ? j << 2 : 0;  // ds_bpermute byte address of the slot's lane
       auto from = [&](float v) { return __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(v))); };
       const float mu0 = from(my.mu0), mu1 = from(my.mu1);
@@ -2212,6 +2226,26 @@ __device__ __forceinline__ void bwd16_body(
         // the floor is dropped here and below, as in the render.
         const float dl = yv[8] - mu1;
         const float z0 = fmaf(wc, dl, b);
+        if (split) {
+          // rem column groups (of four) per slot: groups part * rem .. part * rem + rem - 1
+          for (int k = 0; k < rem; ++k) {
+            const int c4 = part * rem + k;
+            const float4 g4 = *reinterpret_cast<const float4*>(gt + row * kGs + 4 * c4);
+            const float4 gy4 = *reinterpret_cast<const float4*>(gt + row * kGs + 16 + 4 * c4);
+            const float4 gyy4 = *reinterpret_cast<const float4*>(gt + row * kGs + 32 + 4 * c4);
+            const float4 yd4 = *reinterpret_cast<const float4*>(gt + c4 * kGs + 48);
+            const float gq[4] = {g4.x, g4.y, g4.z, g4.w}, gyq[4] = {gy4.x, gy4.y, gy4.z, gy4.w};
+            const float gyyq[4] = {gyy4.x, gyy4.y, gyy4.z, gyy4.w}, ydq[4] = {yd4.x, yd4.y, yd4.z, yd4.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float z = fmaf(wc, ydq[i], z0);
+              const float e = __builtin_amdgcn_exp2f(-fmaf(z, z, A));
+              t0 = fmaf(gq[i], e, t0);
+              t2 = fmaf(gyq[i], e, t2);
+              t3 = fmaf(gyyq[i], e, t3);
+            }
+          }
+        } else {
 #pragma unroll
         for (int c4 = 0; c4 < 4; ++c4) {
           const float4 g4 = *reinterpret_cast<const float4*>(gt + row * kGs + 4 * c4);
@@ -2231,6 +2265,7 @@ __device__ __forceinline__ void bwd16_body(
           // keep each group's three LDS reads beside their use (hoisted, the twelve of a round
           // would hold 48 registers)
           __builtin_amdgcn_sched_barrier(0);
+        }
         }
         t3 = fmaf(dl, fmaf(dl, t0, 2.0f * t2), t3);
         t2 = fmaf(dl, t0, t2);
@@ -2256,8 +2291,14 @@ __device__ __forceinline__ void bwd16_body(
         const float s3 = dpp_row_sum_f32(m3), s4 = dpp_row_sum_f32(m4), s5 = dpp_row_sum_f32(m5);
         const float v0 = dpp_f32<0x105>(s0), v1 = dpp_f32<0x104>(s1), v2 = dpp_f32<0x103>(s2);
         const float v3 = dpp_f32<0x102>(s3), v4 = dpp_f32<0x101>(s4);
-        if (g >= 0 && row >= 10) {
-          const int k = row - 10;
+        const int k = row - 10;
+        if (split) {  // the Gaussian's slots: 0 + 1 and 2 + 3 (two Gaussians) or all four
+          float val = k == 0 ? v0 : k == 1 ? v1 : k == 2 ? v2 : k == 3 ? v3 : k == 4 ? v4 : s5;
+          val += __shfl_xor(val, 16, 64);
+          if (rem == 1) val += __shfl_xor(val, 32, 64);
+          if (g >= 0 && row >= 10 && part == 0)
+            unsafeAtomicAdd(acc_s + (8u * (uint64_t)(uint32_t)g + (uint32_t)k), val);
+        } else if (g >= 0 && row >= 10) {
           const float val = k == 0 ? v0 : k == 1 ? v1 : k == 2 ? v2 : k == 3 ? v3 : k == 4 ? v4 : s5;
           unsafeAtomicAdd(acc_s + (8u * (uint64_t)(uint32_t)g + (uint32_t)k), val);
         }
@@ -2276,7 +2317,13 @@ __device__ __forceinline__ void bwd16_body(
       const float c1 = (hb2 ? a3 : a1) + dpp_f32<0x141>(hb2 ? a1 : a3);
       float d = (hb1 ? c1 : c0) + dpp_f32<0x4e>(hb1 ? c0 : c1);
       d += dpp_f32<0xb1>(d);
-      if (g >= 0 && atomic_lane) unsafeAtomicAdd(acc_s + (8u * (uint64_t)(uint32_t)g + (uint32_t)(row >> 1)), d);
+      if (split) {  // the Gaussian's slots: 0 + 1 and 2 + 3 (two Gaussians) or all four
+        d += __shfl_xor(d, 16, 64);
+        if (rem == 1) d += __shfl_xor(d, 32, 64);
+      }
+      if (g >= 0 && atomic_lane && part == 0)
+        unsafeAtomicAdd(acc_s + (8u * (uint64_t)(uint32_t)g + (uint32_t)(row >> 1)), d);
+    }
     }
     tile_general = tile_general || chunk_general;
   }
