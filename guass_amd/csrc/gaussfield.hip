@@ -2085,6 +2085,7 @@ __device__ __forceinline__ void bwd16_body(
   __shared__ float gtile[kTileThreads / 64][16 * 52];
   float* gt = gtile[__builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6))];
   float gv[16], yv[16];
+  float ydl[4] = {0.f, 0.f, 0.f, 0.f};  // kShifted: the lane's four column offsets from column 8
   {
     const int32_t lr = r0 + (lane >> 2), lc = c0 + ((lane & 3) << 2);
     const float* gp = grad + (int64_t)min(lr, p.M - 1) * p.N + lc;
@@ -2102,9 +2103,8 @@ __device__ __forceinline__ void bwd16_body(
     float* gw = gt + (lane >> 2) * kGs + ((lane & 3) << 2);
     *reinterpret_cast<float4*>(gw) = g4;
     if (kShifted) {
-      // the lane's four column offsets, as the scalar yd[] below computes them
+      // the lane's four column offsets (lanes 0..3 hold the tile's 16, the scalar yd[] below)
       const float yf = col_coords[min(c0 + 8, p.N - 1)];
-      float ydl[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) ydl[i] = col_coords[min(lc + i, p.N - 1)] - yf;
       const float4 gy = make_float4(g4.x * ydl[0], g4.y * ydl[1], g4.z * ydl[2], g4.w * ydl[3]);
@@ -2142,11 +2142,11 @@ __device__ __forceinline__ void bwd16_body(
     for (int c = 0; c < 16; ++c) yv[c] = col_coords[min(c0 + c, p.N - 1)];
   }
   // kShifted: columns as offsets from the tile's middle one, column 8 (uniform: scalar
-  // registers), for the moments about that column below.
+  // registers), for the moments about that column below: column c's is lane c / 4's ydl[c % 4].
   float yd[16];
 #pragma unroll
   for (int c = 0; c < 16; ++c)
-    yd[c] = kShifted ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(yv[c] - yv[8]))) : 0.0f;
+    yd[c] = kShifted ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ydl[c & 3]), c >> 2)) : 0.0f;
   const float x = row_coords[min(pr, p.M - 1)];
   int64_t s = (int64_t)tile_ptr[t], e = (int64_t)tile_ptr[t + 1];
   if (lane == 0) {
