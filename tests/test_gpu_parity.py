@@ -841,6 +841,48 @@ def test_batch_sd15_layers_against_oracle(device):
             grad_close(a, b, name)
 
 
+def test_batch_split_last_rounds(device):
+    """A batch layer whose tiles hold 0..10 Gaussians (and 65, 66: second chunks of one and two),
+    each Gaussian inside one tile: the batched backward takes a tile's last round of one or two
+    Gaussians over all four slots (their columns split, the slots' moments added before the
+    atomics). Binning, field and gradients against the CPU oracle."""
+    from guass_amd.ops import FieldBatchPlan
+
+    M = N = 80
+    counts = [t % 11 for t in range(25)]
+    counts[23], counts[24] = 65, 66
+    g = torch.Generator().manual_seed(11)
+    f64 = torch.float64
+    centres = []
+    for t, c in enumerate(counts):
+        tr, tc = divmod(t, 5)
+        base = torch.tensor([tr * 16 + 7.5, tc * 16 + 7.5], dtype=f64)
+        centres.append(base + (torch.rand(c, 2, generator=g, dtype=f64) * 4.0 - 2.0))
+    mean_px = torch.cat(centres)
+    K = mean_px.shape[0]
+    # sigma 0.8..1.25 px: the 3-sigma box of a centre within 2 px of the tile's middle stays inside the tile
+    log_scale = 0.1 * torch.randn(K, 2, generator=g, dtype=f64).clamp(-2.0, 2.0)
+    theta = torch.rand(K, generator=g, dtype=f64) * math.pi
+    amp = torch.randn(K, generator=g, dtype=f64)
+    mu, raw, amp32 = wl.pixel_to_params(M, N, mean_px, log_scale, theta, amp)
+    rc, cc = wl.axes(M, N)
+    grad = torch.randn(M * N, generator=g, dtype=f64).to(torch.float32)
+    p = wl.FieldProblem("split_rounds", M, N, rc, cc, mu, raw, amp32, grad)
+    say(f"split rounds: K={K} counts={counts}")
+    r = oracle(p, batched=True)
+    assert (r[1][1:] - r[1][:-1]).tolist() == counts  # one tile per Gaussian, as constructed
+    batch = FieldBatchPlan([p.to(device)], device, capacities=[int(r[1][-1])])
+    batch.forward()
+    batch.backward()
+    torch.cuda.synchronize()
+    assert batch.status() == [0]
+    pl = batch.plans[0]
+    binning_equal(pl.tile_ptr, pl.ids[:int(r[1][-1])], r[1], r[2])
+    field_close(pl.delta, r[0])
+    for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), r[3:]):
+        grad_close(a, b, name)
+
+
 def test_cfg4_full_batch_matches_single_fields(device):
     """BASELINE cfg4 at its workload: all 128 SD1.5 attention layers (K = 1024 each) as one
     FieldBatchPlan, forward and backward, against each layer's own single-field run (the drop-in
