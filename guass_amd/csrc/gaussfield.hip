@@ -1077,7 +1077,9 @@ __device__ __forceinline__ void emit_body(const Problem& p, const float* __restr
     for (int j = 0; j < B; ++j) {
       if (lb + sl + j * SG < n) {
         const int64_t pos = bases[j] + (int64_t)slots[j];
-        if (pos < capacity) {
+        if (pos < 0) {
+          set_status(&hdr->status, GF_STATUS_TILE_PTR_ORDER);
+        } else if (pos < capacity) {
           ids[pos] = g;
         } else {
           set_status(&hdr->status, GF_STATUS_CAPACITY);
@@ -1306,6 +1308,7 @@ __device__ void order_segment_wave(int64_t* seg, int64_t n, int64_t K, int32_t* 
 __device__ inline void tile_range(const int64_t* __restrict__ tile_ptr, int64_t t, int64_t capacity,
                                   int64_t* s, int64_t* n) {
   int64_t a = tile_ptr[t], b = tile_ptr[t + 1];
+  if (a < 0) a = 0;  // (a segment never starts below the id buffer)
   if (b > capacity) b = capacity;
   if (a > b) a = b;
   *s = a;
@@ -1567,7 +1570,9 @@ __device__ __forceinline__ void render16_body(
       count = tile_ptr[t + 1] - s;
       if (F == 1 && p.heavy > 0 && count > p.heavy) return;  // a heavy-tile workgroup's
     }
-    const int64_t room = capacity - s < count ? (capacity - s > 0 ? capacity - s : 0) : count;
+    // ids are written to [s, s + room): none for a segment below the id buffer or reversed
+    const int64_t room = s < 0 ? 0 : capacity - s < count ? (capacity - s > 0 ? capacity - s : 0) : count;
+    if ((s < 0 || count < 0) && write_ids && lane == 0) set_status(&hdr->status, GF_STATUS_TILE_PTR_ORDER);
     const uint32_t* rm = rowmask + (int64_t)tr * p.W;
     const uint32_t* cm = colmask + (int64_t)tc * p.W;
     int32_t* keys = wkeys[wid];
@@ -1745,10 +1750,12 @@ __device__ __forceinline__ void render16x2_body(
   // The two segments are adjacent: [sa, sb) and [sb, se).
   const int64_t sa = tile_ptr[ta], sb = tile_ptr[ta + 1], se = has_b ? tile_ptr[ta + 2] : sb;
   const int64_t cnt_a = sb - sa, cnt_b = se - sb;
+  // ids are written to [s, s + room): none for a segment below the id buffer or reversed
   auto room_of = [&](int64_t s, int64_t count) {
-    return capacity - s < count ? (capacity - s > 0 ? capacity - s : 0) : count;
+    return s < 0 ? 0 : capacity - s < count ? (capacity - s > 0 ? capacity - s : 0) : count;
   };
   const int64_t room_a = room_of(sa, cnt_a), room_b = room_of(sb, cnt_b);
+  if ((sa < 0 || cnt_a < 0 || cnt_b < 0) && lane == 0) set_status(&hdr->status, GF_STATUS_TILE_PTR_ORDER);
   const uint32_t* rm = rowmask + (int64_t)tr * p.W;
   const uint32_t* cma = colmask + (int64_t)tc * p.W;
   const uint32_t* cmb = cma + p.W;  // read only when has_b

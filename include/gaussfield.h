@@ -38,7 +38,7 @@ extern "C" {
 #define GF_STATUS_CAPACITY 0x1u        /* more pairs than ids_capacity: ids truncated        */
 #define GF_STATUS_COUNT_MISMATCH 0x2u  /* per-tile counts disagree with per-Gaussian sums    */
 #define GF_STATUS_TILE_PTR_LAST 0x4u   /* backward: tile_ptr[T] != number of pairs           */
-#define GF_STATUS_TILE_PTR_ORDER 0x8u  /* backward: tile_ptr decreasing / outside [0, pairs] */
+#define GF_STATUS_TILE_PTR_ORDER 0x8u  /* render / backward: tile_ptr decreasing / below 0 / outside [0, pairs] */
 #define GF_STATUS_IDS_NEGATIVE 0x10u   /* backward: a gaussian id < 0                        */
 #define GF_STATUS_IDS_RANGE 0x20u      /* backward: a gaussian id >= K                       */
 
