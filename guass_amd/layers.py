@@ -294,6 +294,13 @@ class GaussianFieldBatch:
     grows the capacities and renders again.  All layers must share the tile shape
     (16x16 or 32x32: the batched kernels), sigma multiplier and normalisation.
 
+    ``render(check=False)`` skips the read-back: no host synchronisation at all, so that a step
+    of render + forward + backward can be captured in a HIP graph and replayed.  It needs the
+    plan of an earlier checked render (the same parameter tensors and K, id capacities that
+    held); ``check()`` then reads back every layer's status, pair count and norm once, e.g. after
+    a number of replays, and raises if a layer's pairs passed its id capacity (a checked
+    render() grows them; capture again after it).
+
     Densification (the reference trainer's clone / prune, base_trainer.py:126-220) replaces a
     layer's Gaussian parameters with tensors of another K; the next render() re-plans in place.
     ``k_capacity`` (an int for every layer, or one per layer; e.g. the densify config's
@@ -336,6 +343,8 @@ class GaussianFieldBatch:
         self._ks = [ly.num_gaussians for ly in self.layers]
         self._pairs = None
         self._zero_grads: dict[int, Tensor] = {}
+        self._norms: list[float] = []
+        self._check = True  # the next forward reads back (render(check=...))
         self.replans = 0  # re-plans after the first plan (parameter tensors or K changed)
 
     # ---------------------------------------------------------------- plan
@@ -389,9 +398,15 @@ class GaussianFieldBatch:
 
     # ---------------------------------------------------------------- passes
 
-    def render(self) -> list[Tensor]:
+    def render(self, check: bool = True) -> list[Tensor]:
         """Renders every layer's delta-W for this step (autograd-tracked) and hands each layer
-        its own for its next forward; returns them."""
+        its own for its next forward; returns them.  ``check=False``: no read-back (see the
+        class documentation); each layer's norm metadata is then that of the last checked
+        render."""
+        if not check and (self._plan is None or self._key != self._param_key()):
+            raise RuntimeError("render(check=False) needs the plan of an earlier checked render() "
+                               "with the same parameter tensors and K")
+        self._check = bool(check)
         ctx = torch.autocast(device_type="cuda", enabled=False) if self.device.type == "cuda" else _null()
         with ctx:
             params = []
@@ -402,8 +417,25 @@ class GaussianFieldBatch:
             ly._batched_delta = (d, nrm)
         return list(deltas)
 
+    def check(self) -> list[int]:
+        """Every layer's pair count of the last forward, from one read-back (synchronises).
+        Raises on a device status bit, e.g. a layer whose pairs passed its id capacity during
+        unchecked renders."""
+        Nat = self._Nat
+        status, pairs, self._norms = self._plan.read(clear=True, norms=True)
+        bad = [(i, st) for i, st in enumerate(status) if st]
+        if bad:
+            raise RuntimeError(f"batched fields: device status {bad} (layer, GF_STATUS_* bits; "
+                               f"GF_STATUS_CAPACITY = {Nat.GF_STATUS_CAPACITY}: render() with check=True "
+                               "grows the id capacities)")
+        self._pairs = pairs
+        return pairs
+
     def _run_forward(self) -> list[Tensor]:
         Nat = self._Nat
+        if not self._check:
+            self._plan.forward()
+            return self._deltas
         if self._plan is None or self._key != self._param_key():
             self._build()
         for _ in range(8):

@@ -1215,6 +1215,130 @@ def test_gaussian_field_batch_matches_per_layer(device, tile):
                     pb.copy_(pa)
 
 
+@pytest.mark.skip(reason="kept off the GPU: capturing this step (autograd with the layers' hipBLASLt GEMMs "
+                         "around the batched field kernels) ended the host process with a segmentation fault "
+                         "in torch.cuda.graph's capture_end; no cause in this library's code has been shown")
+def test_gaussian_field_batch_graph_step(device):
+    """A training step through GaussianFieldBatch (render(check=False), the layers' forwards,
+    autograd's backward) captured in a HIP graph and replayed three times, with eager work,
+    cleared outputs and synchronisations between the replays: every replay's delta-W and
+    gradients against an eager step on the same parameters; check() then reads back once."""
+    from guass_amd.layers import GaussianAdapterConfig, GaussianFieldBatch, GaussianLinear
+
+    torch.manual_seed(5)
+    shapes = [(96, 80, 48), (64, 64, 24), (120, 40, 36), (160, 96, 64)]  # (in, out, K)
+    layers = []
+    for n_in, n_out, k in shapes:
+        cfg = GaussianAdapterConfig(init_num_gaussians=k, tile_out=16, tile_in=16, adapter_scale=0.5,
+                                    init_amp_scale=1e-2)
+        ly = GaussianLinear(n_in, n_out, adapter_config=cfg, device=device)
+        with torch.no_grad():
+            ly.chol_raw.add_(torch.randn_like(ly.chol_raw) * 0.2)
+        layers.append(ly)
+    named = [(f"layer {i} {n}", getattr(ly, n)) for i, ly in enumerate(layers) for n in ("mu_raw", "chol_raw", "amp")]
+    xs = [torch.randn(6, n_in, device=device) for n_in, _, _ in shapes]
+    gys = [torch.randn(6, n_out, device=device) for _, n_out, _ in shapes]
+    fb = GaussianFieldBatch(layers)
+
+    def step(check):
+        deltas = fb.render(check=check)
+        torch.autograd.backward([ly(x) for ly, x in zip(layers, xs)], gys)
+        return deltas
+
+    with pytest.raises(RuntimeError, match="earlier checked render"):
+        fb.render(check=False)  # no plan yet
+    say("GaussianFieldBatch step in a HIP graph: eager reference")
+    for _, t in named:
+        t.grad = None
+    ref_d = [d.detach().clone() for d in step(True)]
+    ref_g = [t.grad.clone() for _, t in named]
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):  # warm-up of the unchecked step off the default stream
+        for _ in range(2):
+            for _, t in named:
+                t.grad = None
+            step(False)
+    torch.cuda.current_stream(device).wait_stream(stream)
+    torch.cuda.synchronize()
+    for _, t in named:
+        t.grad = None
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        deltas = step(False)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        say(f"  replay {rep}")
+        junk = torch.randn(1 << 16, device=device)
+        float(junk.sum())  # eager work and a synchronisation between the replays
+        with torch.no_grad():
+            for d in deltas:
+                d.fill_(float("nan"))
+            for _, t in named:
+                t.grad.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (d, r) in enumerate(zip(deltas, ref_d)):
+            assert torch.equal(d, r), f"replay {rep} layer {i}: delta-W"
+        for (name, t), r in zip(named, ref_g):
+            grad_close(t.grad, r, f"replay {rep} {name}", rtol=1e-5)
+    pairs = fb.check()
+    assert len(pairs) == len(layers) and all(n > 0 for n in pairs)
+
+
+def test_gaussian_field_batch_unchecked_render(device):
+    """render(check=False) skips the read-back and renders with the plan of the last checked
+    render: over two eager steps its delta-W equals the checked render's and its gradients agree;
+    check() reads back afterwards; an unchecked render without a plan, or after the parameter
+    tensors changed, raises."""
+    from guass_amd.layers import GaussianAdapterConfig, GaussianFieldBatch, GaussianLinear
+
+    torch.manual_seed(5)
+    shapes = [(96, 80, 48), (64, 64, 24), (120, 40, 36)]  # (in, out, K)
+    layers = []
+    for n_in, n_out, k in shapes:
+        cfg = GaussianAdapterConfig(init_num_gaussians=k, tile_out=16, tile_in=16, adapter_scale=0.5,
+                                    init_amp_scale=1e-2)
+        ly = GaussianLinear(n_in, n_out, adapter_config=cfg, device=device)
+        with torch.no_grad():
+            ly.chol_raw.add_(torch.randn_like(ly.chol_raw) * 0.2)
+        layers.append(ly)
+    named = [(f"layer {i} {n}", getattr(ly, n)) for i, ly in enumerate(layers) for n in ("mu_raw", "chol_raw", "amp")]
+    xs = [torch.randn(6, n_in, device=device) for n_in, _, _ in shapes]
+    gys = [torch.randn(6, n_out, device=device) for _, n_out, _ in shapes]
+    fb = GaussianFieldBatch(layers)
+
+    def step(check):
+        for _, t in named:
+            t.grad = None
+        deltas = [d.detach().clone() for d in fb.render(check=check)]
+        torch.autograd.backward([ly(x) for ly, x in zip(layers, xs)], gys)
+        torch.cuda.synchronize()
+        return deltas, [t.grad.clone() for _, t in named]
+
+    with pytest.raises(RuntimeError, match="earlier checked render"):
+        fb.render(check=False)
+    ref_d, ref_g = step(True)
+    norms = [ly.last_forward_metadata["delta_w_norm"] for ly in layers]
+    for rep in range(2):
+        d, g = step(False)
+        for i, (a, b) in enumerate(zip(d, ref_d)):
+            assert torch.equal(a, b), f"unchecked render {rep} layer {i}: delta-W"
+        for (name, _), a, b in zip(named, g, ref_g):
+            grad_close(a, b, f"unchecked render {rep} {name}", rtol=1e-5)
+        # the norm metadata is the last checked render's
+        assert [ly.last_forward_metadata["delta_w_norm"] for ly in layers] == norms
+    pairs = fb.check()
+    assert len(pairs) == len(layers) and all(n > 0 for n in pairs)
+    with torch.no_grad():  # new parameter tensors: the unchecked render refuses
+        layers[0].replace_gaussian_parameters_(mu_raw=layers[0].mu_raw.detach().clone(),
+                                               chol_raw=layers[0].chol_raw.detach().clone(),
+                                               amp=layers[0].amp.detach().clone())
+    with pytest.raises(RuntimeError, match="earlier checked render"):
+        fb.render(check=False)
+
+
 def _densify_clone(layer, idx, noise):
     """The reference's clone (controllers/clone.py:31-56): the selected Gaussians are appended
     with mu_raw + noise, and the originals and the clones each keep half the amplitude."""
