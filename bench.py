@@ -207,6 +207,10 @@ def model_bench(args) -> int:
         fb.render()  # every layer's delta-W, one read-back; each layer's forward consumes its own
         torch.autograd.backward([ly(x) for ly, x in zip(layers, xs)], gys)
 
+    def batched_unchecked():  # the same step without the read-back (checked once afterwards)
+        fb.render(check=False)
+        torch.autograd.backward([ly(x) for ly, x in zip(layers, xs)], gys)
+
     def per_layer():  # the reference's step: each layer renders its delta-W in its forward
         torch.autograd.backward([ly(x) for ly, x in zip(layers, xs)], gys)
 
@@ -223,6 +227,8 @@ def model_bench(args) -> int:
         return (time.perf_counter() - t0) / steps
 
     t_batch = timed(batched, args.steps, args.warmup)
+    t_unchecked = timed(batched_unchecked, args.steps, args.warmup)
+    fb.check()  # one read-back after the unchecked steps (raises on a status bit)
     if args.skip_per_layer:  # e.g. to trace the batched steps alone
         print(json.dumps({"config": "cfg4-model", "batched_ms_per_step": t_batch * 1e3,
                           "steps": args.steps, "warmup": args.warmup}), flush=True)
@@ -240,6 +246,7 @@ def model_bench(args) -> int:
                                f"layer's forward on {args.model_tokens} rows, autograd backward (eager)",
                    "layers": len(probs), "sum_out_x_in": int(elements), "k_per_layer": 1024,
                    "tokens_per_layer": args.model_tokens, "delta_apply": args.delta_apply},
+        "unchecked_ms_per_step": t_unchecked * 1e3,
         "per_layer_ms_per_step": t_single * 1e3,
         "speedup_vs_per_layer": t_single / t_batch,
         "densify": densify,
