@@ -3436,9 +3436,11 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
     ly.finish_block0 = finish_blocks;
     ly.render_block0 = render_blocks;
     tile_blocks += quad_grid(ly.p);
-    // Tile pairs for 16x16 layers that stay on the mask path at every k up to the capacity (the
-    // grids must not change with k); the others render tile by tile over the tile map.
-    ly.pair_render = (!t32 && kc <= kMaskMaxK) ? 1 : 0;
+    // Tile pairs for 16x16 layers on the mask path at the capacity, hence at every 1 <= k <= kc
+    // (each condition of the mask path bounds K from above; the grids must not change with k).
+    // The others render tile by tile over the tile map: layers past the masks' K, and layers
+    // narrower than a tile, whose tile make_problem clamps to the matrix (emission path).
+    ly.pair_render = (!t32 && pc.W > 0) ? 1 : 0;
     ly.pad = 0;
     if (ly.pair_render)
       render_blocks += ((int64_t)ly.p.R * ((ly.p.C + 1) / 2) + kTileThreads / 64 - 1) / (kTileThreads / 64);

@@ -883,6 +883,86 @@ def test_batch_split_last_rounds(device):
         grad_close(a, b, name)
 
 
+def test_batch_layers_narrower_than_a_tile(device):
+    """Layers with fewer rows or columns than the 16x16 tile (one tile row or column; the tile is
+    clamped to the matrix, which takes them off the mask path) in a batch with an ordinary
+    layer: each renders tile by tile from emitted ids, against the CPU oracle (they used to be
+    planned for the tile-pair render, which found no mask words: delta-W zero, status
+    COUNT_MISMATCH)."""
+    from guass_amd.ops import FieldBatchPlan
+
+    specs = [("rows2", 2, 120, 300, 5062, 1, 3.0), ("cols10", 368, 10, 2500, 5049, 0, math.log(3.0)),
+             ("tiny", 3, 5, 7, 11, 0, 0.0), ("plain", 64, 80, 200, 12, 0, math.log(4.0))]
+    probs = [wl.make_problem(n, M, N, K, ls, 0.5, seed, clusters=cl, cluster_sigma_px=max(4.0, 0.05 * min(M, N)))
+             for n, M, N, K, seed, cl, ls in specs]
+    refs = [oracle(p, batched=True) for p in probs]
+    batch = FieldBatchPlan([p.to(device) for p in probs], device, capacities=[max(1, int(r[1][-1])) for r in refs])
+    batch.forward()
+    batch.backward()
+    torch.cuda.synchronize()
+    assert batch.status() == [0] * len(probs)
+    for p, pl, r in zip(probs, batch.plans, refs):
+        say(f"  {p.name} {p.out_features}x{p.in_features} K={p.k}: pairs={int(r[1][-1])}")
+        binning_equal(pl.tile_ptr, pl.ids[:int(r[1][-1])], r[1], r[2])
+        field_close(pl.delta, r[0])
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), r[3:]):
+            grad_close(a, b, name)
+
+
+def test_random_fields_sweep(device):
+    """40 seeded random fields (ragged sizes from 1 to 520, K from 0 to 2500, tiles 16, 32, 8, 24
+    and mixed, normalisation, clamp 24 / 80 / 200 / none, clustered means, int32 and int64 ids)
+    through the drop-in path against the CPU oracle; then the 16x16 fields, and the 32x32 fields
+    of at least 32 rows and columns, as batches per clamp, against their single-field runs."""
+    import random
+
+    from guass_amd.ops import FieldBatchPlan
+
+    rng = random.Random(4242)
+    groups = {}
+    for case in range(40):
+        s = 4242 + case
+        M, N = rng.randint(1, 520), rng.randint(1, 520)
+        K = rng.choice([0, 1, 5, 63, 64, 65, 300, 1024, 2500])
+        tile = rng.choice([16, 16, 16, 32, 8, 24])
+        tile_in = tile if rng.random() < 0.8 else rng.choice([16, 32])
+        normalize = rng.random() < 0.3
+        clamp = rng.choice([80.0, 80.0, 200.0, 24.0, None])
+        clusters = rng.choice([0, 0, 1, 3])
+        ls = math.log(rng.choice([0.4, 1.0, 3.0, 8.0, 20.0]))
+        idx = rng.choice([torch.int64, torch.int32])
+        p = wl.make_problem(f"sweep{s}", M, N, K, ls, 0.5, s, clusters=clusters,
+                            cluster_sigma_px=max(4.0, 0.05 * min(M, N)))
+        kw = dict(tile_out=tile, tile_in=tile_in, normalize=normalize, clamp=clamp, index_dtype=idx)
+        say(f"case {case}: M={M} N={N} K={K} {kw} clusters={clusters} log-scale {ls:.2f}")
+        g = run_gpu(p, device, **kw)
+        r = oracle(p, **{k: v for k, v in kw.items() if k != "index_dtype"})
+        binning_equal(g[1], g[2], r[1], r[2])
+        field_close(g[0], r[0])
+        if K:
+            for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), g[3:], r[3:]):
+                grad_close(a, b, name)
+        eligible = K > 0 and tile == tile_in and clamp is not None and not normalize and (
+            tile == 16 or (tile == 32 and M >= 32 and N >= 32))
+        if eligible:
+            groups.setdefault((tile, clamp), []).append((p, g))
+    for (tile, clamp), items in groups.items():
+        say(f"batch of {len(items)} fields, tile {tile}, clamp {clamp}")
+        batch = FieldBatchPlan([p.to(device) for p, _ in items], device,
+                               capacities=[max(1, int(g[1][-1])) for _, g in items], tile_out=tile,
+                               tile_in=tile, clamp_quad=clamp)
+        batch.forward()
+        batch.backward()
+        torch.cuda.synchronize()
+        assert batch.status() == [0] * len(items)
+        for (p, g), pl in zip(items, batch.plans):
+            P = int(g[1][-1])
+            binning_equal(pl.tile_ptr, pl.ids[:P], g[1].cpu(), g[2].cpu())
+            field_close(pl.delta, g[0].cpu())
+            for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (pl.d_mu, pl.d_chol_raw, pl.d_amp), g[3:]):
+                grad_close(a, b.cpu(), name)
+
+
 def test_cfg4_full_batch_matches_single_fields(device):
     """BASELINE cfg4 at its workload: all 128 SD1.5 attention layers (K = 1024 each) as one
     FieldBatchPlan, forward and backward, against each layer's own single-field run (the drop-in
