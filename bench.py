@@ -5,7 +5,9 @@ A step is one forward (binning + render) and one backward (gradient reduction + 
 with inputs resident in HBM, issued through the sync-free C ABI path and replayed from a HIP
 graph.  Workloads:
   cfg3 (default, the headline)  one 1280x1280 fp32 delta-W from K=1024 Gaussians
-                                (guass_amd.ops.FieldPlan: five launches per step)
+                                (guass_amd.ops.FieldPlan: three forward launches and the
+                                one-launch backward_direct, which applies the chain rule per
+                                tile; fields it does not take run reduction + finish)
   cfg4                          all 128 attention linears of an SD1.5-shaped UNet, K=1024 each,
                                 as one batch (guass_amd.ops.FieldBatchPlan: five launches per
                                 step for all layers)
@@ -415,17 +417,25 @@ def main() -> int:
         plan = FieldPlan(probs[0].out_features, probs[0].in_features, probs[0].k, dev, ids_capacity=P,
                          tile_out=args.tile, tile_in=args.tile)
 
+        # The backward in one launch where the field allows it (gf_backward_direct: the chain
+        # rule applied per tile, no finish pass); elsewhere the same call runs two.
+        direct_one = plan.direct_launches(P) == 1
+
         def step():
             plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
-            plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
+            plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
 
         phases = {
             "k_bin": [lambda: plan.bin(q.mu, q.chol_raw, q.amp)],
             "k_emit+": [lambda: plan.bin(q.mu, q.chol_raw, q.amp), lambda: plan.emit(q.mu, q.amp)],
             "k_render": [lambda: plan.render(q.row_coords, q.col_coords)],
-            "k_bwd": [lambda: plan.backward_reduce(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, P)],
-            "k_bwd_finish": [lambda: plan.backward_finish(q.chol_raw, q.amp)],
         }
+        if direct_one:
+            phases["k_bwd"] = [lambda: plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw,
+                                                            q.amp, num_pairs=P)]
+        else:
+            phases["k_bwd"] = [lambda: plan.backward_reduce(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, P)]
+            phases["k_bwd_finish"] = [lambda: plan.backward_finish(q.chol_raw, q.amp)]
         status = plan.status
         emits = probs[0].k > 8192 or args.tile not in (16, 32)  # the emission path (no masks)
 
@@ -474,7 +484,8 @@ def main() -> int:
     # trace reports for the same launches (back-to-back kernels, no host gaps).  Every kernel is
     # idempotent under repetition except k_emit (its fill counters advance), so k_emit is timed
     # as (k_bin + k_emit) minus k_bin; repeated k_bwd only grows the accumulators, which the
-    # trailing k_bwd_finish clears.
+    # trailing k_bwd_finish clears (the direct backward's only grow the gradients the next
+    # forward clears).
     def graph_time_us(fns) -> float:
         s = torch.cuda.Stream(dev)
         s.wait_stream(torch.cuda.current_stream(dev))

@@ -30,7 +30,8 @@ EXPORTED = (
     "gf_forward_workspace_bytes_max", "gf_backward_workspace_bytes", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
     "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
     "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward",
-    "gf_batch_set_grads", "gf_batch_read", "gf_backward_noalloc", "gf_forward",
+    "gf_batch_set_grads", "gf_batch_read", "gf_backward_noalloc", "gf_forward", "gf_backward_direct",
+    "gf_forward_grads_offset", "gf_backward_direct_launches",
 )
 
 GF_PHASE_BIN, GF_PHASE_EMIT, GF_PHASE_RENDER = 0x1, 0x2, 0x4
@@ -121,6 +122,12 @@ def lib() -> ctypes.CDLL:
     L.gf_backward_finish.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_size_t, _P]
     L.gf_backward_noalloc.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int32,
                                       _P, c_int32, c_int64, _P, _P, _P, _P, _P]
+    L.gf_backward_direct.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, c_int64,
+                                     _P, c_size_t, _P, c_size_t, _P]
+    L.gf_forward_grads_offset.argtypes = [c_int64, c_int64, c_int64, _CFG]
+    L.gf_forward_grads_offset.restype = c_size_t
+    L.gf_backward_direct_launches.argtypes = [_CFG, c_int64, c_int64, c_int64, c_int64]
+    L.gf_backward_direct_launches.restype = c_int
     L.gf_read_status.argtypes = [_P, c_int32, POINTER(c_uint32), _P]
     L.gf_batch_plan.argtypes = [_CFG, POINTER(GfLayer), c_int32, _P, c_size_t, POINTER(GfBatchInfo), _P]
     L.gf_batch_forward.argtypes = [_P, POINTER(GfBatchInfo), c_uint32, _P]
@@ -132,7 +139,8 @@ def lib() -> ctypes.CDLL:
     for name in ("gf_tile_grid", "gf_forward_bin", "gf_forward_emit", "gf_forward_render",
                  "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
                  "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward",
-                 "gf_batch_set_grads", "gf_batch_read", "gf_backward_noalloc", "gf_forward"):
+                 "gf_batch_set_grads", "gf_batch_read", "gf_backward_noalloc", "gf_forward",
+                 "gf_backward_direct"):
         getattr(L, name).restype = c_int
     _LIB = L
     return L

@@ -155,9 +155,11 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // (int32 ids emitted so far into each tile's segment; emission path), rowmask[R][W] and
 // colmask[C][W] (mask path: bit g%32 of word g/32 is set when Gaussian g's tile rectangle covers
 // the tile row / column), bsq[blocks] (fp32 sum of delta-W^2 over each 16x16 block, written by
-// the batched render for the layer's norm).
+// the batched render for the layer's norm), dcoef[K][6] (float4, mask path: the chain-rule map
+// of each Gaussian, see store_dcoef) and dgrad[K][8] (the gradients of gf_backward_direct, which
+// the binning clears).
 struct FwdLayout {
-  size_t eval, rect, cov, lfac, fill, rowmask, colmask, bsq, total;
+  size_t eval, rect, cov, lfac, fill, rowmask, colmask, bsq, dcoef, dgrad, total;
 };
 FwdLayout fwd_layout(const Problem& p) {
   const int64_t K = p.K, T = (int64_t)p.R * p.C;
@@ -179,6 +181,10 @@ FwdLayout fwd_layout(const Problem& p) {
   o = align256(o + sizeof(uint32_t) * (size_t)p.C * (size_t)p.W);
   L.bsq = o;  // batched render: sum of squares of delta-W over each 16x16 block (block index sidx)
   o = align256(o + sizeof(float) * (size_t)T * (p.tile_out == 32 && p.tile_in == 32 ? 4 : 1));
+  L.dcoef = o;  // k_prep: each Gaussian's chain-rule map from moments to gradients (six float4)
+  o = align256(o + 6 * sizeof(float4) * (size_t)K);
+  L.dgrad = o;  // gf_backward_direct's gradients: [K][8] (d_amp, d_mu x2, d_chol_raw x3, 2 unused)
+  o = align256(o + 8 * sizeof(float) * (size_t)K);
   L.total = o;
   return L;
 }
@@ -207,6 +213,13 @@ __device__ inline void set_status(uint32_t* status, uint32_t bit) { atomicOr(sta
 // tiles must not keep its S stripes on one or two lines (Gaussian-major, 128-byte lines hold
 // four 32-byte slots).
 __device__ inline int64_t acc_slot(const Problem& p, int64_t g, int64_t st) { return st * p.K + g; }
+
+// Index in dgrad of gradient k of Gaussian g, k in the order of the chain-rule map: d_amp, d_mu
+// (2), d_chol_raw (3).  One 32-byte slot per Gaussian: its six atomics stay on one cache line,
+// which four Gaussians share (as the moment accumulators); three arrays of 4, 8 and 12 bytes
+// per Gaussian put up to 32 Gaussians on a line, and the atomics serialised on them (cfg3's
+// backward: 15.8 us against 9.2 us).
+__device__ inline uint32_t direct_slot(int32_t g, int k) { return 8 * (uint32_t)g + (uint32_t)k; }
 
 __device__ inline int32_t clamp_i32(int32_t v, int32_t lo, int32_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
@@ -420,6 +433,16 @@ __device__ inline float dpp_row_sum_f32(float v) {
   v += __int_as_float(dpp_i32<0x112, 0xf>(__float_as_int(v)));
   v += __int_as_float(dpp_i32<0x114, 0xf>(__float_as_int(v)));
   v += __int_as_float(dpp_i32<0x118, 0xf>(__float_as_int(v)));
+  return v;
+}
+
+// Sum over each row of 16 lanes, in every lane of the row: xor butterflies (quad_perm [1,0,3,2],
+// [2,3,0,1], row_half_mirror, row_mirror), each lane adding the same two halves.
+__device__ inline float dpp_row_allsum_f32(float v) {
+  v += dpp_f32<0xb1>(v);
+  v += dpp_f32<0x4e>(v);
+  v += dpp_f32<0x141>(v);
+  v += dpp_f32<0x140>(v);
   return v;
 }
 
@@ -842,6 +865,7 @@ struct PrepOut {
   GfCov cov;
   float mu0, mu1;
   float l11, l22;
+  float r11, r21, r22;  // chol_raw (l21 = r21)
 };
 
 struct PrepLoad {
@@ -861,11 +885,68 @@ __device__ inline PrepOut prep_rect(const Problem& p, const PrepLoad& in) {
   o.cov = gf_cov_from_chol(Lc);
   o.l11 = Lc.l11;
   o.l22 = Lc.l22;
+  o.r11 = in.r11;
+  o.r21 = in.r21;
+  o.r22 = in.r22;
   int32_t touched;
   o.rect = bin_rect(p, o.mu0, o.mu1, o.cov, &touched);
   return o;
 }
 
+// d softplus / dx as torch's softplus backward: x > 20 ? 1 : e^x / (e^x + 1).  In fp32 with the
+// hardware exp2, within 2e-6 relative of the exact value (the argument x log2(e) <= 28.9 is
+// rounded once); the finish's gradients are held to 1e-4.
+__device__ inline float softplus_grad_f32(float x) {
+  if (x > 20.0f) return 1.0f;
+  const float e = __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+  return e / (e + 1.0f);
+}
+
+// Direct gradients (gf_backward_direct).  The chain rule from a Gaussian's six moments
+// S0..S5 to its gradients (finish_body) is linear in the moments, with coefficients that depend
+// only on the Gaussian's parameters.  The map is computed here in double and rounded once to
+// fp32, and the backward applies it to each tile's moments before its atomics.  Output k (0:
+// d_amp, 1, 2: d_mu, 3..5: d_chol_raw) is dcoef[6 g + k] . (P, Q, S4, S5), where (P, Q) is
+// (S1, S2) for k = 1, 2 and (S0, S3) otherwise.  With G = h [[S3, S4], [S4, S5]],
+// h = -amp norm / 2, and the det term f = h S0 (normalize), dL/dcov = -A G A + f A holds
+//   c00 = -h (i00^2 S3 + 2 i00 i01 S4 + i01^2 S5) + f i00
+//   c01 = -h (i00 i01 S3 + (i00 i11 + i01^2) S4 + i01 i11 S5) + f i01
+//   c11 = -h (i01^2 S3 + 2 i01 i11 S4 + i11^2 S5) + f i11,
+// and dL/dL = 2 [[c00 l11 + c01 l21, .], [c01 l11 + c11 l21, c11 l22]] before the softplus'.
+// The Gaussian's gradient slot is cleared for the backward's atomics.  (Single fields only, whose
+// mu is the mean itself: no tanh.)  cov and (l11, l22) are those the binning stored, r = chol_raw.
+__device__ inline void store_dcoef(const Problem& p, GfCov cov, float l11f, float l22f, float r11, float r21,
+                                   float r22, float amp, int64_t g, uint8_t* ws, const FwdLayout& L) {
+  const GfRenderGeom rg = gf_render_geom(cov, p.normalize);
+  const double nrm = (double)rg.norm, an = (double)amp * nrm, h = -0.5 * an;
+  const double i00 = rg.i00, i01 = rg.i01, i11 = rg.i11;
+  const double f = (p.normalize && gf_sqrt_rn(rg.det_f) >= GF_FLT_EPS) ? h : 0.0;
+  // coefficients of (S0, S3, S4, S5) in c00, c01, c11
+  const double c00[4] = {f * i00, -h * i00 * i00, -h * 2.0 * i00 * i01, -h * i01 * i01};
+  const double c01[4] = {f * i01, -h * i00 * i01, -h * (i00 * i11 + i01 * i01), -h * i01 * i11};
+  const double c11[4] = {f * i11, -h * i01 * i01, -h * 2.0 * i01 * i11, -h * i11 * i11};
+  const double l11 = l11f, l21 = r21, l22 = l22f;
+  const double sp11 = (double)softplus_grad_f32(r11), sp22 = (double)softplus_grad_f32(r22);
+  double d11[4], d21[4], d22[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    d11[j] = 2.0 * (c00[j] * l11 + c01[j] * l21) * sp11;
+    d21[j] = 2.0 * (c01[j] * l11 + c11[j] * l21);
+    d22[j] = 2.0 * c11[j] * l22 * sp22;
+  }
+  float4* out = reinterpret_cast<float4*>(ws + L.dcoef) + 6 * g;
+  out[0] = make_float4((float)nrm, 0.0f, 0.0f, 0.0f);
+  out[1] = make_float4((float)(an * i00), (float)(an * i01), 0.0f, 0.0f);
+  out[2] = make_float4((float)(an * i01), (float)(an * i11), 0.0f, 0.0f);
+  out[3] = make_float4((float)d11[0], (float)d11[1], (float)d11[2], (float)d11[3]);
+  out[4] = make_float4((float)d21[0], (float)d21[1], (float)d21[2], (float)d21[3]);
+  out[5] = make_float4((float)d22[0], (float)d22[1], (float)d22[2], (float)d22[3]);
+  float4* dg = reinterpret_cast<float4*>(ws + L.dgrad) + 2 * g;
+  dg[0] = make_float4(0.f, 0.f, 0.f, 0.f);
+  dg[1] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+template <bool kCoef>
 __device__ inline void store_prep(const Problem& p, const PrepOut& o, float amp, int64_t g, uint8_t* ws,
                                   const FwdLayout& L) {
   reinterpret_cast<int4*>(ws + L.rect)[g] = o.rect;
@@ -874,9 +955,12 @@ __device__ inline void store_prep(const Problem& p, const PrepOut& o, float amp,
   GaussEval v = eval_from_cov(p, o.mu0, o.mu1, o.cov, amp);
   v.gid = (int32_t)g;
   store_eval(reinterpret_cast<GaussEval*>(ws + L.eval), g, v);
+  if (kCoef) store_dcoef(p, o.cov, o.l11, o.l22, o.r11, o.r21, o.r22, amp, g, ws, L);
 }
 
-// One thread per Gaussian: rectangle, covariance and evaluation constants.
+// One thread per Gaussian: rectangle, covariance and evaluation constants, and (kCoef: fields
+// binned in the render, with no k_bin_tiles launch) the chain-rule map.
+template <bool kCoef>
 __global__ __launch_bounds__(kTilesThreads) void k_prep(Problem p, const float* __restrict__ mu,
                                                         const float* __restrict__ chol_raw,
                                                         const float* __restrict__ amp, uint8_t* ws,
@@ -888,12 +972,13 @@ __global__ __launch_bounds__(kTilesThreads) void k_prep(Problem p, const float* 
     hdr->heavy = 0u;
     hdr->num_pairs = num_pairs;
   }
-  if (g < p.K) store_prep(p, prep_rect(p, prep_load(mu, chol_raw, g)), amp[g], g, ws, L);
+  if (g < p.K) store_prep<kCoef>(p, prep_rect(p, prep_load(mu, chol_raw, g)), amp[g], g, ws, L);
 }
 
 __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t* __restrict__ tile_ptr,
                                                              int64_t* __restrict__ num_pairs, uint8_t* ws,
-                                                             FwdLayout L) {
+                                                             FwdLayout L, const float* __restrict__ chol_raw,
+                                                             const float* __restrict__ amp) {
   __shared__ int32_t diff[kLdsDiffWords];  // tile-row workgroups: the row's column differences
   const int64_t K = p.K;
   const int32_t R = p.R, C = p.C, W = p.W;
@@ -944,7 +1029,22 @@ __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t*
       if (lane == 1 && w0 + 1 < W) out[w0 + 1] = (uint32_t)(bits >> 32);
     }
   }
-  if (!is_row) return;
+  if (!is_row) {
+    // The chain-rule maps of Gaussians line, line + C, ... (off the binning's critical path: the
+    // column workgroups finish before the row workgroups' scans)
+    const float4* cv = reinterpret_cast<const float4*>(ws + L.cov);
+    const float2* lf = reinterpret_cast<const float2*>(ws + L.lfac);
+    for (int64_t g = line + (int64_t)C * threadIdx.x; g < K; g += (int64_t)C * kTilesThreads) {
+      const float4 c4 = cv[g];
+      const float2 l = lf[g];
+      GfCov c;
+      c.s00 = c4.x;
+      c.s01 = c4.y;
+      c.s11 = c4.z;
+      store_dcoef(p, c, l.x, l.y, chol_raw[3 * g + 0], chol_raw[3 * g + 1], chol_raw[3 * g + 2], amp[g], g, ws, L);
+    }
+    return;
+  }
   __syncthreads();  // the row's differences are complete
   // tile_ptr[line*C + c] = rowbase + sum_{c' < c} diff[c'] * (c - c') = rowbase + c*D(c) - E(c),
   // with D, E the exclusive prefixes of diff[c] and c*diff[c]: one scan of two sums, with
@@ -2052,13 +2152,18 @@ __device__ inline void stage_gaussians(const Problem& p, const GIdx* __restrict_
 // kEvalGiven: ev is never null (batches), so the per-Gaussian recomputation from mu / chol_raw
 // (the exact softplus chain) is left out of the kernel, with its registers.
 template <typename TpIdx, typename GIdx, bool kTransposeSums, bool kMaskClamp, bool kManyRounds = kTransposeSums,
-          bool kEvalGiven = false>
+          bool kEvalGiven = false, bool kDirect = false>
 __device__ __forceinline__ void bwd16_body(
     const Problem& p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
     const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
     const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
-    uint8_t* ws, const BwdLayout& L, const SubTile& st, int q = 0, int F = 1) {
+    uint8_t* ws, const BwdLayout& L, const SubTile& st, int q = 0, int F = 1,
+    const float4* __restrict__ dcoef = nullptr, float* __restrict__ dgrad = nullptr) {
+  // kDirect (row sums only): each tile's moments go through the Gaussian's chain-rule map
+  // (dcoef, store_dcoef) and the gradients are added straight into dgrad (d_mu | d_chol_raw |
+  // d_amp), so that no finish pass follows.
+  static_assert(!kDirect || !kTransposeSums, "direct gradients take the row-sum reduction");
   // F > 1 (heavy tiles): the F = 4 waves of the workgroup share tile st, wave q taking chunks
   // q, q + F, ... of kHeavyChunk Gaussians (and their indefinite-form pass).
   const int cs = F > 1 ? kHeavyChunk : 64;
@@ -2214,6 +2319,10 @@ __device__ __forceinline__ void bwd16_body(
       const float A = a * a;
       const float b = wb * dx;
       if (chunk_general && gen != 0.0f) g = -1;  // indefinite form: the pass below
+      // kDirect: lanes 10..15 of a slot take output row - 10 of the slot's Gaussian; its map
+      // row is requested here, before the pixel loop that hides the load
+      float4 cf = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (kDirect && row >= 10 && g >= 0) cf = dcoef[6 * (uint32_t)g + (uint32_t)(row - 10)];
       float t0 = 0.f, t2 = 0.f, t3 = 0.f, tq = 0.f;
       if (kMaskClamp) {
 #pragma unroll
@@ -2297,6 +2406,17 @@ __device__ __forceinline__ void bwd16_body(
       }
       const float t0q = kMaskClamp ? tq : t0;  // the quadratic-form moments' share of S0
       const float m0 = t0, m1 = dx * t0q, m2 = t2, m3 = dx * dx * t0q, m4 = dx * t2, m5 = t3;
+      if (kDirect) {
+        // the six row sums in every lane of the row (butterfly: the same sum in each lane), then
+        // lane 10 + k forms output k of the map and adds it to the Gaussian's gradient
+        const float s0 = dpp_row_allsum_f32(m0), s1 = dpp_row_allsum_f32(m1), s2 = dpp_row_allsum_f32(m2);
+        const float s3 = dpp_row_allsum_f32(m3), s4 = dpp_row_allsum_f32(m4), s5 = dpp_row_allsum_f32(m5);
+        const int k = row - 10;
+        const float P = (k == 1 || k == 2) ? s1 : s0, Q = k < 3 ? s2 : s3;
+        const float o = fmaf(cf.x, P, fmaf(cf.y, Q, fmaf(cf.z, s4, cf.w * s5)));
+        if (g >= 0 && row >= 10) unsafeAtomicAdd(dgrad + direct_slot(g, k), o);
+        continue;
+      }
       if (!kTransposeSums) {
         // Six independent row sums (the shorter dependency chain, for sparse tiles where a wave
         // makes few rounds).  Lane 15 of the slot's row holds the sums; moment k moves
@@ -2391,9 +2511,19 @@ __device__ __forceinline__ void bwd16_body(
 #pragma unroll
         for (int k = 0; k < 6; ++k) mm[k] = dpp_row_sum_f32(mm[k]);  // row 0: lanes 0..15
         if (lane == 15 && gj >= 0) {
+          if (kDirect) {
 #pragma unroll
-          for (int k = 0; k < 6; ++k)
-            unsafeAtomicAdd(acc + 8 * acc_slot(p, gj, stripe) + k, mm[k]);
+            for (int k = 0; k < 6; ++k) {
+              const float4 c = dcoef[6 * (uint32_t)gj + (uint32_t)k];
+              const float P = (k == 1 || k == 2) ? mm[1] : mm[0], Q = k < 3 ? mm[2] : mm[3];
+              unsafeAtomicAdd(dgrad + direct_slot(gj, k),
+                              fmaf(c.x, P, fmaf(c.y, Q, fmaf(c.z, mm[4], c.w * mm[5]))));
+            }
+          } else {
+#pragma unroll
+            for (int k = 0; k < 6; ++k)
+              unsafeAtomicAdd(acc + 8 * acc_slot(p, gj, stripe) + k, mm[k]);
+          }
         }
       }
     }
@@ -2404,14 +2534,16 @@ __device__ __forceinline__ void bwd16_body(
 // raise the register count and cost the common path occupancy.
 // kEvalGiven: launched with the forward's constants (ev != null); the heavy-tile kernels always
 // are, since their tile list lives in the same workspace.
-template <typename TpIdx, typename GIdx, bool kTransposeSums, bool kMaskClamp, bool kHeavy, bool kEvalGiven = kHeavy>
+template <typename TpIdx, typename GIdx, bool kTransposeSums, bool kMaskClamp, bool kHeavy, bool kEvalGiven = kHeavy,
+          bool kDirect = false>
 __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_bwd16(
     Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const float* __restrict__ mu,
     const float* __restrict__ chol_raw, const GaussEval* __restrict__ ev,
     const TpIdx* __restrict__ tile_ptr, const GIdx* __restrict__ gids, int64_t num_pairs,
     uint8_t* ws, BwdLayout L, const int32_t* __restrict__ heavy_list,
-    const uint32_t* __restrict__ heavy_count, int32_t xh) {
+    const uint32_t* __restrict__ heavy_count, int32_t xh, const float4* __restrict__ dcoef,
+    float* __restrict__ dgrad) {
   HeavyItem it;
   if constexpr (kHeavy) {
     it = heavy_item(p, heavy_list, heavy_count, xh, &reinterpret_cast<WsHeader*>(ws)->status);
@@ -2420,8 +2552,9 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
     it.q = 0;
     it.F = 1;
   }
-  bwd16_body<TpIdx, GIdx, kTransposeSums, kMaskClamp, kTransposeSums || kHeavy, kEvalGiven>(
-      p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gids, num_pairs, ws, L, it.st, it.q, it.F);
+  bwd16_body<TpIdx, GIdx, kTransposeSums, kMaskClamp, kTransposeSums || kHeavy, kEvalGiven, kDirect>(
+      p, grad, row_coords, col_coords, mu, chol_raw, ev, tile_ptr, gids, num_pairs, ws, L, it.st, it.q, it.F,
+      dcoef, dgrad);
 }
 
 __device__ inline float wave_sum(float v) {
@@ -2496,15 +2629,6 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
   }
 }
 
-// d softplus / dx as torch's softplus backward: x > 20 ? 1 : e^x / (e^x + 1).  In fp32 with the
-// hardware exp2, within 2e-6 relative of the exact value (the argument x log2(e) <= 28.9 is
-// rounded once); the finish's gradients are held to 1e-4.
-__device__ inline float softplus_grad_f32(float x) {
-  if (x > 20.0f) return 1.0f;
-  const float e = __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
-  return e / (e + 1.0f);
-}
-
 // Chain rule from the six moments of Gaussian g to (d_mu, d_chol_raw, d_amp), in double:
 //   d_amp = norm S0;  d_mu = amp norm A (S1, S2);  dL/dA = -amp norm / 2 [[S3,S4],[S4,S5]];
 //   dL/ddet = amp S0 (-norm / (2 det)) if normalize and sqrt(det) >= eps (else 0);
@@ -2515,11 +2639,14 @@ __device__ inline float softplus_grad_f32(float x) {
 // takes stripe idx % S of Gaussian idx / S (loads it and clears it), the S threads (adjacent
 // lanes of one wave) sum the six moments with xor shuffles, and the first applies the chain
 // rule.  Every lane of the wave must call it (the shuffles).
+// ostride: floats between consecutive Gaussians' outputs in each of d_mu, d_chol_raw, d_amp (0:
+// the arrays [K][2], [K][3], [K][1]; 8: one slot of 8 floats per Gaussian, as gf_backward_direct's).
 __device__ __forceinline__ void finish_body(
     const Problem& p, const float* __restrict__ chol_raw, const float* __restrict__ amp,
     float* __restrict__ d_mu, float* __restrict__ d_chol_raw, float* __restrict__ d_amp, uint8_t* ws,
     const BwdLayout& L, int64_t idx, const float* __restrict__ mu = nullptr,
-    const float4* __restrict__ fwd_cov = nullptr, const float2* __restrict__ fwd_lfac = nullptr) {
+    const float4* __restrict__ fwd_cov = nullptr, const float2* __restrict__ fwd_lfac = nullptr,
+    int32_t ostride = 0) {
   float* acc = reinterpret_cast<float*>(ws + L.acc);
   const int64_t g = idx / p.S;
   const int32_t st = (int32_t)(idx & (p.S - 1));
@@ -2562,7 +2689,8 @@ __device__ __forceinline__ void finish_body(
   const double a = (double)amp[g];
   const double nrm = (double)rg.norm;
   const double an = a * nrm;
-  d_amp[g] = (float)(nrm * S0);
+  const int64_t om = ostride ? ostride * g : 2 * g, oc = ostride ? ostride * g : 3 * g, oa = ostride ? ostride * g : g;
+  d_amp[oa] = (float)(nrm * S0);
   float dm0 = (float)(an * (rg.i00 * S1 + rg.i01 * S2));
   float dm1 = (float)(an * (rg.i01 * S1 + rg.i11 * S2));
   if (p.mu_tanh) {  // dL/d(mu_raw) = dL/d(mu) * (1 - tanh(mu_raw)^2), as torch's tanh backward
@@ -2570,8 +2698,8 @@ __device__ __forceinline__ void finish_body(
     dm0 = dm0 * (1.0f - y0 * y0);
     dm1 = dm1 * (1.0f - y1 * y1);
   }
-  d_mu[2 * g + 0] = dm0;
-  d_mu[2 * g + 1] = dm1;
+  d_mu[om + 0] = dm0;
+  d_mu[om + 1] = dm1;
   const double G00 = -0.5 * an * S3, G01 = -0.5 * an * S4, G11 = -0.5 * an * S5;
   const double ag00 = rg.i00 * G00 + rg.i01 * G01, ag01 = rg.i00 * G01 + rg.i01 * G11;
   const double ag10 = rg.i01 * G00 + rg.i11 * G01, ag11 = rg.i01 * G01 + rg.i11 * G11;
@@ -2593,17 +2721,17 @@ __device__ __forceinline__ void finish_body(
   const double dl11 = 2.0 * c00 * l11 + (c01 + c10) * l21;
   const double dl21 = (c10 + c01) * l11 + 2.0 * c11 * l21;
   const double dl22 = 2.0 * c11 * l22;
-  d_chol_raw[3 * g + 0] = (float)(dl11 * softplus_grad_f32(raw11));
-  d_chol_raw[3 * g + 1] = (float)dl21;
-  d_chol_raw[3 * g + 2] = (float)(dl22 * softplus_grad_f32(raw22));
+  d_chol_raw[oc + 0] = (float)(dl11 * softplus_grad_f32(raw11));
+  d_chol_raw[oc + 1] = (float)dl21;
+  d_chol_raw[oc + 2] = (float)(dl22 * softplus_grad_f32(raw22));
 }
 
 __global__ __launch_bounds__(kTileThreads) void k_bwd_finish(
     Problem p, const float* __restrict__ chol_raw, const float* __restrict__ amp,
     float* __restrict__ d_mu, float* __restrict__ d_chol_raw, float* __restrict__ d_amp, uint8_t* ws,
-    BwdLayout L, const float4* __restrict__ fwd_cov, const float2* __restrict__ fwd_lfac) {
+    BwdLayout L, const float4* __restrict__ fwd_cov, const float2* __restrict__ fwd_lfac, int32_t ostride) {
   finish_body(p, chol_raw, amp, d_mu, d_chol_raw, d_amp, ws, L,
-              (int64_t)blockIdx.x * blockDim.x + threadIdx.x, nullptr, fwd_cov, fwd_lfac);
+              (int64_t)blockIdx.x * blockDim.x + threadIdx.x, nullptr, fwd_cov, fwd_lfac, ostride);
 }
 
 // Self-test: order-independent checksum of gf_softplus_torch_cpu over all 2^32 inputs.
@@ -2999,7 +3127,7 @@ template <typename TP, typename GI, bool kTS, bool kMC>
 void launch_bwd16(const Problem& p, int32_t xh, hipStream_t st, const float* grad, const float* rc,
                   const float* cc, const float* mu, const float* raw, const GaussEval* ev, const TP* tp,
                   const GI* gi, int64_t num_pairs, uint8_t* ws, const BwdLayout& L, const int32_t* heavy_list,
-                  const uint32_t* heavy_count) {
+                  const uint32_t* heavy_count, const float4* dcoef = nullptr, float* dgrad = nullptr) {
   // heavy-tile kernels for the int64 saved state (FieldPlan, the autograd functions)
   constexpr bool kCanHeavy = std::is_same<TP, int64_t>::value && std::is_same<GI, int64_t>::value;
   if constexpr (kCanHeavy) {
@@ -3008,31 +3136,44 @@ void launch_bwd16(const Problem& p, int32_t xh, hipStream_t st, const float* gra
       q.heavy = kHeavyTile;
       hipLaunchKernelGGL((k_bwd16<TP, GI, kTS, kMC, true>), dim3((unsigned)(xh + quad_grid(p))),
                          dim3(kTileThreads), 0, st, q, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L,
-                         heavy_list, heavy_count, xh);
+                         heavy_list, heavy_count, xh, nullptr, nullptr);
       return;
     }
   }
   Problem q = p;
   q.heavy = 0;
+  if constexpr (kCanHeavy && !kTS) {
+    if (ev && dgrad) {  // gf_backward_direct: gradients straight into dgrad
+      hipLaunchKernelGGL((k_bwd16<TP, GI, false, kMC, false, true, true>), dim3((unsigned)quad_grid(p)),
+                         dim3(kTileThreads), 0, st, q, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L,
+                         heavy_list, heavy_count, 0, dcoef, dgrad);
+      return;
+    }
+  }
   if constexpr (kCanHeavy) {
     if (ev) {  // the forward's constants (FieldPlan, the autograd functions)
       hipLaunchKernelGGL((k_bwd16<TP, GI, kTS, kMC, false, true>), dim3((unsigned)quad_grid(p)), dim3(kTileThreads),
-                         0, st, q, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L, heavy_list, heavy_count, 0);
+                         0, st, q, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L, heavy_list, heavy_count, 0,
+                         nullptr, nullptr);
       return;
     }
   }
   hipLaunchKernelGGL((k_bwd16<TP, GI, kTS, kMC, false>), dim3((unsigned)quad_grid(p)), dim3(kTileThreads), 0, st,
-                     q, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L, heavy_list, heavy_count, 0);
+                     q, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L, heavy_list, heavy_count, 0, nullptr,
+                     nullptr);
 }
+
+// Tiles of many Gaussians (a wave makes >= 4 rounds on average) take the transposing moment
+// reduction (fewer instructions); sparse ones the row sums (shorter chain).
+bool bwd_dense(const Problem& p, int64_t num_pairs) { return num_pairs >= 16 * (int64_t)p.R * p.C; }
 
 template <typename TP, typename GI>
 void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, const float* rc,
                 const float* cc, const float* mu, const float* raw, const GaussEval* ev,
                 const void* tile_ptr, const void* gids, int64_t num_pairs, uint8_t* ws,
-                const BwdLayout& L, const int32_t* heavy_list, const uint32_t* heavy_count) {
-  // Tiles of many Gaussians (a wave makes >= 4 rounds on average) take the transposing
-  // moment reduction (fewer instructions); sparse ones the row sums (shorter chain).
-  const bool dense = num_pairs >= 16 * (int64_t)p.R * p.C;
+                const BwdLayout& L, const int32_t* heavy_list, const uint32_t* heavy_count,
+                const float4* dcoef = nullptr, float* dgrad = nullptr) {
+  const bool dense = bwd_dense(p, num_pairs);
   // heavy-tile workgroups only with the forward's tile list (the forward workspace)
   const int32_t xh = heavy_list ? heavy_grid(p, num_pairs) : 0;
   const TP* tp = reinterpret_cast<const TP*>(tile_ptr);
@@ -3043,13 +3184,13 @@ void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, 
                                        heavy_count);
     else if (p.mask_clamp)
       launch_bwd16<TP, GI, false, true>(p, xh, st, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L, heavy_list,
-                                        heavy_count);
+                                        heavy_count, dcoef, dgrad);
     else if (dense)
       launch_bwd16<TP, GI, true, false>(p, xh, st, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L, heavy_list,
                                         heavy_count);
     else
       launch_bwd16<TP, GI, false, false>(p, xh, st, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L,
-                                         heavy_list, heavy_count);
+                                         heavy_list, heavy_count, dcoef, dgrad);
   } else
     hipLaunchKernelGGL((k_bwd_any<TP, GI>), grid, dim3(kTileThreads), 0, st, p, grad, rc, cc, mu, raw, ev,
                        reinterpret_cast<const TP*>(tile_ptr), reinterpret_cast<const GI*>(gids),
@@ -3179,12 +3320,14 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
     if (!amp) return set_err(GF_E_INVALID_ARGUMENT, "amp must not be NULL");
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
     const unsigned lines = (unsigned)(p.R + p.C);
-    hipLaunchKernelGGL(k_prep, dim3((unsigned)((k + kTilesThreads - 1) / kTilesThreads)), dim3(kTilesThreads), 0,
-                       st, p, mu, chol_raw, amp, ws, L, num_pairs_dev);
+    const bool in_render = tiles_in_render(p);
+    hipLaunchKernelGGL(in_render ? k_prep<true> : k_prep<false>, dim3((unsigned)((k + kTilesThreads - 1) / kTilesThreads)),
+                       dim3(kTilesThreads), 0, st, p, mu, chol_raw, amp, ws, L, num_pairs_dev);
     GF_LAUNCH_CHECK("k_prep");
     p.heavy = heavy_threshold(p);
-    if (!tiles_in_render(p))
-      hipLaunchKernelGGL(k_bin_tiles, dim3(lines), dim3(kTilesThreads), 0, st, p, tile_ptr, num_pairs_dev, ws, L);
+    if (!in_render)
+      hipLaunchKernelGGL(k_bin_tiles, dim3(lines), dim3(kTilesThreads), 0, st, p, tile_ptr, num_pairs_dev, ws, L,
+                         chol_raw, amp);
     else if (num_pairs_host)
       hipLaunchKernelGGL(k_pairs, dim3(1), dim3(kTilesThreads), 0, st, p, num_pairs_dev, ws, L);
   } else {
@@ -3324,10 +3467,24 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
   return GF_OK;
 }
 
+static int backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                           const float* chol_raw, const float* amp, float* d_mu, float* d_chol_raw, float* d_amp,
+                           const void* forward_workspace, void* workspace, size_t workspace_bytes, void* stream,
+                           int32_t ostride);
+
 int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                        const float* chol_raw, const float* amp, float* d_mu, float* d_chol_raw,
                        float* d_amp, const void* forward_workspace, void* workspace, size_t workspace_bytes,
                        void* stream) {
+  return backward_finish(cfg, out_features, in_features, k, chol_raw, amp, d_mu, d_chol_raw, d_amp,
+                         forward_workspace, workspace, workspace_bytes, stream, 0);
+}
+
+// gf_backward_finish with the outputs' per-Gaussian stride (finish_body's ostride).
+static int backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                           const float* chol_raw, const float* amp, float* d_mu, float* d_chol_raw, float* d_amp,
+                           const void* forward_workspace, void* workspace, size_t workspace_bytes, void* stream,
+                           int32_t ostride) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
@@ -3344,7 +3501,7 @@ int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t
   hipLaunchKernelGGL(k_bwd_finish, dim3(blocks), dim3(kTileThreads), 0, st, p, chol_raw, amp, d_mu,
                      d_chol_raw, d_amp, reinterpret_cast<uint8_t*>(workspace), L,
                      fws ? reinterpret_cast<const float4*>(fws + FL.cov) : nullptr,
-                     fws ? reinterpret_cast<const float2*>(fws + FL.lfac) : nullptr);
+                     fws ? reinterpret_cast<const float2*>(fws + FL.lfac) : nullptr, ostride);
   GF_LAUNCH_CHECK("k_bwd_finish");
   return GF_OK;
 }
@@ -3362,6 +3519,72 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
   if (rc) return rc;
   return gf_backward_finish(cfg, out_features, in_features, k, chol_raw, amp, d_mu, d_chol_raw, d_amp,
                             forward_workspace, workspace, workspace_bytes, stream);
+}
+
+// gf_backward_direct runs one launch where k_prep stored the chain-rule maps (the mask path)
+// and the tiles take the plain row-sum kernel: 16x16 or 32x32 tiles, sparse, no heavy-tile
+// workgroups.  Elsewhere it runs the reduction and the finish, which writes the same gradients.
+bool direct_one_launch(const Problem& p, int64_t num_pairs) {
+  return p.W > 0 && quad_tiles(p) && !bwd_dense(p, num_pairs) && heavy_grid(p, num_pairs) == 0;
+}
+
+int gf_backward_direct_launches(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                                int64_t num_pairs) {
+  Problem p;
+  int rc = make_problem(cfg, out_features, in_features, k, &p);
+  if (rc) return -rc;
+  return direct_one_launch(p, num_pairs) && k > 0 ? 1 : 2;
+}
+
+size_t gf_forward_grads_offset(int64_t out_features, int64_t in_features, int64_t k,
+                               const gf_field_config* cfg) {
+  Problem p;
+  if (make_problem(cfg, out_features, in_features, k, &p)) return 0;
+  return fwd_layout(p).dgrad;
+}
+
+int gf_backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                       const float* grad_delta, const float* row_coords, const float* col_coords,
+                       const float* mu, const float* chol_raw, const float* amp, const int64_t* tile_ptr,
+                       const int64_t* gaussian_ids, int64_t num_pairs, void* forward_workspace,
+                       size_t forward_workspace_bytes, void* workspace, size_t workspace_bytes, void* stream) {
+  Problem p;
+  int rc = make_problem(cfg, out_features, in_features, k, &p);
+  if (rc) return rc;
+  const FwdLayout FL = fwd_layout(p);
+  if (!forward_workspace || forward_workspace_bytes < FL.total)
+    return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", FL.total,
+                   forward_workspace_bytes);
+  uint8_t* fws = reinterpret_cast<uint8_t*>(forward_workspace);
+  float* dg = reinterpret_cast<float*>(fws + FL.dgrad);  // [K][8]: d_amp, d_mu x2, d_chol_raw x3
+  if (!direct_one_launch(p, num_pairs) || k == 0) {
+    rc = gf_backward_reduce(cfg, out_features, in_features, k, grad_delta, row_coords, col_coords, mu, chol_raw,
+                            tile_ptr, 1, gaussian_ids, 1, num_pairs, forward_workspace, workspace,
+                            workspace_bytes, stream);
+    if (rc) return rc;
+    return backward_finish(cfg, out_features, in_features, k, chol_raw, amp, dg + 1, dg + 3, dg, forward_workspace,
+                           workspace, workspace_bytes, stream, 8);
+  }
+  const BwdLayout L = bwd_layout(p);
+  if (!workspace || workspace_bytes < L.total)
+    return set_err(GF_E_WORKSPACE, "backward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
+  if (num_pairs < 0) return set_err(GF_E_INVALID_ARGUMENT, "num_pairs must be non-negative");
+  if (!grad_delta || !row_coords || !col_coords || !tile_ptr)
+    return set_err(GF_E_INVALID_ARGUMENT, "grad_delta / coords / tile_ptr must not be NULL");
+  if (num_pairs > 0 && !gaussian_ids) return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids must not be NULL");
+  if (!mu || !chol_raw || !amp) return set_err(GF_E_INVALID_ARGUMENT, "mu / chol_raw / amp must not be NULL");
+  if ((uint64_t)k * 8 >= (uint64_t)UINT32_MAX)
+    return set_err(GF_E_INVALID_ARGUMENT, "k = %lld is too large for the direct gradients", (long long)k);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const GaussEval* ev = reinterpret_cast<const GaussEval*>(fws + FL.eval);
+  launch_bwd<int64_t, int64_t>(p, dim3((unsigned)((int64_t)p.R * p.C)), st, grad_delta, row_coords, col_coords,
+                               mu, chol_raw, ev, tile_ptr, gaussian_ids, num_pairs,
+                               reinterpret_cast<uint8_t*>(workspace), L,
+                               reinterpret_cast<const int32_t*>(fws + FL.fill),
+                               &reinterpret_cast<const WsHeader*>(fws)->heavy,
+                               reinterpret_cast<const float4*>(fws + FL.dcoef), dg);
+  GF_LAUNCH_CHECK("k_bwd");
+  return GF_OK;
 }
 
 // ------------------------------------------------------------------------------------------

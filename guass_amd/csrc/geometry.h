@@ -67,13 +67,11 @@ GF_HD GF_INLINE int64_t gf_clamp_i64(int64_t v, int64_t lo, int64_t hi) {
   return v < lo ? lo : (v > hi ? hi : v);
 }
 
-GF_HD GF_INLINE float gf_sqrt_rn(float x) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  return __fsqrt_rn(x);
-#else
-  return __builtin_sqrtf(x);
-#endif
-}
+// IEEE sqrt, correctly rounded, on host and device alike.  On the device this is the LLVM sqrt,
+// which HIP lowers to the correctly rounded sequence (v_sqrt_f32 and a one-ulp correction);
+// HIP's __fsqrt_rn is the native v_sqrt_f32 unless OCML_BASIC_ROUNDED_OPERATIONS is defined,
+// which is off by one ulp for some inputs.
+GF_HD GF_INLINE float gf_sqrt_rn(float x) { return __builtin_sqrtf(x); }
 
 // torch.clamp(x, min=lo) keeps NaN.
 GF_HD GF_INLINE float gf_clamp_min_nan(float x, float lo) { return (x != x) ? x : (x < lo ? lo : x); }

@@ -166,6 +166,33 @@ class FieldPlan:
         self.backward_reduce(grad, row_coords, col_coords, mu, chol_raw, num_pairs, reuse_forward)
         return self.backward_finish(chol_raw, amp, reuse_forward)
 
+    def backward_direct(self, grad, row_coords, col_coords, mu, chol_raw, amp, num_pairs: int | None = None):
+        """The backward in one launch (gf_backward_direct): the chain rule applied per tile with
+        the maps the last forward stored, the gradients added into the forward workspace.
+        Returns views (d_mu [K,2], d_chol_raw [K,3], d_amp [K,1]) of that workspace, strided over
+        one 8-float slot per Gaussian: the next forward on this plan clears them, so copy what
+        must outlive it.  Fields where the one-launch kernel does not apply run the reduction
+        and the finish into the same slots."""
+        n = self.capacity if num_pairs is None else int(num_pairs)
+        L = N.lib()
+        N.check(L.gf_backward_direct(ctypes.byref(self.cfg), self.M, self.N, self.K, grad.data_ptr(),
+                                     row_coords.data_ptr(), col_coords.data_ptr(), N.ptr(mu), N.ptr(chol_raw),
+                                     N.ptr(amp), self.tile_ptr.data_ptr(), self.ids.data_ptr(), n,
+                                     self.fwd_ws.data_ptr(), self.fwd_ws_bytes, self.bwd_ws.data_ptr(),
+                                     self.bwd_ws_bytes, self._stream()), "gf_backward_direct")
+        off = int(L.gf_forward_grads_offset(self.M, self.N, self.K, ctypes.byref(self.cfg)))
+        slots = self.fwd_ws[off:off + 32 * self.K].view(torch.float32).view(self.K, 8)
+        return slots[:, 1:3], slots[:, 3:6], slots[:, 0:1]
+
+    def direct_launches(self, num_pairs: int | None = None) -> int:
+        """Launches :meth:`backward_direct` makes for ``num_pairs`` (default: the id capacity):
+        1, or 2 where it runs the reduction and the finish."""
+        n = self.capacity if num_pairs is None else int(num_pairs)
+        r = int(N.lib().gf_backward_direct_launches(ctypes.byref(self.cfg), self.M, self.N, self.K, n))
+        if r < 0:
+            N.check(-r, "gf_backward_direct_launches")
+        return r
+
     def pairs(self) -> int:
         """Pair count of the last forward (synchronises)."""
         return int(self.num_pairs.item())

@@ -181,6 +181,36 @@ int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * gf_backward in one launch where it can (replaces reference backward.cu:541-716 like
+ * gf_backward).  The chain rule is linear in the per-tile moments; the forward's first phase
+ * (on the mask path) stores each Gaussian's map from moments to gradients, so the reduction
+ * adds gradients instead of moments and no finish pass follows.  The gradients go to the
+ * forward workspace, which the next forward on it clears: from byte gf_forward_grads_offset(...)
+ * of it, K slots of 8 fp32, slot g = (d_amp[g], d_mu[g][0..1], d_chol_raw[g][0..2], 2 unused),
+ * valid until that next forward (one slot per Gaussian keeps each Gaussian's atomics on one
+ * cache line).  forward_workspace is required: that of the forward over the same
+ * (mu, chol_raw, amp) and config, with its int64 tile_ptr and ids.  Fields off the mask path,
+ * dense fields (num_pairs >= 16 T) and fields with heavy-tile workgroups run
+ * gf_backward_reduce + gf_backward_finish into the same place.  The gradients agree with
+ * gf_backward's within fp32 rounding (the map is applied per tile, in fp32).
+ */
+int gf_backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                       const float* grad_delta, const float* row_coords, const float* col_coords,
+                       const float* mu, const float* chol_raw, const float* amp, const int64_t* tile_ptr,
+                       const int64_t* gaussian_ids, int64_t num_pairs, void* forward_workspace,
+                       size_t forward_workspace_bytes, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Kernel launches gf_backward_direct makes for this field and pair count: 1 (the direct
+ * kernel) or 2 (reduction + finish); the negated error code on an invalid configuration. */
+int gf_backward_direct_launches(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                                int64_t num_pairs);
+
+/* Byte offset, in a forward workspace, of gf_backward_direct's gradient slots (K x 8 floats).
+ * 0 on an invalid configuration. */
+size_t gf_forward_grads_offset(int64_t out_features, int64_t in_features, int64_t k,
+                               const gf_field_config* cfg);
+
+/*
  * Batched fields (no single-call counterpart in the reference, which renders each adapted
  * layer separately, gaussian_linear.py:162-220; this is the batched launch of an SD1.5
  * UNet's adapted attention layers).  Every phase runs as one launch over all layers, each layer with the

@@ -572,6 +572,108 @@ def test_gf_forward_random_fields(device, i):
         assert torch.equal(small.ids[:P // 2], one.ids[:P // 2])
 
 
+def _direct_vs_two_launch(plan, q, P, r64=None, r=None):
+    """FieldPlan.backward_direct against FieldPlan.backward (reduction + finish) on the same
+    forward; with r64 / r (float64 / fp32 oracle results) also against float64."""
+    two = [t.clone() for t in plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
+                                            num_pairs=P)]
+    one = [t.clone() for t in plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
+                                                   num_pairs=P)]
+    torch.cuda.synchronize()
+    assert plan.status("backward") == 0
+    errs = {}
+    for k, (name, a, b) in enumerate(zip(("d_mu", "d_chol_raw", "d_amp"), one, two)):
+        if r64 is not None:
+            c = r64[3 + k]
+            if not bool(torch.isfinite(c).all()):
+                continue
+            cn = float(c.norm())
+            if cn > 0.0:
+                ed = float((a.cpu().double() - c).norm()) / cn
+                eo = float((r[3 + k].double() - c).norm()) / cn
+                assert ed <= eo + 1e-4, (name, ed, eo)
+        errs[name] = grad_close(a, b, f"{name}: direct vs two launches")
+    return one, errs
+
+
+@pytest.mark.parametrize("case", ["cfg1", "cfg2", "cfg3", "cfg3_clamp24", "cfg2_normalize", "cfg2_noclamp",
+                                  "cfg3_tile32"])
+def test_backward_direct_matches_oracle(device, case):
+    """gf_backward_direct (the chain rule applied per tile with the maps k_prep stores, one
+    launch) against the CPU oracle and against the reduction + finish, then a second forward
+    with other parameters on the same plan (the forward clears the gradients the direct
+    backward adds into)."""
+    base, _, opt = case.partition("_")
+    kw = {"clamp24": dict(clamp_quad=24.0), "normalize": dict(normalize=True), "noclamp": dict(clamp_quad=None),
+          "tile32": dict(tile_out=32, tile_in=32), "": {}}[opt]
+    okw = dict(tile_out=kw.get("tile_out", 16), tile_in=kw.get("tile_in", 16), normalize=kw.get("normalize", False),
+               clamp=kw.get("clamp_quad", 80.0))
+    for seed in (11, 12):
+        p = getattr(wl, base)(seed)
+        r = oracle(p, **okw)
+        P = int(r[1][-1])
+        say(f"{case} seed {seed}: M={p.out_features} N={p.in_features} K={p.k} P={P} {kw}")
+        if seed == 11:
+            plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=P + 4096, **kw)
+        q = p.to(device)
+        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+        assert plan.direct_launches(P) == 1
+        one, errs = _direct_vs_two_launch(plan, q, P)
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), one, r[3:]):
+            errs[name + " vs oracle"] = grad_close(a, b, name)
+        say("  ok " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_backward_direct_random_fields(device, i):
+    """The direct backward on the seeded random fields of test_gf_forward_random_fields (ragged
+    sizes, indefinite covariances through the general-form pass, normalisation, clamps 24 / 80 /
+    200 / none, sigma 1.5..3.5): at least as close to the float64 evaluation as the fp32 oracle,
+    and within 1e-4 of the reduction + finish."""
+    p, cfg = _random_forward_problem(i)
+    r = fo.gaussian_field_fwd_bwd_batched(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad, 16, 16,
+                                          cfg["sigma"], cfg["normalize"], cfg["clamp"])
+    r64 = fo.gaussian_field_fwd_bwd_fp64(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad, 16, 16,
+                                         cfg["sigma"], cfg["normalize"], cfg["clamp"])
+    P = int(r[1][-1])
+    say(f"{p.name} P={P} {cfg}")
+    q = p.to(device)
+    plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=max(P, 1),
+                     sigma_multiplier=cfg["sigma"], normalize=cfg["normalize"], clamp_quad=cfg["clamp"])
+    plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+    _direct_vs_two_launch(plan, q, P, r64, r)
+
+
+def test_backward_direct_fallbacks(device):
+    """Fields the one-launch kernel does not take run the reduction + finish into the direct
+    gradients: FieldPlan.backward's kernels (equal up to the order of the float atomics).  Dense
+    tiles (>= 16 pairs a tile), heavy-tile workgroups (K >= 2048), the emission path (K past the
+    masks) and 8x8 tiles; K = 0."""
+    cases = [
+        (wl.make_problem("dense_320_k600", 320, 320, 600, math.log(24.0), 0.2, 31), {}),
+        (wl.make_problem("heavy_640_k2048", 640, 640, 2048, math.log(6.0), 0.5, 32, clusters=4,
+                         cluster_sigma_px=30.0), {}),
+        (wl.make_problem("emit_320_k9000", 320, 320, 9000, math.log(2.0), 0.5, 33), {}),
+        (wl.make_problem("tile8_200_k100", 200, 200, 100, math.log(4.0), 0.5, 34), dict(tile_out=8, tile_in=8)),
+        (wl.make_problem("k0_64", 64, 64, 0, 0.0, 0.5, 35), {}),
+    ]
+    for p, kw in cases:
+        q = p.to(device)
+        plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=max(1, 400 * p.k), **kw)
+        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+        torch.cuda.synchronize()
+        P = plan.pairs()
+        T = plan.T
+        say(f"{p.name}: P={P} T={T} {kw}")
+        assert plan.status() == 0 and plan.direct_launches(P) == 2
+        two = [t.clone() for t in plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
+                                                num_pairs=P)]
+        one = plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
+        torch.cuda.synchronize()
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), one, two):
+            grad_close(a, b, name, rtol=1e-5)
+
+
 def test_backward_stripes(device):
     """Tile grids of >= 8192 tiles spread each Gaussian's accumulators over 4 stripes (>= 16384:
     16): a 1280x1792 field (8960 tiles) against the oracle, alone and as a batch layer next to a
