@@ -865,7 +865,6 @@ struct PrepOut {
   GfCov cov;
   float mu0, mu1;
   float l11, l22;
-  float r11, r21, r22;  // chol_raw (l21 = r21)
 };
 
 struct PrepLoad {
@@ -885,9 +884,6 @@ __device__ inline PrepOut prep_rect(const Problem& p, const PrepLoad& in) {
   o.cov = gf_cov_from_chol(Lc);
   o.l11 = Lc.l11;
   o.l22 = Lc.l22;
-  o.r11 = in.r11;
-  o.r21 = in.r21;
-  o.r22 = in.r22;
   int32_t touched;
   o.rect = bin_rect(p, o.mu0, o.mu1, o.cov, &touched);
   return o;
@@ -946,7 +942,6 @@ __device__ inline void store_dcoef(const Problem& p, GfCov cov, float l11f, floa
   dg[1] = make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
-template <bool kCoef>
 __device__ inline void store_prep(const Problem& p, const PrepOut& o, float amp, int64_t g, uint8_t* ws,
                                   const FwdLayout& L) {
   reinterpret_cast<int4*>(ws + L.rect)[g] = o.rect;
@@ -955,16 +950,30 @@ __device__ inline void store_prep(const Problem& p, const PrepOut& o, float amp,
   GaussEval v = eval_from_cov(p, o.mu0, o.mu1, o.cov, amp);
   v.gid = (int32_t)g;
   store_eval(reinterpret_cast<GaussEval*>(ws + L.eval), g, v);
-  if (kCoef) store_dcoef(p, o.cov, o.l11, o.l22, o.r11, o.r21, o.r22, amp, g, ws, L);
 }
 
-// One thread per Gaussian: rectangle, covariance and evaluation constants, and (kCoef: fields
-// binned in the render, with no k_bin_tiles launch) the chain-rule map.
+// One thread per Gaussian: rectangle, covariance and evaluation constants.  kCoef (fields
+// binned in the render, with no k_bin_tiles launch): a second set of ceil(K / 256) workgroups
+// computes the chain-rule maps, each thread recomputing its Gaussian's covariance (the same
+// functions, so the same bits), beside the first set rather than after it on each thread's
+// dependent chain.
 template <bool kCoef>
 __global__ __launch_bounds__(kTilesThreads) void k_prep(Problem p, const float* __restrict__ mu,
                                                         const float* __restrict__ chol_raw,
                                                         const float* __restrict__ amp, uint8_t* ws,
                                                         FwdLayout L, int64_t* num_pairs) {
+  if (kCoef) {
+    const int64_t nb = (p.K + kTilesThreads - 1) / kTilesThreads;
+    if ((int64_t)blockIdx.x >= nb) {
+      const int64_t g = ((int64_t)blockIdx.x - nb) * kTilesThreads + threadIdx.x;
+      if (g < p.K) {
+        const PrepLoad in = prep_load(mu, chol_raw, g);
+        const GfChol Lc = gf_activate_cholesky(in.r11, in.r21, in.r22);
+        store_dcoef(p, gf_cov_from_chol(Lc), Lc.l11, Lc.l22, in.r11, in.r21, in.r22, amp[g], g, ws, L);
+      }
+      return;
+    }
+  }
   const int64_t g = (int64_t)blockIdx.x * kTilesThreads + threadIdx.x;
   if (g == 0) {
     WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
@@ -972,7 +981,7 @@ __global__ __launch_bounds__(kTilesThreads) void k_prep(Problem p, const float* 
     hdr->heavy = 0u;
     hdr->num_pairs = num_pairs;
   }
-  if (g < p.K) store_prep<kCoef>(p, prep_rect(p, prep_load(mu, chol_raw, g)), amp[g], g, ws, L);
+  if (g < p.K) store_prep(p, prep_rect(p, prep_load(mu, chol_raw, g)), amp[g], g, ws, L);
 }
 
 __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t* __restrict__ tile_ptr,
@@ -3321,8 +3330,9 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
     const unsigned lines = (unsigned)(p.R + p.C);
     const bool in_render = tiles_in_render(p);
-    hipLaunchKernelGGL(in_render ? k_prep<true> : k_prep<false>, dim3((unsigned)((k + kTilesThreads - 1) / kTilesThreads)),
-                       dim3(kTilesThreads), 0, st, p, mu, chol_raw, amp, ws, L, num_pairs_dev);
+    const unsigned nb = (unsigned)((k + kTilesThreads - 1) / kTilesThreads);
+    hipLaunchKernelGGL(in_render ? k_prep<true> : k_prep<false>, dim3(in_render ? 2 * nb : nb), dim3(kTilesThreads), 0,
+                       st, p, mu, chol_raw, amp, ws, L, num_pairs_dev);
     GF_LAUNCH_CHECK("k_prep");
     p.heavy = heavy_threshold(p);
     if (!in_render)
