@@ -122,6 +122,38 @@ def test_workspace_and_pointer_checks():
     assert rc == GF_E_INVALID_ARGUMENT
 
 
+def test_backward_direct_host_logic():
+    """gf_backward_direct's host side: the launch count it will make (1 on the mask path with
+    sparse 16x16 / 32x32 tiles and no heavy-tile workgroups, 2 elsewhere), where its gradient
+    slots lie in the forward workspace, and the workspace check before any device work."""
+    lib = N.lib()
+    cfg = ctypes.byref(_cfg())
+
+    def launches(M, Nf, K, P, c=cfg):
+        return lib.gf_backward_direct_launches(c, M, Nf, K, P)
+
+    assert launches(1280, 1280, 1024, 23618) == 1          # cfg3
+    assert launches(1280, 1280, 1024, 16 * 6400) == 2      # dense tiles: the transposing reduction
+    assert launches(1280, 1280, 2048, 40000) == 2          # heavy-tile workgroups (K >= 2048)
+    assert launches(320, 320, 9000, 20000) == 2            # past the masks: the emission path
+    assert launches(320, 768, 256, 2000) == 1              # cfg2, binned in the render
+    assert launches(1280, 1280, 1024, 23618, ctypes.byref(_cfg(tile_out=32, tile_in=32))) == 1
+    assert launches(200, 200, 100, 500, ctypes.byref(_cfg(tile_out=8, tile_in=8))) == 2
+    assert launches(64, 64, 0, 0) == 2
+    assert launches(64, 64, 4, 10, ctypes.byref(_cfg(tile_out=0))) == -GF_E_INVALID_ARGUMENT
+    for M, Nf, K in ((1280, 1280, 1024), (320, 768, 256), (45, 70, 9000)):
+        off = lib.gf_forward_grads_offset(M, Nf, K, cfg)
+        total = lib.gf_forward_workspace_bytes(M, Nf, K, cfg)
+        assert off % 256 == 0 and 256 <= off and off + 32 * K <= total
+    need = lib.gf_forward_workspace_bytes(64, 64, 4, cfg)
+    rc = lib.gf_backward_direct(cfg, 64, 64, 4, None, None, None, None, None, None, None, None, 10, None,
+                                need, None, 0, None)
+    assert rc == GF_E_WORKSPACE and "forward workspace" in lib.gf_last_error().decode()
+    rc = lib.gf_backward_direct(cfg, 64, 64, 4, None, None, None, None, None, None, None, None, 10, 256,
+                                need - 1, None, 0, None)
+    assert rc == GF_E_WORKSPACE
+
+
 def test_shim_rejects_cpu_tensors_with_reference_messages():
     from guass_amd.cuda_field import ext
 
