@@ -3531,11 +3531,14 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
                             forward_workspace, workspace, workspace_bytes, stream);
 }
 
-// gf_backward_direct runs one launch where k_prep stored the chain-rule maps (the mask path)
-// and the tiles take the plain row-sum kernel: 16x16 or 32x32 tiles, sparse, no heavy-tile
-// workgroups.  Elsewhere it runs the reduction and the finish, which writes the same gradients.
+// gf_backward_direct runs one launch where the binning stored the chain-rule maps (the mask
+// path) and the tiles take the plain row-sum kernel: 16x16 or 32x32 tiles, sparse, no heavy-tile
+// workgroups, and grids whose reduction keeps one accumulator stripe (S = 1: below 8192 tiles).
+// The direct gradients have one slot per Gaussian; on larger grids a Gaussian can touch
+// thousands of tiles, whose atomics the reduction spreads over S stripes.  Elsewhere it runs
+// the reduction and the finish, which writes the same gradients.
 bool direct_one_launch(const Problem& p, int64_t num_pairs) {
-  return p.W > 0 && quad_tiles(p) && !bwd_dense(p, num_pairs) && heavy_grid(p, num_pairs) == 0;
+  return p.W > 0 && quad_tiles(p) && p.S == 1 && !bwd_dense(p, num_pairs) && heavy_grid(p, num_pairs) == 0;
 }
 
 int gf_backward_direct_launches(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,

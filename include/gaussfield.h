@@ -190,7 +190,8 @@ int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t
  * valid until that next forward (one slot per Gaussian keeps each Gaussian's atomics on one
  * cache line).  forward_workspace is required: that of the forward over the same
  * (mu, chol_raw, amp) and config, with its int64 tile_ptr and ids.  Fields off the mask path,
- * dense fields (num_pairs >= 16 T) and fields with heavy-tile workgroups run
+ * dense fields (num_pairs >= 16 T), grids of 8192 tiles or more (whose reduction spreads each
+ * Gaussian's atomics over stripes) and fields with heavy-tile workgroups run
  * gf_backward_reduce + gf_backward_finish into the same place.  The gradients agree with
  * gf_backward's within fp32 rounding (the map is applied per tile, in fp32).
  */

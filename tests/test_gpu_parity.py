@@ -648,13 +648,14 @@ def test_backward_direct_fallbacks(device):
     """Fields the one-launch kernel does not take run the reduction + finish into the direct
     gradients: FieldPlan.backward's kernels (equal up to the order of the float atomics).  Dense
     tiles (>= 16 pairs a tile), heavy-tile workgroups (K >= 2048), the emission path (K past the
-    masks) and 8x8 tiles; K = 0."""
+    masks), 8x8 tiles, a grid of 8960 tiles (4 accumulator stripes); K = 0."""
     cases = [
         (wl.make_problem("dense_320_k600", 320, 320, 600, math.log(24.0), 0.2, 31), {}),
         (wl.make_problem("heavy_640_k2048", 640, 640, 2048, math.log(6.0), 0.5, 32, clusters=4,
                          cluster_sigma_px=30.0), {}),
         (wl.make_problem("emit_320_k9000", 320, 320, 9000, math.log(2.0), 0.5, 33), {}),
         (wl.make_problem("tile8_200_k100", 200, 200, 100, math.log(4.0), 0.5, 34), dict(tile_out=8, tile_in=8)),
+        (wl.make_problem("stripes_1280x1792_k512", 1280, 1792, 512, math.log(8.0), 0.6, 36), {}),
         (wl.make_problem("k0_64", 64, 64, 0, 0.0, 0.5, 35), {}),
     ]
     for p, kw in cases:
