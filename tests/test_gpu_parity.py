@@ -1661,6 +1661,54 @@ def test_field_plan_resize_within_capacity(device, shape):
         field_close(plan.delta, r[0])
         for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), (d_mu, d_chol, d_amp), r[3:]):
             grad_close(a, b, f"K={k} {name}")
+        # the one-launch backward at this K (its maps and gradient slots move with K)
+        if plan.direct_launches(P) == 1:
+            plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+            direct = plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
+                                          num_pairs=P)
+            torch.cuda.synchronize()
+            for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), direct, r[3:]):
+                grad_close(a, b, f"K={k} {name} (direct)")
+
+
+def test_graph_replay_direct_backward(device):
+    """forward + backward_direct captured in one HIP graph (the bench's step), replayed three
+    times with eager work and poisoned outputs between the replays: every replay's delta-W,
+    ids and gradients against the eager step (the forward's clearing of the gradient slots is
+    a kernel, not a memset)."""
+    p = wl.cfg3(7)
+    q = p.to(device)
+    r = oracle(p)
+    P = int(r[1][-1])
+    plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=P)
+    assert plan.direct_launches(P) == 1
+    s = torch.cuda.Stream(device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(s):
+        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+        eager = [t.clone() for t in plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw,
+                                                         q.amp, num_pairs=P)]
+    torch.cuda.current_stream(device).wait_stream(s)
+    torch.cuda.synchronize()
+    delta0, ids0 = plan.delta.clone(), plan.ids[:P].clone()
+    for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), eager, r[3:]):
+        grad_close(a, b, f"eager {name}")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+        views = plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
+    for rep in range(3):
+        plan.delta.fill_(float("nan"))
+        for v in views:
+            v.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert plan.status() == 0 and plan.status("backward") == 0
+        assert torch.equal(plan.delta, delta0), f"replay {rep}: delta"
+        assert torch.equal(plan.ids[:P], ids0), f"replay {rep}: ids"
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), views, eager):
+            grad_close(a, b, f"replay {rep} {name}", rtol=1e-5)
+        _ = (plan.delta * 2.0).sum().item()  # eager work between replays
 
 
 def run_plan(p: wl.FieldProblem, device, capacity: int, **cfg):
