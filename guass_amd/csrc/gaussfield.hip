@@ -181,7 +181,7 @@ FwdLayout fwd_layout(const Problem& p) {
   o = align256(o + sizeof(uint32_t) * (size_t)p.C * (size_t)p.W);
   L.bsq = o;  // batched render: sum of squares of delta-W over each 16x16 block (block index sidx)
   o = align256(o + sizeof(float) * (size_t)T * (p.tile_out == 32 && p.tile_in == 32 ? 4 : 1));
-  L.dcoef = o;  // k_prep: each Gaussian's chain-rule map from moments to gradients (six float4)
+  L.dcoef = o;  // the binning (k_bin_tiles or k_prep): each Gaussian's chain-rule map (six float4)
   o = align256(o + 6 * sizeof(float4) * (size_t)K);
   L.dgrad = o;  // gf_backward_direct's gradients: [K][8] (d_amp, d_mu x2, d_chol_raw x3, 2 unused)
   o = align256(o + 8 * sizeof(float) * (size_t)K);
@@ -2170,8 +2170,8 @@ __device__ __forceinline__ void bwd16_body(
     uint8_t* ws, const BwdLayout& L, const SubTile& st, int q = 0, int F = 1,
     const float4* __restrict__ dcoef = nullptr, float* __restrict__ dgrad = nullptr) {
   // kDirect (row sums only): each tile's moments go through the Gaussian's chain-rule map
-  // (dcoef, store_dcoef) and the gradients are added straight into dgrad (d_mu | d_chol_raw |
-  // d_amp), so that no finish pass follows.
+  // (dcoef, store_dcoef) and the gradients are added straight into the Gaussian's slot of dgrad
+  // (direct_slot), so that no finish pass follows.
   static_assert(!kDirect || !kTransposeSums, "direct gradients take the row-sum reduction");
   // F > 1 (heavy tiles): the F = 4 waves of the workgroup share tile st, wave q taking chunks
   // q, q + F, ... of kHeavyChunk Gaussians (and their indefinite-form pass).
