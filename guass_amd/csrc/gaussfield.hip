@@ -2768,11 +2768,14 @@ __global__ __launch_bounds__(256) void k_selftest_softplus(unsigned long long* o
 // Host helpers.
 
 // Accumulator stripes of the backward: tile grids large enough to hold Gaussians that touch
-// thousands of tiles (whose atomics on one address serialise) get 4 or 16 stripes; the finish
-// then reads and clears K * S * 32 bytes (one thread per stripe).
+// thousands of tiles (whose atomics on one address serialise) get 4 or 32 stripes; the finish
+// then reads and clears K * S * 32 bytes (one thread per stripe).  32 rather than 16 above 16,384
+// tiles: where the memory channels put a Gaussian's stripe lines depends on the accumulators'
+// base address, and with 16 some bases let stripes share a channel (cfg5's reduction 37-56 us
+// over accumulator placements; 35-39 us with 32; 64 made the finish cost more than it saved).
 int32_t backward_stripes(int64_t K, int64_t T) {
   (void)K;
-  return T >= 16384 ? 16 : (T >= 8192 ? 4 : 1);
+  return T >= 16384 ? 32 : (T >= 8192 ? 4 : 1);
 }
 
 int make_problem(const gf_field_config* cfg, int64_t M, int64_t N, int64_t K, Problem* p) {
@@ -3210,7 +3213,7 @@ void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, 
 // Allocation-free backward (gf_backward_noalloc).  Its workspace -- the header with the status
 // word and the S x K accumulator slots -- lives in this static device array, one copy per GPU,
 // held until the process ends.  4 MiB: K up to 131,064 Gaussians for S = 1 (fewer than 8192 tiles),
-// 32,760 for S = 4 and 8,184 for S = 16.
+// 32,766 for S = 4 and 4,095 for S = 32.
 constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;
 
 // Clears n 16-byte words (a fill kernel rather than hipMemsetAsync, which must not be recorded

@@ -677,7 +677,7 @@ def test_backward_direct_fallbacks(device):
 
 def test_backward_stripes(device):
     """Tile grids of >= 8192 tiles spread each Gaussian's accumulators over 4 stripes (>= 16384:
-    16): a 1280x1792 field (8960 tiles) against the oracle, alone and as a batch layer next to a
+    32): a 1280x1792 field (8960 tiles) against the oracle, alone and as a batch layer next to a
     one-stripe layer (the batched finish maps K * stripes threads per layer)."""
     from guass_amd.ops import FieldBatchPlan
 
