@@ -2768,14 +2768,16 @@ __global__ __launch_bounds__(256) void k_selftest_softplus(unsigned long long* o
 // Host helpers.
 
 // Accumulator stripes of the backward: tile grids large enough to hold Gaussians that touch
-// thousands of tiles (whose atomics on one address serialise) get 4 or 32 stripes; the finish
-// then reads and clears K * S * 32 bytes (one thread per stripe).  32 rather than 16 above 16,384
-// tiles: where the memory channels put a Gaussian's stripe lines depends on the accumulators'
-// base address, and with 16 some bases let stripes share a channel (cfg5's reduction 37-56 us
-// over accumulator placements; 35-39 us with 32; 64 made the finish cost more than it saved).
+// thousands of tiles (whose atomics on one cache line serialise) get 4, 8 or 32 stripes; the
+// finish then reads and clears K * S * 32 bytes (one thread per stripe).  One Gaussian over the
+// whole grid took cfg3's reduction from 9 to 85 us with one stripe and 24 us with 4; at 8,960
+// tiles 33 us with 4 stripes and 19 us with 8.  Where the memory channels put a Gaussian's
+// stripe lines depends on the accumulators' base address: above 16,384 tiles 16 stripes left
+// cfg5's reduction at 37-56 us over placements, 32 at 35-39 us (64: the finish cost more than it
+// saved).  Without hot Gaussians the stripes cost the finish 0.5-1.9 us.
 int32_t backward_stripes(int64_t K, int64_t T) {
   (void)K;
-  return T >= 16384 ? 32 : (T >= 8192 ? 4 : 1);
+  return T >= 16384 ? 32 : (T >= 8192 ? 8 : (T >= 2048 ? 4 : 1));
 }
 
 int make_problem(const gf_field_config* cfg, int64_t M, int64_t N, int64_t K, Problem* p) {
@@ -3212,8 +3214,8 @@ void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, 
 // ------------------------------------------------------------------------------------------
 // Allocation-free backward (gf_backward_noalloc).  Its workspace -- the header with the status
 // word and the S x K accumulator slots -- lives in this static device array, one copy per GPU,
-// held until the process ends.  4 MiB: K up to 131,064 Gaussians for S = 1 (fewer than 8192 tiles),
-// 32,766 for S = 4 and 4,095 for S = 32.
+// held until the process ends.  4 MiB: K up to 131,064 Gaussians for S = 1 (fewer than 2048 tiles),
+// 32,766 for S = 4, 16,383 for S = 8 and 4,095 for S = 32.
 constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;
 
 // Clears n 16-byte words (a fill kernel rather than hipMemsetAsync, which must not be recorded
@@ -3536,12 +3538,14 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
 
 // gf_backward_direct runs one launch where the binning stored the chain-rule maps (the mask
 // path) and the tiles take the plain row-sum kernel: 16x16 or 32x32 tiles, sparse, no heavy-tile
-// workgroups, and grids whose reduction keeps one accumulator stripe (S = 1: below 8192 tiles).
-// The direct gradients have one slot per Gaussian; on larger grids a Gaussian can touch
-// thousands of tiles, whose atomics the reduction spreads over S stripes.  Elsewhere it runs
-// the reduction and the finish, which writes the same gradients.
+// workgroups, and fewer than 8192 tiles.  The direct gradients have one slot per Gaussian, so a
+// Gaussian's atomics cannot be spread over stripes: on larger grids, whose Gaussians can touch
+// thousands of tiles, it runs the reduction and the finish, which writes the same gradients.
+// (Below 8192 tiles a Gaussian over the whole grid still costs the direct kernel what it cost
+// the one-stripe reduction: 85 us at cfg3's grid.)
 bool direct_one_launch(const Problem& p, int64_t num_pairs) {
-  return p.W > 0 && quad_tiles(p) && p.S == 1 && !bwd_dense(p, num_pairs) && heavy_grid(p, num_pairs) == 0;
+  return p.W > 0 && quad_tiles(p) && (int64_t)p.R * p.C < 8192 && !bwd_dense(p, num_pairs) &&
+         heavy_grid(p, num_pairs) == 0;
 }
 
 int gf_backward_direct_launches(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,

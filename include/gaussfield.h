@@ -316,8 +316,8 @@ int gf_batch_read(void* plan, const gf_batch_info* info, int32_t clear, uint32_t
  * constants are recomputed from mu / chol_raw), but the backward workspace is a static device
  * array of 4 MiB held by the library on each GPU it runs on until the process ends; the call
  * makes no hipMalloc / hipFree and allocates nothing else.  It covers fields whose workspace
- * (gf_backward_workspace_bytes) fits 4 MiB: K <= 131,064 below 8192 tiles (K <= 32,766 below
- * 16,384 tiles, K <= 4,095 above); larger fields are rejected with GF_E_WORKSPACE before any
+ * (gf_backward_workspace_bytes) fits 4 MiB: K <= 131,064 below 2048 tiles (K <= 32,766 below
+ * 8192 tiles, K <= 16,383 below 16,384 tiles, K <= 4,095 above); larger fields are rejected with GF_E_WORKSPACE before any
  * device work.  Each call clears the part of the array it uses (a kernel, no memset), so it
  * needs no set-up; every call on one GPU shares that GPU's array, so calls that overlap on one
  * GPU (different streams or threads without ordering) race and must be serialised by the caller.

@@ -134,7 +134,7 @@ def test_backward_direct_host_logic():
 
     assert launches(1280, 1280, 1024, 23618) == 1          # cfg3
     assert launches(1280, 1280, 1024, 16 * 6400) == 2      # dense tiles: the transposing reduction
-    assert launches(1280, 1792, 512, 20000) == 2           # 8960 tiles: 4 accumulator stripes
+    assert launches(1280, 1792, 512, 20000) == 2           # 8960 tiles: 8 accumulator stripes
     assert launches(1280, 1280, 2048, 40000) == 2          # heavy-tile workgroups (K >= 2048)
     assert launches(320, 320, 9000, 20000) == 2            # past the masks: the emission path
     assert launches(320, 768, 256, 2000) == 1              # cfg2, binned in the render

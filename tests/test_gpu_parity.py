@@ -648,7 +648,7 @@ def test_backward_direct_fallbacks(device):
     """Fields the one-launch kernel does not take run the reduction + finish into the direct
     gradients: FieldPlan.backward's kernels (equal up to the order of the float atomics).  Dense
     tiles (>= 16 pairs a tile), heavy-tile workgroups (K >= 2048), the emission path (K past the
-    masks), 8x8 tiles, a grid of 8960 tiles (4 accumulator stripes); K = 0."""
+    masks), 8x8 tiles, a grid of 8960 tiles (8 accumulator stripes); K = 0."""
     cases = [
         (wl.make_problem("dense_320_k600", 320, 320, 600, math.log(24.0), 0.2, 31), {}),
         (wl.make_problem("heavy_640_k2048", 640, 640, 2048, math.log(6.0), 0.5, 32, clusters=4,
@@ -676,8 +676,8 @@ def test_backward_direct_fallbacks(device):
 
 
 def test_backward_stripes(device):
-    """Tile grids of >= 8192 tiles spread each Gaussian's accumulators over 4 stripes (>= 16384:
-    32): a 1280x1792 field (8960 tiles) against the oracle, alone and as a batch layer next to a
+    """Tile grids of >= 2048 tiles spread each Gaussian's accumulators over 4 stripes (>= 8192: 8,
+    >= 16384: 32): a 1280x1792 field (8960 tiles) against the oracle, alone and as a batch layer next to a
     one-stripe layer (the batched finish maps K * stripes threads per layer)."""
     from guass_amd.ops import FieldBatchPlan
 
@@ -1630,12 +1630,12 @@ def test_gaussian_field_batch_densification(device, tile):
     assert fb.replans >= len(events)
 
 
-@pytest.mark.parametrize("shape", [(320, 768), (1280, 1792)], ids=["320x768", "1280x1792_stripes4"])
+@pytest.mark.parametrize("shape", [(320, 768), (1280, 1792)], ids=["320x768", "1280x1792_stripes8"])
 def test_field_plan_resize_within_capacity(device, shape):
     """A single-field FieldPlan moved between K values (densification: clone and prune,
     reference controllers/clone.py:31-56, prune.py:34-45) within its k_capacity: forward and
     backward against the oracle at every K, with no buffer reallocated; past the capacity its
-    buffers grow.  The 1280x1792 field (8960 tiles) has four accumulator stripes, laid out
+    buffers grow.  The 1280x1792 field (8960 tiles) has eight accumulator stripes, laid out
     stripe-major by the current K, so the backward after each K change reads slots the previous
     K's layout left zeroed."""
     M, N = shape

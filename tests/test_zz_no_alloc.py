@@ -2,7 +2,7 @@
 
 Called through the C ABI and checked against the existing entry point gf_backward (same
 kernels, a caller-allocated workspace) and against the CPU oracle, on consecutive calls of
-shrinking size: a field with four accumulator stripes, then cfg2, then cfg1.  Each call clears
+shrinking size: a field with eight accumulator stripes, then cfg2, then cfg1.  Each call clears
 only what it uses, so a smaller call after a larger one must not see the larger one's state.
 """
 
