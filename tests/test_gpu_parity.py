@@ -644,6 +644,36 @@ def test_backward_direct_random_fields(device, i):
     _direct_vs_two_launch(plan, q, P, r64, r)
 
 
+@pytest.mark.parametrize("nbig", [1, 4, 16])
+def test_backward_direct_hot_gaussians(device, nbig):
+    """Gaussians over the whole grid (6,400 tiles each, every tile's atomics on their one slot) in
+    the one-launch backward: against the oracle, then a second backward on the same forward
+    adds the same gradients again (each doubles)."""
+    p = wl.cfg3(3)
+    p.chol_raw[:nbig, 0] = 4.0
+    p.chol_raw[:nbig, 2] = 4.0
+    r = oracle(p)
+    P = int(r[1][-1])
+    say(f"cfg3 with {nbig} whole-grid Gaussians: P={P}")
+    q = p.to(device)
+    plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=P)
+    plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+    if plan.direct_launches(P) != 1:
+        pytest.skip("field not on the one-launch path")
+    once = [t.clone() for t in plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
+                                                    num_pairs=P)]
+    torch.cuda.synchronize()
+    assert plan.status() == 0 and plan.status("backward") == 0
+    for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), once, r[3:]):
+        grad_close(a, b, name)
+    twice = plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), twice, once):
+        grad_close(a, 2.0 * b, f"{name} after a second backward", rtol=1e-5)
+    big = twice[2][:nbig].abs().cpu()
+    assert float(big.min()) > 0.0, "hot Gaussians' gradients missing"
+
+
 def test_backward_direct_fallbacks(device):
     """Fields the one-launch kernel does not take run the reduction + finish into the direct
     gradients: FieldPlan.backward's kernels (equal up to the order of the float atomics).  Dense
