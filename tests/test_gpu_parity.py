@@ -648,7 +648,8 @@ def test_backward_direct_random_fields(device, i):
 def test_backward_direct_hot_gaussians(device, nbig):
     """Gaussians over the whole grid (6,400 tiles each, every tile's atomics on their one slot) in
     the one-launch backward: against the oracle, then a second backward on the same forward
-    adds the same gradients again (each doubles)."""
+    adds the same gradients again (each doubles).  With 16 of them the tiles are dense and the
+    call takes the striped reduction + finish, which writes the same gradients again."""
     p = wl.cfg3(3)
     p.chol_raw[:nbig, 0] = 4.0
     p.chol_raw[:nbig, 2] = 4.0
@@ -658,8 +659,7 @@ def test_backward_direct_hot_gaussians(device, nbig):
     q = p.to(device)
     plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=P)
     plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
-    if plan.direct_launches(P) != 1:
-        pytest.skip("field not on the one-launch path")
+    one_launch = plan.direct_launches(P) == 1  # 16 such Gaussians make the tiles dense: the fallback
     once = [t.clone() for t in plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
                                                     num_pairs=P)]
     torch.cuda.synchronize()
@@ -668,8 +668,10 @@ def test_backward_direct_hot_gaussians(device, nbig):
         grad_close(a, b, name)
     twice = plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
     torch.cuda.synchronize()
+    # the one-launch kernel adds into the slots the forward cleared; the fallback's finish writes them
+    factor = 2.0 if one_launch else 1.0
     for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), twice, once):
-        grad_close(a, 2.0 * b, f"{name} after a second backward", rtol=1e-5)
+        grad_close(a, factor * b, f"{name} after a second backward", rtol=1e-5)
     big = twice[2][:nbig].abs().cpu()
     assert float(big.min()) > 0.0, "hot Gaussians' gradients missing"
 
