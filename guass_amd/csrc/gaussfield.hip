@@ -1180,6 +1180,11 @@ __device__ __forceinline__ void emit_body(const Problem& p, const float* __restr
     GaussEval v = eval_from_cov(p, mu_at(p, mu, 2 * g + 0), mu_at(p, mu, 2 * g + 1), c, amp[g]);
     v.gid = (int32_t)g;
     store_eval(reinterpret_cast<GaussEval*>(ws + L.eval), g, v);
+    // gf_backward_direct's gradient slot, which its reduction + finish add into (on the mask
+    // path store_dcoef clears it)
+    float4* dg = reinterpret_cast<float4*>(ws + L.dgrad) + 2 * g;
+    dg[0] = make_float4(0.f, 0.f, 0.f, 0.f);
+    dg[1] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   auto place = [&](int32_t lb) {
 #pragma unroll
@@ -2649,7 +2654,9 @@ __global__ __launch_bounds__(kTileThreads) void k_bwd_any(
 // lanes of one wave) sum the six moments with xor shuffles, and the first applies the chain
 // rule.  Every lane of the wave must call it (the shuffles).
 // ostride: floats between consecutive Gaussians' outputs in each of d_mu, d_chol_raw, d_amp (0:
-// the arrays [K][2], [K][3], [K][1]; 8: one slot of 8 floats per Gaussian, as gf_backward_direct's).
+// the arrays [K][2], [K][3], [K][1], written; 8: one slot of 8 floats per Gaussian, as
+// gf_backward_direct's, added to: the one-launch kernel adds into those slots too, so both paths
+// accumulate until the next forward clears them).
 __device__ __forceinline__ void finish_body(
     const Problem& p, const float* __restrict__ chol_raw, const float* __restrict__ amp,
     float* __restrict__ d_mu, float* __restrict__ d_chol_raw, float* __restrict__ d_amp, uint8_t* ws,
@@ -2699,7 +2706,12 @@ __device__ __forceinline__ void finish_body(
   const double nrm = (double)rg.norm;
   const double an = a * nrm;
   const int64_t om = ostride ? ostride * g : 2 * g, oc = ostride ? ostride * g : 3 * g, oa = ostride ? ostride * g : g;
-  d_amp[oa] = (float)(nrm * S0);
+  // gf_backward_direct's slots accumulate (one thread per Gaussian: no other writer here)
+  auto put = [ostride](float* __restrict__ out, int64_t i, float v) {
+    if (ostride) out[i] += v;
+    else out[i] = v;
+  };
+  put(d_amp, oa, (float)(nrm * S0));
   float dm0 = (float)(an * (rg.i00 * S1 + rg.i01 * S2));
   float dm1 = (float)(an * (rg.i01 * S1 + rg.i11 * S2));
   if (p.mu_tanh) {  // dL/d(mu_raw) = dL/d(mu) * (1 - tanh(mu_raw)^2), as torch's tanh backward
@@ -2707,8 +2719,8 @@ __device__ __forceinline__ void finish_body(
     dm0 = dm0 * (1.0f - y0 * y0);
     dm1 = dm1 * (1.0f - y1 * y1);
   }
-  d_mu[om + 0] = dm0;
-  d_mu[om + 1] = dm1;
+  put(d_mu, om + 0, dm0);
+  put(d_mu, om + 1, dm1);
   const double G00 = -0.5 * an * S3, G01 = -0.5 * an * S4, G11 = -0.5 * an * S5;
   const double ag00 = rg.i00 * G00 + rg.i01 * G01, ag01 = rg.i00 * G01 + rg.i01 * G11;
   const double ag10 = rg.i01 * G00 + rg.i11 * G01, ag11 = rg.i01 * G01 + rg.i11 * G11;
@@ -2730,9 +2742,9 @@ __device__ __forceinline__ void finish_body(
   const double dl11 = 2.0 * c00 * l11 + (c01 + c10) * l21;
   const double dl21 = (c10 + c01) * l11 + 2.0 * c11 * l21;
   const double dl22 = 2.0 * c11 * l22;
-  d_chol_raw[oc + 0] = (float)(dl11 * softplus_grad_f32(raw11));
-  d_chol_raw[oc + 1] = (float)dl21;
-  d_chol_raw[oc + 2] = (float)(dl22 * softplus_grad_f32(raw22));
+  put(d_chol_raw, oc + 0, (float)(dl11 * softplus_grad_f32(raw11)));
+  put(d_chol_raw, oc + 1, (float)dl21);
+  put(d_chol_raw, oc + 2, (float)(dl22 * softplus_grad_f32(raw22)));
 }
 
 __global__ __launch_bounds__(kTileThreads) void k_bwd_finish(

@@ -39,13 +39,18 @@ class CudaFieldTensorContract:
 
 @dataclass(frozen=True, slots=True)
 class CudaFieldSavedTensorSpec:
-    """Tensors kept by ctx.save_for_backward, in order."""
+    """The persistent tensor set of the training path, with the reference's field order
+    (contracts.py:34-46): the forward's inputs, then the tensors it produces.  The order of
+    ctx.save_for_backward is a different one, SAVED_TENSOR_ORDER."""
 
-    row_coords: str = "row_coords"
-    col_coords: str = "col_coords"
+    # forward inputs kept through ctx.save_for_backward(...)
     mu: str = "mu"
     chol_raw: str = "chol_raw"
     amp: str = "amp"
+    row_coords: str = "row_coords"
+    col_coords: str = "col_coords"
+
+    # tensors the forward produces
     tile_ptr: str = "tile_ptr"
     gaussian_ids_sorted: str = "gaussian_ids_sorted"
 
@@ -63,6 +68,8 @@ STAGE0_THRESHOLDS = CudaFieldStage0Thresholds()
 TENSOR_CONTRACT = CudaFieldTensorContract()
 SAVED_TENSOR_SPEC = CudaFieldSavedTensorSpec()
 NON_DIFFERENTIABLE_ARGS = CudaFieldNonDifferentiableArgs()
+# The order of ctx.save_for_backward in the runtime's Functions (runtime.py:148-156), which is
+# also the order ctx.saved_tensors returns.
 SAVED_TENSOR_ORDER = ("row_coords", "col_coords", "mu", "chol_raw", "amp", "tile_ptr",
                       "gaussian_ids_sorted")
 

@@ -68,7 +68,11 @@ class GaussianFieldCudaReferenceFunction(torch.autograd.Function):
 
 
 class GaussianFieldCudaTrainFunction(torch.autograd.Function):
-    """Training entry (reference runtime.py:107-203)."""
+    """Training entry (reference runtime.py:107-203).  Its first backward in a process emits
+    the reference's one-time notice (runtime.py:165-174), flagged in _backward_warning_emitted;
+    the notice's first sentence is the reference's, so filters on it keep matching."""
+
+    _backward_warning_emitted = False
 
     @staticmethod
     def forward(ctx, row_coords: Tensor, col_coords: Tensor, mu: Tensor, chol_raw: Tensor,
@@ -79,6 +83,12 @@ class GaussianFieldCudaTrainFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_delta: Tensor):
+        if not GaussianFieldCudaTrainFunction._backward_warning_emitted:
+            warnings.warn("gaussian_field_train uses the active custom CUDA backward path. "
+                          "This backend reduces per-tile moments on the GPU (gfx950 kernels of "
+                          "libgaussfield.so) into per-Gaussian gradients. Treat current limits as "
+                          "performance-related rather than correctness fallback.", stacklevel=2)
+            GaussianFieldCudaTrainFunction._backward_warning_emitted = True
         return _backward(ctx, grad_delta, "gaussian_field_backward")
 
 

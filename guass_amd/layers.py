@@ -294,12 +294,15 @@ class GaussianFieldBatch:
     grows the capacities and renders again.  All layers must share the tile shape
     (16x16 or 32x32: the batched kernels), sigma multiplier and normalisation.
 
-    ``render(check=False)`` skips the read-back: no host synchronisation at all, so that a step
-    of render + forward + backward can be captured in a HIP graph and replayed.  It needs the
-    plan of an earlier checked render (the same parameter tensors and K, id capacities that
-    held); ``check()`` then reads back every layer's status, pair count and norm once, e.g. after
-    a number of replays, and raises if a layer's pairs passed its id capacity (a checked
-    render() grows them; capture again after it).
+    ``render(check=False)`` skips the read-back: the step then makes no host synchronisation
+    and no library call other than the three batched launches (forward, the gradient pointers,
+    backward).  It needs the plan of an earlier checked render (the same parameter tensors and K,
+    id capacities that held); ``check()`` then reads back every layer's status, pair count and
+    norm once and raises if a layer's pairs passed its id capacity (a checked render() grows
+    them).  The batched kernels themselves capture and replay in a HIP graph
+    (``FieldBatchPlan.forward`` / ``backward``); capturing a whole step, with autograd and the
+    layers' GEMMs around them, is not supported: one such capture ended the process in the HIP
+    runtime's capture_end, with no cause found in this package's calls.
 
     Densification (the reference trainer's clone / prune, base_trainer.py:126-220) replaces a
     layer's Gaussian parameters with tensors of another K; the next render() re-plans in place.

@@ -171,8 +171,9 @@ class FieldPlan:
         the maps the last forward stored, the gradients added into the forward workspace.
         Returns views (d_mu [K,2], d_chol_raw [K,3], d_amp [K,1]) of that workspace, strided over
         one 8-float slot per Gaussian: the next forward on this plan clears them, so copy what
-        must outlive it.  Fields where the one-launch kernel does not apply run the reduction
-        and the finish into the same slots."""
+        must outlive it.  The gradients are added into the slots (a second call after the same
+        forward doubles them).  Fields where the one-launch kernel does not apply run the
+        reduction and the finish, which adds into the same slots."""
         n = self.capacity if num_pairs is None else int(num_pairs)
         L = N.lib()
         N.check(L.gf_backward_direct(ctypes.byref(self.cfg), self.M, self.N, self.K, grad.data_ptr(),

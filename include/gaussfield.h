@@ -184,15 +184,17 @@ int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t
  * gf_backward in one launch where it can (replaces reference backward.cu:541-716 like
  * gf_backward).  The chain rule is linear in the per-tile moments; the forward's first phase
  * (on the mask path) stores each Gaussian's map from moments to gradients, so the reduction
- * adds gradients instead of moments and no finish pass follows.  The gradients go to the
- * forward workspace, which the next forward on it clears: from byte gf_forward_grads_offset(...)
- * of it, K slots of 8 fp32, slot g = (d_amp[g], d_mu[g][0..1], d_chol_raw[g][0..2], 2 unused),
- * valid until that next forward (one slot per Gaussian keeps each Gaussian's atomics on one
- * cache line).  forward_workspace is required: that of the forward over the same
- * (mu, chol_raw, amp) and config, with its int64 tile_ptr and ids.  Fields off the mask path,
- * dense fields (num_pairs >= 16 T), grids of 8192 tiles or more (whose reduction spreads each
- * Gaussian's atomics over stripes) and fields with heavy-tile workgroups run
- * gf_backward_reduce + gf_backward_finish into the same place.  The gradients agree with
+ * adds gradients instead of moments and no finish pass follows.  The gradients are ADDED into
+ * the forward workspace, which every forward on it clears: from byte gf_forward_grads_offset(...)
+ * of it, K slots of 8 fp32, slot g = (d_amp[g], d_mu[g][0..1], d_chol_raw[g][0..2], 2 unused)
+ * (one slot per Gaussian keeps each Gaussian's atomics on one cache line).  A second call after
+ * the same forward therefore leaves twice the gradients in the slots, whichever path runs;
+ * callers that need one backward's gradients copy them out and run the next forward first.
+ * forward_workspace is required: that of the forward over the same (mu, chol_raw, amp) and
+ * config, with its int64 tile_ptr and ids.  Fields off the mask path, dense fields
+ * (num_pairs >= 16 T), grids of 8192 tiles or more (whose reduction spreads each Gaussian's
+ * atomics over stripes) and fields with heavy-tile workgroups run gf_backward_reduce +
+ * gf_backward_finish, whose finish adds into the same slots.  The gradients agree with
  * gf_backward's within fp32 rounding (the map is applied per tile, in fp32).
  */
 int gf_backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
@@ -309,9 +311,10 @@ int gf_batch_read(void* plan, const gf_batch_info* info, int32_t clear, uint32_t
                   int64_t* pairs_host, double* delta_norm_host, void* stream);
 
 /*
- * Allocation-free gf_backward.  No counterpart in the reference (whose backward allocates its
- * buffers on every call, backward.cu:541-716); it is for callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Allocation-free gf_backward.  A project-only interface with no counterpart in the reference,
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Call it once outside any capture first: that call
+ * looks up this GPU's scratch address (hipGetSymbolAddress) and keeps it.
  * Same arguments and gradients as gf_backward with forward_workspace = NULL (the Gaussians'
  * constants are recomputed from mu / chol_raw), but the backward workspace is a static device
  * array of 4 MiB held by the library on each GPU it runs on until the process ends; the call

@@ -188,6 +188,63 @@ def test_runtime_surface():
         assert callable(getattr(ext, name)), name
 
 
+def test_saved_tensor_spec_field_order():
+    """CudaFieldSavedTensorSpec declares its fields in the reference's order (contracts.py:34-46);
+    SAVED_TENSOR_ORDER is the save_for_backward order (runtime.py:148-156)."""
+    import dataclasses
+
+    from guass_amd.cuda_field import contracts
+
+    names = [f.name for f in dataclasses.fields(contracts.CudaFieldSavedTensorSpec)]
+    assert names == ["mu", "chol_raw", "amp", "row_coords", "col_coords", "tile_ptr", "gaussian_ids_sorted"]
+    assert all(getattr(contracts.SAVED_TENSOR_SPEC, n) == n for n in names)
+    assert contracts.SAVED_TENSOR_ORDER == ("row_coords", "col_coords", "mu", "chol_raw", "amp", "tile_ptr",
+                                            "gaussian_ids_sorted")
+
+
+def test_train_function_backward_notice_once(monkeypatch):
+    """The training Function emits its backward notice once per process and keeps
+    _backward_warning_emitted (reference runtime.py:119,165-174).  Runs on the CPU with a
+    stand-in extension that records the calls (no kernels)."""
+    import warnings
+
+    from guass_amd.cuda_field import runtime
+
+    class _Ext:
+        calls = []
+
+        def forward_with_workspace(self, row_coords, col_coords, mu, chol_raw, amp, *cfg):
+            self.calls.append("forward")
+            n = row_coords.numel() * col_coords.numel()
+            return (torch.zeros(n), torch.zeros(2, dtype=torch.int64), torch.zeros(0, dtype=torch.int64),
+                    torch.zeros(1, dtype=torch.uint8))
+
+        def gaussian_field_backward(self, grad, row_coords, col_coords, mu, chol_raw, amp, tile_ptr, ids, *cfg,
+                                    forward_workspace=None):
+            self.calls.append("backward")
+            return [torch.ones_like(mu), torch.ones_like(chol_raw), torch.ones_like(amp)]
+
+    stub = _Ext()
+    monkeypatch.setattr(runtime, "load_extension", lambda verbose=False: stub)
+    monkeypatch.setattr(runtime.GaussianFieldCudaTrainFunction, "_backward_warning_emitted", False)
+    mu = torch.zeros(3, 2, requires_grad=True)
+    raw = torch.zeros(3, 3, requires_grad=True)
+    amp = torch.zeros(3, 1, requires_grad=True)
+    seen = []
+    for _ in range(2):
+        delta = runtime.gaussian_field_train(row_coords=torch.zeros(4), col_coords=torch.zeros(5), mu=mu,
+                                             chol_raw=raw, amp=amp, tile_out=16, tile_in=16, sigma_multiplier=3.0)
+        with warnings.catch_warnings(record=True) as caught:
+            warnings.simplefilter("always")
+            delta.sum().backward()
+        seen.append(sum("gaussian_field_train uses the active custom CUDA backward path" in str(w.message)
+                        for w in caught))
+    assert seen == [1, 0]
+    assert runtime.GaussianFieldCudaTrainFunction._backward_warning_emitted
+    assert stub.calls == ["forward", "backward", "forward", "backward"]
+    assert torch.equal(mu.grad, torch.full((3, 2), 2.0))
+
+
 # names exported by gaussian_peft/cuda_field/__init__.py:20-35
 REFERENCE_CUDA_FIELD_ALL = (
     "CUDA_FIELD_EXTENSION_NAME", "CUDA_FIELD_REFERENCE_EXTENSION_NAME", "CUDA_FIELD_SOURCES",
