@@ -27,7 +27,11 @@ Prints one JSON line (metric contract of the driver) with two extra objects:
                 measured live with HIP events on the launch stream around a graph of repeated
                 launches of that kernel (replay time / launch count);
   cpu_baseline  the CPU oracle (a from-scratch port of the reference's torch CPU path) timed on
-                this host on the same inputs (for cfg4, on a stated subset of the layers).
+                this host on the same inputs (for cfg4, on a stated subset of the layers);
+  dropin        (single fields) wall time per call of the path the reference layer calls: the
+                drop-in extension's forward + backward and gaussian_field_train + autograd
+                backward, each with its host synchronisations, beside torch's own autograd cost
+                for a custom Function that does no work.
 """
 
 from __future__ import annotations
@@ -74,6 +78,13 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--kernel-replays", type=int, default=25, help="timed replays per kernel graph")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--dropin-calls", type=int, default=200,
+                    help="single fields: timed calls of the drop-in path the reference layer takes "
+                         "(0: skip); the median goes to the line's `dropin` object")
+    ap.add_argument("--dropin-only", action="store_true",
+                    help="run only the drop-in calls (e.g. under rocprofv3 --hip-trace) and print them")
+    ap.add_argument("--dropin-leg", default="all", choices=["all", "ext", "train", "floor"],
+                    help="--dropin-only: which of the drop-in timings to run")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB (the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -175,6 +186,76 @@ def cpu_baseline(problems, reps: int, note: str, tile: int = 16) -> dict:
             "affinity_cores": affinity, "cgroup_cpu_quota": quota, "kind": "port",
             "sample": f"{note}: fwd+bwd (per-tile loop + autograd), 1 warmup + median of {reps}, "
                       f"{med:.2f} s each"}
+
+
+def dropin_times(q, args, dev) -> dict:
+    """Wall time of the path the reference layer calls (gaussian_linear.py:178-190 ->
+    runtime.py:273-297): the drop-in extension's forward + backward, and gaussian_field_train's
+    forward + autograd backward, each call followed by a device synchronisation; medians over
+    --dropin-calls.  Beside them, torch's own cost for a custom autograd Function with the same
+    arguments that does no work (its forward returns an empty delta, its backward empty
+    gradients): the floor of any implementation behind this interface."""
+    import warnings
+
+    import torch
+
+    from guass_amd.cuda_field import ext, runtime
+
+    cfg = (args.tile, args.tile, 3.0, False, 80.0)
+    mu, raw, amp = (t.clone().requires_grad_(True) for t in (q.mu, q.chol_raw, q.amp))
+    kw = dict(row_coords=q.row_coords, col_coords=q.col_coords, tile_out=args.tile, tile_in=args.tile,
+              sigma_multiplier=3.0, normalize=False, clamp_quad=80.0)
+    n_el = q.row_coords.numel() * q.col_coords.numel()
+
+    class _Floor(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, row_coords, col_coords, mu, chol_raw, amp, *rest):
+            ctx.save_for_backward(row_coords, col_coords, mu, chol_raw, amp)
+            return torch.empty(n_el, device=mu.device)
+
+        @staticmethod
+        def backward(ctx, g):
+            _, _, mu, chol_raw, amp = ctx.saved_tensors
+            return (None, None, torch.empty_like(mu), torch.empty_like(chol_raw), torch.empty_like(amp)) + (None,) * 5
+
+    def ext_call():
+        d, tp, ids, ws = ext.forward_with_workspace(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, *cfg)
+        ext.gaussian_field_backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, tp, ids, *cfg,
+                                    forward_workspace=ws)
+
+    def train_call():
+        for t in (mu, raw, amp):
+            t.grad = None
+        runtime.gaussian_field_train(mu=mu, chol_raw=raw, amp=amp, **kw).backward(q.grad)
+
+    def floor_call():
+        for t in (mu, raw, amp):
+            t.grad = None
+        _Floor.apply(q.row_coords, q.col_coords, mu, raw, amp, *cfg).backward(q.grad)
+
+    def median_us(fn) -> float:
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(args.dropin_calls):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+        return 1e6 * statistics.median(times)
+
+    legs = {"ext": ("ext_fwd_bwd_us", ext_call), "train": ("train_autograd_fwd_bwd_us", train_call),
+            "floor": ("torch_autograd_floor_us", floor_call)}
+    leg = getattr(args, "dropin_leg", "all")
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")  # the training Function's one-time notice
+        out = {name: median_us(fn) for key, (name, fn) in legs.items() if leg in ("all", key)}
+    out.update({"calls": args.dropin_calls, "host_syncs_per_call": 2,
+                "note": "medians of forward + backward + torch.cuda.synchronize() per call; host syncs: the "
+                        "forward's pair count (sizes gaussian_ids_sorted, as the reference) and the "
+                        "backward's saved-state status word"})
+    return out
 
 
 def model_bench(args) -> int:
@@ -387,6 +468,12 @@ def main() -> int:
     batched = args.config == "cfg4"
     probs = wl.cfg4(args.seed, layers=args.layers) if batched else [wl.CONFIGS[args.config](args.seed)]
     qs = [p.to(dev) for p in probs]
+    if args.dropin_only:
+        if batched:
+            print("--dropin-only times a single field", file=sys.stderr)
+            return 2
+        print(json.dumps({"config": args.config, "dropin": dropin_times(qs[0], args, dev)}), flush=True)
+        return 0
     # Pair count of every field (one synchronising drop-in forward each), then sync-free plans.
     counts = []
     for p, q in zip(probs, qs):
@@ -558,6 +645,8 @@ def main() -> int:
         "kernel_rooflines": kernel_rooflines,
         "gpu_event_ms_per_step": gpu_ms / args.steps,
     }
+    if not batched and args.dropin_calls > 0:
+        out["dropin"] = dropin_times(qs[0], args, dev)
     if not args.no_cpu_baseline:
         if batched:
             sub = probs[:2]

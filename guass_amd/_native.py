@@ -158,4 +158,6 @@ def ptr(t) -> int | None:
 
 
 def stream_handle(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """hipStream_t of torch's current stream on ``device`` (as an integer)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)

@@ -13,6 +13,7 @@ word after its kernels to raise the reference's saved-state errors
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 import torch
@@ -21,6 +22,48 @@ from torch import Tensor
 from guass_amd import _native as N
 
 VALIDATE_SAVED_STATE = True
+
+# Host-side facts of a field, by (M, N, K, config): the tile count and the forward / backward
+# workspace sizes (pure functions of the arguments; each costs a library call to compute).
+_GEOMETRY: dict[tuple, tuple[int, int, int, int]] = {}
+_CONFIGS: dict[tuple, N.GfFieldConfig] = {}
+# The backward workspace, per (device, stream): zero at rest (every backward leaves its accumulators
+# zero and its status word is cleared when read), so it is allocated and cleared once and reused.
+# A call that fails drops it.
+_BWD_WS: dict[tuple[int, int], Tensor] = {}
+
+
+def _config(tile_out, tile_in, sigma_multiplier, normalize, clamp_quad) -> N.GfFieldConfig:
+    key = (int(tile_out), int(tile_in), float(sigma_multiplier), bool(normalize),
+           None if clamp_quad is None else float(clamp_quad))
+    cfg = _CONFIGS.get(key)
+    if cfg is None:
+        cfg = _CONFIGS[key] = N.make_config(tile_out, tile_in, sigma_multiplier, normalize, clamp_quad)
+    return cfg
+
+
+def _geometry(M: int, Nf: int, K: int, cfg: N.GfFieldConfig) -> tuple[int, int, int, int]:
+    """(R, C, forward workspace bytes, backward workspace bytes) of an M x N field of K Gaussians."""
+    key = (M, Nf, K, cfg.tile_out, cfg.tile_in, cfg.sigma_multiplier, cfg.normalize, cfg.has_clamp_quad,
+           cfg.clamp_quad)
+    g = _GEOMETRY.get(key)
+    if g is None:
+        L = N.lib()
+        R, C = ctypes.c_int64(), ctypes.c_int64()
+        N.check(L.gf_tile_grid(M, Nf, ctypes.byref(cfg), ctypes.byref(R), ctypes.byref(C)), "gf_tile_grid")
+        g = (R.value, C.value, int(L.gf_forward_workspace_bytes(M, Nf, K, ctypes.byref(cfg))),
+             int(L.gf_backward_workspace_bytes(M, Nf, K, ctypes.byref(cfg))))
+        if len(_GEOMETRY) > 4096:
+            _GEOMETRY.clear()
+        _GEOMETRY[key] = g
+    return g
+
+
+def _on_device(dev: torch.device):
+    """torch.cuda.device(dev) unless dev is already the current device."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(dev)
 
 
 # ------------------------------------------------------------------ checks (common.h:8-24)
@@ -110,28 +153,28 @@ def forward_with_workspace(row_coords: Tensor, col_coords: Tensor, mu: Tensor, c
     if M == 0 or Nf == 0:
         raise RuntimeError("out_features and in_features must be positive")
     L = N.lib()
-    cfg = N.make_config(tile_out, tile_in, sigma_multiplier, normalize, clamp_quad)
-    R, C = ctypes.c_int64(), ctypes.c_int64()
-    N.check(L.gf_tile_grid(M, Nf, ctypes.byref(cfg), ctypes.byref(R), ctypes.byref(C)), "gf_tile_grid")
-    T = R.value * C.value
-    with torch.cuda.device(dev):
+    cfg = _config(tile_out, tile_in, sigma_multiplier, normalize, clamp_quad)
+    R, C, ws_bytes, _ = _geometry(M, Nf, K, cfg)
+    T = R * C
+    pcfg = ctypes.byref(cfg)
+    with _on_device(dev):
         stream = N.stream_handle(dev)
-        ws_bytes = L.gf_forward_workspace_bytes(M, Nf, K, ctypes.byref(cfg))
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        # the device pair count lives in the 8 bytes after the workspace proper
+        ws = torch.empty(ws_bytes + 256, dtype=torch.uint8, device=dev)
+        ws_ptr = ws.data_ptr()
         tile_ptr = torch.empty(T + 1, dtype=torch.int64, device=dev)
-        num_pairs = torch.empty(1, dtype=torch.int64, device=dev)
         P = ctypes.c_int64(0)
-        N.check(L.gf_forward_bin(ctypes.byref(cfg), M, Nf, K, N.ptr(mu), N.ptr(chol_raw), N.ptr(amp),
-                                 tile_ptr.data_ptr(), num_pairs.data_ptr(), ctypes.byref(P),
-                                 ws.data_ptr(), ws_bytes, stream), "gaussian_field_forward (binning)")
+        N.check(L.gf_forward_bin(pcfg, M, Nf, K, N.ptr(mu), N.ptr(chol_raw), N.ptr(amp),
+                                 tile_ptr.data_ptr(), ws_ptr + ws_bytes, ctypes.byref(P),
+                                 ws_ptr, ws_bytes, stream), "gaussian_field_forward (binning)")
         ids = torch.empty(P.value, dtype=torch.int64, device=dev)
         delta = torch.empty(M * Nf, dtype=torch.float32, device=dev)
-        N.check(L.gf_forward_emit(ctypes.byref(cfg), M, Nf, K, N.ptr(mu), N.ptr(amp),
-                                  tile_ptr.data_ptr(), N.ptr(ids), P.value, ws.data_ptr(), ws_bytes,
+        N.check(L.gf_forward_emit(pcfg, M, Nf, K, N.ptr(mu), N.ptr(amp),
+                                  tile_ptr.data_ptr(), N.ptr(ids), P.value, ws_ptr, ws_bytes,
                                   stream), "gaussian_field_forward (emit)")
-        N.check(L.gf_forward_render(ctypes.byref(cfg), M, Nf, K, row_coords.data_ptr(),
+        N.check(L.gf_forward_render(pcfg, M, Nf, K, row_coords.data_ptr(),
                                     col_coords.data_ptr(), tile_ptr.data_ptr(), N.ptr(ids), P.value,
-                                    delta.data_ptr(), ws.data_ptr(), ws_bytes, stream),
+                                    delta.data_ptr(), ws_ptr, ws_bytes, stream),
                 "gaussian_field_forward (render)")
     return delta, tile_ptr, ids, ws
 
@@ -175,22 +218,24 @@ def _backward(grad_delta, row_coords, col_coords, mu, chol_raw, amp, tile_ptr, g
                        gaussian_ids_sorted)
     K = mu.size(0)
     L = N.lib()
-    cfg = N.make_config(tile_out, tile_in, sigma_multiplier, normalize, clamp_quad)
-    R, C = ctypes.c_int64(), ctypes.c_int64()
-    N.check(L.gf_tile_grid(M, Nf, ctypes.byref(cfg), ctypes.byref(R), ctypes.byref(C)), "gf_tile_grid")
-    if tile_ptr.numel() != R.value * C.value + 1:
+    cfg = _config(tile_out, tile_in, sigma_multiplier, normalize, clamp_quad)
+    R, C, fwd_bytes, ws_bytes = _geometry(M, Nf, K, cfg)
+    if tile_ptr.numel() != R * C + 1:
         raise RuntimeError(
             f"saved.tile_ptr has {tile_ptr.numel()} entries, expected num_tiles + 1 = "
-            f"{R.value * C.value + 1} for a {M}x{Nf} field with {tile_out}x{tile_in} tiles")
-    with torch.cuda.device(dev):
+            f"{R * C + 1} for a {M}x{Nf} field with {tile_out}x{tile_in} tiles")
+    with _on_device(dev):
         stream = N.stream_handle(dev)
-        ws_bytes = L.gf_backward_workspace_bytes(M, Nf, K, ctypes.byref(cfg))
-        ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+        key = (dev.index, stream)
+        ws = _BWD_WS.pop(key, None) if VALIDATE_SAVED_STATE else None
+        if ws is None or ws.numel() < ws_bytes:
+            # zero-filled once; without the status read-back (which clears the status word) a
+            # workspace is not reused
+            ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
         fwd_ptr = None
         if forward_workspace is not None:
-            need = L.gf_forward_workspace_bytes(M, Nf, K, ctypes.byref(cfg))
             if (forward_workspace.device != dev or forward_workspace.dtype != torch.uint8
-                    or forward_workspace.numel() < need):
+                    or forward_workspace.numel() < fwd_bytes):
                 raise RuntimeError("forward_workspace does not belong to this field's forward")
             fwd_ptr = forward_workspace.data_ptr()
         d_mu = torch.empty(K, 2, dtype=torch.float32, device=dev)
@@ -204,7 +249,9 @@ def _backward(grad_delta, row_coords, col_coords, mu, chol_raw, amp, tile_ptr, g
                               fwd_ptr, ws.data_ptr(), ws_bytes, stream), "gaussian_field_backward")
         if VALIDATE_SAVED_STATE:
             status = ctypes.c_uint32(0)
-            N.check(L.gf_read_status(ws.data_ptr(), 0, ctypes.byref(status), stream), "gf_read_status")
+            # reads and clears the status word: the workspace is then zero again and kept
+            N.check(L.gf_read_status(ws.data_ptr(), 1, ctypes.byref(status), stream), "gf_read_status")
+            _BWD_WS[key] = ws
             for bit, msg in _SAVED_STATE_MESSAGES:
                 if status.value & bit:
                     raise RuntimeError(msg)
