@@ -312,8 +312,20 @@ def model_bench(args) -> int:
     t_batch = timed(batched, args.steps, args.warmup)
     t_unchecked = timed(batched_unchecked, args.steps, args.warmup)
     fb.check()  # one read-back after the unchecked steps (raises on a status bit)
+    # torch's share: the same 128 GEMMs (forward, weight gradient) through autograd on plain
+    # fp32 weights, with no field at all -- the floor of any step through the layer API
+    plain_w = [ly.weight.detach().clone().requires_grad_(True) for ly in layers]
+
+    def gemms_only():
+        for w in plain_w:
+            w.grad = None
+        torch.autograd.backward([torch.nn.functional.linear(x, w) for w, x in zip(plain_w, xs)], gys)
+
+    t_floor = timed(gemms_only, args.steps, args.warmup)
     if args.skip_per_layer:  # e.g. to trace the batched steps alone
         print(json.dumps({"config": "cfg4-model", "batched_ms_per_step": t_batch * 1e3,
+                          "unchecked_ms_per_step": t_unchecked * 1e3,
+                          "torch_gemm_autograd_floor_ms_per_step": t_floor * 1e3,
                           "steps": args.steps, "warmup": args.warmup}), flush=True)
         return 0
     t_single = timed(per_layer, max(1, args.steps // 5), max(1, args.warmup // 5))
@@ -330,6 +342,7 @@ def model_bench(args) -> int:
                    "layers": len(probs), "sum_out_x_in": int(elements), "k_per_layer": 1024,
                    "tokens_per_layer": args.model_tokens, "delta_apply": args.delta_apply},
         "unchecked_ms_per_step": t_unchecked * 1e3,
+        "torch_gemm_autograd_floor_ms_per_step": t_floor * 1e3,
         "per_layer_ms_per_step": t_single * 1e3,
         "speedup_vs_per_layer": t_single / t_batch,
         "densify": densify,

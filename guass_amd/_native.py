@@ -9,7 +9,7 @@ missing or a call fails, a ``RuntimeError`` is raised.
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, c_char_p, c_double, c_int, c_int32, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
 from pathlib import Path
 
 import torch  # noqa: F401  (must precede the dlopen below)
@@ -63,7 +63,8 @@ class GfLayer(ctypes.Structure):
         ("forward_workspace_bytes", c_size_t), ("grad_delta", c_void_p), ("d_mu", c_void_p),
         ("d_chol_raw", c_void_p), ("d_amp", c_void_p), ("backward_workspace", c_void_p),
         ("backward_workspace_bytes", c_size_t), ("k_capacity", c_int64), ("mu_tanh", c_int32),
-        ("reserved", c_int32),
+        ("reserved", c_int32), ("base_weight", c_void_p), ("merged_weight", c_void_p), ("delta_scale", c_float),
+        ("reserved2", c_int32),
     ]
 
 

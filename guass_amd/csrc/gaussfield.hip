@@ -376,6 +376,53 @@ __device__ inline float4 load4_stream(const float* q) {
 }
 __device__ inline float load_stream(const float* q) { return __builtin_nontemporal_load(q); }
 
+// The merged consumer of a batched layer (gf_layer.merged_weight): besides (or instead of) delta-W
+// the render writes merged = base + scale * delta-W, each element rounded as the fp32 multiply and
+// then the fp32 add of `weight + delta_weight * adapter_scale` (GaussianLinear, delta_apply
+// "merged"), with no contraction into an FMA.
+struct MergedOut {
+  const float* base;  // [M*N], the frozen base weight
+  float* merged;      // [M*N] out; NULL: no merged output
+  float scale;
+};
+
+__device__ inline float merge_weight(float w, float scale, float d) {
+#pragma clang fp contract(off)
+  const float prod = d * scale;  // two roundings, as torch's two elementwise kernels
+  return w + prod;
+}
+
+// Columns pc .. pc+3 of row pr (those inside the matrix) of delta-W from v[], and of the merged
+// weight where there is one.  delta may be NULL (a merged layer whose delta-W is not kept).
+__device__ inline void store_row4(const Problem& p, float* __restrict__ delta, const MergedOut& mo, int32_t pr,
+                                  int32_t pc, const float (&v)[4]) {
+  const int64_t off = (int64_t)pr * p.N + pc;
+  const bool inner = pc + 3 < p.N;
+  if (delta) {
+    float* out = delta + off;
+    if (inner && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+      store4_stream(out, v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (pc + i < p.N) store_stream(out + i, v[i]);
+    }
+  }
+  if (mo.merged) {
+    const float* w = mo.base + off;
+    float* out = mo.merged + off;
+    if (inner && ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(w)) & 15) == 0) {
+      const float4 w4 = load4_stream(w);
+      store4_stream(out, merge_weight(w4.x, mo.scale, v[0]), merge_weight(w4.y, mo.scale, v[1]),
+                    merge_weight(w4.z, mo.scale, v[2]), merge_weight(w4.w, mo.scale, v[3]));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (pc + i < p.N) store_stream(out + i, merge_weight(load_stream(w + i), mo.scale, v[i]));
+    }
+  }
+}
+
 
 // ------------------------------------------------------------------------------------------
 // DPP wave primitives (gfx9 row_shr / row_bcast; no LDS traffic).
@@ -1526,7 +1573,8 @@ __device__ __forceinline__ void render16_body(
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids,
     int64_t capacity, float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
     const uint32_t* __restrict__ colmask, const SubTile& st, const int4* __restrict__ rects = nullptr,
-    int64_t* __restrict__ tile_ptr_out = nullptr, int q = 0, int F = 1, float* __restrict__ blk_sq = nullptr) {
+    int64_t* __restrict__ tile_ptr_out = nullptr, int q = 0, int F = 1, float* __restrict__ blk_sq = nullptr,
+    const MergedOut& mo = MergedOut{nullptr, nullptr, 1.0f}) {
   // F > 1 (heavy tiles, mask path only): the F = 4 waves of the workgroup share tile st, wave q
   // taking chunks q, q + F, ... of kHeavyChunk Gaussians; wave 0 adds the others' partial sums
   // in wave order and writes the tile.  Every wave must call it (two workgroup barriers).
@@ -1810,16 +1858,7 @@ __device__ __forceinline__ void render16_body(
     sq = dpp_scan_f32(sq);
     if (lane == 63) blk_sq[st.sidx] = sq;
   }
-  if (pr < p.M) {
-    float* out = delta + (int64_t)pr * p.N + pc;
-    if (pc + 3 < p.N && ((reinterpret_cast<uintptr_t>(out) & 15) == 0)) {
-      store4_stream(out, acc[0], acc[1], acc[2], acc[3]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (pc + i < p.N) store_stream(out + i, acc[i]);
-    }
-  }
+  if (pr < p.M) store_row4(p, delta, mo, pr, pc, acc);
 }
 
 // Two horizontally adjacent 16x16 tiles of one field by one wave, on the mask path (p.W > 0):
@@ -1839,7 +1878,8 @@ __device__ __forceinline__ void render16x2_body(
     const Problem& p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* __restrict__ ids,
     int64_t capacity, float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
-    const uint32_t* __restrict__ colmask, int32_t tr, int32_t tc, float* __restrict__ blk_sq) {
+    const uint32_t* __restrict__ colmask, int32_t tr, int32_t tc, float* __restrict__ blk_sq,
+    const MergedOut& mo = MergedOut{nullptr, nullptr, 1.0f}) {
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
@@ -2023,16 +2063,7 @@ __device__ __forceinline__ void render16x2_body(
       sq = dpp_scan_f32(sq);
       if (lane == 63) blk_sq[ta + h] = sq;
     }
-    if (pr < p.M) {
-      float* out = delta + (int64_t)pr * p.N + pc;
-      if (pc + 3 < p.N && ((reinterpret_cast<uintptr_t>(out) & 15) == 0)) {
-        store4_stream(out, acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (pc + i < p.N) store_stream(out + i, acc[h][i]);
-      }
-    }
+    if (pr < p.M) store_row4(p, delta, mo, pr, pc, acc[h]);
   }
 }
 
@@ -2670,7 +2701,7 @@ __device__ __forceinline__ void finish_body(
     float* __restrict__ d_mu, float* __restrict__ d_chol_raw, float* __restrict__ d_amp, uint8_t* ws,
     const BwdLayout& L, int64_t idx, const float* __restrict__ mu = nullptr,
     const float4* __restrict__ fwd_cov = nullptr, const float2* __restrict__ fwd_lfac = nullptr,
-    int32_t ostride = 0) {
+    int32_t ostride = 0, float gscale = 1.0f) {
   float* acc = reinterpret_cast<float*>(ws + L.acc);
   const int64_t g = idx / p.S;
   const int32_t st = (int32_t)(idx & (p.S - 1));
@@ -2709,7 +2740,10 @@ __device__ __forceinline__ void finish_body(
     cov = gf_cov_from_chol(Lc);
   }
   const GfRenderGeom rg = gf_render_geom(cov, p.normalize);
-  const double S0 = m[0], S1 = m[1], S2 = m[2], S3 = m[3], S4 = m[4], S5 = m[5];
+  // gscale: dL/d(delta) = gscale * the gradient the moments were taken of (a merged layer's
+  // dL/d(merged weight)); the moments are linear in it
+  const double gs = gscale;
+  const double S0 = gs * m[0], S1 = gs * m[1], S2 = gs * m[2], S3 = gs * m[3], S4 = gs * m[4], S5 = gs * m[5];
   const double a = (double)amp[g];
   const double nrm = (double)rg.norm;
   const double an = a * nrm;
@@ -2934,7 +2968,8 @@ struct BatchLayer {
   float* d_amp;
   int64_t tile_block0, emit_block0, finish_block0, render_block0;
   int32_t pair_render;  // rendered by tile pairs (render map); else tile by tile (tile map)
-  int32_t pad;
+  float grad_scale;     // the backward's moments are multiplied by it (merged layers: delta_scale)
+  MergedOut mo;         // merged consumer (mo.merged NULL: none)
 };
 
 // Plan regions after the header: layers, the tile / emission / finish block maps, the
@@ -3003,6 +3038,8 @@ __device__ inline BatchLayer global_layer(const BatchLayer& src) {
   ly.d_mu = glob(ly.d_mu);
   ly.d_chol_raw = glob(ly.d_chol_raw);
   ly.d_amp = glob(ly.d_amp);
+  ly.mo.base = glob(ly.mo.base);
+  ly.mo.merged = glob(ly.mo.merged);
   return ly;
 }
 
@@ -3054,7 +3091,7 @@ __global__ __launch_bounds__(kTileThreads) void k_render16_batch(const uint8_t* 
                 reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.rowmask),
                 reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.colmask),
                 sub_tile(p, (int64_t)blk - b0, wave_id()), nullptr, nullptr, 0, 1,
-                reinterpret_cast<float*>(ly.fws + ly.fl.bsq));
+                reinterpret_cast<float*>(ly.fws + ly.fl.bsq), ly.mo);
 }
 
 // Layers rendered by tile pairs (16x16 tiles on the mask path at every k up to the capacity):
@@ -3074,7 +3111,7 @@ __global__ __launch_bounds__(kTileThreads) void k_render16x2_batch(const uint8_t
                   ly.tile_ptr, ly.ids, ly.capacity, ly.delta, ly.fws,
                   reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.rowmask),
                   reinterpret_cast<const uint32_t*>(ly.fws + ly.fl.colmask), tr, tc,
-                  reinterpret_cast<float*>(ly.fws + ly.fl.bsq));
+                  reinterpret_cast<float*>(ly.fws + ly.fl.bsq), ly.mo);
 }
 
 // Eight waves per SIMD: the batch's dense-tile body fits 64 VGPRs without spilling, and the
@@ -3154,7 +3191,8 @@ __global__ __launch_bounds__(kTileThreads) void k_finish_batch(const uint8_t* __
   const BwdLayout L = ly.bl;
   finish_body(p, ly.chol_raw, ly.amp, ly.d_mu, ly.d_chol_raw, ly.d_amp, ly.bws, L,
               ((int64_t)blockIdx.x - b0) * kTileThreads + threadIdx.x, ly.mu,
-              reinterpret_cast<const float4*>(ly.fws + ly.fl.cov), reinterpret_cast<const float2*>(ly.fws + ly.fl.lfac));
+              reinterpret_cast<const float4*>(ly.fws + ly.fl.cov), reinterpret_cast<const float2*>(ly.fws + ly.fl.lfac),
+              0, ly.grad_scale);
 }
 
 template <typename TP, typename GI, bool kTS, bool kMC>
@@ -3697,8 +3735,14 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
     ly.bl = bwd_layout(ly.p);
     if (!in.forward_workspace || in.forward_workspace_bytes < ly.fl.total)
       return set_err(GF_E_WORKSPACE, "layer %zu: forward workspace needs %zu bytes", i, ly.fl.total);
-    if (!in.row_coords || !in.col_coords || !in.delta || !in.tile_ptr || !in.num_pairs)
-      return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: coords / delta / tile_ptr / num_pairs must not be NULL", i);
+    if (!in.row_coords || !in.col_coords || !in.tile_ptr || !in.num_pairs)
+      return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: coords / tile_ptr / num_pairs must not be NULL", i);
+    if (!in.delta && !in.merged_weight)
+      return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: delta must not be NULL without a merged_weight", i);
+    if (in.merged_weight && !in.base_weight)
+      return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: merged_weight needs base_weight", i);
+    if (in.merged_weight && !(std::isfinite(in.delta_scale)))
+      return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: delta_scale must be finite", i);
     if (K > 0 && (!in.mu || !in.chol_raw || !in.amp))
       return set_err(GF_E_INVALID_ARGUMENT, "layer %zu: mu / chol_raw / amp must not be NULL", i);
     if (in.ids_capacity < 0 || (in.ids_capacity > 0 && !in.gaussian_ids))
@@ -3732,7 +3776,10 @@ int gf_batch_plan(const gf_field_config* cfg, const gf_layer* layers, int32_t n_
     // The others render tile by tile over the tile map: layers past the masks' K, and layers
     // narrower than a tile, whose tile make_problem clamps to the matrix (emission path).
     ly.pair_render = (!t32 && pc.W > 0) ? 1 : 0;
-    ly.pad = 0;
+    ly.mo.base = in.merged_weight ? in.base_weight : nullptr;
+    ly.mo.merged = in.merged_weight;
+    ly.mo.scale = in.merged_weight ? in.delta_scale : 1.0f;
+    ly.grad_scale = ly.mo.scale;
     if (ly.pair_render)
       render_blocks += ((int64_t)ly.p.R * ((ly.p.C + 1) / 2) + kTileThreads / 64 - 1) / (kTileThreads / 64);
     else

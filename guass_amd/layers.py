@@ -117,7 +117,9 @@ class GaussianLinear(nn.Linear):
         self.register_buffer("col_coords", torch.linspace(-1.0, 1.0, in_features, device=self.weight.device),
                              persistent=False)
         self.last_forward_metadata: dict = {}
-        self._batched_delta: tuple[Tensor, float] | None = None  # (delta-W, its norm) from GaussianFieldBatch
+        # from GaussianFieldBatch.render(): (tensor, norm of delta-W, kind), kind "delta" (delta-W) or
+        # "merged_weight" (weight + adapter_scale * delta-W, for delta_apply "merged")
+        self._batched_delta: tuple[Tensor, float, str] | None = None
         self.reset_gaussian_parameters()
 
     @classmethod
@@ -199,11 +201,11 @@ class GaussianLinear(nn.Linear):
     def compute_delta_weight(self) -> Tensor:
         cfg = self.adapter_config
         pending = self._batched_delta
-        if pending is not None:
+        if pending is not None and pending[2] == "delta":
             # rendered for this step by GaussianFieldBatch.render(), with its norm from the
             # batch's one read-back (no per-layer synchronisation); used once
             self._batched_delta = None
-            delta_weight, norm = pending
+            delta_weight, norm, _ = pending
             metadata = {"execution_mode": cfg.execution_mode, "accumulate_backend": "batched_fields",
                         "delta_w_norm": norm}
             self.last_forward_metadata = metadata
@@ -231,6 +233,17 @@ class GaussianLinear(nn.Linear):
         return min(self.out_features, max(max(1, int(self.adapter_config.tile_out)), 64))
 
     def forward(self, input: Tensor) -> Tensor:
+        pending = self._batched_delta
+        if pending is not None and pending[2] == "merged_weight":
+            # weight + adapter_scale * delta-W, written by GaussianFieldBatch's render (the same
+            # fp32 roundings as the two elementwise operations below); used once.  (Plain
+            # attributes, set without nn.Module's bookkeeping: this runs per layer per step.)
+            merged, norm, _ = pending
+            self.__dict__["_batched_delta"] = None
+            self.__dict__["last_forward_metadata"] = {
+                "execution_mode": self.adapter_config.execution_mode, "accumulate_backend": "batched_fields",
+                "delta_w_norm": norm, "linear_composition": "merged_weight"}
+            return F.linear(input, merged, self._parameters["bias"])
         delta_weight = self.compute_delta_weight().to(dtype=self.weight.dtype)
         if self.adapter_config.delta_apply == "merged":
             metadata = dict(self.last_forward_metadata)
@@ -288,6 +301,12 @@ class GaussianFieldBatch:
 
     A layer whose forward does not run in the step contributes a zero dL/d(delta-W).  The
     rendered delta-W tensors are the plan's own buffers: they hold until the next render().
+
+    A layer with ``delta_apply="merged"`` and a contiguous fp32 weight gets weight +
+    adapter_scale * delta-W from the render itself (rounded as the layer's own two elementwise
+    operations would round it), and its forward is one GEMM on it; its delta-W is not stored, and
+    the backward takes dL/d(merged weight) with adapter_scale applied in the chain rule.  Such a
+    step makes no elementwise launches around the field kernels.
     The forward reads back every layer's status, pair count and ||delta-W|| (the layer's
     ``delta_w_norm`` metadata) at once: one host synchronisation per step, where the reference
     synchronises per layer (gaussian_linear.py:218).  A pair count past a layer's id capacity
@@ -352,9 +371,25 @@ class GaussianFieldBatch:
 
     # ---------------------------------------------------------------- plan
 
+    @staticmethod
+    def _merges(ly: "GaussianLinear") -> bool:
+        """The layer takes weight + adapter_scale * delta-W from the render."""
+        w = ly._parameters["weight"]
+        return (ly.adapter_config.delta_apply == "merged" and w.dtype == torch.float32 and w.is_contiguous()
+                and not w.requires_grad)
+
     def _param_key(self):
-        return tuple((ly.num_gaussians, ly.mu_raw.data_ptr(), ly.chol_raw.data_ptr(), ly.amp.data_ptr())
-                     for ly in self.layers)
+        """What the plan depends on, per layer: K, the parameter tensors' storage, and for a merging
+        layer its weight's storage and adapter_scale (read through the modules' parameter dicts:
+        this runs at every render)."""
+        key = []
+        for ly in self.layers:
+            prm, cfg = ly._parameters, ly.adapter_config
+            mu = prm["mu_raw"]
+            merges = cfg.delta_apply == "merged"
+            key.append((mu.shape[0], mu.data_ptr(), prm["chol_raw"].data_ptr(), prm["amp"].data_ptr(),
+                        prm["weight"].data_ptr() if merges else 0, cfg.adapter_scale if merges else 0.0))
+        return tuple(key)
 
     def _build(self) -> None:
         """Plans, or re-plans in place, for the layers' current K and parameter tensors (which
@@ -382,6 +417,10 @@ class GaussianFieldBatch:
             v.mu, v.chol_raw, v.amp = ly.mu_raw, ly.chol_raw, ly.amp
             v.mu_tanh = True
             v.grad = None
+            if self._merges(ly):
+                v.base_weight = ly.weight.detach()
+                v.delta_scale = float(ly.adapter_config.adapter_scale)
+                v.keep_delta = False
             views.append(v)
         if self._plan is None:
             c0 = self.layers[0].adapter_config
@@ -393,17 +432,21 @@ class GaussianFieldBatch:
             self._plan.update(views, capacities=self._caps, k_capacities=self._kcaps)
             self.replans += 1
         pl = self._plan
-        self._deltas = [q.delta.view(q.M, q.N) for q in pl.plans]
-        # the gradient buffer split per parameter: d_mu_raw [K,2], d_chol_raw [K,3], d_amp [K,1]
-        self._grad_sizes = [n for q in pl.plans for n in (2 * q.K, 3 * q.K, q.K)]
-        self._grad_shapes = [sh for q in pl.plans for sh in ((q.K, 2), (q.K, 3), (q.K, 1))]
+        # per layer: the merged weight where the layer merges, else delta-W
+        self._kinds = ["merged_weight" if m is not None else "delta" for m in pl.merged]
+        self._deltas = [m if m is not None else q.delta.view(q.M, q.N) for q, m in zip(pl.plans, pl.merged)]
+        # the gradient buffer split per parameter: d_mu_raw [K,2], d_chol_raw [K,3], d_amp [K,1],
+        # described by empty tensors of those shapes (one unflatten call makes all the views)
+        self._grad_like = [torch.empty(sh, dtype=torch.float32, device="meta")
+                           for q in pl.plans for sh in ((q.K, 2), (q.K, 3), (q.K, 1))]
         self._key = self._param_key()
 
     # ---------------------------------------------------------------- passes
 
     def render(self, check: bool = True) -> list[Tensor]:
         """Renders every layer's delta-W for this step (autograd-tracked) and hands each layer
-        its own for its next forward; returns them.  ``check=False``: no read-back (see the
+        its own for its next forward; returns them (a merging layer's entry is its merged
+        weight).  ``check=False``: no read-back (see the
         class documentation); each layer's norm metadata is then that of the last checked
         render."""
         if not check and (self._plan is None or self._key != self._param_key()):
@@ -416,8 +459,8 @@ class GaussianFieldBatch:
             for ly in self.layers:
                 params += [ly.mu_raw, ly.chol_raw, ly.amp]
             deltas = _BatchedFieldFunction.apply(self, *params)
-        for ly, d, nrm in zip(self.layers, deltas, self._norms):
-            ly._batched_delta = (d, nrm)
+        for ly, d, nrm, kind in zip(self.layers, deltas, self._norms, self._kinds):
+            ly.__dict__["_batched_delta"] = (d, nrm, kind)  # a plain attribute (no Module bookkeeping)
         return list(deltas)
 
     def check(self) -> list[int]:
@@ -477,4 +520,4 @@ class GaussianFieldBatch:
         # one copy of every layer's gradients (the plan's buffer is rewritten by the next
         # backward), split into the parameters' shapes
         flat = self._plan.grad_flat[:self._plan.grad_numel].clone()
-        return [t.view(sh) for t, sh in zip(flat.split(self._grad_sizes), self._grad_shapes)]
+        return list(torch._utils._unflatten_dense_tensors(flat, self._grad_like))

@@ -219,6 +219,13 @@ class FieldBatchPlan:
     (``self.plans[i]``: delta, tile_ptr, ids, pair constants, gradients).  16x16 or 32x32 tiles
     (32x32: every layer's K <= 8192).
 
+    A layer with a ``base_weight`` attribute (its frozen fp32 weight [M, N], contiguous) gets a
+    merged output, ``self.merged[i]`` [M, N] = base_weight + ``delta_scale`` * delta-W (rounded as
+    torch's ``weight + delta * scale``), written by the render; its ``grad`` is then
+    dL/d(merged weight) and the gradients are those through delta_scale * delta-W.  With a false
+    ``keep_delta`` attribute such a layer's delta-W is not stored (``plans[i].delta`` is not
+    written; the norms still are).
+
     ``k_capacities`` sizes each layer's buffers and the launch grids for that many Gaussians:
     after a layer's K or tensors change (densification), :meth:`update` re-plans in place, and
     for K within the capacities the launch grids and the plan buffer stay the same, so
@@ -233,6 +240,7 @@ class FieldBatchPlan:
         self._plan_kwargs = dict(tile_out=tile_out, tile_in=tile_in, sigma_multiplier=sigma_multiplier,
                                  normalize=normalize, clamp_quad=clamp_quad)
         self.plans: list[FieldPlan] = []
+        self.merged: list[torch.Tensor | None] = []
         self.plan = None
         self.info = None
         self.grad_flat = None
@@ -274,7 +282,6 @@ class FieldBatchPlan:
             grew = grew or self.grad_flat is not None
             self.grad_flat = torch.empty(max(sum(6 * pl.k_capacity for pl in self.plans), 1),
                                          dtype=torch.float32, device=self.device)
-        self.reallocated = grew
         o = 0
         for pl in self.plans:
             K = pl.K
@@ -282,16 +289,35 @@ class FieldBatchPlan:
             pl.d_chol_raw = self.grad_flat[o + 2 * K:o + 5 * K].view(K, 3)
             pl.d_amp = self.grad_flat[o + 5 * K:o + 6 * K].view(K, 1)
             o += 6 * K
+        while len(self.merged) < n:
+            self.merged.append(None)
         table = (N.GfLayer * max(n, 1))()
         for i, (ly, pl) in enumerate(zip(self.layers, self.plans)):
             grad = getattr(ly, "grad", None)
+            base = getattr(ly, "base_weight", None)
+            merged, scale, keep = None, 1.0, True
+            if base is not None:
+                if (base.dtype != torch.float32 or not base.is_contiguous() or base.numel() != pl.M * pl.N
+                        or base.device != self.device):
+                    raise ValueError(f"layer {i}: base_weight must be a contiguous float32 tensor of "
+                                     f"{pl.M}x{pl.N} elements on {self.device}")
+                merged = self.merged[i]
+                if merged is None or merged.numel() != pl.M * pl.N:
+                    grew = grew or merged is not None
+                    merged = torch.empty(pl.M, pl.N, dtype=torch.float32, device=self.device)
+                scale = float(getattr(ly, "delta_scale", 1.0))
+                keep = bool(getattr(ly, "keep_delta", True))
+            self.merged[i] = merged
             table[i] = N.GfLayer(
                 pl.M, pl.N, pl.K, ly.row_coords.data_ptr(), ly.col_coords.data_ptr(), N.ptr(ly.mu),
-                N.ptr(ly.chol_raw), N.ptr(ly.amp), pl.delta.data_ptr(), pl.tile_ptr.data_ptr(),
+                N.ptr(ly.chol_raw), N.ptr(ly.amp), pl.delta.data_ptr() if keep else None, pl.tile_ptr.data_ptr(),
                 pl.num_pairs.data_ptr(), pl.ids.data_ptr(), pl.capacity,
                 pl.fwd_ws.data_ptr(), pl.fwd_ws_bytes, None if grad is None else grad.data_ptr(),
                 N.ptr(pl.d_mu), N.ptr(pl.d_chol_raw), N.ptr(pl.d_amp), pl.bwd_ws.data_ptr(),
-                pl.bwd_ws_bytes, pl.k_capacity, 1 if getattr(ly, "mu_tanh", False) else 0, 0)
+                pl.bwd_ws_bytes, pl.k_capacity, 1 if getattr(ly, "mu_tanh", False) else 0, 0,
+                None if base is None else base.data_ptr(), None if merged is None else merged.data_ptr(),
+                scale, 0)
+        self.reallocated = grew
         info = N.GfBatchInfo()
         L = N.lib()
         N.check(L.gf_batch_plan(ctypes.byref(self.cfg), table, n, None, 0, ctypes.byref(info),

@@ -251,6 +251,18 @@ typedef struct gf_layer {
    * dL/d(mu_raw).  0: mu is used as given. */
   int32_t mu_tanh;
   int32_t reserved;
+  /* Merged consumer (GaussianLinear with delta_apply "merged", reference
+   * gaussian_linear.py:218-242 composes W + adapter_scale * delta-W before its GEMM).  With
+   * merged_weight set, the batched render also writes merged_weight = base_weight +
+   * delta_scale * delta-W, each element rounded as the fp32 product and then the fp32 sum (no FMA),
+   * so it equals torch's `weight + delta * scale` bit for bit; delta may then be NULL (delta-W not
+   * stored; its norm is still read back).  The backward then takes grad_delta as
+   * dL/d(merged_weight) and returns the gradients of the loss through delta_scale * delta-W.
+   * NULL: no merged output, grad_delta is dL/d(delta). */
+  const float* base_weight;      /* [out_features*in_features], read when merged_weight is set */
+  float* merged_weight;          /* [out_features*in_features] out, or NULL */
+  float delta_scale;             /* finite */
+  int32_t reserved2;
 } gf_layer;
 
 typedef struct gf_batch_info {

@@ -2080,3 +2080,123 @@ def test_delta_apply_merged_matches_row_chunk(device):
     assert float((ya - yb).abs().max()) <= 1e-5 * float(ya.abs().max())
     for name in ("mu_raw", "chol_raw", "amp"):
         grad_close(getattr(b, name).grad, getattr(a, name).grad, name, rtol=1e-4)
+
+
+class _MergedView:
+    """A FieldBatchPlan layer (a problem on the device) with a merged consumer."""
+
+    def __init__(self, q, base_weight=None, delta_scale=1.0, keep_delta=True):
+        for name in ("row_coords", "col_coords", "mu", "chol_raw", "amp"):
+            setattr(self, name, getattr(q, name))
+        self.grad = None
+        if base_weight is not None:
+            self.base_weight, self.delta_scale, self.keep_delta = base_weight, delta_scale, keep_delta
+
+
+@pytest.mark.parametrize("tile", [16, 32])
+def test_batch_merged_weight_matches_torch(device, tile):
+    """The batched render's merged output (gf_layer.merged_weight) equals torch's
+    `weight + delta * scale` on the same delta-W bit for bit, and the backward given
+    dL/d(merged weight) G equals the plain backward given dL/d(delta) = G * scale within 1e-5.
+    Layers: cfg2, a ragged 100x77 field (unaligned rows: the scalar store path), and (16x16) a
+    layer whose K capacity past the masks renders it tile by tile; delta-W kept or not."""
+    from guass_amd.ops import FieldBatchPlan
+
+    probs = [wl.cfg2(3), wl.make_problem("ragged_100x77_k40", 100, 77, 40, math.log(4.0), 0.5, 41)]
+    kcaps = [None, None]
+    if tile == 16:
+        probs.append(wl.cfg1(4))
+        kcaps.append(9000)  # capacity on the emission path: k_render16_batch
+    qs = [p.to(device) for p in probs]
+    gen = torch.Generator(device=device).manual_seed(7)
+    ws = [torch.randn(p.out_features, p.in_features, device=device, generator=gen) * 0.02 for p in probs]
+    gs = [torch.randn(p.out_features * p.in_features, device=device, generator=gen) for p in probs]
+    scale = 0.7
+    caps = [int(oracle(p, tile_out=tile, tile_in=tile)[1][-1]) + 64 for p in probs]
+    plain_views = [_MergedView(q) for q in qs]
+    merged_views = [_MergedView(q, w, scale, keep_delta=(i % 2 == 0)) for i, (q, w) in enumerate(zip(qs, ws))]
+    plain = FieldBatchPlan(plain_views, device, capacities=caps, k_capacities=kcaps, tile_out=tile, tile_in=tile)
+    merged = FieldBatchPlan(merged_views, device, capacities=caps, k_capacities=kcaps, tile_out=tile, tile_in=tile)
+    say(f"merged batch ({tile}x{tile}): {[p.name for p in probs]}, tile_render={merged.info.tile_render}")
+    if tile == 16:
+        assert merged.info.tile_render == 1 and merged.info.render_blocks > 0
+    for v, g in zip(plain_views, gs):
+        v.grad = g * scale  # what autograd hands delta-W through `delta * scale`
+    for v, g in zip(merged_views, gs):
+        v.grad = g
+    plain.update()
+    merged.update()
+    for pl in merged.plans:
+        pl.delta.fill_(float("nan"))
+    plain.forward()
+    merged.forward()
+    plain.backward()
+    merged.backward()
+    torch.cuda.synchronize()
+    assert plain.status() == [0] * len(probs) and merged.status() == [0] * len(probs)
+    _, _, n_plain = plain.read(norms=True)
+    _, _, n_merged = merged.read(norms=True)
+    assert n_plain == n_merged
+    for i, (a, b, w) in enumerate(zip(plain.plans, merged.plans, ws)):
+        d = a.delta.view(a.M, a.N)
+        assert torch.equal(merged.merged[i], w + d * scale), f"layer {i}: merged weight"
+        assert merged.merged[i].shape == (a.M, a.N) and plain.merged[i] is None
+        if i % 2 == 0:
+            assert torch.equal(b.delta, a.delta), f"layer {i}: kept delta-W"
+        else:
+            assert bool(torch.isnan(b.delta).all()), f"layer {i}: delta-W written though not kept"
+        for name in ("d_mu", "d_chol_raw", "d_amp"):
+            grad_close(getattr(b, name), getattr(a, name), f"layer {i} {name}", rtol=1e-5)
+
+
+def test_gaussian_field_batch_merged_layers(device):
+    """GaussianLinear layers with delta_apply="merged" in a GaussianFieldBatch take weight +
+    adapter_scale * delta-W from the batched render: one layer of each SD1.5 attention shape
+    (K = 1024).  Outputs and gradients against the same layers rendering their own delta-W and
+    composing it in eager torch (gradients within 1e-5), and the gradients against the CPU
+    oracle through tanh with dL/d(delta-W) = adapter_scale * dL/d(merged weight)."""
+    import copy
+
+    from guass_amd.layers import GaussianFieldBatch
+
+    probs = [_cfg4_layer(i) for i in SD15_SHAPE_PICK]
+    scale = 0.5
+    batched_layers = _layers_from_problems(probs, device)
+    gen = torch.Generator(device=device).manual_seed(9)
+    for ly in batched_layers:
+        ly.adapter_config.delta_apply = "merged"
+        ly.adapter_config.adapter_scale = scale
+        with torch.no_grad():
+            ly.weight.copy_(torch.randn(ly.weight.shape, device=device, generator=gen) * 0.02)
+    eager_layers = [copy.deepcopy(ly) for ly in batched_layers]
+    for ly in eager_layers:
+        ly.adapter_config = copy.copy(ly.adapter_config)
+    xs = [torch.randn(5, p.in_features, device=device, generator=gen) for p in probs]
+    gys = [torch.randn(5, p.out_features, device=device, generator=gen) for p in probs]
+    fb = GaussianFieldBatch(batched_layers)
+    outs = fb.render()
+    for ly, o in zip(batched_layers, outs):
+        assert ly._batched_delta[2] == "merged_weight" and o.shape == ly.weight.shape
+    yb = [ly(x) for ly, x in zip(batched_layers, xs)]
+    torch.autograd.backward(yb, gys)
+    ye = [ly(x) for ly, x in zip(eager_layers, xs)]
+    torch.autograd.backward(ye, gys)
+    torch.cuda.synchronize()
+    for p, a, b, ya, yq, x, gy in zip(probs, batched_layers, eager_layers, yb, ye, xs, gys):
+        say(f"  {p.name} {p.out_features}x{p.in_features}: merged batch vs eager, vs oracle")
+        assert a.last_forward_metadata["accumulate_backend"] == "batched_fields"
+        assert a.last_forward_metadata["linear_composition"] == "merged_weight"
+        assert abs(a.last_forward_metadata["delta_w_norm"] - b.last_forward_metadata["delta_w_norm"]) <= \
+            1e-6 * b.last_forward_metadata["delta_w_norm"]
+        ya, yq = ya.detach(), yq.detach()
+        assert float((ya - yq).abs().max()) <= 1e-5 * float(yq.abs().max()), "layer output"
+        for name in ("mu_raw", "chol_raw", "amp"):
+            grad_close(getattr(a, name).grad, getattr(b, name).grad, f"{name} vs eager", rtol=1e-5)
+        g_delta = (gy.t() @ x) * scale  # dL/d(delta-W) through weight + delta-W * scale
+        r = fo.gaussian_linear_fwd_bwd(a.row_coords.cpu(), a.col_coords.cpu(), a.mu_raw.detach().cpu(),
+                                       a.chol_raw.detach().cpu(), a.amp.detach().cpu(), g_delta.reshape(-1).cpu(),
+                                       16, 16, 3.0, False, 80.0, mu_values=torch.tanh(a.mu_raw.detach()).cpu(),
+                                       batched=True)
+        for name, got, want in zip(("d_mu_raw", "d_chol_raw", "d_amp"), (a.mu_raw.grad, a.chol_raw.grad, a.amp.grad),
+                                   r[3:]):
+            grad_close(got, want, f"{name} vs oracle")
