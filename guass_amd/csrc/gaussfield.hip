@@ -2610,6 +2610,270 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
       dcoef, dgrad);
 }
 
+// ------------------------------------------------------------------------------------------
+// Forward and backward of a field in one pass (gf_fwd_bwd_fused), for a caller that holds
+// dL/d(delta) before the forward: the reference's tile render (forward.cu:254-368) and its
+// per-pair gradient pass (backward.cu:234-388) share each pixel's exponential.  After k_prep +
+// k_bin_tiles (which store the Gaussians' constants, the coverage masks, tile_ptr, the
+// chain-rule maps and clear the gradient slots), one wave per 16x16 tile, four a workgroup:
+//   * the tile's ids are expanded from rowmask & colmask in ascending order (the canonical order
+//     of the stable sort) and written to its segment of gaussian_ids_sorted, as the render does;
+//   * lanes follow the backward's layout: slot = lane / 16 takes Gaussian jb + slot of a round of
+//     four, row = lane % 16 evaluates its row's 16 pixels; each evaluation feeds the pixel's
+//     delta-W partial (acc[c] += amp norm e) and the six moments, which go through the
+//     Gaussian's map into its gradient slot (as gf_backward_direct);
+//   * indefinite forms (GaussEval.gen) are left out of the rounds and taken one at a time by
+//     lanes 0..15 (slot 0: one row each, their own registers), with the clamped pixels' terms
+//     dropped from the quadratic-form moments;
+//   * the four slots' partial rows are added through LDS (slot order) and each lane stores four
+//     pixels of a row (coalesced float4 rows, as the render).
+// delta-W therefore sums each pixel's Gaussians in a different order than the render (four
+// interleaved partial sums): within fp32 rounding of it, not bit-equal.
+template <bool kMaskClamp>
+__global__ __launch_bounds__(kTileThreads) void k_fused16(
+    Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
+    const float* __restrict__ col_coords, const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr,
+    int64_t* __restrict__ ids, int64_t capacity, float* __restrict__ delta, uint8_t* fws,
+    const uint32_t* __restrict__ rowmask, const uint32_t* __restrict__ colmask, const float4* __restrict__ dcoef,
+    float* __restrict__ dgrad) {
+  // per wave: the four slots' partial rows (4 x 16 x 16 floats); its first 16 x 20 floats stage
+  // the dL/d(delta) tile before the rounds
+  __shared__ float4 dtile[kTileThreads / 64][4 * 64];
+  constexpr int kGs = 20;  // row stride (floats) of the staged dL/d(delta) tile: conflict-free float4 reads
+  WsHeader* hdr = reinterpret_cast<WsHeader*>(fws);
+  const int lane = threadIdx.x & 63;
+  const int wid = wave_id();
+  const SubTile st = sub_tile(p, blockIdx.x, wid);
+  const int64_t T = (int64_t)p.R * p.C;
+  const int64_t t = st.t;
+  if (t >= T) return;
+  const int32_t r0 = st.r0, c0 = st.c0;
+  const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (int64_t)tr * p.C);
+  const int slot = lane >> 4, row = lane & 15;
+  float* gt = reinterpret_cast<float*>(dtile[wid]);
+  float gv[16], yv[16];
+  {
+    const int32_t lr = r0 + (lane >> 2), lc = c0 + ((lane & 3) << 2);
+    const float* gp = grad + (int64_t)min(lr, p.M - 1) * p.N + lc;
+    float4 g4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (lr < p.M) {
+      if (lc + 3 < p.N && ((reinterpret_cast<uintptr_t>(gp) & 15) == 0)) {
+        g4 = load4_stream(gp);
+      } else {
+        g4.x = lc < p.N ? load_stream(gp) : 0.f;
+        g4.y = lc + 1 < p.N ? load_stream(gp + 1) : 0.f;
+        g4.z = lc + 2 < p.N ? load_stream(gp + 2) : 0.f;
+        g4.w = lc + 3 < p.N ? load_stream(gp + 3) : 0.f;
+      }
+    }
+    *reinterpret_cast<float4*>(gt + (lane >> 2) * kGs + ((lane & 3) << 2)) = g4;
+    wave_sync();
+#pragma unroll
+    for (int c = 0; c < 16; c += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(gt + row * kGs + c);
+      gv[c] = v.x;
+      gv[c + 1] = v.y;
+      gv[c + 2] = v.z;
+      gv[c + 3] = v.w;
+    }
+  }
+  if (c0 + 15 < p.N && ((reinterpret_cast<uintptr_t>(col_coords + c0) & 15) == 0)) {
+    const float4* yq = reinterpret_cast<const float4*>(col_coords + c0);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float4 v = yq[c];
+      yv[4 * c] = v.x;
+      yv[4 * c + 1] = v.y;
+      yv[4 * c + 2] = v.z;
+      yv[4 * c + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) yv[c] = col_coords[min(c0 + c, p.N - 1)];
+  }
+  const float x = row_coords[min(r0 + row, p.M - 1)];
+  const int64_t s = tile_ptr[t], count = tile_ptr[t + 1] - s;
+  // ids are written to [s, s + room): none for a segment below the id buffer or reversed
+  const int64_t room = s < 0 ? 0 : capacity - s < count ? (capacity - s > 0 ? capacity - s : 0) : count;
+  if ((s < 0 || count < 0) && lane == 0) set_status(&hdr->status, GF_STATUS_TILE_PTR_ORDER);
+  float acc[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) acc[c] = 0.f;
+  wave_sync();  // the staged dL/d(delta) is read before dtile takes the partial rows
+
+  // The rounds over a chunk of nj <= 64 Gaussians (lane j holds Gaussian j: constants my, id myg).
+  auto run_chunk = [&](const GaussEval& my, int32_t myg, int nj) {
+    const bool chunk_general = __builtin_amdgcn_ballot_w64(lane < nj && my.gen != 0.0f) != 0;
+    for (int jb = 0; jb < nj; jb += 4) {
+      const int j = jb + slot;
+      const int addr = j < nj ? j << 2 : 0;  // ds_bpermute byte address of the slot's lane
+      auto from = [&](float v) { return __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(v))); };
+      const float mu0 = from(my.mu0), mu1 = from(my.mu1);
+      const float wa = from(my.wa), wb = from(my.wb);
+      const float wc = from(my.wc), w = from(my.w);
+      const float gen = chunk_general ? from(my.gen) : 0.0f;
+      int32_t g = __builtin_amdgcn_ds_bpermute(addr, myg);
+      const bool live = j < nj && !(chunk_general && gen != 0.0f);  // indefinite forms: below
+      if (!live) g = -1;
+      const float wr = live ? w : 0.0f;
+      const float dx = x - mu0;
+      const float a = wa * dx;
+      const float A = a * a;
+      const float b = wb * dx;
+      // lanes 10..15 of a slot take output row - 10 of the slot's Gaussian's map
+      float4 cf = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (row >= 10 && g >= 0) cf = dcoef[6 * (uint32_t)g + (uint32_t)(row - 10)];
+      float t0 = 0.f, t2 = 0.f, t3 = 0.f, tq = 0.f;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const float dy = yv[c] - mu1;
+        const float z = fmaf(wc, dy, b);
+        if (kMaskClamp) {
+          // the render's floored basis; clamped pixels (q > clamp_quad) add to S0 only (the
+          // reference's clamp mask, backward.cu:316-320,336-338)
+          const float qv = -fmaf(z, z, A);
+          const float e = __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(qv, p.q_lo, 0.0f));
+          acc[c] = fmaf(wr, e, acc[c]);
+          const float ge = gv[c] * e;
+          t0 += ge;
+          const float gq = qv < p.q_lo ? 0.0f : ge;
+          tq += gq;
+          const float tt = gq * dy;
+          t2 += tt;
+          t3 = fmaf(tt, dy, t3);
+        } else {
+          // clamp >= 80 (or none): the floor only moves bases below e^-40, dropped as in the
+          // render and the backward
+          const float e = __builtin_amdgcn_exp2f(-fmaf(z, z, A));
+          acc[c] = fmaf(wr, e, acc[c]);
+          const float ge = gv[c] * e;
+          t0 += ge;
+          const float tt = ge * dy;
+          t2 += tt;
+          t3 = fmaf(tt, dy, t3);
+        }
+      }
+      const float t0q = kMaskClamp ? tq : t0;
+      const float m0 = t0, m1 = dx * t0q, m2 = t2, m3 = dx * dx * t0q, m4 = dx * t2, m5 = t3;
+      const float s0 = dpp_row_allsum_f32(m0), s1 = dpp_row_allsum_f32(m1), s2 = dpp_row_allsum_f32(m2);
+      const float s3 = dpp_row_allsum_f32(m3), s4 = dpp_row_allsum_f32(m4), s5 = dpp_row_allsum_f32(m5);
+      const int k = row - 10;
+      const float P = (k == 1 || k == 2) ? s1 : s0, Q = k < 3 ? s2 : s3;
+      const float o = fmaf(cf.x, P, fmaf(cf.y, Q, fmaf(cf.z, s4, cf.w * s5)));
+      if (g >= 0 && row >= 10) unsafeAtomicAdd(dgrad + direct_slot(g, k), o);
+    }
+    if (chunk_general) {
+      // indefinite forms of the chunk (q' = z^2 - a^2; rare), one at a time: lanes 0..15 (slot 0)
+      // hold rows 0..15 of the tile in their own registers (x, gv, acc)
+      uint64_t gm = __builtin_amdgcn_ballot_w64(lane < nj && my.gen != 0.0f);
+      while (gm) {
+        const int j = __builtin_ctzll(gm);
+        gm &= gm - 1;
+        const GaussEval u = readlane_eval(my, j);
+        const int32_t gj = __builtin_amdgcn_readlane(myg, j);
+        float mm[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (lane < 16) {
+          const float dx2 = x - u.mu0;
+          const float a2 = u.wa * dx2;
+          const float nA2 = -(a2 * a2);
+          const float b2 = u.wb * dx2;
+#pragma unroll
+          for (int c = 0; c < 16; ++c) {
+            const float dy = yv[c] - u.mu1;
+            const float z = fmaf(u.wc, dy, b2);
+            const float q = fmaf(z, z, nA2);
+            const float qc = __builtin_amdgcn_fmed3f(q, p.q_lo, p.q_hi);
+            const float e = __builtin_amdgcn_exp2f(qc);
+            acc[c] = fmaf(u.w, e, acc[c]);
+            const float ge = gv[c] * e;
+            mm[0] += ge;
+            if (qc == q) {
+              mm[1] += ge * dx2;
+              mm[2] += ge * dy;
+              mm[3] += ge * dx2 * dx2;
+              mm[4] += ge * dx2 * dy;
+              mm[5] += ge * dy * dy;
+            }
+          }
+        }
+#pragma unroll
+        for (int kk = 0; kk < 6; ++kk) mm[kk] = dpp_row_sum_f32(mm[kk]);  // row 0: lanes 0..15
+        if (lane == 15 && gj >= 0) {
+#pragma unroll
+          for (int kk = 0; kk < 6; ++kk) {
+            const float4 c = dcoef[6 * (uint32_t)gj + (uint32_t)kk];
+            const float P = (kk == 1 || kk == 2) ? mm[1] : mm[0], Q = kk < 3 ? mm[2] : mm[3];
+            unsafeAtomicAdd(dgrad + direct_slot(gj, kk), fmaf(c.x, P, fmaf(c.y, Q, fmaf(c.z, mm[4], c.w * mm[5]))));
+          }
+        }
+      }
+    }
+  };
+
+  const uint32_t* rm = rowmask + (int64_t)tr * p.W;
+  const uint32_t* cm = colmask + (int64_t)tc * p.W;
+  int32_t* keys = r16_wkeys[wid];
+  int64_t done = 0;
+  for (int32_t w0 = 0; w0 < p.W; w0 += 64) {
+    const int32_t w = w0 + lane;
+    const uint32_t m = w < p.W ? (rm[w] & cm[w]) : 0u;
+    const int32_t cnt = __popc(m);
+    const int32_t inc = dpp_scan_i32(cnt);
+    const int32_t tot = __builtin_amdgcn_readlane(inc, 63);
+    // Expand the set bits in order, kWaveSortKeys positions at a time.
+    for (int32_t base = 0; base < tot; base += kWaveSortKeys) {
+      uint32_t mm = m;
+      int32_t pos = inc - cnt;
+      while (mm != 0u && pos < base + kWaveSortKeys) {
+        const int32_t bit = __builtin_ctz(mm);
+        mm &= mm - 1u;
+        if (pos >= base) keys[pos - base] = (w << 5) + bit;
+        ++pos;
+      }
+      wave_sync();
+      const int32_t nwin = min(kWaveSortKeys, tot - base);
+      for (int32_t j = lane; j < nwin; j += 64) {
+        const int64_t sl = done + j;
+        if (sl < room) ids[s + sl] = keys[j];
+      }
+      for (int32_t j0 = 0; j0 < nwin; j0 += 64) {
+        const int nj = min(64, nwin - j0);
+        GaussEval my = zero_eval();
+        int32_t myg = -1;
+        if (lane < nj) {
+          myg = keys[j0 + lane];
+          my = load_eval(ev, myg);
+        }
+        run_chunk(my, myg, nj);
+      }
+      done += nwin;
+      wave_sync();  // the keys are read before the next window rewrites them
+    }
+  }
+  if (lane == 0) {
+    if (done != count) set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);
+    if (room < count) set_status(&hdr->status, GF_STATUS_CAPACITY);
+  }
+  // The slots' partial rows through LDS, summed in slot order; lane l stores row l/4,
+  // columns 4 (l % 4) .. + 3.
+  float4* dt = dtile[wid];
+#pragma unroll
+  for (int c = 0; c < 16; c += 4) dt[slot * 64 + row * 4 + (c >> 2)] = make_float4(acc[c], acc[c + 1], acc[c + 2], acc[c + 3]);
+  wave_sync();
+  float4 v = dt[lane];
+#pragma unroll
+  for (int sl = 1; sl < 4; ++sl) {
+    const float4 u = dt[sl * 64 + lane];
+    v.x += u.x;
+    v.y += u.y;
+    v.z += u.z;
+    v.w += u.w;
+  }
+  const int32_t opr = r0 + (lane >> 2), opc = c0 + ((lane & 3) << 2);
+  const float out[4] = {v.x, v.y, v.z, v.w};
+  if (opr < p.M) store_row4(p, delta, MergedOut{nullptr, nullptr, 1.0f}, opr, opc, out);
+}
+
 __device__ inline float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -3398,10 +3662,25 @@ size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, in
   return bwd_layout(p).total;
 }
 
+static int forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                       const float* mu, const float* chol_raw, const float* amp, int64_t* tile_ptr,
+                       int64_t* num_pairs_dev, int64_t* num_pairs_host, void* workspace, size_t workspace_bytes,
+                       void* stream, bool force_tiles);
+
 int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                    const float* mu, const float* chol_raw, const float* amp, int64_t* tile_ptr,
                    int64_t* num_pairs_dev, int64_t* num_pairs_host, void* workspace,
                    size_t workspace_bytes, void* stream) {
+  return forward_bin(cfg, out_features, in_features, k, mu, chol_raw, amp, tile_ptr, num_pairs_dev, num_pairs_host,
+                     workspace, workspace_bytes, stream, false);
+}
+
+// force_tiles: bin the tiles with k_bin_tiles (tile_ptr and the chain-rule maps stored here) also
+// where the render would bin them itself (tiles_in_render).
+static int forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                       const float* mu, const float* chol_raw, const float* amp, int64_t* tile_ptr,
+                       int64_t* num_pairs_dev, int64_t* num_pairs_host, void* workspace, size_t workspace_bytes,
+                       void* stream, bool force_tiles) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
@@ -3415,7 +3694,7 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
     if (!amp) return set_err(GF_E_INVALID_ARGUMENT, "amp must not be NULL");
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
     const unsigned lines = (unsigned)(p.R + p.C);
-    const bool in_render = tiles_in_render(p);
+    const bool in_render = !force_tiles && tiles_in_render(p);
     const unsigned nb = (unsigned)((k + kTilesThreads - 1) / kTilesThreads);
     hipLaunchKernelGGL(in_render ? k_prep<true> : k_prep<false>, dim3(in_render ? 2 * nb : nb), dim3(kTilesThreads), 0,
                        st, p, mu, chol_raw, amp, ws, L, num_pairs_dev);
@@ -3690,6 +3969,58 @@ int gf_backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t
                                &reinterpret_cast<const WsHeader*>(fws)->heavy,
                                reinterpret_cast<const float4*>(fws + FL.dcoef), dg);
   GF_LAUNCH_CHECK("k_bwd");
+  return GF_OK;
+}
+
+// The one-pass kernel takes the fields gf_backward_direct runs in one launch, with 16x16 tiles and
+// at least one Gaussian.
+bool fused_one_pass(const Problem& p, int64_t pair_bound) {
+  return p.K > 0 && p.tile_out == 16 && p.tile_in == 16 && direct_one_launch(p, pair_bound);
+}
+
+int gf_fwd_bwd_fused_supported(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                               int64_t ids_capacity) {
+  Problem p;
+  if (make_problem(cfg, out_features, in_features, k, &p)) return 0;
+  return fused_one_pass(p, ids_capacity) ? 1 : 0;
+}
+
+int gf_fwd_bwd_fused(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                     const float* row_coords, const float* col_coords, const float* mu, const float* chol_raw,
+                     const float* amp, const float* grad_delta, int64_t* tile_ptr, int64_t* num_pairs_dev,
+                     int64_t* gaussian_ids_sorted, int64_t ids_capacity, float* delta, void* forward_workspace,
+                     size_t forward_workspace_bytes, void* stream) {
+  Problem p;
+  int rc = make_problem(cfg, out_features, in_features, k, &p);
+  if (rc) return rc;
+  if (!fused_one_pass(p, ids_capacity))
+    return set_err(GF_E_INVALID_ARGUMENT,
+                   "gf_fwd_bwd_fused takes 16x16 tiles on the mask path (1 <= k <= %lld) with fewer than 8192 "
+                   "tiles, sparse and without heavy tiles (gf_fwd_bwd_fused_supported); run gf_forward + "
+                   "gf_backward_direct for this field", (long long)kMaskMaxK);
+  const FwdLayout FL = fwd_layout(p);
+  if (!forward_workspace || forward_workspace_bytes < FL.total)
+    return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", FL.total, forward_workspace_bytes);
+  if (!row_coords || !col_coords || !grad_delta || !delta || !amp)
+    return set_err(GF_E_INVALID_ARGUMENT, "coords / grad_delta / delta / amp must not be NULL");
+  if (ids_capacity < 0 || (ids_capacity > 0 && !gaussian_ids_sorted))
+    return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / ids_capacity invalid");
+  if ((uint64_t)k * 8 >= (uint64_t)UINT32_MAX)
+    return set_err(GF_E_INVALID_ARGUMENT, "k = %lld is too large for the direct gradients", (long long)k);
+  rc = forward_bin(cfg, out_features, in_features, k, mu, chol_raw, amp, tile_ptr, num_pairs_dev, nullptr,
+                   forward_workspace, forward_workspace_bytes, stream, true);
+  if (rc) return rc;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  uint8_t* fws = reinterpret_cast<uint8_t*>(forward_workspace);
+  p.heavy = 0;
+  const dim3 grid((unsigned)quad_grid(p));
+  auto kern = p.mask_clamp ? k_fused16<true> : k_fused16<false>;
+  hipLaunchKernelGGL(kern, grid, dim3(kTileThreads), 0, st, p, grad_delta, row_coords, col_coords,
+                     reinterpret_cast<const GaussEval*>(fws + FL.eval), tile_ptr, gaussian_ids_sorted, ids_capacity,
+                     delta, fws, reinterpret_cast<const uint32_t*>(fws + FL.rowmask),
+                     reinterpret_cast<const uint32_t*>(fws + FL.colmask), reinterpret_cast<const float4*>(fws + FL.dcoef),
+                     reinterpret_cast<float*>(fws + FL.dgrad));
+  GF_LAUNCH_CHECK("k_fused16");
   return GF_OK;
 }
 

@@ -185,6 +185,33 @@ class FieldPlan:
         slots = self.fwd_ws[off:off + 32 * self.K].view(torch.float32).view(self.K, 8)
         return slots[:, 1:3], slots[:, 3:6], slots[:, 0:1]
 
+    def fused_supported(self) -> bool:
+        """Whether :meth:`fwd_bwd_fused` runs the one-pass kernel for this field at the plan's id
+        capacity (16x16 tiles on the mask path, fewer than 8192 tiles, sparse, no heavy tiles)."""
+        return bool(N.lib().gf_fwd_bwd_fused_supported(ctypes.byref(self.cfg), self.M, self.N, self.K,
+                                                       self.capacity))
+
+    def fwd_bwd_fused(self, row_coords, col_coords, mu, chol_raw, amp, grad, num_pairs: int | None = None):
+        """Forward and backward with dL/d(delta) given up front (gf_fwd_bwd_fused): the binning,
+        then one kernel that renders delta-W and reduces ``grad`` with the same exponentials.
+        Returns (delta, (d_mu, d_chol_raw, d_amp)), the gradients as :meth:`backward_direct`
+        returns them (views of the forward workspace, added into slots the binning cleared).
+        Fields the one-pass kernel does not take run :meth:`forward` + :meth:`backward_direct`
+        (``num_pairs`` as there)."""
+        if not self.fused_supported():
+            self.forward(row_coords, col_coords, mu, chol_raw, amp)
+            grads = self.backward_direct(grad, row_coords, col_coords, mu, chol_raw, amp, num_pairs)
+            return self.delta, grads
+        L = N.lib()
+        N.check(L.gf_fwd_bwd_fused(ctypes.byref(self.cfg), self.M, self.N, self.K, row_coords.data_ptr(),
+                                   col_coords.data_ptr(), N.ptr(mu), N.ptr(chol_raw), N.ptr(amp), grad.data_ptr(),
+                                   self.tile_ptr.data_ptr(), self.num_pairs.data_ptr(), self.ids.data_ptr(),
+                                   self.capacity, self.delta.data_ptr(), self.fwd_ws.data_ptr(), self.fwd_ws_bytes,
+                                   self._stream()), "gf_fwd_bwd_fused")
+        off = int(L.gf_forward_grads_offset(self.M, self.N, self.K, ctypes.byref(self.cfg)))
+        slots = self.fwd_ws[off:off + 32 * self.K].view(torch.float32).view(self.K, 8)
+        return self.delta, (slots[:, 1:3], slots[:, 3:6], slots[:, 0:1])
+
     def direct_launches(self, num_pairs: int | None = None) -> int:
         """Launches :meth:`backward_direct` makes for ``num_pairs`` (default: the id capacity):
         1, or 2 where it runs the reduction and the finish."""

@@ -203,6 +203,30 @@ int gf_backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t
                        const int64_t* gaussian_ids, int64_t num_pairs, void* forward_workspace,
                        size_t forward_workspace_bytes, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Forward and backward in one pass, for callers that hold dL/d(delta) before the forward (fits to
+ * a fixed target, benchmarks of the path): gf_forward's outputs (tile_ptr, P into num_pairs_dev,
+ * the ids, delta) and gf_backward_direct's gradients (added into the forward workspace's slots at
+ * gf_forward_grads_offset, which this call's binning clears first) from the binning (two launches)
+ * and one tile kernel that renders delta-W and reduces grad_delta with the same exponentials.
+ * Replaces reference forward.cu:372-511 (binning), then forward.cu:254-368 (tile_accumulate_kernel)
+ * and backward.cu:234-388 (backward_pair_partial_kernel) run back to back on the same tiles.
+ * delta agrees with gf_forward's within fp32 rounding (each pixel's Gaussians are summed as four
+ * interleaved partial sums), the gradients with gf_backward_direct's; binning is identical.
+ * Takes the fields gf_fwd_bwd_fused_supported accepts: 16x16 tiles on the mask path
+ * (1 <= k <= 8192), fewer than 8192 tiles, sparse (ids_capacity < 16 T) and no heavy tiles; others
+ * return GF_E_INVALID_ARGUMENT before any device work.  No host synchronisation.
+ */
+int gf_fwd_bwd_fused(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                     const float* row_coords, const float* col_coords, const float* mu, const float* chol_raw,
+                     const float* amp, const float* grad_delta, int64_t* tile_ptr, int64_t* num_pairs_dev,
+                     int64_t* gaussian_ids_sorted, int64_t ids_capacity, float* delta, void* forward_workspace,
+                     size_t forward_workspace_bytes, void* stream);
+
+/* 1 if gf_fwd_bwd_fused takes this field and id capacity, else 0 (also on an invalid configuration). */
+int gf_fwd_bwd_fused_supported(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                               int64_t ids_capacity);
+
 /* Kernel launches gf_backward_direct makes for this field and pair count: 1 (the direct
  * kernel) or 2 (reduction + finish); the negated error code on an invalid configuration. */
 int gf_backward_direct_launches(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,

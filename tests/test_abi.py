@@ -321,3 +321,25 @@ def test_batch_plan_reserves_emission_blocks_for_capacity():
     info = N.GfBatchInfo()
     rc = lib.gf_batch_plan(ctypes.byref(cfg), table, 1, None, 0, ctypes.byref(info), None)
     assert rc == GF_E_INVALID_ARGUMENT and "k_capacity" in lib.gf_last_error().decode()
+
+
+def test_fused_entry_refuses_other_fields_before_device_work():
+    """gf_fwd_bwd_fused takes 16x16 tiles on the mask path, fewer than 8192 tiles, sparse fields
+    without heavy tiles (gf_fwd_bwd_fused_supported); other fields are refused with
+    GF_E_INVALID_ARGUMENT before any device work (safe without a GPU)."""
+    L = N.lib()
+    c16, c32 = N.make_config(16, 16, 3.0, False, 80.0), N.make_config(32, 32, 3.0, False, 80.0)
+    ok = lambda cfg, m, n, k, cap: L.gf_fwd_bwd_fused_supported(ctypes.byref(cfg), m, n, k, cap)  # noqa: E731
+    assert ok(c16, 1280, 1280, 1024, 24000) == 1
+    assert ok(c16, 320, 320, 64, 500) == 1
+    assert ok(c32, 1280, 1280, 1024, 24000) == 0          # 32x32 tiles
+    assert ok(c16, 320, 320, 9000, 9000) == 0             # past the masks: emission path
+    assert ok(c16, 1280, 1792, 512, 4000) == 0            # 8960 tiles
+    assert ok(c16, 320, 320, 600, 16 * 400) == 0          # dense (>= 16 pairs a tile)
+    assert ok(c16, 640, 640, 2048, 20000) == 0            # heavy-tile workgroups
+    assert ok(c16, 320, 320, 0, 1) == 0                   # no Gaussian
+    d = ctypes.c_void_p(16)  # never dereferenced: the field is refused first
+    rc = L.gf_fwd_bwd_fused(ctypes.byref(c32), 1280, 1280, 1024, d, d, d, d, d, d, d, d, d, 24000, d, d, 1 << 30,
+                            None)
+    assert rc == GF_E_INVALID_ARGUMENT
+    assert "gf_fwd_bwd_fused_supported" in L.gf_last_error().decode()

@@ -2200,3 +2200,139 @@ def test_gaussian_field_batch_merged_layers(device):
         for name, got, want in zip(("d_mu_raw", "d_chol_raw", "d_amp"), (a.mu_raw.grad, a.chol_raw.grad, a.amp.grad),
                                    r[3:]):
             grad_close(got, want, f"{name} vs oracle")
+
+
+def _fused_vs_plan(p, device, cfg_kw, cap, P, label):
+    """FieldPlan.fwd_bwd_fused against FieldPlan.forward + backward_direct on the same inputs:
+    binning identical, delta-W within 1e-5 of the render's maximum (another summation order and
+    the backward's form of the exponent), gradients within 1e-5."""
+    q = p.to(device)
+    fused = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=cap, **cfg_kw)
+    ref = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=cap, **cfg_kw)
+    fused.delta.fill_(float("nan"))
+    d, grads = fused.fwd_bwd_fused(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, q.grad, num_pairs=P)
+    grads = [t.clone() for t in grads]
+    ref.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+    want = [t.clone() for t in ref.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
+                                                   num_pairs=P)]
+    torch.cuda.synchronize()
+    assert fused.status() == 0, f"{label}: forward status {fused.status():#x}"
+    assert torch.equal(fused.tile_ptr, ref.tile_ptr) and fused.pairs() == P
+    assert torch.equal(fused.ids[:P], ref.ids[:P]), f"{label}: ids"
+    fin = torch.isfinite(ref.delta)
+    assert torch.equal(torch.isfinite(d), fin), f"{label}: non-finite pattern"
+    if bool(fin.any()):
+        scale = max(float(ref.delta[fin].abs().max()), 1e-30)
+        err = float((d[fin] - ref.delta[fin]).abs().max()) / scale
+        assert err <= 1e-5, f"{label}: delta-W {err:.2e} from the render"
+    for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), grads, want):
+        if bool(torch.isfinite(b).all()):
+            grad_close(a, b, f"{label} {name} vs forward + backward_direct", rtol=1e-5)
+    return fused, d, grads
+
+
+@pytest.mark.parametrize("case", ["cfg1", "cfg2", "cfg3", "cfg3_clamp24", "cfg2_normalize", "cfg2_noclamp"])
+def test_fused_matches_oracle(device, case):
+    """gf_fwd_bwd_fused (binning, then one kernel rendering delta-W and reducing dL/d(delta) with the
+    same exponentials) against the CPU oracle: binning bit-exact, delta-W within 1e-5, gradients
+    within 1e-4; against forward + backward_direct; then a second call with other parameters on
+    the same plan (the binning clears the gradient slots the kernel adds into)."""
+    base, _, opt = case.partition("_")
+    kw = {"clamp24": dict(clamp_quad=24.0), "normalize": dict(normalize=True), "noclamp": dict(clamp_quad=None),
+          "": {}}[opt]
+    okw = dict(normalize=kw.get("normalize", False), clamp=kw.get("clamp_quad", 80.0))
+    plan = None
+    for seed in (21, 22):
+        p = getattr(wl, base)(seed)
+        r = oracle(p, **okw)
+        P = int(r[1][-1])
+        say(f"fused {case} seed {seed}: M={p.out_features} N={p.in_features} K={p.k} P={P}")
+        q = p.to(device)
+        if plan is None:
+            plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=P + 4096, **kw)
+            assert plan.fused_supported()
+            _fused_vs_plan(p, device, kw, P + 4096, P, case)
+        plan.delta.fill_(float("nan"))
+        d, grads = plan.fwd_bwd_fused(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, q.grad)
+        torch.cuda.synchronize()
+        assert plan.status() == 0
+        binning_equal(plan.tile_ptr, plan.ids[:P], r[1], r[2])
+        field_close(d, r[0])
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), grads, r[3:]):
+            grad_close(a, b, f"fused {name}")
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_fused_random_fields(device, i):
+    """gf_fwd_bwd_fused on the seeded random fields of test_gf_forward_random_fields (ragged
+    sizes, indefinite covariances, normalisation, clamps 24 / 80 / 200 / none, sigma 1.5..3.5):
+    against forward + backward_direct, and delta-W at least as close to the float64 evaluation as
+    the fp32 oracle.  Fields the one-pass kernel does not take (dense tiles) run the fallback."""
+    p, cfg = _random_forward_problem(i)
+    r = fo.gaussian_field_fwd_bwd_batched(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad, 16, 16,
+                                          cfg["sigma"], cfg["normalize"], cfg["clamp"])
+    P = int(r[1][-1])
+    kw = dict(sigma_multiplier=cfg["sigma"], normalize=cfg["normalize"], clamp_quad=cfg["clamp"])
+    cap = max(P, 1)
+    say(f"fused {p.name} P={P} {cfg}")
+    fused, d, grads = _fused_vs_plan(p, device, kw, cap, P, p.name)
+    say(f"  one pass: {fused.fused_supported()}")
+    binning_equal(fused.tile_ptr, fused.ids[:P], r[1], r[2])
+    r64 = fo.gaussian_field_fwd_bwd_fp64(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, p.grad, 16, 16,
+                                         cfg["sigma"], cfg["normalize"], cfg["clamp"])
+    finite = torch.isfinite(r64[0])
+    assert torch.equal(torch.isfinite(d.cpu()), finite)
+    if bool(finite.any()):
+        scale = max(float(r64[0][finite].abs().max()), 1e-30)
+        err_g = float((d.cpu().double() - r64[0])[finite].abs().max()) / scale
+        err_o = float((r[0].double() - r64[0])[finite].abs().max()) / scale
+        assert err_g <= err_o + 1e-5, (err_g, err_o)
+    for k, (name, a) in enumerate(zip(("d_mu", "d_chol_raw", "d_amp"), grads)):
+        c = r64[3 + k]
+        if not bool(torch.isfinite(c).all()):
+            continue
+        cn = float(c.norm())
+        if cn > 0.0:
+            ed = float((a.cpu().double() - c).norm()) / cn
+            eo = float((r[3 + k].double() - c).norm()) / cn
+            assert ed <= eo + 1e-4, (name, ed, eo)
+
+
+def test_fused_graph_replay(device):
+    """The fused step (binning + one-pass kernel) captured in a HIP graph and replayed three times
+    with eager work and poisoned outputs between the replays: every replay's delta-W, ids and
+    gradients equal the eager call's (the binning's clearing of the gradient slots is a kernel)."""
+    p = wl.cfg3(8)
+    q = p.to(device)
+    r = oracle(p)
+    P = int(r[1][-1])
+    plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=P)
+    assert plan.fused_supported()
+    s = torch.cuda.Stream(device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(s):
+        d, grads = plan.fwd_bwd_fused(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, q.grad)
+        eager = [t.clone() for t in grads]
+        delta0 = d.clone()
+    torch.cuda.current_stream(device).wait_stream(s)
+    torch.cuda.synchronize()
+    ids0 = plan.ids[:P].clone()
+    field_close(delta0, r[0])
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        d, views = plan.fwd_bwd_fused(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, q.grad)
+    for rep in range(3):
+        say(f"  fused replay {rep}")
+        plan.delta.fill_(float("nan"))
+        plan.ids.fill_(-1)
+        for v in views:
+            v.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert plan.status() == 0
+        assert torch.equal(plan.delta, delta0), f"replay {rep}: delta"
+        assert torch.equal(plan.ids[:P], ids0), f"replay {rep}: ids"
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), views, eager):
+            grad_close(a, b, f"replay {rep} {name}", rtol=1e-5)
+        _ = (plan.delta * 2.0).sum().item()  # eager work between replays
