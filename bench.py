@@ -28,6 +28,9 @@ Prints one JSON line (metric contract of the driver) with two extra objects:
                 launches of that kernel (replay time / launch count);
   cpu_baseline  the CPU oracle (a from-scratch port of the reference's torch CPU path) timed on
                 this host on the same inputs (for cfg4, on a stated subset of the layers);
+  fused         (single fields the one-pass kernel takes) the same field through gf_fwd_bwd_fused,
+                dL/d(delta) given before the forward: step time, and the one-pass kernel's
+                roofline (56 flops per evaluation: the forward's 15 and the backward's 41);
   dropin        (single fields) wall time per call of the path the reference layer calls: the
                 drop-in extension's forward + backward and gaussian_field_train + autograd
                 backward, each with its host synchronisations, beside torch's own autograd cost
@@ -186,6 +189,51 @@ def cpu_baseline(problems, reps: int, note: str, tile: int = 16) -> dict:
             "affinity_cores": affinity, "cgroup_cpu_quota": quota, "kind": "port",
             "sample": f"{note}: fwd+bwd (per-tile loop + autograd), 1 warmup + median of {reps}, "
                       f"{med:.2f} s each"}
+
+
+def fused_times(plan, q, total, per_run, args, graph_time_us, t_bin_ms) -> dict:
+    """The same field through gf_fwd_bwd_fused (dL/d(delta) given up front: the binning, then one
+    kernel that renders delta-W and reduces dL/d(delta) with the same exponentials), timed as the
+    main step (graph replay of --steps steps); the one-pass kernel's duration is the fused call's
+    minus the binning's, both from graphs of repeated launches timed with HIP events on their
+    stream."""
+    import torch
+
+    dev = plan.device
+
+    def fused():
+        plan.fwd_bwd_fused(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, q.grad)
+
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fused()
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(per_run):
+            fused()
+    for _ in range(max(1, args.warmup // per_run)):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps // per_run):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = 1e3 * (time.perf_counter() - t0) / args.steps
+    if plan.status():
+        raise RuntimeError(f"fused: device status {plan.status():#x}")
+    t_call_us = graph_time_us([fused])
+    t_kernel_s = (t_call_us - t_bin_ms * 1e3) / 1e6
+    flops = total["flops_fwd"] + total["flops_bwd"]
+    return {"ms_per_step": ms, "value": total["elements"] / (ms / 1e3), "unit": "ΔW elements/s",
+            "kernels_us": {"k_bin": t_bin_ms * 1e3, "k_fused16": t_kernel_s * 1e6},
+            "roofline": dict(roofline(total["bytes_step"], flops, t_kernel_s), kernel="k_fused16",
+                             duration_us=t_kernel_s * 1e6),
+            "step_roofline": roofline(total["bytes_step"], flops, ms / 1e3),
+            "launch": f"hip graph replay, {per_run} steps per graph; binning (2 launches) + k_fused16"}
 
 
 def dropin_times(q, args, dev) -> dict:
@@ -658,6 +706,8 @@ def main() -> int:
         "kernel_rooflines": kernel_rooflines,
         "gpu_event_ms_per_step": gpu_ms / args.steps,
     }
+    if not batched and plan.fused_supported():
+        out["fused"] = fused_times(plan, q, total, per_run, args, graph_time_us, ph["k_bin"])
     if not batched and args.dropin_calls > 0:
         out["dropin"] = dropin_times(qs[0], args, dev)
     if not args.no_cpu_baseline:

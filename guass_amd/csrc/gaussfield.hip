@@ -2625,21 +2625,39 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
 //   * indefinite forms (GaussEval.gen) are left out of the rounds and taken one at a time by
 //     lanes 0..15 (slot 0: one row each, their own registers), with the clamped pixels' terms
 //     dropped from the quadratic-form moments;
-//   * the four slots' partial rows are added through LDS (slot order) and each lane stores four
-//     pixels of a row (coalesced float4 rows, as the render).
+//   * the four slots' partial rows are added in registers with gfx950's lane swaps (halves of
+//     the wave, then rows of 16 lanes): lane (slot, row) ends with columns 4 slot .. 4 slot + 3 of
+//     its row, summed as (slot 0 + slot 2) + (slot 1 + slot 3), and stores them (coalesced float4
+//     rows, as the render).
 // delta-W therefore sums each pixel's Gaussians in a different order than the render (four
 // interleaved partial sums): within fp32 rounding of it, not bit-equal.
+constexpr int kFusedKeys = 128;  // ids expanded per window (a tile of more takes several windows)
+
+// Lanes 0..31 of the result: a + (a of lane + 32); lanes 32..63: (b of lane - 32) + b
+// (v_permlane32_swap exchanges lanes 32..63 of its first operand with lanes 0..31 of its second).
+__device__ inline float swap32_add(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Rows of 16 lanes: row 2i + 0 of the result: a + (a of lane + 16); row 2i + 1: (b of lane - 16) + b
+// (v_permlane16_swap exchanges the odd rows of its first operand with the even rows of its second).
+__device__ inline float swap16_add(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <bool kMaskClamp>
-__global__ __launch_bounds__(kTileThreads) void k_fused16(
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_fused16(
     Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr,
     int64_t* __restrict__ ids, int64_t capacity, float* __restrict__ delta, uint8_t* fws,
     const uint32_t* __restrict__ rowmask, const uint32_t* __restrict__ colmask, const float4* __restrict__ dcoef,
     float* __restrict__ dgrad) {
-  // per wave: the four slots' partial rows (4 x 16 x 16 floats); its first 16 x 20 floats stage
-  // the dL/d(delta) tile before the rounds
-  __shared__ float4 dtile[kTileThreads / 64][4 * 64];
   constexpr int kGs = 20;  // row stride (floats) of the staged dL/d(delta) tile: conflict-free float4 reads
+  __shared__ float gstage[kTileThreads / 64][16 * kGs];
+  __shared__ int32_t fkeys[kTileThreads / 64][kFusedKeys];
+  // per wave: a chunk's constants, Gaussian j in [j] (mu0, mu1, wa, wb) and [64 + j] (wc, w, id, gen)
+  __shared__ float4 fevals[kTileThreads / 64][128];
   WsHeader* hdr = reinterpret_cast<WsHeader*>(fws);
   const int lane = threadIdx.x & 63;
   const int wid = wave_id();
@@ -2650,8 +2668,8 @@ __global__ __launch_bounds__(kTileThreads) void k_fused16(
   const int32_t r0 = st.r0, c0 = st.c0;
   const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (int64_t)tr * p.C);
   const int slot = lane >> 4, row = lane & 15;
-  float* gt = reinterpret_cast<float*>(dtile[wid]);
-  float gv[16], yv[16];
+  float* gt = gstage[wid];
+  float yv[16];
   {
     const int32_t lr = r0 + (lane >> 2), lc = c0 + ((lane & 3) << 2);
     const float* gp = grad + (int64_t)min(lr, p.M - 1) * p.N + lc;
@@ -2668,15 +2686,11 @@ __global__ __launch_bounds__(kTileThreads) void k_fused16(
     }
     *reinterpret_cast<float4*>(gt + (lane >> 2) * kGs + ((lane & 3) << 2)) = g4;
     wave_sync();
-#pragma unroll
-    for (int c = 0; c < 16; c += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(gt + row * kGs + c);
-      gv[c] = v.x;
-      gv[c + 1] = v.y;
-      gv[c + 2] = v.z;
-      gv[c + 3] = v.w;
-    }
   }
+  // The lane's row of dL/d(delta), four columns at a time from the stage (held in LDS for the
+  // whole tile rather than in 16 registers: the kernel then fits seven waves per SIMD).
+  const float* grow = gt + row * kGs;
+  auto g4_at = [&](int c4) { return *reinterpret_cast<const float4*>(grow + 4 * c4); };
   if (c0 + 15 < p.N && ((reinterpret_cast<uintptr_t>(col_coords + c0) & 15) == 0)) {
     const float4* yq = reinterpret_cast<const float4*>(col_coords + c0);
 #pragma unroll
@@ -2691,6 +2705,9 @@ __global__ __launch_bounds__(kTileThreads) void k_fused16(
 #pragma unroll
     for (int c = 0; c < 16; ++c) yv[c] = col_coords[min(c0 + c, p.N - 1)];
   }
+  // the tile's column coordinates are the same in every lane: scalar registers
+#pragma unroll
+  for (int c = 0; c < 16; ++c) yv[c] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(yv[c])));
   const float x = row_coords[min(r0 + row, p.M - 1)];
   const int64_t s = tile_ptr[t], count = tile_ptr[t + 1] - s;
   // ids are written to [s, s + room): none for a segment below the id buffer or reversed
@@ -2699,21 +2716,18 @@ __global__ __launch_bounds__(kTileThreads) void k_fused16(
   float acc[16];
 #pragma unroll
   for (int c = 0; c < 16; ++c) acc[c] = 0.f;
-  wave_sync();  // the staged dL/d(delta) is read before dtile takes the partial rows
 
-  // The rounds over a chunk of nj <= 64 Gaussians (lane j holds Gaussian j: constants my, id myg).
-  auto run_chunk = [&](const GaussEval& my, int32_t myg, int nj) {
-    const bool chunk_general = __builtin_amdgcn_ballot_w64(lane < nj && my.gen != 0.0f) != 0;
+  // The rounds over a chunk of nj <= 64 Gaussians, staged in the wave's fevals (Gaussian j at
+  // [j], [64 + j]); chunk_general: some of them have the indefinite form.
+  float4* ew = fevals[wid];
+  auto run_chunk = [&](int nj, bool chunk_general) {
     for (int jb = 0; jb < nj; jb += 4) {
-      const int j = jb + slot;
-      const int addr = j < nj ? j << 2 : 0;  // ds_bpermute byte address of the slot's lane
-      auto from = [&](float v) { return __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(v))); };
-      const float mu0 = from(my.mu0), mu1 = from(my.mu1);
-      const float wa = from(my.wa), wb = from(my.wb);
-      const float wc = from(my.wc), w = from(my.w);
-      const float gen = chunk_general ? from(my.gen) : 0.0f;
-      int32_t g = __builtin_amdgcn_ds_bpermute(addr, myg);
-      const bool live = j < nj && !(chunk_general && gen != 0.0f);  // indefinite forms: below
+      const int j = min(jb + slot, nj - 1);  // a slot past the chunk reads a real Gaussian, unused
+      const float4 ea = ew[j], eb = ew[64 + j];
+      const float mu0 = ea.x, mu1 = ea.y, wa = ea.z, wb = ea.w;
+      const float wc = eb.x, w = eb.y, gen = eb.w;
+      int32_t g = __float_as_int(eb.z);
+      const bool live = jb + slot < nj && !(chunk_general && gen != 0.0f);  // indefinite forms: below
       if (!live) g = -1;
       const float wr = live ? w : 0.0f;
       const float dx = x - mu0;
@@ -2724,8 +2738,11 @@ __global__ __launch_bounds__(kTileThreads) void k_fused16(
       float4 cf = make_float4(0.f, 0.f, 0.f, 0.f);
       if (row >= 10 && g >= 0) cf = dcoef[6 * (uint32_t)g + (uint32_t)(row - 10)];
       float t0 = 0.f, t2 = 0.f, t3 = 0.f, tq = 0.f;
+      float4 g4 = g4_at(0);
 #pragma unroll
       for (int c = 0; c < 16; ++c) {
+        if ((c & 3) == 0 && c > 0) g4 = g4_at(c >> 2);
+        const float gc = (c & 3) == 0 ? g4.x : (c & 3) == 1 ? g4.y : (c & 3) == 2 ? g4.z : g4.w;
         const float dy = yv[c] - mu1;
         const float z = fmaf(wc, dy, b);
         if (kMaskClamp) {
@@ -2734,7 +2751,7 @@ __global__ __launch_bounds__(kTileThreads) void k_fused16(
           const float qv = -fmaf(z, z, A);
           const float e = __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(qv, p.q_lo, 0.0f));
           acc[c] = fmaf(wr, e, acc[c]);
-          const float ge = gv[c] * e;
+          const float ge = gc * e;
           t0 += ge;
           const float gq = qv < p.q_lo ? 0.0f : ge;
           tq += gq;
@@ -2746,12 +2763,15 @@ __global__ __launch_bounds__(kTileThreads) void k_fused16(
           // render and the backward
           const float e = __builtin_amdgcn_exp2f(-fmaf(z, z, A));
           acc[c] = fmaf(wr, e, acc[c]);
-          const float ge = gv[c] * e;
+          const float ge = gc * e;
           t0 += ge;
           const float tt = ge * dy;
           t2 += tt;
           t3 = fmaf(tt, dy, t3);
         }
+        // keep each group of four columns' work beside its LDS read (interleaved across groups,
+        // the round would hold more registers than seven waves a SIMD leave)
+        if ((c & 3) == 3) __builtin_amdgcn_sched_barrier(0);
       }
       const float t0q = kMaskClamp ? tq : t0;
       const float m0 = t0, m1 = dx * t0q, m2 = t2, m3 = dx * dx * t0q, m4 = dx * t2, m5 = t3;
@@ -2765,12 +2785,19 @@ __global__ __launch_bounds__(kTileThreads) void k_fused16(
     if (chunk_general) {
       // indefinite forms of the chunk (q' = z^2 - a^2; rare), one at a time: lanes 0..15 (slot 0)
       // hold rows 0..15 of the tile in their own registers (x, gv, acc)
-      uint64_t gm = __builtin_amdgcn_ballot_w64(lane < nj && my.gen != 0.0f);
+      uint64_t gm = __builtin_amdgcn_ballot_w64(lane < nj && ew[64 + min(lane, nj - 1)].w != 0.0f);
       while (gm) {
         const int j = __builtin_ctzll(gm);
         gm &= gm - 1;
-        const GaussEval u = readlane_eval(my, j);
-        const int32_t gj = __builtin_amdgcn_readlane(myg, j);
+        const float4 ea = ew[j], eb = ew[64 + j];
+        GaussEval u;
+        u.mu0 = ea.x;
+        u.mu1 = ea.y;
+        u.wa = ea.z;
+        u.wb = ea.w;
+        u.wc = eb.x;
+        u.w = eb.y;
+        const int32_t gj = __float_as_int(eb.z);
         float mm[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         if (lane < 16) {
           const float dx2 = x - u.mu0;
@@ -2779,13 +2806,15 @@ __global__ __launch_bounds__(kTileThreads) void k_fused16(
           const float b2 = u.wb * dx2;
 #pragma unroll
           for (int c = 0; c < 16; ++c) {
+            const float4 gq4 = g4_at(c >> 2);
+            const float gc = (c & 3) == 0 ? gq4.x : (c & 3) == 1 ? gq4.y : (c & 3) == 2 ? gq4.z : gq4.w;
             const float dy = yv[c] - u.mu1;
             const float z = fmaf(u.wc, dy, b2);
             const float q = fmaf(z, z, nA2);
             const float qc = __builtin_amdgcn_fmed3f(q, p.q_lo, p.q_hi);
             const float e = __builtin_amdgcn_exp2f(qc);
             acc[c] = fmaf(u.w, e, acc[c]);
-            const float ge = gv[c] * e;
+            const float ge = gc * e;
             mm[0] += ge;
             if (qc == q) {
               mm[1] += ge * dx2;
@@ -2812,7 +2841,7 @@ __global__ __launch_bounds__(kTileThreads) void k_fused16(
 
   const uint32_t* rm = rowmask + (int64_t)tr * p.W;
   const uint32_t* cm = colmask + (int64_t)tc * p.W;
-  int32_t* keys = r16_wkeys[wid];
+  int32_t* keys = fkeys[wid];
   int64_t done = 0;
   for (int32_t w0 = 0; w0 < p.W; w0 += 64) {
     const int32_t w = w0 + lane;
@@ -2820,31 +2849,36 @@ __global__ __launch_bounds__(kTileThreads) void k_fused16(
     const int32_t cnt = __popc(m);
     const int32_t inc = dpp_scan_i32(cnt);
     const int32_t tot = __builtin_amdgcn_readlane(inc, 63);
-    // Expand the set bits in order, kWaveSortKeys positions at a time.
-    for (int32_t base = 0; base < tot; base += kWaveSortKeys) {
+    // Expand the set bits in order, kFusedKeys positions at a time.
+    for (int32_t base = 0; base < tot; base += kFusedKeys) {
       uint32_t mm = m;
       int32_t pos = inc - cnt;
-      while (mm != 0u && pos < base + kWaveSortKeys) {
+      while (mm != 0u && pos < base + kFusedKeys) {
         const int32_t bit = __builtin_ctz(mm);
         mm &= mm - 1u;
         if (pos >= base) keys[pos - base] = (w << 5) + bit;
         ++pos;
       }
       wave_sync();
-      const int32_t nwin = min(kWaveSortKeys, tot - base);
+      const int32_t nwin = min(kFusedKeys, tot - base);
       for (int32_t j = lane; j < nwin; j += 64) {
         const int64_t sl = done + j;
         if (sl < room) ids[s + sl] = keys[j];
       }
       for (int32_t j0 = 0; j0 < nwin; j0 += 64) {
         const int nj = min(64, nwin - j0);
-        GaussEval my = zero_eval();
-        int32_t myg = -1;
+        bool gen_here = false;
         if (lane < nj) {
-          myg = keys[j0 + lane];
-          my = load_eval(ev, myg);
+          const int32_t g = keys[j0 + lane];
+          const GaussEval my = load_eval(ev, g);
+          ew[lane] = make_float4(my.mu0, my.mu1, my.wa, my.wb);
+          ew[64 + lane] = make_float4(my.wc, my.w, __int_as_float(g), my.gen);
+          gen_here = my.gen != 0.0f;
         }
-        run_chunk(my, myg, nj);
+        const bool chunk_general = __builtin_amdgcn_ballot_w64(gen_here) != 0;
+        wave_sync();
+        run_chunk(nj, chunk_general);
+        wave_sync();  // every lane has read the chunk before the next one is staged
       }
       done += nwin;
       wave_sync();  // the keys are read before the next window rewrites them
@@ -2854,23 +2888,17 @@ __global__ __launch_bounds__(kTileThreads) void k_fused16(
     if (done != count) set_status(&hdr->status, GF_STATUS_COUNT_MISMATCH);
     if (room < count) set_status(&hdr->status, GF_STATUS_CAPACITY);
   }
-  // The slots' partial rows through LDS, summed in slot order; lane l stores row l/4,
-  // columns 4 (l % 4) .. + 3.
-  float4* dt = dtile[wid];
+  // The slots' partial rows summed in registers.  After the 32-lane swaps, lanes of slots 0, 1
+  // hold columns 0..7 summed over slots (s, s + 2) and lanes of slots 2, 3 columns 8..15 over
+  // (s - 2, s); after the 16-lane swaps, lane (slot, row) holds columns 4 slot .. 4 slot + 3 of its
+  // row over all four slots.
+  float h8[8];
 #pragma unroll
-  for (int c = 0; c < 16; c += 4) dt[slot * 64 + row * 4 + (c >> 2)] = make_float4(acc[c], acc[c + 1], acc[c + 2], acc[c + 3]);
-  wave_sync();
-  float4 v = dt[lane];
+  for (int c = 0; c < 8; ++c) h8[c] = swap32_add(acc[c], acc[c + 8]);
+  float out[4];
 #pragma unroll
-  for (int sl = 1; sl < 4; ++sl) {
-    const float4 u = dt[sl * 64 + lane];
-    v.x += u.x;
-    v.y += u.y;
-    v.z += u.z;
-    v.w += u.w;
-  }
-  const int32_t opr = r0 + (lane >> 2), opc = c0 + ((lane & 3) << 2);
-  const float out[4] = {v.x, v.y, v.z, v.w};
+  for (int c = 0; c < 4; ++c) out[c] = swap16_add(h8[c], h8[c + 4]);
+  const int32_t opr = r0 + row, opc = c0 + (slot << 2);
   if (opr < p.M) store_row4(p, delta, MergedOut{nullptr, nullptr, 1.0f}, opr, opc, out);
 }
 
