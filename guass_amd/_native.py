@@ -9,12 +9,14 @@ missing or a call fails, a ``RuntimeError`` is raised.
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
 from pathlib import Path
 
 import torch  # noqa: F401  (must precede the dlopen below)
 
-LIB_PATH = Path(__file__).resolve().with_name("libgaussfield.so")
+# GUASS_AMD_LIB names another build of the library (e.g. the host-sanitized one the CPU tests run)
+LIB_PATH = Path(os.environ.get("GUASS_AMD_LIB") or Path(__file__).resolve().with_name("libgaussfield.so"))
 
 GF_OK = 0
 GF_STATUS_CAPACITY = 0x1

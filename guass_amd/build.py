@@ -4,6 +4,8 @@
 * ``guass_amd/libgaussfield_host.so``  host build of the per-Gaussian geometry (g++), used by
                                        CPU tests to pin the exact arithmetic the GPU runs
 * ``oracle/_build/libm_sweep``         exhaustive libm check (test infrastructure)
+* ``_build/sanitize/``                 (``build_sanitized``, for the CPU tests) both libraries with
+                                       their host code under ASan + UBSan
 
 ``python -m guass_amd.build`` builds all three; ``build_all()`` is what ``__graft_entry__.build``
 calls.  Every call compiles (no up-to-date check), so a stale library is never picked up.
@@ -75,6 +77,46 @@ def build_oracle_tools() -> Path:
     _run(["gcc", "-O2", "-fopenmp", "-ffp-contract=off", str(ROOT / "oracle" / "libm_sweep.c"),
           "-o", str(exe), "-lm"])
     return exe
+
+
+SANITIZE_DIR = ROOT / "_build" / "sanitize"
+SANITIZE_FLAGS = ["-fsanitize=address", "-fsanitize=undefined", "-fno-omit-frame-pointer"]
+
+
+def clangxx() -> str:
+    """The clang++ of the ROCm toolchain (hipcc's host compiler, whose sanitizer runtime the
+    host-sanitized builds link against)."""
+    for cand in ("/opt/rocm/llvm/bin/clang++", shutil.which("amdclang++")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("the ROCm clang++ was not found")
+
+
+def asan_runtime() -> Path:
+    """The shared AddressSanitizer runtime (with the UndefinedBehaviorSanitizer handlers) that a
+    process must preload to load the host-sanitized libraries."""
+    out = subprocess.run([clangxx(), "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True,
+                         text=True, check=True).stdout.strip()
+    path = Path(out)
+    if not path.is_file():
+        raise RuntimeError(f"no shared ASan runtime at {out}")
+    return path
+
+
+def build_sanitized(out_dir: Path = SANITIZE_DIR) -> dict[str, Path]:
+    """Both native libraries with their HOST code under AddressSanitizer and
+    UndefinedBehaviorSanitizer (-O1 -g): the C ABI's argument checks, layout and block-map
+    arithmetic (gf_batch_plan) and the host geometry build.  The gfx950 device code is compiled
+    as usual (each -fsanitize= reaches the host compilation only, through -Xarch_host).  Load them
+    with asan_runtime() preloaded and GUASS_AMD_LIB pointing at the library."""
+    out_dir.mkdir(parents=True, exist_ok=True)
+    lib, host = out_dir / "libgaussfield.so", out_dir / "libgaussfield_host.so"
+    hip = [f for f in HIP_FLAGS if f != "-O3"] + ["-O1", "-g"]
+    host_only = [a for f in SANITIZE_FLAGS for a in ("-Xarch_host", f)]
+    _run([hipcc(), *hip, *host_only, str(CSRC / "gaussfield.hip"), "-o", str(lib)])
+    _run([clangxx(), "-O1", "-g", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off", *SANITIZE_FLAGS,
+          str(CSRC / "host_geometry.cpp"), "-o", str(host)])
+    return {"lib": lib, "host_lib": host}
 
 
 def build_all(verbose: bool = True) -> None:

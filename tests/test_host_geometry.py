@@ -13,6 +13,7 @@ libm_f32.h) with g++ and no FP contraction.  These tests pin them bit for bit:
 from __future__ import annotations
 
 import ctypes
+import os
 import re
 import subprocess
 from pathlib import Path
@@ -27,7 +28,7 @@ from oracle import field_oracle as fo
 from tests.parity import SOFTPLUS_CHECKSUM
 
 ROOT = Path(__file__).resolve().parent.parent
-HOST_LIB = ROOT / "guass_amd" / "libgaussfield_host.so"
+HOST_LIB = Path(os.environ.get("GUASS_AMD_HOST_LIB") or ROOT / "guass_amd" / "libgaussfield_host.so")
 SWEEP = ROOT / "oracle" / "_build" / "libm_sweep"
 _P = ctypes.c_void_p
 _I = ctypes.c_int64
