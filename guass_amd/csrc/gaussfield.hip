@@ -1879,11 +1879,14 @@ __device__ __forceinline__ void render16x2_body(
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* __restrict__ ids,
     int64_t capacity, float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
     const uint32_t* __restrict__ colmask, int32_t tr, int32_t tc, float* __restrict__ blk_sq,
-    const MergedOut& mo = MergedOut{nullptr, nullptr, 1.0f}) {
+    const MergedOut& mo = MergedOut{nullptr, nullptr, 1.0f}, uint32_t skip = 0u) {
+  // skip: bit 0 leaves tile A, bit 1 tile B to another workgroup (a heavy tile): no Gaussians,
+  // ids, checks or stores of that tile here
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
-  const bool has_b = tc + 1 < p.C;
+  const bool has_a = (skip & 1u) == 0u;
+  const bool has_b = tc + 1 < p.C && (skip & 2u) == 0u;
   const int64_t ta = (int64_t)tr * p.C + tc;
   const int32_t pr = tr * 16 + (lane >> 2);
   const int32_t pc0 = tc * 16 + ((lane & 3) << 2);
@@ -1911,7 +1914,7 @@ __device__ __forceinline__ void render16x2_body(
   const bool floor_free = !p.mask_clamp;
   // The two segments are adjacent: [sa, sb) and [sb, se).
   const int64_t sa = tile_ptr[ta], sb = tile_ptr[ta + 1], se = has_b ? tile_ptr[ta + 2] : sb;
-  const int64_t cnt_a = sb - sa, cnt_b = se - sb;
+  const int64_t cnt_a = has_a ? sb - sa : 0, cnt_b = se - sb;
   // ids are written to [s, s + room): none for a segment below the id buffer or reversed
   auto room_of = [&](int64_t s, int64_t count) {
     return s < 0 ? 0 : capacity - s < count ? (capacity - s > 0 ? capacity - s : 0) : count;
@@ -2019,7 +2022,7 @@ __device__ __forceinline__ void render16x2_body(
     uint32_t ma = 0u, mb = 0u;
     if (w < p.W) {
       const uint32_t r = rm[w];
-      ma = r & cma[w];
+      if (has_a) ma = r & cma[w];
       if (has_b) mb = r & cmb[w];
     }
     const uint32_t u = ma | mb;
@@ -2051,6 +2054,7 @@ __device__ __forceinline__ void render16x2_body(
   }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
+    if (h == 0 && !has_a) continue;
     if (h == 1 && !has_b) break;
     const int32_t pc = pc0 + 16 * h;
     if (blk_sq) {  // as in render16_body
@@ -2080,6 +2084,42 @@ __global__ __launch_bounds__(kTileThreads) void k_render16x2(
   const int32_t tr = (int32_t)pi / cp, tc = 2 * ((int32_t)pi - tr * cp);
   render16x2_body<false>(p, row_coords, col_coords, ev, tile_ptr, ids, capacity, delta, ws, rowmask, colmask, tr,
                          tc, nullptr);
+}
+
+// Single 16x16 fields on the mask path with heavy-tile workgroups: the first workgroups take one
+// listed heavy tile each (four waves, as k_render16<true>), the rest a pair of horizontally
+// adjacent tiles a wave (R x ceil(C / 2) pairs, four a workgroup, as k_render16x2), leaving a
+// heavy member of the pair to its own workgroup.
+__global__ __launch_bounds__(kTileThreads) void k_render16x2_heavy(
+    Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
+    const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids, int64_t capacity,
+    float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
+    const uint32_t* __restrict__ colmask, const int32_t* __restrict__ heavy_list, int32_t xh) {
+  const int64_t T = (int64_t)p.R * p.C;
+  const int64_t b = blockIdx.x;
+  int64_t nh = (int64_t)reinterpret_cast<const WsHeader*>(ws)->heavy;
+  if (nh > xh) {
+    if (b == 0 && threadIdx.x == 0) atomicOr(&reinterpret_cast<WsHeader*>(ws)->status, GF_STATUS_CAPACITY);
+    nh = xh;
+  }
+  if (b < nh) {  // the workgroup's four waves share one listed tile
+    const int64_t t = heavy_list[b];
+    render16_body(p, row_coords, col_coords, ev, tile_ptr, ids, capacity, delta, ws, rowmask, colmask,
+                  tile16(p, t < 0 || t >= T ? T : t), nullptr, nullptr, wave_id(), kTileThreads / 64);
+    return;
+  }
+  const int32_t cp = (p.C + 1) / 2;
+  const int64_t pi = (b - nh) * (kTileThreads / 64) + wave_id();
+  if (pi >= (int64_t)p.R * cp) return;
+  const int32_t tr = (int32_t)pi / cp, tc = 2 * ((int32_t)pi - tr * cp);
+  const int64_t ta = (int64_t)tr * p.C + tc;
+  const bool pair = tc + 1 < p.C;
+  const int64_t s0 = tile_ptr[ta], s1 = tile_ptr[ta + 1], s2 = pair ? tile_ptr[ta + 2] : s1;
+  // the listing rule of k_bin_tiles: a tile of more than p.heavy Gaussians is heavy
+  const uint32_t skip = (s1 - s0 > p.heavy ? 1u : 0u) | (pair && s2 - s1 > p.heavy ? 2u : 0u);
+  if (skip == (pair ? 3u : 1u)) return;
+  render16x2_body<false>(p, row_coords, col_coords, ev, tile_ptr, ids, capacity, delta, ws, rowmask, colmask, tr,
+                         tc, nullptr, MergedOut{nullptr, nullptr, 1.0f}, skip);
 }
 
 template <bool kHeavy>
@@ -3800,13 +3840,23 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
     const bool binned_here = tiles_in_render(p);
     const int32_t xh = heavy_grid(p, ids_capacity);
     p.heavy = xh > 0 ? kHeavyTile : 0;
-    if (p.tile_out == 16 && p.tile_in == 16 && p.W > 0 && !binned_here && xh == 0) {
+    if (p.tile_out == 16 && p.tile_in == 16 && p.W > 0 && !binned_here) {
       const int64_t pairs = (int64_t)p.R * ((p.C + 1) / 2);
-      hipLaunchKernelGGL(k_render16x2, dim3((unsigned)((pairs + kTileThreads / 64 - 1) / (kTileThreads / 64))),
-                         dim3(kTileThreads), 0, st, p, row_coords, col_coords, ev, tile_ptr, gaussian_ids_sorted,
-                         ids_capacity, delta, ws, reinterpret_cast<const uint32_t*>(ws + L.rowmask),
-                         reinterpret_cast<const uint32_t*>(ws + L.colmask));
-      GF_LAUNCH_CHECK("k_render16x2");
+      const unsigned pair_blocks = (unsigned)((pairs + kTileThreads / 64 - 1) / (kTileThreads / 64));
+      if (xh == 0) {
+        hipLaunchKernelGGL(k_render16x2, dim3(pair_blocks), dim3(kTileThreads), 0, st, p, row_coords, col_coords, ev,
+                           tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws,
+                           reinterpret_cast<const uint32_t*>(ws + L.rowmask),
+                           reinterpret_cast<const uint32_t*>(ws + L.colmask));
+        GF_LAUNCH_CHECK("k_render16x2");
+      } else {
+        hipLaunchKernelGGL(k_render16x2_heavy, dim3((unsigned)xh + pair_blocks), dim3(kTileThreads), 0, st, p,
+                           row_coords, col_coords, ev, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws,
+                           reinterpret_cast<const uint32_t*>(ws + L.rowmask),
+                           reinterpret_cast<const uint32_t*>(ws + L.colmask),
+                           reinterpret_cast<const int32_t*>(ws + L.fill), xh);
+        GF_LAUNCH_CHECK("k_render16x2_heavy");
+      }
       return GF_OK;
     }
     hipLaunchKernelGGL(xh > 0 ? k_render16<true> : k_render16<false>, dim3((unsigned)(xh + quad_grid(p))),
