@@ -231,7 +231,8 @@ def fused_times(plan, q, total, per_run, args, graph_time_us, t_bin_ms) -> dict:
     return {"ms_per_step": ms, "value": total["elements"] / (ms / 1e3), "unit": "ΔW elements/s",
             "kernels_us": {"k_bin": t_bin_ms * 1e3, "k_fused16": t_kernel_s * 1e6},
             "roofline": dict(roofline(total["bytes_step"], flops, t_kernel_s), kernel="k_fused16",
-                             duration_us=t_kernel_s * 1e6),
+                             duration_us=t_kernel_s * 1e6,
+                             traffic=traffic_bytes(args.traffic_file, args.config, "k_fused16")),
             "step_roofline": roofline(total["bytes_step"], flops, ms / 1e3),
             "launch": f"hip graph replay, {per_run} steps per graph; binning (2 launches) + k_fused16"}
 
