@@ -34,6 +34,7 @@ EXPORTED = (
     "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward",
     "gf_batch_set_grads", "gf_batch_read", "gf_backward_noalloc", "gf_forward", "gf_backward_direct",
     "gf_forward_grads_offset", "gf_backward_direct_launches", "gf_fwd_bwd_fused", "gf_fwd_bwd_fused_supported",
+    "gf_forward_kcap", "gf_backward_direct_kcap",
 )
 
 GF_PHASE_BIN, GF_PHASE_EMIT, GF_PHASE_RENDER = 0x1, 0x2, 0x4
@@ -134,6 +135,10 @@ def lib() -> ctypes.CDLL:
     L.gf_fwd_bwd_fused.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, _P,
                                    _P, c_size_t, _P]
     L.gf_fwd_bwd_fused_supported.argtypes = [_CFG, c_int64, c_int64, c_int64, c_int64]
+    L.gf_forward_kcap.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, _P, _P,
+                                  c_size_t, _P]
+    L.gf_backward_direct_kcap.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                          c_int64, _P, c_size_t, _P, c_size_t, _P]
     L.gf_fwd_bwd_fused_supported.restype = c_int
     L.gf_read_status.argtypes = [_P, c_int32, POINTER(c_uint32), _P]
     L.gf_batch_plan.argtypes = [_CFG, POINTER(GfLayer), c_int32, _P, c_size_t, POINTER(GfBatchInfo), _P]
@@ -147,7 +152,7 @@ def lib() -> ctypes.CDLL:
                  "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
                  "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward",
                  "gf_batch_set_grads", "gf_batch_read", "gf_backward_noalloc", "gf_forward",
-                 "gf_backward_direct", "gf_fwd_bwd_fused"):
+                 "gf_backward_direct", "gf_fwd_bwd_fused", "gf_forward_kcap", "gf_backward_direct_kcap"):
         getattr(L, name).restype = c_int
     _LIB = L
     return L

@@ -120,7 +120,23 @@ struct Problem {
                        // form moments (at 80 and above their terms are below e^-40)
   int32_t heavy;  // > 0 (single fields on the k_bin_tiles path): tiles of more than `heavy`
                   // Gaussians are listed by k_bin_tiles and rendered / reduced by four waves
+  // Capacity mode (gf_forward_kcap, gf_backward_direct_kcap): K above is the capacity, which
+  // fixes the workspace layouts, mask words and launch grids; the live number of Gaussians is
+  // *kdev and the live pair count *pdev, read by the kernels.  NULL: K and the host's pair count.
+  const int64_t* kdev;
+  const int64_t* pdev;
 };
+
+// The Gaussians the kernels take: K, or in capacity mode the device value clamped to [0, K].
+__device__ inline int64_t live_k(const Problem& p) {
+  if (!p.kdev) return p.K;
+  const int64_t k = *p.kdev;
+  return k < 0 ? 0 : (k > p.K ? p.K : k);
+}
+
+// The pair count the backward's saved-state checks use: num_pairs, or in capacity mode the
+// forward's device value.
+__device__ inline int64_t live_pairs(const Problem& p, int64_t num_pairs) { return p.pdev ? *p.pdev : num_pairs; }
 
 // A Gaussian's mean coordinate i (0: row, 1: column) as the field uses it.
 __device__ inline float mu_at(const Problem& p, const float* __restrict__ mu, int64_t i) {
@@ -1017,7 +1033,7 @@ __global__ __launch_bounds__(kTilesThreads) void k_prep(Problem p, const float* 
     const int64_t nb = (p.K + kTilesThreads - 1) / kTilesThreads;
     if ((int64_t)blockIdx.x >= nb) {
       const int64_t g = ((int64_t)blockIdx.x - nb) * kTilesThreads + threadIdx.x;
-      if (g < p.K) {
+      if (g < live_k(p)) {
         const PrepLoad in = prep_load(mu, chol_raw, g);
         const GfChol Lc = gf_activate_cholesky(in.r11, in.r21, in.r22);
         store_dcoef(p, gf_cov_from_chol(Lc), Lc.l11, Lc.l22, in.r11, in.r21, in.r22, amp[g], g, ws, L);
@@ -1032,7 +1048,7 @@ __global__ __launch_bounds__(kTilesThreads) void k_prep(Problem p, const float* 
     hdr->heavy = 0u;
     hdr->num_pairs = num_pairs;
   }
-  if (g < p.K) store_prep(p, prep_rect(p, prep_load(mu, chol_raw, g)), amp[g], g, ws, L);
+  if (g < live_k(p)) store_prep(p, prep_rect(p, prep_load(mu, chol_raw, g)), amp[g], g, ws, L);
 }
 
 __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t* __restrict__ tile_ptr,
@@ -1040,8 +1056,11 @@ __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t*
                                                              FwdLayout L, const float* __restrict__ chol_raw,
                                                              const float* __restrict__ amp) {
   __shared__ int32_t diff[kLdsDiffWords];  // tile-row workgroups: the row's column differences
-  const int64_t K = p.K;
+  const int64_t K = live_k(p);
   const int32_t R = p.R, C = p.C, W = p.W;
+  // every mask word is written, those of Gaussians past K as zero (in capacity mode a workspace
+  // keeps the words of an earlier, larger K)
+  const int64_t Kw = 32 * (int64_t)W;
   const int32_t b = (int32_t)blockIdx.x;
   const bool is_row = b < R;
   const int32_t line = is_row ? b : b - R;
@@ -1055,7 +1074,7 @@ __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t*
   // The rectangles are loaded kBinPrefetch rounds at a time, so that the rounds do not each wait
   // for their own load (4 rounds at cfg3).
   constexpr int kBinPrefetch = 8;
-  for (int64_t gb = threadIdx.x & ~63; gb < K; gb += kBinPrefetch * kTilesThreads) {  // wave-uniform
+  for (int64_t gb = threadIdx.x & ~63; gb < Kw; gb += kBinPrefetch * kTilesThreads) {  // wave-uniform
     int4 rr[kBinPrefetch];
 #pragma unroll
     for (int i = 0; i < kBinPrefetch; ++i) {
@@ -1065,7 +1084,7 @@ __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t*
 #pragma unroll
     for (int i = 0; i < kBinPrefetch; ++i) {
       const int64_t g0 = gb + (int64_t)i * kTilesThreads;
-      if (g0 >= K) break;
+      if (g0 >= Kw) break;
       const int64_t g = g0 + lane;
       bool covers = false;
       if (g < K) {
@@ -1166,7 +1185,8 @@ __global__ __launch_bounds__(kTilesThreads) void k_pairs(Problem p, int64_t* __r
   __shared__ int64_t scan_lds[kTilesThreads / 64 + 1];
   const int4* __restrict__ rect = reinterpret_cast<const int4*>(ws + L.rect);
   int64_t s = 0;
-  for (int64_t g = threadIdx.x; g < p.K; g += kTilesThreads) {
+  const int64_t K = live_k(p);
+  for (int64_t g = threadIdx.x; g < K; g += kTilesThreads) {
     const int4 r = rect[g];
     s += (int64_t)(r.y - r.x + 1) * (r.w - r.z + 1);
   }
@@ -1696,20 +1716,22 @@ __device__ __forceinline__ void render16_body(
       uint32_t* mw = wmask[wid];
       int64_t before = 0, cnt = 0;
       constexpr int kPre = 4;  // rounds of rectangle loads in flight (K <= 256: all of them)
-      for (int64_t gb = 0; gb < p.K; gb += kPre * 64) {
+      // every mask word of the tile is written, those of Gaussians past the live K as zero
+      const int64_t Kl = live_k(p), Kw = 32 * (int64_t)p.W;
+      for (int64_t gb = 0; gb < Kw; gb += kPre * 64) {
         int4 rr[kPre];
 #pragma unroll
         for (int i = 0; i < kPre; ++i) {
           const int64_t g = gb + 64 * i + lane;
-          rr[i] = g < p.K ? rects[g] : make_int4(0, -1, 0, -1);
+          rr[i] = g < Kl ? rects[g] : make_int4(0, -1, 0, -1);
         }
 #pragma unroll
         for (int i = 0; i < kPre; ++i) {
           const int64_t g0 = gb + 64 * i;
-          if (g0 >= p.K) break;
+          if (g0 >= Kw) break;
           const int64_t g = g0 + lane;
           bool covers = false;
-          if (g < p.K) {
+          if (g < Kl) {
             const int4 r = rr[i];
             const int32_t h = r.y - r.x + 1, wd = r.w - r.z + 1;
             const bool in_row = r.x <= tr && tr <= r.y;
@@ -2361,6 +2383,8 @@ __device__ __forceinline__ void bwd16_body(
     yd[c] = kShifted ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ydl[c & 3]), c >> 2)) : 0.0f;
   const float x = row_coords[min(pr, p.M - 1)];
   int64_t s = (int64_t)tile_ptr[t], e = (int64_t)tile_ptr[t + 1];
+  num_pairs = live_pairs(p, num_pairs);
+  const int64_t Kl = live_k(p);
   if (lane == 0) {
     if (s < 0 || e < s || e > num_pairs) set_status(&hdr->status, GF_STATUS_TILE_PTR_ORDER);
     if (t == T - 1 && e != num_pairs) set_status(&hdr->status, GF_STATUS_TILE_PTR_LAST);
@@ -2378,7 +2402,7 @@ __device__ __forceinline__ void bwd16_body(
     int32_t myg = -1;
     if (lane < nj) {
       const int64_t g = (int64_t)gids[s + j0 + lane];
-      if (g < 0 || g >= p.K) {
+      if (g < 0 || g >= Kl) {
         set_status(&hdr->status, g < 0 ? GF_STATUS_IDS_NEGATIVE : GF_STATUS_IDS_RANGE);
       } else {
         my = (kEvalGiven || ev) ? load_eval(ev, g) : eval_geom(p, mu, chol_raw, nullptr, g);
@@ -2565,7 +2589,7 @@ __device__ __forceinline__ void bwd16_body(
       int32_t myg = -1;
       if (lane < nj) {
         const int64_t g = (int64_t)gids[s + j0 + lane];
-        if (g >= 0 && g < p.K) {
+        if (g >= 0 && g < Kl) {
           my = (kEvalGiven || ev) ? load_eval(ev, g) : eval_geom(p, mu, chol_raw, nullptr, g);
           myg = (int32_t)g;
         }
@@ -3038,7 +3062,8 @@ __device__ __forceinline__ void finish_body(
   const int64_t g = idx / p.S;
   const int32_t st = (int32_t)(idx & (p.S - 1));
   float m[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (g < p.K) {
+  const int64_t Kl = live_k(p);
+  if (g < Kl) {
     float4* ag = reinterpret_cast<float4*>(acc) + 2 * acc_slot(p, g, st);
     const float4 b0 = ag[0], b1 = ag[1];
     ag[0] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -3054,7 +3079,7 @@ __device__ __forceinline__ void finish_body(
 #pragma unroll
     for (int k = 0; k < 6; ++k) m[k] += __shfl_xor(m[k], o, 64);
   }
-  if (g >= p.K || st != 0) return;
+  if (g >= Kl || st != 0) return;
   const float raw11 = chol_raw[3 * g + 0], raw21 = chol_raw[3 * g + 1], raw22 = chol_raw[3 * g + 2];
   GfChol Lc;
   GfCov cov;
@@ -3202,6 +3227,8 @@ int make_problem(const gf_field_config* cfg, int64_t M, int64_t N, int64_t K, Pr
   p->mu_tanh = 0;
   p->mask_clamp = (cfg->has_clamp_quad && cfg->clamp_quad < 80.0) ? 1 : 0;
   p->heavy = 0;  // set per launch (heavy_threshold)
+  p->kdev = nullptr;
+  p->pdev = nullptr;
   // Mask path (no emission kernel): 16x16 or 32x32 tiles, 1 <= K <= kMaskMaxK, a tile grid
   // k_bin bins in LDS, and masks of a bounded total size.
   p->W = 0;
@@ -3733,7 +3760,7 @@ size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, in
 static int forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                        const float* mu, const float* chol_raw, const float* amp, int64_t* tile_ptr,
                        int64_t* num_pairs_dev, int64_t* num_pairs_host, void* workspace, size_t workspace_bytes,
-                       void* stream, bool force_tiles);
+                       void* stream, bool force_tiles, const int64_t* kdev = nullptr);
 
 int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                    const float* mu, const float* chol_raw, const float* amp, int64_t* tile_ptr,
@@ -3744,14 +3771,16 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
 }
 
 // force_tiles: bin the tiles with k_bin_tiles (tile_ptr and the chain-rule maps stored here) also
-// where the render would bin them itself (tiles_in_render).
+// where the render would bin them itself (tiles_in_render).  kdev: capacity mode (k is the capacity,
+// the live K is *kdev; see Problem::kdev).
 static int forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                        const float* mu, const float* chol_raw, const float* amp, int64_t* tile_ptr,
                        int64_t* num_pairs_dev, int64_t* num_pairs_host, void* workspace, size_t workspace_bytes,
-                       void* stream, bool force_tiles) {
+                       void* stream, bool force_tiles, const int64_t* kdev) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
+  p.kdev = kdev;
   const FwdLayout L = fwd_layout(p);
   if (!workspace || workspace_bytes < L.total)
     return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
@@ -3818,13 +3847,27 @@ int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in
   return GF_OK;
 }
 
+static int forward_render(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                          const float* row_coords, const float* col_coords, int64_t* tile_ptr,
+                          int64_t* gaussian_ids_sorted, int64_t ids_capacity, float* delta, void* workspace,
+                          size_t workspace_bytes, void* stream, const int64_t* kdev);
+
 int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                       const float* row_coords, const float* col_coords, int64_t* tile_ptr,
                       int64_t* gaussian_ids_sorted, int64_t ids_capacity,
                       float* delta, void* workspace, size_t workspace_bytes, void* stream) {
+  return forward_render(cfg, out_features, in_features, k, row_coords, col_coords, tile_ptr, gaussian_ids_sorted,
+                        ids_capacity, delta, workspace, workspace_bytes, stream, nullptr);
+}
+
+static int forward_render(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                          const float* row_coords, const float* col_coords, int64_t* tile_ptr,
+                          int64_t* gaussian_ids_sorted, int64_t ids_capacity, float* delta, void* workspace,
+                          size_t workspace_bytes, void* stream, const int64_t* kdev) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
+  p.kdev = kdev;
   const int64_t T = (int64_t)p.R * p.C;
   const FwdLayout L = fwd_layout(p);
   if (!workspace || workspace_bytes < L.total)
@@ -3887,15 +3930,37 @@ int gf_forward(const gf_field_config* cfg, int64_t out_features, int64_t in_feat
                            gaussian_ids_sorted, ids_capacity, delta, workspace, workspace_bytes, stream);
 }
 
+static int backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                           const float* grad_delta, const float* row_coords, const float* col_coords,
+                           const float* mu, const float* chol_raw, const void* tile_ptr, int32_t tile_ptr_is_int64,
+                           const void* gaussian_ids, int32_t ids_is_int64, int64_t num_pairs,
+                           const void* forward_workspace, void* workspace, size_t workspace_bytes, void* stream,
+                           const int64_t* kdev, const int64_t* pdev);
+
 int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                        const float* grad_delta, const float* row_coords, const float* col_coords,
                        const float* mu, const float* chol_raw, const void* tile_ptr,
                        int32_t tile_ptr_is_int64, const void* gaussian_ids, int32_t ids_is_int64,
                        int64_t num_pairs, const void* forward_workspace, void* workspace,
                        size_t workspace_bytes, void* stream) {
+  return backward_reduce(cfg, out_features, in_features, k, grad_delta, row_coords, col_coords, mu, chol_raw,
+                         tile_ptr, tile_ptr_is_int64, gaussian_ids, ids_is_int64, num_pairs, forward_workspace,
+                         workspace, workspace_bytes, stream, nullptr, nullptr);
+}
+
+// kdev / pdev: capacity mode (k is the capacity; see Problem::kdev); num_pairs then only bounds
+// the launch (its heavy-tile and dense-tile choices).
+static int backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                           const float* grad_delta, const float* row_coords, const float* col_coords,
+                           const float* mu, const float* chol_raw, const void* tile_ptr, int32_t tile_ptr_is_int64,
+                           const void* gaussian_ids, int32_t ids_is_int64, int64_t num_pairs,
+                           const void* forward_workspace, void* workspace, size_t workspace_bytes, void* stream,
+                           const int64_t* kdev, const int64_t* pdev) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
+  p.kdev = kdev;
+  p.pdev = pdev;
   const int64_t T = (int64_t)p.R * p.C;
   const BwdLayout L = bwd_layout(p);
   if (!workspace || workspace_bytes < L.total)
@@ -3928,7 +3993,7 @@ int gf_backward_reduce(const gf_field_config* cfg, int64_t out_features, int64_t
 static int backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                            const float* chol_raw, const float* amp, float* d_mu, float* d_chol_raw, float* d_amp,
                            const void* forward_workspace, void* workspace, size_t workspace_bytes, void* stream,
-                           int32_t ostride);
+                           int32_t ostride, const int64_t* kdev = nullptr);
 
 int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                        const float* chol_raw, const float* amp, float* d_mu, float* d_chol_raw,
@@ -3938,14 +4003,15 @@ int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t
                          forward_workspace, workspace, workspace_bytes, stream, 0);
 }
 
-// gf_backward_finish with the outputs' per-Gaussian stride (finish_body's ostride).
+// gf_backward_finish with the outputs' per-Gaussian stride (finish_body's ostride); kdev: capacity mode.
 static int backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                            const float* chol_raw, const float* amp, float* d_mu, float* d_chol_raw, float* d_amp,
                            const void* forward_workspace, void* workspace, size_t workspace_bytes, void* stream,
-                           int32_t ostride) {
+                           int32_t ostride, const int64_t* kdev) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
+  p.kdev = kdev;
   const BwdLayout L = bwd_layout(p);
   if (!workspace || workspace_bytes < L.total)
     return set_err(GF_E_WORKSPACE, "backward workspace needs %zu bytes, got %zu", L.total, workspace_bytes);
@@ -4006,14 +4072,34 @@ size_t gf_forward_grads_offset(int64_t out_features, int64_t in_features, int64_
   return fwd_layout(p).dgrad;
 }
 
+static int backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                           const float* grad_delta, const float* row_coords, const float* col_coords,
+                           const float* mu, const float* chol_raw, const float* amp, const int64_t* tile_ptr,
+                           const int64_t* gaussian_ids, int64_t num_pairs, void* forward_workspace,
+                           size_t forward_workspace_bytes, void* workspace, size_t workspace_bytes, void* stream,
+                           const int64_t* kdev, const int64_t* pdev);
+
 int gf_backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                        const float* grad_delta, const float* row_coords, const float* col_coords,
                        const float* mu, const float* chol_raw, const float* amp, const int64_t* tile_ptr,
                        const int64_t* gaussian_ids, int64_t num_pairs, void* forward_workspace,
                        size_t forward_workspace_bytes, void* workspace, size_t workspace_bytes, void* stream) {
+  return backward_direct(cfg, out_features, in_features, k, grad_delta, row_coords, col_coords, mu, chol_raw, amp,
+                         tile_ptr, gaussian_ids, num_pairs, forward_workspace, forward_workspace_bytes, workspace,
+                         workspace_bytes, stream, nullptr, nullptr);
+}
+
+static int backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                           const float* grad_delta, const float* row_coords, const float* col_coords,
+                           const float* mu, const float* chol_raw, const float* amp, const int64_t* tile_ptr,
+                           const int64_t* gaussian_ids, int64_t num_pairs, void* forward_workspace,
+                           size_t forward_workspace_bytes, void* workspace, size_t workspace_bytes, void* stream,
+                           const int64_t* kdev, const int64_t* pdev) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
+  p.kdev = kdev;
+  p.pdev = pdev;
   const FwdLayout FL = fwd_layout(p);
   if (!forward_workspace || forward_workspace_bytes < FL.total)
     return set_err(GF_E_WORKSPACE, "forward workspace needs %zu bytes, got %zu", FL.total,
@@ -4021,12 +4107,12 @@ int gf_backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t
   uint8_t* fws = reinterpret_cast<uint8_t*>(forward_workspace);
   float* dg = reinterpret_cast<float*>(fws + FL.dgrad);  // [K][8]: d_amp, d_mu x2, d_chol_raw x3
   if (!direct_one_launch(p, num_pairs) || k == 0) {
-    rc = gf_backward_reduce(cfg, out_features, in_features, k, grad_delta, row_coords, col_coords, mu, chol_raw,
-                            tile_ptr, 1, gaussian_ids, 1, num_pairs, forward_workspace, workspace,
-                            workspace_bytes, stream);
+    rc = backward_reduce(cfg, out_features, in_features, k, grad_delta, row_coords, col_coords, mu, chol_raw,
+                         tile_ptr, 1, gaussian_ids, 1, num_pairs, forward_workspace, workspace, workspace_bytes,
+                         stream, kdev, pdev);
     if (rc) return rc;
     return backward_finish(cfg, out_features, in_features, k, chol_raw, amp, dg + 1, dg + 3, dg, forward_workspace,
-                           workspace, workspace_bytes, stream, 8);
+                           workspace, workspace_bytes, stream, 8, kdev);
   }
   const BwdLayout L = bwd_layout(p);
   if (!workspace || workspace_bytes < L.total)
@@ -4048,6 +4134,51 @@ int gf_backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t
                                reinterpret_cast<const float4*>(fws + FL.dcoef), dg);
   GF_LAUNCH_CHECK("k_bwd");
   return GF_OK;
+}
+
+// Capacity mode: the mask path at the capacity (every live K in [0, k_capacity] then takes the
+// same kernels, grids and layouts).
+static int check_kcap(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k_capacity,
+                      const int64_t* k_dev, Problem* p) {
+  int rc = make_problem(cfg, out_features, in_features, k_capacity, p);
+  if (rc) return rc;
+  if (p->W == 0)
+    return set_err(GF_E_INVALID_ARGUMENT,
+                   "capacity mode takes 16x16 or 32x32 tiles with 1 <= k_capacity <= %lld (the mask path); "
+                   "k_capacity = %lld", (long long)kMaskMaxK, (long long)k_capacity);
+  if (!k_dev) return set_err(GF_E_INVALID_ARGUMENT, "k_dev must not be NULL");
+  return GF_OK;
+}
+
+int gf_forward_kcap(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k_capacity,
+                    const int64_t* k_dev, const float* row_coords, const float* col_coords, const float* mu,
+                    const float* chol_raw, const float* amp, int64_t* tile_ptr, int64_t* num_pairs_dev,
+                    int64_t* gaussian_ids_sorted, int64_t ids_capacity, float* delta, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  Problem p;
+  int rc = check_kcap(cfg, out_features, in_features, k_capacity, k_dev, &p);
+  if (rc) return rc;
+  rc = forward_bin(cfg, out_features, in_features, k_capacity, mu, chol_raw, amp, tile_ptr, num_pairs_dev, nullptr,
+                   workspace, workspace_bytes, stream, false, k_dev);
+  if (rc) return rc;
+  return forward_render(cfg, out_features, in_features, k_capacity, row_coords, col_coords, tile_ptr,
+                        gaussian_ids_sorted, ids_capacity, delta, workspace, workspace_bytes, stream, k_dev);
+}
+
+int gf_backward_direct_kcap(const gf_field_config* cfg, int64_t out_features, int64_t in_features,
+                            int64_t k_capacity, const int64_t* k_dev, const float* grad_delta,
+                            const float* row_coords, const float* col_coords, const float* mu,
+                            const float* chol_raw, const float* amp, const int64_t* tile_ptr,
+                            const int64_t* gaussian_ids, const int64_t* num_pairs_dev, int64_t ids_capacity,
+                            void* forward_workspace, size_t forward_workspace_bytes, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  Problem p;
+  int rc = check_kcap(cfg, out_features, in_features, k_capacity, k_dev, &p);
+  if (rc) return rc;
+  if (!num_pairs_dev) return set_err(GF_E_INVALID_ARGUMENT, "num_pairs_dev must not be NULL");
+  return backward_direct(cfg, out_features, in_features, k_capacity, grad_delta, row_coords, col_coords, mu,
+                         chol_raw, amp, tile_ptr, gaussian_ids, ids_capacity, forward_workspace,
+                         forward_workspace_bytes, workspace, workspace_bytes, stream, k_dev, num_pairs_dev);
 }
 
 // The one-pass kernel takes the fields gf_backward_direct runs in one launch, with 16x16 tiles and

@@ -404,3 +404,106 @@ class FieldBatchPlan:
     def status(self) -> list[int]:
         """Forward | backward GF_STATUS_* bits per layer (synchronises)."""
         return self.read()[0]
+
+
+class StaticFieldPlan:
+    """One field whose forward and one-launch backward can be captured in a HIP graph once and
+    replayed across changes of K (gf_forward_kcap / gf_backward_direct_kcap).
+
+    Densification clones and prunes Gaussians every 50-200 steps (reference
+    controllers/clone.py:31-56, prune.py:34-45), which gives the parameters another K.  Here
+    everything a launch depends on is fixed by ``k_capacity``: the plan owns the parameter buffers
+    (``mu`` [k_capacity, 2], ``chol_raw`` [k_capacity, 3], ``amp`` [k_capacity, 1]) and the device K
+    (``k_dev``), and the kernels read the live K and pair count from device memory.
+    :meth:`set_params` copies a new parameter set in (any K up to the capacity) and writes K, on
+    the current stream and outside any capture; a graph captured over :meth:`forward` and
+    :meth:`backward_direct` then replays with the new field and no re-capture.
+
+    The mask path only: 16x16 or 32x32 tiles, 1 <= k_capacity <= 8192.  ``ids_capacity`` bounds the
+    pairs of every K the plan will see (past it GF_STATUS_CAPACITY is set: check :meth:`status`).
+    """
+
+    def __init__(self, out_features: int, in_features: int, k_capacity: int, device, *, ids_capacity: int,
+                 tile_out: int = 16, tile_in: int = 16, sigma_multiplier: float = 3.0, normalize: bool = False,
+                 clamp_quad: float | None = 80.0):
+        kc = int(k_capacity)
+        # workspaces, tile_ptr, ids and delta of a FieldPlan laid out for the capacity
+        self.buffers = FieldPlan(out_features, in_features, kc, device, tile_out=tile_out, tile_in=tile_in,
+                                 sigma_multiplier=sigma_multiplier, normalize=normalize, clamp_quad=clamp_quad,
+                                 ids_capacity=ids_capacity, grads=False)
+        b = self.buffers
+        self.M, self.N, self.k_capacity, self.device, self.cfg = b.M, b.N, kc, b.device, b.cfg
+        self.mu = torch.zeros(kc, 2, dtype=torch.float32, device=self.device)
+        self.chol_raw = torch.zeros(kc, 3, dtype=torch.float32, device=self.device)
+        self.amp = torch.zeros(kc, 1, dtype=torch.float32, device=self.device)
+        self.k_dev = torch.zeros(1, dtype=torch.int64, device=self.device)
+        self.live_k = 0
+
+    @property
+    def delta(self) -> torch.Tensor:
+        return self.buffers.delta
+
+    @property
+    def tile_ptr(self) -> torch.Tensor:
+        return self.buffers.tile_ptr
+
+    @property
+    def ids(self) -> torch.Tensor:
+        return self.buffers.ids
+
+    def set_params(self, mu, chol_raw, amp) -> None:
+        """The field's Gaussians for the next forward: K = mu.shape[0] <= k_capacity rows of
+        mu [K, 2], chol_raw [K, 3], amp [K, 1] (fp32, on the plan's device), copied in on the current
+        stream; the capacity's other rows are left as they are (the kernels read only K rows)."""
+        k = int(mu.shape[0])
+        if not (0 <= k <= self.k_capacity):
+            raise ValueError(f"K = {k} outside [0, {self.k_capacity}] (the plan's capacity)")
+        if tuple(chol_raw.shape) != (k, 3) or tuple(amp.shape) != (k, 1) or tuple(mu.shape) != (k, 2):
+            raise ValueError("mu / chol_raw / amp must have shapes [K,2], [K,3], [K,1]")
+        with torch.no_grad():
+            self.mu[:k].copy_(mu)
+            self.chol_raw[:k].copy_(chol_raw)
+            self.amp[:k].copy_(amp)
+            self.k_dev.fill_(k)
+        self.live_k = k
+
+    def forward(self, row_coords, col_coords) -> torch.Tensor:
+        """Bins and renders the current parameters into ``delta`` (and tile_ptr, the ids, P)."""
+        b = self.buffers
+        N.check(N.lib().gf_forward_kcap(ctypes.byref(self.cfg), self.M, self.N, self.k_capacity, self.k_dev.data_ptr(),
+                                        row_coords.data_ptr(), col_coords.data_ptr(), self.mu.data_ptr(),
+                                        self.chol_raw.data_ptr(), self.amp.data_ptr(), b.tile_ptr.data_ptr(),
+                                        b.num_pairs.data_ptr(), b.ids.data_ptr(), b.capacity, b.delta.data_ptr(),
+                                        b.fwd_ws.data_ptr(), b.fwd_ws_bytes, b._stream()), "gf_forward_kcap")
+        return b.delta
+
+    def backward_direct(self, grad, row_coords, col_coords):
+        """The gradients of the last forward's field into the forward workspace's slots (as
+        FieldPlan.backward_direct: added into slots the forward cleared); returns views
+        (d_mu, d_chol_raw, d_amp) of the slots of the capacity: rows 0 .. live_k - 1 are the field's."""
+        b = self.buffers
+        N.check(N.lib().gf_backward_direct_kcap(
+            ctypes.byref(self.cfg), self.M, self.N, self.k_capacity, self.k_dev.data_ptr(), grad.data_ptr(),
+            row_coords.data_ptr(), col_coords.data_ptr(), self.mu.data_ptr(), self.chol_raw.data_ptr(),
+            self.amp.data_ptr(), b.tile_ptr.data_ptr(), b.ids.data_ptr(), b.num_pairs.data_ptr(), b.capacity,
+            b.fwd_ws.data_ptr(), b.fwd_ws_bytes, b.bwd_ws.data_ptr(), b.bwd_ws_bytes, b._stream()),
+            "gf_backward_direct_kcap")
+        off = int(N.lib().gf_forward_grads_offset(self.M, self.N, self.k_capacity, ctypes.byref(self.cfg)))
+        slots = b.fwd_ws[off:off + 32 * self.k_capacity].view(torch.float32).view(self.k_capacity, 8)
+        return slots[:, 1:3], slots[:, 3:6], slots[:, 0:1]
+
+    def direct_launches(self) -> int:
+        """Launches :meth:`backward_direct` makes (1, or 2 for reduction + finish), the same for every K."""
+        r = int(N.lib().gf_backward_direct_launches(ctypes.byref(self.cfg), self.M, self.N, self.k_capacity,
+                                                    self.buffers.capacity))
+        if r < 0:
+            N.check(-r, "gf_backward_direct_launches")
+        return r
+
+    def pairs(self) -> int:
+        """Pair count of the last forward (synchronises)."""
+        return self.buffers.pairs()
+
+    def status(self, which: str = "forward") -> int:
+        """GF_STATUS_* bits of the last forward or backward (synchronises)."""
+        return self.buffers.status(which)

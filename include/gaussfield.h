@@ -204,6 +204,36 @@ int gf_backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t
                        size_t forward_workspace_bytes, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Capacity mode of gf_forward and gf_backward_direct, for graphs that must outlive a change of K
+ * (densification clones and prunes Gaussians every 50-200 steps, reference
+ * controllers/clone.py:31-56, prune.py:34-45, base_trainer.py:126-220; the reference re-runs its
+ * whole forward per call, field_impl.cu:135-179).  k_capacity fixes everything the host decides and
+ * every kernel argument -- workspace layouts (gf_forward_workspace_bytes / gf_backward_workspace_bytes
+ * at k_capacity), mask words, launch grids, the kernels taken -- and the kernels read the live K
+ * from k_dev (device int64, clamped to [0, k_capacity]) and the backward the live pair count from
+ * num_pairs_dev (the forward's output).  A HIP graph captured over these two calls therefore stays
+ * valid when *k_dev changes: the caller keeps mu [k_capacity,2], chol_raw [k_capacity,3] and
+ * amp [k_capacity,1] in fixed buffers whose first *k_dev rows are the live Gaussians, and writes
+ * the new K before replaying.  Outputs as gf_forward / gf_backward_direct for the live field (the
+ * gradient slots of Gaussians 0 .. *k_dev - 1).  The mask path only: 16x16 or 32x32 tiles,
+ * 1 <= k_capacity <= 8192; other fields are refused with GF_E_INVALID_ARGUMENT.  ids_capacity bounds
+ * the pairs of every live K (pairs past it are dropped and GF_STATUS_CAPACITY is set).
+ */
+int gf_forward_kcap(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k_capacity,
+                    const int64_t* k_dev, const float* row_coords, const float* col_coords, const float* mu,
+                    const float* chol_raw, const float* amp, int64_t* tile_ptr, int64_t* num_pairs_dev,
+                    int64_t* gaussian_ids_sorted, int64_t ids_capacity, float* delta, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+int gf_backward_direct_kcap(const gf_field_config* cfg, int64_t out_features, int64_t in_features,
+                            int64_t k_capacity, const int64_t* k_dev, const float* grad_delta,
+                            const float* row_coords, const float* col_coords, const float* mu,
+                            const float* chol_raw, const float* amp, const int64_t* tile_ptr,
+                            const int64_t* gaussian_ids, const int64_t* num_pairs_dev, int64_t ids_capacity,
+                            void* forward_workspace, size_t forward_workspace_bytes, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/*
  * Forward and backward in one pass, for callers that hold dL/d(delta) before the forward (fits to
  * a fixed target, benchmarks of the path): gf_forward's outputs (tile_ptr, P into num_pairs_dev,
  * the ids, delta) and gf_backward_direct's gradients (added into the forward workspace's slots at

@@ -2336,3 +2336,64 @@ def test_fused_graph_replay(device):
         for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), views, eager):
             grad_close(a, b, f"replay {rep} {name}", rtol=1e-5)
         _ = (plan.delta * 2.0).sum().item()  # eager work between replays
+
+
+@pytest.mark.parametrize("variant", ["tile16", "tile32", "tile16_two_launch"])
+def test_static_plan_graph_survives_k_changes(device, variant):
+    """Capacity mode (gf_forward_kcap + gf_backward_direct_kcap through StaticFieldPlan): forward
+    and backward captured once at K = 200 (capacity 512) and replayed after set_params with
+    K = 480, 90, 0 and 200 again -- no re-capture -- with poisoned outputs and eager work between
+    the replays: every replay's binning bit-exact, delta-W and gradients against the oracle of the
+    live field.  tile16_two_launch: an id capacity that makes the tiles dense, so the backward is
+    the reduction + finish (the same two launches at every K)."""
+    from guass_amd.ops import StaticFieldPlan
+
+    tile = 32 if variant == "tile32" else 16
+    M = N = 640
+    T = (M // tile) * (N // tile)
+    full = wl.make_problem("static_640_k480", M, N, 480, math.log(8.0), 0.6, 51)
+    # 8 T - 1 (16x16): sparse, no heavy-tile workgroups: the one-launch backward; 16 T: dense, with
+    # heavy-tile workgroups (render and reduction) and the finish; 32x32 tiles have no heavy tiles
+    cap = {"tile16": 8 * T - 1, "tile32": 16 * T - 1, "tile16_two_launch": 16 * T}[variant]
+    plan = StaticFieldPlan(M, N, 512, device, ids_capacity=cap, tile_out=tile, tile_in=tile)
+    assert plan.direct_launches() == (2 if variant.endswith("two_launch") else 1)
+    q = full.to(device)
+    say(f"static plan {variant}: capacity 512, ids capacity {cap}")
+
+    def sub(k):
+        return wl.FieldProblem(f"static_k{k}", M, N, full.row_coords, full.col_coords, full.mu[:k].clone(),
+                               full.chol_raw[:k].clone(), full.amp[:k].clone(), full.grad)
+
+    plan.set_params(q.mu[:200], q.chol_raw[:200], q.amp[:200])
+    s = torch.cuda.Stream(device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(s):  # warm-up off the capture
+        plan.forward(q.row_coords, q.col_coords)
+        plan.backward_direct(q.grad, q.row_coords, q.col_coords)
+    torch.cuda.current_stream(device).wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.forward(q.row_coords, q.col_coords)
+        views = plan.backward_direct(q.grad, q.row_coords, q.col_coords)
+    for k in (200, 480, 90, 0, 200):
+        say(f"  replay with K = {k}")
+        plan.set_params(q.mu[:k], q.chol_raw[:k], q.amp[:k])
+        plan.delta.fill_(float("nan"))
+        for v in views:
+            v.fill_(float("nan"))
+        float(torch.randn(1 << 12, device=device).sum())  # eager work between the replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert plan.status() == 0 and plan.status("backward") == 0, f"K = {k}: status"
+        r = oracle(sub(k), tile_out=tile, tile_in=tile)
+        P = int(r[1][-1])
+        assert plan.pairs() == P
+        binning_equal(plan.tile_ptr, plan.ids[:P], r[1], r[2])
+        if k == 0:
+            assert P == 0 and float(plan.delta.abs().max()) == 0.0
+            continue
+        field_close(plan.delta, r[0])
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), views, r[3:]):
+            grad_close(a[:k], b, f"K = {k} {name}")
