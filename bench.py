@@ -567,12 +567,16 @@ def main() -> int:
                          tile_out=args.tile, tile_in=args.tile)
 
         # The backward in one launch where the field allows it (gf_backward_direct: the chain
-        # rule applied per tile, no finish pass); elsewhere the same call runs two.
-        direct_one = plan.direct_launches(P) == 1
+        # rule applied per tile, no finish pass); elsewhere the same call runs two.  The widest
+        # tile rectangle takes part in the choice as in training (gf_backward_train).
+        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+        _, span = plan.bin_info()
+        direct_one = plan.direct_launches(P, span) == 1
 
         def step():
             plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
-            plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P)
+            plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P,
+                                 max_span=span)
 
         phases = {
             "k_bin": [lambda: plan.bin(q.mu, q.chol_raw, q.amp)],
@@ -581,7 +585,7 @@ def main() -> int:
         }
         if direct_one:
             phases["k_bwd"] = [lambda: plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw,
-                                                            q.amp, num_pairs=P)]
+                                                            q.amp, num_pairs=P, max_span=span)]
         else:
             phases["k_bwd"] = [lambda: plan.backward_reduce(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, P)]
             phases["k_bwd_finish"] = [lambda: plan.backward_finish(q.chol_raw, q.amp)]
@@ -707,7 +711,10 @@ def main() -> int:
         "kernel_rooflines": kernel_rooflines,
         "gpu_event_ms_per_step": gpu_ms / args.steps,
     }
-    if not batched and plan.fused_supported():
+    if not batched:
+        out["config"]["max_span"] = span
+        out["config"]["backward_launches"] = 1 if direct_one else 2
+    if not batched and plan.fused_supported(span):
         out["fused"] = fused_times(plan, q, total, per_run, args, graph_time_us, ph["k_bin"])
     if not batched and args.dropin_calls > 0:
         out["dropin"] = dropin_times(qs[0], args, dev)

@@ -34,7 +34,7 @@ EXPORTED = (
     "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward",
     "gf_batch_set_grads", "gf_batch_read", "gf_backward_noalloc", "gf_forward", "gf_backward_direct",
     "gf_forward_grads_offset", "gf_backward_direct_launches", "gf_fwd_bwd_fused", "gf_fwd_bwd_fused_supported",
-    "gf_forward_kcap", "gf_backward_direct_kcap",
+    "gf_forward_kcap", "gf_backward_direct_kcap", "gf_forward_bin_info", "gf_read_bin_info", "gf_backward_train",
 )
 
 GF_PHASE_BIN, GF_PHASE_EMIT, GF_PHASE_RENDER = 0x1, 0x2, 0x4
@@ -69,6 +69,12 @@ class GfLayer(ctypes.Structure):
         ("reserved", c_int32), ("base_weight", c_void_p), ("merged_weight", c_void_p), ("delta_scale", c_float),
         ("reserved2", c_int32),
     ]
+
+
+class GfBinInfo(ctypes.Structure):
+    """``gf_bin_info``: P and the most tiles one Gaussian's rectangle covers."""
+
+    _fields_ = [("num_pairs", c_int64), ("max_span", c_int64)]
 
 
 class GfBatchInfo(ctypes.Structure):
@@ -127,14 +133,19 @@ def lib() -> ctypes.CDLL:
     L.gf_backward_noalloc.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int32,
                                       _P, c_int32, c_int64, _P, _P, _P, _P, _P]
     L.gf_backward_direct.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, c_int64,
-                                     _P, c_size_t, _P, c_size_t, _P]
+                                     c_int64, _P, c_size_t, _P, c_size_t, _P]
+    L.gf_forward_bin_info.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, POINTER(GfBinInfo), _P,
+                                      c_size_t, _P]
+    L.gf_read_bin_info.argtypes = [_P, POINTER(GfBinInfo), _P]
+    L.gf_backward_train.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int32, _P, c_int32,
+                                    c_int64, c_int64, _P, _P, _P, _P, _P, c_size_t, _P]
     L.gf_forward_grads_offset.argtypes = [c_int64, c_int64, c_int64, _CFG]
     L.gf_forward_grads_offset.restype = c_size_t
-    L.gf_backward_direct_launches.argtypes = [_CFG, c_int64, c_int64, c_int64, c_int64]
+    L.gf_backward_direct_launches.argtypes = [_CFG, c_int64, c_int64, c_int64, c_int64, c_int64]
     L.gf_backward_direct_launches.restype = c_int
     L.gf_fwd_bwd_fused.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, _P,
                                    _P, c_size_t, _P]
-    L.gf_fwd_bwd_fused_supported.argtypes = [_CFG, c_int64, c_int64, c_int64, c_int64]
+    L.gf_fwd_bwd_fused_supported.argtypes = [_CFG, c_int64, c_int64, c_int64, c_int64, c_int64]
     L.gf_forward_kcap.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, _P, _P,
                                   c_size_t, _P]
     L.gf_backward_direct_kcap.argtypes = [_CFG, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
@@ -152,7 +163,8 @@ def lib() -> ctypes.CDLL:
                  "gf_backward", "gf_backward_reduce", "gf_backward_finish", "gf_read_status",
                  "gf_selftest_softplus", "gf_batch_plan", "gf_batch_forward", "gf_batch_backward",
                  "gf_batch_set_grads", "gf_batch_read", "gf_backward_noalloc", "gf_forward",
-                 "gf_backward_direct", "gf_fwd_bwd_fused", "gf_forward_kcap", "gf_backward_direct_kcap"):
+                 "gf_backward_direct", "gf_fwd_bwd_fused", "gf_forward_kcap", "gf_backward_direct_kcap",
+                 "gf_forward_bin_info", "gf_read_bin_info", "gf_backward_train"):
         getattr(L, name).restype = c_int
     _LIB = L
     return L

@@ -162,8 +162,9 @@ struct WsHeader {
   uint32_t heavy;      // forward, heavy-tile mode: tiles in the heavy-tile list
   int64_t* num_pairs;  // forward, tiles binned in the render: where the render stores P
   int64_t pairs;       // forward: P as the binning computed it, beside the status word, so that
-                       // one 24-byte copy reads both back (gf_forward_bin's num_pairs_host)
-  uint32_t pad[58];
+                       // one 32-byte copy reads both back (gf_forward_bin's num_pairs_host)
+  int64_t max_span;    // forward: the most tiles one Gaussian's rectangle covers (gf_bin_info)
+  uint32_t pad[56];
 };
 static_assert(sizeof(WsHeader) == 256, "workspace header must be 256 bytes");
 
@@ -648,6 +649,7 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
   __shared__ int32_t rowdiff[kBinMaxBandRows + 1];
   __shared__ int64_t scan_lds[kBinThreads / 64 + 1];
   __shared__ unsigned long long pairs_lds;
+  __shared__ int32_t span_lds;  // the most tiles of one rectangle
   // rectangles with long row / column spans: Gaussian, first row / column in the band, span,
   // columns (row spans), and the prefix of the spans
   __shared__ int32_t long_g[kLongMax], long_lo[kLongMax], long_n[kLongMax];
@@ -665,6 +667,7 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
   if (threadIdx.x == 0) {
     hdr->status = 0u;
     pairs_lds = 0ull;
+    span_lds = 0;
     nlong = 0u;
   }
 
@@ -745,6 +748,7 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
   // kBinRectRegs * kBinThreads Gaussians keep their rectangle in registers.
   int4 myrect[kBinRectRegs];
   int64_t my_pairs = 0;
+  int32_t my_span = 0;
   struct PrepIn {
     float mu0, mu1, r11, r21, r22, amp;
   };
@@ -761,6 +765,7 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
     covs[g] = make_float4(c.s00, c.s01, c.s11, 0.0f);
     reinterpret_cast<float2*>(ws + L.lfac)[g] = make_float2(Lc.l11, Lc.l22);
     my_pairs += touched;
+    my_span = max(my_span, touched);
     if (kEval) {
       GaussEval v = eval_from_cov(p, in.mu0, in.mu1, c, in.amp);
       v.gid = (int32_t)g;
@@ -779,8 +784,12 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
   // B: P = total pairs: wave sums, one LDS atomic per wave after the barrier that orders them
   // behind the counter's initialisation; read by thread 0 after later barriers.
   const int64_t wave_pairs = readlane_i64(wave_inclusive_scan(my_pairs), 63);
+  for (int off = 32; off > 0; off >>= 1) my_span = max(my_span, __shfl_xor(my_span, off));
   __syncthreads();
-  if (lane == 0) atomicAdd(&pairs_lds, (unsigned long long)wave_pairs);
+  if (lane == 0) {
+    atomicAdd(&pairs_lds, (unsigned long long)wave_pairs);
+    atomicMax(&span_lds, my_span);
+  }
 
   // C: each covered row of each rectangle adds +1 at its first column and -1 after its last;
   // the rectangle's width is added over its rows through a difference array over rows (and,
@@ -903,6 +912,7 @@ __device__ __forceinline__ void bin_body(const Problem& p, const float* __restri
     tile_ptr[T] = Pc;
     *num_pairs = P;
     hdr->pairs = P;
+    hdr->max_span = span_lds;
     if (Pc != P) hdr->status |= GF_STATUS_COUNT_MISMATCH;
   }
 }
@@ -1071,6 +1081,7 @@ __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t*
     for (int32_t i = threadIdx.x; i <= C; i += kTilesThreads) diff[i] = 0;
   __syncthreads();
   int64_t before = 0, pairs = 0;
+  int32_t span = 0;  // the most tiles of one rectangle (row workgroups; the last one reports it)
   // The rectangles are loaded kBinPrefetch rounds at a time, so that the rounds do not each wait
   // for their own load (4 rounds at cfg3).
   constexpr int kBinPrefetch = 8;
@@ -1093,6 +1104,7 @@ __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t*
           const int32_t h = r.y - r.x + 1, w = r.w - r.z + 1;
           before += (int64_t)w * clamp_i32(line - r.x, 0, h);
           pairs += (int64_t)w * h;
+          span = max(span, w * h);
           covers = r.x <= line && line <= r.y;
           if (covers) {
             atomicAdd(diff + r.z, 1);
@@ -1131,7 +1143,12 @@ __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t*
   // [t*per, t*per + per).
   constexpr int kWaves = kTilesThreads / 64;
   __shared__ int64_t wsum[4][kWaves];
+  __shared__ int32_t wspan[kWaves];
   const int wid = threadIdx.x >> 6;
+  if (line == R - 1) {  // workgroup-uniform
+    for (int off = 32; off > 0; off >>= 1) span = max(span, __shfl_xor(span, off));
+    if (lane == 0) wspan[wid] = span;
+  }
   const int32_t per = (C + kTilesThreads - 1) / kTilesThreads;
   const int32_t cb = (int32_t)threadIdx.x * per, ce = min(cb + per, C);
   int64_t d = 0, e = 0;
@@ -1174,6 +1191,10 @@ __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t*
     tile_ptr[(int64_t)R * C] = P;
     *num_pairs = P;
     reinterpret_cast<WsHeader*>(ws)->pairs = P;
+    int32_t most = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) most = max(most, wspan[w]);
+    reinterpret_cast<WsHeader*>(ws)->max_span = most;
     reinterpret_cast<WsHeader*>(ws)->status = P == total ? 0u : GF_STATUS_COUNT_MISMATCH;
   }
 }
@@ -1184,17 +1205,25 @@ __global__ __launch_bounds__(kTilesThreads) void k_pairs(Problem p, int64_t* __r
                                                          uint8_t* __restrict__ ws, FwdLayout L) {
   __shared__ int64_t scan_lds[kTilesThreads / 64 + 1];
   const int4* __restrict__ rect = reinterpret_cast<const int4*>(ws + L.rect);
+  __shared__ int32_t span_lds;
   int64_t s = 0;
+  int32_t span = 0;
   const int64_t K = live_k(p);
+  if (threadIdx.x == 0) span_lds = 0;
   for (int64_t g = threadIdx.x; g < K; g += kTilesThreads) {
     const int4 r = rect[g];
-    s += (int64_t)(r.y - r.x + 1) * (r.w - r.z + 1);
+    const int32_t n = (r.y - r.x + 1) * (r.w - r.z + 1);
+    s += n;
+    span = max(span, n);
   }
   int64_t total;
-  (void)block_exclusive_scan<kTilesThreads>(s, &total, scan_lds);
+  (void)block_exclusive_scan<kTilesThreads>(s, &total, scan_lds);  // its barriers order span_lds's
+  atomicMax(&span_lds, span);                                      // initialisation before these
+  __syncthreads();
   if (threadIdx.x == 0) {
     *num_pairs = total;
     reinterpret_cast<WsHeader*>(ws)->pairs = total;
+    reinterpret_cast<WsHeader*>(ws)->max_span = span_lds;
   }
 }
 
@@ -1715,6 +1744,7 @@ __device__ __forceinline__ void render16_body(
       __shared__ uint32_t wmask[kTileThreads / 64][kMaskMaxK / 32];
       uint32_t* mw = wmask[wid];
       int64_t before = 0, cnt = 0;
+      int32_t span = 0;  // the most tiles of one rectangle, for the workspace header
       constexpr int kPre = 4;  // rounds of rectangle loads in flight (K <= 256: all of them)
       // every mask word of the tile is written, those of Gaussians past the live K as zero
       const int64_t Kl = live_k(p), Kw = 32 * (int64_t)p.W;
@@ -1736,6 +1766,7 @@ __device__ __forceinline__ void render16_body(
             const int32_t h = r.y - r.x + 1, wd = r.w - r.z + 1;
             const bool in_row = r.x <= tr && tr <= r.y;
             before += (int64_t)wd * clamp_i32(tr - r.x, 0, h) + (in_row ? clamp_i32(tc - r.z, 0, wd) : 0);
+            span = max(span, wd * h);
             covers = in_row && r.z <= tc && tc <= r.w;
           }
           const uint64_t bits = __builtin_amdgcn_ballot_w64(covers);
@@ -1747,9 +1778,16 @@ __device__ __forceinline__ void render16_body(
       }
       s = readlane_i64(wave_inclusive_scan(before), 63);
       count = cnt;
+      const int64_t T = (int64_t)p.R * p.C;
+      if (write_ids && t == T - 1) {  // wave-uniform
+        for (int off = 32; off > 0; off >>= 1) span = max(span, __shfl_xor(span, off));
+        if (lane == 0) {
+          hdr->pairs = s + count;
+          hdr->max_span = span;
+        }
+      }
       if (write_ids && lane == 0) {
         tile_ptr_out[t] = s;
-        const int64_t T = (int64_t)p.R * p.C;
         if (t == T - 1) {
           tile_ptr_out[T] = s + count;
           *hdr->num_pairs = s + count;
@@ -3643,6 +3681,24 @@ __global__ __launch_bounds__(256) void k_fill_zero(uint4* __restrict__ p, int64_
 }
 
 // Clears a workspace's status word (a kernel, ordered after a read-back copy on the stream).
+// The one-launch backward's gradients out of their slots (dgrad[K][8]: d_amp, d_mu x2,
+// d_chol_raw x3) into the caller's arrays, clearing each slot for the next backward on the same
+// forward (gf_backward_train).
+__global__ __launch_bounds__(256) void k_slots_out(float4* __restrict__ slots, int64_t K, float* __restrict__ d_mu,
+                                                   float* __restrict__ d_chol_raw, float* __restrict__ d_amp) {
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (g >= K) return;
+  const float4 a = slots[2 * g], b = slots[2 * g + 1];
+  d_amp[g] = a.x;
+  d_mu[2 * g + 0] = a.y;
+  d_mu[2 * g + 1] = a.z;
+  d_chol_raw[3 * g + 0] = a.w;
+  d_chol_raw[3 * g + 1] = b.x;
+  d_chol_raw[3 * g + 2] = b.y;
+  slots[2 * g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  slots[2 * g + 1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
 __global__ __launch_bounds__(64) void k_clear_status(uint32_t* __restrict__ status) {
   if (threadIdx.x == 0) *status = 0u;
 }
@@ -3759,14 +3815,26 @@ size_t gf_backward_workspace_bytes(int64_t out_features, int64_t in_features, in
 
 static int forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                        const float* mu, const float* chol_raw, const float* amp, int64_t* tile_ptr,
-                       int64_t* num_pairs_dev, int64_t* num_pairs_host, void* workspace, size_t workspace_bytes,
+                       int64_t* num_pairs_dev, gf_bin_info* info, void* workspace, size_t workspace_bytes,
                        void* stream, bool force_tiles, const int64_t* kdev = nullptr);
 
 int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                    const float* mu, const float* chol_raw, const float* amp, int64_t* tile_ptr,
                    int64_t* num_pairs_dev, int64_t* num_pairs_host, void* workspace,
                    size_t workspace_bytes, void* stream) {
-  return forward_bin(cfg, out_features, in_features, k, mu, chol_raw, amp, tile_ptr, num_pairs_dev, num_pairs_host,
+  gf_bin_info info;
+  const int rc = forward_bin(cfg, out_features, in_features, k, mu, chol_raw, amp, tile_ptr, num_pairs_dev,
+                             num_pairs_host ? &info : nullptr, workspace, workspace_bytes, stream, false);
+  if (rc == GF_OK && num_pairs_host) *num_pairs_host = info.num_pairs;
+  return rc;
+}
+
+int gf_forward_bin_info(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                        const float* mu, const float* chol_raw, const float* amp, int64_t* tile_ptr,
+                        int64_t* num_pairs_dev, gf_bin_info* info, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  if (!info) return set_err(GF_E_INVALID_ARGUMENT, "info must not be NULL");
+  return forward_bin(cfg, out_features, in_features, k, mu, chol_raw, amp, tile_ptr, num_pairs_dev, info,
                      workspace, workspace_bytes, stream, false);
 }
 
@@ -3775,7 +3843,7 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
 // the live K is *kdev; see Problem::kdev).
 static int forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                        const float* mu, const float* chol_raw, const float* amp, int64_t* tile_ptr,
-                       int64_t* num_pairs_dev, int64_t* num_pairs_host, void* workspace, size_t workspace_bytes,
+                       int64_t* num_pairs_dev, gf_bin_info* info, void* workspace, size_t workspace_bytes,
                        void* stream, bool force_tiles, const int64_t* kdev) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
@@ -3800,23 +3868,25 @@ static int forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t
     if (!in_render)
       hipLaunchKernelGGL(k_bin_tiles, dim3(lines), dim3(kTilesThreads), 0, st, p, tile_ptr, num_pairs_dev, ws, L,
                          chol_raw, amp);
-    else if (num_pairs_host)
+    else if (info)
       hipLaunchKernelGGL(k_pairs, dim3(1), dim3(kTilesThreads), 0, st, p, num_pairs_dev, ws, L);
   } else {
     hipLaunchKernelGGL(k_bin, dim3(1), dim3(kBinThreads), 0, st, p, mu, chol_raw, tile_ptr,
                        num_pairs_dev, reinterpret_cast<uint8_t*>(workspace), L);
   }
   GF_LAUNCH_CHECK("k_bin");
-  if (num_pairs_host) {
-    // the status word and P sit in the first 24 bytes of the header: one copy into page-locked memory
+  if (info) {
+    // the status word, P and the widest rectangle sit in the first 32 bytes of the header: one
+    // copy into page-locked memory
     void* pinned = nullptr;
     rc = pinned_readback(&pinned);
     if (rc) return rc;
-    GF_HIP_CHECK(hipMemcpyAsync(pinned, workspace, offsetof(WsHeader, pairs) + sizeof(int64_t),
+    GF_HIP_CHECK(hipMemcpyAsync(pinned, workspace, offsetof(WsHeader, max_span) + sizeof(int64_t),
                                 hipMemcpyDeviceToHost, st));
     GF_HIP_CHECK(hipStreamSynchronize(st));
     const WsHeader* h = reinterpret_cast<const WsHeader*>(pinned);
-    *num_pairs_host = h->pairs;
+    info->num_pairs = h->pairs;
+    info->max_span = h->max_span;
     if (h->status & GF_STATUS_COUNT_MISMATCH)
       return set_err(GF_E_INTERNAL, "binning: per-tile counts disagree with per-Gaussian tile totals");
   }
@@ -4050,19 +4120,25 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
 // workgroups, and fewer than 8192 tiles.  The direct gradients have one slot per Gaussian, so a
 // Gaussian's atomics cannot be spread over stripes: on larger grids, whose Gaussians can touch
 // thousands of tiles, it runs the reduction and the finish, which writes the same gradients.
-// (Below 8192 tiles a Gaussian over the whole grid still costs the direct kernel what it cost
-// the one-stripe reduction: 85 us at cfg3's grid.)
-bool direct_one_launch(const Problem& p, int64_t num_pairs) {
+// Below 8192 tiles one wide Gaussian still serialises the direct kernel's atomics on its slot,
+// about 10 ns a tile.  Measured at cfg3's grid with one centred Gaussian of growing rectangle:
+//   tiles of the rectangle    15    256    625    1369   2401   6400
+//   one launch, us            9.3   10.8   15.3   23.7   36.6   85.1
+//   reduction + finish, us    11.7  11.6   11.7   13.8   17.0   27.3
+// so where the binning's widest rectangle is known (gf_bin_info.max_span; negative: not known)
+// one of kDirectMaxSpan tiles or more sends the call to the reduction + finish.
+constexpr int64_t kDirectMaxSpan = 320;
+bool direct_one_launch(const Problem& p, int64_t num_pairs, int64_t max_span) {
   return p.W > 0 && quad_tiles(p) && (int64_t)p.R * p.C < 8192 && !bwd_dense(p, num_pairs) &&
-         heavy_grid(p, num_pairs) == 0;
+         heavy_grid(p, num_pairs) == 0 && max_span < kDirectMaxSpan;
 }
 
 int gf_backward_direct_launches(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                                int64_t num_pairs) {
+                                int64_t num_pairs, int64_t max_span) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return -rc;
-  return direct_one_launch(p, num_pairs) && k > 0 ? 1 : 2;
+  return direct_one_launch(p, num_pairs, max_span) && k > 0 ? 1 : 2;
 }
 
 size_t gf_forward_grads_offset(int64_t out_features, int64_t in_features, int64_t k,
@@ -4075,26 +4151,27 @@ size_t gf_forward_grads_offset(int64_t out_features, int64_t in_features, int64_
 static int backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                            const float* grad_delta, const float* row_coords, const float* col_coords,
                            const float* mu, const float* chol_raw, const float* amp, const int64_t* tile_ptr,
-                           const int64_t* gaussian_ids, int64_t num_pairs, void* forward_workspace,
+                           const int64_t* gaussian_ids, int64_t num_pairs, int64_t max_span, void* forward_workspace,
                            size_t forward_workspace_bytes, void* workspace, size_t workspace_bytes, void* stream,
-                           const int64_t* kdev, const int64_t* pdev);
+                           const int64_t* kdev, const int64_t* pdev, bool* one_launch = nullptr);
 
 int gf_backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                        const float* grad_delta, const float* row_coords, const float* col_coords,
                        const float* mu, const float* chol_raw, const float* amp, const int64_t* tile_ptr,
-                       const int64_t* gaussian_ids, int64_t num_pairs, void* forward_workspace,
+                       const int64_t* gaussian_ids, int64_t num_pairs, int64_t max_span, void* forward_workspace,
                        size_t forward_workspace_bytes, void* workspace, size_t workspace_bytes, void* stream) {
   return backward_direct(cfg, out_features, in_features, k, grad_delta, row_coords, col_coords, mu, chol_raw, amp,
-                         tile_ptr, gaussian_ids, num_pairs, forward_workspace, forward_workspace_bytes, workspace,
-                         workspace_bytes, stream, nullptr, nullptr);
+                         tile_ptr, gaussian_ids, num_pairs, max_span, forward_workspace, forward_workspace_bytes,
+                         workspace, workspace_bytes, stream, nullptr, nullptr);
 }
 
+// one_launch (optional): set to whether the one-launch kernel ran.
 static int backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                            const float* grad_delta, const float* row_coords, const float* col_coords,
                            const float* mu, const float* chol_raw, const float* amp, const int64_t* tile_ptr,
-                           const int64_t* gaussian_ids, int64_t num_pairs, void* forward_workspace,
+                           const int64_t* gaussian_ids, int64_t num_pairs, int64_t max_span, void* forward_workspace,
                            size_t forward_workspace_bytes, void* workspace, size_t workspace_bytes, void* stream,
-                           const int64_t* kdev, const int64_t* pdev) {
+                           const int64_t* kdev, const int64_t* pdev, bool* one_launch) {
   Problem p;
   int rc = make_problem(cfg, out_features, in_features, k, &p);
   if (rc) return rc;
@@ -4106,7 +4183,9 @@ static int backward_direct(const gf_field_config* cfg, int64_t out_features, int
                    forward_workspace_bytes);
   uint8_t* fws = reinterpret_cast<uint8_t*>(forward_workspace);
   float* dg = reinterpret_cast<float*>(fws + FL.dgrad);  // [K][8]: d_amp, d_mu x2, d_chol_raw x3
-  if (!direct_one_launch(p, num_pairs) || k == 0) {
+  const bool direct = direct_one_launch(p, num_pairs, max_span) && k > 0;
+  if (one_launch) *one_launch = direct;
+  if (!direct) {
     rc = backward_reduce(cfg, out_features, in_features, k, grad_delta, row_coords, col_coords, mu, chol_raw,
                          tile_ptr, 1, gaussian_ids, 1, num_pairs, forward_workspace, workspace, workspace_bytes,
                          stream, kdev, pdev);
@@ -4133,6 +4212,43 @@ static int backward_direct(const gf_field_config* cfg, int64_t out_features, int
                                &reinterpret_cast<const WsHeader*>(fws)->heavy,
                                reinterpret_cast<const float4*>(fws + FL.dcoef), dg);
   GF_LAUNCH_CHECK("k_bwd");
+  return GF_OK;
+}
+
+// The training backward: the one-launch kernel where the binning's facts allow it, its
+// gradients then moved out of the slots (k_slots_out), otherwise gf_backward's reduction +
+// finish.  The one-launch kernel reads what the mask-path binning left in forward_workspace (the
+// constants, the chain-rule maps and the cleared slots), so it needs that workspace, int64 saved
+// state, and the widest rectangle known (max_span >= 0).
+int gf_backward_train(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                      const float* grad_delta, const float* row_coords, const float* col_coords, const float* mu,
+                      const float* chol_raw, const float* amp, const void* tile_ptr, int32_t tile_ptr_is_int64,
+                      const void* gaussian_ids, int32_t ids_is_int64, int64_t num_pairs, int64_t max_span,
+                      float* d_mu, float* d_chol_raw, float* d_amp, void* forward_workspace, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  Problem p;
+  int rc = make_problem(cfg, out_features, in_features, k, &p);
+  if (rc) return rc;
+  const bool direct = forward_workspace && tile_ptr_is_int64 == 1 && ids_is_int64 == 1 && max_span >= 0 &&
+                      k > 0 && direct_one_launch(p, num_pairs, max_span);
+  if (!direct)
+    return gf_backward(cfg, out_features, in_features, k, grad_delta, row_coords, col_coords, mu, chol_raw, amp,
+                       tile_ptr, tile_ptr_is_int64, gaussian_ids, ids_is_int64, num_pairs, d_mu, d_chol_raw, d_amp,
+                       forward_workspace, workspace, workspace_bytes, stream);
+  if (!d_mu || !d_chol_raw || !d_amp) return set_err(GF_E_INVALID_ARGUMENT, "d_mu / d_chol_raw / d_amp must not be NULL");
+  const FwdLayout FL = fwd_layout(p);
+  bool one = false;
+  rc = backward_direct(cfg, out_features, in_features, k, grad_delta, row_coords, col_coords, mu, chol_raw, amp,
+                       reinterpret_cast<const int64_t*>(tile_ptr), reinterpret_cast<const int64_t*>(gaussian_ids),
+                       num_pairs, max_span, forward_workspace, FL.total, workspace, workspace_bytes, stream, nullptr,
+                       nullptr, &one);
+  if (rc) return rc;
+  if (!one) return set_err(GF_E_INTERNAL, "gf_backward_train: the one-launch backward was not taken");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  float4* slots = reinterpret_cast<float4*>(reinterpret_cast<uint8_t*>(forward_workspace) + FL.dgrad);
+  hipLaunchKernelGGL(k_slots_out, dim3((unsigned)((k + 255) / 256)), dim3(256), 0, st, slots, k, d_mu, d_chol_raw,
+                     d_amp);
+  GF_LAUNCH_CHECK("k_slots_out");
   return GF_OK;
 }
 
@@ -4177,21 +4293,21 @@ int gf_backward_direct_kcap(const gf_field_config* cfg, int64_t out_features, in
   if (rc) return rc;
   if (!num_pairs_dev) return set_err(GF_E_INVALID_ARGUMENT, "num_pairs_dev must not be NULL");
   return backward_direct(cfg, out_features, in_features, k_capacity, grad_delta, row_coords, col_coords, mu,
-                         chol_raw, amp, tile_ptr, gaussian_ids, ids_capacity, forward_workspace,
+                         chol_raw, amp, tile_ptr, gaussian_ids, ids_capacity, -1, forward_workspace,
                          forward_workspace_bytes, workspace, workspace_bytes, stream, k_dev, num_pairs_dev);
 }
 
 // The one-pass kernel takes the fields gf_backward_direct runs in one launch, with 16x16 tiles and
 // at least one Gaussian.
 bool fused_one_pass(const Problem& p, int64_t pair_bound) {
-  return p.K > 0 && p.tile_out == 16 && p.tile_in == 16 && direct_one_launch(p, pair_bound);
+  return p.K > 0 && p.tile_out == 16 && p.tile_in == 16 && direct_one_launch(p, pair_bound, -1);
 }
 
 int gf_fwd_bwd_fused_supported(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                               int64_t ids_capacity) {
+                               int64_t ids_capacity, int64_t max_span) {
   Problem p;
   if (make_problem(cfg, out_features, in_features, k, &p)) return 0;
-  return fused_one_pass(p, ids_capacity) ? 1 : 0;
+  return fused_one_pass(p, ids_capacity) && max_span < kDirectMaxSpan ? 1 : 0;
 }
 
 int gf_fwd_bwd_fused(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
@@ -4493,6 +4609,22 @@ int gf_backward_noalloc(const gf_field_config* cfg, int64_t out_features, int64_
     hipLaunchKernelGGL(k_copy_status, dim3(1), dim3(64), 0, st, reinterpret_cast<const uint32_t*>(ws), status_dev);
     GF_LAUNCH_CHECK("k_copy_status");
   }
+  return GF_OK;
+}
+
+int gf_read_bin_info(const void* forward_workspace, gf_bin_info* info, void* stream) {
+  if (!forward_workspace || !info)
+    return set_err(GF_E_INVALID_ARGUMENT, "forward_workspace / info must not be NULL");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  void* pinned = nullptr;
+  int rc = pinned_readback(&pinned);
+  if (rc) return rc;
+  GF_HIP_CHECK(hipMemcpyAsync(pinned, forward_workspace, offsetof(WsHeader, max_span) + sizeof(int64_t),
+                              hipMemcpyDeviceToHost, st));
+  GF_HIP_CHECK(hipStreamSynchronize(st));
+  const WsHeader* h = reinterpret_cast<const WsHeader*>(pinned);
+  info->num_pairs = h->pairs;
+  info->max_span = h->max_span;
   return GF_OK;
 }
 

@@ -6,9 +6,14 @@ module (reference ``gaussian_peft/cuda_field/csrc/ext.cpp:9-110``); the work is 
 torch's *current* stream of the input device.
 
 Host synchronisation: the forward reads the pair count P once (as the reference does at
-``forward.cu:48-73``) to size ``gaussian_ids_sorted`` exactly.  The backward reads one status
-word after its kernels to raise the reference's saved-state errors
-(``field_impl.cu:86-108``); set ``VALIDATE_SAVED_STATE = False`` to skip that read.
+``forward.cu:48-73``) to size ``gaussian_ids_sorted`` exactly; the same copy brings back the
+widest Gaussian's tile count.  The backward reads one status word after its kernels to raise
+the reference's saved-state errors (``field_impl.cu:86-108``); set ``VALIDATE_SAVED_STATE =
+False`` to skip that read.
+
+Backward kernels: given the forward workspace (the training Function passes it), int64 saved
+state and no Gaussian over 320 tiles, the backward is the one-launch kernel plus a small kernel
+that moves its gradients out (``gf_backward_train``); otherwise the reduction + finish.
 """
 
 from __future__ import annotations
@@ -163,10 +168,14 @@ def forward_with_workspace(row_coords: Tensor, col_coords: Tensor, mu: Tensor, c
         ws = torch.empty(ws_bytes + 256, dtype=torch.uint8, device=dev)
         ws_ptr = ws.data_ptr()
         tile_ptr = torch.empty(T + 1, dtype=torch.int64, device=dev)
-        P = ctypes.c_int64(0)
-        N.check(L.gf_forward_bin(pcfg, M, Nf, K, N.ptr(mu), N.ptr(chol_raw), N.ptr(amp),
-                                 tile_ptr.data_ptr(), ws_ptr + ws_bytes, ctypes.byref(P),
-                                 ws_ptr, ws_bytes, stream), "gaussian_field_forward (binning)")
+        info = N.GfBinInfo()
+        N.check(L.gf_forward_bin_info(pcfg, M, Nf, K, N.ptr(mu), N.ptr(chol_raw), N.ptr(amp),
+                                      tile_ptr.data_ptr(), ws_ptr + ws_bytes, ctypes.byref(info),
+                                      ws_ptr, ws_bytes, stream), "gaussian_field_forward (binning)")
+        P = ctypes.c_int64(info.num_pairs)
+        # the widest tile rectangle travels with the workspace: it picks the training backward's
+        # kernels (gf_backward_train)
+        ws.gf_max_span = int(info.max_span)
         ids = torch.empty(P.value, dtype=torch.int64, device=dev)
         delta = torch.empty(M * Nf, dtype=torch.float32, device=dev)
         N.check(L.gf_forward_emit(pcfg, M, Nf, K, N.ptr(mu), N.ptr(amp),
@@ -232,21 +241,24 @@ def _backward(grad_delta, row_coords, col_coords, mu, chol_raw, amp, tile_ptr, g
             # zero-filled once; without the status read-back (which clears the status word) a
             # workspace is not reused
             ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
-        fwd_ptr = None
+        fwd_ptr, max_span = None, -1
         if forward_workspace is not None:
             if (forward_workspace.device != dev or forward_workspace.dtype != torch.uint8
                     or forward_workspace.numel() < fwd_bytes):
                 raise RuntimeError("forward_workspace does not belong to this field's forward")
             fwd_ptr = forward_workspace.data_ptr()
+            max_span = int(getattr(forward_workspace, "gf_max_span", -1))
         d_mu = torch.empty(K, 2, dtype=torch.float32, device=dev)
         d_chol_raw = torch.empty(K, 3, dtype=torch.float32, device=dev)
         d_amp = torch.empty(K, 1, dtype=torch.float32, device=dev)
-        N.check(L.gf_backward(ctypes.byref(cfg), M, Nf, K, grad_delta.data_ptr(), row_coords.data_ptr(),
-                              col_coords.data_ptr(), N.ptr(mu), N.ptr(chol_raw), N.ptr(amp),
-                              tile_ptr.data_ptr(), int(tile_ptr.dtype == torch.int64),
-                              N.ptr(gaussian_ids_sorted), int(gaussian_ids_sorted.dtype == torch.int64),
-                              gaussian_ids_sorted.numel(), N.ptr(d_mu), N.ptr(d_chol_raw), N.ptr(d_amp),
-                              fwd_ptr, ws.data_ptr(), ws_bytes, stream), "gaussian_field_backward")
+        # the one-launch kernel where the forward's binning allows it, else reduction + finish
+        N.check(L.gf_backward_train(ctypes.byref(cfg), M, Nf, K, grad_delta.data_ptr(), row_coords.data_ptr(),
+                                    col_coords.data_ptr(), N.ptr(mu), N.ptr(chol_raw), N.ptr(amp),
+                                    tile_ptr.data_ptr(), int(tile_ptr.dtype == torch.int64),
+                                    N.ptr(gaussian_ids_sorted), int(gaussian_ids_sorted.dtype == torch.int64),
+                                    gaussian_ids_sorted.numel(), max_span, N.ptr(d_mu), N.ptr(d_chol_raw),
+                                    N.ptr(d_amp), fwd_ptr, ws.data_ptr(), ws_bytes, stream),
+                "gaussian_field_backward")
         if VALIDATE_SAVED_STATE:
             status = ctypes.c_uint32(0)
             # reads and clears the status word: the workspace is then zero again and kept

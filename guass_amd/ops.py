@@ -166,41 +166,47 @@ class FieldPlan:
         self.backward_reduce(grad, row_coords, col_coords, mu, chol_raw, num_pairs, reuse_forward)
         return self.backward_finish(chol_raw, amp, reuse_forward)
 
-    def backward_direct(self, grad, row_coords, col_coords, mu, chol_raw, amp, num_pairs: int | None = None):
+    def backward_direct(self, grad, row_coords, col_coords, mu, chol_raw, amp, num_pairs: int | None = None,
+                        max_span: int | None = None):
         """The backward in one launch (gf_backward_direct): the chain rule applied per tile with
         the maps the last forward stored, the gradients added into the forward workspace.
         Returns views (d_mu [K,2], d_chol_raw [K,3], d_amp [K,1]) of that workspace, strided over
         one 8-float slot per Gaussian: the next forward on this plan clears them, so copy what
         must outlive it.  The gradients are added into the slots (a second call after the same
         forward doubles them).  Fields where the one-launch kernel does not apply run the
-        reduction and the finish, which adds into the same slots."""
+        reduction and the finish, which adds into the same slots; so do fields whose widest
+        rectangle ``max_span`` (from :meth:`bin_info`; None: not known) covers 320 tiles or more."""
         n = self.capacity if num_pairs is None else int(num_pairs)
+        span = -1 if max_span is None else int(max_span)
         L = N.lib()
         N.check(L.gf_backward_direct(ctypes.byref(self.cfg), self.M, self.N, self.K, grad.data_ptr(),
                                      row_coords.data_ptr(), col_coords.data_ptr(), N.ptr(mu), N.ptr(chol_raw),
-                                     N.ptr(amp), self.tile_ptr.data_ptr(), self.ids.data_ptr(), n,
+                                     N.ptr(amp), self.tile_ptr.data_ptr(), self.ids.data_ptr(), n, span,
                                      self.fwd_ws.data_ptr(), self.fwd_ws_bytes, self.bwd_ws.data_ptr(),
                                      self.bwd_ws_bytes, self._stream()), "gf_backward_direct")
         off = int(L.gf_forward_grads_offset(self.M, self.N, self.K, ctypes.byref(self.cfg)))
         slots = self.fwd_ws[off:off + 32 * self.K].view(torch.float32).view(self.K, 8)
         return slots[:, 1:3], slots[:, 3:6], slots[:, 0:1]
 
-    def fused_supported(self) -> bool:
+    def fused_supported(self, max_span: int | None = None) -> bool:
         """Whether :meth:`fwd_bwd_fused` runs the one-pass kernel for this field at the plan's id
-        capacity (16x16 tiles on the mask path, fewer than 8192 tiles, sparse, no heavy tiles)."""
+        capacity (16x16 tiles on the mask path, fewer than 8192 tiles, sparse, no heavy tiles) and,
+        if given, widest rectangle (an earlier step's :meth:`bin_info`: under 320 tiles)."""
+        span = -1 if max_span is None else int(max_span)
         return bool(N.lib().gf_fwd_bwd_fused_supported(ctypes.byref(self.cfg), self.M, self.N, self.K,
-                                                       self.capacity))
+                                                       self.capacity, span))
 
-    def fwd_bwd_fused(self, row_coords, col_coords, mu, chol_raw, amp, grad, num_pairs: int | None = None):
+    def fwd_bwd_fused(self, row_coords, col_coords, mu, chol_raw, amp, grad, num_pairs: int | None = None,
+                      max_span: int | None = None):
         """Forward and backward with dL/d(delta) given up front (gf_fwd_bwd_fused): the binning,
         then one kernel that renders delta-W and reduces ``grad`` with the same exponentials.
         Returns (delta, (d_mu, d_chol_raw, d_amp)), the gradients as :meth:`backward_direct`
         returns them (views of the forward workspace, added into slots the binning cleared).
-        Fields the one-pass kernel does not take run :meth:`forward` + :meth:`backward_direct`
-        (``num_pairs`` as there)."""
-        if not self.fused_supported():
+        Fields the one-pass kernel does not take (see :meth:`fused_supported`, ``max_span`` as
+        there) run :meth:`forward` + :meth:`backward_direct` (``num_pairs`` as there)."""
+        if not self.fused_supported(max_span):
             self.forward(row_coords, col_coords, mu, chol_raw, amp)
-            grads = self.backward_direct(grad, row_coords, col_coords, mu, chol_raw, amp, num_pairs)
+            grads = self.backward_direct(grad, row_coords, col_coords, mu, chol_raw, amp, num_pairs, max_span)
             return self.delta, grads
         L = N.lib()
         N.check(L.gf_fwd_bwd_fused(ctypes.byref(self.cfg), self.M, self.N, self.K, row_coords.data_ptr(),
@@ -212,11 +218,12 @@ class FieldPlan:
         slots = self.fwd_ws[off:off + 32 * self.K].view(torch.float32).view(self.K, 8)
         return self.delta, (slots[:, 1:3], slots[:, 3:6], slots[:, 0:1])
 
-    def direct_launches(self, num_pairs: int | None = None) -> int:
-        """Launches :meth:`backward_direct` makes for ``num_pairs`` (default: the id capacity):
-        1, or 2 where it runs the reduction and the finish."""
+    def direct_launches(self, num_pairs: int | None = None, max_span: int | None = None) -> int:
+        """Launches :meth:`backward_direct` makes for ``num_pairs`` (default: the id capacity) and
+        ``max_span`` (None: not known): 1, or 2 where it runs the reduction and the finish."""
         n = self.capacity if num_pairs is None else int(num_pairs)
-        r = int(N.lib().gf_backward_direct_launches(ctypes.byref(self.cfg), self.M, self.N, self.K, n))
+        span = -1 if max_span is None else int(max_span)
+        r = int(N.lib().gf_backward_direct_launches(ctypes.byref(self.cfg), self.M, self.N, self.K, n, span))
         if r < 0:
             N.check(-r, "gf_backward_direct_launches")
         return r
@@ -224,6 +231,14 @@ class FieldPlan:
     def pairs(self) -> int:
         """Pair count of the last forward (synchronises)."""
         return int(self.num_pairs.item())
+
+    def bin_info(self) -> tuple[int, int]:
+        """(P, max_span) of the last forward: its pair count and the most tiles one Gaussian's
+        rectangle covers (gf_read_bin_info; synchronises)."""
+        info = N.GfBinInfo()
+        N.check(N.lib().gf_read_bin_info(self.fwd_ws.data_ptr(), ctypes.byref(info), self._stream()),
+                "gf_read_bin_info")
+        return int(info.num_pairs), int(info.max_span)
 
     def status(self, which: str = "forward") -> int:
         """GF_STATUS_* bits of the last forward or backward (synchronises)."""
@@ -495,7 +510,7 @@ class StaticFieldPlan:
     def direct_launches(self) -> int:
         """Launches :meth:`backward_direct` makes (1, or 2 for reduction + finish), the same for every K."""
         r = int(N.lib().gf_backward_direct_launches(ctypes.byref(self.cfg), self.M, self.N, self.k_capacity,
-                                                    self.buffers.capacity))
+                                                    self.buffers.capacity, -1))
         if r < 0:
             N.check(-r, "gf_backward_direct_launches")
         return r

@@ -10,8 +10,8 @@
  * (thread-local).  `stream` is a hipStream_t (NULL = the legacy default stream).
  *
  * Reference interface replaced (Plutohr/GUASS, paths under gaussian_peft/cuda_field):
- *   csrc/ext.cpp:9-37     gaussian_field_forward           -> gf_forward_bin + gf_forward_render
- *   csrc/ext.cpp:38-72    gaussian_field_backward          -> gf_backward
+ *   csrc/ext.cpp:9-37     gaussian_field_forward           -> gf_forward_bin(_info) + gf_forward_render
+ *   csrc/ext.cpp:38-72    gaussian_field_backward          -> gf_backward_train (or gf_backward)
  *   csrc/ext.cpp:73-110   gaussian_field_backward_reference-> gf_backward (same gradients)
  *   csrc/field.h:11-18    ForwardConfig                    -> gf_field_config
  *   csrc/field_impl.cu:52-108 input / saved-state checks   -> GF_E_* codes + device-side checks
@@ -94,6 +94,28 @@ int gf_forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t in_
                    const float* mu, const float* chol_raw, const float* amp,
                    int64_t* tile_ptr, int64_t* num_pairs_dev, int64_t* num_pairs_host,
                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* What the binning learnt of a field, for the host. */
+typedef struct gf_bin_info {
+  int64_t num_pairs; /* P */
+  int64_t max_span;  /* the most tiles one Gaussian's tile rectangle covers (0 for K = 0) */
+} gf_bin_info;
+
+/*
+ * gf_forward_bin with the read-back of P widened to gf_bin_info (the same one synchronisation
+ * and copy).  max_span decides between the one-launch backward and the reduction + finish
+ * (gf_backward_train, gf_backward_direct): one Gaussian over many tiles serialises the one-launch
+ * kernel's atomics on its gradient slot.  info must not be NULL.
+ */
+int gf_forward_bin_info(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                        const float* mu, const float* chol_raw, const float* amp, int64_t* tile_ptr,
+                        int64_t* num_pairs_dev, gf_bin_info* info, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* gf_bin_info of the last forward on a forward workspace (gf_forward, gf_forward_bin + _render,
+ * gf_fwd_bwd_fused, the capacity-mode forward), after that forward in `stream` order:
+ * synchronises `stream`. */
+int gf_read_bin_info(const void* forward_workspace, gf_bin_info* info, void* stream);
 
 /*
  * Forward phase 2 (emission; returns at once on the mask path): writes the (tile, gaussian)
@@ -181,6 +203,25 @@ int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * gf_backward for the training entry (replaces reference backward.cu:541-716, the backward
+ * of runtime.py:107-203's GaussianFieldCudaTrainFunction): the same arguments and outputs,
+ * plus max_span, gf_bin_info.max_span of the forward that filled forward_workspace.  Where that
+ * forward's binning allows it -- forward_workspace given, int64 tile_ptr and ids, max_span known
+ * (>= 0) and below the one-launch limit, and a field gf_backward_direct runs in one launch -- the
+ * gradients come from gf_backward_direct's kernel and one small kernel moves them into d_mu,
+ * d_chol_raw, d_amp and clears the forward workspace's slots, so that a further backward on the
+ * same forward starts from zero.  Otherwise it is gf_backward.  The outputs are written, not
+ * added to, either way; they agree within fp32 rounding.  Two backwards on one forward workspace
+ * must not run concurrently.
+ */
+int gf_backward_train(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
+                      const float* grad_delta, const float* row_coords, const float* col_coords, const float* mu,
+                      const float* chol_raw, const float* amp, const void* tile_ptr, int32_t tile_ptr_is_int64,
+                      const void* gaussian_ids, int32_t ids_is_int64, int64_t num_pairs, int64_t max_span,
+                      float* d_mu, float* d_chol_raw, float* d_amp, void* forward_workspace, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/*
  * gf_backward in one launch where it can (replaces reference backward.cu:541-716 like
  * gf_backward).  The chain rule is linear in the per-tile moments; the forward's first phase
  * (on the mask path) stores each Gaussian's map from moments to gradients, so the reduction
@@ -194,13 +235,17 @@ int gf_backward_finish(const gf_field_config* cfg, int64_t out_features, int64_t
  * config, with its int64 tile_ptr and ids.  Fields off the mask path, dense fields
  * (num_pairs >= 16 T), grids of 8192 tiles or more (whose reduction spreads each Gaussian's
  * atomics over stripes) and fields with heavy-tile workgroups run gf_backward_reduce +
- * gf_backward_finish, whose finish adds into the same slots.  The gradients agree with
- * gf_backward's within fp32 rounding (the map is applied per tile, in fp32).
+ * gf_backward_finish, whose finish adds into the same slots; so do fields whose widest tile
+ * rectangle is known (max_span >= 0, gf_bin_info.max_span of the forward) to cover 320 tiles or
+ * more, where one Gaussian's atomics on its one slot would cost the kernel more than the second
+ * launch (about 10 ns a tile).  max_span < 0: not known (graphs captured before the content is),
+ * the choice is then made on the other conditions alone.  The gradients agree with gf_backward's
+ * within fp32 rounding (the map is applied per tile, in fp32).
  */
 int gf_backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
                        const float* grad_delta, const float* row_coords, const float* col_coords,
                        const float* mu, const float* chol_raw, const float* amp, const int64_t* tile_ptr,
-                       const int64_t* gaussian_ids, int64_t num_pairs, void* forward_workspace,
+                       const int64_t* gaussian_ids, int64_t num_pairs, int64_t max_span, void* forward_workspace,
                        size_t forward_workspace_bytes, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -253,14 +298,18 @@ int gf_fwd_bwd_fused(const gf_field_config* cfg, int64_t out_features, int64_t i
                      int64_t* gaussian_ids_sorted, int64_t ids_capacity, float* delta, void* forward_workspace,
                      size_t forward_workspace_bytes, void* stream);
 
-/* 1 if gf_fwd_bwd_fused takes this field and id capacity, else 0 (also on an invalid configuration). */
+/* 1 if gf_fwd_bwd_fused takes this field and id capacity, else 0 (also on an invalid configuration).
+ * max_span as for gf_backward_direct: the one-pass kernel adds into the same slots, so a known
+ * rectangle of 320 tiles or more (from an earlier step's gf_read_bin_info) answers 0; the call
+ * itself reads nothing back and cannot see the widest rectangle of its own binning. */
 int gf_fwd_bwd_fused_supported(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                               int64_t ids_capacity);
+                               int64_t ids_capacity, int64_t max_span);
 
-/* Kernel launches gf_backward_direct makes for this field and pair count: 1 (the direct
- * kernel) or 2 (reduction + finish); the negated error code on an invalid configuration. */
+/* Kernel launches gf_backward_direct makes for this field, pair count and widest rectangle
+ * (max_span < 0: not known): 1 (the direct kernel) or 2 (reduction + finish); the negated error
+ * code on an invalid configuration. */
 int gf_backward_direct_launches(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
-                                int64_t num_pairs);
+                                int64_t num_pairs, int64_t max_span);
 
 /* Byte offset, in a forward workspace, of gf_backward_direct's gradient slots (K x 8 floats).
  * 0 on an invalid configuration. */

@@ -124,13 +124,21 @@ def test_workspace_and_pointer_checks():
 
 def test_backward_direct_host_logic():
     """gf_backward_direct's host side: the launch count it will make (1 on the mask path with
-    sparse 16x16 / 32x32 tiles and no heavy-tile workgroups, 2 elsewhere), where its gradient
-    slots lie in the forward workspace, and the workspace check before any device work."""
+    sparse 16x16 / 32x32 tiles, no heavy-tile workgroups and no known rectangle of 320 tiles or
+    more, 2 elsewhere), where its gradient slots lie in the forward workspace, and the workspace
+    check before any device work."""
     lib = N.lib()
     cfg = ctypes.byref(_cfg())
 
-    def launches(M, Nf, K, P, c=cfg):
-        return lib.gf_backward_direct_launches(c, M, Nf, K, P)
+    def launches(M, Nf, K, P, c=cfg, span=-1):
+        return lib.gf_backward_direct_launches(c, M, Nf, K, P, span)
+
+    # the widest rectangle: one Gaussian's atomics serialise on its slot
+    assert launches(1280, 1280, 1024, 23618, span=15) == 1
+    assert launches(1280, 1280, 1024, 23618, span=319) == 1
+    assert launches(1280, 1280, 1024, 23618, span=320) == 2
+    assert launches(1280, 1280, 1024, 30003, span=6400) == 2
+    assert launches(1280, 1280, 1024, 30003, span=-1) == 1  # not known: the shape decides
 
     assert launches(1280, 1280, 1024, 23618) == 1          # cfg3
     assert launches(1280, 1280, 1024, 16 * 6400) == 2      # dense tiles: the transposing reduction
@@ -147,11 +155,39 @@ def test_backward_direct_host_logic():
         total = lib.gf_forward_workspace_bytes(M, Nf, K, cfg)
         assert off % 256 == 0 and 256 <= off and off + 32 * K <= total
     need = lib.gf_forward_workspace_bytes(64, 64, 4, cfg)
-    rc = lib.gf_backward_direct(cfg, 64, 64, 4, None, None, None, None, None, None, None, None, 10, None,
+    rc = lib.gf_backward_direct(cfg, 64, 64, 4, None, None, None, None, None, None, None, None, 10, -1, None,
                                 need, None, 0, None)
     assert rc == GF_E_WORKSPACE and "forward workspace" in lib.gf_last_error().decode()
-    rc = lib.gf_backward_direct(cfg, 64, 64, 4, None, None, None, None, None, None, None, None, 10, 256,
+    rc = lib.gf_backward_direct(cfg, 64, 64, 4, None, None, None, None, None, None, None, None, 10, -1, 256,
                                 need - 1, None, 0, None)
+    assert rc == GF_E_WORKSPACE
+
+
+def test_bin_info_and_train_backward_host_checks():
+    """gf_forward_bin_info / gf_read_bin_info refuse NULL outputs, and gf_backward_train checks
+    its field and buffers before any device work on either of its paths (safe without a GPU)."""
+    lib = N.lib()
+    cfg = _cfg()
+    need = lib.gf_forward_workspace_bytes(64, 64, 4, ctypes.byref(cfg))
+    rc = lib.gf_forward_bin_info(ctypes.byref(cfg), 64, 64, 4, None, None, None, None, None, None, None, need, None)
+    assert rc == GF_E_INVALID_ARGUMENT and "info" in lib.gf_last_error().decode()
+    info = N.GfBinInfo()
+    rc = lib.gf_forward_bin_info(ctypes.byref(cfg), 64, 64, 4, None, None, None, None, None, ctypes.byref(info),
+                                 None, need - 1, None)
+    assert rc == GF_E_WORKSPACE
+    assert lib.gf_read_bin_info(None, ctypes.byref(info), None) == GF_E_INVALID_ARGUMENT
+    assert lib.gf_read_bin_info(ctypes.c_void_p(256), None, None) == GF_E_INVALID_ARGUMENT
+    rc = lib.gf_backward_train(ctypes.byref(_cfg(tile_out=0)), 64, 64, 4, None, None, None, None, None, None,
+                               None, 1, None, 1, 10, 15, None, None, None, None, None, 0, None)
+    assert rc == GF_E_INVALID_ARGUMENT and "tile_out must be positive" in lib.gf_last_error().decode()
+    # the one-launch path (mask path, sparse, span known and small) checks its backward workspace
+    d = ctypes.c_void_p(256)  # never dereferenced: the workspace check comes first
+    rc = lib.gf_backward_train(ctypes.byref(cfg), 64, 64, 4, d, d, d, d, d, d, d, 1, d, 1, 10, 15, d, d, d, d,
+                               None, 0, None)
+    assert rc == GF_E_WORKSPACE and "backward workspace" in lib.gf_last_error().decode()
+    # the reduction path (span not known) likewise
+    rc = lib.gf_backward_train(ctypes.byref(cfg), 64, 64, 4, d, d, d, d, d, d, d, 1, d, 1, 10, -1, d, d, d, d,
+                               None, 0, None)
     assert rc == GF_E_WORKSPACE
 
 
@@ -329,8 +365,11 @@ def test_fused_entry_refuses_other_fields_before_device_work():
     GF_E_INVALID_ARGUMENT before any device work (safe without a GPU)."""
     L = N.lib()
     c16, c32 = N.make_config(16, 16, 3.0, False, 80.0), N.make_config(32, 32, 3.0, False, 80.0)
-    ok = lambda cfg, m, n, k, cap: L.gf_fwd_bwd_fused_supported(ctypes.byref(cfg), m, n, k, cap)  # noqa: E731
+    ok = lambda cfg, m, n, k, cap, span=-1: L.gf_fwd_bwd_fused_supported(ctypes.byref(cfg), m, n, k, cap,  # noqa: E731
+                                                                          span)
     assert ok(c16, 1280, 1280, 1024, 24000) == 1
+    assert ok(c16, 1280, 1280, 1024, 24000, 100) == 1
+    assert ok(c16, 1280, 1280, 1024, 24000, 320) == 0       # a known rectangle of 320 tiles or more
     assert ok(c16, 320, 320, 64, 500) == 1
     assert ok(c32, 1280, 1280, 1024, 24000) == 0          # 32x32 tiles
     assert ok(c16, 320, 320, 9000, 9000) == 0             # past the masks: emission path

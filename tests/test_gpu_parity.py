@@ -7,6 +7,7 @@ tests/parity.py.
 
 from __future__ import annotations
 
+import ctypes
 import math
 import warnings
 
@@ -463,6 +464,119 @@ def test_autograd_train_function(device):
         grad_close(amp.grad, r[5], "amp.grad")
 
 
+def _oracle_span(p: wl.FieldProblem, tile_out=16, tile_in=16, sigma=3.0) -> int:
+    """The most tiles one Gaussian's rectangle covers, from the oracle's bounds (bounds.py:24-75)."""
+    if p.k == 0:
+        return 0
+    b = fo.tile_bounds(p.mu, fo.activate_cholesky(p.chol_raw), p.out_features, p.in_features, tile_out, tile_in,
+                       sigma)
+    return int(b.tiles_touched.max())
+
+
+def _wide(p: wl.FieldProblem, n: int) -> wl.FieldProblem:
+    """p with its first n Gaussians spread over the whole grid."""
+    p.chol_raw[:n, 0] = 4.0
+    p.chol_raw[:n, 2] = 4.0
+    return p
+
+
+@pytest.mark.parametrize("case", ["cfg1", "cfg2", "cfg3", "cfg3_wide", "tile32", "emit_k9000", "k0", "ragged"])
+def test_bin_info_matches_oracle(device, case):
+    """gf_bin_info (P and the widest rectangle) from the binning's own read-back
+    (gf_forward_bin_info, the drop-in forward) and from gf_read_bin_info after gf_forward, on
+    each binning path: k_bin_tiles (cfg3, 32x32 tiles), binning in the render (cfg1, cfg2), the
+    emission path (K past the masks) and K = 0: equal to the oracle's pair count and largest
+    tiles_touched."""
+    kw = {}
+    if case == "cfg1":
+        p = wl.cfg1(11)
+    elif case == "cfg2":
+        p = wl.cfg2(11)
+    elif case == "cfg3":
+        p = wl.cfg3(11)
+    elif case == "cfg3_wide":
+        p = _wide(wl.cfg3(11), 1)
+    elif case == "tile32":
+        p, kw = wl.cfg3(12), dict(tile_out=32, tile_in=32)
+    elif case == "emit_k9000":
+        p = wl.make_problem("emit_320_k9000", 320, 320, 9000, math.log(2.0), 0.5, 13)
+    elif case == "k0":
+        p = wl.make_problem("k0_64", 64, 64, 0, 0.0, 0.5, 14)
+    else:
+        p = wl.make_problem("ragged_333x517_k700", 333, 517, 700, math.log(6.0), 0.7, 15)
+    to = kw.get("tile_out", 16)
+    span = _oracle_span(p, to, to)
+    P = int(fo.tile_bounds(p.mu, fo.activate_cholesky(p.chol_raw), p.out_features, p.in_features, to, to,
+                           3.0).tiles_touched.sum()) if p.k else 0
+    say(f"{case}: P={P} max_span={span}")
+    q = p.to(device)
+    plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=max(P, 1), **kw)
+    plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+    assert plan.bin_info() == (P, span)
+    assert plan.status() == 0
+    if p.k:
+        _, tp, _, ws = ext.forward_with_workspace(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, to, to, 3.0,
+                                                  False, 80.0)
+        torch.cuda.synchronize()
+        assert int(tp[-1]) == P and ws.gf_max_span == span
+
+
+@pytest.mark.parametrize("case", ["cfg2", "cfg3", "cfg3_wide", "cfg3_int32"])
+def test_train_backward_paths(device, case):
+    """gaussian_field_train's backward (gf_backward_train): the one-launch kernel + slot move-out
+    where the forward's binning allows it (cfg2 binned in the render, cfg3), the reduction +
+    finish for a Gaussian over the whole grid (6400 tiles) and for int32 saved state.  Each
+    against the oracle; a second backward through the same graph (retain_graph) returns the same
+    gradients, so the move-out left the slots clear; and the gradients agree with the reduction
+    path's (ext backward without the forward workspace) to fp32 rounding."""
+    p = {"cfg2": lambda: wl.cfg2(21), "cfg3": lambda: wl.cfg3(21), "cfg3_wide": lambda: _wide(wl.cfg3(21), 1),
+         "cfg3_int32": lambda: wl.cfg3(21)}[case]()
+    r = oracle(p)
+    P, span = int(r[1][-1]), _oracle_span(p)
+    q = p.to(device)
+    cfg = _native.make_config(16, 16, 3.0, False, 80.0)
+    one = _native.lib().gf_backward_direct_launches(ctypes.byref(cfg), p.out_features, p.in_features, p.k, P,
+                                                    span) == 1
+    say(f"{case}: P={P} max_span={span} field takes the one-launch kernel: {one}")
+    assert one == (case != "cfg3_wide")  # int32 saved state takes gf_backward all the same
+    mu = q.mu.clone().requires_grad_(True)
+    raw = q.chol_raw.clone().requires_grad_(True)
+    amp = q.amp.clone().requires_grad_(True)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        if case == "cfg3_int32":
+            # int32 saved state through the training Function's backward, as the reference permits
+            delta, tp, ids, ws = ext.forward_with_workspace(q.row_coords, q.col_coords, mu, raw, amp, 16, 16, 3.0,
+                                                            False, 80.0)
+            grads = [ext.gaussian_field_backward(q.grad, q.row_coords, q.col_coords, mu.detach(), raw.detach(),
+                                                 amp.detach(), tp.to(torch.int32), ids.to(torch.int32), 16, 16, 3.0,
+                                                 False, 80.0, forward_workspace=ws) for _ in range(2)]
+        else:
+            delta = runtime.gaussian_field_train(row_coords=q.row_coords, col_coords=q.col_coords, mu=mu,
+                                                 chol_raw=raw, amp=amp, tile_out=16, tile_in=16,
+                                                 sigma_multiplier=3.0, normalize=False, clamp_quad=80.0)
+            grads = []
+            for _ in range(2):
+                for t in (mu, raw, amp):
+                    t.grad = None
+                (delta * q.grad).sum().backward(retain_graph=True)
+                grads.append([mu.grad.clone(), raw.grad.clone(), amp.grad.clone()])
+    torch.cuda.synchronize()
+    field_close(delta, r[0])
+    for i, g in enumerate(grads):
+        for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), g, r[3:]):
+            grad_close(a, b, f"{name} (backward {i + 1})")
+    for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), grads[1], grads[0]):
+        grad_close(a, b, f"{name}, second backward vs first", rtol=1e-5)  # float atomics: not bit-equal
+    _, tp, ids, ws = ext.forward_with_workspace(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, 16, 16, 3.0,
+                                                False, 80.0)
+    two = ext.gaussian_field_backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, tp, ids, 16, 16,
+                                      3.0, False, 80.0)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), grads[0], two):
+        grad_close(a, b, f"{name} vs the reduction + finish", rtol=1e-5)
+
+
 def test_stage2_validation_metadata(device):
     p = wl.cfg1(2)
     q = p.to(device)
@@ -690,6 +804,15 @@ def test_backward_direct_hot_gaussians(device, nbig):
         grad_close(a, 2.0 * b, f"{name} after a second backward", rtol=1e-5)
     big = twice[2][:nbig].abs().cpu()
     assert float(big.min()) > 0.0, "hot Gaussians' gradients missing"
+    # with the widest rectangle known (6400 tiles) the call takes the reduction + finish
+    P2, span = plan.bin_info()
+    assert P2 == P and span == 6400 and plan.direct_launches(P, span) == 2
+    plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+    known = plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P,
+                                 max_span=span)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), known, r[3:]):
+        grad_close(a, b, f"{name} (max_span known)")
 
 
 def test_backward_direct_fallbacks(device):
