@@ -91,9 +91,13 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB (the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
-    ap.add_argument("--traffic-file", default=str(ROOT / "profiles" / "cfg3_hbm_traffic.json"),
-                    help="per-kernel HBM bytes per launch measured with rocprofv3 --pmc")
-    return ap.parse_args()
+    ap.add_argument("--traffic-file", default=None,
+                    help="per-kernel HBM bytes per launch measured with rocprofv3 --pmc "
+                         "(default: profiles/<config>_hbm_traffic.json)")
+    args = ap.parse_args()
+    if args.traffic_file is None:
+        args.traffic_file = str(ROOT / "profiles" / f"{args.config}_hbm_traffic.json")
+    return args
 
 
 def algorithmic_counts(tile_ptr, M: int, N: int, K: int, tile_out: int, tile_in: int) -> dict:
