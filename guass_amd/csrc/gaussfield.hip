@@ -2,8 +2,8 @@
 //
 // Forward (reference forward.cu:372-569).  Mask path (16x16 or 32x32 tiles, K <= 8192), three
 // kernels:
-//   k_prep     one thread per Gaussian: bit-exact sigma-box tile rectangle, fp32 covariance
-//              and evaluation constants.
+//   k_prep     four lanes per Gaussian (one thread above 2048 Gaussians): bit-exact sigma-box
+//              tile rectangle, fp32 covariance and evaluation constants.
 //   k_bin_tiles one workgroup per tile row and per tile column, none waiting for another: the
 //              row's or column's bitmask of the Gaussians whose tile range covers it (wave
 //              ballots), and per tile row the tile_ptr of its tiles (a closed-form count of
@@ -934,15 +934,8 @@ __global__ __launch_bounds__(kBinThreads) void k_bin(Problem p, const float* __r
 //   rowbase[r] = sum_g w_g * clamp(r - x_g, 0, h_g)   (g's tiles in rows before r),
 // with the row's counts from a difference array over its columns.  A mask word pair is one
 // wave's ballot over 64 consecutive Gaussians.  k_prep, launched before, stores each
-// Gaussian's rectangle, covariance and evaluation constants (one thread per Gaussian).
+// Gaussian's rectangle, covariance and evaluation constants (four lanes per Gaussian).
 constexpr int kTilesThreads = 256;
-
-struct PrepOut {
-  int4 rect;
-  GfCov cov;
-  float mu0, mu1;
-  float l11, l22;
-};
 
 struct PrepLoad {
   float mu0, mu1, r11, r21, r22;
@@ -951,19 +944,6 @@ struct PrepLoad {
 __device__ inline PrepLoad prep_load(const float* __restrict__ mu, const float* __restrict__ chol_raw,
                                      int64_t g) {
   return PrepLoad{mu[2 * g + 0], mu[2 * g + 1], chol_raw[3 * g + 0], chol_raw[3 * g + 1], chol_raw[3 * g + 2]};
-}
-
-__device__ inline PrepOut prep_rect(const Problem& p, const PrepLoad& in) {
-  PrepOut o;
-  o.mu0 = in.mu0;
-  o.mu1 = in.mu1;
-  const GfChol Lc = gf_activate_cholesky(in.r11, in.r21, in.r22);
-  o.cov = gf_cov_from_chol(Lc);
-  o.l11 = Lc.l11;
-  o.l22 = Lc.l22;
-  int32_t touched;
-  o.rect = bin_rect(p, o.mu0, o.mu1, o.cov, &touched);
-  return o;
 }
 
 // d softplus / dx as torch's softplus backward: x > 20 ? 1 : e^x / (e^x + 1).  In fp32 with the
@@ -1019,46 +999,90 @@ __device__ inline void store_dcoef(const Problem& p, GfCov cov, float l11f, floa
   dg[1] = make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
-__device__ inline void store_prep(const Problem& p, const PrepOut& o, float amp, int64_t g, uint8_t* ws,
-                                  const FwdLayout& L) {
-  reinterpret_cast<int4*>(ws + L.rect)[g] = o.rect;
-  reinterpret_cast<float4*>(ws + L.cov)[g] = make_float4(o.cov.s00, o.cov.s01, o.cov.s11, 0.0f);
-  reinterpret_cast<float2*>(ws + L.lfac)[g] = make_float2(o.l11, o.l22);
-  GaussEval v = eval_from_cov(p, o.mu0, o.mu1, o.cov, amp);
-  v.gid = (int32_t)g;
-  store_eval(reinterpret_cast<GaussEval*>(ws + L.eval), g, v);
+// The Gaussians' rectangles, covariances and evaluation constants.  Up to kPrepSplitMaxK
+// Gaussians, four lanes per Gaussian: the lanes of a pair each take one of the two softplus
+// evaluations of the Cholesky diagonal (the longest part of a Gaussian's preparation: correctly
+// rounded expf and log1pf, in double) and swap the results, and the pairs of waves 0-1 then
+// store the rectangle, covariance and factor (which k_bin_tiles waits for) while those of waves
+// 2-3 compute and store the evaluation constants (which only the render reads), 64 Gaussians a
+// workgroup: the chain each lane runs is about half as long (cfg3's binning: 7.9 -> 7.2 us).
+// Beyond that, one thread per Gaussian (cfg5, K = 4096: the same time either way, and its step
+// measured 1.4 us slower with the split).  Every lane runs the same functions on the same
+// inputs as one thread per Gaussian would, so the results are the same bits.  kCoef (fields
+// binned in the render, K <= 256, no k_bin_tiles launch): workgroups past the preparation's
+// compute the chain-rule maps, a lane pair per Gaussian likewise, beside the others rather than
+// after them on each thread's dependent chain.
+constexpr int64_t kPrepSplitMaxK = 2048;
+constexpr int64_t kCoefPerBlock = kTilesThreads / 2;  // chain-rule maps: two lanes each
+bool prep_split(const Problem& p) { return p.K <= kPrepSplitMaxK; }
+
+// One diagonal entry per lane of a pair (lane parity `half`), swapped: the pair's Cholesky factor.
+__device__ inline GfChol prep_chol_pair(const PrepLoad& in, int half) {
+  const float mine = gf_activate_diag(half ? in.r22 : in.r11);
+  const float other = __int_as_float(__shfl_xor(__float_as_int(mine), 1));
+  GfChol Lc;
+  Lc.l11 = half ? other : mine;
+  Lc.l21 = in.r21;
+  Lc.l22 = half ? mine : other;
+  return Lc;
 }
 
-// One thread per Gaussian: rectangle, covariance and evaluation constants.  kCoef (fields
-// binned in the render, with no k_bin_tiles launch): a second set of ceil(K / 256) workgroups
-// computes the chain-rule maps, each thread recomputing its Gaussian's covariance (the same
-// functions, so the same bits), beside the first set rather than after it on each thread's
-// dependent chain.
-template <bool kCoef>
+// parts: 1 the rectangle, covariance and factor, 2 the evaluation constants.
+__device__ inline void prep_store(const Problem& p, const PrepLoad& in, const GfChol& Lc, const float* __restrict__ amp,
+                                  int64_t g, uint8_t* ws, const FwdLayout& L, int parts) {
+  const GfCov c = gf_cov_from_chol(Lc);
+  if (parts & 1) {
+    int32_t touched;
+    reinterpret_cast<int4*>(ws + L.rect)[g] = bin_rect(p, in.mu0, in.mu1, c, &touched);
+    reinterpret_cast<float4*>(ws + L.cov)[g] = make_float4(c.s00, c.s01, c.s11, 0.0f);
+    reinterpret_cast<float2*>(ws + L.lfac)[g] = make_float2(Lc.l11, Lc.l22);
+  }
+  if (parts & 2) {
+    GaussEval v = eval_from_cov(p, in.mu0, in.mu1, c, amp[g]);
+    v.gid = (int32_t)g;
+    store_eval(reinterpret_cast<GaussEval*>(ws + L.eval), g, v);
+  }
+}
+
+template <bool kCoef, bool kSplit>
 __global__ __launch_bounds__(kTilesThreads) void k_prep(Problem p, const float* __restrict__ mu,
                                                         const float* __restrict__ chol_raw,
                                                         const float* __restrict__ amp, uint8_t* ws,
                                                         FwdLayout L, int64_t* num_pairs) {
-  if (kCoef) {
-    const int64_t nb = (p.K + kTilesThreads - 1) / kTilesThreads;
-    if ((int64_t)blockIdx.x >= nb) {
-      const int64_t g = ((int64_t)blockIdx.x - nb) * kTilesThreads + threadIdx.x;
-      if (g < live_k(p)) {
-        const PrepLoad in = prep_load(mu, chol_raw, g);
-        const GfChol Lc = gf_activate_cholesky(in.r11, in.r21, in.r22);
-        store_dcoef(p, gf_cov_from_chol(Lc), Lc.l11, Lc.l22, in.r11, in.r21, in.r22, amp[g], g, ws, L);
-      }
-      return;
-    }
+  static_assert(kSplit || !kCoef, "the chain-rule workgroups follow the split preparation");
+  constexpr int64_t per = kSplit ? kTilesThreads / 4 : kTilesThreads;  // Gaussians a workgroup
+  const int64_t nbp = (p.K + per - 1) / per;
+  const int64_t K = live_k(p);
+  const int half = threadIdx.x & 1;
+  if (kCoef && (int64_t)blockIdx.x >= nbp) {
+    const int64_t g = ((int64_t)blockIdx.x - nbp) * kCoefPerBlock + (threadIdx.x >> 1);
+    const bool valid = g < K;
+    const PrepLoad in = valid ? prep_load(mu, chol_raw, g) : PrepLoad{0.f, 0.f, 0.f, 0.f, 0.f};
+    const GfChol Lc = prep_chol_pair(in, half);  // every lane takes part in the swap
+    if (valid && !half)
+      store_dcoef(p, gf_cov_from_chol(Lc), Lc.l11, Lc.l22, in.r11, in.r21, in.r22, amp[g], g, ws, L);
+    return;
   }
-  const int64_t g = (int64_t)blockIdx.x * kTilesThreads + threadIdx.x;
-  if (g == 0) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
     WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
     hdr->status = 0u;
     hdr->heavy = 0u;
     hdr->num_pairs = num_pairs;
   }
-  if (g < live_k(p)) store_prep(p, prep_rect(p, prep_load(mu, chol_raw, g)), amp[g], g, ws, L);
+  if constexpr (!kSplit) {  // one thread per Gaussian
+    const int64_t g = (int64_t)blockIdx.x * kTilesThreads + threadIdx.x;
+    if (g < K) {
+      const PrepLoad in = prep_load(mu, chol_raw, g);
+      prep_store(p, in, gf_activate_cholesky(in.r11, in.r21, in.r22), amp, g, ws, L, 3);
+    }
+    return;
+  }
+  const int role = threadIdx.x >> 7;  // wave-uniform: 0 rectangle, 1 evaluation constants
+  const int64_t g = (int64_t)blockIdx.x * per + ((threadIdx.x & 127) >> 1);
+  const bool valid = g < K;
+  const PrepLoad in = valid ? prep_load(mu, chol_raw, g) : PrepLoad{0.f, 0.f, 0.f, 0.f, 0.f};
+  const GfChol Lc = prep_chol_pair(in, half);  // every lane takes part in the swap
+  if (valid && !half) prep_store(p, in, Lc, amp, g, ws, L, role == 0 ? 1 : 2);
 }
 
 __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t* __restrict__ tile_ptr,
@@ -3860,9 +3884,12 @@ static int forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
     const unsigned lines = (unsigned)(p.R + p.C);
     const bool in_render = !force_tiles && tiles_in_render(p);
-    const unsigned nb = (unsigned)((k + kTilesThreads - 1) / kTilesThreads);
-    hipLaunchKernelGGL(in_render ? k_prep<true> : k_prep<false>, dim3(in_render ? 2 * nb : nb), dim3(kTilesThreads), 0,
-                       st, p, mu, chol_raw, amp, ws, L, num_pairs_dev);
+    const bool split = in_render || prep_split(p);  // in_render: K <= 256
+    const int64_t per = split ? kTilesThreads / 4 : kTilesThreads;
+    const unsigned nbp = (unsigned)((k + per - 1) / per);
+    const unsigned nbc = in_render ? (unsigned)((k + kCoefPerBlock - 1) / kCoefPerBlock) : 0u;
+    auto prep = in_render ? k_prep<true, true> : split ? k_prep<false, true> : k_prep<false, false>;
+    hipLaunchKernelGGL(prep, dim3(nbp + nbc), dim3(kTilesThreads), 0, st, p, mu, chol_raw, amp, ws, L, num_pairs_dev);
     GF_LAUNCH_CHECK("k_prep");
     p.heavy = heavy_threshold(p);
     if (!in_render)

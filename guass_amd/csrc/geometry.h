@@ -38,12 +38,17 @@ typedef struct GfRect {
   int64_t r0, r1, c0, c1;  // inclusive tile ranges
 } GfRect;
 
-GF_HD GF_INLINE GfChol gf_activate_cholesky(float raw11, float raw21, float raw22) {
+// One diagonal entry of the Cholesky factor: softplus(raw) + eps, the sum rounded on its own.
+GF_HD GF_INLINE float gf_activate_diag(float raw) {
 #pragma clang fp contract(off)
+  return gf_softplus_torch_cpu(raw) + GF_CHOL_EPS;
+}
+
+GF_HD GF_INLINE GfChol gf_activate_cholesky(float raw11, float raw21, float raw22) {
   GfChol L;
-  L.l11 = gf_softplus_torch_cpu(raw11) + GF_CHOL_EPS;
+  L.l11 = gf_activate_diag(raw11);
   L.l21 = raw21;
-  L.l22 = gf_softplus_torch_cpu(raw22) + GF_CHOL_EPS;
+  L.l22 = gf_activate_diag(raw22);
   return L;
 }
 
