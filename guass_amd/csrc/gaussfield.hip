@@ -3327,9 +3327,10 @@ bool tiles_in_render(const Problem& p) {
 // 67.  Single 16x16 fields on the k_bin_tiles path therefore list the tiles of more than
 // kHeavyTile Gaussians while binning; the render and backward give each listed tile a
 // workgroup of four waves, dispatched before the one-wave-per-tile workgroups, which skip them
-// (heavy_item).  Thresholds 24..64 measured at cfg5 / cfg5c: 32 is best for cfg5 (100 us; 64:
-// 107 us) and within 1.5 us of the best for cfg5c.  K <= kHeavyTile cannot make a heavy tile.
-constexpr int32_t kHeavyTile = 32;
+// (heavy_item).  With the pair render for the light tiles, thresholds 12..64 measured as cfg5 /
+// cfg5c steps: 12: 100.4 / 52.6 us, 16: 85.7 / 52.7, 20: 82.3 / 53.9, 24: 80.6 / 53.7,
+// 32: 81.1 / 55.3, 48: 83.7 / 58.6, 64: 87.6 / 63.6.  K <= kHeavyTile cannot make a heavy tile.
+constexpr int32_t kHeavyTile = 24;
 int32_t heavy_threshold(const Problem& p) {
   return p.W > 0 && p.tile_out == 16 && p.tile_in == 16 && !tiles_in_render(p) && p.K > kHeavyTile
              ? kHeavyTile : 0;

@@ -152,7 +152,10 @@ int gf_forward_render(const gf_field_config* cfg, int64_t out_features, int64_t 
  * The whole forward in one call, without a host synchronisation: gf_forward_bin +
  * gf_forward_emit + gf_forward_render into a gaussian-id buffer of fixed capacity (pairs past it
  * are dropped and GF_STATUS_CAPACITY is set; P goes to num_pairs_dev), for callers that keep
- * their buffers, e.g. under HIP graph capture.  Replaces reference field_impl.cu:135-163
+ * their buffers, e.g. under HIP graph capture.  The capacity also sizes the launch of the
+ * heavy-tile workgroups: past it, on a field with such workgroups, tiles of more than 24
+ * Gaussians beyond the bound are left unrendered.  GF_STATUS_CAPACITY asks for a larger capacity
+ * either way; tile_ptr and P are complete.  Replaces reference field_impl.cu:135-163
  * (gaussian_field_forward, which reads P back to size its id buffer).
  */
 int gf_forward(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,

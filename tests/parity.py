@@ -14,6 +14,11 @@ import torch
 FWD_RTOL = 1e-5
 GRAD_RTOL = 1e-4
 
+# A tile of more than this many Gaussians is a heavy tile (the library's kHeavyTile): where a
+# single field launches heavy-tile workgroups, four waves share such a tile and their partial sums
+# are added in a different order from one wave's.
+HEAVY_TILE = 24
+
 # Order-independent checksum of F.softplus over all 2^32 fp32 inputs, computed from the host C
 # library by oracle/libm_sweep.c; the GPU self-test (gf_selftest_softplus) must reproduce it.
 SOFTPLUS_CHECKSUM = 0x06C0D4E444E1424F

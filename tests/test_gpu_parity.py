@@ -19,7 +19,7 @@ from guass_amd import workloads as wl
 from guass_amd.cuda_field import ext, runtime
 from guass_amd.ops import FieldPlan
 from oracle import field_oracle as fo
-from tests.parity import SOFTPLUS_CHECKSUM, binning_equal, field_close, grad_close
+from tests.parity import HEAVY_TILE, SOFTPLUS_CHECKSUM, binning_equal, field_close, grad_close
 
 pytestmark = pytest.mark.gpu
 
@@ -407,10 +407,17 @@ def test_int32_saved_state(device):
 
 
 @pytest.mark.parametrize("kind", ["last", "order", "negative", "range"])
-def test_saved_state_errors(kind, device):
+@pytest.mark.parametrize("route", ["reduction", "one_launch"])
+def test_saved_state_errors(kind, route, device):
+    """The reference's saved-state errors from the drop-in backward, on both of its routes: without
+    the forward workspace (reduction + finish) and with it (the training Function's route, the
+    one-launch kernel for this small field), the kernels skipping the offending pairs."""
     p = tiny_problem(48, 48, 12, 12).to(device)
-    delta, tp, ids = ext.gaussian_field_forward(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp,
-                                                16, 16, 3.0, False, 80.0)
+    delta, tp, ids, ws = ext.forward_with_workspace(p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp,
+                                                    16, 16, 3.0, False, 80.0)
+    extra = {"forward_workspace": ws} if route == "one_launch" else {}
+    if route == "one_launch":
+        assert 0 <= ws.gf_max_span < 320
     tp, ids = tp.clone(), ids.clone()
     if kind == "last":
         tp[-1] += 1
@@ -428,7 +435,7 @@ def test_saved_state_errors(kind, device):
         msg = "out-of-range"
     with pytest.raises(RuntimeError, match=msg):
         ext.gaussian_field_backward(p.grad, p.row_coords, p.col_coords, p.mu, p.chol_raw, p.amp, tp,
-                                    ids, 16, 16, 3.0, False, 80.0)
+                                    ids, 16, 16, 3.0, False, 80.0, **extra)
     torch.cuda.synchronize()
 
 
@@ -692,13 +699,18 @@ def test_gf_forward_random_fields(device, i):
             eg = float((a.cpu().double() - c).norm()) / cn
             eo = float((o.double() - c).norm()) / cn
             assert eg <= eo + 1e-4, (name, eg, eo)
-    if P > 1:  # an id capacity below the pair count: ids truncated, the rest unchanged
+    if P > 1:  # an id capacity below the pair count: status CAPACITY, tile_ptr and P complete
         small = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=P // 2, **kw)
         small.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
         torch.cuda.synchronize()
         assert small.status() & _native.GF_STATUS_CAPACITY and small.pairs() == P
-        assert torch.equal(small.tile_ptr, one.tile_ptr) and torch.equal(small.delta, one.delta)
-        assert torch.equal(small.ids[:P // 2], one.ids[:P // 2])
+        assert torch.equal(small.tile_ptr, one.tile_ptr)
+        if int((one.tile_ptr[1:] - one.tile_ptr[:-1]).max()) <= HEAVY_TILE:
+            # no heavy tile: both plans render every tile the same way
+            assert torch.equal(small.delta, one.delta)
+            assert torch.equal(small.ids[:P // 2], one.ids[:P // 2])
+        # else the capacity bounds the heavy-tile workgroups too: past it, heavy tiles beyond the
+        # bound may go unrendered (the status bit asks for a larger capacity; tile_ptr and P hold)
 
 
 def _direct_vs_two_launch(plan, q, P, r64=None, r=None):
@@ -962,7 +974,7 @@ def test_batch_tile_pairs_match_single_fields(device):
     indefinite forms, clamps, normalisation, sub-pixel to whole-matrix Gaussians) plus two fields
     on the emission path (K > 8192; odd and even tile columns), against each field's
     single-field run: tile_ptr and ids bit for bit; delta-W bit for bit where no tile holds more
-    than 32 Gaussians (beyond that the single-field render may split a tile over four waves, a
+    than HEAVY_TILE Gaussians (beyond that the single-field render may split a tile over four waves, a
     different fp32 summation order: 1e-6 of the peak); the delta-W norm of the read-back; the
     gradients to 1e-4 of each other, each batch gradient at least as close to the float64
     evaluation as the single field's (+ 1e-5)."""
@@ -994,7 +1006,7 @@ def test_batch_tile_pairs_match_single_fields(device):
             assert torch.equal(pl.tile_ptr, sg[1]), f"{p.name}: tile_ptr"
             assert torch.equal(pl.ids[:P], sg[2]), f"{p.name}: ids"
             odd += (-(-p.in_features // 16)) % 2
-            if int((sg[1][1:] - sg[1][:-1]).max()) <= 32:
+            if int((sg[1][1:] - sg[1][:-1]).max()) <= HEAVY_TILE:
                 exact += 1
                 assert torch.equal(pl.delta.nan_to_num(7.0), sg[0].nan_to_num(7.0)), f"{p.name}: delta"
             else:
@@ -1024,7 +1036,7 @@ def test_batch_tile_pairs_match_single_fields(device):
                     assert eb <= es + 1e-5, (p.name, name, eb, es)
     say(f"  batch gradients at most {worst_gap:.1e} further from float64 than the single fields'")
     say(f"  {exact} of 26 fields bit-equal, {odd} with an odd tile-column count")
-    assert exact >= 20 and odd >= 6
+    assert exact >= 18 and odd >= 6  # 19 of 26 have no tile of more than HEAVY_TILE Gaussians
 
 
 def test_dense_tiles_narrow_gaussians_against_float64(device):
@@ -1243,7 +1255,7 @@ def test_cfg4_full_batch_matches_single_fields(device):
     ext path; reference: each adapted layer renders its own delta-W, gaussian_linear.py:162-220).
     Binning is bit-equal for every layer.  delta-W is bit-equal where the single-field render
     has no heavy-tile workgroups; a field of >= 8 pairs per tile (the 320- and 640-wide layers,
-    12-53 pairs per tile) renders its tiles of more than 32 Gaussians with four waves whose
+    12-53 pairs per tile) renders its tiles of more than HEAVY_TILE Gaussians with four waves whose
     partial sums wave 0 adds, a different fp32 summation order from the batch's one wave per
     tile, so there delta-W agrees to 1e-6 of the field's peak.  Gradients agree to the atomics'
     summation order."""
@@ -1908,7 +1920,7 @@ def _clustered_problem(name, M, N, K, seed, clusters, cluster_sigma_px, log_scal
 
 
 def _heavy_tiles(tile_ptr) -> int:
-    return int(((tile_ptr[1:] - tile_ptr[:-1]) > 32).sum())
+    return int(((tile_ptr[1:] - tile_ptr[:-1]) > HEAVY_TILE).sum())
 
 
 HEAVY_CASES = {
@@ -1928,7 +1940,7 @@ HEAVY_CASES = {
 
 @pytest.mark.parametrize("case", list(HEAVY_CASES))
 def test_heavy_tiles_plan(device, case):
-    """Tiles of more than 32 Gaussians (k_bin_tiles lists them; the render and backward give each
+    """Tiles of more than HEAVY_TILE Gaussians (k_bin_tiles lists them; the render and backward give each
     a workgroup of four waves) through the sync-free plan, against the oracle: binning bit-exact,
     field and gradients at the parity bars."""
     c = dict(HEAVY_CASES[case])
