@@ -9,6 +9,10 @@
 //              ballots), and per tile row the tile_ptr of its tiles (a closed-form count of
 //              the pairs in earlier rows plus a scan of the row's column differences).
 //   k_render16 (below).
+//   Single 16x16 fields of 257..1024 Gaussians skip k_bin_tiles: k_render16x2_rows bins a tile
+//   row per workgroup (the K rectangles tested against the row once, a barrier, the row's
+//   Gaussians listed in LDS in id order, each wave's two tiles taken from that list), and
+//   k_prep also stores the chain-rule maps.  Up to 256 Gaussians each tile's wave bins itself.
 // Emission path, three kernels:
 //   k_bin      one workgroup per field: rectangles, the pair total, per-tile Gaussian counts
 //              from row-wise difference arrays and their scan -> tile_ptr; every scan runs in
@@ -1957,15 +1961,29 @@ __device__ __forceinline__ void render16_body(
 constexpr int32_t kPairInA = 1 << 14, kPairInB = 1 << 15, kPairIdMask = kPairInA - 1;  // ids < kMaskMaxK
 static_assert(kMaskMaxK <= kPairInA, "pair keys hold the id below the tile flags");
 
-template <bool kSkipHalves>
+// A tile row binned by its render workgroup (k_render16x2_rows): the row's Gaussians in
+// ascending id order, each with its first and last tile column, the pairs of the tile rows
+// above, and where the row's segment starts go.
+struct RowBin {
+  const int2* list;          // LDS: (id, first column | last column << 16)
+  int32_t n;                 // entries
+  int64_t base;              // pairs in tile rows 0 .. tr - 1
+  int32_t span;              // the most tiles one rectangle covers (the field's)
+  int64_t* tile_ptr_out;     // tile_ptr, written for the wave's tiles (and [T] by tile T - 1's wave)
+};
+
+template <bool kSkipHalves, bool kRows = false>
 __device__ __forceinline__ void render16x2_body(
     const Problem& p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* __restrict__ ids,
     int64_t capacity, float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
     const uint32_t* __restrict__ colmask, int32_t tr, int32_t tc, float* __restrict__ blk_sq,
-    const MergedOut& mo = MergedOut{nullptr, nullptr, 1.0f}, uint32_t skip = 0u) {
+    const MergedOut& mo = MergedOut{nullptr, nullptr, 1.0f}, uint32_t skip = 0u,
+    const RowBin& rb = RowBin{nullptr, 0, 0, 0, nullptr}) {
   // skip: bit 0 leaves tile A, bit 1 tile B to another workgroup (a heavy tile): no Gaussians,
-  // ids, checks or stores of that tile here
+  // ids, checks or stores of that tile here.  kRows: the segments and the Gaussians come from
+  // the workgroup's row list rb (tile_ptr, rowmask and colmask are not read), and the wave
+  // writes its tiles' segment starts.
   WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
@@ -1997,7 +2015,53 @@ __device__ __forceinline__ void render16x2_body(
   float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
   const bool floor_free = !p.mask_clamp;
   // The two segments are adjacent: [sa, sb) and [sb, se).
-  const int64_t sa = tile_ptr[ta], sb = tile_ptr[ta + 1], se = has_b ? tile_ptr[ta + 2] : sb;
+  int64_t sa, sb, se;
+  int32_t key0 = 0;  // kRows: the first chunk (row entries 0 .. 63)
+  bool keep0 = false;
+  GaussEval pre0 = zero_eval();
+  if constexpr (kRows) {
+    // Segment start of tile A in closed form, the pairs of every Gaussian in earlier tiles
+    // (row-major): the rows above (rb.base) plus clamp(tc - first, 0, width) over the row's
+    // Gaussians; tile B starts after tile A's count.
+    // (32-bit sums: before <= n * C < 2^25, counts <= n <= 1024 in two 16-bit halves).  The
+    // first 64 entries' keys and constants are kept for the first chunk: the constants' gather
+    // overlaps the sums.
+    int32_t before = 0, nab = 0;
+    for (int32_t j = lane; j < rb.n; j += 64) {
+      const int2 e = rb.list[j];
+      const int32_t z = e.y & 0xffff, w = e.y >> 16;
+      const bool ia = z <= tc && tc <= w, ib = has_b && z <= tc + 1 && tc + 1 <= w;
+      before += clamp_i32(tc - z, 0, w - z + 1);
+      nab += (ia ? 1 : 0) + (ib ? 0x10000 : 0);
+      if (j < 64) {
+        keep0 = ia || ib;
+        key0 = e.x | (ia ? kPairInA : 0) | (ib ? kPairInB : 0);
+        if (keep0) pre0 = load_eval(ev, e.x);
+      }
+    }
+    before = __builtin_amdgcn_readlane(dpp_scan_i32(before), 63);
+    nab = __builtin_amdgcn_readlane(dpp_scan_i32(nab), 63);
+    const int32_t na = nab & 0xffff, nb = nab >> 16;
+    sa = rb.base + before;
+    sb = sa + na;
+    se = sb + nb;
+    const int64_t T = (int64_t)p.R * p.C;
+    const int64_t last = has_b ? ta + 1 : ta;
+    if (lane == 0) {
+      rb.tile_ptr_out[ta] = sa;
+      if (has_b) rb.tile_ptr_out[ta + 1] = sb;
+      if (last == T - 1) {
+        rb.tile_ptr_out[T] = se;
+        *hdr->num_pairs = se;
+        hdr->pairs = se;
+        hdr->max_span = rb.span;
+      }
+    }
+  } else {
+    sa = tile_ptr[ta];
+    sb = tile_ptr[ta + 1];
+    se = has_b ? tile_ptr[ta + 2] : sb;
+  }
   const int64_t cnt_a = has_a ? sb - sa : 0, cnt_b = se - sb;
   // ids are written to [s, s + room): none for a segment below the id buffer or reversed
   auto room_of = [&](int64_t s, int64_t count) {
@@ -2005,19 +2069,16 @@ __device__ __forceinline__ void render16x2_body(
   };
   const int64_t room_a = room_of(sa, cnt_a), room_b = room_of(sb, cnt_b);
   if ((sa < 0 || cnt_a < 0 || cnt_b < 0) && lane == 0) set_status(&hdr->status, GF_STATUS_TILE_PTR_ORDER);
-  const uint32_t* rm = rowmask + (int64_t)tr * p.W;
-  const uint32_t* cma = colmask + (int64_t)tc * p.W;
-  const uint32_t* cmb = cma + p.W;  // read only when has_b
   int32_t* keys = r16_wkeys[wid];
   float4* ew = r16_wevals[wid];
 
-  // One chunk of nj <= 64 union Gaussians (key kf in lane j < nj): each tile's ids go to its
-  // segment at the lane's rank among the chunk's keys of that tile; lane j stages Gaussian j
-  // (constants, each tile's amplitude, flags: 1 tile A, 2 tile B, 4 indefinite form) and every
-  // lane adds its 8 pixels.
+  // One chunk of nj <= 64 union Gaussians (key kf in the active lanes, ascending with the lane):
+  // each tile's ids go to its segment at the lane's rank among the chunk's keys of that tile;
+  // the active lane of rank j stages Gaussian j (constants, each tile's amplitude, flags: 1 tile
+  // A, 2 tile B, 4 indefinite form) and every lane adds its 8 pixels.
   int32_t done_a = 0, done_b = 0;  // ids of each tile so far (< K)
-  auto run_chunk = [&](int32_t kf, int nj) {
-    const bool in_a = lane < nj && (kf & kPairInA) != 0, in_b = lane < nj && (kf & kPairInB) != 0;
+  auto run_chunk = [&](int32_t kf, bool active, int nj, const GaussEval* given = nullptr) {
+    const bool in_a = active && (kf & kPairInA) != 0, in_b = active && (kf & kPairInB) != 0;
     const uint64_t bal_a = __builtin_amdgcn_ballot_w64(in_a), bal_b = __builtin_amdgcn_ballot_w64(in_b);
     const int32_t id = kf & kPairIdMask;
     if (in_a) {
@@ -2033,11 +2094,19 @@ __device__ __forceinline__ void render16x2_body(
     done_a += __popcll(bal_a);
     done_b += __popcll(bal_b);
     GaussEval my = zero_eval();
-    if (lane < nj) my = load_eval(ev, id);
+    if (active) my = given ? *given : load_eval(ev, id);
     const int32_t fl = (in_a ? 1 : 0) | (in_b ? 2 : 0) | (my.gen != 0.0f ? 4 : 0);
     // two arrays of 64 float4 (conflict-free writes, broadcast reads)
-    ew[lane] = make_float4(my.mu0, my.mu1, my.wa, my.wb);
-    ew[64 + lane] = make_float4(my.wc, in_a ? my.w : 0.0f, in_b ? my.w : 0.0f, __int_as_float(fl));
+    // (the mask path's active lanes are 0 .. nj - 1, its own ranks)
+    int si = lane;
+    if constexpr (kRows) {
+      const uint64_t bal = __builtin_amdgcn_ballot_w64(active);
+      si = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+    }
+    if (!kRows || active) {
+      ew[si] = make_float4(my.mu0, my.mu1, my.wa, my.wb);
+      ew[64 + si] = make_float4(my.wc, in_a ? my.w : 0.0f, in_b ? my.w : 0.0f, __int_as_float(fl));
+    }
     const bool general = __builtin_amdgcn_ballot_w64((fl & 4) != 0) != 0;
     wave_sync();
     // kSkipHalves (batches): a Gaussian of one tile only (a third of the union at cfg4) skips the
@@ -2101,7 +2170,31 @@ __device__ __forceinline__ void render16x2_body(
     wave_sync();  // every lane has read the slots before the next chunk rewrites them
   };
 
-  for (int32_t w0 = 0; w0 < p.W; w0 += 64) {
+  if constexpr (kRows) {
+    // 64 row Gaussians at a time: those in tile A or B are a chunk, staged in id order
+    {
+      const uint64_t bal = __builtin_amdgcn_ballot_w64(keep0);
+      if (bal != 0ull) run_chunk(key0, keep0, __popcll(bal), &pre0);  // wave-uniform
+    }
+    for (int32_t j0 = 64; j0 < rb.n; j0 += 64) {
+      const int32_t j = j0 + lane;
+      int32_t kf = 0;
+      bool keep = false;
+      if (j < rb.n) {
+        const int2 e = rb.list[j];
+        const int32_t z = e.y & 0xffff, w = e.y >> 16;
+        const bool ia = z <= tc && tc <= w, ib = has_b && z <= tc + 1 && tc + 1 <= w;
+        keep = ia || ib;
+        kf = e.x | (ia ? kPairInA : 0) | (ib ? kPairInB : 0);
+      }
+      const uint64_t bal = __builtin_amdgcn_ballot_w64(keep);
+      if (bal != 0ull) run_chunk(kf, keep, __popcll(bal));  // wave-uniform
+    }
+  }
+  const uint32_t* rm = kRows ? nullptr : rowmask + (int64_t)tr * p.W;
+  const uint32_t* cma = kRows ? nullptr : colmask + (int64_t)tc * p.W;
+  const uint32_t* cmb = kRows ? nullptr : cma + p.W;  // read only when has_b
+  for (int32_t w0 = 0; !kRows && w0 < p.W; w0 += 64) {
     const int32_t w = w0 + lane;
     uint32_t ma = 0u, mb = 0u;
     if (w < p.W) {
@@ -2127,7 +2220,7 @@ __device__ __forceinline__ void render16x2_body(
       const int32_t nwin = min(kWaveSortKeys, tot_u - base);
       for (int32_t j0 = 0; j0 < nwin; j0 += 64) {
         const int nj = min(64, nwin - j0);
-        run_chunk(lane < nj ? keys[j0 + lane] : 0, nj);
+        run_chunk(lane < nj ? keys[j0 + lane] : 0, lane < nj, nj);
       }
       wave_sync();
     }
@@ -2168,6 +2261,92 @@ __global__ __launch_bounds__(kTileThreads) void k_render16x2(
   const int32_t tr = (int32_t)pi / cp, tc = 2 * ((int32_t)pi - tr * cp);
   render16x2_body<false>(p, row_coords, col_coords, ev, tile_ptr, ids, capacity, delta, ws, rowmask, colmask, tr,
                          tc, nullptr);
+}
+
+// Single 16x16 fields of up to kRowsMaxK Gaussians (rows_in_render): the render bins its own
+// tile row, so no k_bin_tiles launch precedes it.  A workgroup takes four tile pairs of one
+// tile row (ceil(ceil(C / 2) / 4) workgroups a row).  Its 256 threads test the K rectangles
+// (four each, loads in flight together) against the row: a ballot per 64 Gaussians gives the
+// row's mask words, and each thread adds the pairs its Gaussians have in the rows above,
+// w * clamp(tr - first row, 0, h).  After a barrier each thread places its row Gaussians in the
+// row list at their rank (the mask words' popcounts before its word, then its lane's rank in
+// the word), with their column ranges; after a second barrier each wave renders its pair from
+// the list (render16x2_body<kRows>), which also gives the segment starts in closed form.
+constexpr int64_t kRowsMaxK = 1024;
+constexpr int kRowsPer = (int)(kRowsMaxK / kTileThreads);  // rectangles a thread
+__global__ __launch_bounds__(kTileThreads) void k_render16x2_rows(
+    Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
+    const GaussEval* __restrict__ ev, int64_t* tile_ptr, int64_t* ids, int64_t capacity,
+    float* __restrict__ delta, uint8_t* ws, const int4* __restrict__ rects) {
+  __shared__ int2 row_list[kRowsMaxK];
+  __shared__ uint64_t row_bits[kRowsMaxK / 64];
+  __shared__ int32_t wave_before[kTileThreads / 64];
+  __shared__ int32_t wave_span[kTileThreads / 64];
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
+  const int32_t cp = (p.C + 1) / 2;
+  const int32_t G = (cp + kTileThreads / 64 - 1) / (kTileThreads / 64);  // workgroups a tile row
+  const int32_t tr = (int32_t)blockIdx.x / G;
+  const int32_t pc = ((int32_t)blockIdx.x - tr * G) * (kTileThreads / 64) + wid;  // the wave's pair
+  const int64_t Kl = live_k(p);
+  int4 rr[kRowsPer];
+#pragma unroll
+  for (int i = 0; i < kRowsPer; ++i) {
+    const int64_t g = (int64_t)kTileThreads * i + threadIdx.x;
+    rr[i] = g < Kl ? rects[g] : make_int4(0, -1, 0, -1);
+  }
+  // (32-bit sums: the pairs of the rows above are at most P <= K * T < 2^31, rows_in_render)
+  int32_t before = 0, span = 0;
+  const bool last_wg = blockIdx.x == gridDim.x - 1;  // tile T - 1's: writes the widest rectangle
+  uint64_t bits[kRowsPer];
+#pragma unroll
+  for (int i = 0; i < kRowsPer; ++i) {
+    const int4 r = rr[i];
+    const bool live = (int64_t)kTileThreads * i + threadIdx.x < Kl;
+    const int32_t h = r.y - r.x + 1, wd = r.w - r.z + 1;
+    const bool in_row = live && r.x <= tr && tr <= r.y;
+    if (live) {
+      before += wd * clamp_i32(tr - r.x, 0, h);
+      if (last_wg) span = max(span, wd * h);
+    }
+    bits[i] = __builtin_amdgcn_ballot_w64(in_row);
+    if (lane == 0) row_bits[i * (kTileThreads / 64) + wid] = bits[i];
+  }
+  before = __builtin_amdgcn_readlane(dpp_scan_i32(before), 63);
+  if (last_wg)
+    for (int off = 32; off > 0; off >>= 1) span = max(span, __shfl_xor(span, off));
+  if (lane == 0) {
+    wave_before[wid] = before;
+    wave_span[wid] = span;
+  }
+  __syncthreads();
+  // Word q = i * 4 + wave holds Gaussians 64 q .. 64 q + 63, so ranks follow ascending ids: lane
+  // q < 16 takes word q's popcount, and an exclusive scan gives each word's first rank.
+  const int32_t cq = lane < kRowsMaxK / 64 ? __popcll(row_bits[lane]) : 0;
+  const int32_t iq = dpp_scan_i32(cq);
+  const int32_t n = __builtin_amdgcn_readlane(iq, kRowsMaxK / 64 - 1);
+#pragma unroll
+  for (int i = 0; i < kRowsPer; ++i) {
+    const int q = i * (kTileThreads / 64) + wid;  // wave-uniform
+    const int32_t first = __builtin_amdgcn_readlane(iq - cq, q);
+    if ((bits[i] >> lane) & 1ull) {
+      const int32_t rank = first + (int32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(bits[i] >> 32),
+                                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)bits[i], 0u));
+      row_list[rank] = make_int2(kTileThreads * i + (int32_t)threadIdx.x, rr[i].z | (rr[i].w << 16));
+    }
+  }
+  int64_t base = 0;
+  int32_t fspan = 0;
+#pragma unroll
+  for (int w = 0; w < kTileThreads / 64; ++w) {
+    base += wave_before[w];
+    fspan = max(fspan, wave_span[w]);
+  }
+  __syncthreads();
+  if (pc >= cp) return;  // past the row's last pair (no barrier follows)
+  const RowBin rb{row_list, n, base, fspan, tile_ptr};
+  render16x2_body<false, true>(p, row_coords, col_coords, ev, nullptr, ids, capacity, delta, ws, nullptr, nullptr,
+                               tr, 2 * pc, nullptr, MergedOut{nullptr, nullptr, 1.0f}, 0u, rb);
 }
 
 // Single 16x16 fields on the mask path with heavy-tile workgroups: the first workgroups take one
@@ -3321,6 +3500,18 @@ bool tiles_in_render(const Problem& p) {
          (int64_t)p.R * p.C * p.K <= kTilesInRenderMaxTests;
 }
 
+// Single 16x16 fields of more Gaussians, up to kRowsMaxK, bin in the pair render a tile row per
+// workgroup (k_render16x2_rows): K rectangle tests per workgroup, shared by its eight tiles,
+// instead of the k_bin_tiles launch.  Column ranges travel as 16-bit halves, and the pair
+// counts the kernel sums (at most K * T) fit 31 bits.
+bool rows_in_render(const Problem& p) {
+  return p.W > 0 && p.tile_out == 16 && p.tile_in == 16 && !tiles_in_render(p) && p.K <= kRowsMaxK &&
+         p.C <= 0x7fff && (int64_t)p.R * p.C * p.K < (int64_t(1) << 31);
+}
+
+// Either form: no k_bin_tiles launch (k_prep stores the chain-rule maps) and no heavy-tile list.
+bool binned_in_render(const Problem& p) { return tiles_in_render(p) || rows_in_render(p); }
+
 // Heavy tiles.  One wave per tile leaves a tile of many Gaussians as the tail of the render
 // and the backward: at cfg5 (clustered, up to 166 Gaussians per tile) the 364 tiles of more
 // than 64 Gaussians, 12% of the pairs, cost the render 12 us of 42 and the backward 19 us of
@@ -3332,7 +3523,7 @@ bool tiles_in_render(const Problem& p) {
 // 32: 81.1 / 55.3, 48: 83.7 / 58.6, 64: 87.6 / 63.6.  K <= kHeavyTile cannot make a heavy tile.
 constexpr int32_t kHeavyTile = 24;
 int32_t heavy_threshold(const Problem& p) {
-  return p.W > 0 && p.tile_out == 16 && p.tile_in == 16 && !tiles_in_render(p) && p.K > kHeavyTile
+  return p.W > 0 && p.tile_out == 16 && p.tile_in == 16 && !binned_in_render(p) && p.K > kHeavyTile
              ? kHeavyTile : 0;
 }
 // The kernels with heavy-tile workgroups (kHeavy) run about 1 us slower than the plain ones
@@ -3884,8 +4075,8 @@ static int forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t
     if (!amp) return set_err(GF_E_INVALID_ARGUMENT, "amp must not be NULL");
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
     const unsigned lines = (unsigned)(p.R + p.C);
-    const bool in_render = !force_tiles && tiles_in_render(p);
-    const bool split = in_render || prep_split(p);  // in_render: K <= 256
+    const bool in_render = !force_tiles && binned_in_render(p);
+    const bool split = in_render || prep_split(p);  // in_render: K <= kRowsMaxK
     const int64_t per = split ? kTilesThreads / 4 : kTilesThreads;
     const unsigned nbp = (unsigned)((k + per - 1) / per);
     const unsigned nbc = in_render ? (unsigned)((k + kCoefPerBlock - 1) / kCoefPerBlock) : 0u;
@@ -3978,6 +4169,14 @@ static int forward_render(const gf_field_config* cfg, int64_t out_features, int6
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
   const GaussEval* ev = reinterpret_cast<const GaussEval*>(ws + L.eval);
   if (quad_render(p)) {
+    if (rows_in_render(p)) {
+      const int32_t cp = (p.C + 1) / 2, G = (cp + kTileThreads / 64 - 1) / (kTileThreads / 64);
+      hipLaunchKernelGGL(k_render16x2_rows, dim3((unsigned)((int64_t)p.R * G)), dim3(kTileThreads), 0, st, p,
+                         row_coords, col_coords, ev, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws,
+                         reinterpret_cast<const int4*>(ws + L.rect));
+      GF_LAUNCH_CHECK("k_render16x2_rows");
+      return GF_OK;
+    }
     const bool binned_here = tiles_in_render(p);
     const int32_t xh = heavy_grid(p, ids_capacity);
     p.heavy = xh > 0 ? kHeavyTile : 0;

@@ -237,10 +237,11 @@ def test_sigma_multiplier_2_5(device):
 
 @pytest.mark.parametrize("shape", [(100, 200), (1250, 700)])
 @pytest.mark.parametrize("tile", [16, 32])
-@pytest.mark.parametrize("k", [1, 31, 32, 33, 63, 64, 65, 127, 129, 257, 1000, 8192])
+@pytest.mark.parametrize("k", [1, 31, 32, 33, 63, 64, 65, 127, 129, 257, 1000, 2048, 2049, 8192])
 def test_mask_path_binning_k_boundaries(device, k, tile, shape):
-    """The mask path's binning at K around the 64-Gaussian ballot groups (a mask word pair each)
-    and at the path's largest K, with Gaussians spanning the whole grid and Gaussians in the
+    """The mask path's binning at K around the 64-Gaussian ballot groups (a mask word pair each),
+    around the preparation's lane split (four lanes per Gaussian up to 2048, one above) and at
+    the path's largest K, with Gaussians spanning the whole grid and Gaussians in the
     last, partial tile row and column.  K <= 256 bins in the render, larger K in k_bin_tiles (a
     workgroup per tile row and column): tile_ptr and ids bit-exact against the oracle's binning
     (bounds.py:24-75, tile_index.py:51-99), delta-W at the field tolerance on the small grid."""
