@@ -2274,20 +2274,22 @@ __global__ __launch_bounds__(kTileThreads) void k_render16x2(
 // the list (render16x2_body<kRows>), which also gives the segment starts in closed form.
 constexpr int64_t kRowsMaxK = 1024;
 constexpr int kRowsPer = (int)(kRowsMaxK / kTileThreads);  // rectangles a thread
-__global__ __launch_bounds__(kTileThreads) void k_render16x2_rows(
-    Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
-    const GaussEval* __restrict__ ev, int64_t* tile_ptr, int64_t* ids, int64_t capacity,
-    float* __restrict__ delta, uint8_t* ws, const int4* __restrict__ rects) {
-  __shared__ int2 row_list[kRowsMaxK];
-  __shared__ uint64_t row_bits[kRowsMaxK / 64];
-  __shared__ int32_t wave_before[kTileThreads / 64];
-  __shared__ int32_t wave_span[kTileThreads / 64];
+
+// LDS of a workgroup's tile-row binning.
+struct RowLds {
+  int2 list[kRowsMaxK];
+  uint64_t bits[kRowsMaxK / 64];
+  int32_t before[kTileThreads / 64];
+  int32_t span[kTileThreads / 64];
+};
+
+// Tile row tr of a field binned by the whole workgroup (every thread calls it; two barriers):
+// the row's Gaussians in rl.list in ascending id order, the pairs of the rows above and, in the
+// grid's last workgroup (which holds tile T - 1), the widest rectangle.
+__device__ inline RowBin bin_tile_row(const Problem& p, const int4* __restrict__ rects, int32_t tr, RowLds& rl,
+                                      int64_t* tile_ptr_out) {
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
-  const int32_t cp = (p.C + 1) / 2;
-  const int32_t G = (cp + kTileThreads / 64 - 1) / (kTileThreads / 64);  // workgroups a tile row
-  const int32_t tr = (int32_t)blockIdx.x / G;
-  const int32_t pc = ((int32_t)blockIdx.x - tr * G) * (kTileThreads / 64) + wid;  // the wave's pair
   const int64_t Kl = live_k(p);
   int4 rr[kRowsPer];
 #pragma unroll
@@ -2310,19 +2312,19 @@ __global__ __launch_bounds__(kTileThreads) void k_render16x2_rows(
       if (last_wg) span = max(span, wd * h);
     }
     bits[i] = __builtin_amdgcn_ballot_w64(in_row);
-    if (lane == 0) row_bits[i * (kTileThreads / 64) + wid] = bits[i];
+    if (lane == 0) rl.bits[i * (kTileThreads / 64) + wid] = bits[i];
   }
   before = __builtin_amdgcn_readlane(dpp_scan_i32(before), 63);
   if (last_wg)
     for (int off = 32; off > 0; off >>= 1) span = max(span, __shfl_xor(span, off));
   if (lane == 0) {
-    wave_before[wid] = before;
-    wave_span[wid] = span;
+    rl.before[wid] = before;
+    rl.span[wid] = span;
   }
   __syncthreads();
   // Word q = i * 4 + wave holds Gaussians 64 q .. 64 q + 63, so ranks follow ascending ids: lane
   // q < 16 takes word q's popcount, and an exclusive scan gives each word's first rank.
-  const int32_t cq = lane < kRowsMaxK / 64 ? __popcll(row_bits[lane]) : 0;
+  const int32_t cq = lane < kRowsMaxK / 64 ? __popcll(rl.bits[lane]) : 0;
   const int32_t iq = dpp_scan_i32(cq);
   const int32_t n = __builtin_amdgcn_readlane(iq, kRowsMaxK / 64 - 1);
 #pragma unroll
@@ -2332,19 +2334,31 @@ __global__ __launch_bounds__(kTileThreads) void k_render16x2_rows(
     if ((bits[i] >> lane) & 1ull) {
       const int32_t rank = first + (int32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(bits[i] >> 32),
                                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)bits[i], 0u));
-      row_list[rank] = make_int2(kTileThreads * i + (int32_t)threadIdx.x, rr[i].z | (rr[i].w << 16));
+      rl.list[rank] = make_int2(kTileThreads * i + (int32_t)threadIdx.x, rr[i].z | (rr[i].w << 16));
     }
   }
   int64_t base = 0;
   int32_t fspan = 0;
 #pragma unroll
   for (int w = 0; w < kTileThreads / 64; ++w) {
-    base += wave_before[w];
-    fspan = max(fspan, wave_span[w]);
+    base += rl.before[w];
+    fspan = max(fspan, rl.span[w]);
   }
   __syncthreads();
+  return RowBin{rl.list, n, base, fspan, tile_ptr_out};
+}
+
+__global__ __launch_bounds__(kTileThreads) void k_render16x2_rows(
+    Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
+    const GaussEval* __restrict__ ev, int64_t* tile_ptr, int64_t* ids, int64_t capacity,
+    float* __restrict__ delta, uint8_t* ws, const int4* __restrict__ rects) {
+  __shared__ RowLds rl;
+  const int32_t cp = (p.C + 1) / 2;
+  const int32_t G = (cp + kTileThreads / 64 - 1) / (kTileThreads / 64);  // workgroups a tile row
+  const int32_t tr = (int32_t)blockIdx.x / G;
+  const int32_t pc = ((int32_t)blockIdx.x - tr * G) * (kTileThreads / 64) + wave_id();  // the wave's pair
+  const RowBin rb = bin_tile_row(p, rects, tr, rl, tile_ptr);
   if (pc >= cp) return;  // past the row's last pair (no barrier follows)
-  const RowBin rb{row_list, n, base, fspan, tile_ptr};
   render16x2_body<false, true>(p, row_coords, col_coords, ev, nullptr, ids, capacity, delta, ws, nullptr, nullptr,
                                tr, 2 * pc, nullptr, MergedOut{nullptr, nullptr, 1.0f}, 0u, rb);
 }
@@ -2951,13 +2965,17 @@ __device__ inline float swap16_add(float a, float b) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <bool kMaskClamp>
+// kRows (rows_in_render fields): a workgroup takes four tiles of one tile row (ceil(C / 4)
+// workgroups a row), bins that row first (bin_tile_row: no k_bin_tiles launch, k_prep stores the
+// chain-rule maps and clears the slots) and writes its tiles' tile_ptr entries; each wave takes
+// its tile's Gaussians from the row list.
+template <bool kMaskClamp, bool kRows = false>
 __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_fused16(
     Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr,
     int64_t* __restrict__ ids, int64_t capacity, float* __restrict__ delta, uint8_t* fws,
     const uint32_t* __restrict__ rowmask, const uint32_t* __restrict__ colmask, const float4* __restrict__ dcoef,
-    float* __restrict__ dgrad) {
+    float* __restrict__ dgrad, const int4* __restrict__ rects = nullptr, int64_t* tile_ptr_out = nullptr) {
   constexpr int kGs = 20;  // row stride (floats) of the staged dL/d(delta) tile: conflict-free float4 reads
   __shared__ float gstage[kTileThreads / 64][16 * kGs];
   __shared__ int32_t fkeys[kTileThreads / 64][kFusedKeys];
@@ -2966,12 +2984,29 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
   WsHeader* hdr = reinterpret_cast<WsHeader*>(fws);
   const int lane = threadIdx.x & 63;
   const int wid = wave_id();
-  const SubTile st = sub_tile(p, blockIdx.x, wid);
   const int64_t T = (int64_t)p.R * p.C;
-  const int64_t t = st.t;
-  if (t >= T) return;
-  const int32_t r0 = st.r0, c0 = st.c0;
-  const int32_t tr = (int32_t)(t / p.C), tc = (int32_t)(t - (int64_t)tr * p.C);
+  int64_t t;
+  int32_t r0, c0, tr, tc;
+  RowBin rb{nullptr, 0, 0, 0, nullptr};
+  if constexpr (kRows) {
+    __shared__ RowLds rl;
+    const int32_t G4 = (p.C + kTileThreads / 64 - 1) / (kTileThreads / 64);  // workgroups a tile row
+    tr = (int32_t)blockIdx.x / G4;
+    tc = ((int32_t)blockIdx.x - tr * G4) * (kTileThreads / 64) + wid;
+    rb = bin_tile_row(p, rects, tr, rl, tile_ptr_out);
+    if (tc >= p.C) return;  // past the row's last tile (no barrier follows)
+    t = (int64_t)tr * p.C + tc;
+    r0 = tr * 16;
+    c0 = tc * 16;
+  } else {
+    const SubTile st = sub_tile(p, blockIdx.x, wid);
+    t = st.t;
+    if (t >= T) return;
+    r0 = st.r0;
+    c0 = st.c0;
+    tr = (int32_t)(t / p.C);
+    tc = (int32_t)(t - (int64_t)tr * p.C);
+  }
   const int slot = lane >> 4, row = lane & 15;
   float* gt = gstage[wid];
   float yv[16];
@@ -3014,7 +3049,40 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
 #pragma unroll
   for (int c = 0; c < 16; ++c) yv[c] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(yv[c])));
   const float x = row_coords[min(r0 + row, p.M - 1)];
-  const int64_t s = tile_ptr[t], count = tile_ptr[t + 1] - s;
+  int64_t s, count;
+  int32_t key0 = 0;  // kRows: the first 64 row entries' keys and constants
+  bool keep0 = false;
+  GaussEval pre0 = zero_eval();
+  if constexpr (kRows) {
+    // the tile's segment start in closed form (as render16x2_body<kRows>) and its count
+    int32_t before = 0, cnt = 0;
+    for (int32_t j = lane; j < rb.n; j += 64) {
+      const int2 e = rb.list[j];
+      const int32_t z = e.y & 0xffff, w = e.y >> 16;
+      const bool in = z <= tc && tc <= w;
+      before += clamp_i32(tc - z, 0, w - z + 1);
+      cnt += in ? 1 : 0;
+      if (j < 64) {
+        keep0 = in;
+        key0 = e.x;
+        if (in) pre0 = load_eval(ev, e.x);
+      }
+    }
+    s = rb.base + __builtin_amdgcn_readlane(dpp_scan_i32(before), 63);
+    count = __builtin_amdgcn_readlane(dpp_scan_i32(cnt), 63);
+    if (lane == 0) {
+      rb.tile_ptr_out[t] = s;
+      if (t == T - 1) {
+        rb.tile_ptr_out[T] = s + count;
+        *hdr->num_pairs = s + count;
+        hdr->pairs = s + count;
+        hdr->max_span = rb.span;
+      }
+    }
+  } else {
+    s = tile_ptr[t];
+    count = tile_ptr[t + 1] - s;
+  }
   // ids are written to [s, s + room): none for a segment below the id buffer or reversed
   const int64_t room = s < 0 ? 0 : capacity - s < count ? (capacity - s > 0 ? capacity - s : 0) : count;
   if ((s < 0 || count < 0) && lane == 0) set_status(&hdr->status, GF_STATUS_TILE_PTR_ORDER);
@@ -3144,11 +3212,43 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
     }
   };
 
-  const uint32_t* rm = rowmask + (int64_t)tr * p.W;
-  const uint32_t* cm = colmask + (int64_t)tc * p.W;
-  int32_t* keys = fkeys[wid];
   int64_t done = 0;
-  for (int32_t w0 = 0; w0 < p.W; w0 += 64) {
+  if constexpr (kRows) {
+    // 64 row entries at a time: the tile's Gaussians among them are a chunk, in id order
+    for (int32_t j0 = 0; j0 < rb.n; j0 += 64) {
+      int32_t g = key0;
+      bool in = keep0;
+      GaussEval my = pre0;
+      if (j0 > 0) {
+        in = false;
+        if (j0 + lane < rb.n) {
+          const int2 e = rb.list[j0 + lane];
+          const int32_t z = e.y & 0xffff, w = e.y >> 16;
+          in = z <= tc && tc <= w;
+          g = e.x;
+          if (in) my = load_eval(ev, g);
+        }
+      }
+      const uint64_t bal = __builtin_amdgcn_ballot_w64(in);
+      if (bal == 0ull) continue;  // wave-uniform
+      const int nj = __popcll(bal);
+      if (in) {
+        const int r = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        if (done + r < room) ids[s + done + r] = g;
+        ew[r] = make_float4(my.mu0, my.mu1, my.wa, my.wb);
+        ew[64 + r] = make_float4(my.wc, my.w, __int_as_float(g), my.gen);
+      }
+      const bool chunk_general = __builtin_amdgcn_ballot_w64(in && my.gen != 0.0f) != 0;
+      wave_sync();
+      run_chunk(nj, chunk_general);
+      wave_sync();  // every lane has read the chunk before the next one is staged
+      done += nj;
+    }
+  }
+  const uint32_t* rm = kRows ? nullptr : rowmask + (int64_t)tr * p.W;
+  const uint32_t* cm = kRows ? nullptr : colmask + (int64_t)tc * p.W;
+  int32_t* keys = fkeys[wid];
+  for (int32_t w0 = 0; !kRows && w0 < p.W; w0 += 64) {
     const int32_t w = w0 + lane;
     const uint32_t m = w < p.W ? (rm[w] & cm[w]) : 0u;
     const int32_t cnt = __popc(m);
@@ -4559,19 +4659,25 @@ int gf_fwd_bwd_fused(const gf_field_config* cfg, int64_t out_features, int64_t i
     return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / ids_capacity invalid");
   if ((uint64_t)k * 8 >= (uint64_t)UINT32_MAX)
     return set_err(GF_E_INVALID_ARGUMENT, "k = %lld is too large for the direct gradients", (long long)k);
+  // Fields whose render bins its tile rows (rows_in_render) bin them in the fused kernel too;
+  // the others (the per-tile in-render form included) take k_bin_tiles' masks.
+  const bool rows = rows_in_render(p);
   rc = forward_bin(cfg, out_features, in_features, k, mu, chol_raw, amp, tile_ptr, num_pairs_dev, nullptr,
-                   forward_workspace, forward_workspace_bytes, stream, true);
+                   forward_workspace, forward_workspace_bytes, stream, !rows);
   if (rc) return rc;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* fws = reinterpret_cast<uint8_t*>(forward_workspace);
   p.heavy = 0;
-  const dim3 grid((unsigned)quad_grid(p));
-  auto kern = p.mask_clamp ? k_fused16<true> : k_fused16<false>;
+  const dim3 grid(rows ? (unsigned)((int64_t)p.R * ((p.C + kTileThreads / 64 - 1) / (kTileThreads / 64)))
+                       : (unsigned)quad_grid(p));
+  auto kern = rows ? (p.mask_clamp ? k_fused16<true, true> : k_fused16<false, true>)
+                   : (p.mask_clamp ? k_fused16<true, false> : k_fused16<false, false>);
   hipLaunchKernelGGL(kern, grid, dim3(kTileThreads), 0, st, p, grad_delta, row_coords, col_coords,
                      reinterpret_cast<const GaussEval*>(fws + FL.eval), tile_ptr, gaussian_ids_sorted, ids_capacity,
                      delta, fws, reinterpret_cast<const uint32_t*>(fws + FL.rowmask),
                      reinterpret_cast<const uint32_t*>(fws + FL.colmask), reinterpret_cast<const float4*>(fws + FL.dcoef),
-                     reinterpret_cast<float*>(fws + FL.dgrad));
+                     reinterpret_cast<float*>(fws + FL.dgrad), rows ? reinterpret_cast<const int4*>(fws + FL.rect) : nullptr,
+                     rows ? tile_ptr : nullptr);
   GF_LAUNCH_CHECK("k_fused16");
   return GF_OK;
 }
