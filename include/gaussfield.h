@@ -138,8 +138,10 @@ int gf_forward_emit(const gf_field_config* cfg, int64_t out_features, int64_t in
  * delta-W from the Gaussian constants stored by gf_forward_emit (or, on the mask path,
  * gf_forward_bin, in which case the render writes the ids itself from the masks).  Must follow
  * gf_forward_emit on the same stream with the same workspace and ids.
- *   tile_ptr        [T+1] int64, from gf_forward_bin; written here instead on the mask path with
- *                   k <= 256 and k * T <= 2^23 (with P to gf_forward_bin's num_pairs_dev)
+ *   tile_ptr        [T+1] int64, from gf_forward_bin; written here instead where the render
+ *                   bins the tiles itself (with P to gf_forward_bin's num_pairs_dev): the mask
+ *                   path with k <= 256 and k * T <= 2^23, and single 16x16 fields with
+ *                   k <= 1024, C < 2^15 and k * T < 2^31 (a workgroup per tile row)
  *   delta           [out_features*in_features] fp32 out, row-major; every element written
  * Replaces reference forward.cu:513-569 (tile_accumulate_kernel; delta needs no pre-zeroing).
  */
