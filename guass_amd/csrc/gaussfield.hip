@@ -1644,6 +1644,11 @@ __device__ inline SubTile sub_tile(const Problem& p, int64_t idx, int wave) {
 // one kernel share one allocation: per wave, sort / expansion keys and a chunk's constants.
 __shared__ int32_t r16_wkeys[kTileThreads / 64][kWaveSortKeys];
 __shared__ float4 r16_wevals[kTileThreads / 64][128];
+// The row-binned render's workgroups of kRowsThreads threads (a chunk's constants per wave):
+// eight tile pairs share each row binning (cfg3's step 19.8 -> 19.6 us against four; sixteen
+// took 20.1 us).
+constexpr int kRowsThreads = 512;
+__shared__ float4 r16_rows_wevals[kRowsThreads / 64][128];
 
 __device__ __forceinline__ void render16_body(
     const Problem& p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
@@ -2069,8 +2074,8 @@ __device__ __forceinline__ void render16x2_body(
   };
   const int64_t room_a = room_of(sa, cnt_a), room_b = room_of(sb, cnt_b);
   if ((sa < 0 || cnt_a < 0 || cnt_b < 0) && lane == 0) set_status(&hdr->status, GF_STATUS_TILE_PTR_ORDER);
-  int32_t* keys = r16_wkeys[wid];
-  float4* ew = r16_wevals[wid];
+  int32_t* keys = r16_wkeys[kRows ? 0 : wid];  // (not used by kRows)
+  float4* ew = kRows ? r16_rows_wevals[wid] : r16_wevals[wid];
 
   // One chunk of nj <= 64 union Gaussians (key kf in the active lanes, ascending with the lane):
   // each tile's ids go to its segment at the lane's rank among the chunk's keys of that tile;
@@ -2264,37 +2269,39 @@ __global__ __launch_bounds__(kTileThreads) void k_render16x2(
 }
 
 // Single 16x16 fields of up to kRowsMaxK Gaussians (rows_in_render): the render bins its own
-// tile row, so no k_bin_tiles launch precedes it.  A workgroup takes four tile pairs of one
-// tile row (ceil(ceil(C / 2) / 4) workgroups a row).  Its 256 threads test the K rectangles
-// (four each, loads in flight together) against the row: a ballot per 64 Gaussians gives the
+// tile row, so no k_bin_tiles launch precedes it.  A workgroup takes eight tile pairs of one
+// tile row (ceil(ceil(C / 2) / 8) workgroups a row).  Its 512 threads test the K rectangles
+// (two each, loads in flight together) against the row: a ballot per 64 Gaussians gives the
 // row's mask words, and each thread adds the pairs its Gaussians have in the rows above,
 // w * clamp(tr - first row, 0, h).  After a barrier each thread places its row Gaussians in the
 // row list at their rank (the mask words' popcounts before its word, then its lane's rank in
 // the word), with their column ranges; after a second barrier each wave renders its pair from
 // the list (render16x2_body<kRows>), which also gives the segment starts in closed form.
 constexpr int64_t kRowsMaxK = 1024;
-constexpr int kRowsPer = (int)(kRowsMaxK / kTileThreads);  // rectangles a thread
 
-// LDS of a workgroup's tile-row binning.
+// LDS of a workgroup's tile-row binning (up to kRowsThreads / 64 waves).
 struct RowLds {
   int2 list[kRowsMaxK];
   uint64_t bits[kRowsMaxK / 64];
-  int32_t before[kTileThreads / 64];
-  int32_t span[kTileThreads / 64];
+  int32_t before[kRowsThreads / 64];
+  int32_t span[kRowsThreads / 64];
 };
 
 // Tile row tr of a field binned by the whole workgroup (every thread calls it; two barriers):
 // the row's Gaussians in rl.list in ascending id order, the pairs of the rows above and, in the
 // grid's last workgroup (which holds tile T - 1), the widest rectangle.
+template <int kThreads>
 __device__ inline RowBin bin_tile_row(const Problem& p, const int4* __restrict__ rects, int32_t tr, RowLds& rl,
                                       int64_t* tile_ptr_out) {
+  constexpr int kRowsPer = (int)(kRowsMaxK / kThreads);  // rectangles a thread
+  constexpr int kWaves = kThreads / 64;
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane((int32_t)(threadIdx.x >> 6));
   const int64_t Kl = live_k(p);
   int4 rr[kRowsPer];
 #pragma unroll
   for (int i = 0; i < kRowsPer; ++i) {
-    const int64_t g = (int64_t)kTileThreads * i + threadIdx.x;
+    const int64_t g = (int64_t)kThreads * i + threadIdx.x;
     rr[i] = g < Kl ? rects[g] : make_int4(0, -1, 0, -1);
   }
   // (32-bit sums: the pairs of the rows above are at most P <= K * T < 2^31, rows_in_render)
@@ -2304,7 +2311,7 @@ __device__ inline RowBin bin_tile_row(const Problem& p, const int4* __restrict__
 #pragma unroll
   for (int i = 0; i < kRowsPer; ++i) {
     const int4 r = rr[i];
-    const bool live = (int64_t)kTileThreads * i + threadIdx.x < Kl;
+    const bool live = (int64_t)kThreads * i + threadIdx.x < Kl;
     const int32_t h = r.y - r.x + 1, wd = r.w - r.z + 1;
     const bool in_row = live && r.x <= tr && tr <= r.y;
     if (live) {
@@ -2312,7 +2319,7 @@ __device__ inline RowBin bin_tile_row(const Problem& p, const int4* __restrict__
       if (last_wg) span = max(span, wd * h);
     }
     bits[i] = __builtin_amdgcn_ballot_w64(in_row);
-    if (lane == 0) rl.bits[i * (kTileThreads / 64) + wid] = bits[i];
+    if (lane == 0) rl.bits[i * kWaves + wid] = bits[i];
   }
   before = __builtin_amdgcn_readlane(dpp_scan_i32(before), 63);
   if (last_wg)
@@ -2329,18 +2336,18 @@ __device__ inline RowBin bin_tile_row(const Problem& p, const int4* __restrict__
   const int32_t n = __builtin_amdgcn_readlane(iq, kRowsMaxK / 64 - 1);
 #pragma unroll
   for (int i = 0; i < kRowsPer; ++i) {
-    const int q = i * (kTileThreads / 64) + wid;  // wave-uniform
+    const int q = i * kWaves + wid;  // wave-uniform
     const int32_t first = __builtin_amdgcn_readlane(iq - cq, q);
     if ((bits[i] >> lane) & 1ull) {
       const int32_t rank = first + (int32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(bits[i] >> 32),
                                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)bits[i], 0u));
-      rl.list[rank] = make_int2(kTileThreads * i + (int32_t)threadIdx.x, rr[i].z | (rr[i].w << 16));
+      rl.list[rank] = make_int2(kThreads * i + (int32_t)threadIdx.x, rr[i].z | (rr[i].w << 16));
     }
   }
   int64_t base = 0;
   int32_t fspan = 0;
 #pragma unroll
-  for (int w = 0; w < kTileThreads / 64; ++w) {
+  for (int w = 0; w < kWaves; ++w) {
     base += rl.before[w];
     fspan = max(fspan, rl.span[w]);
   }
@@ -2348,16 +2355,17 @@ __device__ inline RowBin bin_tile_row(const Problem& p, const int4* __restrict__
   return RowBin{rl.list, n, base, fspan, tile_ptr_out};
 }
 
-__global__ __launch_bounds__(kTileThreads) void k_render16x2_rows(
+__global__ __launch_bounds__(kRowsThreads) void k_render16x2_rows(
     Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, int64_t* tile_ptr, int64_t* ids, int64_t capacity,
     float* __restrict__ delta, uint8_t* ws, const int4* __restrict__ rects) {
   __shared__ RowLds rl;
+  constexpr int kWaves = kRowsThreads / 64;
   const int32_t cp = (p.C + 1) / 2;
-  const int32_t G = (cp + kTileThreads / 64 - 1) / (kTileThreads / 64);  // workgroups a tile row
+  const int32_t G = (cp + kWaves - 1) / kWaves;  // workgroups a tile row
   const int32_t tr = (int32_t)blockIdx.x / G;
-  const int32_t pc = ((int32_t)blockIdx.x - tr * G) * (kTileThreads / 64) + wave_id();  // the wave's pair
-  const RowBin rb = bin_tile_row(p, rects, tr, rl, tile_ptr);
+  const int32_t pc = ((int32_t)blockIdx.x - tr * G) * kWaves + wave_id();  // the wave's pair
+  const RowBin rb = bin_tile_row<kRowsThreads>(p, rects, tr, rl, tile_ptr);
   if (pc >= cp) return;  // past the row's last pair (no barrier follows)
   render16x2_body<false, true>(p, row_coords, col_coords, ev, nullptr, ids, capacity, delta, ws, nullptr, nullptr,
                                tr, 2 * pc, nullptr, MergedOut{nullptr, nullptr, 1.0f}, 0u, rb);
@@ -2993,7 +3001,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
     const int32_t G4 = (p.C + kTileThreads / 64 - 1) / (kTileThreads / 64);  // workgroups a tile row
     tr = (int32_t)blockIdx.x / G4;
     tc = ((int32_t)blockIdx.x - tr * G4) * (kTileThreads / 64) + wid;
-    rb = bin_tile_row(p, rects, tr, rl, tile_ptr_out);
+    rb = bin_tile_row<kTileThreads>(p, rects, tr, rl, tile_ptr_out);
     if (tc >= p.C) return;  // past the row's last tile (no barrier follows)
     t = (int64_t)tr * p.C + tc;
     r0 = tr * 16;
@@ -4270,8 +4278,8 @@ static int forward_render(const gf_field_config* cfg, int64_t out_features, int6
   const GaussEval* ev = reinterpret_cast<const GaussEval*>(ws + L.eval);
   if (quad_render(p)) {
     if (rows_in_render(p)) {
-      const int32_t cp = (p.C + 1) / 2, G = (cp + kTileThreads / 64 - 1) / (kTileThreads / 64);
-      hipLaunchKernelGGL(k_render16x2_rows, dim3((unsigned)((int64_t)p.R * G)), dim3(kTileThreads), 0, st, p,
+      const int32_t cp = (p.C + 1) / 2, G = (cp + kRowsThreads / 64 - 1) / (kRowsThreads / 64);
+      hipLaunchKernelGGL(k_render16x2_rows, dim3((unsigned)((int64_t)p.R * G)), dim3(kRowsThreads), 0, st, p,
                          row_coords, col_coords, ev, tile_ptr, gaussian_ids_sorted, ids_capacity, delta, ws,
                          reinterpret_cast<const int4*>(ws + L.rect));
       GF_LAUNCH_CHECK("k_render16x2_rows");
