@@ -2973,22 +2973,23 @@ __device__ inline float swap16_add(float a, float b) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// kRows (rows_in_render fields): a workgroup takes four tiles of one tile row (ceil(C / 4)
-// workgroups a row), bins that row first (bin_tile_row: no k_bin_tiles launch, k_prep stores the
-// chain-rule maps and clears the slots) and writes its tiles' tile_ptr entries; each wave takes
-// its tile's Gaussians from the row list.
+// kRows (rows_in_render fields): a workgroup of kRowsThreads takes eight tiles of one tile row
+// (ceil(C / 8) workgroups a row), bins that row first (bin_tile_row: no k_bin_tiles launch,
+// k_prep stores the chain-rule maps and clears the slots) and writes its tiles' tile_ptr
+// entries; each wave takes its tile's Gaussians from the row list.
 template <bool kMaskClamp, bool kRows = false>
-__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_fused16(
+__global__ __launch_bounds__(kRows ? kRowsThreads : kTileThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_fused16(
     Problem p, const float* __restrict__ grad, const float* __restrict__ row_coords,
     const float* __restrict__ col_coords, const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr,
     int64_t* __restrict__ ids, int64_t capacity, float* __restrict__ delta, uint8_t* fws,
     const uint32_t* __restrict__ rowmask, const uint32_t* __restrict__ colmask, const float4* __restrict__ dcoef,
     float* __restrict__ dgrad, const int4* __restrict__ rects = nullptr, int64_t* tile_ptr_out = nullptr) {
   constexpr int kGs = 20;  // row stride (floats) of the staged dL/d(delta) tile: conflict-free float4 reads
-  __shared__ float gstage[kTileThreads / 64][16 * kGs];
-  __shared__ int32_t fkeys[kTileThreads / 64][kFusedKeys];
+  constexpr int kThreads = kRows ? kRowsThreads : kTileThreads, kWaves = kThreads / 64;
+  __shared__ float gstage[kWaves][16 * kGs];
+  __shared__ int32_t fkeys[kTileThreads / 64][kFusedKeys];  // (not used by kRows)
   // per wave: a chunk's constants, Gaussian j in [j] (mu0, mu1, wa, wb) and [64 + j] (wc, w, id, gen)
-  __shared__ float4 fevals[kTileThreads / 64][128];
+  __shared__ float4 fevals[kWaves][128];
   WsHeader* hdr = reinterpret_cast<WsHeader*>(fws);
   const int lane = threadIdx.x & 63;
   const int wid = wave_id();
@@ -2998,10 +2999,10 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
   RowBin rb{nullptr, 0, 0, 0, nullptr};
   if constexpr (kRows) {
     __shared__ RowLds rl;
-    const int32_t G4 = (p.C + kTileThreads / 64 - 1) / (kTileThreads / 64);  // workgroups a tile row
-    tr = (int32_t)blockIdx.x / G4;
-    tc = ((int32_t)blockIdx.x - tr * G4) * (kTileThreads / 64) + wid;
-    rb = bin_tile_row<kTileThreads>(p, rects, tr, rl, tile_ptr_out);
+    const int32_t G = (p.C + kWaves - 1) / kWaves;  // workgroups a tile row
+    tr = (int32_t)blockIdx.x / G;
+    tc = ((int32_t)blockIdx.x - tr * G) * kWaves + wid;
+    rb = bin_tile_row<kThreads>(p, rects, tr, rl, tile_ptr_out);
     if (tc >= p.C) return;  // past the row's last tile (no barrier follows)
     t = (int64_t)tr * p.C + tc;
     r0 = tr * 16;
@@ -3255,7 +3256,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(7)
   }
   const uint32_t* rm = kRows ? nullptr : rowmask + (int64_t)tr * p.W;
   const uint32_t* cm = kRows ? nullptr : colmask + (int64_t)tc * p.W;
-  int32_t* keys = fkeys[wid];
+  int32_t* keys = fkeys[kRows ? 0 : wid];
   for (int32_t w0 = 0; !kRows && w0 < p.W; w0 += 64) {
     const int32_t w = w0 + lane;
     const uint32_t m = w < p.W ? (rm[w] & cm[w]) : 0u;
@@ -4676,11 +4677,11 @@ int gf_fwd_bwd_fused(const gf_field_config* cfg, int64_t out_features, int64_t i
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* fws = reinterpret_cast<uint8_t*>(forward_workspace);
   p.heavy = 0;
-  const dim3 grid(rows ? (unsigned)((int64_t)p.R * ((p.C + kTileThreads / 64 - 1) / (kTileThreads / 64)))
+  const dim3 grid(rows ? (unsigned)((int64_t)p.R * ((p.C + kRowsThreads / 64 - 1) / (kRowsThreads / 64)))
                        : (unsigned)quad_grid(p));
   auto kern = rows ? (p.mask_clamp ? k_fused16<true, true> : k_fused16<false, true>)
                    : (p.mask_clamp ? k_fused16<true, false> : k_fused16<false, false>);
-  hipLaunchKernelGGL(kern, grid, dim3(kTileThreads), 0, st, p, grad_delta, row_coords, col_coords,
+  hipLaunchKernelGGL(kern, grid, dim3(rows ? kRowsThreads : kTileThreads), 0, st, p, grad_delta, row_coords, col_coords,
                      reinterpret_cast<const GaussEval*>(fws + FL.eval), tile_ptr, gaussian_ids_sorted, ids_capacity,
                      delta, fws, reinterpret_cast<const uint32_t*>(fws + FL.rowmask),
                      reinterpret_cast<const uint32_t*>(fws + FL.colmask), reinterpret_cast<const float4*>(fws + FL.dcoef),
