@@ -80,8 +80,10 @@ size_t gf_forward_workspace_bytes_max(int64_t out_features, int64_t in_features,
  * Gaussian counts and their exclusive scan.  For 16x16 or 32x32 tiles with 1 <= k <= 8192 (the
  * mask path) it also stores every Gaussian's evaluation constants and, per tile row and tile
  * column, a bitmask of the Gaussians whose tile range covers it; the render then reads each
- * tile's ids from those masks and gf_forward_emit has nothing to do.  On the mask path with
- * k <= 256 (and k * T <= 2^23) the render bins each tile itself: tile_ptr and num_pairs_dev are then written by
+ * tile's ids from those masks and gf_forward_emit has nothing to do.  Where the render bins the
+ * tiles itself -- the mask path with k <= 256 (and k * T <= 2^23), each tile by its wave, and
+ * single 16x16 fields with k <= 1024 (C < 2^15, k * T < 2^31), each tile row by a render
+ * workgroup -- no masks are stored, and tile_ptr and num_pairs_dev are written by
  * gf_forward_render (num_pairs_dev here too when num_pairs_host is given).
  *   amp             [K,1] fp32 (read on the mask path; may be NULL otherwise)
  *   tile_ptr        [T+1] int64 out: tile t owns gaussian_ids_sorted[tile_ptr[t] : tile_ptr[t+1]]
