@@ -3609,14 +3609,19 @@ bool tiles_in_render(const Problem& p) {
          (int64_t)p.R * p.C * p.K <= kTilesInRenderMaxTests;
 }
 
-// Single 16x16 fields of more Gaussians, up to kRowsMaxK, bin in the pair render a tile row per
-// workgroup (k_render16x2_rows): K rectangle tests per workgroup, shared by its eight tiles,
-// instead of the k_bin_tiles launch.  Column ranges travel as 16-bit halves, and the pair
-// counts the kernel sums (at most K * T) fit 31 bits.
-bool rows_in_render(const Problem& p) {
-  return p.W > 0 && p.tile_out == 16 && p.tile_in == 16 && !tiles_in_render(p) && p.K <= kRowsMaxK &&
-         p.C <= 0x7fff && (int64_t)p.R * p.C * p.K < (int64_t(1) << 31);
+// The limits of the row binning (bin_tile_row): single 16x16 fields on the mask path of at most
+// kRowsMaxK Gaussians; column ranges travel as 16-bit halves, and the pair counts it sums (at
+// most K * T) fit 31 bits.
+bool rows_fit(const Problem& p) {
+  return p.W > 0 && p.tile_out == 16 && p.tile_in == 16 && p.K <= kRowsMaxK && p.C <= 0x7fff &&
+         (int64_t)p.R * p.C * p.K < (int64_t(1) << 31);
 }
+
+// Single 16x16 fields of more Gaussians, up to kRowsMaxK, bin in the pair render a tile row per
+// workgroup (k_render16x2_rows): K rectangle tests per workgroup, shared by its sixteen tiles,
+// instead of the k_bin_tiles launch.  (Up to 256 the per-tile form above renders faster: cfg2
+// 14.05 against 14.17 us per step.)
+bool rows_in_render(const Problem& p) { return rows_fit(p) && !tiles_in_render(p); }
 
 // Either form: no k_bin_tiles launch (k_prep stores the chain-rule maps) and no heavy-tile list.
 bool binned_in_render(const Problem& p) { return tiles_in_render(p) || rows_in_render(p); }
@@ -4668,9 +4673,10 @@ int gf_fwd_bwd_fused(const gf_field_config* cfg, int64_t out_features, int64_t i
     return set_err(GF_E_INVALID_ARGUMENT, "gaussian_ids_sorted / ids_capacity invalid");
   if ((uint64_t)k * 8 >= (uint64_t)UINT32_MAX)
     return set_err(GF_E_INVALID_ARGUMENT, "k = %lld is too large for the direct gradients", (long long)k);
-  // Fields whose render bins its tile rows (rows_in_render) bin them in the fused kernel too;
-  // the others (the per-tile in-render form included) take k_bin_tiles' masks.
-  const bool rows = rows_in_render(p);
+  // Fields within the row binning's limits (rows_fit) bin their tile rows in the fused kernel,
+  // those of up to 256 Gaussians included (cfg1 11.0 -> 8.3 us, cfg2 13.0 -> 10.4 us against
+  // k_bin_tiles' masks); the others take k_bin_tiles' masks.
+  const bool rows = rows_fit(p);
   rc = forward_bin(cfg, out_features, in_features, k, mu, chol_raw, amp, tile_ptr, num_pairs_dev, nullptr,
                    forward_workspace, forward_workspace_bytes, stream, !rows);
   if (rc) return rc;
