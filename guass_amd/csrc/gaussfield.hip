@@ -168,7 +168,11 @@ struct WsHeader {
   int64_t pairs;       // forward: P as the binning computed it, beside the status word, so that
                        // one 32-byte copy reads both back (gf_forward_bin's num_pairs_host)
   int64_t max_span;    // forward: the most tiles one Gaussian's rectangle covers (gf_bin_info)
-  uint32_t pad[56];
+  // forward, tiles binned in the render: per k_prep workgroup, the pairs of its Gaussians and
+  // its widest rectangle, which the host read-back after the binning sums (gf_forward_bin's
+  // num_pairs_host, gf_forward_bin_info) in the same copy as the status word
+  int32_t part[16][2];
+  uint32_t pad[24];
 };
 static_assert(sizeof(WsHeader) == 256, "workspace header must be 256 bytes");
 
@@ -1032,11 +1036,13 @@ __device__ inline GfChol prep_chol_pair(const PrepLoad& in, int half) {
 }
 
 // parts: 1 the rectangle, covariance and factor, 2 the evaluation constants.
-__device__ inline void prep_store(const Problem& p, const PrepLoad& in, const GfChol& Lc, const float* __restrict__ amp,
-                                  int64_t g, uint8_t* ws, const FwdLayout& L, int parts) {
+// Returns the tiles the rectangle covers (parts & 1; else 0).
+__device__ inline int32_t prep_store(const Problem& p, const PrepLoad& in, const GfChol& Lc,
+                                     const float* __restrict__ amp, int64_t g, uint8_t* ws, const FwdLayout& L,
+                                     int parts) {
   const GfCov c = gf_cov_from_chol(Lc);
+  int32_t touched = 0;
   if (parts & 1) {
-    int32_t touched;
     reinterpret_cast<int4*>(ws + L.rect)[g] = bin_rect(p, in.mu0, in.mu1, c, &touched);
     reinterpret_cast<float4*>(ws + L.cov)[g] = make_float4(c.s00, c.s01, c.s11, 0.0f);
     reinterpret_cast<float2*>(ws + L.lfac)[g] = make_float2(Lc.l11, Lc.l22);
@@ -1046,7 +1052,12 @@ __device__ inline void prep_store(const Problem& p, const PrepLoad& in, const Gf
     v.gid = (int32_t)g;
     store_eval(reinterpret_cast<GaussEval*>(ws + L.eval), g, v);
   }
+  return touched;
 }
+
+// kCoef (tiles binned in the render) has at most kRowsMaxK / 64 preparation workgroups, one
+// WsHeader::part entry each.
+static_assert(1024 / 64 <= 16, "a part entry per preparation workgroup");
 
 template <bool kCoef, bool kSplit>
 __global__ __launch_bounds__(kTilesThreads) void k_prep(Problem p, const float* __restrict__ mu,
@@ -1086,7 +1097,33 @@ __global__ __launch_bounds__(kTilesThreads) void k_prep(Problem p, const float* 
   const bool valid = g < K;
   const PrepLoad in = valid ? prep_load(mu, chol_raw, g) : PrepLoad{0.f, 0.f, 0.f, 0.f, 0.f};
   const GfChol Lc = prep_chol_pair(in, half);  // every lane takes part in the swap
-  if (valid && !half) prep_store(p, in, Lc, amp, g, ws, L, role == 0 ? 1 : 2);
+  int32_t touched = 0;
+  if (valid && !half) touched = prep_store(p, in, Lc, amp, g, ws, L, role == 0 ? 1 : 2);
+  if constexpr (kCoef) {
+    // the workgroup's pairs and widest rectangle for the host read-back (the pairs of a
+    // workgroup are at most K * T < 2^31 where the render bins the tiles)
+    __shared__ int32_t part_sum[kTilesThreads / 64], part_max[kTilesThreads / 64];
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int32_t sum = __builtin_amdgcn_readlane(dpp_scan_i32(touched), 63);
+    int32_t most = touched;
+    for (int off = 32; off > 0; off >>= 1) most = max(most, __shfl_xor(most, off));
+    if (lane == 0) {
+      part_sum[wid] = sum;
+      part_max[wid] = most;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int32_t ps = 0, pm = 0;
+#pragma unroll
+      for (int w = 0; w < kTilesThreads / 64; ++w) {
+        ps += part_sum[w];
+        pm = max(pm, part_max[w]);
+      }
+      WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
+      hdr->part[blockIdx.x][0] = ps;
+      hdr->part[blockIdx.x][1] = pm;
+    }
+  }
 }
 
 __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t* __restrict__ tile_ptr,
@@ -1224,34 +1261,6 @@ __global__ __launch_bounds__(kTilesThreads) void k_bin_tiles(Problem p, int64_t*
     for (int w = 0; w < kWaves; ++w) most = max(most, wspan[w]);
     reinterpret_cast<WsHeader*>(ws)->max_span = most;
     reinterpret_cast<WsHeader*>(ws)->status = P == total ? 0u : GF_STATUS_COUNT_MISMATCH;
-  }
-}
-
-// P = sum_g h_g * w_g from the stored rectangles, for a host read-back right after binning
-// when the render bins the tiles (tiles_in_render).
-__global__ __launch_bounds__(kTilesThreads) void k_pairs(Problem p, int64_t* __restrict__ num_pairs,
-                                                         uint8_t* __restrict__ ws, FwdLayout L) {
-  __shared__ int64_t scan_lds[kTilesThreads / 64 + 1];
-  const int4* __restrict__ rect = reinterpret_cast<const int4*>(ws + L.rect);
-  __shared__ int32_t span_lds;
-  int64_t s = 0;
-  int32_t span = 0;
-  const int64_t K = live_k(p);
-  if (threadIdx.x == 0) span_lds = 0;
-  for (int64_t g = threadIdx.x; g < K; g += kTilesThreads) {
-    const int4 r = rect[g];
-    const int32_t n = (r.y - r.x + 1) * (r.w - r.z + 1);
-    s += n;
-    span = max(span, n);
-  }
-  int64_t total;
-  (void)block_exclusive_scan<kTilesThreads>(s, &total, scan_lds);  // its barriers order span_lds's
-  atomicMax(&span_lds, span);                                      // initialisation before these
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    *num_pairs = total;
-    reinterpret_cast<WsHeader*>(ws)->pairs = total;
-    reinterpret_cast<WsHeader*>(ws)->max_span = span_lds;
   }
 }
 
@@ -4185,6 +4194,7 @@ static int forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t
   if (!tile_ptr || !num_pairs_dev) return set_err(GF_E_INVALID_ARGUMENT, "tile_ptr / num_pairs_dev must not be NULL");
   if (k > 0 && (!mu || !chol_raw)) return set_err(GF_E_INVALID_ARGUMENT, "mu / chol_raw must not be NULL");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  unsigned parts = 0;  // WsHeader::part entries that hold P (tiles binned in the render)
   if (p.W > 0) {
     if (!amp) return set_err(GF_E_INVALID_ARGUMENT, "amp must not be NULL");
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
@@ -4197,29 +4207,39 @@ static int forward_bin(const gf_field_config* cfg, int64_t out_features, int64_t
     auto prep = in_render ? k_prep<true, true> : split ? k_prep<false, true> : k_prep<false, false>;
     hipLaunchKernelGGL(prep, dim3(nbp + nbc), dim3(kTilesThreads), 0, st, p, mu, chol_raw, amp, ws, L, num_pairs_dev);
     GF_LAUNCH_CHECK("k_prep");
+    if (in_render) parts = nbp;
     p.heavy = heavy_threshold(p);
     if (!in_render)
       hipLaunchKernelGGL(k_bin_tiles, dim3(lines), dim3(kTilesThreads), 0, st, p, tile_ptr, num_pairs_dev, ws, L,
                          chol_raw, amp);
-    else if (info)
-      hipLaunchKernelGGL(k_pairs, dim3(1), dim3(kTilesThreads), 0, st, p, num_pairs_dev, ws, L);
   } else {
     hipLaunchKernelGGL(k_bin, dim3(1), dim3(kBinThreads), 0, st, p, mu, chol_raw, tile_ptr,
                        num_pairs_dev, reinterpret_cast<uint8_t*>(workspace), L);
   }
   GF_LAUNCH_CHECK("k_bin");
   if (info) {
-    // the status word, P and the widest rectangle sit in the first 32 bytes of the header: one
-    // copy into page-locked memory
+    // the status word, P and the widest rectangle sit in the first 32 bytes of the header (or
+    // P in the preparation workgroups' part entries after them, where the render bins the
+    // tiles): one copy into page-locked memory
     void* pinned = nullptr;
     rc = pinned_readback(&pinned);
     if (rc) return rc;
-    GF_HIP_CHECK(hipMemcpyAsync(pinned, workspace, offsetof(WsHeader, max_span) + sizeof(int64_t),
-                                hipMemcpyDeviceToHost, st));
+    const size_t bytes = parts ? offsetof(WsHeader, pad) : offsetof(WsHeader, max_span) + sizeof(int64_t);
+    GF_HIP_CHECK(hipMemcpyAsync(pinned, workspace, bytes, hipMemcpyDeviceToHost, st));
     GF_HIP_CHECK(hipStreamSynchronize(st));
     const WsHeader* h = reinterpret_cast<const WsHeader*>(pinned);
-    info->num_pairs = h->pairs;
-    info->max_span = h->max_span;
+    if (parts) {
+      int64_t P = 0, span = 0;
+      for (unsigned b = 0; b < parts; ++b) {
+        P += h->part[b][0];
+        span = std::max<int64_t>(span, h->part[b][1]);
+      }
+      info->num_pairs = P;
+      info->max_span = span;
+    } else {
+      info->num_pairs = h->pairs;
+      info->max_span = h->max_span;
+    }
     if (h->status & GF_STATUS_COUNT_MISMATCH)
       return set_err(GF_E_INTERNAL, "binning: per-tile counts disagree with per-Gaussian tile totals");
   }

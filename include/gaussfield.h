@@ -84,7 +84,8 @@ size_t gf_forward_workspace_bytes_max(int64_t out_features, int64_t in_features,
  * tiles itself -- the mask path with k <= 256 (and k * T <= 2^23), each tile by its wave, and
  * single 16x16 fields with k <= 1024 (C < 2^15, k * T < 2^31), each tile row by a render
  * workgroup -- no masks are stored, and tile_ptr and num_pairs_dev are written by
- * gf_forward_render (num_pairs_dev here too when num_pairs_host is given).
+ * gf_forward_render (num_pairs_host, when given, is still P, summed on the host from
+ * per-workgroup counts in the workspace header).
  *   amp             [K,1] fp32 (read on the mask path; may be NULL otherwise)
  *   tile_ptr        [T+1] int64 out: tile t owns gaussian_ids_sorted[tile_ptr[t] : tile_ptr[t+1]]
  *   num_pairs_dev   [1] int64 out: P = tile_ptr[T] = sum over Gaussians of tiles touched
