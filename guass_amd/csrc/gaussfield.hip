@@ -5004,12 +5004,13 @@ int gf_read_status(void* workspace, int32_t clear, uint32_t* status_host, void* 
   int rc = pinned_readback(&pinned);
   if (rc) return rc;
   GF_HIP_CHECK(hipMemcpyAsync(pinned, &hdr->status, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-  if (clear) {  // after the copy in stream order: one synchronisation for both
+  GF_HIP_CHECK(hipStreamSynchronize(st));
+  const uint32_t v = *reinterpret_cast<const uint32_t*>(pinned);
+  *status_host = v;
+  if (clear && v != 0u) {  // a clean word (the usual case) needs no clearing launch
     hipLaunchKernelGGL(k_clear_status, dim3(1), dim3(64), 0, st, &hdr->status);
     GF_LAUNCH_CHECK("k_clear_status");
   }
-  GF_HIP_CHECK(hipStreamSynchronize(st));
-  *status_host = *reinterpret_cast<const uint32_t*>(pinned);
   return GF_OK;
 }
 

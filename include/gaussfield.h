@@ -459,7 +459,9 @@ int gf_backward_noalloc(const gf_field_config* cfg, int64_t out_features, int64_
 
 /*
  * Reads (and, if clear != 0, resets) the device status word of a workspace produced by the
- * calls above.  Synchronises `stream`.  *status_host receives GF_STATUS_* bits.
+ * calls above.  Synchronises `stream` for the read; a reset (needed only when a bit is set) is
+ * queued on `stream` after it, ahead of any later work there.  *status_host receives
+ * GF_STATUS_* bits.
  */
 int gf_read_status(void* workspace, int32_t clear, uint32_t* status_host, void* stream);
 
