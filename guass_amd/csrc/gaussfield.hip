@@ -2277,15 +2277,7 @@ __global__ __launch_bounds__(kTileThreads) void k_render16x2(
                          tc, nullptr);
 }
 
-// Single 16x16 fields of up to kRowsMaxK Gaussians (rows_in_render): the render bins its own
-// tile row, so no k_bin_tiles launch precedes it.  A workgroup takes eight tile pairs of one
-// tile row (ceil(ceil(C / 2) / 8) workgroups a row).  Its 512 threads test the K rectangles
-// (two each, loads in flight together) against the row: a ballot per 64 Gaussians gives the
-// row's mask words, and each thread adds the pairs its Gaussians have in the rows above,
-// w * clamp(tr - first row, 0, h).  After a barrier each thread places its row Gaussians in the
-// row list at their rank (the mask words' popcounts before its word, then its lane's rank in
-// the word), with their column ranges; after a second barrier each wave renders its pair from
-// the list (render16x2_body<kRows>), which also gives the segment starts in closed form.
+// The row binning (bin_tile_row) lists at most kRowsMaxK Gaussians a tile row.
 constexpr int64_t kRowsMaxK = 1024;
 
 // LDS of a workgroup's tile-row binning (up to kRowsThreads / 64 waves).
@@ -2313,7 +2305,7 @@ __device__ inline RowBin bin_tile_row(const Problem& p, const int4* __restrict__
     const int64_t g = (int64_t)kThreads * i + threadIdx.x;
     rr[i] = g < Kl ? rects[g] : make_int4(0, -1, 0, -1);
   }
-  // (32-bit sums: the pairs of the rows above are at most P <= K * T < 2^31, rows_in_render)
+  // (32-bit sums: the pairs of the rows above are at most P <= K * T < 2^31, rows_fit)
   int32_t before = 0, span = 0;
   const bool last_wg = blockIdx.x == gridDim.x - 1;  // tile T - 1's: writes the widest rectangle
   uint64_t bits[kRowsPer];
@@ -2338,8 +2330,8 @@ __device__ inline RowBin bin_tile_row(const Problem& p, const int4* __restrict__
     rl.span[wid] = span;
   }
   __syncthreads();
-  // Word q = i * 4 + wave holds Gaussians 64 q .. 64 q + 63, so ranks follow ascending ids: lane
-  // q < 16 takes word q's popcount, and an exclusive scan gives each word's first rank.
+  // Word q = i * kWaves + wave holds Gaussians 64 q .. 64 q + 63, so ranks follow ascending ids:
+  // lane q < 16 takes word q's popcount, and an exclusive scan gives each word's first rank.
   const int32_t cq = lane < kRowsMaxK / 64 ? __popcll(rl.bits[lane]) : 0;
   const int32_t iq = dpp_scan_i32(cq);
   const int32_t n = __builtin_amdgcn_readlane(iq, kRowsMaxK / 64 - 1);
@@ -2364,6 +2356,15 @@ __device__ inline RowBin bin_tile_row(const Problem& p, const int4* __restrict__
   return RowBin{rl.list, n, base, fspan, tile_ptr_out};
 }
 
+// Single 16x16 fields of up to kRowsMaxK Gaussians (rows_in_render): the render bins its own
+// tile row, so no k_bin_tiles launch precedes it.  A workgroup takes eight tile pairs of one
+// tile row (ceil(ceil(C / 2) / 8) workgroups a row).  Its 512 threads test the K rectangles
+// (two each, loads in flight together) against the row: a ballot per 64 Gaussians gives the
+// row's mask words, and each thread adds the pairs its Gaussians have in the rows above,
+// w * clamp(tr - first row, 0, h).  After a barrier each thread places its row Gaussians in the
+// row list at their rank (the mask words' popcounts before its word, then its lane's rank in
+// the word), with their column ranges; after a second barrier each wave renders its pair from
+// the list (render16x2_body<kRows>), which also gives the segment starts in closed form.
 __global__ __launch_bounds__(kRowsThreads) void k_render16x2_rows(
     Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, int64_t* tile_ptr, int64_t* ids, int64_t capacity,
