@@ -2799,12 +2799,26 @@ __device__ __forceinline__ void bwd16_body(
       if (kDirect) {
         // the six row sums in every lane of the row (butterfly: the same sum in each lane), then
         // lane 10 + k forms output k of the map and adds it to the Gaussian's gradient
-        const float s0 = dpp_row_allsum_f32(m0), s1 = dpp_row_allsum_f32(m1), s2 = dpp_row_allsum_f32(m2);
-        const float s3 = dpp_row_allsum_f32(m3), s4 = dpp_row_allsum_f32(m4), s5 = dpp_row_allsum_f32(m5);
+        float s0 = dpp_row_allsum_f32(m0), s1 = dpp_row_allsum_f32(m1), s2 = dpp_row_allsum_f32(m2);
+        float s3 = dpp_row_allsum_f32(m3), s4 = dpp_row_allsum_f32(m4), s5 = dpp_row_allsum_f32(m5);
+        if (split) {  // (heavy tiles) the Gaussian's slots: 0 + 1 and 2 + 3 (two Gaussians) or all four
+          float sv[6] = {s0, s1, s2, s3, s4, s5};
+#pragma unroll
+          for (int i = 0; i < 6; ++i) {
+            sv[i] += __shfl_xor(sv[i], 16, 64);
+            if (rem == 1) sv[i] += __shfl_xor(sv[i], 32, 64);
+          }
+          s0 = sv[0];
+          s1 = sv[1];
+          s2 = sv[2];
+          s3 = sv[3];
+          s4 = sv[4];
+          s5 = sv[5];
+        }
         const int k = row - 10;
         const float P = (k == 1 || k == 2) ? s1 : s0, Q = k < 3 ? s2 : s3;
         const float o = fmaf(cf.x, P, fmaf(cf.y, Q, fmaf(cf.z, s4, cf.w * s5)));
-        if (g >= 0 && row >= 10) unsafeAtomicAdd(dgrad + direct_slot(g, k), o);
+        if (g >= 0 && row >= 10 && part == 0) unsafeAtomicAdd(dgrad + direct_slot(g, k), o);
         continue;
       }
       if (!kTransposeSums) {
@@ -3943,6 +3957,14 @@ void launch_bwd16(const Problem& p, int32_t xh, hipStream_t st, const float* gra
     if (xh > 0) {
       Problem q = p;
       q.heavy = kHeavyTile;
+      if constexpr (!kTS) {
+        if (ev && dgrad) {  // gf_backward_direct on a field with heavy tiles
+          hipLaunchKernelGGL((k_bwd16<TP, GI, false, kMC, true, true, true>), dim3((unsigned)(xh + quad_grid(p))),
+                             dim3(kTileThreads), 0, st, q, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L,
+                             heavy_list, heavy_count, xh, dcoef, dgrad);
+          return;
+        }
+      }
       hipLaunchKernelGGL((k_bwd16<TP, GI, kTS, kMC, true>), dim3((unsigned)(xh + quad_grid(p))),
                          dim3(kTileThreads), 0, st, q, grad, rc, cc, mu, raw, ev, tp, gi, num_pairs, ws, L,
                          heavy_list, heavy_count, xh, nullptr, nullptr);
@@ -4478,12 +4500,13 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
 }
 
 // gf_backward_direct runs one launch where the binning stored the chain-rule maps (the mask
-// path) and the tiles take the plain row-sum kernel: 16x16 or 32x32 tiles, sparse, no heavy-tile
-// workgroups, and fewer than 8192 tiles.  The direct gradients have one slot per Gaussian, so a
-// Gaussian's atomics cannot be spread over stripes: on larger grids, whose Gaussians can touch
-// thousands of tiles, it runs the reduction and the finish, which writes the same gradients.
-// Below 8192 tiles one wide Gaussian still serialises the direct kernel's atomics on its slot,
-// about 10 ns a tile.  Measured at cfg3's grid with one centred Gaussian of growing rectangle:
+// path) and the tiles take the row-sum kernels: 16x16 or 32x32 tiles, sparse (heavy tiles
+// included: their four-wave workgroups add into the slots too).  The direct gradients have one
+// slot per Gaussian, so a Gaussian's atomics cannot be spread over stripes: on grids of 8192
+// tiles or more, whose Gaussians can touch thousands of tiles, it runs the reduction and the
+// finish, which writes the same gradients, unless the binning's widest rectangle is known to be
+// under kDirectMaxSpan tiles.  One wide Gaussian serialises the direct kernel's atomics on its
+// slot, about 10 ns a tile.  Measured at cfg3's grid with one centred Gaussian of growing rectangle:
 //   tiles of the rectangle    15    256    625    1369   2401   6400
 //   one launch, us            9.3   10.8   15.3   23.7   36.6   85.1
 //   reduction + finish, us    11.7  11.6   11.7   13.8   17.0   27.3
@@ -4491,8 +4514,9 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
 // one of kDirectMaxSpan tiles or more sends the call to the reduction + finish.
 constexpr int64_t kDirectMaxSpan = 320;
 bool direct_one_launch(const Problem& p, int64_t num_pairs, int64_t max_span) {
-  return p.W > 0 && quad_tiles(p) && (int64_t)p.R * p.C < 8192 && !bwd_dense(p, num_pairs) &&
-         heavy_grid(p, num_pairs) == 0 && max_span < kDirectMaxSpan;
+  const bool small_grid = (int64_t)p.R * p.C < 8192;
+  return p.W > 0 && quad_tiles(p) && (small_grid || max_span >= 0) && !bwd_dense(p, num_pairs) &&
+         max_span < kDirectMaxSpan;
 }
 
 int gf_backward_direct_launches(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
@@ -4661,8 +4685,10 @@ int gf_backward_direct_kcap(const gf_field_config* cfg, int64_t out_features, in
 
 // The one-pass kernel takes the fields gf_backward_direct runs in one launch, with 16x16 tiles and
 // at least one Gaussian.
+// (the fused kernel has no heavy-tile workgroups)
 bool fused_one_pass(const Problem& p, int64_t pair_bound) {
-  return p.K > 0 && p.tile_out == 16 && p.tile_in == 16 && direct_one_launch(p, pair_bound, -1);
+  return p.K > 0 && p.tile_out == 16 && p.tile_in == 16 && direct_one_launch(p, pair_bound, -1) &&
+         heavy_grid(p, pair_bound) == 0;
 }
 
 int gf_fwd_bwd_fused_supported(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,

@@ -124,9 +124,10 @@ def test_workspace_and_pointer_checks():
 
 def test_backward_direct_host_logic():
     """gf_backward_direct's host side: the launch count it will make (1 on the mask path with
-    sparse 16x16 / 32x32 tiles, no heavy-tile workgroups and no known rectangle of 320 tiles or
-    more, 2 elsewhere), where its gradient slots lie in the forward workspace, and the workspace
-    check before any device work."""
+    sparse 16x16 / 32x32 tiles, heavy tiles included, below 8192 tiles or with the widest
+    rectangle known, and no known rectangle of 320 tiles or more; 2 elsewhere), where its
+    gradient slots lie in the forward workspace, and the workspace check before any device
+    work."""
     lib = N.lib()
     cfg = ctypes.byref(_cfg())
 
@@ -142,8 +143,11 @@ def test_backward_direct_host_logic():
 
     assert launches(1280, 1280, 1024, 23618) == 1          # cfg3
     assert launches(1280, 1280, 1024, 16 * 6400) == 2      # dense tiles: the transposing reduction
-    assert launches(1280, 1792, 512, 20000) == 2           # 8960 tiles: 8 accumulator stripes
-    assert launches(1280, 1280, 2048, 40000) == 2          # heavy-tile workgroups (K >= 2048)
+    assert launches(1280, 1792, 512, 20000) == 2           # 8960 tiles, widest rectangle not known
+    assert launches(1280, 1792, 512, 20000, span=100) == 1  # ... known to be narrow
+    assert launches(1280, 1792, 512, 20000, span=400) == 2
+    assert launches(1280, 1280, 2048, 40000) == 1          # heavy-tile workgroups add into the slots too
+    assert launches(1280, 5120, 4096, 52094, span=90) == 1  # cfg5c: heavy tiles, 25600 tiles
     assert launches(320, 320, 9000, 20000) == 2            # past the masks: the emission path
     assert launches(320, 768, 256, 2000) == 1              # cfg2, binned in the render
     assert launches(1280, 1280, 1024, 23618, ctypes.byref(_cfg(tile_out=32, tile_in=32))) == 1

@@ -831,12 +831,10 @@ def test_backward_direct_hot_gaussians(device, nbig):
 def test_backward_direct_fallbacks(device):
     """Fields the one-launch kernel does not take run the reduction + finish into the direct
     gradients: FieldPlan.backward's kernels (equal up to the order of the float atomics).  Dense
-    tiles (>= 16 pairs a tile), heavy-tile workgroups (K >= 2048), the emission path (K past the
-    masks), 8x8 tiles, a grid of 8960 tiles (8 accumulator stripes); K = 0."""
+    tiles (>= 16 pairs a tile), the emission path (K past the masks), 8x8 tiles, a grid of 8960
+    tiles (8 accumulator stripes) whose widest rectangle is not given; K = 0."""
     cases = [
         (wl.make_problem("dense_320_k600", 320, 320, 600, math.log(24.0), 0.2, 31), {}),
-        (wl.make_problem("heavy_640_k2048", 640, 640, 2048, math.log(6.0), 0.5, 32, clusters=4,
-                         cluster_sigma_px=30.0), {}),
         (wl.make_problem("emit_320_k9000", 320, 320, 9000, math.log(2.0), 0.5, 33), {}),
         (wl.make_problem("tile8_200_k100", 200, 200, 100, math.log(4.0), 0.5, 34), dict(tile_out=8, tile_in=8)),
         (wl.make_problem("stripes_1280x1792_k512", 1280, 1792, 512, math.log(8.0), 0.6, 36), {}),
@@ -857,6 +855,41 @@ def test_backward_direct_fallbacks(device):
         torch.cuda.synchronize()
         for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), one, two):
             grad_close(a, b, name, rtol=1e-5)
+
+
+def test_backward_direct_heavy_tiles_and_large_grids(device):
+    """The one-launch backward on fields with heavy-tile workgroups (four waves a tile, their last
+    rounds split over the slots) and on grids of 8192 tiles or more whose widest rectangle is
+    known to be under 320 tiles: one launch, against the reduction + finish on the same forward
+    (equal up to the order of the float atomics), twice in a row (the second call adds the same
+    gradients again), and cfg5c's against the oracle."""
+    cases = [
+        wl.make_problem("heavy_640_k2048", 640, 640, 2048, math.log(6.0), 0.5, 32, clusters=4, cluster_sigma_px=30.0),
+        wl.make_problem("stripes_1280x1792_k512", 1280, 1792, 512, math.log(8.0), 0.6, 36),
+        wl.cfg5c(0),
+    ]
+    for p in cases:
+        q = p.to(device)
+        plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=max(1, 400 * p.k))
+        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+        torch.cuda.synchronize()
+        P, span = plan.bin_info()
+        say(f"{p.name}: P={P} T={plan.T} widest rectangle {span}")
+        assert plan.status() == 0 and span < 320 and plan.direct_launches(P, span) == 1
+        two = [t.clone() for t in plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
+                                                num_pairs=P)]
+        one = [t.clone() for t in plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw,
+                                                       q.amp, num_pairs=P, max_span=span)]
+        again = plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp, num_pairs=P,
+                                     max_span=span)
+        torch.cuda.synchronize()
+        for name, a, b, c in zip(("d_mu", "d_chol_raw", "d_amp"), one, two, again):
+            grad_close(a, b, name, rtol=1e-5)
+            grad_close(c, 2.0 * b, f"{name} (second call)", rtol=1e-5)
+        if p.name.startswith("cfg5c"):
+            r = oracle(p, batched=True)
+            for name, a, b in zip(("d_mu", "d_chol_raw", "d_amp"), one, r[3:]):
+                grad_close(a, b, f"{name} vs oracle")
 
 
 def test_backward_stripes(device):
@@ -1985,8 +2018,9 @@ def test_heavy_tiles_cfg5c_plan_and_determinism(device):
 @pytest.mark.parametrize("case", ["dense", "indefinite"])
 def test_heavy_tiles_autograd_train_function(device, case):
     """Heavy tiles through the reference's autograd entry point (runtime.gaussian_field_train,
-    runtime.py:273-297): its backward receives the forward workspace kept on ctx, so the
-    reduction takes the heavy-tile kernels; gradients against the oracle."""
+    runtime.py:273-297): its backward receives the forward workspace kept on ctx, so it takes the
+    heavy-tile kernels (the one-launch kernel where the widest rectangle allows it, else the
+    reduction + finish); gradients against the oracle."""
     c = dict(HEAVY_CASES[case])
     c.pop("cfg", None)
     p = _clustered_problem(f"heavy_autograd_{case}", seed=42, **c)
