@@ -240,14 +240,15 @@ int gf_backward_train(const gf_field_config* cfg, int64_t out_features, int64_t 
  * the same forward therefore leaves twice the gradients in the slots, whichever path runs;
  * callers that need one backward's gradients copy them out and run the next forward first.
  * forward_workspace is required: that of the forward over the same (mu, chol_raw, amp) and
- * config, with its int64 tile_ptr and ids.  Fields off the mask path, dense fields
- * (num_pairs >= 16 T), grids of 8192 tiles or more (whose reduction spreads each Gaussian's
- * atomics over stripes) and fields with heavy-tile workgroups run gf_backward_reduce +
- * gf_backward_finish, whose finish adds into the same slots; so do fields whose widest tile
- * rectangle is known (max_span >= 0, gf_bin_info.max_span of the forward) to cover 320 tiles or
- * more, where one Gaussian's atomics on its one slot would cost the kernel more than the second
- * launch (about 10 ns a tile).  max_span < 0: not known (graphs captured before the content is),
- * the choice is then made on the other conditions alone.  The gradients agree with gf_backward's
+ * config, with its int64 tile_ptr and ids (fields with heavy tiles included: their four-wave
+ * workgroups add into the slots too).  Fields off the mask path and dense fields
+ * (num_pairs >= 16 T) run gf_backward_reduce + gf_backward_finish, whose finish adds into the
+ * same slots; so do fields whose widest tile rectangle is known (max_span >= 0,
+ * gf_bin_info.max_span of the forward) to cover 320 tiles or more, where one Gaussian's atomics
+ * on its one slot would cost the kernel more than the second launch (about 10 ns a tile), and
+ * grids of 8192 tiles or more whose widest rectangle is not known (max_span < 0: graphs
+ * captured before the content is; their reduction spreads each Gaussian's atomics over
+ * stripes).  The gradients agree with gf_backward's
  * within fp32 rounding (the map is applied per tile, in fp32).
  */
 int gf_backward_direct(const gf_field_config* cfg, int64_t out_features, int64_t in_features, int64_t k,
