@@ -11,7 +11,8 @@ graph.  Workloads:
   cfg4                          all 128 attention linears of an SD1.5-shaped UNet, K=1024 each,
                                 as one batch (guass_amd.ops.FieldBatchPlan: five launches per
                                 step for all layers)
-  cfg1, cfg2, cfg5, cfg5c       single fields as cfg3
+  cfg1, cfg2, cfg5, cfg5c, cfg5s  single fields as cfg3 (cfg5s: cfg5's stress variant, Student-t
+                                log-scale scale 1.0)
   delta-apply                   the layer's composition with delta-W over the cfg4 shapes (x of
                                 --tokens rows, fp32, forward + backward into delta-W): the
                                 reference's row-chunked composition against one merged GEMM
@@ -63,7 +64,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="cfg3",
-                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "cfg5c", "cfg4-model", "delta-apply"])
+                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "cfg5c", "cfg5s", "cfg4-model", "delta-apply"])
     ap.add_argument("--tokens", type=int, default=4096, help="delta-apply: rows of x per layer")
     ap.add_argument("--model-tokens", type=int, default=64, help="cfg4-model: rows of x per layer")
     ap.add_argument("--delta-apply", default="merged", choices=["merged", "row_chunk"],

@@ -160,4 +160,10 @@ def cfg4(seed: int = 0, layers: int | None = None, **kw) -> list[FieldProblem]:
             for i, (name, m, n) in enumerate(shapes)]
 
 
-CONFIGS = {"cfg1": cfg1, "cfg2": cfg2, "cfg3": cfg3, "cfg5": cfg5, "cfg5c": cfg5c}
+def cfg5s(seed: int = 0, **kw) -> FieldProblem:
+    """cfg5's stress variant: Student-t log-scale scale 1.0 instead of 0.5 (1.67M pairs, 65 a
+    tile on average, up to 255)."""
+    return cfg5(seed, t_scale=1.0, **kw)
+
+
+CONFIGS = {"cfg1": cfg1, "cfg2": cfg2, "cfg3": cfg3, "cfg5": cfg5, "cfg5c": cfg5c, "cfg5s": cfg5s}
