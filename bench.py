@@ -123,6 +123,9 @@ def algorithmic_counts(tile_ptr, M: int, N: int, K: int, tile_out: int, tile_in:
         "bytes_bwd": 4.0 * M * N + 48.0 * K,
         "flops_fwd": FWD_FLOPS_PER_EVAL * E,
         "flops_bwd": BWD_FLOPS_PER_EVAL * E,
+        # the binning state the forward hands to the backward, reported beside the algorithmic
+        # bytes rather than in them: tile_ptr [T+1] and gaussian_ids_sorted [P], int64 each
+        "bytes_binning_state": 8.0 * (R * C + 1 + int(tile_ptr[-1].item())),
     }
 
 
@@ -708,6 +711,7 @@ def main() -> int:
         "data": "synthetic (seeded Gaussian field, BASELINE.json distribution)",
         "config": {"workload": workload, **shape, "pairs": int(total["pairs"]),
                    "pair_pixel_evals": total["evals"],
+                   "binning_state_bytes": int(total["bytes_binning_state"]),
                    "launch": (f"hip graph replay, {per_run} steps per graph" if graph is not None
                               else "eager")},
         "roofline": roof,
