@@ -2134,14 +2134,18 @@ __device__ __forceinline__ void render16x2_body(
       const float aa = a.z * dx;
       const float bb = a.w * dx;
       const float A = aa * aa;
+      // kSkipHalves: the slot's per-tile constants in registers before the per-tile branches,
+      // one LDS read of the slot and one address, not a read and an address per branch
+      const float mu1 = a.y, wc = b.x, wab[2] = {b.y, b.z};
+      if constexpr (kSkipHalves) __asm__ volatile("" ::"v"(mu1), "v"(wc), "v"(wab[0]), "v"(wab[1]));
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         if ((f & (1 << h)) == 0) continue;
-        const float wh = h == 0 ? b.y : b.z;
-        const float z0 = fmaf(b.x, y0[h] - a.y, bb);
+        const float wh = wab[h];
+        const float z0 = fmaf(wc, y0[h] - mu1, bb);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float z = i == 0 ? z0 : fmaf(b.x, yd[h][i], z0);
+          const float z = i == 0 ? z0 : fmaf(wc, yd[h][i], z0);
           const float e = free_form ? __builtin_amdgcn_exp2f(-fmaf(z, z, A)) : basis_w(p, A, z);
           acc[h][i] = fmaf(wh, e, acc[h][i]);
         }
