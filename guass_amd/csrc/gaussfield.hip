@@ -521,6 +521,22 @@ __device__ inline float dpp_row_allsum_f32(float v) {
   return v;
 }
 
+// dst = src[partner] + src in the lanes 8..15 of each row of 16 (DPP banks 2 and 3), partner
+// = 15 - lane (row_mirror); dst unchanged in lanes 0..7 (the bank mask leaves them unwritten).
+// One v_add_f32_dpp where a select per operand would take three instructions; the s_nop gives
+// the two wait states a DPP read needs after a VALU write of its source.
+__device__ inline float row_mirror_sum_upper(float dst, float src) {
+  __asm__("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_mirror row_mask:0xf bank_mask:0xc" : "+v"(dst) : "v"(src));
+  return dst;
+}
+
+// The same in lanes 4..7 and 12..15 of each row (banks 1 and 3), partner = lane ^ 7 within
+// each half row (row_half_mirror).
+__device__ inline float row_half_mirror_sum_odd_banks(float dst, float src) {
+  __asm__("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0xa" : "+v"(dst) : "v"(src));
+  return dst;
+}
+
 // ------------------------------------------------------------------------------------------
 // Workgroup scans.
 
@@ -2851,12 +2867,18 @@ __device__ __forceinline__ void bwd16_body(
       // half of a lane's values, sends the other half to its partner (lane ^ 15, ^ 7, ^ 2, ^ 1:
       // row_mirror, row_half_mirror, two quad_perms) and adds what it receives.  Lane r ends
       // with moment r >> 1 (moments 6, 7 are zero padding); even lanes 0..10 add it atomically.
-      const float a0 = (hb3 ? m4 : m0) + dpp_f32<0x140>(hb3 ? m0 : m4);
-      const float a1 = (hb3 ? m5 : m1) + dpp_f32<0x140>(hb3 ? m1 : m5);
-      const float a2 = (hb3 ? 0.0f : m2) + dpp_f32<0x140>(hb3 ? m2 : 0.0f);
-      const float a3 = (hb3 ? 0.0f : m3) + dpp_f32<0x140>(hb3 ? m3 : 0.0f);
-      const float c0 = (hb2 ? a2 : a0) + dpp_f32<0x141>(hb2 ? a0 : a2);
-      const float c1 = (hb2 ? a3 : a1) + dpp_f32<0x141>(hb2 ? a1 : a3);
+      // Each step adds the partner's copy of both halves in every lane (one DPP add each) and
+      // then, for the lanes that keep the second half, overwrites with that half's sum (a DPP
+      // add under a bank mask): two instructions per kept pair instead of two selects and an
+      // add.  The halves a lane drops carry whatever they carry; they only reach lanes 12..15
+      // (the padding moments, no atomics).  Each sum is the same two operands as a select-and-
+      // add, so the results are bit-identical.
+      const float a0 = row_mirror_sum_upper(dpp_f32<0x140>(m0) + m0, m4);
+      const float a1 = row_mirror_sum_upper(dpp_f32<0x140>(m1) + m1, m5);
+      const float a2 = dpp_f32<0x140>(m2) + m2;  // lanes 8..15: padding
+      const float a3 = dpp_f32<0x140>(m3) + m3;
+      const float c0 = row_half_mirror_sum_odd_banks(dpp_f32<0x141>(a0) + a0, a2);
+      const float c1 = row_half_mirror_sum_odd_banks(dpp_f32<0x141>(a1) + a1, a3);
       float d = (hb1 ? c1 : c0) + dpp_f32<0x4e>(hb1 ? c0 : c1);
       d += dpp_f32<0xb1>(d);
       if (split) {  // the Gaussian's slots: 0 + 1 and 2 + 3 (two Gaussians) or all four
