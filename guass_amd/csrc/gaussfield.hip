@@ -537,6 +537,14 @@ __device__ inline float row_half_mirror_sum_odd_banks(float dst, float src) {
   return dst;
 }
 
+// v + v[lane ^ 1] in every lane, as one DPP add where the wave's lanes all still run (volatile:
+// not moved into a branch whose lanes are a subset, where the partner's value would not be read).
+__device__ inline float pair_sum_all_lanes(float v) {
+  float r;
+  __asm__ volatile("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v));
+  return r;
+}
+
 // ------------------------------------------------------------------------------------------
 // Workgroup scans.
 
@@ -2872,15 +2880,19 @@ __device__ __forceinline__ void bwd16_body(
       // add under a bank mask): two instructions per kept pair instead of two selects and an
       // add.  The halves a lane drops carry whatever they carry; they only reach lanes 12..15
       // (the padding moments, no atomics).  Each sum is the same two operands as a select-and-
-      // add, so the results are bit-identical.
-      const float a0 = row_mirror_sum_upper(dpp_f32<0x140>(m0) + m0, m4);
-      const float a1 = row_mirror_sum_upper(dpp_f32<0x140>(m1) + m1, m5);
-      const float a2 = dpp_f32<0x140>(m2) + m2;  // lanes 8..15: padding
-      const float a3 = dpp_f32<0x140>(m3) + m3;
-      const float c0 = row_half_mirror_sum_odd_banks(dpp_f32<0x141>(a0) + a0, a2);
-      const float c1 = row_half_mirror_sum_odd_banks(dpp_f32<0x141>(a1) + a1, a3);
-      float d = (hb1 ? c1 : c0) + dpp_f32<0x4e>(hb1 ? c0 : c1);
-      d += dpp_f32<0xb1>(d);
+      // add, so the results are bit-identical (no contraction: m1 and m3 are products, which
+      // an fma would fold into the first add, unrounded).
+      float d;
+      {
+#pragma clang fp contract(off)
+        const float a0 = row_mirror_sum_upper(dpp_f32<0x140>(m0) + m0, m4);
+        const float a1 = row_mirror_sum_upper(dpp_f32<0x140>(m1) + m1, m5);
+        const float a2 = dpp_f32<0x140>(m2) + m2;  // lanes 8..15: padding
+        const float a3 = dpp_f32<0x140>(m3) + m3;
+        const float c0 = row_half_mirror_sum_odd_banks(dpp_f32<0x141>(a0) + a0, a2);
+        const float c1 = row_half_mirror_sum_odd_banks(dpp_f32<0x141>(a1) + a1, a3);
+        d = pair_sum_all_lanes((hb1 ? c1 : c0) + dpp_f32<0x4e>(hb1 ? c0 : c1));
+      }
       if (split) {  // the Gaussian's slots: 0 + 1 and 2 + 3 (two Gaussians) or all four
         d += __shfl_xor(d, 16, 64);
         if (rem == 1) d += __shfl_xor(d, 32, 64);
