@@ -4032,9 +4032,13 @@ void launch_bwd16(const Problem& p, int32_t xh, hipStream_t st, const float* gra
                      nullptr);
 }
 
-// Tiles of many Gaussians (a wave makes >= 4 rounds on average) take the transposing moment
-// reduction (fewer instructions); sparse ones the row sums (shorter chain).
-bool bwd_dense(const Problem& p, int64_t num_pairs) { return num_pairs >= 16 * (int64_t)p.R * p.C; }
+// Tiles of several Gaussians (P >= 8 T: a wave makes two or more rounds on average) take the
+// transposing moment reduction (fewer instructions); sparse ones the row sums (shorter chain).
+// cfg5 (11.6 pairs a tile) 34.6 -> 29.8 us with the transposing form; at 4.5 pairs a tile
+// (cfg2) it would cost the one-launch form below.
+bool bwd_dense(const Problem& p, int64_t num_pairs) { return num_pairs >= 8 * (int64_t)p.R * p.C; }
+// The one-launch backward's limit: fewer than 16 pairs a tile.
+bool direct_pairs_fit(const Problem& p, int64_t num_pairs) { return num_pairs < 16 * (int64_t)p.R * p.C; }
 
 template <typename TP, typename GI>
 void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, const float* rc,
@@ -4042,7 +4046,8 @@ void launch_bwd(const Problem& p, dim3 grid, hipStream_t st, const float* grad, 
                 const void* tile_ptr, const void* gids, int64_t num_pairs, uint8_t* ws,
                 const BwdLayout& L, const int32_t* heavy_list, const uint32_t* heavy_count,
                 const float4* dcoef = nullptr, float* dgrad = nullptr) {
-  const bool dense = bwd_dense(p, num_pairs);
+  // (the one-launch gradients, dgrad, take the row sums: up to 16 pairs a tile)
+  const bool dense = !dgrad && bwd_dense(p, num_pairs);
   // heavy-tile workgroups only with the forward's tile list (the forward workspace)
   const int32_t xh = heavy_list ? heavy_grid(p, num_pairs) : 0;
   const TP* tp = reinterpret_cast<const TP*>(tile_ptr);
@@ -4553,7 +4558,7 @@ int gf_backward(const gf_field_config* cfg, int64_t out_features, int64_t in_fea
 constexpr int64_t kDirectMaxSpan = 320;
 bool direct_one_launch(const Problem& p, int64_t num_pairs, int64_t max_span) {
   const bool small_grid = (int64_t)p.R * p.C < 8192;
-  return p.W > 0 && quad_tiles(p) && (small_grid || max_span >= 0) && !bwd_dense(p, num_pairs) &&
+  return p.W > 0 && quad_tiles(p) && (small_grid || max_span >= 0) && direct_pairs_fit(p, num_pairs) &&
          max_span < kDirectMaxSpan;
 }
 

@@ -143,6 +143,7 @@ def test_backward_direct_host_logic():
 
     assert launches(1280, 1280, 1024, 23618) == 1          # cfg3
     assert launches(1280, 1280, 1024, 16 * 6400) == 2      # dense tiles: the transposing reduction
+    assert launches(1280, 1280, 1024, 12 * 6400, span=9) == 1  # 8..16 a tile: still one launch (row sums)
     assert launches(1280, 1792, 512, 20000) == 2           # 8960 tiles, widest rectangle not known
     assert launches(1280, 1792, 512, 20000, span=100) == 1  # ... known to be narrow
     assert launches(1280, 1792, 512, 20000, span=400) == 2

@@ -901,6 +901,35 @@ def test_backward_direct_heavy_tiles_and_large_grids(device):
                 grad_close(a, b, f"{name} vs oracle")
 
 
+def test_backward_both_reductions_between_8_and_16_pairs_a_tile(device):
+    """Fields of 8 to 16 pairs a tile: the reduction + finish takes the transposing moment
+    reduction there (from 8 pairs a tile), the one-launch backward still the row sums (up to 16).
+    Both against the oracle and against each other (the order of the float atomics), with and
+    without heavy-tile workgroups."""
+    cases = [
+        wl.make_problem("band_640_k900", 640, 640, 900, math.log(8.0), 0.5, 40),
+        wl.make_problem("heavy_640_k2048", 640, 640, 2048, math.log(6.0), 0.5, 32, clusters=4, cluster_sigma_px=30.0),
+    ]
+    for p in cases:
+        q = p.to(device)
+        plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=max(1, 400 * p.k))
+        plan.forward(q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp)
+        torch.cuda.synchronize()
+        P, span = plan.bin_info()
+        say(f"{p.name}: P={P} T={plan.T} ({P / plan.T:.2f} a tile) widest rectangle {span}")
+        assert plan.status() == 0 and 8 * plan.T <= P < 16 * plan.T and plan.direct_launches(P, span) == 1
+        two = [t.clone() for t in plan.backward(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw, q.amp,
+                                                num_pairs=P)]
+        one = [t.clone() for t in plan.backward_direct(q.grad, q.row_coords, q.col_coords, q.mu, q.chol_raw,
+                                                       q.amp, num_pairs=P, max_span=span)]
+        torch.cuda.synchronize()
+        r = oracle(p, batched=True)
+        for name, a, b, c in zip(("d_mu", "d_chol_raw", "d_amp"), one, two, r[3:]):
+            grad_close(a, b, f"{name}: one launch vs reduction + finish", rtol=1e-5)
+            grad_close(b, c, f"{name}: reduction + finish vs oracle")
+            grad_close(a, c, f"{name}: one launch vs oracle")
+
+
 def test_backward_stripes(device):
     """Tile grids of >= 2048 tiles spread each Gaussian's accumulators over 4 stripes (>= 8192: 8,
     >= 16384: 32): a 1280x1792 field (8960 tiles) against the oracle, alone and as a batch layer next to a
