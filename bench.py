@@ -61,7 +61,11 @@ BWD_FLOPS_PER_EVAL = 41    # reference backward.cu:313-351
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=500)
+    # Default: 5000 graph-replayed steps (about 0.1 s at cfg3, 2.7 s at cfg4): the timed region's
+    # fixed start-up cost, about 1.2 ms between the clock's start and the first step's kernel on
+    # some boxes (outside the HIP events, inside the wall clock), is 0.24 us a step there
+    # instead of 2.4 at 500.  The model-step and delta-apply modes default to 500.
+    ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="cfg3",
                     choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "cfg5c", "cfg5s", "cfg4-model", "delta-apply"])
@@ -96,6 +100,8 @@ def parse() -> argparse.Namespace:
                     help="per-kernel HBM bytes per launch measured with rocprofv3 --pmc "
                          "(default: profiles/<config>_hbm_traffic.json)")
     args = ap.parse_args()
+    if args.steps is None:
+        args.steps = 500 if args.config in ("cfg4-model", "delta-apply") else 5000
     if args.traffic_file is None:
         args.traffic_file = str(ROOT / "profiles" / f"{args.config}_hbm_traffic.json")
     return args
