@@ -420,12 +420,17 @@ __device__ inline float merge_weight(float w, float scale, float d) {
 // Columns pc .. pc+3 of row pr (those inside the matrix) of delta-W from v[], and of the merged
 // weight where there is one.  delta may be NULL (a merged layer whose delta-W is not kept).
 __device__ inline void store_row4(const Problem& p, float* __restrict__ delta, const MergedOut& mo, int32_t pr,
-                                  int32_t pc, const float (&v)[4]) {
+                                  int32_t pc, const float (&v)[4], bool tile_inner = false) {
   const int64_t off = (int64_t)pr * p.N + pc;
   const bool inner = pc + 3 < p.N;
+  // tile_inner (the same in every lane): the lane's tile lies inside the matrix, so with rows of
+  // N % 4 == 0 floats from a 16-byte aligned base every lane's float4 is inside and aligned --
+  // a scalar test instead of per-lane ones
+  const bool rows4 = tile_inner && (p.N & 3) == 0;
   if (delta) {
     float* out = delta + off;
-    if (inner && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+    if ((rows4 && (reinterpret_cast<uintptr_t>(delta) & 15) == 0) ||
+        (inner && (reinterpret_cast<uintptr_t>(out) & 15) == 0)) {
       store4_stream(out, v[0], v[1], v[2], v[3]);
     } else {
 #pragma unroll
@@ -436,7 +441,8 @@ __device__ inline void store_row4(const Problem& p, float* __restrict__ delta, c
   if (mo.merged) {
     const float* w = mo.base + off;
     float* out = mo.merged + off;
-    if (inner && ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(w)) & 15) == 0) {
+    if ((rows4 && ((reinterpret_cast<uintptr_t>(mo.merged) | reinterpret_cast<uintptr_t>(mo.base)) & 15) == 0) ||
+        (inner && ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(w)) & 15) == 0)) {
       const float4 w4 = load4_stream(w);
       store4_stream(out, merge_weight(w4.x, mo.scale, v[0]), merge_weight(w4.y, mo.scale, v[1]),
                     merge_weight(w4.z, mo.scale, v[2]), merge_weight(w4.w, mo.scale, v[3]));
@@ -2276,9 +2282,15 @@ __device__ __forceinline__ void render16x2_body(
     if (h == 0 && !has_a) continue;
     if (h == 1 && !has_b) break;
     const int32_t pc = pc0 + 16 * h;
+    const bool tile_inner = (tr + 1) * 16 <= p.M && (tc + h + 1) * 16 <= p.N;  // wave-uniform
     if (blk_sq) {  // as in render16_body
       float sq = 0.f;
-      if (pr < p.M) {
+      if (tile_inner) {
+        // a tile inside the matrix (the same answer in every lane: a scalar branch) sums its
+        // pixels without the per-pixel bounds selects, in the same order
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sq = fmaf(acc[h][i], acc[h][i], sq);
+      } else if (pr < p.M) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           if (pc + i < p.N) sq = fmaf(acc[h][i], acc[h][i], sq);
@@ -2286,7 +2298,9 @@ __device__ __forceinline__ void render16x2_body(
       sq = dpp_scan_f32(sq);
       if (lane == 63) blk_sq[ta + h] = sq;
     }
-    if (pr < p.M) store_row4(p, delta, mo, pr, pc, acc[h]);
+    // (the row-binned single-field kernel keeps the per-lane test: there the scalar one measured
+    // no faster, 8.44 against 8.36 us at cfg3 over three A/B pairs, where batches gained 3%)
+    if (pr < p.M) store_row4(p, delta, mo, pr, pc, acc[h], !kRows && tile_inner);
   }
 }
 
@@ -2413,7 +2427,7 @@ __global__ __launch_bounds__(kRowsThreads) void k_render16x2_rows(
 // listed heavy tile each (four waves, as k_render16<true>), the rest a pair of horizontally
 // adjacent tiles a wave (R x ceil(C / 2) pairs, four a workgroup, as k_render16x2), leaving a
 // heavy member of the pair to its own workgroup.
-__global__ __launch_bounds__(kTileThreads) void k_render16x2_heavy(
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(8))) void k_render16x2_heavy(
     Problem p, const float* __restrict__ row_coords, const float* __restrict__ col_coords,
     const GaussEval* __restrict__ ev, const int64_t* __restrict__ tile_ptr, int64_t* ids, int64_t capacity,
     float* __restrict__ delta, uint8_t* ws, const uint32_t* __restrict__ rowmask,
