@@ -2038,11 +2038,15 @@ __device__ __forceinline__ void render16x2_body(
   const int32_t pc0 = tc * 16 + ((lane & 3) << 2);
   const float x = row_coords[min(pr, p.M - 1)];
   float y0[2], yd[2][4];
+  // both tiles' columns inside the matrix from a 16-byte aligned base (the same in every lane):
+  // every lane's four columns are one aligned float4, without per-lane tests (the row-binned
+  // kernel keeps those, as in the stores below)
+  const bool cols4 = !kRows && (tc + 2) * 16 <= p.N && (reinterpret_cast<uintptr_t>(col_coords) & 15) == 0;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int32_t pc = pc0 + 16 * h;
     float y[4];
-    if (pc + 3 < p.N && ((reinterpret_cast<uintptr_t>(col_coords + pc) & 15) == 0)) {
+    if (cols4 || (pc + 3 < p.N && ((reinterpret_cast<uintptr_t>(col_coords + pc) & 15) == 0))) {
       const float4 v = *reinterpret_cast<const float4*>(col_coords + pc);
       y[0] = v.x;
       y[1] = v.y;
