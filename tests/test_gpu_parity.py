@@ -930,6 +930,44 @@ def test_backward_both_reductions_between_8_and_16_pairs_a_tile(device):
             grad_close(a, c, f"{name}: one launch vs oracle")
 
 
+def test_pair_render_unaligned_column_coordinates(device):
+    """The pair renders' wave-wide fast paths (one aligned float4 of column coordinates a lane,
+    the block sums and stores without per-lane tests) need a 16-byte aligned coordinate base; a
+    column-coordinate view 4 bytes off takes the per-lane path.  ΔW, tile_ptr and ids bit-equal
+    to the aligned call, for a single field on the mask path (the tile-pair kernel with
+    heavy-tile workgroups) and for the same field as a batch layer (with its block sums)."""
+    from guass_amd.ops import FieldBatchPlan
+
+    p = wl.make_problem("unaligned_640_k2000", 640, 640, 2000, math.log(6.0), 0.5, 44)
+    q = p.to(device)
+    buf = torch.zeros(p.in_features + 1, device=device)
+    buf[1:] = q.col_coords
+    cc = buf[1:]
+    assert cc.data_ptr() % 16 != 0 and torch.equal(cc, q.col_coords)
+    cap = 400 * p.k
+    outs = []
+    for cols in (q.col_coords, cc):
+        plan = FieldPlan(p.out_features, p.in_features, p.k, device, ids_capacity=cap)
+        plan.forward(q.row_coords, cols, q.mu, q.chol_raw, q.amp)
+        torch.cuda.synchronize()
+        assert plan.status() == 0
+        P = plan.pairs()
+        outs.append((plan.delta.clone(), plan.tile_ptr.clone(), plan.ids[:P].clone()))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    P = int(outs[0][1][-1])
+    layers = [q, wl.FieldProblem(p.name + "_unaligned", p.out_features, p.in_features, q.row_coords, cc, q.mu,
+                                 q.chol_raw, q.amp, q.grad)]
+    batch = FieldBatchPlan(layers, device, capacities=[P, P])
+    batch.forward()
+    torch.cuda.synchronize()
+    st, pairs, norms = batch.read(norms=True)
+    assert st == [0, 0] and pairs == [P, P]
+    a, b = batch.plans
+    assert torch.equal(a.delta, b.delta) and torch.equal(a.ids[:P], b.ids[:P]) and norms[0] == norms[1]
+    field_close(a.delta, outs[0][0], rtol=1e-6)  # the single field's heavy tiles sum in another order
+
+
 def test_backward_stripes(device):
     """Tile grids of >= 2048 tiles spread each Gaussian's accumulators over 4 stripes (>= 8192: 8,
     >= 16384: 32): a 1280x1792 field (8960 tiles) against the oracle, alone and as a batch layer next to a
